@@ -1,0 +1,120 @@
+// Device-side helpers shared by the gfx950 kernels.
+//
+// Every kernel is compiled with -ffp-contract=off and without fast-math, so a
+// float expression is evaluated in the order written with one rounding per
+// operation; where an operation order below mirrors a reference function it
+// says which (paths relative to vendor/embeddinggemma.c/src/).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eg2 {
+
+constexpr int kEmbd = 768;      // model.h:9
+constexpr int kFF = 1152;       // model.h:10
+constexpr int kHeads = 3;       // model.h:11
+constexpr int kHeadDim = 256;   // model.h:13
+constexpr int kCtx = 2048;      // model.h:14 and the executor's wave cap
+constexpr int kVocab = 262144;  // model.h:15
+constexpr int kQK = 32;         // Q8_0 block length (quants.h:6)
+constexpr int kQKVCols = kEmbd + 2 * kHeadDim;  // fused Q|K|V projection width
+constexpr int kDenseFF = 3072;                  // dense head hidden width
+
+// fp32 -> fp16 bits with the reference's rounding (quants.c:13-37): the
+// dropped mantissa bits round half-up in magnitude (not to nearest-even),
+// and any value of 2^16 or more with a nonzero mantissa maps to a NaN.
+__device__ __forceinline__ uint32_t fp32_to_fp16_bits(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t mant = x & 0x007FFFFFu;
+  const int32_t e = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    mant |= 0x00800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    uint32_t h = sign | (mant >> shift);
+    if ((mant >> (shift - 1u)) & 1u) h++;
+    return h;
+  }
+  if (e >= 31) {
+    if (mant == 0) return sign | 0x7C00u;
+    return sign | 0x7C00u | (mant >> 13) | 1u;
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (mant >> 13);
+  if (mant & 0x00001000u) h++;
+  return h;
+}
+
+// Exact fp16 bits -> fp32 (common.h:17-40); the hardware conversion is exact
+// for every fp16 value including subnormals.
+__device__ __forceinline__ float fp16_bits_to_fp32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Round-half-away-from-zero like C roundf, clamped to int8 (quants.c:169-174).
+__device__ __forceinline__ int32_t q8_round(float v) {
+  int32_t q = (int32_t)__builtin_roundf(v);
+  q = q < -128 ? -128 : q;
+  q = q > 127 ? 127 : q;
+  return q;
+}
+
+// Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Quantizes one Q8_0 block whose 32 values sit one per lane in a half-wave
+// (quants.c:97-177, scalar path). Every lane of the half-wave receives the
+// block's stored scale (as the float value of its fp16) and its own int8.
+struct Q8Lane {
+  float d;
+  int32_t q;
+};
+__device__ __forceinline__ Q8Lane q8_quantize_lane(float x) {
+  const float amax = half_wave_max(fabsf(x));
+  const float d = amax / 127.0f;
+  Q8Lane r;
+  r.d = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+  if (amax == 0.0f) {
+    r.q = 0;
+  } else {
+    const float id = 1.0f / d;
+    r.q = q8_round(x * id);
+  }
+  return r;
+}
+
+// Sum of squares of an LDS row of n floats (n % 8 == 0) in the reference's
+// SSE2 order (kernels.c:82-94): lane c < 8 runs the sequential chain over
+// x[8t + c] (lanes 0-3 are the first 4-lane accumulator, 4-7 the second),
+// then v[j] = acc0[j] + acc1[j] and the horizontal sum is
+// (v0 + v2) + (v1 + v3) (kernels.c:35-39). The result is returned to every
+// lane of the calling wave. All 64 lanes must call it.
+__device__ __forceinline__ float sum_squares_sse2(const float* row, int n) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+  if (lane < 8) {
+    for (int t = 0; t < n / 8; ++t) {
+      const float v = row[8 * t + lane];
+      const float p = v * v;
+      s = s + p;
+    }
+  }
+  const float hi = __shfl(s, (lane + 4) & 63, 64);
+  const float v = s + hi;  // lanes 0..3 hold v[0..3]
+  const float v0 = __shfl(v, 0, 64), v1 = __shfl(v, 1, 64);
+  const float v2 = __shfl(v, 2, 64), v3 = __shfl(v, 3, 64);
+  return (v0 + v2) + (v1 + v3);
+}
+
+// 1 / sqrtf(ss / n + eps) with correctly rounded division and square root
+// (kernels.c:144, :154, :165).
+__device__ __forceinline__ float rms_inverse(float ss, int n, float eps) {
+  return 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+}
+
+}  // namespace eg2

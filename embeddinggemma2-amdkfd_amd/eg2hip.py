@@ -1,0 +1,292 @@
+"""Python binding of libeg2hip.so (the gfx950 executor and its operators).
+
+Mirrors the reference's executor interface (src/gemma2_kfd.h:7-10):
+`Encoder(gguf_path)` wraps ei_gemma2_kfd_create / _free and
+`Encoder.batch(ids, offsets)` wraps ei_gemma2_kfd_batch, raising on the
+same conditions the C ABI reports with `false` + message. `ops` exposes the
+operator-level entry points of include/eg2_hip.h for device buffers (torch
+tensors are used only as device allocations and for their streams).
+
+The library must be built (`make -C embeddinggemma2-amdkfd_amd`); there is
+no fallback path: a missing library raises immediately.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libeg2hip.so")
+
+N_EMBD, N_FF, HEAD_DIM, N_CTX, VOCAB = 768, 1152, 256, 2048, 262144
+QKV_COLS = N_EMBD + 2 * HEAD_DIM
+
+_vp, _f, _i32 = C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int32)
+_u = C.c_uint
+
+
+class EiStr(C.Structure):
+    _fields_ = [("str", C.c_void_p), ("len", C.c_uint64)]
+
+
+class _KvValue(C.Union):
+    _fields_ = [("u64", C.c_uint64), ("i64", C.c_int64), ("f64", C.c_double), ("b", C.c_bool), ("s", EiStr)]
+
+
+class EiKv(C.Structure):
+    _fields_ = [("key", EiStr), ("type", C.c_uint32), ("v", _KvValue), ("arr_type", C.c_uint32),
+                ("arr_n", C.c_uint64), ("arr_data", C.c_void_p)]
+
+
+class EiTensor(C.Structure):
+    _fields_ = [("name", EiStr), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4), ("type", C.c_uint32),
+                ("offset", C.c_uint64), ("data", C.c_void_p), ("n_bytes", C.c_uint64)]
+
+
+class EiGguf(C.Structure):
+    _fields_ = [("map", C.c_void_p), ("map_len", C.c_size_t), ("version", C.c_uint32), ("n_kv", C.c_uint64),
+                ("n_tensors", C.c_uint64), ("alignment", C.c_uint64), ("data_off", C.c_uint64),
+                ("kv", C.POINTER(EiKv)), ("tensors", C.POINTER(EiTensor))]
+
+
+class SynthConfig(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("n_layer", C.c_uint), ("dense_head", C.c_uint), ("weight_std", C.c_float),
+                ("embed_std", C.c_float), ("norm_std", C.c_float), ("rope_base_full", C.c_float),
+                ("rope_base_swa", C.c_float), ("sliding_window", C.c_uint), ("sliding_window_pattern", C.c_uint),
+                ("threads", C.c_uint)]
+
+
+# Every symbol declared in include/eg2_hip.h and include/gemma2_kfd.h.
+SIGNATURES = {
+    "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
+    "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
+    "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _vp, _vp, _vp]),
+    "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
+    "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
+    "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
+    "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _u, _u, _vp]),
+    "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
+    "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "eg2_q8_split": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
+    "eg2_rope_table": (None, [C.c_float, _u, _vp]),
+    "eg2_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
+    "eg2_gguf_close": (None, [C.POINTER(EiGguf)]),
+    "eg2_synth_write_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthConfig), C.c_char_p, C.c_size_t]),
+    "ei_gemma2_kfd_create": (C.c_void_p, [C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
+    "ei_gemma2_kfd_free": (None, [C.c_void_p]),
+    "eg2_kfd_stage": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p, C.c_size_t]),
+    "eg2_kfd_launch_staged": (C.c_bool, [C.c_void_p, C.c_uint, C.c_char_p, C.c_size_t]),
+    "eg2_kfd_collect": (C.c_bool, [C.c_void_p, _f, C.c_char_p, C.c_size_t]),
+    "ei_gemma2_kfd_batch": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, _f, C.c_char_p,
+                                       C.c_size_t]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `make -C {HERE}`")
+        handle = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(code, what):
+    if code != 0:
+        raise HipError(f"{what}: {lib().eg2_hip_error_string(code).decode()} ({code})")
+
+
+def synth_gguf(path, seed=0, n_layer=24, dense_head=True, weight_std=0.02, embed_std=0.02, norm_std=0.1,
+               rope_base_full=10000.0, rope_base_swa=10000.0, sliding_window=0, sliding_window_pattern=6,
+               threads=8):
+    """Writes a synthetic gemma-embedding GGUF (see eg2_synth_write_gguf)."""
+    cfg = SynthConfig(seed, n_layer, 1 if dense_head else 0, weight_std, embed_std, norm_std, rope_base_full,
+                      rope_base_swa, sliding_window, sliding_window_pattern, threads)
+    err = C.create_string_buffer(512)
+    if lib().eg2_synth_write_gguf(os.fsencode(path), C.byref(cfg), err, 512) != 0:
+        raise HipError("synthetic GGUF: " + err.value.decode())
+
+
+class Gguf:
+    """A GGUF file parsed into the engine's ei_gguf layout."""
+
+    def __init__(self, path):
+        self.g = EiGguf()
+        err = C.create_string_buffer(512)
+        if lib().eg2_gguf_open(os.fsencode(path), C.byref(self.g), err, 512) != 0:
+            raise HipError(err.value.decode())
+
+    def close(self):
+        if self.g is not None:
+            lib().eg2_gguf_close(C.byref(self.g))
+            self.g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Encoder:
+    """ei_gemma2_kfd_create / _batch / _free over a GGUF file."""
+
+    def __init__(self, gguf_path):
+        self.gguf = Gguf(gguf_path)
+        err = C.create_string_buffer(1024)
+        self.ctx = lib().ei_gemma2_kfd_create(C.byref(self.gguf.g), err, 1024)
+        if not self.ctx:
+            raise HipError(err.value.decode())
+
+    def batch(self, ids, offsets):
+        """ids: int32 array of offsets[-1] tokens; offsets: batch+1 sizes.
+        Returns float32 [batch, 768] (numpy)."""
+        import numpy as np
+
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+        batch = len(offsets) - 1
+        out = np.zeros((max(batch, 1), N_EMBD), dtype=np.float32)
+        err = C.create_string_buffer(1024)
+        ok = lib().ei_gemma2_kfd_batch(self.ctx, ids.ctypes.data_as(_i32), offs, batch,
+                                       out.ctypes.data_as(_f), err, 1024)
+        if not ok:
+            raise HipError(err.value.decode())
+        return out[:batch]
+
+    def stage(self, ids, offsets):
+        """Uploads one wave (eg2_kfd_stage); launch()/collect() then run it."""
+        import numpy as np
+
+        self._ids = np.ascontiguousarray(ids, dtype=np.int32)
+        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+        self._batch = len(offsets) - 1
+        err = C.create_string_buffer(1024)
+        if not lib().eg2_kfd_stage(self.ctx, self._ids.ctypes.data_as(_i32), offs, self._batch, err, 1024):
+            raise HipError(err.value.decode())
+
+    def launch(self, repeats=1):
+        err = C.create_string_buffer(1024)
+        if not lib().eg2_kfd_launch_staged(self.ctx, repeats, err, 1024):
+            raise HipError(err.value.decode())
+
+    def collect(self):
+        import numpy as np
+
+        out = np.zeros((self._batch, N_EMBD), dtype=np.float32)
+        err = C.create_string_buffer(1024)
+        if not lib().eg2_kfd_collect(self.ctx, out.ctypes.data_as(_f), err, 1024):
+            raise HipError(err.value.decode())
+        return out
+
+    def close(self):
+        if getattr(self, "ctx", None):
+            lib().ei_gemma2_kfd_free(self.ctx)
+            self.ctx = None
+        if getattr(self, "gguf", None) is not None:
+            self.gguf.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rope_table(base, n_pos=N_CTX):
+    import numpy as np
+
+    t = np.zeros((n_pos, HEAD_DIM), dtype=np.float32)
+    lib().eg2_rope_table(base, n_pos, t.ctypes.data)
+    return t
+
+
+def q8_split(blocks_u8, rows, k):
+    """GGUF Q8_0 bytes -> (int8 [rows, k], float32 [rows, k/32])."""
+    import numpy as np
+
+    src = np.ascontiguousarray(blocks_u8, dtype=np.uint8)
+    q = np.zeros((rows, k), dtype=np.int8)
+    d = np.zeros((rows, k // 32), dtype=np.float32)
+    lib().eg2_q8_split(src.ctypes.data, rows, k, q.ctypes.data, d.ctypes.data)
+    return q, d
+
+
+class ops:
+    """Operator entry points on torch device tensors (current torch stream)."""
+
+    @staticmethod
+    def _stream():
+        import torch
+
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    @staticmethod
+    def _p(t):
+        return C.c_void_p(t.data_ptr()) if t is not None else None
+
+    @classmethod
+    def embed_norm_quant(cls, table, ids, embed_scale, norm_w, eps, x, xq, xd):
+        check(lib().eg2_hip_embed_norm_quant(cls._p(table), cls._p(ids), ids.numel(), embed_scale, cls._p(norm_w),
+                                             eps, cls._p(x), cls._p(xq), cls._p(xd), cls._stream()),
+              "embed_norm_quant")
+
+    @classmethod
+    def residual_norm_quant(cls, x, h, post_w, next_w, eps, xq, xd):
+        check(lib().eg2_hip_residual_norm_quant(cls._p(x), cls._p(h), cls._p(post_w), cls._p(next_w), eps,
+                                                cls._p(xq), cls._p(xd), x.shape[0], cls._stream()),
+              "residual_norm_quant")
+
+    @classmethod
+    def qk_norm_rope(cls, qkv, q_w, k_w, table, pos, eps, qh, kh, vh):
+        check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos), eps,
+                                         cls._p(qh), cls._p(kh), cls._p(vh), qkv.shape[0], cls._stream()),
+              "qk_norm_rope")
+
+    @classmethod
+    def attention(cls, qh, kh, vh, seg_lo, seg_hi, window, cq, cd):
+        check(lib().eg2_hip_attention(cls._p(qh), cls._p(kh), cls._p(vh), cls._p(seg_lo), cls._p(seg_hi), window,
+                                      qh.shape[0], cls._p(cq), cls._p(cd), cls._stream()), "attention")
+
+    @classmethod
+    def gelu_quant(cls, gu, gq, gd):
+        check(lib().eg2_hip_gelu_quant(cls._p(gu), cls._p(gq), cls._p(gd), gu.shape[0], cls._stream()),
+              "gelu_quant")
+
+    @classmethod
+    def quantize_rows(cls, x, q, d):
+        check(lib().eg2_hip_quantize_rows(cls._p(x), x.shape[1], cls._p(q), cls._p(d), x.shape[0], cls._stream()),
+              "quantize_rows")
+
+    @classmethod
+    def rms_norm_rows(cls, x, w, eps):
+        check(lib().eg2_hip_rms_norm_rows(cls._p(x), cls._p(w), eps, x.shape[0], cls._stream()), "rms_norm_rows")
+
+    @classmethod
+    def pool_l2(cls, x, offsets, out):
+        check(lib().eg2_hip_pool_l2(cls._p(x), cls._p(offsets), cls._p(out), out.shape[0], cls._stream()),
+              "pool_l2")
+
+    @classmethod
+    def l2_prefix(cls, x, dims):
+        check(lib().eg2_hip_l2_prefix(cls._p(x), x.shape[1], dims, x.shape[0], cls._stream()), "l2_prefix")
+
+    @classmethod
+    def gemm_q8(cls, xq, xd, wq, wd, y):
+        n, k = xq.shape
+        m = wq.shape[0]
+        check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), cls._p(wq), cls._p(wd), cls._p(y), n, m, k,
+                                    y.shape[1], cls._stream()), "gemm_q8")

@@ -1,0 +1,154 @@
+/*
+ * Operator-level C ABI of the gfx950 kernels behind the executor, plus the
+ * host helpers the executor and its tests share.
+ *
+ * Device entry points take device pointers, unsigned sizes and a HIP stream
+ * (hipStream_t passed as void*, NULL = the null stream). They enqueue work
+ * and return 0 or a hipError_t code (eg2_hip_error_string names it); they
+ * never synchronise. Activations in Q8_0 use a split layout: int8 values
+ * [rows][k] and one float per 32-block [rows][k/32] holding the value of the
+ * block's fp16 scale. fp16 buffers are passed as uint16_t bit patterns.
+ *
+ * Each entry names the reference function whose semantics it implements
+ * (paths relative to vendor/embeddinggemma.c/src/ unless they start with
+ * src/ or kernels/).
+ */
+#ifndef EG2_HIP_H
+#define EG2_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gguf.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ device ops */
+
+/* engine.c:288-295 input_embeddings (x = fp16(d)*sqrt(768)*q from the raw
+ * GGUF Q8_0 table) fused with kernels.c:139-151 ei_rms_norm_quantize_q8_0
+ * (layer-0 attn_norm) into xq/xd. Replaces kernels/eg2.c:36-39 eg2_gather. */
+int eg2_hip_embed_norm_quant(const void *table_q8, const int32_t *ids, unsigned rows, float embed_scale,
+                             const float *norm_w, float eps, float *x, int8_t *xq, float *xd, void *stream);
+
+/* kernels.c:163-188 ei_rms_norm_residual_inplace (x += rms(h)*post_w) then,
+ * when next_w != NULL, kernels.c:139-151 on the updated x. Replaces
+ * kernels/eg2.c:192-202 eg2_norm_residual + the following eg2_norm. */
+int eg2_hip_residual_norm_quant(float *x, const float *h, const float *post_w, const float *next_w, float eps,
+                                int8_t *xq, float *xd, unsigned rows, void *stream);
+
+/* kernels.c:233-264 ei_qk_norm_rope_qk_inplace on rows of the fused
+ * [q 768 | k 256 | v 256] projection; rope_table[pos][0..127] = cos,
+ * [128..255] = sin (eg2_rope_table). Writes fp16 q (x0.0625), k, v.
+ * Replaces kernels/eg2.c:204-217 eg2_norm_rope. */
+int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, const float *rope_table,
+                         const int32_t *pos, float eps, uint16_t *qh, uint16_t *kh, uint16_t *vh, unsigned rows,
+                         void *stream);
+
+/* kernels.c:324-360 ei_attention_mha_range over packed sequences
+ * (engine.c:850-873): token t attends to keys [seg_lo[t], seg_hi[t])
+ * intersected with |t - s| <= window/2 when window > 0; 3 query heads share
+ * one KV head, head_dim 256. The fp32 context is quantized to Q8_0
+ * (quants.c:97-177) into cq/cd. rows % 32 == 0. Replaces
+ * kernels/eg2.c:145-170 eg2_attention256. */
+int eg2_hip_attention(const uint16_t *qh, const uint16_t *kh, const uint16_t *vh, const uint32_t *seg_lo,
+                      const uint32_t *seg_hi, unsigned window, unsigned rows, int8_t *cq, float *cd, void *stream);
+
+/* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
+ * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */
+int eg2_hip_gelu_quant(const float *gate_up, int8_t *gq, float *gd, unsigned rows, void *stream);
+
+/* quants.c:97-177 ei_quantize_row_q8_0 on rows of width k (k % 64 == 0). */
+int eg2_hip_quantize_rows(const float *x, unsigned k, int8_t *q, float *d, unsigned rows, void *stream);
+
+/* kernels.c:158-161 ei_rms_norm_inplace on rows of width 768. */
+int eg2_hip_rms_norm_rows(float *x, const float *w, float eps, unsigned rows, void *stream);
+
+/* kernels.c:417-427 ei_mean_pool_rms_l2 after the per-token RMS
+ * (eg2_hip_rms_norm_rows): mean over [offsets[s], offsets[s+1]) then L2.
+ * Replaces kernels/eg2.c:181-188 eg2_pool + the host L2 of
+ * src/gemma2_kfd.cpp:337-343. */
+int eg2_hip_pool_l2(const float *x, const uint32_t *offsets, float *out, unsigned batch, void *stream);
+
+/* kernels.c:393-407 ei_l2_normalize / ei_embedding_normalize_prefix on the
+ * first `dims` entries of rows of width `width` (dims % 8 == 0). */
+int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, void *stream);
+
+/* y[n][m] (row stride ldy) = Q8_0 activations [n][k] . Q8_0 weights [m][k]^T
+ * on MFMA with fp16-dequantized operands and fp32 accumulation.
+ * Replaces kernels/eg2.c:41-119 eg2_mm* and, numerically, the Q8_0 x Q8_0
+ * dot of gemma2.c:120-141. k % 32 == 0. */
+int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, const int8_t *wq, const float *wd, float *y, unsigned n,
+                    unsigned m, unsigned k, unsigned ldy, void *stream);
+
+/* ------------------------------------------------------------ executor phases
+ * ei_gemma2_kfd_batch (gemma2_kfd.h) is stage + launch_staged(1) + collect.
+ * The phases have no counterpart in the reference; they let a benchmark
+ * time the device-resident forward apart from the host transfers. Same
+ * validation, locking, poisoning and "HIP: ..." error contract as the batch
+ * call. */
+
+/* Validates one wave, uploads its ids and packing metadata, and builds (once
+ * per padded wave size) its hipGraph. */
+bool eg2_kfd_stage(void *ctx, const int32_t *ids, const size_t *offsets, size_t batch, char *err, size_t len);
+/* Enqueues the staged wave's forward `repeats` times (no host copies, no wait). */
+bool eg2_kfd_launch_staged(void *ctx, unsigned repeats, char *err, size_t len);
+/* Waits for the wave and copies its [batch][768] embeddings to out. */
+bool eg2_kfd_collect(void *ctx, float *out, char *err, size_t len);
+
+/* ------------------------------------------------------------ host helpers */
+
+/* Name of a code returned by the device ops. */
+const char *eg2_hip_error_string(int code);
+
+/* 0 when the current HIP device is a gfx950; otherwise -1 and a reason. */
+int eg2_hip_device_check(char *err, size_t len);
+
+/* GGUF Q8_0 rows (34-byte blocks) -> split layout q[rows][k], d[rows][k/32]
+ * (d = exact float value of the fp16 scale, common.h:17-40). */
+void eg2_q8_split(const void *blocks, size_t rows, unsigned k, int8_t *q, float *d);
+
+/* RoPE table for positions 0..n_pos-1: row p = [cos(theta_0..127) |
+ * sin(theta_0..127)], theta_i = p * powf(base, -2i/256), computed with the
+ * host libm exactly as kernels.c:245-249 does per call. */
+void eg2_rope_table(float base, unsigned n_pos, float *table);
+
+/* ------------------------------------------------------------ GGUF files */
+
+/* Parses a GGUF v3 file into the engine's ei_gguf layout (gguf.c:119-196:
+ * same KV normalisation, alignment rules and tensor validation). The file is
+ * mapped read-only. Returns 0, or -1 with a reason in err. */
+int eg2_gguf_open(const char *path, ei_gguf *g, char *err, size_t len);
+void eg2_gguf_close(ei_gguf *g);
+
+/* Synthetic `gemma-embedding` model with the 300M tensor names and shapes
+ * (model.c:61-105) and Q8_0 matrices, for tests and benchmarks (no weights
+ * are available offline). Values come from a counter-based generator
+ * (splitmix64 + Box-Muller, seeded per tensor row) so they do not depend on
+ * the thread count: matrices ~N(0, weight_std) and the embedding table
+ * ~N(0, embed_std), both quantized to Q8_0 with the reference quantizer
+ * rules; norm weights 1 + norm_std*N(0,1). dense_head adds dense_2 {768,
+ * 3072} and dense_3 {3072, 768} (Q8_0). */
+typedef struct {
+    uint64_t seed;
+    unsigned n_layer;
+    unsigned dense_head;
+    float weight_std;
+    float embed_std;
+    float norm_std;
+    float rope_base_full;
+    float rope_base_swa;
+    unsigned sliding_window;
+    unsigned sliding_window_pattern;
+    unsigned threads;
+} eg2_synth_config;
+
+int eg2_synth_write_gguf(const char *path, const eg2_synth_config *cfg, char *err, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

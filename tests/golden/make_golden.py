@@ -1,0 +1,144 @@
+"""Writes tests/golden/reference_vectors.npz: seeded inputs and the outputs of
+the reference's own CPU functions (vendor/embeddinggemma.c/src/quants.c,
+kernels.c and the Q8_0 x Q8_0 `mm` of gemma2.c), compiled from the reference
+tree by oracle/Makefile into oracle/_ref/libref.so.
+
+Run where the reference tree is present:
+    make -C oracle ref && python tests/golden/make_golden.py
+The fixture holds data only (inputs and expected outputs).
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(HERE)), "oracle"))
+from oracle_lib import Q8, fptr, ref, vptr  # noqa: E402
+
+
+def main():
+    r = ref()
+    if r is None:
+        raise SystemExit("oracle/_ref/libref.so is not built (make -C oracle ref)")
+    rng = np.random.default_rng(20260101)
+    out = {}
+
+    # fp16 conversion (quants.c:13-37): specials, ties, subnormals, random.
+    special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.0, 65520.0, 65536.0, 70000.0, 1e-8, 2.98e-8,
+                        2.9802322e-8, 5.96e-8, 6.1e-5, 6.097555e-5, np.inf, -np.inf, np.nan, 0.5 + 2 ** -12,
+                        1.0 + 2 ** -11, 1.0 + 3 * 2 ** -12, 2049.0, 2051.0], dtype=np.float32)
+    rand = (rng.standard_normal(4000) * 10.0 ** rng.integers(-8, 5, 4000)).astype(np.float32)
+    f16_in = np.concatenate([special, rand])
+    out["fp16_in"] = f16_in
+    out["fp16_out"] = np.array([r.ei_fp32_to_fp16(float(v)) for v in f16_in], dtype=np.uint16)
+
+    # Q8_0 quantizer (quants.c:97-177): random scales plus edge rows.
+    x = (rng.standard_normal((48, 64)) * 10.0 ** rng.uniform(-4, 3, (48, 1))).astype(np.float32)
+    x[0] = 0.0
+    x[1, :32] = 0.5
+    x[1, 32:] = np.float32(127.0 / 2)
+    x[2] = np.arange(64, dtype=np.float32) - 31.5
+    x[3, :] = 1e-30
+    qb = np.zeros((48, 2), dtype=Q8)
+    for i in range(48):
+        r.ei_quantize_row_q8_0(fptr(x[i]), vptr(qb[i]), 64)
+    out["quant_in"], out["quant_out"] = x, qb.view(np.uint8).reshape(48, 68)
+
+    # RMSNorm variants on 768-wide rows (kernels.c:139-188).
+    rows = (rng.standard_normal((6, 768)) * rng.uniform(0.1, 30, (6, 1))).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(768)).astype(np.float32)
+    h = (rng.standard_normal((6, 768)) * 2).astype(np.float32)
+    norm = np.zeros_like(rows)
+    nq = np.zeros((6, 24), dtype=Q8)
+    resid = rows.copy()
+    for i in range(6):
+        r.ei_rms_norm(fptr(rows[i]), fptr(w), 768, 1e-6, fptr(norm[i]))
+        r.ei_rms_norm_quantize_q8_0(fptr(rows[i]), fptr(w), 768, 1e-6, vptr(nq[i]))
+        r.ei_rms_norm_residual_inplace(fptr(resid[i]), fptr(h[i]), fptr(w), 768, 1e-6)
+    out.update(norm_x=rows, norm_w=w, norm_h=h, norm_out=norm, norm_q8=nq.view(np.uint8).reshape(6, 816),
+               resid_out=resid)
+
+    # QK-norm + RoPE + q scale (kernels.c:233-264).
+    qw = (1.0 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    kw = (1.0 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    cases = [(0, 10000.0), (1, 10000.0), (127, 10000.0), (2047, 10000.0), (511, 1000000.0), (1500, 1000000.0)]
+    q_in = rng.standard_normal((len(cases), 768)).astype(np.float32)
+    k_in = rng.standard_normal((len(cases), 256)).astype(np.float32)
+    q_out, k_out = q_in.copy(), k_in.copy()
+    for i, (p, base) in enumerate(cases):
+        r.ei_qk_norm_rope_qk_inplace(fptr(q_out[i]), fptr(k_out[i]), fptr(qw), fptr(kw), p, base, 1e-6)
+    out.update(qk_qw=qw, qk_kw=kw, qk_pos=np.array([c[0] for c in cases], np.int32),
+               qk_base=np.array([c[1] for c in cases], np.float32), qk_q_in=q_in, qk_k_in=k_in, qk_q_out=q_out,
+               qk_k_out=k_out)
+
+    # Attention over one sequence, full and windowed (kernels.c:324-360).
+    T = 24
+    aq = (rng.standard_normal((T, 768)) * 0.3).astype(np.float32)
+    ak = rng.standard_normal((T, 256)).astype(np.float32)
+    av = rng.standard_normal((T, 256)).astype(np.float32)
+    scores = np.zeros(4096, np.float32)
+    att = {}
+    for win in (0, 8):
+        ctx = np.zeros((T, 768), np.float32)
+        r.ei_attention_mha_range(fptr(aq), fptr(ak), fptr(av), T, win, 0, T, fptr(ctx), fptr(scores))
+        att[win] = ctx
+    out.update(att_q=aq, att_k=ak, att_v=av, att_full=att[0], att_win8=att[8])
+
+    # GELU (kernels.c:367-371) and GeGLU + Q8_0 (kernels.c:377-391).
+    gx = (rng.standard_normal(2000) * 4).astype(np.float32)
+    out["gelu_in"] = gx
+    out["gelu_out"] = np.array([r.ei_gelu_tanh(float(v)) for v in gx], np.float32)
+    gate = (rng.standard_normal((3, 1152)) * 2).astype(np.float32)
+    up = rng.standard_normal((3, 1152)).astype(np.float32)
+    gq = np.zeros((3, 36), dtype=Q8)
+    for i in range(3):
+        r.ei_gelu_mul_quantize_q8_0(fptr(gate[i]), fptr(up[i]), 1152, vptr(gq[i]))
+    out.update(geglu_gate=gate, geglu_up=up, geglu_q8=gq.view(np.uint8).reshape(3, 36 * 34))
+
+    # L2 and Matryoshka prefixes (kernels.c:393-407), mean pool (:417-427).
+    e = rng.standard_normal((4, 768)).astype(np.float32)
+    pref = np.zeros((4, 4, 768), np.float32)
+    for i in range(4):
+        for j, dims in enumerate((128, 256, 512, 768)):
+            v = e[i].copy()
+            assert r.ei_embedding_normalize_prefix(fptr(v), dims)
+            pref[i, j] = v
+    l2 = e.copy()
+    for i in range(4):
+        r.ei_l2_normalize(fptr(l2[i]), 768)
+    px = (rng.standard_normal((5, 768)) * 3).astype(np.float32)
+    pooled = np.zeros(768, np.float32)
+    r.ei_mean_pool_rms_l2(fptr(px.copy()), 5, fptr(w), 1e-6, fptr(pooled))
+    out.update(l2_in=e, l2_out=l2, prefix_out=pref, pool_x=px, pool_out=pooled)
+
+    # Q8_0 x Q8_0 projection (gemma2.c:142-153: quantize x, block dots).
+    for name, (n, k, m) in {"mm_a": (5, 64, 7), "mm_b": (4, 768, 16)}.items():
+        wf = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
+        wq = np.zeros((m, k // 32), dtype=Q8)
+        for i in range(m):
+            r.ei_quantize_row_q8_0(fptr(wf[i]), vptr(wq[i]), k)
+        xf = rng.standard_normal((n, k)).astype(np.float32)
+        y = np.zeros((n, m), np.float32)
+        r.ref_mm_q8_0(vptr(wq), k, m, fptr(xf), n, fptr(y))
+        out[name + "_w"] = wq.view(np.uint8).reshape(m, k // 32 * 34)
+        out[name + "_x"], out[name + "_y"] = xf, y
+
+    # Embedding rows (engine.c:288-295).
+    tab = np.zeros((4, 24), dtype=Q8)
+    tf = (rng.standard_normal((4, 768)) * 0.05).astype(np.float32)
+    for i in range(4):
+        r.ei_quantize_row_q8_0(fptr(tf[i]), vptr(tab[i]), 768)
+    emb = np.zeros((4, 768), np.float32)
+    for i in range(4):
+        r.ref_embed_row(vptr(tab), 4, i, fptr(emb[i]))
+    out.update(embed_table=tab.view(np.uint8).reshape(4, 816), embed_out=emb)
+
+    path = os.path.join(HERE, "reference_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+"""End-to-end parity of the executor ABI (ei_gemma2_kfd_create/_batch/_free)
+against the CPU oracle, on synthetic Q8_0 gemma-embedding models.
+
+Bar: per embedding cosine >= 0.9999 and max-abs <= 2e-3 against the oracle
+on the same seeded weights and ids (fp32 embeddings)."""
+import os
+
+import numpy as np
+import pytest
+
+import gguf_py
+import oracle_lib as OL
+
+pytestmark = pytest.mark.gpu
+COS_MIN, MAX_ABS = 0.9999, 2e-3
+
+
+def cosines(a, b):
+    return (a * b).sum(1) / np.linalg.norm(a, axis=1) / np.linalg.norm(b, axis=1)
+
+
+@pytest.fixture(scope="module")
+def small_model(eg2, tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("m") / "small.gguf")
+    # Real-model attention pattern: SWA (window 512, base 1e4) except every
+    # 3rd layer full (base 1e6), plus the dense head.
+    eg2.synth_gguf(path, seed=21, n_layer=3, dense_head=True, sliding_window=512, sliding_window_pattern=3,
+                   rope_base_full=1e6, rope_base_swa=1e4, threads=16)
+    return path
+
+
+@pytest.fixture(scope="module")
+def small_encoder(eg2, gpu, small_model):
+    enc = eg2.Encoder(small_model)
+    yield enc
+    enc.close()
+
+
+def run_oracle(path, ids, offsets):
+    return OL.forward(gguf_py.oracle_model(path), ids, np.asarray(offsets, np.uint64), threads=16)
+
+
+@pytest.mark.parametrize("lens", [[5], [1, 1, 1], [37, 3, 100, 1, 64], [700, 300, 1], [2048]])
+def test_small_model_parity(small_encoder, small_model, lens):
+    rng = np.random.default_rng(sum(lens))
+    ids = rng.integers(0, OL.VOCAB, sum(lens)).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    got = small_encoder.batch(ids, offsets)
+    want = run_oracle(small_model, ids, offsets)
+    c = cosines(got, want)
+    print(f"lens={lens} min cos {c.min():.7f} max abs {np.abs(got - want).max():.3e}")
+    assert c.min() >= COS_MIN
+    assert np.abs(got - want).max() <= MAX_ABS
+    assert np.allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+
+
+def test_packing_invariance(small_encoder):
+    rng = np.random.default_rng(3)
+    lens = [10, 200, 33, 1]
+    ids = rng.integers(0, OL.VOCAB, sum(lens)).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    packed = small_encoder.batch(ids, offsets)
+    for s, n in enumerate(lens):
+        solo = small_encoder.batch(ids[offsets[s]:offsets[s + 1]], [0, n])
+        assert cosines(solo, packed[s:s + 1]).min() >= 0.99999
+
+
+def test_repeatable_and_graph_matches_eager(eg2, small_encoder, small_model):
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, OL.VOCAB, 300).astype(np.int32)
+    offsets = [0, 100, 300]
+    a = small_encoder.batch(ids, offsets)
+    b = small_encoder.batch(ids, offsets)
+    assert np.array_equal(a, b)
+    os.environ["EG2_HIP_GRAPH"] = "0"
+    try:
+        eager = eg2.Encoder(small_model)
+        c = eager.batch(ids, offsets)
+        eager.close()
+    finally:
+        del os.environ["EG2_HIP_GRAPH"]
+    assert np.array_equal(a, c)
+
+
+def test_invalid_batches_fail_without_poisoning(eg2, small_encoder):
+    ids = np.zeros(10, np.int32)
+    cases = [([0, 5, 5, 10], "offsets"), ([1, 10], "1..2048"), ([0, 0], "offsets")]
+    for offsets, msg in cases:
+        with pytest.raises(eg2.HipError, match=msg):
+            small_encoder.batch(ids, offsets)
+    with pytest.raises(eg2.HipError, match="out of range"):
+        small_encoder.batch(np.array([0, OL.VOCAB], np.int32), [0, 2])
+    with pytest.raises(eg2.HipError, match="1..2048"):
+        small_encoder.batch(np.zeros(2049, np.int32), [0, 2049])
+    out = small_encoder.batch(ids, [0, 10])  # still usable
+    assert np.isfinite(out).all()
+
+
+def test_env_flags_are_validated(eg2, small_model):
+    os.environ["EG2_HIP_GRAPH"] = "yes"
+    try:
+        with pytest.raises(eg2.HipError, match="EG2_HIP_GRAPH must be 0 or 1"):
+            eg2.Encoder(small_model)
+    finally:
+        del os.environ["EG2_HIP_GRAPH"]
+
+
+@pytest.fixture(scope="module")
+def full_model(eg2, tmp_path_factory):
+    """Config 4: 24 layers, full attention with RoPE base 1e4, dense head."""
+    path = str(tmp_path_factory.mktemp("full") / "full.gguf")
+    eg2.synth_gguf(path, seed=0, n_layer=24, dense_head=True, sliding_window=0, rope_base_full=1e4,
+                   rope_base_swa=1e4, threads=16)
+    return path
+
+
+def test_full_model_16x128_parity(eg2, gpu, full_model):
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, OL.VOCAB, 16 * 128).astype(np.int32)
+    offsets = np.arange(0, 16 * 128 + 1, 128)
+    enc = eg2.Encoder(full_model)
+    try:
+        got = enc.batch(ids, offsets)
+    finally:
+        enc.close()
+    want = run_oracle(full_model, ids, offsets)
+    c = cosines(got, want)
+    print(f"config4 min cos {c.min():.7f} max abs {np.abs(got - want).max():.3e}")
+    assert c.min() >= COS_MIN
+    assert np.abs(got - want).max() <= MAX_ABS
+    # Matryoshka prefixes of the served embedding (kernels.c:398-407).
+    for dims in (128, 256, 512):
+        a, b = got[:, :dims].copy(), want[:, :dims].copy()
+        a /= np.linalg.norm(a, axis=1, keepdims=True)
+        b /= np.linalg.norm(b, axis=1, keepdims=True)
+        assert cosines(a, b).min() >= COS_MIN
