@@ -4,7 +4,8 @@
 // Create (src/gemma2_kfd.cpp:86-155): select the gfx950 device, read the
 // `gemma-embedding` hyper-parameters and tensors from the caller's ei_gguf
 // (model.c:61-105 names, Q8_0 matrices), repack every matrix once into the
-// kernels' split Q8_0 layout (int8 values + one float scale per 32-block),
+// kernels' split Q8_0 layout (the int8 values as exact fp16 integers + one
+// float scale per 32-block),
 // fuse Q|K|V and gate|up into single projections, upload the raw Q8_0
 // embedding table, build the RoPE tables on the host, and allocate a
 // 2048-token workspace.
@@ -59,7 +60,7 @@ bool env_flag(const char* name, bool dflt) {
 }
 
 struct DevMat {
-  int8_t* q = nullptr;
+  _Float16* q = nullptr;
   float* d = nullptr;
   int m = 0, k = 0;
 };
@@ -103,13 +104,13 @@ class Backend {
 
   // Workspace for kCap tokens.
   float *x_, *h_, *qkv_, *gu_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
-  int8_t *xq_, *cq_, *mid_q_;
-  _Float16 *qh_, *kh_, *vh_;
+  _Float16 *xq_, *cq_, *mid_q_;
+  _Float16 *qs_, *ks_, *vs_;
   int32_t *ids_d_, *pos_d_;
-  uint32_t *lo_d_, *hi_d_, *off_d_;
+  uint32_t *tiles_d_, *off_d_;  // tiles_d_: attention query tiles, then their count
   // Pinned staging.
   int32_t *ids_h_, *pos_h_;
-  uint32_t *lo_h_, *hi_h_, *off_h_;
+  uint32_t *tiles_h_, *off_h_;
   float* out_h_;
 
   std::map<unsigned, hipGraphExec_t> graphs_;
@@ -208,7 +209,7 @@ std::vector<uint8_t> Backend::q8_rows(const std::string& name, int k, int m) con
 DevMat Backend::upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k) {
   size_t rows = 0;
   for (auto* p : parts) rows += p->size() / ((size_t)(k / 32) * 34);
-  std::vector<int8_t> q(rows * k);
+  std::vector<uint16_t> q(rows * k);
   std::vector<float> d(rows * (k / 32));
   size_t r0 = 0;
   for (auto* p : parts) {
@@ -219,9 +220,9 @@ DevMat Backend::upload_q8(const std::vector<const std::vector<uint8_t>*>& parts,
   DevMat mat;
   mat.m = (int)rows;
   mat.k = k;
-  mat.q = dalloc<int8_t>(q.size());
+  mat.q = dalloc<_Float16>(q.size());
   mat.d = dalloc<float>(d.size());
-  check(hipMemcpy(mat.q, q.data(), q.size(), hipMemcpyHostToDevice), "upload");
+  check(hipMemcpy(mat.q, q.data(), q.size() * sizeof(uint16_t), hipMemcpyHostToDevice), "upload");
   check(hipMemcpy(mat.d, d.data(), d.size() * sizeof(float), hipMemcpyHostToDevice), "upload");
   return mat;
 }
@@ -319,33 +320,31 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   h_ = dalloc<float>((size_t)kCap * kEmbd);
   qkv_ = dalloc<float>((size_t)kCap * kQKV);
   gu_ = dalloc<float>((size_t)kCap * 2 * kFF);
-  xq_ = dalloc<int8_t>((size_t)kCap * kFF);
+  xq_ = dalloc<_Float16>((size_t)kCap * kFF);
   xd_ = dalloc<float>((size_t)kCap * (kFF / 32));
-  cq_ = dalloc<int8_t>((size_t)kCap * kEmbd);
+  cq_ = dalloc<_Float16>((size_t)kCap * kEmbd);
   cd_ = dalloc<float>((size_t)kCap * (kEmbd / 32));
-  qh_ = dalloc<_Float16>((size_t)kCap * kEmbd);
-  kh_ = dalloc<_Float16>((size_t)kCap * kHeadDim);
-  vh_ = dalloc<_Float16>((size_t)kCap * kHeadDim);
+  qs_ = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
+  ks_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
+  vs_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
   ids_d_ = dalloc<int32_t>(kCap);
   pos_d_ = dalloc<int32_t>(kCap);
-  lo_d_ = dalloc<uint32_t>(kCap);
-  hi_d_ = dalloc<uint32_t>(kCap);
+  tiles_d_ = dalloc<uint32_t>(4 * kCap + 4);
   off_d_ = dalloc<uint32_t>(kCap + 1);
   pooled_ = dalloc<float>((size_t)kCap * kEmbd);
   mid_ = dalloc<float>((size_t)kCap * kDenseFF);
-  mid_q_ = dalloc<int8_t>((size_t)kCap * kDenseFF);
+  mid_q_ = dalloc<_Float16>((size_t)kCap * kDenseFF);
   mid_d_ = dalloc<float>((size_t)kCap * (kDenseFF / 32));
   ids_h_ = halloc<int32_t>(kCap);
   pos_h_ = halloc<int32_t>(kCap);
-  lo_h_ = halloc<uint32_t>(kCap);
-  hi_h_ = halloc<uint32_t>(kCap);
+  tiles_h_ = halloc<uint32_t>(4 * kCap + 4);
   off_h_ = halloc<uint32_t>(kCap + 1);
   out_h_ = halloc<float>((size_t)kCap * kEmbd);
   check(hipDeviceSynchronize(), "upload");
 
   size_t bytes = 0;
-  for (auto& L : layers_) bytes += (size_t)(L.qkv.m + L.o.m + L.gu.m) * kEmbd * 9 / 8 + (size_t)L.down.m * kFF * 9 / 8;
-  std::fprintf(stderr, "HIP: gfx950, %zu layers, Q8_0 layer weights %.1f MiB, embedding table %.1f MiB, cap %u packed tokens%s\n",
+  for (auto& L : layers_) bytes += (size_t)(L.qkv.m + L.o.m + L.gu.m) * kEmbd * 2 + (size_t)L.down.m * kFF * 2;
+  std::fprintf(stderr, "HIP: gfx950, %zu layers, Q8_0 layer weights %.1f MiB (fp16 integers), embedding table %.1f MiB, cap %u packed tokens%s\n",
                layers_.size(), bytes / 1048576.0, emb->n_bytes / 1048576.0, kCap, dense_ ? ", dense head" : "");
 }
 
@@ -374,8 +373,9 @@ void Backend::record_layers(unsigned rows) {
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
     launch("gemm_qkv", eg2::launch_gemm_q8(xq_, xd_, L.qkv.q, L.qkv.d, qkv_, n, L.qkv.m, kEmbd, kQKV, s));
-    launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, eps_, qh_, kh_, vh_, n, s));
-    launch("attention", eg2::launch_attention(qh_, kh_, vh_, lo_d_, hi_d_, L.window, n, cq_, cd_, s));
+    launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, eps_, qs_, ks_, vs_, n, s));
+    launch("attention", eg2::launch_attention(qs_, ks_, vs_, tiles_d_, tiles_d_ + 4 * kCap, (n + 15) / 16, L.window,
+                                              n, cq_, cd_, s));
     launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
     launch("gemm_gate_up", eg2::launch_gemm_q8(xq_, xd_, L.gu.q, L.gu.d, gu_, n, 2 * kFF, kEmbd, 2 * kFF, s));
@@ -431,23 +431,26 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
     for (size_t t = offsets[s]; t < offsets[s + 1]; ++t) {
       ids_h_[t] = ids[t];
       pos_h_[t] = (int32_t)(t - offsets[s]);
-      lo_h_[t] = (uint32_t)offsets[s];
-      hi_h_[t] = (uint32_t)offsets[s + 1];
     }
   for (unsigned t = n; t < rows; ++t) {
     ids_h_[t] = 0;
     pos_h_[t] = (int32_t)(t - n);
-    lo_h_[t] = n;
-    hi_h_[t] = rows;
   }
   for (size_t s = 0; s <= batch; ++s) off_h_[s] = (uint32_t)offsets[s];
+  unsigned n_tiles = eg2::build_attention_tiles(offsets, batch, tiles_h_);
+  if (rows > n) {
+    const size_t pad[2] = {n, rows};
+    n_tiles += eg2::build_attention_tiles(pad, 1, tiles_h_ + 4 * n_tiles);
+  }
+  tiles_h_[4 * kCap] = n_tiles;
 
   poisoned_ = true;  // cleared only when the whole wave completed
   hipStream_t s = stream_;
   check(hipMemcpyAsync(ids_d_, ids_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
   check(hipMemcpyAsync(pos_d_, pos_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
-  check(hipMemcpyAsync(lo_d_, lo_h_, rows * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy bounds");
-  check(hipMemcpyAsync(hi_d_, hi_h_, rows * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy bounds");
+  check(hipMemcpyAsync(tiles_d_, tiles_h_, 4 * n_tiles * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy tiles");
+  check(hipMemcpyAsync(tiles_d_ + 4 * kCap, tiles_h_ + 4 * kCap, sizeof(uint32_t), hipMemcpyHostToDevice, s),
+        "copy tiles");
   check(hipMemcpyAsync(off_d_, off_h_, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy offsets");
   if (use_graph_ && !profile_ && graphs_.find(rows) == graphs_.end()) {
     hipGraph_t graph = nullptr;

@@ -11,10 +11,11 @@ namespace eg2 {
 
 // Normalises the LDS row `row` (kEmbd floats) with weight w and inverse rms
 // `inv` as (x*w)*inv (kernels.c:124-133, SSE2 branch), then quantizes it to
-// Q8_0 blocks in place of the token's activation row (quants.c:97-177).
-// Lane l owns elements l + 64r: its half-wave holds block 2r + l/32.
+// Q8_0 blocks (quants.c:97-177) written as fp16 integers plus one float
+// scale per block. Lane l owns elements l + 64r: its half-wave holds block
+// 2r + l/32.
 __device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w,
-                                                  float inv, int8_t* __restrict__ qs,
+                                                  float inv, _Float16* __restrict__ qs,
                                                   float* __restrict__ qd, int k) {
   const int lane = threadIdx.x & 63;
   for (int r = 0; r < k / 64; ++r) {
@@ -22,7 +23,7 @@ __device__ __forceinline__ void norm_quantize_row(const float* row, const float*
     const float p = row[e] * w[e];
     const float v = p * inv;
     const Q8Lane q = q8_quantize_lane(v);
-    qs[e] = (int8_t)q.q;
+    qs[e] = (_Float16)q.q;
     if ((lane & 31) == 0) qd[e / kQK] = q.d;
   }
 }
@@ -33,7 +34,7 @@ __device__ __forceinline__ void norm_quantize_row(const float* row, const float*
 __global__ void __launch_bounds__(64)
 embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __restrict__ ids,
                         float embed_scale, const float* __restrict__ norm_w, float eps,
-                        float* __restrict__ x, int8_t* __restrict__ xq, float* __restrict__ xd) {
+                        float* __restrict__ x, _Float16* __restrict__ xq, float* __restrict__ xd) {
   __shared__ __align__(16) uint8_t raw[kEmbd / kQK * 34];
   __shared__ float row[kEmbd];
   const int t = blockIdx.x;
@@ -63,7 +64,7 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
 __global__ void __launch_bounds__(64)
 residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h,
                            const float* __restrict__ post_w, const float* __restrict__ next_w,
-                           float eps, int8_t* __restrict__ xq, float* __restrict__ xd) {
+                           float eps, _Float16* __restrict__ xq, float* __restrict__ xd) {
   __shared__ float hrow[kEmbd];
   __shared__ float xrow[kEmbd];
   const int t = blockIdx.x;
@@ -85,23 +86,33 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h,
   norm_quantize_row(xrow, next_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * (kEmbd / kQK), kEmbd);
 }
 
+// Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
+// exact in fp32, so hi + lo carries 22 of the 24 significand bits.
+__device__ __forceinline__ void store_split(_Float16* row, int width, int i, float x) {
+  const _Float16 h = (_Float16)x;
+  row[i] = h;
+  row[width + i] = (_Float16)(x - (float)h);
+}
+
 // kernels.c:233-264 on one token of the fused QKV projection output
 // [q0 q1 q2 | k | v] (fp32, kQKVCols wide): per-head RMS with the weight
 // applied before the inverse, NeoX rotation of pairs (d, d+128) with the
 // host-built cos/sin row of this token's position, Q scaled by 0.0625 after
-// rotation. Writes the fp16 attention operands.
+// rotation. The fp32 results (bit-identical to the reference) are written as
+// split fp16 pairs for the attention kernel, rows [hi | lo]; q is stored
+// times 16 (exact) to keep its low half clear of fp16 subnormals.
 __global__ void __launch_bounds__(64)
 qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w,
                     const float* __restrict__ k_w, const float* __restrict__ rope,
-                    const int32_t* __restrict__ pos, float eps, _Float16* __restrict__ qh,
-                    _Float16* __restrict__ kh, _Float16* __restrict__ vh) {
+                    const int32_t* __restrict__ pos, float eps, _Float16* __restrict__ qs,
+                    _Float16* __restrict__ ks, _Float16* __restrict__ vs) {
   __shared__ float rows[4][kHeadDim];
   __shared__ float inv[4];
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const float* src = qkv + (size_t)t * kQKVCols;
   for (int i = lane; i < 4 * kHeadDim; i += 64) rows[i / kHeadDim][i % kHeadDim] = src[i];
-  for (int i = lane; i < kHeadDim; i += 64) vh[(size_t)t * kHeadDim + i] = (_Float16)src[4 * kHeadDim + i];
+  for (int i = lane; i < kHeadDim; i += 64) store_split(vs + (size_t)t * 2 * kHeadDim, kHeadDim, i, src[4 * kHeadDim + i]);
   __syncthreads();
   for (int hd = 0; hd < 4; ++hd) {
     const float ss = sum_squares_sse2(rows[hd], kHeadDim);
@@ -122,11 +133,13 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
     if (hd < kHeads) {
       lo = lo * 0.0625f;
       hi = hi * 0.0625f;
-      qh[(size_t)t * kEmbd + hd * kHeadDim + d] = (_Float16)lo;
-      qh[(size_t)t * kEmbd + hd * kHeadDim + d + half] = (_Float16)hi;
+      _Float16* row = qs + (size_t)t * 2 * kEmbd;
+      store_split(row, kEmbd, hd * kHeadDim + d, lo * 16.0f);
+      store_split(row, kEmbd, hd * kHeadDim + d + half, hi * 16.0f);
     } else {
-      kh[(size_t)t * kHeadDim + d] = (_Float16)lo;
-      kh[(size_t)t * kHeadDim + d + half] = (_Float16)hi;
+      _Float16* row = ks + (size_t)t * 2 * kHeadDim;
+      store_split(row, kHeadDim, d, lo);
+      store_split(row, kHeadDim, d + half, hi);
     }
   }
 }
@@ -134,7 +147,7 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
 // kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0.
 // gu rows hold [gate 0..1151 | up 0..1151].
 __global__ void __launch_bounds__(64)
-gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* __restrict__ gd) {
+gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float* __restrict__ gd) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const float* g = gu + (size_t)t * (2 * kFF);
@@ -148,20 +161,20 @@ gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* 
     const float gelu = 0.5f * x * (1.0f + tanhf(inner));
     const float v = gelu * u[e];
     const Q8Lane q = q8_quantize_lane(v);
-    gq[(size_t)t * kFF + e] = (int8_t)q.q;
+    gq[(size_t)t * kFF + e] = (_Float16)q.q;
     if ((lane & 31) == 0) gd[(size_t)t * (kFF / kQK) + e / kQK] = q.d;
   }
 }
 
 // quants.c:97-177 on rows of width k (k % 64 == 0).
 __global__ void __launch_bounds__(64)
-quantize_rows_kernel(const float* __restrict__ x, int k, int8_t* __restrict__ q,
+quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ q,
                      float* __restrict__ d) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   for (int e = lane; e < k; e += 64) {
     const Q8Lane r = q8_quantize_lane(x[(size_t)t * k + e]);
-    q[(size_t)t * k + e] = (int8_t)r.q;
+    q[(size_t)t * k + e] = (_Float16)r.q;
     if ((lane & 31) == 0) d[(size_t)t * (k / kQK) + e / kQK] = r.d;
   }
 }
@@ -225,7 +238,7 @@ l2_prefix_kernel(float* __restrict__ x, int width, int dims) {
 // ---------------------------------------------------------------- launchers
 
 hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int rows, float embed_scale,
-                                   const float* norm_w, float eps, float* x, int8_t* xq, float* xd,
+                                   const float* norm_w, float eps, float* x, _Float16* xq, float* xd,
                                    hipStream_t st) {
   hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(rows), dim3(64), 0, st, table, ids, embed_scale, norm_w,
                      eps, x, xq, xd);
@@ -233,26 +246,26 @@ hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int
 }
 
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
-                                      float eps, int8_t* xq, float* xd, int rows, hipStream_t st) {
+                                      float eps, _Float16* xq, float* xd, int rows, hipStream_t st) {
   hipLaunchKernelGGL(residual_norm_quant_kernel, dim3(rows), dim3(64), 0, st, x, h, post_w, next_w, eps, xq,
                      xd);
   return hipGetLastError();
 }
 
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
-                               const int32_t* pos, float eps, _Float16* qh, _Float16* kh, _Float16* vh,
+                               const int32_t* pos, float eps, _Float16* qs, _Float16* ks, _Float16* vs,
                                int rows, hipStream_t st) {
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, qh, kh,
-                     vh);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, qs, ks,
+                     vs);
   return hipGetLastError();
 }
 
-hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, hipStream_t st) {
+hipError_t launch_gelu_quant(const float* gu, _Float16* gq, float* gd, int rows, hipStream_t st) {
   hipLaunchKernelGGL(gelu_quant_kernel, dim3(rows), dim3(64), 0, st, gu, gq, gd);
   return hipGetLastError();
 }
 
-hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st) {
+hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, int rows, hipStream_t st) {
   hipLaunchKernelGGL(quantize_rows_kernel, dim3(rows), dim3(64), 0, st, x, k, q, d);
   return hipGetLastError();
 }

@@ -11,6 +11,19 @@
 
 namespace {
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+_Float16* h16(uint16_t* p) { return reinterpret_cast<_Float16*>(p); }
+const _Float16* h16(const uint16_t* p) { return reinterpret_cast<const _Float16*>(p); }
+
+// IEEE fp16 bit pattern of an int8 value (exact: |q| <= 128 < 2^11).
+uint16_t int8_to_fp16_bits(int8_t q) {
+  if (q == 0) return 0;
+  const uint32_t sign = q < 0 ? 0x8000u : 0u;
+  uint32_t mag = (uint32_t)(q < 0 ? -(int)q : (int)q);
+  int e = 0;
+  while ((mag >> e) > 1) ++e;  // mag in [2^e, 2^(e+1))
+  const uint32_t mant = (mag << (10 - e)) & 0x3FFu;
+  return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | mant);
+}
 int code(hipError_t e) { return (int)e; }
 constexpr int kInvalid = (int)hipErrorInvalidValue;
 
@@ -45,45 +58,50 @@ float fp16_to_fp32_host(uint16_t h) {
 extern "C" {
 
 int eg2_hip_embed_norm_quant(const void* table_q8, const int32_t* ids, unsigned rows, float embed_scale,
-                             const float* norm_w, float eps, float* x, int8_t* xq, float* xd, void* stream) {
+                             const float* norm_w, float eps, float* x, uint16_t* xq, float* xd, void* stream) {
   if (!table_q8 || !ids || !norm_w || !x || !xq || !xd || rows == 0) return kInvalid;
   return code(eg2::launch_embed_norm_quant(static_cast<const uint8_t*>(table_q8), ids, (int)rows, embed_scale,
-                                           norm_w, eps, x, xq, xd, as_stream(stream)));
+                                           norm_w, eps, x, h16(xq), xd, as_stream(stream)));
 }
 
 int eg2_hip_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w, float eps,
-                                int8_t* xq, float* xd, unsigned rows, void* stream) {
+                                uint16_t* xq, float* xd, unsigned rows, void* stream) {
   if (!x || !h || !post_w || rows == 0 || (next_w && (!xq || !xd))) return kInvalid;
-  return code(eg2::launch_residual_norm_quant(x, h, post_w, next_w, eps, xq, xd, (int)rows, as_stream(stream)));
+  return code(
+      eg2::launch_residual_norm_quant(x, h, post_w, next_w, eps, h16(xq), xd, (int)rows, as_stream(stream)));
 }
 
 int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope_table,
-                         const int32_t* pos, float eps, uint16_t* qh, uint16_t* kh, uint16_t* vh, unsigned rows,
+                         const int32_t* pos, float eps, uint16_t* qs, uint16_t* ks, uint16_t* vs, unsigned rows,
                          void* stream) {
-  if (!qkv || !q_w || !k_w || !rope_table || !pos || !qh || !kh || !vh || rows == 0) return kInvalid;
-  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, eps, reinterpret_cast<_Float16*>(qh),
-                                       reinterpret_cast<_Float16*>(kh), reinterpret_cast<_Float16*>(vh),
-                                       (int)rows, as_stream(stream)));
+  if (!qkv || !q_w || !k_w || !rope_table || !pos || !qs || !ks || !vs || rows == 0) return kInvalid;
+  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, eps, h16(qs), h16(ks), h16(vs), (int)rows,
+                                       as_stream(stream)));
 }
 
-int eg2_hip_attention(const uint16_t* qh, const uint16_t* kh, const uint16_t* vh, const uint32_t* seg_lo,
-                      const uint32_t* seg_hi, unsigned window, unsigned rows, int8_t* cq, float* cd, void* stream) {
-  if (!qh || !kh || !vh || !seg_lo || !seg_hi || !cq || !cd || rows == 0 || rows % 32 != 0 ||
+int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vs, const uint32_t* tiles,
+                      const uint32_t* tile_count, unsigned grid, unsigned window, unsigned rows, uint16_t* cq,
+                      float* cd, void* stream) {
+  if (!qs || !ks || !vs || !tiles || !tile_count || !cq || !cd || rows == 0 || grid == 0 || grid > 65536 ||
       window > 4096u)
     return kInvalid;
-  return code(eg2::launch_attention(reinterpret_cast<const _Float16*>(qh), reinterpret_cast<const _Float16*>(kh),
-                                    reinterpret_cast<const _Float16*>(vh), seg_lo, seg_hi, (int)window, (int)rows,
-                                    cq, cd, as_stream(stream)));
+  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vs), tiles, tile_count, (int)grid, (int)window, (int)rows,
+                                    h16(cq), cd, as_stream(stream)));
 }
 
-int eg2_hip_gelu_quant(const float* gate_up, int8_t* gq, float* gd, unsigned rows, void* stream) {
+unsigned eg2_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
+  if (!offsets || !tiles) return 0;
+  return eg2::build_attention_tiles(offsets, batch, tiles);
+}
+
+int eg2_hip_gelu_quant(const float* gate_up, uint16_t* gq, float* gd, unsigned rows, void* stream) {
   if (!gate_up || !gq || !gd || rows == 0) return kInvalid;
-  return code(eg2::launch_gelu_quant(gate_up, gq, gd, (int)rows, as_stream(stream)));
+  return code(eg2::launch_gelu_quant(gate_up, h16(gq), gd, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_quantize_rows(const float* x, unsigned k, int8_t* q, float* d, unsigned rows, void* stream) {
+int eg2_hip_quantize_rows(const float* x, unsigned k, uint16_t* q, float* d, unsigned rows, void* stream) {
   if (!x || !q || !d || rows == 0 || k == 0 || k % 64 != 0) return kInvalid;
-  return code(eg2::launch_quantize_rows(x, (int)k, q, d, (int)rows, as_stream(stream)));
+  return code(eg2::launch_quantize_rows(x, (int)k, h16(q), d, (int)rows, as_stream(stream)));
 }
 
 int eg2_hip_rms_norm_rows(float* x, const float* w, float eps, unsigned rows, void* stream) {
@@ -101,10 +119,10 @@ int eg2_hip_l2_prefix(float* x, unsigned width, unsigned dims, unsigned rows, vo
   return code(eg2::launch_l2_prefix(x, (int)width, (int)dims, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_gemm_q8(const int8_t* xq, const float* xd, const int8_t* wq, const float* wd, float* y, unsigned n,
-                    unsigned m, unsigned k, unsigned ldy, void* stream) {
+int eg2_hip_gemm_q8(const uint16_t* xq, const float* xd, const uint16_t* wq, const float* wd, float* y,
+                    unsigned n, unsigned m, unsigned k, unsigned ldy, void* stream) {
   if (!xq || !xd || !wq || !wd || !y || n == 0 || m == 0 || k == 0 || k % 32 != 0 || ldy < m) return kInvalid;
-  return code(eg2::launch_gemm_q8(xq, xd, wq, wd, y, (int)n, (int)m, (int)k, (int)ldy, as_stream(stream)));
+  return code(eg2::launch_gemm_q8(h16(xq), xd, h16(wq), wd, y, (int)n, (int)m, (int)k, (int)ldy, as_stream(stream)));
 }
 
 const char* eg2_hip_error_string(int c) { return hipGetErrorString((hipError_t)c); }
@@ -128,14 +146,14 @@ int eg2_hip_device_check(char* err, size_t len) {
   return 0;
 }
 
-void eg2_q8_split(const void* blocks, size_t rows, unsigned k, int8_t* q, float* d) {
+void eg2_q8_split(const void* blocks, size_t rows, unsigned k, uint16_t* q, float* d) {
   const uint8_t* src = static_cast<const uint8_t*>(blocks);
   const size_t nb = k / 32;
   for (size_t r = 0; r < rows; ++r)
     for (size_t b = 0; b < nb; ++b) {
       const uint8_t* blk = src + (r * nb + b) * 34;
       d[r * nb + b] = fp16_to_fp32_host((uint16_t)(blk[0] | (blk[1] << 8)));
-      std::memcpy(q + r * k + b * 32, blk + 2, 32);
+      for (int i = 0; i < 32; ++i) q[r * k + b * 32 + i] = int8_to_fp16_bits((int8_t)blk[2 + i]);
     }
 }
 

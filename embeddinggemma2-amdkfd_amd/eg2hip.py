@@ -59,7 +59,8 @@ SIGNATURES = {
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _vp, _vp, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
+    "eg2_attention_tiles": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
@@ -215,11 +216,11 @@ def rope_table(base, n_pos=N_CTX):
 
 
 def q8_split(blocks_u8, rows, k):
-    """GGUF Q8_0 bytes -> (int8 [rows, k], float32 [rows, k/32])."""
+    """GGUF Q8_0 bytes -> (fp16 integer values [rows, k], float32 scales [rows, k/32])."""
     import numpy as np
 
     src = np.ascontiguousarray(blocks_u8, dtype=np.uint8)
-    q = np.zeros((rows, k), dtype=np.int8)
+    q = np.zeros((rows, k), dtype=np.float16)
     d = np.zeros((rows, k // 32), dtype=np.float32)
     lib().eg2_q8_split(src.ctypes.data, rows, k, q.ctypes.data, d.ctypes.data)
     return q, d
@@ -257,9 +258,21 @@ class ops:
               "qk_norm_rope")
 
     @classmethod
-    def attention(cls, qh, kh, vh, seg_lo, seg_hi, window, cq, cd):
-        check(lib().eg2_hip_attention(cls._p(qh), cls._p(kh), cls._p(vh), cls._p(seg_lo), cls._p(seg_hi), window,
-                                      qh.shape[0], cls._p(cq), cls._p(cd), cls._stream()), "attention")
+    def attention(cls, qs, ks, vs, offsets, window, cq, cd):
+        """Packed attention over sequences [offsets[s], offsets[s+1])."""
+        import numpy as np
+        import torch
+
+        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+        tiles = np.zeros(4 * int(offsets[-1]) + 4, dtype=np.uint32)
+        n = lib().eg2_attention_tiles(offs, len(offsets) - 1, tiles.ctypes.data)
+        tiles[-1] = n
+        dev = torch.from_numpy(tiles.view(np.int32)).to(qs.device)
+        grid = max(1, (qs.shape[0] + 15) // 16)
+        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vs), cls._p(dev),
+                                      C.c_void_p(dev.data_ptr() + 4 * (len(tiles) - 1)), grid, window, qs.shape[0],
+                                      cls._p(cq), cls._p(cd), cls._stream()), "attention")
+        torch.cuda.current_stream().synchronize()  # keeps `dev` alive until the kernel ran
 
     @classmethod
     def gelu_quant(cls, gu, gq, gd):

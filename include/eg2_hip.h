@@ -5,9 +5,12 @@
  * Device entry points take device pointers, unsigned sizes and a HIP stream
  * (hipStream_t passed as void*, NULL = the null stream). They enqueue work
  * and return 0 or a hipError_t code (eg2_hip_error_string names it); they
- * never synchronise. Activations in Q8_0 use a split layout: int8 values
- * [rows][k] and one float per 32-block [rows][k/32] holding the value of the
- * block's fp16 scale. fp16 buffers are passed as uint16_t bit patterns.
+ * never synchronise. Q8_0 operands (activations and weights) use a split
+ * layout: the int8 values stored as fp16 integers [rows][k] (exact) and one
+ * float per 32-block [rows][k/32] holding the value of the block's fp16
+ * scale. fp16 buffers are passed as uint16_t bit patterns. The attention
+ * operands are fp32 values split into fp16 pairs, rows [hi | lo] with
+ * hi = fp16(x), lo = fp16(x - hi).
  *
  * Each entry names the reference function whose semantics it implements
  * (paths relative to vendor/embeddinggemma.c/src/ unless they start with
@@ -32,37 +35,49 @@ extern "C" {
  * GGUF Q8_0 table) fused with kernels.c:139-151 ei_rms_norm_quantize_q8_0
  * (layer-0 attn_norm) into xq/xd. Replaces kernels/eg2.c:36-39 eg2_gather. */
 int eg2_hip_embed_norm_quant(const void *table_q8, const int32_t *ids, unsigned rows, float embed_scale,
-                             const float *norm_w, float eps, float *x, int8_t *xq, float *xd, void *stream);
+                             const float *norm_w, float eps, float *x, uint16_t *xq, float *xd, void *stream);
 
 /* kernels.c:163-188 ei_rms_norm_residual_inplace (x += rms(h)*post_w) then,
  * when next_w != NULL, kernels.c:139-151 on the updated x. Replaces
  * kernels/eg2.c:192-202 eg2_norm_residual + the following eg2_norm. */
 int eg2_hip_residual_norm_quant(float *x, const float *h, const float *post_w, const float *next_w, float eps,
-                                int8_t *xq, float *xd, unsigned rows, void *stream);
+                                uint16_t *xq, float *xd, unsigned rows, void *stream);
 
 /* kernels.c:233-264 ei_qk_norm_rope_qk_inplace on rows of the fused
  * [q 768 | k 256 | v 256] projection; rope_table[pos][0..127] = cos,
- * [128..255] = sin (eg2_rope_table). Writes fp16 q (x0.0625), k, v.
+ * [128..255] = sin (eg2_rope_table). The fp32 results are written as split
+ * fp16 rows: qs [rows][2][768] holding 16*q (q includes the 0.0625 scale),
+ * ks [rows][2][256], vs [rows][2][256] (v unchanged).
  * Replaces kernels/eg2.c:204-217 eg2_norm_rope. */
 int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, const float *rope_table,
-                         const int32_t *pos, float eps, uint16_t *qh, uint16_t *kh, uint16_t *vh, unsigned rows,
+                         const int32_t *pos, float eps, uint16_t *qs, uint16_t *ks, uint16_t *vs, unsigned rows,
                          void *stream);
 
 /* kernels.c:324-360 ei_attention_mha_range over packed sequences
- * (engine.c:850-873): token t attends to keys [seg_lo[t], seg_hi[t])
- * intersected with |t - s| <= window/2 when window > 0; 3 query heads share
- * one KV head, head_dim 256. The fp32 context is quantized to Q8_0
- * (quants.c:97-177) into cq/cd. rows % 32 == 0. Replaces
- * kernels/eg2.c:145-170 eg2_attention256. */
-int eg2_hip_attention(const uint16_t *qh, const uint16_t *kh, const uint16_t *vh, const uint32_t *seg_lo,
-                      const uint32_t *seg_hi, unsigned window, unsigned rows, int8_t *cq, float *cd, void *stream);
+ * (engine.c:850-873): each token attends to the keys of its own sequence,
+ * limited to |t - s| <= window/2 when window > 0; 3 query heads share one KV
+ * head, head_dim 256. Inputs are the split rows of eg2_hip_qk_norm_rope.
+ * The work list `tiles` (device, 4 uint32 per tile, from
+ * eg2_attention_tiles) holds *tile_count (device) query tiles; `grid`
+ * workgroups stride over it. The fp32 context is quantized to Q8_0
+ * (quants.c:97-177) into cq/cd. A sequence's result does not depend on its
+ * place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
+int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vs, const uint32_t *tiles,
+                      const uint32_t *tile_count, unsigned grid, unsigned window, unsigned rows, uint16_t *cq,
+                      float *cd, void *stream);
+
+/* Host: the query-tile list of a packed wave with sequences
+ * [offsets[s], offsets[s+1]) -- up to 32 queries of one sequence per tile as
+ * {first query, end, sequence start, sequence end}. `tiles` must hold
+ * 4 * offsets[batch] entries; returns the tile count. */
+unsigned eg2_attention_tiles(const size_t *offsets, size_t batch, uint32_t *tiles);
 
 /* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
  * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */
-int eg2_hip_gelu_quant(const float *gate_up, int8_t *gq, float *gd, unsigned rows, void *stream);
+int eg2_hip_gelu_quant(const float *gate_up, uint16_t *gq, float *gd, unsigned rows, void *stream);
 
 /* quants.c:97-177 ei_quantize_row_q8_0 on rows of width k (k % 64 == 0). */
-int eg2_hip_quantize_rows(const float *x, unsigned k, int8_t *q, float *d, unsigned rows, void *stream);
+int eg2_hip_quantize_rows(const float *x, unsigned k, uint16_t *q, float *d, unsigned rows, void *stream);
 
 /* kernels.c:158-161 ei_rms_norm_inplace on rows of width 768. */
 int eg2_hip_rms_norm_rows(float *x, const float *w, float eps, unsigned rows, void *stream);
@@ -78,10 +93,11 @@ int eg2_hip_pool_l2(const float *x, const uint32_t *offsets, float *out, unsigne
 int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, void *stream);
 
 /* y[n][m] (row stride ldy) = Q8_0 activations [n][k] . Q8_0 weights [m][k]^T
- * on MFMA with fp16-dequantized operands and fp32 accumulation.
- * Replaces kernels/eg2.c:41-119 eg2_mm* and, numerically, the Q8_0 x Q8_0
- * dot of gemma2.c:120-141. k % 32 == 0. */
-int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, const int8_t *wq, const float *wd, float *y, unsigned n,
+ * with the reference's arithmetic (gemma2.c:120-141): exact integer block
+ * dots on MFMA, each scaled ((float)dot * d_w) * d_x and summed in block
+ * order in fp32 -- bit-identical to the CPU path. Replaces
+ * kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0. */
+int eg2_hip_gemm_q8(const uint16_t *xq, const float *xd, const uint16_t *wq, const float *wd, float *y, unsigned n,
                     unsigned m, unsigned k, unsigned ldy, void *stream);
 
 /* ------------------------------------------------------------ executor phases
@@ -107,9 +123,10 @@ const char *eg2_hip_error_string(int code);
 /* 0 when the current HIP device is a gfx950; otherwise -1 and a reason. */
 int eg2_hip_device_check(char *err, size_t len);
 
-/* GGUF Q8_0 rows (34-byte blocks) -> split layout q[rows][k], d[rows][k/32]
- * (d = exact float value of the fp16 scale, common.h:17-40). */
-void eg2_q8_split(const void *blocks, size_t rows, unsigned k, int8_t *q, float *d);
+/* GGUF Q8_0 rows (34-byte blocks) -> split layout: q[rows][k] as fp16
+ * integer bit patterns, d[rows][k/32] the exact float value of each fp16
+ * scale (common.h:17-40). */
+void eg2_q8_split(const void *blocks, size_t rows, unsigned k, uint16_t *q, float *d);
 
 /* RoPE table for positions 0..n_pos-1: row p = [cos(theta_0..127) |
  * sin(theta_0..127)], theta_i = p * powf(base, -2i/256), computed with the

@@ -62,7 +62,10 @@ def test_packing_invariance(small_encoder):
     packed = small_encoder.batch(ids, offsets)
     for s, n in enumerate(lens):
         solo = small_encoder.batch(ids[offsets[s]:offsets[s + 1]], [0, n])
-        assert cosines(solo, packed[s:s + 1]).min() >= 0.99999
+        # Every kernel's result for a sequence is independent of the others
+        # in the wave (row-wise GEMMs and norms, sequence-aligned attention
+        # tiles), so packing does not change a single bit.
+        assert np.array_equal(solo[0], packed[s])
 
 
 def test_repeatable_and_graph_matches_eager(eg2, small_encoder, small_model):

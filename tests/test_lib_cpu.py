@@ -59,12 +59,28 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, p, p, p, 4, 4, 33, 4, None) == inval  # k % 32
     assert lib.eg2_hip_gemm_q8(p, p, p, p, p, 4, 8, 32, 4, None) == inval  # ldy < m
     assert lib.eg2_hip_gemm_q8(None, p, p, p, p, 4, 4, 32, 4, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, p, p, 0, 33, p, p, None) == inval  # rows % 32
-    assert lib.eg2_hip_attention(p, p, p, p, p, 99999, 32, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, p, p, 4, 99999, 32, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, None, p, 4, 0, 32, p, p, None) == inval
     assert lib.eg2_hip_quantize_rows(p, 96, p, p, 1, None) == inval  # k % 64
     assert lib.eg2_hip_l2_prefix(p, 768, 769, 1, None) == inval
     assert lib.eg2_hip_l2_prefix(p, 768, 100, 1, None) == inval
     assert lib.eg2_hip_pool_l2(p, p, p, 0, None) == inval
+
+
+def test_attention_tiles_cover_each_sequence(eg2):
+    offs = [0, 1, 33, 97, 98, 200]
+    arr = (C.c_size_t * len(offs))(*offs)
+    tiles = np.zeros(4 * 200, np.uint32)
+    n = eg2.lib().eg2_attention_tiles(arr, len(offs) - 1, tiles.ctypes.data)
+    t = tiles[:4 * n].reshape(n, 4)
+    covered = np.zeros(200, int)
+    for q0, q1, lo, hi in t:
+        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0
+        assert [lo, hi] in [[offs[s], offs[s + 1]] for s in range(len(offs) - 1)]
+        covered[q0:q1] += 1
+    assert (covered == 1).all()
+    assert n == sum((offs[s + 1] - offs[s] + 31) // 32 for s in range(len(offs) - 1))
 
 
 @pytest.mark.parametrize("base", [10000.0, 1000000.0])
@@ -82,8 +98,10 @@ def test_rope_table_matches_oracle(eg2, base):
 def test_q8_split_is_the_exact_decode(eg2):
     rng = np.random.default_rng(0)
     blocks = quantize_q8_0((rng.standard_normal((10, 96)) * 10.0 ** rng.uniform(-6, 2, (10, 1))).astype(np.float32))
+    blocks[0, 0]["qs"][:4] = [-128, 127, 0, -1]
     q, d = eg2.q8_split(blocks.view(np.uint8), 10, 96)
-    assert np.array_equal(q.reshape(10, 3, 32), blocks["qs"])
+    assert q.dtype == np.float16
+    assert np.array_equal(q.reshape(10, 3, 32).astype(np.int32), blocks["qs"].astype(np.int32))
     assert np.array_equal(d, blocks["d"].view(np.float16).astype(np.float32))
     deq = (q.reshape(10, 3, 32).astype(np.float32) * d[:, :, None]).reshape(10, 96)
     assert np.array_equal(deq, dequantize_q8_0(blocks))
