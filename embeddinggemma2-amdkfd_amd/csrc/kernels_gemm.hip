@@ -25,10 +25,17 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 32;              // one Q8_0 block per k-step
 constexpr int kLdsStride = kBK + 8;  // fp16 elements per LDS row (padding against bank conflicts)
+constexpr int kXcds = 8;             // MI355X: 8 XCDs of 32 CUs, each with its own L2
 
 // BN x BM output tile per workgroup of WN x WM waves; each wave owns a
 // (BN/WN) x (BM/WM) sub-tile of 32x32 MFMA tiles. k % 32 == 0.
-template <int BN, int BM, int WN, int WM>
+//
+// K loop: operands of a 32-block travel HBM/L2 -> registers -> LDS (double
+// buffered) -> MFMA. With a 2048-token wave there are too few waves per CU
+// to hide memory latency, so each thread keeps DEPTH blocks of loads in
+// flight in a register ring; the loop is unrolled by DEPTH so ring slots are
+// compile-time registers.
+template <int BN, int BM, int WN, int WM, int DEPTH>
 __global__ void __launch_bounds__(WN * WM * 64)
 gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
                const _Float16* __restrict__ wq, const float* __restrict__ wd,
@@ -44,43 +51,54 @@ gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave / WM, wm = wave % WM;
-  const int n0 = blockIdx.y * BN, m0 = blockIdx.x * BM;
+  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs,
+  // so workgroup b runs on XCD b % 8. Renumbering gives each XCD one
+  // contiguous run of tiles in column-block-major order, i.e. a slice of
+  // the weight columns plus the activations, which stay in that XCD's L2.
+  const int n_tiles_n = (n + BN - 1) / BN, n_tiles = n_tiles_n * ((m + BM - 1) / BM);
+  const int per_xcd = (n_tiles + kXcds - 1) / kXcds;
+  const int tile = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+  if (tile >= n_tiles) return;
+  const int n0 = (tile % n_tiles_n) * BN, m0 = (tile / n_tiles_n) * BM;
   const int nb = k / kBK;
 
-  half8 ra[A_LOADS], rb[B_LOADS];
-  float sa[A_LOADS], sb[B_LOADS];
+  struct Stage {
+    half8 a[A_LOADS], b[B_LOADS];
+    float sa[A_LOADS], sb[B_LOADS];
+  };
+  Stage ring[DEPTH];
 
-  auto load = [&](int kb) {
+  // Rows past n (or m) load the last valid row instead: always in bounds,
+  // never stored, and free of per-lane branches.
+  auto load = [&](Stage& st, int kb) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + i * NT, row = idx >> 2, part = idx & 3, g = n0 + row;
-      const bool ok = idx < 4 * BN && g < n;
-      ra[i] = ok ? *reinterpret_cast<const half8*>(xq + (size_t)g * k + kb * kBK + part * 8) : half8{};
-      sa[i] = ok ? xd[(size_t)g * nb + kb] : 0.0f;
+      const int idx = tid + i * NT, row = (idx >> 2) % BN, part = idx & 3, g = min(n0 + row, n - 1);
+      st.a[i] = *reinterpret_cast<const half8*>(xq + (size_t)g * k + kb * kBK + part * 8);
+      st.sa[i] = xd[(size_t)g * nb + kb];
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + i * NT, row = idx >> 2, part = idx & 3, g = m0 + row;
-      const bool ok = idx < 4 * BM && g < m;
-      rb[i] = ok ? *reinterpret_cast<const half8*>(wq + (size_t)g * k + kb * kBK + part * 8) : half8{};
-      sb[i] = ok ? wd[(size_t)g * nb + kb] : 0.0f;
+      const int idx = tid + i * NT, row = (idx >> 2) % BM, part = idx & 3, g = min(m0 + row, m - 1);
+      st.b[i] = *reinterpret_cast<const half8*>(wq + (size_t)g * k + kb * kBK + part * 8);
+      st.sb[i] = wd[(size_t)g * nb + kb];
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](const Stage& st, int buf) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
       const int idx = tid + i * NT;
       if (idx < 4 * BN) {
-        *reinterpret_cast<half8*>(&As[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = ra[i];
-        if ((idx & 3) == 0) Ad[buf][idx >> 2] = sa[i];
+        *reinterpret_cast<half8*>(&As[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = st.a[i];
+        if ((idx & 3) == 0) Ad[buf][idx >> 2] = st.sa[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
       const int idx = tid + i * NT;
       if (idx < 4 * BM) {
-        *reinterpret_cast<half8*>(&Bs[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = rb[i];
-        if ((idx & 3) == 0) Bd[buf][idx >> 2] = sb[i];
+        *reinterpret_cast<half8*>(&Bs[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = st.b[i];
+        if ((idx & 3) == 0) Bd[buf][idx >> 2] = st.sb[i];
       }
     }
   };
@@ -91,13 +109,8 @@ gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
 #pragma unroll
     for (int b = 0; b < TM; ++b) acc[a][b] = floatx16{};
 
-  load(0);
-  store(0);
-  __syncthreads();
   const int g = lane >> 5, r32 = lane & 31;
-  for (int kb = 0; kb < nb; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nb) load(kb + 1);
+  auto compute = [&](int cur) {
     half8 af[TN][2], bf[TM][2];
 #pragma unroll
     for (int a = 0; a < TN; ++a)
@@ -112,6 +125,15 @@ gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
     float dw[TM];
 #pragma unroll
     for (int b = 0; b < TM; ++b) dw[b] = Bd[cur][wm * TM * 32 + b * 32 + r32];
+    // All block dots first (independent MFMAs), then the dependent scaling.
+    floatx16 dot[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        dot[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][0], bf[b][0], floatx16{}, 0, 0, 0);
+        dot[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][1], bf[b][1], dot[a][b], 0, 0, 0);
+      }
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
       // Row scales of this lane's 16 outputs: rows 8*(v/4) + 4*g + (v%4).
@@ -125,19 +147,35 @@ gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
         dx[4 * q + 3] = s4.w;
       }
 #pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        floatx16 dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][0], bf[b][0], floatx16{}, 0, 0, 0);
-        dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][1], bf[b][1], dot, 0, 0, 0);
+      for (int b = 0; b < TM; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float t = dot[v] * dw[b];
+          const float t = dot[a][b][v] * dw[b];
           const float u = t * dx[v];
           acc[a][b][v] = acc[a][b][v] + u;
         }
+    }
+  };
+
+  // Prologue: DEPTH blocks in flight, block 0 staged in LDS.
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u)
+    if (u < nb) load(ring[u], u);
+  store(ring[0], 0);
+  __syncthreads();
+  // Block kb sits in ring slot kb % DEPTH; it went to LDS during block kb-1,
+  // so that slot is refilled with block kb + DEPTH during block kb.
+  for (int kb0 = 0; kb0 < nb; kb0 += DEPTH) {
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) {
+      const int kb = kb0 + u;
+      if (kb < nb) {
+        compute(kb & 1);
+        if (kb + 1 < nb) store(ring[(u + 1) % DEPTH], (kb + 1) & 1);
+        if (kb + DEPTH < nb) load(ring[u], kb + DEPTH);
+        __syncthreads();
       }
     }
-    if (kb + 1 < nb) store(cur ^ 1);
-    __syncthreads();
   }
 
   // MFMA 32x32 output layout: lane holds column (lane & 31) and rows
@@ -155,6 +193,13 @@ gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
     }
 }
 
+// Grid for the XCD-aware order: the tile count rounded up to whole XCD slices.
+template <int BN, int BM>
+dim3 gemm_grid(int n, int m) {
+  const int tiles = ((n + BN - 1) / BN) * ((m + BM - 1) / BM);
+  return dim3(((tiles + kXcds - 1) / kXcds) * kXcds);
+}
+
 hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, const _Float16* wq, const float* wd, float* y, int n,
                           int m, int k, int ldy, hipStream_t st) {
   if (n <= 0 || m <= 0 || k <= 0 || k % kBK != 0 || ldy < m) return hipErrorInvalidValue;
@@ -162,11 +207,11 @@ hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, const _Float16* w
   // spread the waves over all 256 CUs rather than for operand reuse.
   const int tiles64 = ((m + 63) / 64) * ((n + 63) / 64);
   if (tiles64 >= 1024) {
-    hipLaunchKernelGGL((gemm_q8_kernel<64, 64, 2, 2>), dim3((m + 63) / 64, (n + 63) / 64), dim3(256), 0, st, xq, xd,
-                       wq, wd, y, n, m, k, ldy);
+    const dim3 grid = gemm_grid<64, 64>(n, m);
+    hipLaunchKernelGGL((gemm_q8_kernel<64, 64, 2, 2, 4>), grid, dim3(256), 0, st, xq, xd, wq, wd, y, n, m, k, ldy);
   } else {
-    hipLaunchKernelGGL((gemm_q8_kernel<32, 64, 1, 2>), dim3((m + 63) / 64, (n + 31) / 32), dim3(128), 0, st, xq, xd,
-                       wq, wd, y, n, m, k, ldy);
+    const dim3 grid = gemm_grid<32, 64>(n, m);
+    hipLaunchKernelGGL((gemm_q8_kernel<32, 64, 1, 2, 4>), grid, dim3(128), 0, st, xq, xd, wq, wd, y, n, m, k, ldy);
   }
   return hipGetLastError();
 }
