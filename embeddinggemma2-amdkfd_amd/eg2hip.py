@@ -54,8 +54,53 @@ class SynthConfig(C.Structure):
                 ("threads", C.c_uint)]
 
 
-# Every symbol declared in include/eg2_hip.h and include/gemma2_kfd.h.
+# The operator records of include/abi.h (kernels/abi.h:3-11) and EgSaxpy.
+class EgGather(C.Structure):
+    _fields_ = [("out", _vp), ("weight", _vp), ("ids", _vp), ("n", _u)]
+
+
+class EgMM(C.Structure):
+    _fields_ = [("out", _vp), ("x", _vp), ("weight", _vp), ("n", _u), ("k", _u), ("m", _u), ("type", _u)]
+
+
+class EgNorm(C.Structure):
+    _fields_ = [("out", _vp), ("x", _vp), ("weight", _vp), ("rows", _u), ("d", _u), ("scale", C.c_float)]
+
+
+class EgRope(C.Structure):
+    _fields_ = [("x", _vp), ("table", _vp), ("n", _u), ("heads", _u), ("d", _u)]
+
+
+class EgAttention(C.Structure):
+    _fields_ = [("out", _vp), ("q", _vp), ("k", _vp), ("v", _vp), ("bounds", _vp), ("n", _u), ("window", _u)]
+
+
+class EgElement(C.Structure):
+    _fields_ = [("out", _vp), ("x", _vp), ("other", _vp), ("n", _u), ("mode", _u), ("layer", _u),
+                ("scale", C.c_float)]
+
+
+class EgPool(C.Structure):
+    _fields_ = [("out", _vp), ("x", _vp), ("offsets", _vp), ("batch", _u)]
+
+
+class EgNormResidual(C.Structure):
+    _fields_ = [("out", _vp), ("x", _vp), ("weight", _vp), ("rows", _u), ("d", _u), ("scale", C.c_float)]
+
+
+class EgNormRope(C.Structure):
+    _fields_ = [("x", _vp), ("weight", _vp), ("table", _vp), ("rows", _u), ("d", _u), ("heads", _u)]
+
+
+class EgSaxpy(C.Structure):
+    _fields_ = [("y", _vp), ("x", _vp), ("a", C.c_float), ("n", _u)]
+
+
+# Every symbol declared in include/eg2_hip.h, include/eg2_ops.h and include/gemma2_kfd.h.
 SIGNATURES = {
+    "eg2_op_launch": (C.c_int, [C.c_char_p, _vp, C.c_size_t, _u, _u, _u, _vp]),
+    "eg2_op_count": (C.c_uint, []),
+    "eg2_op_name": (C.c_char_p, [_u]),
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _vp]),
@@ -296,6 +341,14 @@ class ops:
     @classmethod
     def l2_prefix(cls, x, dims):
         check(lib().eg2_hip_l2_prefix(cls._p(x), x.shape[1], dims, x.shape[0], cls._stream()), "l2_prefix")
+
+    @classmethod
+    def op(cls, name, record, grid, block):
+        """Launches operator `name` (include/eg2_ops.h) with a record from
+        this module; `grid` is a workgroup count or an (x, y) pair."""
+        gx, gy = (grid, 1) if isinstance(grid, int) else grid
+        check(lib().eg2_op_launch(name.encode(), C.byref(record), C.sizeof(record), gx, gy, block, cls._stream()),
+              name)
 
     @classmethod
     def gemm_q8(cls, xq, xd, wq, wd, y):

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_functions():
     names = set()
-    for h in ("gemma2_kfd.h", "eg2_hip.h"):
+    for h in ("gemma2_kfd.h", "eg2_hip.h", "eg2_ops.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b((?:ei|eg2)_[a-z0-9_]+)\s*\(", text):
@@ -179,3 +179,100 @@ def test_executor_create_reports_missing_device(eg2, small_gguf):
         pytest.skip("a gfx950 device is present; covered by the GPU tests")
     with pytest.raises(eg2.HipError, match=r"^HIP: supported HIP device not found"):
         eg2.Encoder(small_gguf)
+
+
+REFERENCE_OPERATORS = {"eg2_saxpy", "eg2_gather", "eg2_mm", "eg2_mm64", "eg2_mm64x64", "eg2_mmstep8", "eg2_norm",
+                       "eg2_rope", "eg2_attention256", "eg2_attention512", "eg2_element", "eg2_pool",
+                       "eg2_norm_residual", "eg2_norm_rope"}  # kernels/eg2.c
+
+
+def test_operator_names_cover_the_reference_set(eg2):
+    lib = eg2.lib()
+    names = {lib.eg2_op_name(i).decode() for i in range(lib.eg2_op_count())}
+    assert names == REFERENCE_OPERATORS | {"eg2_gather768", "eg2_attention256x3"}
+    assert lib.eg2_op_name(lib.eg2_op_count()) is None
+
+
+def test_operator_records_match_the_c_layout(tmp_path, eg2):
+    """ctypes records == the C layout of include/abi.h (size and offsets)."""
+    import subprocess
+
+    recs = ["EgGather", "EgMM", "EgNorm", "EgRope", "EgAttention", "EgElement", "EgPool", "EgNormResidual",
+            "EgNormRope", "EgSaxpy"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "eg2_ops.h"', "int main(void) {"]
+    for r in recs:
+        lines.append(f'  printf("{r} %zu\\n", sizeof({r}));')
+        for f, _ in getattr(eg2, r)._fields_:
+            lines.append(f'  printf("{r}.{f} %zu\\n", offsetof({r}, {f}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                        text=True).stdout.splitlines())
+    for r in recs:
+        cls = getattr(eg2, r)
+        assert int(out[r]) == C.sizeof(cls), r
+        for f, _ in cls._fields_:
+            assert int(out[f"{r}.{f}"]) == getattr(cls, f).offset, (r, f)
+
+
+def test_operator_launch_rejects_bad_arguments_without_launching(eg2):
+    """Every case fails validation before any launch (no device needed)."""
+    lib = eg2.lib()
+    p = 16  # a non-null pointer value; nothing is launched
+
+    def launch(name, rec, gx=1, gy=1, block=256, size=None):
+        return lib.eg2_op_launch(name.encode(), C.byref(rec), C.sizeof(rec) if size is None else size, gx, gy,
+                                 block, None)
+
+    inval = 1
+    mm = eg2.EgMM(p, p, p, 4, 32, 4, 8)
+    assert launch("eg2_nope", mm) == inval
+    assert launch("eg2_mm", mm, size=C.sizeof(mm) - 4) == inval
+    assert launch("eg2_mm", mm, gx=0) == inval
+    assert launch("eg2_mm", mm, block=128) == inval
+    assert launch("eg2_mm", eg2.EgMM(p, p, p, 4, 32, 4, 2)) == inval  # GGML type 2 is not supported
+    assert launch("eg2_mm", eg2.EgMM(None, p, p, 4, 32, 4, 8)) == inval
+    assert launch("eg2_norm", eg2.EgNorm(p, p, None, 1, 16, 1.0), block=256) == inval
+    assert launch("eg2_norm", eg2.EgNorm(p, p, None, 1, 0, 1.0), block=64) == inval
+    assert launch("eg2_rope", eg2.EgRope(p, p, 1, 1, 7)) == inval
+    assert launch("eg2_norm_rope", eg2.EgNormRope(p, p, p, 1, 256, 0), block=64) == inval
+    assert launch("eg2_element", eg2.EgElement(p, p, p, 8, 3, 0, 1.0)) == inval
+    assert launch("eg2_attention256", eg2.EgAttention(p, p, p, p, None, 1, 0), block=64) == inval
+    assert launch("eg2_pool", eg2.EgPool(p, p, None, 1)) == inval
+    assert launch("eg2_saxpy", eg2.EgSaxpy(None, p, 1.0, 4)) == inval
+    assert lib.eg2_op_launch(None, C.byref(mm), C.sizeof(mm), 1, 1, 256, None) == inval
+
+
+def elf_symbols(path):
+    """Names in the .symtab of a 64-bit little-endian ELF file."""
+    import struct
+
+    data = open(path, "rb").read()
+    assert data[:4] == b"\x7fELF" and data[4] == 2 and data[5] == 1
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    sections = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    names = set()
+    for sh in sections:
+        if sh[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = sections[sh[6]]
+        for off in range(sh[4], sh[4] + sh[5], sh[9]):
+            name_off, = struct.unpack_from("<I", data, off)
+            s = data[strtab[4] + name_off:data.index(b"\0", strtab[4] + name_off)]
+            names.add(s.decode())
+    return names
+
+
+def test_code_object_exports_the_operator_kernels(eg2):
+    """The stand-alone gfx950 code object carries NAME and NAME.kd for every
+    operator, as a by-name loader expects (src/gemma2_kfd.cpp:106-110)."""
+    co = os.path.join(ROOT, "embeddinggemma2-amdkfd_amd", "eg2_ops_gfx950.co")
+    syms = elf_symbols(co)
+    lib = eg2.lib()
+    for i in range(lib.eg2_op_count()):
+        name = lib.eg2_op_name(i).decode()
+        assert name in syms and name + ".kd" in syms, name
