@@ -1,89 +1,188 @@
-// Row kernels of the packed encoder forward: one 64-lane workgroup per token
-// row. They are HBM-bound; each one fuses the element-wise work between two
-// GEMMs so a token row is read and written once. Each reproduces the
-// reference's operation order, so its results are bit-identical to the CPU
-// path for identical inputs (tanhf in the GeGLU kernel is the one libm
-// function evaluated on the device).
+// Row kernels of the packed encoder forward. They are HBM-bound; each one
+// fuses the element-wise work between two GEMMs so a token row is read and
+// written once, and each reproduces the reference's operation order, so its
+// results are bit-identical to the CPU path for identical inputs (tanhf in
+// the GeGLU kernel is the one libm function evaluated on the device).
+//
+// Work mapping. One 64-lane wave per token row (a 2048-token wave gives two
+// waves per SIMD):
+//  * element-wise work runs one float4 per lane per 256 columns, coalesced,
+//    with the row kept in registers;
+//  * the SSE2-order sum of squares (kernels.c:82-94) runs one lane per
+//    chain: lane c owns chain c (the sequential sum of row[8t + c]^2) over
+//    the row staged in LDS, with every read issued before the dependent
+//    additions; every 8-lane group computes the same chains, so every lane
+//    ends with the total;
+//  * Q8_0 quantization splits each 32-value block over P adjacent lanes,
+//    which combine the block maximum with log2(P) shuffles.
+// Rows are staged in LDS with every 32-value block padded to 36 floats so
+// that the per-chain and per-block reads spread over the banks.
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
 namespace eg2 {
 
-// Normalises the LDS row `row` (kEmbd floats) with weight w and inverse rms
-// `inv` as (x*w)*inv (kernels.c:124-133, SSE2 branch), then quantizes it to
-// Q8_0 blocks (quants.c:97-177) written as fp16 integers plus one float
-// scale per block. Lane l owns elements l + 64r: its half-wave holds block
-// 2r + l/32.
-__device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w,
-                                                  float inv, _Float16* __restrict__ qs,
-                                                  float* __restrict__ qd, int k) {
-  const int lane = threadIdx.x & 63;
-  for (int r = 0; r < k / 64; ++r) {
-    const int e = lane + 64 * r;
-    const float p = row[e] * w[e];
-    const float v = p * inv;
-    const Q8Lane q = q8_quantize_lane(v);
-    qs[e] = (_Float16)q.q;
-    if ((lane & 31) == 0) qd[e / kQK] = q.d;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+constexpr int kBlkStride = kQK + 4;                    // padded 32-value block in LDS
+constexpr int kRowFloats = kEmbd / kQK * kBlkStride;   // 864 floats per padded row
+constexpr int kBlocks = kEmbd / kQK;                   // 24 blocks per row
+constexpr int kVec = kEmbd / 256;                      // float4 per lane per row
+
+// LDS index of element e of a padded row.
+__device__ __forceinline__ int pad(int e) { return e + (e / kQK) * (kBlkStride - kQK); }
+
+// Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):
+// the sequential sum over t of x[8t + c]^2, squares rounded then added.
+template <int N, bool PADDED>
+__device__ __forceinline__ float sse2_chain(const float* row, int c) {
+  float v[N / 8];
+#pragma unroll
+  for (int t = 0; t < N / 8; ++t) v[t] = row[PADDED ? pad(8 * t + c) : 8 * t + c];
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < N / 8; ++t) {
+    const float p = v[t] * v[t];
+    s = s + p;
   }
+  return s;
 }
 
-// engine.c:288-295 + kernels.c:139-151 (the next projection's input):
+// Horizontal step of the SSE2 sum for the 8-lane group holding chains 0..7
+// (chains 0-3 are the first 4-wide accumulator, 4-7 the second):
+// v[j] = acc0[j] + acc1[j], total (v0 + v2) + (v1 + v3) (kernels.c:35-39).
+// Every lane of the group receives the total. All 64 lanes must call it.
+__device__ __forceinline__ float sse2_combine(float s) {
+  const int lane = threadIdx.x & 63, base = lane & ~7;
+  const float up = __shfl(s, base + ((lane + 4) & 7), 64);
+  const float v = s + up;
+  const float v0 = __shfl(v, base, 64), v1 = __shfl(v, base + 1, 64);
+  const float v2 = __shfl(v, base + 2, 64), v3 = __shfl(v, base + 3, 64);
+  return (v0 + v2) + (v1 + v3);
+}
+
+// SSE2 sum of squares of a padded 768-float LDS row, on every lane.
+__device__ __forceinline__ float row_sum_squares(const float* row) {
+  return sse2_combine(sse2_chain<kEmbd, true>(row, threadIdx.x & 7));
+}
+
+// quants.c:97-177 (scalar path) on one block spread over P adjacent lanes
+// (lanes P*i .. P*i+P-1, all active), each holding N = 32/P consecutive
+// values: amax, d = amax/127 stored as fp16 (round-half-up), id = 1/d,
+// q = roundf(v*id) clamped; an all-zero block stores d = 0 and q = 0. Each
+// lane writes its N values as fp16 integers at q (16-byte aligned); the
+// first lane of the group writes the float value of the stored scale.
+template <int P>
+__device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], bool store, _Float16* __restrict__ q,
+                                                    float* __restrict__ d_out) {
+  constexpr int N = kQK / P;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int m = 1; m < P; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  const float d = amax / 127.0f;
+  const float id = amax != 0.0f ? 1.0f / d : 0.0f;
+  if (!store) return;
+  if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+  half8 out[N / 8];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i / 8][i % 8] = (_Float16)(amax != 0.0f ? q8_round(v[i] * id) : 0);
+#pragma unroll
+  for (int i = 0; i < N / 8; ++i) reinterpret_cast<half8*>(q)[i] = out[i];
+}
+
+// (x*w)*inv on a padded LDS row (kernels.c:124-133, SSE2 branch), quantized
+// to Q8_0 (kernels.c:139-151): lane pairs take the 24 blocks (lanes 48-63
+// repeat the last block and store nothing).
+__device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w, float inv,
+                                                  _Float16* __restrict__ q, float* __restrict__ d) {
+  const int lane = threadIdx.x;
+  const int b = min(lane >> 1, kBlocks - 1), part = lane & 1, e0 = b * kQK + part * (kQK / 2);
+  float v[kQK / 2];
+#pragma unroll
+  for (int i = 0; i < kQK / 8; ++i) {
+    const float4 xv = *reinterpret_cast<const float4*>(row + pad(e0) + 4 * i);
+    const float4 wv = *reinterpret_cast<const float4*>(w + e0 + 4 * i);
+    const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
+    v[4 * i + 0] = p0 * inv;
+    v[4 * i + 1] = p1 * inv;
+    v[4 * i + 2] = p2 * inv;
+    v[4 * i + 3] = p3 * inv;
+  }
+  quantize_block_part<2>(v, lane < 2 * kBlocks, q + e0, d + b);
+}
+
+// engine.c:288-295 + kernels.c:139-151 (the first projection's input):
 // x = (fp16(d) * sqrt(768)) * q from the raw GGUF Q8_0 row of token_embd,
 // then the layer-0 attn_norm RMSNorm quantized to Q8_0.
 __global__ void __launch_bounds__(64)
-embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __restrict__ ids,
-                        float embed_scale, const float* __restrict__ norm_w, float eps,
-                        float* __restrict__ x, _Float16* __restrict__ xq, float* __restrict__ xd) {
-  __shared__ __align__(16) uint8_t raw[kEmbd / kQK * 34];
-  __shared__ float row[kEmbd];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  const uint8_t* src = table + (size_t)ids[t] * (kEmbd / kQK * 34);
-  // 816 bytes per row = 51 16-byte chunks; GGUF rows of this tensor are
-  // 16-byte aligned because 816 = 16 * 51 and tensor data is 32-aligned.
-  if (lane < 51) reinterpret_cast<uint4*>(raw)[lane] = reinterpret_cast<const uint4*>(src)[lane];
+embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __restrict__ ids, float embed_scale,
+                        const float* __restrict__ norm_w, float eps, float* __restrict__ x,
+                        _Float16* __restrict__ xq, float* __restrict__ xd) {
+  constexpr int kRaw = kBlocks * 34;  // 816 bytes = 51 x 16
+  __shared__ __align__(16) uint8_t raw[kRaw];
+  __shared__ __align__(16) float row[kRowFloats];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  // GGUF rows of this tensor are 16-byte aligned: 816 = 16 * 51 and tensor
+  // data is 32-byte aligned.
+  if (lane < kRaw / 16)
+    reinterpret_cast<uint4*>(raw)[lane] = reinterpret_cast<const uint4*>(table + (size_t)ids[t] * kRaw)[lane];
   __syncthreads();
-  for (int r = 0; r < kEmbd / 64; ++r) {
-    const int e = lane + 64 * r;
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const int e = 4 * (lane + 64 * r);
     const uint8_t* blk = raw + (e / kQK) * 34;
-    const uint32_t hbits = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
-    const float d = fp16_bits_to_fp32(hbits) * embed_scale;  // quants.c:67
-    const float v = d * (float)(int8_t)blk[2 + e % kQK];      // quants.c:87
-    row[e] = v;
-    x[(size_t)t * kEmbd + e] = v;
+    const float dd = fp16_bits_to_fp32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * embed_scale;  // quants.c:67
+    const uint8_t* qs = blk + 2 + e % kQK;
+    float4 v;
+    v.x = dd * (float)(int8_t)qs[0];  // quants.c:87
+    v.y = dd * (float)(int8_t)qs[1];
+    v.z = dd * (float)(int8_t)qs[2];
+    v.w = dd * (float)(int8_t)qs[3];
+    *reinterpret_cast<float4*>(&row[pad(e)]) = v;
+    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v;
   }
   __syncthreads();
-  const float inv = rms_inverse(sum_squares_sse2(row, kEmbd), kEmbd, eps);
-  norm_quantize_row(row, norm_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * (kEmbd / kQK), kEmbd);
+  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
+  norm_quantize_row(row, norm_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * kBlocks);
 }
 
 // kernels.c:163-188 (SSE2 build: scalar branch, residual += (h*inv)*w), then
 // kernels.c:139-151 with the next norm weight on the updated residual. With
 // next_w == nullptr only the residual update runs.
 __global__ void __launch_bounds__(64)
-residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h,
-                           const float* __restrict__ post_w, const float* __restrict__ next_w,
-                           float eps, _Float16* __restrict__ xq, float* __restrict__ xd) {
-  __shared__ float hrow[kEmbd];
-  __shared__ float xrow[kEmbd];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  for (int r = 0; r < kEmbd / 64; ++r) hrow[lane + 64 * r] = h[(size_t)t * kEmbd + lane + 64 * r];
+residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, const float* __restrict__ post_w,
+                           const float* __restrict__ next_w, float eps, _Float16* __restrict__ xq,
+                           float* __restrict__ xd) {
+  __shared__ __align__(16) float row[kRowFloats];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float4 hv[kVec], xv[kVec], wv[kVec];
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const int e = 4 * (lane + 64 * r);
+    hv[r] = *reinterpret_cast<const float4*>(h + (size_t)t * kEmbd + e);
+    xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + e);
+    wv[r] = *reinterpret_cast<const float4*>(post_w + e);
+  }
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) *reinterpret_cast<float4*>(&row[pad(4 * (lane + 64 * r))]) = hv[r];
   __syncthreads();
-  const float inv_h = rms_inverse(sum_squares_sse2(hrow, kEmbd), kEmbd, eps);
-  for (int r = 0; r < kEmbd / 64; ++r) {
-    const int e = lane + 64 * r;
-    const float a = hrow[e] * inv_h;
-    const float b = a * post_w[e];
-    const float v = x[(size_t)t * kEmbd + e] + b;
-    xrow[e] = v;
-    x[(size_t)t * kEmbd + e] = v;
+  const float inv_h = rms_inverse(row_sum_squares(row), kEmbd, eps);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const int e = 4 * (lane + 64 * r);
+    const float a0 = hv[r].x * inv_h, a1 = hv[r].y * inv_h, a2 = hv[r].z * inv_h, a3 = hv[r].w * inv_h;
+    const float b0 = a0 * wv[r].x, b1 = a1 * wv[r].y, b2 = a2 * wv[r].z, b3 = a3 * wv[r].w;
+    const float4 v = make_float4(xv[r].x + b0, xv[r].y + b1, xv[r].z + b2, xv[r].w + b3);
+    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v;
+    *reinterpret_cast<float4*>(&row[pad(e)]) = v;
   }
   if (!next_w) return;
   __syncthreads();
-  const float inv = rms_inverse(sum_squares_sse2(xrow, kEmbd), kEmbd, eps);
-  norm_quantize_row(xrow, next_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * (kEmbd / kQK), kEmbd);
+  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
+  norm_quantize_row(row, next_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * kBlocks);
 }
 
 // Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
@@ -94,6 +193,8 @@ __device__ __forceinline__ void store_split(_Float16* row, int width, int i, flo
   row[width + i] = (_Float16)(x - (float)h);
 }
 
+constexpr int kHeadStride = kHeadDim + 8;  // LDS row of one head: 8 banks apart
+
 // kernels.c:233-264 on one token of the fused QKV projection output
 // [q0 q1 q2 | k | v] (fp32, kQKVCols wide): per-head RMS with the weight
 // applied before the inverse, NeoX rotation of pairs (d, d+128) with the
@@ -102,120 +203,164 @@ __device__ __forceinline__ void store_split(_Float16* row, int width, int i, flo
 // split fp16 pairs for the attention kernel, rows [hi | lo]; q is stored
 // times 16 (exact) to keep its low half clear of fp16 subnormals.
 __global__ void __launch_bounds__(64)
-qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w,
-                    const float* __restrict__ k_w, const float* __restrict__ rope,
-                    const int32_t* __restrict__ pos, float eps, _Float16* __restrict__ qs,
-                    _Float16* __restrict__ ks, _Float16* __restrict__ vs) {
-  __shared__ float rows[4][kHeadDim];
-  __shared__ float inv[4];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  const float* src = qkv + (size_t)t * kQKVCols;
-  for (int i = lane; i < 4 * kHeadDim; i += 64) rows[i / kHeadDim][i % kHeadDim] = src[i];
-  for (int i = lane; i < kHeadDim; i += 64) store_split(vs + (size_t)t * 2 * kHeadDim, kHeadDim, i, src[4 * kHeadDim + i]);
-  __syncthreads();
-  for (int hd = 0; hd < 4; ++hd) {
-    const float ss = sum_squares_sse2(rows[hd], kHeadDim);
-    if (lane == 0) inv[hd] = rms_inverse(ss, kHeadDim, eps);
-  }
-  __syncthreads();
-  const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
+qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w, const float* __restrict__ k_w,
+                    const float* __restrict__ rope, const int32_t* __restrict__ pos, float eps,
+                    _Float16* __restrict__ qs, _Float16* __restrict__ ks, _Float16* __restrict__ vs) {
+  constexpr int kRows = kHeads + 1;  // q heads, then k
   constexpr int half = kHeadDim / 2;
-  for (int i = lane; i < 4 * half; i += 64) {
-    const int hd = i / half, d = i % half;
+  __shared__ __align__(16) float rows[kRows][kHeadStride];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const float* src = qkv + (size_t)t * kQKVCols;
+  const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
+  const float c0 = cs[lane], c1 = cs[lane + 64], s0 = cs[half + lane], s1 = cs[half + lane + 64];
+#pragma unroll
+  for (int r = 0; r < kRows * kHeadDim / 256; ++r) {
+    const int e = 4 * (lane + 64 * r);
+    *reinterpret_cast<float4*>(&rows[e / kHeadDim][e % kHeadDim]) = *reinterpret_cast<const float4*>(src + e);
+  }
+  const float4 v = *reinterpret_cast<const float4*>(src + kRows * kHeadDim + 4 * lane);
+  _Float16* vrow = vs + (size_t)t * 2 * kHeadDim;
+  store_split(vrow, kHeadDim, 4 * lane + 0, v.x);
+  store_split(vrow, kHeadDim, 4 * lane + 1, v.y);
+  store_split(vrow, kHeadDim, 4 * lane + 2, v.z);
+  store_split(vrow, kHeadDim, 4 * lane + 3, v.w);
+  __syncthreads();
+  // lanes 8r..8r+7 run the chains of head row r (r < 4); the rest repeat row 0
+  const int hr = (lane >> 3) < kRows ? (lane >> 3) : 0;
+  const float ss = sse2_combine(sse2_chain<kHeadDim, false>(rows[hr], lane & 7));
+  float inv[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) inv[r] = rms_inverse(__shfl(ss, 8 * r, 64), kHeadDim, eps);
+#pragma unroll
+  for (int hd = 0; hd < kRows; ++hd) {
     const float* w = hd < kHeads ? q_w : k_w;
-    const float c = cs[d], s = cs[half + d];
-    const float x0 = rows[hd][d] * w[d] * inv[hd];
-    const float x1 = rows[hd][d + half] * w[d + half] * inv[hd];
-    const float a0 = x0 * c, a1 = x1 * s;
-    const float b0 = x0 * s, b1 = x1 * c;
-    float lo = a0 - a1, hi = b0 + b1;
-    if (hd < kHeads) {
-      lo = lo * 0.0625f;
-      hi = hi * 0.0625f;
-      _Float16* row = qs + (size_t)t * 2 * kEmbd;
-      store_split(row, kEmbd, hd * kHeadDim + d, lo * 16.0f);
-      store_split(row, kEmbd, hd * kHeadDim + d + half, hi * 16.0f);
-    } else {
-      _Float16* row = ks + (size_t)t * 2 * kHeadDim;
-      store_split(row, kHeadDim, d, lo);
-      store_split(row, kHeadDim, d + half, hi);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int d = lane + 64 * j;
+      const float c = j ? c1 : c0, s = j ? s1 : s0;
+      const float x0 = rows[hd][d] * w[d] * inv[hd];
+      const float x1 = rows[hd][d + half] * w[d + half] * inv[hd];
+      const float a0 = x0 * c, a1 = x1 * s;
+      const float b0 = x0 * s, b1 = x1 * c;
+      float lo = a0 - a1, hi = b0 + b1;
+      if (hd < kHeads) {
+        lo = lo * 0.0625f;
+        hi = hi * 0.0625f;
+        _Float16* row = qs + (size_t)t * 2 * kEmbd;
+        store_split(row, kEmbd, hd * kHeadDim + d, lo * 16.0f);
+        store_split(row, kEmbd, hd * kHeadDim + d + half, hi * 16.0f);
+      } else {
+        _Float16* row = ks + (size_t)t * 2 * kHeadDim;
+        store_split(row, kHeadDim, d, lo);
+        store_split(row, kHeadDim, d + half, hi);
+      }
     }
   }
 }
 
-// kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0.
+// kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0,
+// each 32-value block over 4 lanes (8 values each).
 // gu rows hold [gate 0..1151 | up 0..1151].
-__global__ void __launch_bounds__(64)
-gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float* __restrict__ gd) {
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  const float* g = gu + (size_t)t * (2 * kFF);
+__global__ void __launch_bounds__(256)
+gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float* __restrict__ gd, int n_rows) {
+  constexpr int kB = kFF / kQK;  // 36 blocks per row
+  const int j = blockIdx.x * 256 + threadIdx.x;  // quarter block
+  const int jb = min(j >> 2, n_rows * kB - 1);   // the last wave may run past the end: repeat, store nothing
+  const int t = jb / kB, b = jb - t * kB, e0 = b * kQK + (j & 3) * 8;
+  const float* g = gu + (size_t)t * (2 * kFF) + e0;
   const float* u = g + kFF;
   const float a = 0.044715f;
   const float s = 0.79788456080286535587989211986876f;
-  for (int r = 0; r < kFF / 64; ++r) {
-    const int e = lane + 64 * r;
-    const float x = g[e];
-    const float inner = s * x * (1.0f + a * x * x);
-    const float gelu = 0.5f * x * (1.0f + tanhf(inner));
-    const float v = gelu * u[e];
-    const Q8Lane q = q8_quantize_lane(v);
-    gq[(size_t)t * kFF + e] = (_Float16)q.q;
-    if ((lane & 31) == 0) gd[(size_t)t * (kFF / kQK) + e / kQK] = q.d;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 g4 = *reinterpret_cast<const float4*>(g + 4 * i);
+    const float4 u4 = *reinterpret_cast<const float4*>(u + 4 * i);
+    const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float x = gs[c];
+      const float inner = s * x * (1.0f + a * x * x);
+      const float gelu = 0.5f * x * (1.0f + tanhf(inner));
+      v[4 * i + c] = gelu * us[c];
+    }
   }
+  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + (size_t)t * kFF + e0, gd + (size_t)t * kB + b);
 }
 
-// quants.c:97-177 on rows of width k (k % 64 == 0).
-__global__ void __launch_bounds__(64)
-quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ q,
-                     float* __restrict__ d) {
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  for (int e = lane; e < k; e += 64) {
-    const Q8Lane r = q8_quantize_lane(x[(size_t)t * k + e]);
-    q[(size_t)t * k + e] = (_Float16)r.q;
-    if ((lane & 31) == 0) d[(size_t)t * (k / kQK) + e / kQK] = r.d;
+// quants.c:97-177 on rows of width k (k % 32 == 0), each block over 4 lanes.
+__global__ void __launch_bounds__(256)
+quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ q, float* __restrict__ d,
+                     int n_rows) {
+  const int nb = k / kQK;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int jb = min(j >> 2, n_rows * nb - 1);
+  const int t = jb / nb, b = jb - t * nb, e0 = b * kQK + (j & 3) * 8;
+  const float* src = x + (size_t)t * k + e0;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 x4 = *reinterpret_cast<const float4*>(src + 4 * i);
+    v[4 * i + 0] = x4.x;
+    v[4 * i + 1] = x4.y;
+    v[4 * i + 2] = x4.z;
+    v[4 * i + 3] = x4.w;
   }
+  quantize_block_part<4>(v, (j >> 2) < n_rows * nb, q + (size_t)t * k + e0, d + (size_t)t * nb + b);
 }
 
 // kernels.c:153-161 in place on a token row: x = (x*w)*inv.
 __global__ void __launch_bounds__(64)
 rms_norm_rows_kernel(float* __restrict__ x, const float* __restrict__ w, float eps) {
-  __shared__ float row[kEmbd];
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  for (int r = 0; r < kEmbd / 64; ++r) row[lane + 64 * r] = x[(size_t)t * kEmbd + lane + 64 * r];
+  __shared__ __align__(16) float row[kRowFloats];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float4 xv[kVec];
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + 4 * (lane + 64 * r));
+    *reinterpret_cast<float4*>(&row[pad(4 * (lane + 64 * r))]) = xv[r];
+  }
   __syncthreads();
-  const float inv = rms_inverse(sum_squares_sse2(row, kEmbd), kEmbd, eps);
-  for (int r = 0; r < kEmbd / 64; ++r) {
-    const int e = lane + 64 * r;
-    const float p = row[e] * w[e];
-    x[(size_t)t * kEmbd + e] = p * inv;
+  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const int e = 4 * (lane + 64 * r);
+    const float4 wv = *reinterpret_cast<const float4*>(w + e);
+    const float p0 = xv[r].x * wv.x, p1 = xv[r].y * wv.y, p2 = xv[r].z * wv.z, p3 = xv[r].w * wv.w;
+    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = make_float4(p0 * inv, p1 * inv, p2 * inv, p3 * inv);
   }
 }
 
 // kernels.c:417-427 after the per-token RMS (rms_norm_rows_kernel): one
-// workgroup per sequence sums its normalised rows in token order, scales by
-// 1/n, then L2-normalises in the SSE2 order (kernels.c:393-396).
-__global__ void __launch_bounds__(256)
-pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets,
-               float* __restrict__ out) {
+// workgroup per sequence, one thread per column, sums the normalised rows in
+// token order (loads issued kPoolBatch rows ahead of the additions), scales
+// by 1/n, then L2-normalises in the SSE2 order (kernels.c:393-396).
+constexpr int kPoolBatch = 32;
+__global__ void __launch_bounds__(kEmbd)
+pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets, float* __restrict__ out) {
   __shared__ float acc[kEmbd];
-  const int s = blockIdx.x;
+  __shared__ float total;
+  const int s = blockIdx.x, e = threadIdx.x;
   const uint32_t lo = offsets[s], hi = offsets[s + 1];
-  for (int e = threadIdx.x; e < kEmbd; e += 256) {
-    float sum = 0.0f;
-    for (uint32_t t = lo; t < hi; ++t) sum = sum + x[(size_t)t * kEmbd + e];
-    const float scale = 1.0f / (float)(hi - lo);
-    acc[e] = sum * scale;
+  float sum = 0.0f;
+  for (uint32_t t = lo; t < hi; t += kPoolBatch) {
+    float v[kPoolBatch];
+#pragma unroll
+    for (int i = 0; i < kPoolBatch; ++i) v[i] = t + i < hi ? x[(size_t)(t + i) * kEmbd + e] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPoolBatch; ++i)
+      if (t + i < hi) sum = sum + v[i];
+  }
+  const float scale = 1.0f / (float)(hi - lo);
+  acc[e] = sum * scale;
+  __syncthreads();
+  if (e < 64) {
+    const float ss = sse2_combine(sse2_chain<kEmbd, false>(acc, e & 7));
+    if (e == 0) total = ss;
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const float ss = sum_squares_sse2(acc, kEmbd);
-    const float scale = ss != 0.0f ? 1.0f / __builtin_sqrtf(ss) : 1.0f;
-    for (int e = threadIdx.x; e < kEmbd; e += 64) out[(size_t)s * kEmbd + e] = ss != 0.0f ? acc[e] * scale : acc[e];
-  }
+  const float ss = total;
+  out[(size_t)s * kEmbd + e] = ss != 0.0f ? acc[e] * (1.0f / __builtin_sqrtf(ss)) : acc[e];
 }
 
 // kernels.c:393-396 on the first `dims` elements of rows of width `width`
@@ -237,36 +382,40 @@ l2_prefix_kernel(float* __restrict__ x, int width, int dims) {
 
 // ---------------------------------------------------------------- launchers
 
+namespace {
+dim3 quarter_block_groups(int blocks) { return dim3((4 * blocks + 255) / 256); }
+}  // namespace
+
 hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int rows, float embed_scale,
                                    const float* norm_w, float eps, float* x, _Float16* xq, float* xd,
                                    hipStream_t st) {
-  hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(rows), dim3(64), 0, st, table, ids, embed_scale, norm_w,
-                     eps, x, xq, xd);
+  hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(rows), dim3(64), 0, st, table, ids, embed_scale, norm_w, eps, x,
+                     xq, xd);
   return hipGetLastError();
 }
 
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
                                       float eps, _Float16* xq, float* xd, int rows, hipStream_t st) {
-  hipLaunchKernelGGL(residual_norm_quant_kernel, dim3(rows), dim3(64), 0, st, x, h, post_w, next_w, eps, xq,
-                     xd);
+  hipLaunchKernelGGL(residual_norm_quant_kernel, dim3(rows), dim3(64), 0, st, x, h, post_w, next_w, eps, xq, xd);
   return hipGetLastError();
 }
 
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
                                const int32_t* pos, float eps, _Float16* qs, _Float16* ks, _Float16* vs,
                                int rows, hipStream_t st) {
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, qs, ks,
-                     vs);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, qs, ks, vs);
   return hipGetLastError();
 }
 
 hipError_t launch_gelu_quant(const float* gu, _Float16* gq, float* gd, int rows, hipStream_t st) {
-  hipLaunchKernelGGL(gelu_quant_kernel, dim3(rows), dim3(64), 0, st, gu, gq, gd);
+  hipLaunchKernelGGL(gelu_quant_kernel, quarter_block_groups(rows * (kFF / kQK)), dim3(256), 0, st, gu, gq, gd,
+                     rows);
   return hipGetLastError();
 }
 
 hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, int rows, hipStream_t st) {
-  hipLaunchKernelGGL(quantize_rows_kernel, dim3(rows), dim3(64), 0, st, x, k, q, d);
+  hipLaunchKernelGGL(quantize_rows_kernel, quarter_block_groups(rows * (k / kQK)), dim3(256), 0, st, x, k, q, d,
+                     rows);
   return hipGetLastError();
 }
 
@@ -276,7 +425,7 @@ hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, h
 }
 
 hipError_t launch_pool_l2(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st) {
-  hipLaunchKernelGGL(pool_l2_kernel, dim3(batch), dim3(256), 0, st, x, offsets, out);
+  hipLaunchKernelGGL(pool_l2_kernel, dim3(batch), dim3(kEmbd), 0, st, x, offsets, out);
   return hipGetLastError();
 }
 
