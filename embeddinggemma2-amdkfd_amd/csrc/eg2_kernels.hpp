@@ -1,7 +1,7 @@
 // Launchers of the gfx950 kernels (host side). All pointers are device
 // pointers; row counts are token rows of the packed wave. Q8_0 activations
-// and weights are fp16 integers [rows][k] plus one float scale per 32-block
-// [rows][k/32]; attention operands are split fp16 rows [hi | lo].
+// are fp16 integers [rows][k] plus one float scale per 32-block stored
+// transposed, [k/32][rows]; attention operands are split fp16 rows [hi | lo].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,8 +22,11 @@ hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, in
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);
 hipError_t launch_pool_l2(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st);
 hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t st);
-hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, const _Float16* wq, const float* wd, float* y, int n,
-                          int m, int k, int ldy, hipStream_t st);
+// xd: activation block scales transposed, [k/32][ldx]; wf/wdf: weights in
+// the fragment-major layout of eg2_q8_fragments.
+hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
+                          float* y, int n, int m, int k, int ldy, hipStream_t st);
+size_t gemm_q8_max_k();
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vs, const uint32_t* tiles,
                             const uint32_t* tile_count, int grid, int window, int rows, _Float16* cq, float* cd,
                             hipStream_t st);

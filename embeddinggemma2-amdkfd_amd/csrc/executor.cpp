@@ -4,8 +4,8 @@
 // Create (src/gemma2_kfd.cpp:86-155): select the gfx950 device, read the
 // `gemma-embedding` hyper-parameters and tensors from the caller's ei_gguf
 // (model.c:61-105 names, Q8_0 matrices), repack every matrix once into the
-// kernels' split Q8_0 layout (the int8 values as exact fp16 integers + one
-// float scale per 32-block),
+// projection GEMM's fragment-major Q8_0 layout (the int8 values as exact
+// fp16 integers + one float scale per 32-block, see eg2_q8_fragments),
 // fuse Q|K|V and gate|up into single projections, upload the raw Q8_0
 // embedding table, build the RoPE tables on the host, and allocate a
 // 2048-token workspace.
@@ -205,18 +205,14 @@ std::vector<uint8_t> Backend::q8_rows(const std::string& name, int k, int m) con
 }
 
 // Concatenates matrices along the output dimension and uploads them in the
-// split layout.
+// GEMM's fragment-major layout.
 DevMat Backend::upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k) {
-  size_t rows = 0;
-  for (auto* p : parts) rows += p->size() / ((size_t)(k / 32) * 34);
-  std::vector<uint16_t> q(rows * k);
-  std::vector<float> d(rows * (k / 32));
-  size_t r0 = 0;
-  for (auto* p : parts) {
-    const size_t r = p->size() / ((size_t)(k / 32) * 34);
-    eg2_q8_split(p->data(), r, (unsigned)k, q.data() + r0 * k, d.data() + r0 * (k / 32));
-    r0 += r;
-  }
+  std::vector<uint8_t> rows_q8;
+  for (auto* p : parts) rows_q8.insert(rows_q8.end(), p->begin(), p->end());
+  const size_t rows = rows_q8.size() / ((size_t)(k / 32) * 34);
+  std::vector<uint16_t> q(eg2_q8_fragment_halves(rows, (unsigned)k));
+  std::vector<float> d(q.size() / 16);
+  eg2_q8_fragments(rows_q8.data(), rows, (unsigned)k, q.data(), d.data());
   DevMat mat;
   mat.m = (int)rows;
   mat.k = k;
@@ -372,15 +368,15 @@ void Backend::record_layers(unsigned rows) {
                                                eps_, x_, xq_, xd_, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
-    launch("gemm_qkv", eg2::launch_gemm_q8(xq_, xd_, L.qkv.q, L.qkv.d, qkv_, n, L.qkv.m, kEmbd, kQKV, s));
+    launch("gemm_qkv", eg2::launch_gemm_q8(xq_, xd_, n, L.qkv.q, L.qkv.d, qkv_, n, L.qkv.m, kEmbd, kQKV, s));
     launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, eps_, qs_, ks_, vs_, n, s));
     launch("attention", eg2::launch_attention(qs_, ks_, vs_, tiles_d_, tiles_d_ + 4 * kCap, (n + 15) / 16, L.window,
                                               n, cq_, cd_, s));
-    launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
+    launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, n, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
-    launch("gemm_gate_up", eg2::launch_gemm_q8(xq_, xd_, L.gu.q, L.gu.d, gu_, n, 2 * kFF, kEmbd, 2 * kFF, s));
+    launch("gemm_gate_up", eg2::launch_gemm_q8(xq_, xd_, n, L.gu.q, L.gu.d, gu_, n, 2 * kFF, kEmbd, 2 * kFF, s));
     launch("gelu", eg2::launch_gelu_quant(gu_, xq_, xd_, n, s));
-    launch("gemm_down", eg2::launch_gemm_q8(xq_, xd_, L.down.q, L.down.d, h_, n, kEmbd, kFF, kEmbd, s));
+    launch("gemm_down", eg2::launch_gemm_q8(xq_, xd_, n, L.down.q, L.down.d, h_, n, kEmbd, kFF, kEmbd, s));
     const float* next = il + 1 < layers_.size() ? layers_[il + 1].attn_norm : nullptr;
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_ffw, next, eps_, xq_, xd_, n, s));
   }
@@ -505,10 +501,10 @@ void Backend::launch_staged(unsigned repeats) {
     launch("pool", eg2::launch_pool_l2(x_, off_d_, pooled_, B, s));
     if (dense_) {
       launch("dense_quant", eg2::launch_quantize_rows(pooled_, kEmbd, cq_, cd_, B, s));
-      launch("dense_2", eg2::launch_gemm_q8(cq_, cd_, dense2_.q, dense2_.d, mid_, B, kDenseFF, kEmbd, kDenseFF, s));
+      launch("dense_2", eg2::launch_gemm_q8(cq_, cd_, B, dense2_.q, dense2_.d, mid_, B, kDenseFF, kEmbd, kDenseFF, s));
       launch("dense_quant", eg2::launch_quantize_rows(mid_, kDenseFF, mid_q_, mid_d_, B, s));
       launch("dense_3",
-             eg2::launch_gemm_q8(mid_q_, mid_d_, dense3_.q, dense3_.d, pooled_, B, kEmbd, kDenseFF, kEmbd, s));
+             eg2::launch_gemm_q8(mid_q_, mid_d_, B, dense3_.q, dense3_.d, pooled_, B, kEmbd, kDenseFF, kEmbd, s));
       launch("dense_l2", eg2::launch_l2_prefix(pooled_, kEmbd, kEmbd, B, s));
     }
   }

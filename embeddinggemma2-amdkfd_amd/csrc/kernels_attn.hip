@@ -192,7 +192,8 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 
     // Epilogue: context = acc / l, then Q8_0 per 32 dims (one d-tile = one
     // block; quants.c:97-177). acc[dt][v] is dim dt*32 + 8*(v/4) + 4*g + (v%4)
-    // of query t. Values are stored as fp16 integers with a float scale.
+    // of query t. Values are stored as fp16 integers with a float scale, the
+    // scales transposed ([block][row]) for the projection GEMM.
     const float inv_l = 1.0f / l_run;
     _Float16* out = cq + (size_t)t * kEmbd + head * kHeadDim;
 #pragma unroll
@@ -216,7 +217,7 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
         for (int c = 0; c < 4; ++c) q4[c] = (_Float16)(amax == 0.0f ? 0 : q8_round(vals[4 * a + c] * id));
         *reinterpret_cast<half4*>(out + dt * 32 + 8 * a + 4 * g) = q4;
       }
-      if (g == 0) cd[(size_t)t * (kEmbd / kQK) + head * (kHeadDim / kQK) + dt] = dq;
+      if (g == 0) cd[(size_t)(head * (kHeadDim / kQK) + dt) * rows + t] = dq;
     }
   }
 }

@@ -7,14 +7,38 @@
 // added in block order with one fp32 rounding per operation. Results are
 // bit-identical to the CPU path.
 //
-// Both operands hold Q8_0 integers stored as fp16 (every int8 is exact in
-// fp16) with one float scale per 32-block: activations as written by the
-// fused quantizing row kernels, weights repacked once at load. A 32-block
-// dot is two v_mfma_f32_32x32x16_f16 with a zero accumulator; its products
-// (|q| <= 128) and partial sums (|sum| <= 2^19) are exact in fp32, so the
-// MFMA returns the integer dot exactly. The per-block scaling then costs
-// three VALU operations per output, which bounds this kernel (it cannot be
-// folded into the operands without changing the rounding).
+// Operands hold Q8_0 integers as fp16 (every int8 is exact in fp16). A
+// 32-block dot is two v_mfma_f32_32x32x16_f16 with a zero accumulator; its
+// products (|q| <= 128) and partial sums (|sum| <= 2^19) are exact in fp32,
+// so the MFMA returns the integer dot exactly. The scaling then costs three
+// VALU operations per output and block (it cannot be folded into the
+// operands without changing the rounding).
+//
+// Data layout (chosen for this kernel):
+//  * activations xq [rows][k] fp16, block scales transposed xd [k/32][ldx]
+//    (the quantizing row kernels write them that way);
+//  * weights in a fragment-major layout, repacked once at load:
+//    wf [m/32][k/32][64 lanes][16 fp16] where lane l holds row l % 32 and
+//    columns 16 * (l / 32) .. +15 of the 32-block, and their scales
+//    wdf [m/32][k/32][64 lanes] (one per lane, the row's block scale).
+//
+// One workgroup computes a 32-row x (32 * WM)-column tile with WM waves, one
+// 32x32 output tile per wave. The 32 activation rows of each block go from
+// global memory straight into an LDS ring (global_load_lds_dwordx4, one
+// 1 KB instruction per 16 rows, XOR-swizzled 16-byte chunks so the fragment
+// reads are free of bank conflicts) shared by the WM waves; each wave reads
+// its weight fragments from global memory into a register ring, fully
+// coalesced thanks to the fragment-major layout. LDS read bandwidth
+// (~64 B/clk per CU on this part) is the scarce resource: this split moves
+// only the shared operand through LDS. The activation scales of all blocks
+// are preloaded into LDS once per workgroup.
+//
+// In the MFMA 32x32 output layout a lane holds one weight column and 16
+// token rows; each row's activation scale reaches the lane through a DPP
+// row broadcast folded into the multiply (v_mul_f32_dpp row_newbcast), so
+// the per-block scale traffic is one float per lane.
+#include <utility>
+
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
@@ -23,197 +47,180 @@ namespace eg2 {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 32;              // one Q8_0 block per k-step
-constexpr int kLdsStride = kBK + 8;  // fp16 elements per LDS row (padding against bank conflicts)
-constexpr int kXcds = 8;             // MI355X: 8 XCDs of 32 CUs, each with its own L2
+constexpr int kBK = 32;   // one Q8_0 block per k-step
+constexpr int kXcds = 8;  // MI355X: 8 XCDs of 32 CUs, each with its own L2
 
-// BN x BM output tile per workgroup of WN x WM waves; each wave owns a
-// (BN/WN) x (BM/WM) sub-tile of 32x32 MFMA tiles. k % 32 == 0.
-//
-// K loop: operands of a 32-block travel HBM/L2 -> registers -> LDS (double
-// buffered) -> MFMA. With a 2048-token wave there are too few waves per CU
-// to hide memory latency, so each thread keeps DEPTH blocks of loads in
-// flight in a register ring; the loop is unrolled by DEPTH so ring slots are
-// compile-time registers.
-template <int BN, int BM, int WN, int WM, int DEPTH>
-__global__ void __launch_bounds__(WN * WM * 64)
-gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd,
-               const _Float16* __restrict__ wq, const float* __restrict__ wd,
-               float* __restrict__ y, int n, int m, int k, int ldy) {
-  constexpr int NT = WN * WM * 64;
-  constexpr int TN = BN / WN / 32, TM = BM / WM / 32;
-  constexpr int A_LOADS = (4 * BN + NT - 1) / NT;  // 16-byte quarter-block loads
-  constexpr int B_LOADS = (4 * BM + NT - 1) / NT;
-  __shared__ __align__(16) _Float16 As[2][BN * kLdsStride];
-  __shared__ __align__(16) _Float16 Bs[2][BM * kLdsStride];
-  __shared__ __align__(16) float Ad[2][BN];
-  __shared__ __align__(16) float Bd[2][BM];
+extern __shared__ __align__(16) unsigned char gemm_lds[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave / WM, wm = wave % WM;
-  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs,
-  // so workgroup b runs on XCD b % 8. Renumbering gives each XCD one
-  // contiguous run of tiles in column-block-major order, i.e. a slice of
-  // the weight columns plus the activations, which stay in that XCD's L2.
-  const int n_tiles_n = (n + BN - 1) / BN, n_tiles = n_tiles_n * ((m + BM - 1) / BM);
+// 4 / 16 bytes per lane from global memory straight into LDS at
+// lds + 4 * lane / lds + 16 * lane (the LDS base is wave-uniform).
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are in
+// flight, then joins the workgroup barrier. The LDS ring is filled by DMA,
+// which the compiler does not track, so the wait is explicit; the memory
+// clobber keeps LDS reads from moving across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Chunk swizzle of a 64-byte LDS row: 16-byte chunk c of row r is stored at
+// c ^ swz(r). The MFMA fragment reads (lane i of each half-wave reads row i)
+// then spread every 8- and 16-lane group over distinct banks.
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// Broadcast of lane V of each 16-lane row to the whole row.
+template <int V>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + V, 0xf, 0xf, true));
+}
+
+// acc[v] += (dot[v] * dw) * dx(row v): the lane's 16 output rows take their
+// activation scales from lanes 0..15 of its 16-lane row.
+template <int... V>
+__device__ __forceinline__ void scale_accumulate(floatx16& acc, const floatx16& dot, float dw, float dxv,
+                                                 std::integer_sequence<int, V...>) {
+  ((acc[V] = acc[V] + (dot[V] * dw) * row_bcast<V>(dxv)), ...);
+}
+
+template <int WM, int D>
+__global__ void __launch_bounds__(WM * 64)
+gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd, int ldx,
+               const _Float16* __restrict__ wf, const float* __restrict__ wdf, float* __restrict__ y, int n, int m,
+               int k, int ldy) {
+  constexpr int S = 2 * D;        // LDS ring stages
+  constexpr int STAGE = 32 * 64;  // 32 rows x 64 bytes
+  constexpr int QA = 2;           // 1 KB DMA instructions per stage
+  static_assert(QA % WM == 0 || WM % QA == 0, "DMA split");
+  constexpr int QAW = QA >= WM ? QA / WM : 1;  // per issuing wave
+  constexpr int QB = 3;                        // weight loads per block
+  static_assert((D & (D - 1)) == 0, "D must be a power of two");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_tiles_n = (n + 31) / 32, mt_count = (m + 31) / 32;
+  const int n_tiles = n_tiles_n * ((mt_count + WM - 1) / WM);
+  // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes one
+  // contiguous run of tiles (column-group major), so the weight columns it
+  // needs stay in its own L2.
   const int per_xcd = (n_tiles + kXcds - 1) / kXcds;
   const int tile = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
   if (tile >= n_tiles) return;
-  const int n0 = (tile % n_tiles_n) * BN, m0 = (tile / n_tiles_n) * BM;
+  const int n0 = (tile % n_tiles_n) * 32;
+  const int mt_raw = (tile / n_tiles_n) * WM + wave, mt = min(mt_raw, mt_count - 1);
   const int nb = k / kBK;
+  unsigned char* smem = gemm_lds;
+  float* sA = reinterpret_cast<float*>(smem + S * STAGE);  // [nb rounded up to 2][32]
 
-  struct Stage {
-    half8 a[A_LOADS], b[B_LOADS];
-    float sa[A_LOADS], sb[B_LOADS];
+  // Activation scales of all blocks: two blocks (2 x 32 rows) per instruction.
+  for (int b0 = 2 * wave; b0 < nb; b0 += 2 * WM) {
+    const int b = min(b0 + (lane >> 5), nb - 1);
+    dma4(xd + (size_t)b * ldx + min(n0 + (lane & 31), n - 1), sA + b0 * 32);
+  }
+  // Activation DMA: instruction q fills stage rows 16q..16q+15; lane L takes
+  // (row 16q + L/4, stored chunk L%4) = global chunk (L%4) ^ swz(row).
+  const bool dma_wave = wave < QA;
+  const _Float16* asrc[QAW];
+  int aoff[QAW];
+#pragma unroll
+  for (int t = 0; t < QAW; ++t) {
+    const int q = min(wave * QAW + t, QA - 1), row = 16 * q + (lane >> 2), c = (lane & 3) ^ swz(row);
+    asrc[t] = xq + (size_t)min(n0 + row, n - 1) * k + 8 * c;
+    aoff[t] = 1024 * q;
+  }
+  auto issue_a = [&](int slot, int kb) {
+    if (!dma_wave) return;
+    unsigned char* base = smem + (slot & (S - 1)) * STAGE;
+#pragma unroll
+    for (int t = 0; t < QAW; ++t) dma16(asrc[t] + kb * kBK, base + aoff[t]);
   };
-  Stage ring[DEPTH];
-
-  // Rows past n (or m) load the last valid row instead: always in bounds,
-  // never stored, and free of per-lane branches.
-  auto load = [&](Stage& st, int kb) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + i * NT, row = (idx >> 2) % BN, part = idx & 3, g = min(n0 + row, n - 1);
-      st.a[i] = *reinterpret_cast<const half8*>(xq + (size_t)g * k + kb * kBK + part * 8);
-      st.sa[i] = xd[(size_t)g * nb + kb];
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + i * NT, row = (idx >> 2) % BM, part = idx & 3, g = min(m0 + row, m - 1);
-      st.b[i] = *reinterpret_cast<const half8*>(wq + (size_t)g * k + kb * kBK + part * 8);
-      st.sb[i] = wd[(size_t)g * nb + kb];
-    }
+  // Weight fragments, D blocks ahead in registers.
+  const _Float16* bsrc = wf + ((size_t)mt * nb * 64 + lane) * 16;
+  const float* dsrc = wdf + (size_t)mt * nb * 64 + lane;
+  struct BStage {
+    half8 b0, b1;
+    float dw;
   };
-  auto store = [&](const Stage& st, int buf) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < 4 * BN) {
-        *reinterpret_cast<half8*>(&As[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = st.a[i];
-        if ((idx & 3) == 0) Ad[buf][idx >> 2] = st.sa[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < 4 * BM) {
-        *reinterpret_cast<half8*>(&Bs[buf][(idx >> 2) * kLdsStride + (idx & 3) * 8]) = st.b[i];
-        if ((idx & 3) == 0) Bd[buf][idx >> 2] = st.sb[i];
-      }
-    }
+  BStage ring[D];
+  auto load_b = [&](BStage& r, int kb) {
+    const half8* p = reinterpret_cast<const half8*>(bsrc + (size_t)kb * 64 * 16);
+    r.b0 = p[0];
+    r.b1 = p[1];
+    r.dw = dsrc[kb * 64];
   };
 
-  floatx16 acc[TN][TM];
-#pragma unroll
-  for (int a = 0; a < TN; ++a)
-#pragma unroll
-    for (int b = 0; b < TM; ++b) acc[a][b] = floatx16{};
-
+  floatx16 acc = floatx16{};
   const int g = lane >> 5, r32 = lane & 31;
-  auto compute = [&](int cur) {
-    half8 af[TN][2], bf[TM][2];
-#pragma unroll
-    for (int a = 0; a < TN; ++a)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        af[a][h] = *reinterpret_cast<const half8*>(&As[cur][(wn * TN * 32 + a * 32 + r32) * kLdsStride + h * 16 + g * 8]);
-#pragma unroll
-    for (int b = 0; b < TM; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        bf[b][h] = *reinterpret_cast<const half8*>(&Bs[cur][(wm * TM * 32 + b * 32 + r32) * kLdsStride + h * 16 + g * 8]);
-    float dw[TM];
-#pragma unroll
-    for (int b = 0; b < TM; ++b) dw[b] = Bd[cur][wm * TM * 32 + b * 32 + r32];
-    // All block dots first (independent MFMAs), then the dependent scaling.
-    floatx16 dot[TN][TM];
-#pragma unroll
-    for (int a = 0; a < TN; ++a)
-#pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        dot[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][0], bf[b][0], floatx16{}, 0, 0, 0);
-        dot[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][1], bf[b][1], dot[a][b], 0, 0, 0);
-      }
-#pragma unroll
-    for (int a = 0; a < TN; ++a) {
-      // Row scales of this lane's 16 outputs: rows 8*(v/4) + 4*g + (v%4).
-      float dx[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 s4 = *reinterpret_cast<const float4*>(&Ad[cur][wn * TN * 32 + a * 32 + 8 * q + 4 * g]);
-        dx[4 * q + 0] = s4.x;
-        dx[4 * q + 1] = s4.y;
-        dx[4 * q + 2] = s4.z;
-        dx[4 * q + 3] = s4.w;
-      }
-#pragma unroll
-      for (int b = 0; b < TM; ++b)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float t = dot[a][b][v] * dw[b];
-          const float u = t * dx[v];
-          acc[a][b][v] = acc[a][b][v] + u;
-        }
-    }
-  };
+  // Row whose scale this lane supplies to the DPP broadcast: lane 16r + v
+  // carries the scale of output register v for the lanes of 16-lane row r.
+  const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
+  const int af = swz(r32);
 
-  // Prologue: DEPTH blocks in flight, block 0 staged in LDS.
 #pragma unroll
-  for (int u = 0; u < DEPTH; ++u)
-    if (u < nb) load(ring[u], u);
-  store(ring[0], 0);
-  __syncthreads();
-  // Block kb sits in ring slot kb % DEPTH; it went to LDS during block kb-1,
-  // so that slot is refilled with block kb + DEPTH during block kb.
-  for (int kb0 = 0; kb0 < nb; kb0 += DEPTH) {
+  for (int u = 0; u < D; ++u) {
+    issue_a(u, min(u, nb - 1));
+    load_b(ring[u], min(u, nb - 1));
+  }
+  // Block kb: its DMA and weight loads were issued D blocks earlier; the
+  // stage it refills, (kb + D) % S, was last read in block kb - D.
+  for (int kb0 = 0; kb0 < nb; kb0 += D) {
+    const unsigned char* st0 = smem + (kb0 & D) * STAGE;
 #pragma unroll
-    for (int u = 0; u < DEPTH; ++u) {
+    for (int u = 0; u < D; ++u) {
       const int kb = kb0 + u;
-      if (kb < nb) {
-        compute(kb & 1);
-        if (kb + 1 < nb) store(ring[(u + 1) % DEPTH], (kb + 1) & 1);
-        if (kb + DEPTH < nb) load(ring[u], kb + DEPTH);
-        __syncthreads();
-      }
+      if (dma_wave) wait_vm_barrier<(D - 1) * (QAW + QB)>();
+      else wait_vm_barrier<(D - 1) * QB>();
+      const unsigned char* st = st0 + u * STAGE;
+      const half8 a0 = *reinterpret_cast<const half8*>(st + r32 * 64 + 16 * ((2 * g) ^ af));
+      const half8 a1 = *reinterpret_cast<const half8*>(st + r32 * 64 + 16 * ((2 * g + 1) ^ af));
+      const float dx = sA[kb * 32 + srow];
+      floatx16 dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ring[u].b0, floatx16{}, 0, 0, 0);
+      dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ring[u].b1, dot, 0, 0, 0);
+      issue_a(kb + D, min(kb + D, nb - 1));
+      scale_accumulate(acc, dot, ring[u].dw, dx, std::make_integer_sequence<int, 16>{});
+      load_b(ring[u], min(kb + D, nb - 1));
     }
   }
-
-  // MFMA 32x32 output layout: lane holds column (lane & 31) and rows
-  // 8*(v/4) + 4*(lane/32) + (v%4) for v = 0..15.
+  // The ring's last refills are redundant; they must land before the
+  // workgroup's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (mt_raw >= mt_count) return;
+  const int col = mt * 32 + r32;
 #pragma unroll
-  for (int a = 0; a < TN; ++a)
-#pragma unroll
-    for (int b = 0; b < TM; ++b) {
-      const int col = m0 + wm * TM * 32 + b * 32 + r32;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = n0 + wn * TN * 32 + a * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-        if (row < n && col < m) y[(size_t)row * ldy + col] = acc[a][b][v];
-      }
-    }
-}
-
-// Grid for the XCD-aware order: the tile count rounded up to whole XCD slices.
-template <int BN, int BM>
-dim3 gemm_grid(int n, int m) {
-  const int tiles = ((n + BN - 1) / BN) * ((m + BM - 1) / BM);
-  return dim3(((tiles + kXcds - 1) / kXcds) * kXcds);
-}
-
-hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, const _Float16* wq, const float* wd, float* y, int n,
-                          int m, int k, int ldy, hipStream_t st) {
-  if (n <= 0 || m <= 0 || k <= 0 || k % kBK != 0 || ldy < m) return hipErrorInvalidValue;
-  // The kernel is bound by per-block VALU scaling, so the tile is chosen to
-  // spread the waves over all 256 CUs rather than for operand reuse.
-  const int tiles64 = ((m + 63) / 64) * ((n + 63) / 64);
-  if (tiles64 >= 1024) {
-    const dim3 grid = gemm_grid<64, 64>(n, m);
-    hipLaunchKernelGGL((gemm_q8_kernel<64, 64, 2, 2, 4>), grid, dim3(256), 0, st, xq, xd, wq, wd, y, n, m, k, ldy);
-  } else {
-    const dim3 grid = gemm_grid<32, 64>(n, m);
-    hipLaunchKernelGGL((gemm_q8_kernel<32, 64, 1, 2, 4>), grid, dim3(128), 0, st, xq, xd, wq, wd, y, n, m, k, ldy);
+  for (int v = 0; v < 16; ++v) {
+    const int row = n0 + 8 * (v >> 2) + 4 * g + (v & 3);
+    if (row < n && col < m) y[(size_t)row * ldy + col] = acc[v];
   }
+}
+
+template <int WM, int D>
+static hipError_t launch_gemm(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
+                              float* y, int n, int m, int k, int ldy, hipStream_t st) {
+  const int tiles = ((n + 31) / 32) * (((m + 31) / 32 + WM - 1) / WM);
+  const dim3 grid(((tiles + kXcds - 1) / kXcds) * kXcds);
+  const int nb = k / kBK;
+  const size_t lds = (size_t)(2 * D) * 32 * 64 + (size_t)((nb + 1) / 2 * 2) * 32 * 4;
+  hipLaunchKernelGGL((gemm_q8_kernel<WM, D>), grid, dim3(WM * 64), lds, st, xq, xd, ldx, wf, wdf, y, n, m, k, ldy);
   return hipGetLastError();
+}
+
+size_t gemm_q8_max_k() {
+  // LDS: 4 stages of 2 KB plus 128 bytes of scales per block, within 64 KB.
+  return (65536 - 4 * 2048) / 128 * 32;
+}
+
+hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
+                          float* y, int n, int m, int k, int ldy, hipStream_t st) {
+  if (n <= 0 || m <= 0 || k <= 0 || k % kBK != 0 || ldy < m || ldx < n || (size_t)k > gemm_q8_max_k())
+    return hipErrorInvalidValue;
+  // Two waves per 32 x 64 tile, weight fragments two blocks ahead.
+  if ((k / kBK) % 2 == 0) return launch_gemm<2, 2>(xq, xd, ldx, wf, wdf, y, n, m, k, ldy, st);
+  return launch_gemm<2, 1>(xq, xd, ldx, wf, wdf, y, n, m, k, ldy, st);
 }
 
 }  // namespace eg2

@@ -94,9 +94,10 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
 
 // (x*w)*inv on a padded LDS row (kernels.c:124-133, SSE2 branch), quantized
 // to Q8_0 (kernels.c:139-151): lane pairs take the 24 blocks (lanes 48-63
-// repeat the last block and store nothing).
+// repeat the last block and store nothing). Block scales are stored
+// transposed, block b of this row at d[b * ld].
 __device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w, float inv,
-                                                  _Float16* __restrict__ q, float* __restrict__ d) {
+                                                  _Float16* __restrict__ q, float* __restrict__ d, int ld) {
   const int lane = threadIdx.x;
   const int b = min(lane >> 1, kBlocks - 1), part = lane & 1, e0 = b * kQK + part * (kQK / 2);
   float v[kQK / 2];
@@ -110,7 +111,7 @@ __device__ __forceinline__ void norm_quantize_row(const float* row, const float*
     v[4 * i + 2] = p2 * inv;
     v[4 * i + 3] = p3 * inv;
   }
-  quantize_block_part<2>(v, lane < 2 * kBlocks, q + e0, d + b);
+  quantize_block_part<2>(v, lane < 2 * kBlocks, q + e0, d + (size_t)b * ld);
 }
 
 // engine.c:288-295 + kernels.c:139-151 (the first projection's input):
@@ -145,7 +146,7 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
   }
   __syncthreads();
   const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, norm_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * kBlocks);
+  norm_quantize_row(row, norm_w, inv, xq + (size_t)t * kEmbd, xd + t, (int)gridDim.x);
 }
 
 // kernels.c:163-188 (SSE2 build: scalar branch, residual += (h*inv)*w), then
@@ -182,7 +183,7 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   if (!next_w) return;
   __syncthreads();
   const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, next_w, inv, xq + (size_t)t * kEmbd, xd + (size_t)t * kBlocks);
+  norm_quantize_row(row, next_w, inv, xq + (size_t)t * kEmbd, xd + t, (int)gridDim.x);
 }
 
 // Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
@@ -259,7 +260,8 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
 }
 
 // kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0,
-// each 32-value block over 4 lanes (8 values each).
+// each 32-value block over 4 lanes (8 values each); block scales transposed
+// ([block][row]).
 // gu rows hold [gate 0..1151 | up 0..1151].
 __global__ void __launch_bounds__(256)
 gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float* __restrict__ gd, int n_rows) {
@@ -285,10 +287,11 @@ gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float
       v[4 * i + c] = gelu * us[c];
     }
   }
-  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + (size_t)t * kFF + e0, gd + (size_t)t * kB + b);
+  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + (size_t)t * kFF + e0, gd + (size_t)b * n_rows + t);
 }
 
-// quants.c:97-177 on rows of width k (k % 32 == 0), each block over 4 lanes.
+// quants.c:97-177 on rows of width k (k % 32 == 0), each block over 4 lanes;
+// block scales transposed ([block][row]).
 __global__ void __launch_bounds__(256)
 quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ q, float* __restrict__ d,
                      int n_rows) {
@@ -306,7 +309,7 @@ quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ 
     v[4 * i + 2] = x4.z;
     v[4 * i + 3] = x4.w;
   }
-  quantize_block_part<4>(v, (j >> 2) < n_rows * nb, q + (size_t)t * k + e0, d + (size_t)t * nb + b);
+  quantize_block_part<4>(v, (j >> 2) < n_rows * nb, q + (size_t)t * k + e0, d + (size_t)b * n_rows + t);
 }
 
 // kernels.c:153-161 in place on a token row: x = (x*w)*inv.

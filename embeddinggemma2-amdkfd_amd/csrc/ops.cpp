@@ -119,10 +119,13 @@ int eg2_hip_l2_prefix(float* x, unsigned width, unsigned dims, unsigned rows, vo
   return code(eg2::launch_l2_prefix(x, (int)width, (int)dims, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_gemm_q8(const uint16_t* xq, const float* xd, const uint16_t* wq, const float* wd, float* y,
-                    unsigned n, unsigned m, unsigned k, unsigned ldy, void* stream) {
-  if (!xq || !xd || !wq || !wd || !y || n == 0 || m == 0 || k == 0 || k % 32 != 0 || ldy < m) return kInvalid;
-  return code(eg2::launch_gemm_q8(h16(xq), xd, h16(wq), wd, y, (int)n, (int)m, (int)k, (int)ldy, as_stream(stream)));
+int eg2_hip_gemm_q8(const uint16_t* xq, const float* xd, unsigned ldx, const uint16_t* wf, const float* wdf,
+                    float* y, unsigned n, unsigned m, unsigned k, unsigned ldy, void* stream) {
+  if (!xq || !xd || !wf || !wdf || !y || n == 0 || m == 0 || k == 0 || k % 32 != 0 || ldy < m || ldx < n ||
+      k > eg2::gemm_q8_max_k())
+    return kInvalid;
+  return code(eg2::launch_gemm_q8(h16(xq), xd, (int)ldx, h16(wf), wdf, y, (int)n, (int)m, (int)k, (int)ldy,
+                                  as_stream(stream)));
 }
 
 const char* eg2_hip_error_string(int c) { return hipGetErrorString((hipError_t)c); }
@@ -156,6 +159,22 @@ void eg2_q8_split(const void* blocks, size_t rows, unsigned k, uint16_t* q, floa
       for (int i = 0; i < 32; ++i) q[r * k + b * 32 + i] = int8_to_fp16_bits((int8_t)blk[2 + i]);
     }
 }
+
+void eg2_q8_fragments(const void* blocks, size_t rows, unsigned k, uint16_t* wf, float* wdf) {
+  const uint8_t* src = static_cast<const uint8_t*>(blocks);
+  const size_t nb = k / 32, tiles = (rows + 31) / 32;
+  for (size_t mt = 0; mt < tiles; ++mt)
+    for (size_t b = 0; b < nb; ++b)
+      for (unsigned lane = 0; lane < 64; ++lane) {
+        const size_t r = mt * 32 + lane % 32, f = (mt * nb + b) * 64 + lane;
+        const uint8_t* blk = r < rows ? src + (r * nb + b) * 34 : nullptr;
+        wdf[f] = blk ? fp16_to_fp32_host((uint16_t)(blk[0] | (blk[1] << 8))) : 0.0f;
+        for (unsigned i = 0; i < 16; ++i)
+          wf[f * 16 + i] = blk ? int8_to_fp16_bits((int8_t)blk[2 + 16 * (lane / 32) + i]) : 0;
+      }
+}
+
+size_t eg2_q8_fragment_halves(size_t rows, unsigned k) { return (rows + 31) / 32 * (k / 32) * 64 * 16; }
 
 void eg2_rope_table(float base, unsigned n_pos, float* table) {
   for (unsigned p = 0; p < n_pos; ++p)

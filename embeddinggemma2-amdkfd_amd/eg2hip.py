@@ -111,10 +111,12 @@ SIGNATURES = {
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
-    "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _u, _u, _vp]),
+    "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
     "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
     "eg2_q8_split": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
+    "eg2_q8_fragments": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
+    "eg2_q8_fragment_halves": (C.c_size_t, [C.c_size_t, _u]),
     "eg2_rope_table": (None, [C.c_float, _u, _vp]),
     "eg2_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
     "eg2_gguf_close": (None, [C.POINTER(EiGguf)]),
@@ -260,6 +262,20 @@ def rope_table(base, n_pos=N_CTX):
     return t
 
 
+def q8_fragments(blocks_u8, rows, k):
+    """GGUF Q8_0 bytes [rows, k] -> the projection GEMM's fragment-major weights
+    (wf: fp16 integers [ceil(rows/32), k/32, 64, 16], wdf: float32 scales
+    [ceil(rows/32), k/32, 64])."""
+    import numpy as np
+
+    src = np.ascontiguousarray(blocks_u8, dtype=np.uint8)
+    tiles = (rows + 31) // 32
+    wf = np.zeros((tiles, k // 32, 64, 16), dtype=np.float16)
+    wdf = np.zeros((tiles, k // 32, 64), dtype=np.float32)
+    lib().eg2_q8_fragments(src.ctypes.data, rows, k, wf.ctypes.data, wdf.ctypes.data)
+    return wf, wdf
+
+
 def q8_split(blocks_u8, rows, k):
     """GGUF Q8_0 bytes -> (fp16 integer values [rows, k], float32 scales [rows, k/32])."""
     import numpy as np
@@ -351,8 +367,10 @@ class ops:
               name)
 
     @classmethod
-    def gemm_q8(cls, xq, xd, wq, wd, y):
+    def gemm_q8(cls, xq, xd, wf, wdf, y, m=None):
+        """y[:, :m] = xq . W^T with xd the activation scales [k/32, ldx] and
+        (wf, wdf) the weights from q8_fragments (m defaults to y's width)."""
         n, k = xq.shape
-        m = wq.shape[0]
-        check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), cls._p(wq), cls._p(wd), cls._p(y), n, m, k,
+        m = y.shape[1] if m is None else m
+        check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wf), cls._p(wdf), cls._p(y), n, m, k,
                                     y.shape[1], cls._stream()), "gemm_q8")

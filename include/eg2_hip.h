@@ -5,10 +5,12 @@
  * Device entry points take device pointers, unsigned sizes and a HIP stream
  * (hipStream_t passed as void*, NULL = the null stream). They enqueue work
  * and return 0 or a hipError_t code (eg2_hip_error_string names it); they
- * never synchronise. Q8_0 operands (activations and weights) use a split
- * layout: the int8 values stored as fp16 integers [rows][k] (exact) and one
- * float per 32-block [rows][k/32] holding the value of the block's fp16
- * scale. fp16 buffers are passed as uint16_t bit patterns. The attention
+ * never synchronise. Q8_0 activations use a split layout: the int8 values
+ * stored as fp16 integers [rows][k] (exact) and one float per 32-block
+ * holding the value of the block's fp16 scale, stored transposed as
+ * [k/32][rows] (the order the projection GEMM reads them in). Q8_0 weights
+ * use the fragment-major layout of eg2_q8_fragments. fp16 buffers are passed
+ * as uint16_t bit patterns. The attention
  * operands are fp32 values split into fp16 pairs, rows [hi | lo] with
  * hi = fp16(x), lo = fp16(x - hi).
  *
@@ -95,10 +97,12 @@ int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, vo
 /* y[n][m] (row stride ldy) = Q8_0 activations [n][k] . Q8_0 weights [m][k]^T
  * with the reference's arithmetic (gemma2.c:120-141): exact integer block
  * dots on MFMA, each scaled ((float)dot * d_w) * d_x and summed in block
- * order in fp32 -- bit-identical to the CPU path. Replaces
- * kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0. */
-int eg2_hip_gemm_q8(const uint16_t *xq, const float *xd, const uint16_t *wq, const float *wd, float *y, unsigned n,
-                    unsigned m, unsigned k, unsigned ldy, void *stream);
+ * order in fp32 -- bit-identical to the CPU path. xd holds the activation
+ * block scales [k/32][ldx] (ldx >= n); wf/wdf are the weights as written by
+ * eg2_q8_fragments. Replaces kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0,
+ * k <= 14336. */
+int eg2_hip_gemm_q8(const uint16_t *xq, const float *xd, unsigned ldx, const uint16_t *wf, const float *wdf,
+                    float *y, unsigned n, unsigned m, unsigned k, unsigned ldy, void *stream);
 
 /* ------------------------------------------------------------ executor phases
  * ei_gemma2_kfd_batch (gemma2_kfd.h) is stage + launch_staged(1) + collect.
@@ -127,6 +131,16 @@ int eg2_hip_device_check(char *err, size_t len);
  * integer bit patterns, d[rows][k/32] the exact float value of each fp16
  * scale (common.h:17-40). */
 void eg2_q8_split(const void *blocks, size_t rows, unsigned k, uint16_t *q, float *d);
+
+/* GGUF Q8_0 rows [rows][k] (34-byte blocks) -> the projection GEMM's
+ * fragment-major weight layout: wf [ceil(rows/32)][k/32][64][16] fp16 integer
+ * bit patterns, where entry (t, b, lane) holds row 32t + lane % 32, columns
+ * 32b + 16 * (lane / 32) .. +15, and wdf [ceil(rows/32)][k/32][64] the float
+ * value of that row's block scale. Rows past `rows` are zero.
+ * eg2_q8_fragment_halves gives the size of wf in fp16 values (wdf has 1/16
+ * of it). */
+void eg2_q8_fragments(const void *blocks, size_t rows, unsigned k, uint16_t *wf, float *wdf);
+size_t eg2_q8_fragment_halves(size_t rows, unsigned k);
 
 /* RoPE table for positions 0..n_pos-1: row p = [cos(theta_0..127) |
  * sin(theta_0..127)], theta_i = p * powf(base, -2i/256), computed with the

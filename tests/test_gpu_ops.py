@@ -62,11 +62,11 @@ def test_quantize_rows_bit_exact(eg2, gpu):
     x[1, :32] = 0.5
     x[1, 32:64] = 63.5
     x[2, ::2] = -x[2, ::2]
-    q, d = empty((96, N_EMBD), torch.float16, gpu), empty((96, 24), torch.float32, gpu)
+    q, d = empty((96, N_EMBD), torch.float16, gpu), empty((24, 96), torch.float32, gpu)
     eg2.ops.quantize_rows(dev(x, gpu), q, d)
     wq, wd = split(quantize_q8_0(x), N_EMBD)
     assert np.array_equal(qvals(q), wq)
-    assert np.array_equal(host(d), wd)
+    assert np.array_equal(host(d).T, wd)
 
 
 def test_embed_norm_quant_bit_exact(eg2, gpu):
@@ -78,7 +78,7 @@ def test_embed_norm_quant_bit_exact(eg2, gpu):
     w = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     scale = float(np.sqrt(np.float32(768)))
     x, xq, xd = empty((128, N_EMBD), torch.float32, gpu), empty((128, N_EMBD), torch.float16, gpu), \
-        empty((128, 24), torch.float32, gpu)
+        empty((24, 128), torch.float32, gpu)
     eg2.ops.embed_norm_quant(dev(table.view(np.uint8), gpu), dev(ids, gpu), scale, dev(w, gpu), 1e-6, x, xq, xd)
     o = oracle()
     want_x = np.zeros((128, N_EMBD), np.float32)
@@ -90,7 +90,7 @@ def test_embed_norm_quant_bit_exact(eg2, gpu):
         o.or_rms_norm_quantize_q8_0(fptr(want_x[t]), fptr(w), N_EMBD, 1e-6, vptr(blocks[t]))
     wq, wd = split(blocks, N_EMBD)
     assert np.array_equal(qvals(xq), wq)
-    assert np.array_equal(host(xd), wd)
+    assert np.array_equal(host(xd).T, wd)
 
 
 @pytest.mark.parametrize("with_next", [True, False])
@@ -103,7 +103,7 @@ def test_residual_norm_quant_bit_exact(eg2, gpu, with_next):
     pw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     nw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     xg = dev(x, gpu)
-    xq, xd = empty((rows, N_EMBD), torch.float16, gpu), empty((rows, 24), torch.float32, gpu)
+    xq, xd = empty((rows, N_EMBD), torch.float16, gpu), empty((24, rows), torch.float32, gpu)
     eg2.ops.residual_norm_quant(xg, dev(h, gpu), dev(pw, gpu), dev(nw, gpu) if with_next else None, 1e-6, xq, xd)
     o = oracle()
     want = x.copy()
@@ -115,7 +115,7 @@ def test_residual_norm_quant_bit_exact(eg2, gpu, with_next):
     if with_next:
         wq, wd = split(blocks, N_EMBD)
         assert np.array_equal(qvals(xq), wq)
-        assert np.array_equal(host(xd), wd)
+        assert np.array_equal(host(xd).T, wd)
 
 
 @pytest.mark.parametrize("base", [10000.0, 1000000.0])
@@ -154,14 +154,14 @@ def test_gelu_quant_matches_up_to_tanh_ulps(eg2, gpu):
     rows = 128
     gate = (RNG.standard_normal((rows, N_FF)) * 2).astype(np.float32)
     up = RNG.standard_normal((rows, N_FF)).astype(np.float32)
-    gq, gd = empty((rows, N_FF), torch.float16, gpu), empty((rows, 36), torch.float32, gpu)
+    gq, gd = empty((rows, N_FF), torch.float16, gpu), empty((36, rows), torch.float32, gpu)
     eg2.ops.gelu_quant(dev(np.concatenate([gate, up], 1), gpu), gq, gd)
     o = oracle()
     blocks = np.zeros((rows, 36), dtype=Q8)
     for t in range(rows):
         o.or_gelu_mul_quantize_q8_0(fptr(gate[t]), fptr(up[t]), N_FF, vptr(blocks[t]))
     wq, wd = split(blocks, N_FF)
-    gq, gd = qvals(gq), host(gd)
+    gq, gd = qvals(gq), host(gd).T
     same_d = gd == wd
     assert same_d.mean() > 0.99
     qd = np.abs(gq.astype(np.int32) - wq).reshape(rows, 36, 32)
@@ -170,9 +170,16 @@ def test_gelu_quant_matches_up_to_tanh_ulps(eg2, gpu):
 
 
 def device_q8(blocks, k, gpu):
-    """Oracle Q8_0 blocks -> the kernels' layout (fp16 integers + float scales)."""
+    """Oracle Q8_0 activation blocks -> the kernels' layout (fp16 integers
+    [rows, k] + float scales transposed [k/32, rows])."""
     q, d = split(blocks, k)
-    return dev(q.astype(np.float16), gpu), dev(d, gpu)
+    return dev(q.astype(np.float16), gpu), dev(d.T, gpu)
+
+
+def device_weights(eg2, blocks, k, gpu):
+    """Oracle Q8_0 weight blocks -> the GEMM's fragment-major layout."""
+    wf, wdf = eg2.q8_fragments(blocks.view(np.uint8), blocks.shape[0], k)
+    return dev(wf, gpu), dev(wdf, gpu)
 
 
 @pytest.mark.parametrize("n,m,k", [(512, 2304, 768), (2048, 1280, 768), (2048, 768, 1152), (33, 40, 64),
@@ -186,7 +193,7 @@ def test_gemm_q8_bit_exact(eg2, gpu, n, m, k):
     xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
     xb[0, 0]["qs"][:] = -128  # the most negative Q8_0 value round-trips too
     y = empty((n, m), torch.float32, gpu)
-    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_q8(w, k, gpu), y)
+    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_weights(eg2, w, k, gpu), y)
     assert np.array_equal(host(y), OL.gemm_q8_0(w, xb))
 
 
@@ -198,7 +205,7 @@ def test_gemm_q8_strided_output(eg2, gpu):
     w = quantize_q8_0((RNG.standard_normal((m, k)) * 0.02).astype(np.float32))
     xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
     y = torch.full((n, 160), 7.0, dtype=torch.float32, device=gpu)
-    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_q8(w, k, gpu), y)
+    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_weights(eg2, w, k, gpu), y, m=m)
     got = host(y)
     assert np.array_equal(got[:, :m], OL.gemm_q8_0(w, xb))
     assert (got[:, m:] == 7.0).all()
@@ -224,10 +231,10 @@ def run_attention(eg2, gpu, q, k, v, offsets, window):
     import torch
 
     T = q.shape[0]
-    cq, cd = empty((T, N_EMBD), torch.float16, gpu), empty((T, 24), torch.float32, gpu)
+    cq, cd = empty((T, N_EMBD), torch.float16, gpu), empty((24, T), torch.float32, gpu)
     eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), dev(split_pairs(v), gpu),
                       offsets, window, cq, cd)
-    return qvals(cq), host(cd)
+    return qvals(cq), np.ascontiguousarray(host(cd).T)
 
 
 def attention_double(q, k, v, offsets, window):

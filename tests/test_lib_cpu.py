@@ -56,9 +56,11 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     lib = eg2.lib()
     inval = 1  # hipErrorInvalidValue
     p = C.c_void_p(16)
-    assert lib.eg2_hip_gemm_q8(p, p, p, p, p, 4, 4, 33, 4, None) == inval  # k % 32
-    assert lib.eg2_hip_gemm_q8(p, p, p, p, p, 4, 8, 32, 4, None) == inval  # ldy < m
-    assert lib.eg2_hip_gemm_q8(None, p, p, p, p, 4, 4, 32, 4, None) == inval
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 4, 33, 4, None) == inval  # k % 32
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 8, 32, 4, None) == inval  # ldy < m
+    assert lib.eg2_hip_gemm_q8(p, p, 3, p, p, p, 4, 4, 32, 4, None) == inval  # ldx < n
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 4, 32 * 449, 4, None) == inval  # k above the LDS limit
+    assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, p, 4, 4, 32, 4, None) == inval
     assert lib.eg2_hip_attention(p, p, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
     assert lib.eg2_hip_attention(p, p, p, p, p, 4, 99999, 32, p, p, None) == inval
     assert lib.eg2_hip_attention(p, p, p, None, p, 4, 0, 32, p, p, None) == inval
@@ -105,6 +107,29 @@ def test_q8_split_is_the_exact_decode(eg2):
     assert np.array_equal(d, blocks["d"].view(np.float16).astype(np.float32))
     deq = (q.reshape(10, 3, 32).astype(np.float32) * d[:, :, None]).reshape(10, 96)
     assert np.array_equal(deq, dequantize_q8_0(blocks))
+
+
+def test_q8_fragments_layout(eg2):
+    """Fragment-major weights: entry (t, b, lane) = row 32t + lane % 32,
+    columns 32b + 16 * (lane // 32) .. +15 of the block, with the row's
+    block scale; rows past the matrix are zero."""
+    rng = np.random.default_rng(1)
+    rows, k = 45, 96
+    blocks = quantize_q8_0((rng.standard_normal((rows, k)) * 0.02).astype(np.float32))
+    wf, wdf = eg2.q8_fragments(blocks.view(np.uint8), rows, k)
+    assert wf.shape == (2, 3, 64, 16) and wdf.shape == (2, 3, 64)
+    assert eg2.lib().eg2_q8_fragment_halves(rows, k) == wf.size
+    q, d = eg2.q8_split(blocks.view(np.uint8), rows, k)
+    for t in range(2):
+        for b in range(3):
+            for lane in range(64):
+                r = 32 * t + lane % 32
+                if r < rows:
+                    c0 = 32 * b + 16 * (lane // 32)
+                    assert np.array_equal(wf[t, b, lane], q[r, c0:c0 + 16])
+                    assert wdf[t, b, lane] == d[r, b]
+                else:
+                    assert not wf[t, b, lane].any() and wdf[t, b, lane] == 0
 
 
 @pytest.fixture(scope="module")
