@@ -15,8 +15,8 @@ hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
                                       float eps, _Float16* xq, float* xd, int rows, hipStream_t st);
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
-                               const int32_t* pos, float eps, _Float16* qs, _Float16* ks, _Float16* vs,
-                               int rows, hipStream_t st);
+                               const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
+                               _Float16* vt, int ldv, int rows, hipStream_t st);
 hipError_t launch_gelu_quant(const float* gu, _Float16* gq, float* gd, int rows, hipStream_t st);
 hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, int rows, hipStream_t st);
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);
@@ -27,13 +27,18 @@ hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t
 hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
 size_t gemm_q8_max_k();
-hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vs, const uint32_t* tiles,
-                            const uint32_t* tile_count, int grid, int window, int rows, _Float16* cq, float* cd,
-                            hipStream_t st);
+hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
+                            const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
+                            _Float16* cq, float* cd, hipStream_t st);
 
 // Query tiles for launch_attention: up to 32 tokens of one sequence each,
 // {first query, end, sequence start, sequence end}, for the sequences
 // [offsets[s], offsets[s+1]). Returns the tile count (<= offsets[batch]).
 unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles);
+
+// V^T column of every token: each sequence starts at a multiple of 32,
+// consecutive tokens take consecutive columns. Returns the column count
+// used (sequences rounded up to 32 tokens each).
+size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol);
 
 }  // namespace eg2

@@ -38,6 +38,9 @@
 namespace {
 
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
+// Transposed-v columns: every sequence (and the padding sequence) starts at
+// a multiple of 32, so at most kCap + 31 * (kCap + 1) columns, rounded to 32.
+constexpr unsigned kVtCols = (kCap + 31 * (kCap + 1) + 31) / 32 * 32;
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
 constexpr double kTimeoutSeconds = 30.0;  // src/gemma2_kfd.cpp:21
@@ -105,11 +108,11 @@ class Backend {
   // Workspace for kCap tokens.
   float *x_, *h_, *qkv_, *gu_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
   _Float16 *xq_, *cq_, *mid_q_;
-  _Float16 *qs_, *ks_, *vs_;
-  int32_t *ids_d_, *pos_d_;
+  _Float16 *qs_, *ks_, *vt_;
+  int32_t *ids_d_, *pos_d_, *vcol_d_;
   uint32_t *tiles_d_, *off_d_;  // tiles_d_: attention query tiles, then their count
   // Pinned staging.
-  int32_t *ids_h_, *pos_h_;
+  int32_t *ids_h_, *pos_h_, *vcol_h_;
   uint32_t *tiles_h_, *off_h_;
   float* out_h_;
 
@@ -322,9 +325,13 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   cd_ = dalloc<float>((size_t)kCap * (kEmbd / 32));
   qs_ = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
   ks_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
-  vs_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
+  // Columns no token writes are read (masked) by the attention kernel and
+  // must hold finite values: zero the buffer once.
+  vt_ = dalloc<_Float16>((size_t)2 * kHeadDim * kVtCols);
+  check(hipMemset(vt_, 0, (size_t)2 * kHeadDim * kVtCols * sizeof(_Float16)), "hipMemset");
   ids_d_ = dalloc<int32_t>(kCap);
   pos_d_ = dalloc<int32_t>(kCap);
+  vcol_d_ = dalloc<int32_t>(kCap);
   tiles_d_ = dalloc<uint32_t>(4 * kCap + 4);
   off_d_ = dalloc<uint32_t>(kCap + 1);
   pooled_ = dalloc<float>((size_t)kCap * kEmbd);
@@ -333,6 +340,7 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   mid_d_ = dalloc<float>((size_t)kCap * (kDenseFF / 32));
   ids_h_ = halloc<int32_t>(kCap);
   pos_h_ = halloc<int32_t>(kCap);
+  vcol_h_ = halloc<int32_t>(kCap);
   tiles_h_ = halloc<uint32_t>(4 * kCap + 4);
   off_h_ = halloc<uint32_t>(kCap + 1);
   out_h_ = halloc<float>((size_t)kCap * kEmbd);
@@ -369,8 +377,10 @@ void Backend::record_layers(unsigned rows) {
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
     launch("gemm_qkv", eg2::launch_gemm_q8(xq_, xd_, n, L.qkv.q, L.qkv.d, qkv_, n, L.qkv.m, kEmbd, kQKV, s));
-    launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, eps_, qs_, ks_, vs_, n, s));
-    launch("attention", eg2::launch_attention(qs_, ks_, vs_, tiles_d_, tiles_d_ + 4 * kCap, (n + 15) / 16, L.window,
+    launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, vcol_d_, eps_, qs_, ks_,
+                                                    vt_, kVtCols, n, s));
+    launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, tiles_d_, tiles_d_ + 4 * kCap,
+                                              (n + 15) / 16, L.window,
                                               n, cq_, cd_, s));
     launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, n, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
@@ -439,11 +449,15 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
     n_tiles += eg2::build_attention_tiles(pad, 1, tiles_h_ + 4 * n_tiles);
   }
   tiles_h_[4 * kCap] = n_tiles;
+  // Transposed-v columns: the padding rows form one more sequence.
+  const size_t cols = eg2::build_vt_columns(offsets, batch, vcol_h_);
+  for (unsigned t = n; t < rows; ++t) vcol_h_[t] = (int32_t)(cols + (t - n));
 
   poisoned_ = true;  // cleared only when the whole wave completed
   hipStream_t s = stream_;
   check(hipMemcpyAsync(ids_d_, ids_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
   check(hipMemcpyAsync(pos_d_, pos_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
+  check(hipMemcpyAsync(vcol_d_, vcol_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy columns");
   check(hipMemcpyAsync(tiles_d_, tiles_h_, 4 * n_tiles * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy tiles");
   check(hipMemcpyAsync(tiles_d_ + 4 * kCap, tiles_h_ + 4 * kCap, sizeof(uint32_t), hipMemcpyHostToDevice, s),
         "copy tiles");

@@ -14,17 +14,28 @@
 // fp32 accumulation: about 2^-21 relative error per product, i.e. fp32-level
 // attention. Softmax runs in fp32 (online, one pass over 32-key tiles).
 //
-// Layout: work is cut into query tiles of up to 32 tokens of ONE sequence
-// (host-built list: first query, end, sequence start, sequence end); the
-// key tiles of a query tile start at its sequence's first token. A query's
-// arithmetic therefore depends only on its own sequence, never on where the
-// sequence sits in the packed wave, so packed and single-sequence calls give
-// bit-identical results. One workgroup (one wave per query head; the three
-// waves share each 32-key K tile and transposed V tile in LDS) loops over
-// the tile list with a grid stride. Scores are computed transposed,
-// S^T = K . Q^T, so each lane owns one query (lane & 31) and 16 of the
-// tile's keys, and the softmax reductions stay in the lane plus one
-// exchange with lane ^ 32.
+// Work: query tiles of up to 32 tokens of ONE sequence (host-built list:
+// first query, end, sequence start, sequence end); the key tiles of a query
+// tile start at its sequence's first token, so a query's arithmetic depends
+// only on its own sequence and packed and single-sequence calls give
+// bit-identical results. One workgroup per query tile, one wave per query
+// head; the three waves share each 32-key tile of K and V^T in LDS.
+//
+// Data movement: K rows ([hi 256 | lo 256] fp16 per token) and V^T rows
+// (V transposed by the QK-norm/RoPE kernel into [hi|lo][256 dims][column],
+// each sequence starting at a 32-aligned column, so a key tile is 64
+// contiguous bytes per dimension) go from global memory straight into a
+// double-buffered LDS ring by DMA (global_load_lds_dwordx4), the next tile
+// in flight while the current one is used. 16-byte chunks are XOR-swizzled
+// so the MFMA fragment reads hit distinct banks.
+//
+// Scores are computed transposed, S^T = K . Q^T, so each lane owns one
+// query (lane & 31) and 16 of the tile's keys and the softmax reductions
+// stay in the lane plus one exchange with lane ^ 32. The K rows are fed to
+// the score MFMA in a permuted order chosen so that lane group g ends up
+// holding the probabilities of keys 8g..8g+7 and 16+8g..16+8g+7: exactly
+// the k-slots it supplies to the two P.V MFMAs, whose V^T operand is then
+// one aligned 16-byte chunk per lane.
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
@@ -35,24 +46,38 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kKvTile = 32;
-constexpr int kKStride = kHeadDim + 8;  // fp16 per K row in LDS
-constexpr int kVStride = kKvTile + 8;   // fp16 per transposed-V row in LDS
+constexpr int kKStage = kKvTile * 2 * kHeadDim * 2;  // [key][hi|lo][256] fp16 = 32 KB
+constexpr int kVStage = 2 * kHeadDim * kKvTile * 2;  // [hi|lo][dim][32 keys] fp16 = 32 KB
+constexpr int kStage = kKStage + kVStage;
+constexpr int kDmaPerStage = kStage / 1024;          // 1 KB DMA instructions per tile
 
 __device__ __forceinline__ floatx16 mfma(const half8& a, const half8& b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Key fed to row r of the score MFMA (see the header comment): r holds
+// register v = 4 * (r / 8) + r % 4 of lane group g = (r / 4) % 2, which is
+// to carry key 8g + v (v < 8) or 16 + 8g + (v - 8) (v >= 8).
+__device__ __forceinline__ int score_row_key(int r) {
+  const int v = 4 * (r >> 3) + (r & 3), g = (r >> 2) & 1;
+  return v < 8 ? 8 * g + v : 16 + 8 * g + (v - 8);
+}
+// Chunk swizzles: K rows hold 32 chunks of 16 bytes per half (key-XOR);
+// V^T rows hold 4 chunks (the GEMM's pattern).
+__device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+
 __global__ void __launch_bounds__(192)
-attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks,
-                 const _Float16* __restrict__ vs, const uint4* __restrict__ tiles,
+attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks, const _Float16* __restrict__ vt,
+                 int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ tiles,
                  const uint32_t* __restrict__ tile_count, int window, int rows, _Float16* __restrict__ cq,
                  float* __restrict__ cd) {
-  __shared__ __align__(16) _Float16 Kh[kKvTile * kKStride];
-  __shared__ __align__(16) _Float16 Kl[kKvTile * kKStride];
-  __shared__ __align__(16) _Float16 Vh[kHeadDim * kVStride];
-  __shared__ __align__(16) _Float16 Vl[kHeadDim * kVStride];
+  __shared__ __align__(16) unsigned char lds[2 * kStage];
 
-  const int tid = threadIdx.x, lane = tid & 63, head = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, head = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, j = lane & 31;
   const uint32_t count = *tile_count;
   for (uint32_t tile = blockIdx.x; tile < count; tile += gridDim.x) {
@@ -79,8 +104,32 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       kv_lo = min(kv_lo, (uint32_t)__shfl_xor((int)kv_lo, mk, 64));
       kv_hi = max(kv_hi, (uint32_t)__shfl_xor((int)kv_hi, mk, 64));
     }
-    // Key tiles are aligned to the sequence start.
+    kv_lo = __builtin_amdgcn_readfirstlane(kv_lo);
+    kv_hi = __builtin_amdgcn_readfirstlane(kv_hi);
+    // Key tiles are aligned to the sequence start; so are the V^T columns.
     const uint32_t k_first = kv_lo >= kv_hi ? kv_hi : seg_lo + ((kv_lo - seg_lo) & ~31u);
+    const int col_base = __builtin_amdgcn_readfirstlane(vcol[min(seg_lo, (uint32_t)rows - 1)]) - (int)seg_lo;
+
+    // DMA of key tile k0 into stage s: instructions q = head, head + 3, ...
+    // q < 32: K row of key q; lane L takes half L/32, stored chunk L%32 =
+    // global chunk (L%32) ^ q. q >= 32: V^T rows 16(q-32)..+15 of half
+    // (q-32)/16; lane L takes dim row L/4, stored chunk L%4 = global chunk
+    // (L%4) ^ vswz(row).
+    auto issue = [&](uint32_t k0, int s) {
+      unsigned char* base = lds + s * kStage;
+      for (int q = head; q < kDmaPerStage; q += 3) {
+        const _Float16* src;
+        if (q < kKvTile) {
+          const uint32_t key = min(k0 + q, (uint32_t)rows - 1);
+          src = ks + (size_t)key * (2 * kHeadDim) + (lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ q);
+        } else {
+          const int vq = q - kKvTile, hl = vq >> 4, d = 16 * (vq & 15) + (lane >> 2);
+          const int c = (lane & 3) ^ vswz(d);
+          src = vt + ((size_t)hl * kHeadDim + d) * ldv + (col_base + (int)k0) + 8 * c;
+        }
+        dma16(src, base + q * 1024);
+      }
+    };
 
     // Q^T operand: lane holds query t, dims 16s + 8g .. +7 for s = 0..15.
     // Rows of qs are [hi 768 | lo 768].
@@ -97,43 +146,36 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     for (int dt = 0; dt < 8; ++dt) acc[dt] = floatx16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    for (uint32_t k0 = k_first; k0 < kv_hi; k0 += kKvTile) {
-      __syncthreads();
-      // Rows past the wave (last tile of the last sequence) are read from the
-      // final row and masked below.
-      for (int c = tid; c < kKvTile * 32; c += 192) {
-        const int row = c >> 5, col = (c & 31) * 8;
-        const _Float16* src = ks + (size_t)min(k0 + row, (uint32_t)rows - 1) * (2 * kHeadDim) + col;
-        *reinterpret_cast<half8*>(&Kh[row * kKStride + col]) = *reinterpret_cast<const half8*>(src);
-        *reinterpret_cast<half8*>(&Kl[row * kKStride + col]) = *reinterpret_cast<const half8*>(src + kHeadDim);
-      }
-      for (int c = tid; c < kKvTile * 32; c += 192) {
-        const int key = c & 31, d0 = (c >> 5) * 8;
-        const _Float16* src = vs + (size_t)min(k0 + key, (uint32_t)rows - 1) * (2 * kHeadDim) + d0;
-        const half8 a = *reinterpret_cast<const half8*>(src);
-        const half8 b = *reinterpret_cast<const half8*>(src + kHeadDim);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          Vh[(d0 + i) * kVStride + key] = a[i];
-          Vl[(d0 + i) * kVStride + key] = b[i];
-        }
-      }
-      __syncthreads();
+    // Every wave has finished with both stages (previous tile of the grid
+    // stride) before the first DMA overwrites them.
+    __syncthreads();
+    if (k_first < kv_hi) issue(k_first, 0);
+    const int kkey = score_row_key(j);  // key row this lane feeds to the score MFMA
+    int stage = 0;
+    for (uint32_t k0 = k_first; k0 < kv_hi; k0 += kKvTile, stage ^= 1) {
+      // This tile's DMA has landed for every wave, and every wave is done
+      // with the other stage, which the next tile's DMA now refills.
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (k0 + kKvTile < kv_hi) issue(k0 + kKvTile, stage ^ 1);
+      const unsigned char* kst = lds + stage * kStage;
+      const unsigned char* vst = kst + kKStage;
 
       floatx16 s = floatx16{};
+      const unsigned char* krow = kst + kkey * 1024;
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
-        const half8 kh = *reinterpret_cast<const half8*>(&Kh[j * kKStride + 16 * st + 8 * g]);
-        const half8 kl = *reinterpret_cast<const half8*>(&Kl[j * kKStride + 16 * st + 8 * g]);
+        const int c = (2 * st + g) ^ kkey;
+        const half8 kh = *reinterpret_cast<const half8*>(krow + 16 * c);
+        const half8 kl = *reinterpret_cast<const half8*>(krow + 512 + 16 * c);
         s = mfma(kh, qh[st], s);
         s = mfma(kh, ql[st], s);
         s = mfma(kl, qh[st], s);
       }
-      // s[v] is 16x the score of key k0 + 8*(v/4) + 4*g + (v%4) for query t.
+      // s[v] is 16x the score of key k0 + (v < 8 ? 8g + v : 16 + 8g + v - 8).
       float mt = -INFINITY;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const uint32_t key = k0 + 8 * (v >> 2) + 4 * g + (v & 3);
+        const uint32_t key = k0 + (v < 8 ? 8 * g + v : 16 + 8 * g + (v - 8));
         const bool valid = key >= lo && key < hi;
         s[v] = valid ? s[v] * 0.0625f : -INFINITY;
         mt = fmaxf(mt, s[v]);
@@ -163,24 +205,17 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
 
-      // O^T += V^T . P^T. The k-slots of lane group g map to keys
-      // {4g..4g+3, 8+4g..8+4g+3} (first MFMA) and {16+4g.., 24+4g..} (second),
-      // matching the keys this lane holds probabilities for.
+      // O^T += V^T . P^T: lane group g supplies keys 8g..8g+7 (first MFMA)
+      // and 16+8g..16+8g+7 (second), i.e. V^T chunks g and 2 + g.
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int r = (dt * 32 + j) * kVStride;
-        const half4 a0 = *reinterpret_cast<const half4*>(&Vh[r + 4 * g]);
-        const half4 a1 = *reinterpret_cast<const half4*>(&Vh[r + 8 + 4 * g]);
-        const half4 a2 = *reinterpret_cast<const half4*>(&Vh[r + 16 + 4 * g]);
-        const half4 a3 = *reinterpret_cast<const half4*>(&Vh[r + 24 + 4 * g]);
-        const half4 b0 = *reinterpret_cast<const half4*>(&Vl[r + 4 * g]);
-        const half4 b1 = *reinterpret_cast<const half4*>(&Vl[r + 8 + 4 * g]);
-        const half4 b2 = *reinterpret_cast<const half4*>(&Vl[r + 16 + 4 * g]);
-        const half4 b3 = *reinterpret_cast<const half4*>(&Vl[r + 24 + 4 * g]);
-        const half8 vh0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        const half8 vh1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
-        const half8 vl0 = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-        const half8 vl1 = {b2[0], b2[1], b2[2], b2[3], b3[0], b3[1], b3[2], b3[3]};
+        const int d = dt * 32 + j, f = vswz(d);
+        const unsigned char* vh = vst + d * 64;
+        const unsigned char* vl = vst + (kHeadDim + d) * 64;
+        const half8 vh0 = *reinterpret_cast<const half8*>(vh + 16 * (g ^ f));
+        const half8 vh1 = *reinterpret_cast<const half8*>(vh + 16 * ((2 + g) ^ f));
+        const half8 vl0 = *reinterpret_cast<const half8*>(vl + 16 * (g ^ f));
+        const half8 vl1 = *reinterpret_cast<const half8*>(vl + 16 * ((2 + g) ^ f));
         acc[dt] = mfma(vh0, ph0, acc[dt]);
         acc[dt] = mfma(vh0, pl0, acc[dt]);
         acc[dt] = mfma(vl0, ph0, acc[dt]);
@@ -220,6 +255,9 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       if (g == 0) cd[(size_t)(head * (kHeadDim / kQK) + dt) * rows + t] = dq;
     }
   }
+  // The last tile's prefetch never runs past the key range, but a wave may
+  // still have DMA in flight if the loop ran no tile; drain before exit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
@@ -236,11 +274,20 @@ unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* ti
   return n;
 }
 
-hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vs, const uint32_t* tiles,
-                            const uint32_t* tile_count, int grid, int window, int rows, _Float16* cq, float* cd,
-                            hipStream_t st) {
-  if (rows <= 0 || grid <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(192), 0, st, qs, ks, vs,
+size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
+  size_t base = 0;
+  for (size_t s = 0; s < batch; ++s) {
+    for (size_t t = offsets[s]; t < offsets[s + 1]; ++t) vcol[t] = (int32_t)(base + (t - offsets[s]));
+    base += (offsets[s + 1] - offsets[s] + 31) / 32 * 32;
+  }
+  return base;
+}
+
+hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
+                            const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
+                            _Float16* cq, float* cd, hipStream_t st) {
+  if (rows <= 0 || grid <= 0 || ldv <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(192), 0, st, qs, ks, vt, ldv, vcol,
                      reinterpret_cast<const uint4*>(tiles), tile_count, window, rows, cq, cd);
   return hipGetLastError();
 }

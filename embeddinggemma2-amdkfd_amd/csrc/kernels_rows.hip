@@ -201,12 +201,15 @@ constexpr int kHeadStride = kHeadDim + 8;  // LDS row of one head: 8 banks apart
 // applied before the inverse, NeoX rotation of pairs (d, d+128) with the
 // host-built cos/sin row of this token's position, Q scaled by 0.0625 after
 // rotation. The fp32 results (bit-identical to the reference) are written as
-// split fp16 pairs for the attention kernel, rows [hi | lo]; q is stored
-// times 16 (exact) to keep its low half clear of fp16 subnormals.
+// split fp16 pairs for the attention kernel: q and k as rows [hi | lo] (q
+// times 16, exact, to keep its low half clear of fp16 subnormals), v
+// transposed as vt[hi|lo][dim][vcol[t]] so that a 32-key tile of a sequence
+// is one contiguous 64-byte run per dimension.
 __global__ void __launch_bounds__(64)
 qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w, const float* __restrict__ k_w,
-                    const float* __restrict__ rope, const int32_t* __restrict__ pos, float eps,
-                    _Float16* __restrict__ qs, _Float16* __restrict__ ks, _Float16* __restrict__ vs) {
+                    const float* __restrict__ rope, const int32_t* __restrict__ pos,
+                    const int32_t* __restrict__ vcol, float eps, _Float16* __restrict__ qs,
+                    _Float16* __restrict__ ks, _Float16* __restrict__ vt, int ldv) {
   constexpr int kRows = kHeads + 1;  // q heads, then k
   constexpr int half = kHeadDim / 2;
   __shared__ __align__(16) float rows[kRows][kHeadStride];
@@ -220,11 +223,16 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
     *reinterpret_cast<float4*>(&rows[e / kHeadDim][e % kHeadDim]) = *reinterpret_cast<const float4*>(src + e);
   }
   const float4 v = *reinterpret_cast<const float4*>(src + kRows * kHeadDim + 4 * lane);
-  _Float16* vrow = vs + (size_t)t * 2 * kHeadDim;
-  store_split(vrow, kHeadDim, 4 * lane + 0, v.x);
-  store_split(vrow, kHeadDim, 4 * lane + 1, v.y);
-  store_split(vrow, kHeadDim, 4 * lane + 2, v.z);
-  store_split(vrow, kHeadDim, 4 * lane + 3, v.w);
+  {
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    _Float16* vcol_ptr = vt + vcol[t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 h = (_Float16)vv[i];
+      vcol_ptr[(size_t)(4 * lane + i) * ldv] = h;
+      vcol_ptr[(size_t)(kHeadDim + 4 * lane + i) * ldv] = (_Float16)(vv[i] - (float)h);
+    }
+  }
   __syncthreads();
   // lanes 8r..8r+7 run the chains of head row r (r < 4); the rest repeat row 0
   const int hr = (lane >> 3) < kRows ? (lane >> 3) : 0;
@@ -404,9 +412,10 @@ hipError_t launch_residual_norm_quant(float* x, const float* h, const float* pos
 }
 
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
-                               const int32_t* pos, float eps, _Float16* qs, _Float16* ks, _Float16* vs,
-                               int rows, hipStream_t st) {
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, qs, ks, vs);
+                               const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
+                               _Float16* vt, int ldv, int rows, hipStream_t st) {
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, vcol, eps, qs, ks,
+                     vt, ldv);
   return hipGetLastError();
 }
 

@@ -72,26 +72,33 @@ int eg2_hip_residual_norm_quant(float* x, const float* h, const float* post_w, c
 }
 
 int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope_table,
-                         const int32_t* pos, float eps, uint16_t* qs, uint16_t* ks, uint16_t* vs, unsigned rows,
-                         void* stream) {
-  if (!qkv || !q_w || !k_w || !rope_table || !pos || !qs || !ks || !vs || rows == 0) return kInvalid;
-  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, eps, h16(qs), h16(ks), h16(vs), (int)rows,
-                                       as_stream(stream)));
+                         const int32_t* pos, const int32_t* vcol, float eps, uint16_t* qs, uint16_t* ks, uint16_t* vt,
+                         unsigned ldv, unsigned rows, void* stream) {
+  if (!qkv || !q_w || !k_w || !rope_table || !pos || !vcol || !qs || !ks || !vt || rows == 0 || ldv == 0 ||
+      ldv % 32 != 0 || ldv > (1u << 20))
+    return kInvalid;
+  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, vcol, eps, h16(qs), h16(ks), h16(vt),
+                                       (int)ldv, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vs, const uint32_t* tiles,
-                      const uint32_t* tile_count, unsigned grid, unsigned window, unsigned rows, uint16_t* cq,
-                      float* cd, void* stream) {
-  if (!qs || !ks || !vs || !tiles || !tile_count || !cq || !cd || rows == 0 || grid == 0 || grid > 65536 ||
-      window > 4096u)
+int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const int32_t* vcol,
+                      const uint32_t* tiles, const uint32_t* tile_count, unsigned grid, unsigned window,
+                      unsigned rows, uint16_t* cq, float* cd, void* stream) {
+  if (!qs || !ks || !vt || !vcol || !tiles || !tile_count || !cq || !cd || rows == 0 || grid == 0 ||
+      grid > 65536 || window > 4096u || ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
     return kInvalid;
-  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vs), tiles, tile_count, (int)grid, (int)window, (int)rows,
-                                    h16(cq), cd, as_stream(stream)));
+  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, vcol, tiles, tile_count, (int)grid,
+                                    (int)window, (int)rows, h16(cq), cd, as_stream(stream)));
 }
 
 unsigned eg2_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
   if (!offsets || !tiles) return 0;
   return eg2::build_attention_tiles(offsets, batch, tiles);
+}
+
+size_t eg2_attention_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
+  if (!offsets || !vcol) return 0;
+  return eg2::build_vt_columns(offsets, batch, vcol);
 }
 
 int eg2_hip_gelu_quant(const float* gate_up, uint16_t* gq, float* gd, unsigned rows, void* stream) {

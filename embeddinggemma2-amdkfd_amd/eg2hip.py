@@ -103,9 +103,10 @@ SIGNATURES = {
     "eg2_op_name": (C.c_char_p, [_u]),
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
-    "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
+    "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _u, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
     "eg2_attention_tiles": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
+    "eg2_attention_vt_columns": (C.c_size_t, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
@@ -262,6 +263,17 @@ def rope_table(base, n_pos=N_CTX):
     return t
 
 
+def attention_vt_columns(offsets):
+    """(vcol int32 [offsets[-1]], ldv): the transposed-v column of every token
+    and a row pitch (multiple of 32) that holds them."""
+    import numpy as np
+
+    offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+    vcol = np.zeros(max(1, int(offsets[-1])), dtype=np.int32)
+    cols = lib().eg2_attention_vt_columns(offs, len(offsets) - 1, vcol.ctypes.data)
+    return vcol, max(32, (cols + 31) // 32 * 32)
+
+
 def q8_fragments(blocks_u8, rows, k):
     """GGUF Q8_0 bytes [rows, k] -> the projection GEMM's fragment-major weights
     (wf: fp16 integers [ceil(rows/32), k/32, 64, 16], wdf: float32 scales
@@ -313,14 +325,16 @@ class ops:
               "residual_norm_quant")
 
     @classmethod
-    def qk_norm_rope(cls, qkv, q_w, k_w, table, pos, eps, qh, kh, vh):
-        check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos), eps,
-                                         cls._p(qh), cls._p(kh), cls._p(vh), qkv.shape[0], cls._stream()),
-              "qk_norm_rope")
+    def qk_norm_rope(cls, qkv, q_w, k_w, table, pos, vcol, eps, qh, kh, vt):
+        """vt: [2, 256, ldv] transposed v, written at columns vcol (attention_vt_columns)."""
+        check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos),
+                                         cls._p(vcol), eps, cls._p(qh), cls._p(kh), cls._p(vt), vt.shape[2],
+                                         qkv.shape[0], cls._stream()), "qk_norm_rope")
 
     @classmethod
-    def attention(cls, qs, ks, vs, offsets, window, cq, cd):
-        """Packed attention over sequences [offsets[s], offsets[s+1])."""
+    def attention(cls, qs, ks, vt, vcol, offsets, window, cq, cd):
+        """Packed attention over sequences [offsets[s], offsets[s+1]); vt and
+        vcol as written by qk_norm_rope."""
         import numpy as np
         import torch
 
@@ -330,7 +344,7 @@ class ops:
         tiles[-1] = n
         dev = torch.from_numpy(tiles.view(np.int32)).to(qs.device)
         grid = max(1, (qs.shape[0] + 15) // 16)
-        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vs), cls._p(dev),
+        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol), cls._p(dev),
                                       C.c_void_p(dev.data_ptr() + 4 * (len(tiles) - 1)), grid, window, qs.shape[0],
                                       cls._p(cq), cls._p(cd), cls._stream()), "attention")
         torch.cuda.current_stream().synchronize()  # keeps `dev` alive until the kernel ran

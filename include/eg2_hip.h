@@ -48,31 +48,40 @@ int eg2_hip_residual_norm_quant(float *x, const float *h, const float *post_w, c
 /* kernels.c:233-264 ei_qk_norm_rope_qk_inplace on rows of the fused
  * [q 768 | k 256 | v 256] projection; rope_table[pos][0..127] = cos,
  * [128..255] = sin (eg2_rope_table). The fp32 results are written as split
- * fp16 rows: qs [rows][2][768] holding 16*q (q includes the 0.0625 scale),
- * ks [rows][2][256], vs [rows][2][256] (v unchanged).
+ * fp16 values: qs [rows][2][768] holding 16*q (q includes the 0.0625 scale),
+ * ks [rows][2][256], and v (unchanged) transposed into vt [2][256][ldv] at
+ * column vcol[t] (eg2_attention_vt_columns). ldv % 32 == 0.
  * Replaces kernels/eg2.c:204-217 eg2_norm_rope. */
 int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, const float *rope_table,
-                         const int32_t *pos, float eps, uint16_t *qs, uint16_t *ks, uint16_t *vs, unsigned rows,
-                         void *stream);
+                         const int32_t *pos, const int32_t *vcol, float eps, uint16_t *qs, uint16_t *ks, uint16_t *vt,
+                         unsigned ldv, unsigned rows, void *stream);
 
 /* kernels.c:324-360 ei_attention_mha_range over packed sequences
  * (engine.c:850-873): each token attends to the keys of its own sequence,
  * limited to |t - s| <= window/2 when window > 0; 3 query heads share one KV
- * head, head_dim 256. Inputs are the split rows of eg2_hip_qk_norm_rope.
- * The work list `tiles` (device, 4 uint32 per tile, from
- * eg2_attention_tiles) holds *tile_count (device) query tiles; `grid`
- * workgroups stride over it. The fp32 context is quantized to Q8_0
- * (quants.c:97-177) into cq/cd. A sequence's result does not depend on its
- * place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
-int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vs, const uint32_t *tiles,
-                      const uint32_t *tile_count, unsigned grid, unsigned window, unsigned rows, uint16_t *cq,
-                      float *cd, void *stream);
+ * head, head_dim 256. Inputs are the split q/k rows and the transposed v of
+ * eg2_hip_qk_norm_rope (same vt, ldv and vcol; vt columns that no token
+ * wrote must hold finite values, e.g. zeros). The work list `tiles`
+ * (device, 4 uint32 per tile, from eg2_attention_tiles) holds *tile_count
+ * (device) query tiles; `grid` workgroups stride over it. The fp32 context
+ * is quantized to Q8_0 (quants.c:97-177) into cq [rows][768] and cd
+ * [24][rows]. A sequence's result does not depend on its place in the wave.
+ * Replaces kernels/eg2.c:145-170 eg2_attention256. */
+int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const int32_t *vcol,
+                      const uint32_t *tiles, const uint32_t *tile_count, unsigned grid, unsigned window,
+                      unsigned rows, uint16_t *cq, float *cd, void *stream);
 
 /* Host: the query-tile list of a packed wave with sequences
  * [offsets[s], offsets[s+1]) -- up to 32 queries of one sequence per tile as
  * {first query, end, sequence start, sequence end}. `tiles` must hold
  * 4 * offsets[batch] entries; returns the tile count. */
 unsigned eg2_attention_tiles(const size_t *offsets, size_t batch, uint32_t *tiles);
+
+/* Host: the transposed-v column of every token (vcol[offsets[batch]]):
+ * each sequence starts at a multiple of 32 and its tokens take consecutive
+ * columns. Returns the columns used, at most offsets[batch] + 31 * batch;
+ * vt needs ldv >= that, rounded up to 32. */
+size_t eg2_attention_vt_columns(const size_t *offsets, size_t batch, int32_t *vcol);
 
 /* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
  * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */

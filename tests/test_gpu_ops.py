@@ -129,15 +129,24 @@ def test_qk_norm_rope_bit_exact(eg2, gpu, base):
     pos = RNG.integers(0, 2048, rows).astype(np.int32)
     pos[:3] = [0, 1, 2047]
     table = eg2.rope_table(base)
-    qs, ks, vs = (empty((rows, 2 * n), torch.float16, gpu) for n in (N_EMBD, HEAD_DIM, HEAD_DIM))
-    eg2.ops.qk_norm_rope(dev(qkv, gpu), dev(qw, gpu), dev(kw, gpu), dev(table, gpu), dev(pos, gpu), 1e-6, qs, ks, vs)
+    qs, ks = (empty((rows, 2 * n), torch.float16, gpu) for n in (N_EMBD, HEAD_DIM))
+    # v goes transposed to columns vcol: here two sequences, so the second
+    # starts at the next multiple of 32
+    vcol, ldv = eg2.attention_vt_columns([0, 40, rows])
+    vt = empty((2, HEAD_DIM, ldv), torch.float16, gpu)
+    eg2.ops.qk_norm_rope(dev(qkv, gpu), dev(qw, gpu), dev(kw, gpu), dev(table, gpu), dev(pos, gpu), dev(vcol, gpu),
+                         1e-6, qs, ks, vt)
+    assert vcol[39] == 39 and vcol[40] == 64
+    vt = host(vt)
+    assert not vt[:, :, 40:64].any()  # columns between the sequences stay untouched
+    vs = torch.from_numpy(np.concatenate([vt[0][:, vcol].T, vt[1][:, vcol].T], axis=1))
     o = oracle()
     q, k = qkv[:, :N_EMBD].copy(), qkv[:, N_EMBD:N_EMBD + HEAD_DIM].copy()
     for t in range(rows):
         o.or_qk_norm_rope_qk_inplace(fptr(q[t]), fptr(k[t]), fptr(qw), fptr(kw), int(pos[t]), base, 1e-6)
     v = qkv[:, N_EMBD + HEAD_DIM:]
     for got, want in ((qs, q * np.float32(16)), (ks, k), (vs, v)):
-        got = host(got)
+        got = host(got) if got.is_cuda else got.numpy()
         assert np.array_equal(got.view(np.uint16), split_pairs(want).view(np.uint16))
         # hi + lo recovers the fp32 value to 22 significand bits.
         w = got.shape[1] // 2
@@ -227,12 +236,24 @@ def segments_log_uniform(rng, n_seg=16, total=2048, lo=8, hi=512):
     return lens
 
 
-def run_attention(eg2, gpu, q, k, v, offsets, window):
+def transposed_v(eg2, v, offsets, gpu, fill=0.0):
+    """v [T, 256] -> (vt [2, 256, ldv] split fp16 at the columns of
+    eg2_attention_vt_columns, vcol); other columns hold `fill`."""
+    vcol, ldv = eg2.attention_vt_columns(offsets)
+    vt = np.full((2, HEAD_DIM, ldv), fill, dtype=np.float16)
+    pairs = split_pairs(v)
+    vt[0][:, vcol] = pairs[:, :HEAD_DIM].T
+    vt[1][:, vcol] = pairs[:, HEAD_DIM:].T
+    return dev(vt, gpu), dev(vcol, gpu)
+
+
+def run_attention(eg2, gpu, q, k, v, offsets, window, fill=0.0):
     import torch
 
     T = q.shape[0]
     cq, cd = empty((T, N_EMBD), torch.float16, gpu), empty((24, T), torch.float32, gpu)
-    eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), dev(split_pairs(v), gpu),
+    vt, vcol = transposed_v(eg2, v, offsets, gpu, fill)
+    eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), vt, vcol,
                       offsets, window, cq, cd)
     return qvals(cq), np.ascontiguousarray(host(cd).T)
 
@@ -325,6 +346,21 @@ def test_attention_independent_of_packing(eg2, gpu, window):
         a, b = offsets[s], offsets[s + 1]
         sq, sd = run_attention(eg2, gpu, q[a:b], k[a:b], v[a:b], [0, b - a], window)
         assert np.array_equal(sq, cq[a:b]) and np.array_equal(sd, cd[a:b])
+
+
+def test_attention_ignores_unused_vt_columns(eg2, gpu):
+    """Key tiles overrun short sequences into their 32-aligned column
+    padding; those keys are masked, so any finite filler gives the same bits."""
+    rng = np.random.default_rng(9)
+    lens = [3, 40, 1, 70]
+    T = sum(lens)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    q = (rng.standard_normal((T, N_EMBD)) * 0.0625).astype(np.float32)
+    k = rng.standard_normal((T, HEAD_DIM)).astype(np.float32)
+    v = rng.standard_normal((T, HEAD_DIM)).astype(np.float32)
+    a = run_attention(eg2, gpu, q, k, v, offsets, 0, fill=0.0)
+    b = run_attention(eg2, gpu, q, k, v, offsets, 0, fill=1000.0)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
 
 
 def test_pool_and_l2_bit_exact(eg2, gpu):

@@ -61,13 +61,26 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 3, p, p, p, 4, 4, 32, 4, None) == inval  # ldx < n
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 4, 32 * 449, 4, None) == inval  # k above the LDS limit
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, p, 4, 4, 32, 4, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention(p, p, p, p, p, 4, 99999, 32, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, None, p, 4, 0, 32, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 48, p, p, p, 4, 0, 32, p, p, None) == inval  # ldv % 32
+    assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, p, 1e-6, p, p, p, 40, 4, None) == inval  # ldv % 32
     assert lib.eg2_hip_quantize_rows(p, 96, p, p, 1, None) == inval  # k % 64
     assert lib.eg2_hip_l2_prefix(p, 768, 769, 1, None) == inval
     assert lib.eg2_hip_l2_prefix(p, 768, 100, 1, None) == inval
     assert lib.eg2_hip_pool_l2(p, p, p, 0, None) == inval
+
+
+def test_vt_columns_align_each_sequence(eg2):
+    offs = [0, 1, 33, 97, 98, 200]
+    vcol, ldv = eg2.attention_vt_columns(offs)
+    base = 0
+    for s in range(len(offs) - 1):
+        n = offs[s + 1] - offs[s]
+        assert list(vcol[offs[s]:offs[s + 1]]) == list(range(base, base + n))
+        base += (n + 31) // 32 * 32
+    assert ldv == base and ldv <= offs[-1] + 31 * (len(offs) - 1)
 
 
 def test_attention_tiles_cover_each_sequence(eg2):
