@@ -31,7 +31,7 @@ hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float
                             const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
                             _Float16* cq, float* cd, hipStream_t st);
 
-// Query tiles for launch_attention: up to 32 tokens of one sequence each,
+// Query tiles for launch_attention: up to 16 tokens of one sequence each,
 // {first query, end, sequence start, sequence end}, for the sequences
 // [offsets[s], offsets[s+1]). Returns the tile count (<= offsets[batch]).
 unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles);

@@ -380,7 +380,7 @@ void Backend::record_layers(unsigned rows) {
     launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, vcol_d_, eps_, qs_, ks_,
                                                     vt_, kVtCols, n, s));
     launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, tiles_d_, tiles_d_ + 4 * kCap,
-                                              (n + 15) / 16, L.window,
+                                              (n + 7) / 8, L.window,
                                               n, cq_, cd_, s));
     launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, n, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));

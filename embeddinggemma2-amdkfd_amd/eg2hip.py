@@ -343,7 +343,7 @@ class ops:
         n = lib().eg2_attention_tiles(offs, len(offsets) - 1, tiles.ctypes.data)
         tiles[-1] = n
         dev = torch.from_numpy(tiles.view(np.int32)).to(qs.device)
-        grid = max(1, (qs.shape[0] + 15) // 16)
+        grid = max(1, (qs.shape[0] + 7) // 8)
         check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol), cls._p(dev),
                                       C.c_void_p(dev.data_ptr() + 4 * (len(tiles) - 1)), grid, window, qs.shape[0],
                                       cls._p(cq), cls._p(cd), cls._stream()), "attention")

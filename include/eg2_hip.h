@@ -72,7 +72,7 @@ int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt
                       unsigned rows, uint16_t *cq, float *cd, void *stream);
 
 /* Host: the query-tile list of a packed wave with sequences
- * [offsets[s], offsets[s+1]) -- up to 32 queries of one sequence per tile as
+ * [offsets[s], offsets[s+1]) -- up to 16 queries of one sequence per tile as
  * {first query, end, sequence start, sequence end}. `tiles` must hold
  * 4 * offsets[batch] entries; returns the tile count. */
 unsigned eg2_attention_tiles(const size_t *offsets, size_t batch, uint32_t *tiles);

@@ -91,11 +91,11 @@ def test_attention_tiles_cover_each_sequence(eg2):
     t = tiles[:4 * n].reshape(n, 4)
     covered = np.zeros(200, int)
     for q0, q1, lo, hi in t:
-        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0
+        assert lo <= q0 < q1 <= hi and q1 - q0 <= 16 and (q0 - lo) % 16 == 0
         assert [lo, hi] in [[offs[s], offs[s + 1]] for s in range(len(offs) - 1)]
         covered[q0:q1] += 1
     assert (covered == 1).all()
-    assert n == sum((offs[s + 1] - offs[s] + 31) // 32 for s in range(len(offs) - 1))
+    assert n == sum((offs[s + 1] - offs[s] + 15) // 16 for s in range(len(offs) - 1))
 
 
 @pytest.mark.parametrize("base", [10000.0, 1000000.0])
