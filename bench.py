@@ -77,6 +77,52 @@ def time_gemm(eg2, torch, steps, warmup):
     return ms
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q8_gate_up_2048x2304x768_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate|up GEMM from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), or
+    None when that summary is absent."""
+    if not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    vals = {}
+    for line in open(TRAFFIC_PROFILE):
+        if line.startswith("- ") and ":" in line:
+            k, v = line[2:].split(":", 1)
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except ValueError:
+                pass
+    if "calibrated_fetch_bytes_per_launch" not in vals or "calibrated_write_bytes_per_launch" not in vals:
+        return None
+    return int(vals["calibrated_fetch_bytes_per_launch"] + vals["calibrated_write_bytes_per_launch"])
+
+
+def kernel_only(kind, steps):
+    """Counter-collection mode: only the gate|up GEMM, or a plain device copy
+    of COPY_MIB (the calibration kernel for FETCH_SIZE/WRITE_SIZE)."""
+    import torch
+
+    import __graft_entry__
+
+    eg2 = __graft_entry__._package()
+    torch.cuda.set_device(0)
+    if kind == "gate_up":
+        ms = time_gemm(eg2, torch, steps, 2)
+        print(json.dumps({"kernel": "gemm_q8 gate|up 2048x2304x768", "avg_us": round(ms * 1e3, 2), "launches": steps + 2}))
+    else:
+        src = torch.empty(COPY_MIB << 18, dtype=torch.float32, device="cuda:0").uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel": "copy", "bytes_each_way": COPY_MIB << 20, "launches": steps}))
+
+
+COPY_MIB = 256
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,11 +130,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", choices=["gate_up", "copy"],
+                    help="run only the dominant GEMM (or the copy calibration kernel) for counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has a single MI355X and this path runs "
               "independent waves per GPU (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.kernel_only:
+        kernel_only(args.kernel_only, args.steps)
+        return
 
     import numpy as np
     import torch
@@ -170,7 +221,7 @@ def main():
                    "attention": "full within sequence, RoPE base 1e4"},
         "roofline": {"bound": "mfma", "kernel": "gemm_q8 gate|up 2048x2304x768",
                      "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": measured_traffic(),
                      "avg_us": round(gemm_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),
