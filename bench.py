@@ -56,12 +56,12 @@ def time_gemm(eg2, torch, steps, warmup):
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device="cpu").manual_seed(0)
-    # Q8_0 operands in the kernel layouts: int8 values held as fp16 integers,
-    # activation scales [k/32][n], weights fragment-major.
-    xq = torch.randint(-127, 128, (GEMM_N, GEMM_K), generator=g).to(torch.float16).to(dev)
-    wq = torch.randint(-127, 128, (GEMM_M // 32, GEMM_K // 32, 64, 16), generator=g).to(torch.float16).to(dev)
+    # Q8_0 operands in the kernel layouts: int8 row tiles, block scales
+    # transposed [k/32][rows].
+    xq = torch.randint(-127, 128, (eg2.q8_tile_bytes(GEMM_N, GEMM_K),), generator=g, dtype=torch.int8).to(dev)
+    wq = torch.randint(-127, 128, (eg2.q8_tile_bytes(GEMM_M, GEMM_K),), generator=g, dtype=torch.int8).to(dev)
     xd = (torch.rand((GEMM_K // 32, GEMM_N), generator=g) * 0.01).to(dev)
-    wd = (torch.rand((GEMM_M // 32, GEMM_K // 32, 64), generator=g) * 0.001).to(dev)
+    wd = (torch.rand((GEMM_K // 32, GEMM_M), generator=g) * 0.001).to(dev)
     y = torch.empty((GEMM_N, GEMM_M), dtype=torch.float32, device=dev)
     for _ in range(warmup):
         eg2.ops.gemm_q8(xq, xd, wq, wd, y)

@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace eg2 {
@@ -20,6 +21,20 @@ constexpr int kVocab = 262144;  // model.h:15
 constexpr int kQK = 32;         // Q8_0 block length (quants.h:6)
 constexpr int kQKVCols = kEmbd + 2 * kHeadDim;  // fused Q|K|V projection width
 constexpr int kDenseFF = 3072;                  // dense head hidden width
+
+// Q8_0 values of activations and weights are stored as int8 "row tiles",
+// [rows/32][k/32][2][32][16]: each block of 32 rows x 32 values is 1 KB in
+// the register order of the int8 MFMA operand. Byte offset of value e of
+// row r in a buffer with nb = k/32 blocks per row (rows padded to 32).
+__host__ __device__ inline size_t q8_tile_offset(size_t r, unsigned e, unsigned nb) {
+  return (((r >> 5) * nb + (e >> 5)) * 2 + ((e >> 4) & 1)) * 512 + (r & 31) * 16 + (e & 15);
+}
+
+// Four int8 values (low byte of each) in one little-endian word.
+__device__ __forceinline__ uint32_t pack_i8x4(int32_t a, int32_t b, int32_t c, int32_t d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
 
 // fp32 -> fp16 bits with the reference's rounding (quants.c:13-37): the
 // dropped mantissa bits round half-up in magnitude (not to nearest-even),

@@ -1,7 +1,8 @@
 // Launchers of the gfx950 kernels (host side). All pointers are device
 // pointers; row counts are token rows of the packed wave. Q8_0 activations
-// are fp16 integers [rows][k] plus one float scale per 32-block stored
-// transposed, [k/32][rows]; attention operands are split fp16 rows [hi | lo].
+// are int8 row tiles (q8_tile_offset; buffers hold the rows rounded up to
+// 32) plus one float scale per 32-block stored transposed, [k/32][rows];
+// attention operands are split fp16 rows [hi | lo].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -10,26 +11,25 @@
 namespace eg2 {
 
 hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int rows, float embed_scale,
-                                   const float* norm_w, float eps, float* x, _Float16* xq, float* xd,
+                                   const float* norm_w, float eps, float* x, int8_t* xq, float* xd,
                                    hipStream_t st);
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
-                                      float eps, _Float16* xq, float* xd, int rows, hipStream_t st);
+                                      float eps, int8_t* xq, float* xd, int rows, hipStream_t st);
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
                                const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
                                _Float16* vt, int ldv, int rows, hipStream_t st);
-hipError_t launch_gelu_quant(const float* gu, _Float16* gq, float* gd, int rows, hipStream_t st);
-hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, int rows, hipStream_t st);
+hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, hipStream_t st);
+hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st);
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);
 hipError_t launch_pool_l2(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st);
 hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t st);
-// xd: activation block scales transposed, [k/32][ldx]; wf/wdf: weights in
-// the fragment-major layout of eg2_q8_fragments.
-hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
+// xq/wq: int8 row tiles of the activations [n][k] and weights [m][k];
+// xd/wd: their block scales transposed, [k/32][ldx] and [k/32][ldw].
+hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
-size_t gemm_q8_max_k();
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
                             const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
-                            _Float16* cq, float* cd, hipStream_t st);
+                            int8_t* cq, float* cd, hipStream_t st);
 
 // Query tiles for launch_attention: up to 16 tokens of one sequence each,
 // {first query, end, sequence start, sequence end}, for the sequences

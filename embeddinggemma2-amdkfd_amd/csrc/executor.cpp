@@ -4,9 +4,9 @@
 // Create (src/gemma2_kfd.cpp:86-155): select the gfx950 device, read the
 // `gemma-embedding` hyper-parameters and tensors from the caller's ei_gguf
 // (model.c:61-105 names, Q8_0 matrices), repack every matrix once into the
-// projection GEMM's fragment-major Q8_0 layout (the int8 values as exact
-// fp16 integers + one float scale per 32-block, see eg2_q8_fragments),
-// fuse Q|K|V and gate|up into single projections, upload the raw Q8_0
+// projection GEMM's operand layout (the int8 values as row tiles + the
+// block scales transposed, see eg2_q8_weight_tiles), fuse Q|K|V and
+// gate|up into single projections, upload the raw Q8_0
 // embedding table, build the RoPE tables on the host, and allocate a
 // 2048-token workspace.
 //
@@ -63,9 +63,9 @@ bool env_flag(const char* name, bool dflt) {
 }
 
 struct DevMat {
-  _Float16* q = nullptr;
-  float* d = nullptr;
-  int m = 0, k = 0;
+  int8_t* q = nullptr;  // row tiles
+  float* d = nullptr;   // block scales [k/32][ld]
+  int m = 0, k = 0, ld = 0;
 };
 
 struct Layer {
@@ -107,7 +107,7 @@ class Backend {
 
   // Workspace for kCap tokens.
   float *x_, *h_, *qkv_, *gu_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
-  _Float16 *xq_, *cq_, *mid_q_;
+  int8_t *xq_, *cq_, *mid_q_;
   _Float16 *qs_, *ks_, *vt_;
   int32_t *ids_d_, *pos_d_, *vcol_d_;
   uint32_t *tiles_d_, *off_d_;  // tiles_d_: attention query tiles, then their count
@@ -144,6 +144,8 @@ class Backend {
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
   void launch(const char* name, hipError_t e);
   void record_layers(unsigned rows);
+  void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
+            hipStream_t s);
   void wait(const char* what);
 };
 
@@ -208,20 +210,21 @@ std::vector<uint8_t> Backend::q8_rows(const std::string& name, int k, int m) con
 }
 
 // Concatenates matrices along the output dimension and uploads them in the
-// GEMM's fragment-major layout.
+// GEMM's operand layout (row tiles + transposed block scales).
 DevMat Backend::upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k) {
   std::vector<uint8_t> rows_q8;
   for (auto* p : parts) rows_q8.insert(rows_q8.end(), p->begin(), p->end());
   const size_t rows = rows_q8.size() / ((size_t)(k / 32) * 34);
-  std::vector<uint16_t> q(eg2_q8_fragment_halves(rows, (unsigned)k));
-  std::vector<float> d(q.size() / 16);
-  eg2_q8_fragments(rows_q8.data(), rows, (unsigned)k, q.data(), d.data());
   DevMat mat;
   mat.m = (int)rows;
   mat.k = k;
-  mat.q = dalloc<_Float16>(q.size());
+  mat.ld = (int)((rows + 31) / 32 * 32);
+  std::vector<int8_t> q(eg2_q8_tile_bytes(rows, (unsigned)k));
+  std::vector<float> d((size_t)(k / 32) * mat.ld);
+  eg2_q8_weight_tiles(rows_q8.data(), rows, (unsigned)k, q.data(), d.data());
+  mat.q = dalloc<int8_t>(q.size());
   mat.d = dalloc<float>(d.size());
-  check(hipMemcpy(mat.q, q.data(), q.size() * sizeof(uint16_t), hipMemcpyHostToDevice), "upload");
+  check(hipMemcpy(mat.q, q.data(), q.size(), hipMemcpyHostToDevice), "upload");
   check(hipMemcpy(mat.d, d.data(), d.size() * sizeof(float), hipMemcpyHostToDevice), "upload");
   return mat;
 }
@@ -319,9 +322,9 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   h_ = dalloc<float>((size_t)kCap * kEmbd);
   qkv_ = dalloc<float>((size_t)kCap * kQKV);
   gu_ = dalloc<float>((size_t)kCap * 2 * kFF);
-  xq_ = dalloc<_Float16>((size_t)kCap * kFF);
+  xq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kFF));
   xd_ = dalloc<float>((size_t)kCap * (kFF / 32));
-  cq_ = dalloc<_Float16>((size_t)kCap * kEmbd);
+  cq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
   cd_ = dalloc<float>((size_t)kCap * (kEmbd / 32));
   qs_ = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
   ks_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
@@ -336,7 +339,7 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   off_d_ = dalloc<uint32_t>(kCap + 1);
   pooled_ = dalloc<float>((size_t)kCap * kEmbd);
   mid_ = dalloc<float>((size_t)kCap * kDenseFF);
-  mid_q_ = dalloc<_Float16>((size_t)kCap * kDenseFF);
+  mid_q_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kDenseFF));
   mid_d_ = dalloc<float>((size_t)kCap * (kDenseFF / 32));
   ids_h_ = halloc<int32_t>(kCap);
   pos_h_ = halloc<int32_t>(kCap);
@@ -347,8 +350,10 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   check(hipDeviceSynchronize(), "upload");
 
   size_t bytes = 0;
-  for (auto& L : layers_) bytes += (size_t)(L.qkv.m + L.o.m + L.gu.m) * kEmbd * 2 + (size_t)L.down.m * kFF * 2;
-  std::fprintf(stderr, "HIP: gfx950, %zu layers, Q8_0 layer weights %.1f MiB (fp16 integers), embedding table %.1f MiB, cap %u packed tokens%s\n",
+  for (auto& L : layers_)
+    for (const DevMat* w : {&L.qkv, &L.o, &L.gu, &L.down})
+      bytes += eg2_q8_tile_bytes(w->m, w->k) + (size_t)(w->k / 32) * w->ld * sizeof(float);
+  std::fprintf(stderr, "HIP: gfx950, %zu layers, Q8_0 layer weights %.1f MiB (int8 row tiles + scales), embedding table %.1f MiB, cap %u packed tokens%s\n",
                layers_.size(), bytes / 1048576.0, emb->n_bytes / 1048576.0, kCap, dense_ ? ", dense head" : "");
 }
 
@@ -364,6 +369,13 @@ void Backend::launch(const char* name, hipError_t e) {
   if (e != hipSuccess) throw std::runtime_error(std::string(name) + ": " + hipGetErrorString(e));
 }
 
+// y[n][w.m] (row stride ldy) = activations (row tiles xq, scales xd
+// [k/32][n]) times the weights w.
+void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
+                   hipStream_t s) {
+  launch(name, eg2::launch_gemm_q8(xq, xd, n, w.q, w.d, w.ld, y, n, w.m, w.k, ldy, s));
+}
+
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
 // then per layer (engine.c:1115-1127 order) QKV GEMM, QK-norm/RoPE,
 // attention (+Q8_0), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM,
@@ -376,17 +388,17 @@ void Backend::record_layers(unsigned rows) {
                                                eps_, x_, xq_, xd_, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
-    launch("gemm_qkv", eg2::launch_gemm_q8(xq_, xd_, n, L.qkv.q, L.qkv.d, qkv_, n, L.qkv.m, kEmbd, kQKV, s));
+    gemm("gemm_qkv", xq_, xd_, L.qkv, qkv_, n, kQKV, s);
     launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, vcol_d_, eps_, qs_, ks_,
                                                     vt_, kVtCols, n, s));
     launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, tiles_d_, tiles_d_ + 4 * kCap,
                                               (n + 7) / 8, L.window,
                                               n, cq_, cd_, s));
-    launch("gemm_o", eg2::launch_gemm_q8(cq_, cd_, n, L.o.q, L.o.d, h_, n, kEmbd, kEmbd, kEmbd, s));
+    gemm("gemm_o", cq_, cd_, L.o, h_, n, kEmbd, s);
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
-    launch("gemm_gate_up", eg2::launch_gemm_q8(xq_, xd_, n, L.gu.q, L.gu.d, gu_, n, 2 * kFF, kEmbd, 2 * kFF, s));
+    gemm("gemm_gate_up", xq_, xd_, L.gu, gu_, n, 2 * kFF, s);
     launch("gelu", eg2::launch_gelu_quant(gu_, xq_, xd_, n, s));
-    launch("gemm_down", eg2::launch_gemm_q8(xq_, xd_, n, L.down.q, L.down.d, h_, n, kEmbd, kFF, kEmbd, s));
+    gemm("gemm_down", xq_, xd_, L.down, h_, n, kEmbd, s);
     const float* next = il + 1 < layers_.size() ? layers_[il + 1].attn_norm : nullptr;
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_ffw, next, eps_, xq_, xd_, n, s));
   }
@@ -515,10 +527,9 @@ void Backend::launch_staged(unsigned repeats) {
     launch("pool", eg2::launch_pool_l2(x_, off_d_, pooled_, B, s));
     if (dense_) {
       launch("dense_quant", eg2::launch_quantize_rows(pooled_, kEmbd, cq_, cd_, B, s));
-      launch("dense_2", eg2::launch_gemm_q8(cq_, cd_, B, dense2_.q, dense2_.d, mid_, B, kDenseFF, kEmbd, kDenseFF, s));
+      gemm("dense_2", cq_, cd_, dense2_, mid_, B, kDenseFF, s);
       launch("dense_quant", eg2::launch_quantize_rows(mid_, kDenseFF, mid_q_, mid_d_, B, s));
-      launch("dense_3",
-             eg2::launch_gemm_q8(mid_q_, mid_d_, B, dense3_.q, dense3_.d, pooled_, B, kEmbd, kDenseFF, kEmbd, s));
+      gemm("dense_3", mid_q_, mid_d_, dense3_, pooled_, B, kEmbd, s);
       launch("dense_l2", eg2::launch_l2_prefix(pooled_, kEmbd, kEmbd, B, s));
     }
   }

@@ -43,7 +43,6 @@
 namespace eg2 {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kQTile = 16;   // queries per work tile (one 16x16x32 MFMA column block)
@@ -76,7 +75,7 @@ __device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
 __global__ void __launch_bounds__(192)
 attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks, const _Float16* __restrict__ vt,
                  int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ tiles,
-                 const uint32_t* __restrict__ tile_count, int window, int rows, _Float16* __restrict__ cq,
+                 const uint32_t* __restrict__ tile_count, int window, int rows, int8_t* __restrict__ cq,
                  float* __restrict__ cd) {
   __shared__ __align__(16) unsigned char lds[2 * kStage];
 
@@ -243,11 +242,10 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 
     // Epilogue: context = acc / l, then Q8_0 per 32 dims (quants.c:97-177).
     // acc[db][v] is dim 16db + 4grp + v of query t, so Q8_0 block b (dims
-    // 32b..32b+31) sits in acc[2b], acc[2b+1] of the four lane groups.
-    // Values are stored as fp16 integers with a float scale, the scales
-    // transposed ([block][row]) for the projection GEMM.
+    // 32b..32b+31) sits in acc[2b], acc[2b+1] of the four lane groups. The
+    // int8 values go to the row-tile layout of the projection GEMM (4 bytes
+    // per lane and half-block), the scales transposed ([block][row]).
     const float inv_l = 1.0f / l_run;
-    _Float16* out = cq + (size_t)t * kEmbd + head * kHeadDim;
 #pragma unroll
     for (int b = 0; b < kHeadDim / kQK; ++b) {
       float vals[8];
@@ -265,14 +263,13 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       const float dq = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
       const float id = amax == 0.0f ? 0.0f : 1.0f / d;
       if (!active) continue;
-      half4 q0v, q1v;
+      int32_t qv[8];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        q0v[v] = (_Float16)(amax == 0.0f ? 0 : q8_round(vals[v] * id));
-        q1v[v] = (_Float16)(amax == 0.0f ? 0 : q8_round(vals[4 + v] * id));
-      }
-      *reinterpret_cast<half4*>(out + 32 * b + 4 * grp) = q0v;
-      *reinterpret_cast<half4*>(out + 32 * b + 16 + 4 * grp) = q1v;
+      for (int i = 0; i < 8; ++i) qv[i] = amax == 0.0f ? 0 : q8_round(vals[i] * id);
+      const unsigned e = head * kHeadDim + 32 * b + 4 * grp;
+      *reinterpret_cast<uint32_t*>(cq + q8_tile_offset(t, e, kEmbd / kQK)) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
+      *reinterpret_cast<uint32_t*>(cq + q8_tile_offset(t, e + 16, kEmbd / kQK)) =
+          pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
       if (grp == 0) cd[(size_t)(head * (kHeadDim / kQK) + b) * rows + t] = dq;
     }
   }
@@ -305,7 +302,7 @@ size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
 
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
                             const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
-                            _Float16* cq, float* cd, hipStream_t st) {
+                            int8_t* cq, float* cd, hipStream_t st) {
   if (rows <= 0 || grid <= 0 || ldv <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(192), 0, st, qs, ks, vt, ldv, vcol,
                      reinterpret_cast<const uint4*>(tiles), tile_count, window, rows, cq, cd);

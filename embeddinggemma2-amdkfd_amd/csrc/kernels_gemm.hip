@@ -1,4 +1,4 @@
-// Q8_0 x Q8_0 projection GEMM on MFMA (gfx950).
+// Q8_0 x Q8_0 projection GEMM on int8 MFMA (gfx950).
 //
 //   y[n][m] = sum over 32-blocks b of ((float)dot_b(n, m) * d_w[m][b]) * d_x[n][b]
 //
@@ -7,36 +7,32 @@
 // added in block order with one fp32 rounding per operation. Results are
 // bit-identical to the CPU path.
 //
-// Operands hold Q8_0 integers as fp16 (every int8 is exact in fp16). A
-// 32-block dot is two v_mfma_f32_32x32x16_f16 with a zero accumulator; its
-// products (|q| <= 128) and partial sums (|sum| <= 2^19) are exact in fp32,
-// so the MFMA returns the integer dot exactly. The scaling then costs three
-// VALU operations per output and block (it cannot be folded into the
-// operands without changing the rounding).
+// Exactness. A 32-block dot is one v_mfma_i32_32x32x32_i8 (exact int32).
+// Its accumulator input is the integer 0x4B400000, the bit pattern of the
+// float 1.5 * 2^23; |dot| <= 32 * 128 * 128 = 2^19 keeps the result's bits a
+// float in [2^23, 2^24), where every float is an integer, and that float is
+// exactly 12582912 + dot. fma(it, d_w, -12582912 * d_w) is then dot * d_w
+// rounded once -- the reference's (float)dot * d_w -- since 12582912 * d_w
+// is exact (d_w is the value of an fp16: at most 11 significant bits). The
+// int-to-float conversion thus costs nothing, and a block costs three VALU
+// operations per output (fma, multiply, add); they cannot be merged
+// without changing the rounding, and they, not the MFMA, bound the kernel.
 //
-// Data layout (chosen for this kernel):
-//  * activations xq [rows][k] fp16, block scales transposed xd [k/32][ldx]
-//    (the quantizing row kernels write them that way);
-//  * weights in a fragment-major layout, repacked once at load:
-//    wf [m/32][k/32][64 lanes][16 fp16] where lane l holds row l % 32 and
-//    columns 16 * (l / 32) .. +15 of the 32-block, and their scales
-//    wdf [m/32][k/32][64 lanes] (one per lane, the row's block scale).
+// Operand layout ("row tiles"; the quantizing kernels write activations in
+// it, eg2_q8_weight_tiles writes weights): int8 [rows/32][k/32][2][32][16],
+// so each 32-row x 32-value block is 1 KB in the register order of the
+// MFMA operand (lane 32h + r holds row r, values 16h .. 16h + 15): one
+// 1 KB global_load_lds_dwordx4 moves it, one ds_read_b128 per lane reads
+// it. Block scales are stored transposed, [k/32][ld], one float per row.
 //
-// One workgroup computes a 32-row x (32 * WM)-column tile with WM waves, one
-// 32x32 output tile per wave. The 32 activation rows of each block go from
-// global memory straight into an LDS ring (global_load_lds_dwordx4, one
-// 1 KB instruction per 16 rows, XOR-swizzled 16-byte chunks so the fragment
-// reads are free of bank conflicts) shared by the WM waves; each wave reads
-// its weight fragments from global memory into a register ring, fully
-// coalesced thanks to the fragment-major layout. LDS read bandwidth
-// (~64 B/clk per CU on this part) is the scarce resource: this split moves
-// only the shared operand through LDS. The activation scales of all blocks
-// are preloaded into LDS once per workgroup.
-//
-// In the MFMA 32x32 output layout a lane holds one weight column and 16
-// token rows; each row's activation scale reaches the lane through a DPP
-// row broadcast folded into the multiply (v_mul_f32_dpp row_newbcast), so
-// the per-block scale traffic is one float per lane.
+// Work: a workgroup of 4 waves computes a 64 x 64 output tile, wave w the
+// 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Per block, the
+// four operand tiles and the 64 + 64 scales go by DMA into a 4-stage LDS
+// ring (each wave moves one tile and one scale vector), two blocks in
+// flight beyond the one being read; the MFMA of block kb + 1 is issued
+// before the scaling of block kb. In the MFMA 32x32 output layout a lane
+// holds one column and 16 rows; each row's activation scale reaches it
+// through a DPP row broadcast folded into the multiply.
 #include <utility>
 
 #include "eg2_device.hpp"
@@ -44,183 +40,190 @@
 
 namespace eg2 {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 32;   // one Q8_0 block per k-step
-constexpr int kXcds = 8;  // MI355X: 8 XCDs of 32 CUs, each with its own L2
+constexpr int kXcds = 8;     // MI355X: 8 XCDs of 32 CUs, each with its own L2
+constexpr int kStages = 4;   // LDS ring depth (even: see the loop below)
+constexpr int kTile = 1024;  // one 32 x 32 int8 operand block
+constexpr int kDxOff = 4 * kTile, kDwOff = kDxOff + 64 * 4;
+constexpr int kStageBytes = kDwOff + 64 * 4;  // A0 A1 B0 B1 | d_x[64] | d_w[64]
+constexpr float kMagic = 12582912.0f;         // 1.5 * 2^23
+constexpr int kMagicBits = 0x4B400000;
 
 extern __shared__ __align__(16) unsigned char gemm_lds[];
 
-// 4 / 16 bytes per lane from global memory straight into LDS at
-// lds + 4 * lane / lds + 16 * lane (the LDS base is wave-uniform).
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+// LDS DMA from a wave-uniform global base (SGPR pair) plus a per-lane byte
+// offset, 16 or 4 bytes per lane, to the wave-uniform LDS address `lds`
+// (+16 or +4 bytes per lane), which the instruction takes from M0. The
+// builtin form would address through a 64-bit VGPR pair per lane (more
+// address arithmetic and ten more VGPRs); this kernel has no other M0 user,
+// so setting M0 here disturbs nothing the compiler keeps there.
+__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
 }
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
 }
 
-// Waits until at most N vector-memory operations of this wave are in
-// flight, then joins the workgroup barrier. The LDS ring is filled by DMA,
-// which the compiler does not track, so the wait is explicit; the memory
-// clobber keeps LDS reads from moving across it.
+// Waits until at most N vector-memory operations of this wave are in flight
+// and its LDS reads are done, then joins the workgroup barrier. The ring is
+// filled by DMA, which the compiler does not track, so the wait is
+// explicit; the memory clobber keeps LDS reads from moving across it.
 template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+__device__ __forceinline__ void wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Chunk swizzle of a 64-byte LDS row: 16-byte chunk c of row r is stored at
-// c ^ swz(r). The MFMA fragment reads (lane i of each half-wave reads row i)
-// then spread every 8- and 16-lane group over distinct banks.
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
-
-// Broadcast of lane V of each 16-lane row to the whole row.
+// Broadcast of lane V of each 16-lane row to the whole row (row_newbcast).
 template <int V>
 __device__ __forceinline__ float row_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + V, 0xf, 0xf, true));
 }
 
-// acc[v] += (dot[v] * dw) * dx(row v): the lane's 16 output rows take their
-// activation scales from lanes 0..15 of its 16-lane row.
+// acc[v] += ((dot[v] * d_w) * d_x(row v)) from the biased MFMA result; the
+// lane's 16 output rows take their activation scales from lanes 0..15 of
+// its 16-lane row. The three phases are kept apart so 16 independent
+// operations separate each dependent pair.
 template <int... V>
-__device__ __forceinline__ void scale_accumulate(floatx16& acc, const floatx16& dot, float dw, float dxv,
+__device__ __forceinline__ void scale_accumulate(floatx16& acc, const intx16& biased, float dw, float dxv,
                                                  std::integer_sequence<int, V...>) {
-  ((acc[V] = acc[V] + (dot[V] * dw) * row_bcast<V>(dxv)), ...);
+  const float bias = dw * -kMagic;
+  const floatx16 f = __builtin_bit_cast(floatx16, biased);
+  floatx16 t;
+  ((t[V] = __builtin_fmaf(f[V], dw, bias)), ...);
+  __builtin_amdgcn_sched_barrier(0);
+  ((t[V] = t[V] * row_bcast<V>(dxv)), ...);
+  __builtin_amdgcn_sched_barrier(0);
+  ((acc[V] = acc[V] + t[V]), ...);
 }
 
-template <int WM, int D>
-__global__ void __launch_bounds__(WM * 64)
-gemm_q8_kernel(const _Float16* __restrict__ xq, const float* __restrict__ xd, int ldx,
-               const _Float16* __restrict__ wf, const float* __restrict__ wdf, float* __restrict__ y, int n, int m,
-               int k, int ldy) {
-  constexpr int S = 2 * D;        // LDS ring stages
-  constexpr int STAGE = 32 * 64;  // 32 rows x 64 bytes
-  constexpr int QA = 2;           // 1 KB DMA instructions per stage
-  static_assert(QA % WM == 0 || WM % QA == 0, "DMA split");
-  constexpr int QAW = QA >= WM ? QA / WM : 1;  // per issuing wave
-  constexpr int QB = 3;                        // weight loads per block
-  static_assert((D & (D - 1)) == 0, "D must be a power of two");
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n_tiles_n = (n + 31) / 32, mt_count = (m + 31) / 32;
-  const int n_tiles = n_tiles_n * ((mt_count + WM - 1) / WM);
+// TAIL: nb % kStages != 0 (a separate instantiation: the tail code costs
+// registers, and every projection of the model has nb % 4 == 0).
+template <bool TAIL>
+__global__ void __launch_bounds__(256)
+gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx, const int8_t* __restrict__ wq,
+               const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tr_count = (n + 63) / 64, tc_count = (m + 63) / 64, tiles = tr_count * tc_count;
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes one
   // contiguous run of tiles (column-group major), so the weight columns it
   // needs stay in its own L2.
-  const int per_xcd = (n_tiles + kXcds - 1) / kXcds;
+  const int per_xcd = (tiles + kXcds - 1) / kXcds;
   const int tile = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
-  if (tile >= n_tiles) return;
-  const int n0 = (tile % n_tiles_n) * 32;
-  const int mt_raw = (tile / n_tiles_n) * WM + wave, mt = min(mt_raw, mt_count - 1);
-  const int nb = k / kBK;
-  unsigned char* smem = gemm_lds;
-  float* sA = reinterpret_cast<float*>(smem + S * STAGE);  // [nb rounded up to 2][32]
+  if (tile >= tiles) return;
+  const int tr = tile % tr_count, tc = tile / tr_count;
 
-  // Activation scales of all blocks: two blocks (2 x 32 rows) per instruction.
-  for (int b0 = 2 * wave; b0 < nb; b0 += 2 * WM) {
-    const int b = min(b0 + (lane >> 5), nb - 1);
-    dma4(xd + (size_t)b * ldx + min(n0 + (lane & 31), n - 1), sA + b0 * 32);
+  // DMA roles: wave w moves operand tile w of each block -- activation rows
+  // 64 tr + 32 w (w < 2) or weight rows 64 tc + 32 (w - 2), clamped to the
+  // last tile -- and one scale vector: the 64 activation scales (waves 0-1)
+  // or weight scales (waves 2-3), clamped to the last row. Each pair writes
+  // identical data, so every wave has the same loads in flight.
+  const int8_t* tbase;
+  const float* sbase;
+  unsigned soff;
+  int sld;
+  if (w < 2) {
+    tbase = xq + (size_t)min(2 * tr + w, (n + 31) / 32 - 1) * nb * kTile;
+    sbase = xd;
+    sld = ldx;
+    soff = 4u * (unsigned)min(64 * tr + lane, n - 1);
+  } else {
+    tbase = wq + (size_t)min(2 * tc + w - 2, (m + 31) / 32 - 1) * nb * kTile;
+    sbase = wd;
+    sld = ldw;
+    soff = 4u * (unsigned)min(64 * tc + lane, m - 1);
   }
-  // Activation DMA: instruction q fills stage rows 16q..16q+15; lane L takes
-  // (row 16q + L/4, stored chunk L%4) = global chunk (L%4) ^ swz(row).
-  const bool dma_wave = wave < QA;
-  const _Float16* asrc[QAW];
-  int aoff[QAW];
-#pragma unroll
-  for (int t = 0; t < QAW; ++t) {
-    const int q = min(wave * QAW + t, QA - 1), row = 16 * q + (lane >> 2), c = (lane & 3) ^ swz(row);
-    asrc[t] = xq + (size_t)min(n0 + row, n - 1) * k + 8 * c;
-    aoff[t] = 1024 * q;
-  }
-  auto issue_a = [&](int slot, int kb) {
-    if (!dma_wave) return;
-    unsigned char* base = smem + (slot & (S - 1)) * STAGE;
-#pragma unroll
-    for (int t = 0; t < QAW; ++t) dma16(asrc[t] + kb * kBK, base + aoff[t]);
-  };
-  // Weight fragments, D blocks ahead in registers.
-  const _Float16* bsrc = wf + ((size_t)mt * nb * 64 + lane) * 16;
-  const float* dsrc = wdf + (size_t)mt * nb * 64 + lane;
-  struct BStage {
-    half8 b0, b1;
-    float dw;
-  };
-  BStage ring[D];
-  auto load_b = [&](BStage& r, int kb) {
-    const half8* p = reinterpret_cast<const half8*>(bsrc + (size_t)kb * 64 * 16);
-    r.b0 = p[0];
-    r.b1 = p[1];
-    r.dw = dsrc[kb * 64];
+  const unsigned lds0 = (unsigned)(uintptr_t)gemm_lds;
+  const unsigned t_lds = lds0 + kTile * w, s_lds = lds0 + (w < 2 ? kDxOff : kDwOff);
+  auto issue = [&](int slot, int kb) {
+    kb = min(kb, nb - 1);
+    dma16(tbase + (size_t)kb * kTile, 16u * lane, __builtin_amdgcn_readfirstlane(t_lds + slot * kStageBytes));
+    dma4(sbase + (size_t)kb * sld, soff, __builtin_amdgcn_readfirstlane(s_lds + slot * kStageBytes));
   };
 
-  floatx16 acc = floatx16{};
-  const int g = lane >> 5, r32 = lane & 31;
+  const int wr = w >> 1, wc = w & 1, g = lane >> 5;
   // Row whose scale this lane supplies to the DPP broadcast: lane 16r + v
   // carries the scale of output register v for the lanes of 16-lane row r.
   const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
-  const int af = swz(r32);
+  const unsigned char* a_p = gemm_lds + kTile * wr + 16 * lane;
+  const unsigned char* b_p = gemm_lds + 2 * kTile + kTile * wc + 16 * lane;
+  const unsigned char* dx_p = gemm_lds + kDxOff + 4 * (32 * wr + srow);
+  const unsigned char* dw_p = gemm_lds + kDwOff + 4 * (32 * wc + (lane & 31));
+  intx16 magic = (intx16)(kMagicBits);
+  asm volatile("" : "+v"(magic));  // one register copy, not rebuilt per MFMA
+  struct Frag {
+    intx4 a, b;
+    float dx, dw;
+  };
+  auto frag = [&](int slot) {
+    Frag f;
+    f.a = *reinterpret_cast<const intx4*>(a_p + slot * kStageBytes);
+    f.b = *reinterpret_cast<const intx4*>(b_p + slot * kStageBytes);
+    f.dx = *reinterpret_cast<const float*>(dx_p + slot * kStageBytes);
+    f.dw = *reinterpret_cast<const float*>(dw_p + slot * kStageBytes);
+    return f;
+  };
 
+  // Ring protocol: block kb sits in slot kb % kStages. Iteration kb refills
+  // slot (kb - 1) % kStages, last read in iteration kb - 2 (a barrier
+  // ago), then waits until block kb + 1 has landed for every wave.
 #pragma unroll
-  for (int u = 0; u < D; ++u) {
-    issue_a(u, min(u, nb - 1));
-    load_b(ring[u], min(u, nb - 1));
+  for (int s = 0; s < kStages - 1; ++s) issue(s, s);
+  wait_barrier<2 * (kStages - 2)>();
+  Frag f[2];
+  intx16 d[2];
+  f[0] = frag(0);
+  d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[0].a, f[0].b, magic, 0, 0, 0);
+  floatx16 acc = floatx16{};
+  // One block: j = kb % kStages (a constant after unrolling, so slots are
+  // immediate offsets and the register pair alternates with kb's parity).
+  auto step = [&](int j, int kb) {
+    const int cur = j & 1, nxt = cur ^ 1;
+    issue((j + kStages - 1) % kStages, kb + kStages - 1);
+    wait_barrier<2 * (kStages - 2)>();
+    f[nxt] = frag((j + 1) % kStages);
+    d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
+    scale_accumulate(acc, d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+  };
+  int kb0 = 0;
+  for (; kb0 + kStages <= nb; kb0 += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) step(j, kb0 + j);
   }
-  // Block kb: its DMA and weight loads were issued D blocks earlier; the
-  // stage it refills, (kb + D) % S, was last read in block kb - D.
-  for (int kb0 = 0; kb0 < nb; kb0 += D) {
-    const unsigned char* st0 = smem + (kb0 & D) * STAGE;
+  // The last nb % kStages blocks (the branch stays out of the main loop,
+  // whose straight-line body lets the DPP broadcasts fold into the multiplies).
+  if constexpr (TAIL) {
 #pragma unroll
-    for (int u = 0; u < D; ++u) {
-      const int kb = kb0 + u;
-      if (dma_wave) wait_vm_barrier<(D - 1) * (QAW + QB)>();
-      else wait_vm_barrier<(D - 1) * QB>();
-      const unsigned char* st = st0 + u * STAGE;
-      const half8 a0 = *reinterpret_cast<const half8*>(st + r32 * 64 + 16 * ((2 * g) ^ af));
-      const half8 a1 = *reinterpret_cast<const half8*>(st + r32 * 64 + 16 * ((2 * g + 1) ^ af));
-      const float dx = sA[kb * 32 + srow];
-      floatx16 dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ring[u].b0, floatx16{}, 0, 0, 0);
-      dot = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ring[u].b1, dot, 0, 0, 0);
-      issue_a(kb + D, min(kb + D, nb - 1));
-      scale_accumulate(acc, dot, ring[u].dw, dx, std::make_integer_sequence<int, 16>{});
-      load_b(ring[u], min(kb + D, nb - 1));
-    }
+    for (int j = 0; j < kStages - 1; ++j)
+      if (kb0 + j < nb) step(j, kb0 + j);
   }
   // The ring's last refills are redundant; they must land before the
   // workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (mt_raw >= mt_count) return;
-  const int col = mt * 32 + r32;
+  const int col = 64 * tc + 32 * wc + (lane & 31);
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
-    const int row = n0 + 8 * (v >> 2) + 4 * g + (v & 3);
+    const int row = 64 * tr + 32 * wr + 8 * (v >> 2) + 4 * g + (v & 3);
     if (row < n && col < m) y[(size_t)row * ldy + col] = acc[v];
   }
 }
 
-template <int WM, int D>
-static hipError_t launch_gemm(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
-                              float* y, int n, int m, int k, int ldy, hipStream_t st) {
-  const int tiles = ((n + 31) / 32) * (((m + 31) / 32 + WM - 1) / WM);
-  const dim3 grid(((tiles + kXcds - 1) / kXcds) * kXcds);
-  const int nb = k / kBK;
-  const size_t lds = (size_t)(2 * D) * 32 * 64 + (size_t)((nb + 1) / 2 * 2) * 32 * 4;
-  hipLaunchKernelGGL((gemm_q8_kernel<WM, D>), grid, dim3(WM * 64), lds, st, xq, xd, ldx, wf, wdf, y, n, m, k, ldy);
-  return hipGetLastError();
-}
-
-size_t gemm_q8_max_k() {
-  // LDS: 4 stages of 2 KB plus 128 bytes of scales per block, within 64 KB.
-  return (65536 - 4 * 2048) / 128 * 32;
-}
-
-hipError_t launch_gemm_q8(const _Float16* xq, const float* xd, int ldx, const _Float16* wf, const float* wdf,
+hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st) {
-  if (n <= 0 || m <= 0 || k <= 0 || k % kBK != 0 || ldy < m || ldx < n || (size_t)k > gemm_q8_max_k())
-    return hipErrorInvalidValue;
-  // Two waves per 32 x 64 tile, weight fragments two blocks ahead.
-  if ((k / kBK) % 2 == 0) return launch_gemm<2, 2>(xq, xd, ldx, wf, wdf, y, n, m, k, ldy, st);
-  return launch_gemm<2, 1>(xq, xd, ldx, wf, wdf, y, n, m, k, ldy, st);
+  if (n <= 0 || m <= 0 || k <= 0 || k % kQK != 0 || ldy < m || ldx < n || ldw < m) return hipErrorInvalidValue;
+  const int tiles = ((n + 63) / 64) * ((m + 63) / 64);
+  const dim3 grid(((tiles + kXcds - 1) / kXcds) * kXcds);
+  const int nb = k / kQK;
+  if (nb % kStages == 0)
+    hipLaunchKernelGGL(gemm_q8_kernel<false>, grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd, ldw, y,
+                       n, m, nb, ldy);
+  else
+    hipLaunchKernelGGL(gemm_q8_kernel<true>, grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd, ldw, y,
+                       n, m, nb, ldy);
+  return hipGetLastError();
 }
 
 }  // namespace eg2

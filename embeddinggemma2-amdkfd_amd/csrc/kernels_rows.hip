@@ -22,8 +22,6 @@
 
 namespace eg2 {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-
 constexpr int kBlkStride = kQK + 4;                    // padded 32-value block in LDS
 constexpr int kRowFloats = kEmbd / kQK * kBlkStride;   // 864 floats per padded row
 constexpr int kBlocks = kEmbd / kQK;                   // 24 blocks per row
@@ -70,12 +68,14 @@ __device__ __forceinline__ float row_sum_squares(const float* row) {
 // (lanes P*i .. P*i+P-1, all active), each holding N = 32/P consecutive
 // values: amax, d = amax/127 stored as fp16 (round-half-up), id = 1/d,
 // q = roundf(v*id) clamped; an all-zero block stores d = 0 and q = 0. Each
-// lane writes its N values as fp16 integers at q (16-byte aligned); the
-// first lane of the group writes the float value of the stored scale.
+// lane writes its N int8 values at q (N-byte aligned, consecutive in the
+// row-tile layout since N <= 16); the first lane of the group writes the
+// float value of the stored scale.
 template <int P>
-__device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], bool store, _Float16* __restrict__ q,
+__device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], bool store, int8_t* __restrict__ q,
                                                     float* __restrict__ d_out) {
   constexpr int N = kQK / P;
+  static_assert(N == 8 || N == 16, "8 or 16 values per lane");
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -85,19 +85,25 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
   const float id = amax != 0.0f ? 1.0f / d : 0.0f;
   if (!store) return;
   if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
-  half8 out[N / 8];
+  int32_t qi[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) out[i / 8][i % 8] = (_Float16)(amax != 0.0f ? q8_round(v[i] * id) : 0);
+  for (int i = 0; i < N; ++i) qi[i] = amax != 0.0f ? q8_round(v[i] * id) : 0;
+  uint32_t w[N / 4];
 #pragma unroll
-  for (int i = 0; i < N / 8; ++i) reinterpret_cast<half8*>(q)[i] = out[i];
+  for (int i = 0; i < N / 4; ++i) w[i] = pack_i8x4(qi[4 * i], qi[4 * i + 1], qi[4 * i + 2], qi[4 * i + 3]);
+  if constexpr (N == 16)
+    *reinterpret_cast<uint4*>(q) = make_uint4(w[0], w[1], w[2], w[3]);
+  else
+    *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
 }
 
 // (x*w)*inv on a padded LDS row (kernels.c:124-133, SSE2 branch), quantized
 // to Q8_0 (kernels.c:139-151): lane pairs take the 24 blocks (lanes 48-63
-// repeat the last block and store nothing). Block scales are stored
+// repeat the last block and store nothing), each lane one 16-value half.
+// Values go to row t of the row-tile buffer q; block scales are stored
 // transposed, block b of this row at d[b * ld].
-__device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w, float inv,
-                                                  _Float16* __restrict__ q, float* __restrict__ d, int ld) {
+__device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w, float inv, int t,
+                                                  int8_t* __restrict__ q, float* __restrict__ d, int ld) {
   const int lane = threadIdx.x;
   const int b = min(lane >> 1, kBlocks - 1), part = lane & 1, e0 = b * kQK + part * (kQK / 2);
   float v[kQK / 2];
@@ -111,7 +117,7 @@ __device__ __forceinline__ void norm_quantize_row(const float* row, const float*
     v[4 * i + 2] = p2 * inv;
     v[4 * i + 3] = p3 * inv;
   }
-  quantize_block_part<2>(v, lane < 2 * kBlocks, q + e0, d + (size_t)b * ld);
+  quantize_block_part<2>(v, lane < 2 * kBlocks, q + q8_tile_offset(t, e0, kBlocks), d + (size_t)b * ld);
 }
 
 // engine.c:288-295 + kernels.c:139-151 (the first projection's input):
@@ -120,7 +126,7 @@ __device__ __forceinline__ void norm_quantize_row(const float* row, const float*
 __global__ void __launch_bounds__(64)
 embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __restrict__ ids, float embed_scale,
                         const float* __restrict__ norm_w, float eps, float* __restrict__ x,
-                        _Float16* __restrict__ xq, float* __restrict__ xd) {
+                        int8_t* __restrict__ xq, float* __restrict__ xd) {
   constexpr int kRaw = kBlocks * 34;  // 816 bytes = 51 x 16
   __shared__ __align__(16) uint8_t raw[kRaw];
   __shared__ __align__(16) float row[kRowFloats];
@@ -146,7 +152,7 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
   }
   __syncthreads();
   const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, norm_w, inv, xq + (size_t)t * kEmbd, xd + t, (int)gridDim.x);
+  norm_quantize_row(row, norm_w, inv, t, xq, xd + t, (int)gridDim.x);
 }
 
 // kernels.c:163-188 (SSE2 build: scalar branch, residual += (h*inv)*w), then
@@ -154,7 +160,7 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
 // next_w == nullptr only the residual update runs.
 __global__ void __launch_bounds__(64)
 residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, const float* __restrict__ post_w,
-                           const float* __restrict__ next_w, float eps, _Float16* __restrict__ xq,
+                           const float* __restrict__ next_w, float eps, int8_t* __restrict__ xq,
                            float* __restrict__ xd) {
   __shared__ __align__(16) float row[kRowFloats];
   const int t = blockIdx.x, lane = threadIdx.x;
@@ -183,7 +189,7 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   if (!next_w) return;
   __syncthreads();
   const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, next_w, inv, xq + (size_t)t * kEmbd, xd + t, (int)gridDim.x);
+  norm_quantize_row(row, next_w, inv, t, xq, xd + t, (int)gridDim.x);
 }
 
 // Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
@@ -268,11 +274,11 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
 }
 
 // kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0,
-// each 32-value block over 4 lanes (8 values each); block scales transposed
-// ([block][row]).
+// each 32-value block over 4 lanes (8 values each), values in the row-tile
+// layout, block scales transposed ([block][row]).
 // gu rows hold [gate 0..1151 | up 0..1151].
 __global__ void __launch_bounds__(256)
-gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float* __restrict__ gd, int n_rows) {
+gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* __restrict__ gd, int n_rows) {
   constexpr int kB = kFF / kQK;  // 36 blocks per row
   const int j = blockIdx.x * 256 + threadIdx.x;  // quarter block
   const int jb = min(j >> 2, n_rows * kB - 1);   // the last wave may run past the end: repeat, store nothing
@@ -295,13 +301,13 @@ gelu_quant_kernel(const float* __restrict__ gu, _Float16* __restrict__ gq, float
       v[4 * i + c] = gelu * us[c];
     }
   }
-  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + (size_t)t * kFF + e0, gd + (size_t)b * n_rows + t);
+  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + q8_tile_offset(t, e0, kB), gd + (size_t)b * n_rows + t);
 }
 
 // quants.c:97-177 on rows of width k (k % 32 == 0), each block over 4 lanes;
-// block scales transposed ([block][row]).
+// values in the row-tile layout, block scales transposed ([block][row]).
 __global__ void __launch_bounds__(256)
-quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ q, float* __restrict__ d,
+quantize_rows_kernel(const float* __restrict__ x, int k, int8_t* __restrict__ q, float* __restrict__ d,
                      int n_rows) {
   const int nb = k / kQK;
   const int j = blockIdx.x * 256 + threadIdx.x;
@@ -317,7 +323,7 @@ quantize_rows_kernel(const float* __restrict__ x, int k, _Float16* __restrict__ 
     v[4 * i + 2] = x4.z;
     v[4 * i + 3] = x4.w;
   }
-  quantize_block_part<4>(v, (j >> 2) < n_rows * nb, q + (size_t)t * k + e0, d + (size_t)b * n_rows + t);
+  quantize_block_part<4>(v, (j >> 2) < n_rows * nb, q + q8_tile_offset(t, e0, nb), d + (size_t)b * n_rows + t);
 }
 
 // kernels.c:153-161 in place on a token row: x = (x*w)*inv.
@@ -398,7 +404,7 @@ dim3 quarter_block_groups(int blocks) { return dim3((4 * blocks + 255) / 256); }
 }  // namespace
 
 hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int rows, float embed_scale,
-                                   const float* norm_w, float eps, float* x, _Float16* xq, float* xd,
+                                   const float* norm_w, float eps, float* x, int8_t* xq, float* xd,
                                    hipStream_t st) {
   hipLaunchKernelGGL(embed_norm_quant_kernel, dim3(rows), dim3(64), 0, st, table, ids, embed_scale, norm_w, eps, x,
                      xq, xd);
@@ -406,7 +412,7 @@ hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int
 }
 
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
-                                      float eps, _Float16* xq, float* xd, int rows, hipStream_t st) {
+                                      float eps, int8_t* xq, float* xd, int rows, hipStream_t st) {
   hipLaunchKernelGGL(residual_norm_quant_kernel, dim3(rows), dim3(64), 0, st, x, h, post_w, next_w, eps, xq, xd);
   return hipGetLastError();
 }
@@ -419,13 +425,13 @@ hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* 
   return hipGetLastError();
 }
 
-hipError_t launch_gelu_quant(const float* gu, _Float16* gq, float* gd, int rows, hipStream_t st) {
+hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, hipStream_t st) {
   hipLaunchKernelGGL(gelu_quant_kernel, quarter_block_groups(rows * (kFF / kQK)), dim3(256), 0, st, gu, gq, gd,
                      rows);
   return hipGetLastError();
 }
 
-hipError_t launch_quantize_rows(const float* x, int k, _Float16* q, float* d, int rows, hipStream_t st) {
+hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st) {
   hipLaunchKernelGGL(quantize_rows_kernel, quarter_block_groups(rows * (k / kQK)), dim3(256), 0, st, x, k, q, d,
                      rows);
   return hipGetLastError();

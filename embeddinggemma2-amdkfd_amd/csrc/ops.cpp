@@ -7,6 +7,7 @@
 #include <cstring>
 
 #include "eg2_hip.h"
+#include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
 namespace {
@@ -14,16 +15,6 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 _Float16* h16(uint16_t* p) { return reinterpret_cast<_Float16*>(p); }
 const _Float16* h16(const uint16_t* p) { return reinterpret_cast<const _Float16*>(p); }
 
-// IEEE fp16 bit pattern of an int8 value (exact: |q| <= 128 < 2^11).
-uint16_t int8_to_fp16_bits(int8_t q) {
-  if (q == 0) return 0;
-  const uint32_t sign = q < 0 ? 0x8000u : 0u;
-  uint32_t mag = (uint32_t)(q < 0 ? -(int)q : (int)q);
-  int e = 0;
-  while ((mag >> e) > 1) ++e;  // mag in [2^e, 2^(e+1))
-  const uint32_t mant = (mag << (10 - e)) & 0x3FFu;
-  return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | mant);
-}
 int code(hipError_t e) { return (int)e; }
 constexpr int kInvalid = (int)hipErrorInvalidValue;
 
@@ -58,17 +49,16 @@ float fp16_to_fp32_host(uint16_t h) {
 extern "C" {
 
 int eg2_hip_embed_norm_quant(const void* table_q8, const int32_t* ids, unsigned rows, float embed_scale,
-                             const float* norm_w, float eps, float* x, uint16_t* xq, float* xd, void* stream) {
+                             const float* norm_w, float eps, float* x, int8_t* xq, float* xd, void* stream) {
   if (!table_q8 || !ids || !norm_w || !x || !xq || !xd || rows == 0) return kInvalid;
   return code(eg2::launch_embed_norm_quant(static_cast<const uint8_t*>(table_q8), ids, (int)rows, embed_scale,
-                                           norm_w, eps, x, h16(xq), xd, as_stream(stream)));
+                                           norm_w, eps, x, xq, xd, as_stream(stream)));
 }
 
 int eg2_hip_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w, float eps,
-                                uint16_t* xq, float* xd, unsigned rows, void* stream) {
+                                int8_t* xq, float* xd, unsigned rows, void* stream) {
   if (!x || !h || !post_w || rows == 0 || (next_w && (!xq || !xd))) return kInvalid;
-  return code(
-      eg2::launch_residual_norm_quant(x, h, post_w, next_w, eps, h16(xq), xd, (int)rows, as_stream(stream)));
+  return code(eg2::launch_residual_norm_quant(x, h, post_w, next_w, eps, xq, xd, (int)rows, as_stream(stream)));
 }
 
 int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope_table,
@@ -83,12 +73,12 @@ int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, c
 
 int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const int32_t* vcol,
                       const uint32_t* tiles, const uint32_t* tile_count, unsigned grid, unsigned window,
-                      unsigned rows, uint16_t* cq, float* cd, void* stream) {
+                      unsigned rows, int8_t* cq, float* cd, void* stream) {
   if (!qs || !ks || !vt || !vcol || !tiles || !tile_count || !cq || !cd || rows == 0 || grid == 0 ||
       grid > 65536 || window > 4096u || ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
     return kInvalid;
   return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, vcol, tiles, tile_count, (int)grid,
-                                    (int)window, (int)rows, h16(cq), cd, as_stream(stream)));
+                                    (int)window, (int)rows, cq, cd, as_stream(stream)));
 }
 
 unsigned eg2_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
@@ -101,14 +91,14 @@ size_t eg2_attention_vt_columns(const size_t* offsets, size_t batch, int32_t* vc
   return eg2::build_vt_columns(offsets, batch, vcol);
 }
 
-int eg2_hip_gelu_quant(const float* gate_up, uint16_t* gq, float* gd, unsigned rows, void* stream) {
+int eg2_hip_gelu_quant(const float* gate_up, int8_t* gq, float* gd, unsigned rows, void* stream) {
   if (!gate_up || !gq || !gd || rows == 0) return kInvalid;
-  return code(eg2::launch_gelu_quant(gate_up, h16(gq), gd, (int)rows, as_stream(stream)));
+  return code(eg2::launch_gelu_quant(gate_up, gq, gd, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_quantize_rows(const float* x, unsigned k, uint16_t* q, float* d, unsigned rows, void* stream) {
+int eg2_hip_quantize_rows(const float* x, unsigned k, int8_t* q, float* d, unsigned rows, void* stream) {
   if (!x || !q || !d || rows == 0 || k == 0 || k % 64 != 0) return kInvalid;
-  return code(eg2::launch_quantize_rows(x, (int)k, h16(q), d, (int)rows, as_stream(stream)));
+  return code(eg2::launch_quantize_rows(x, (int)k, q, d, (int)rows, as_stream(stream)));
 }
 
 int eg2_hip_rms_norm_rows(float* x, const float* w, float eps, unsigned rows, void* stream) {
@@ -126,12 +116,13 @@ int eg2_hip_l2_prefix(float* x, unsigned width, unsigned dims, unsigned rows, vo
   return code(eg2::launch_l2_prefix(x, (int)width, (int)dims, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_gemm_q8(const uint16_t* xq, const float* xd, unsigned ldx, const uint16_t* wf, const float* wdf,
+int eg2_hip_gemm_q8(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd, unsigned ldw,
                     float* y, unsigned n, unsigned m, unsigned k, unsigned ldy, void* stream) {
-  if (!xq || !xd || !wf || !wdf || !y || n == 0 || m == 0 || k == 0 || k % 32 != 0 || ldy < m || ldx < n ||
-      k > eg2::gemm_q8_max_k())
+  constexpr unsigned kMax = 1u << 24;  // keeps every index inside 32-bit arithmetic
+  if (!xq || !xd || !wq || !wd || !y || n == 0 || m == 0 || k == 0 || k % 32 != 0 || ldy < m || ldx < n ||
+      ldw < m || n > kMax || m > kMax || k > kMax || ldx > kMax || ldw > kMax || ldy > kMax)
     return kInvalid;
-  return code(eg2::launch_gemm_q8(h16(xq), xd, (int)ldx, h16(wf), wdf, y, (int)n, (int)m, (int)k, (int)ldy,
+  return code(eg2::launch_gemm_q8(xq, xd, (int)ldx, wq, wd, (int)ldw, y, (int)n, (int)m, (int)k, (int)ldy,
                                   as_stream(stream)));
 }
 
@@ -156,32 +147,31 @@ int eg2_hip_device_check(char* err, size_t len) {
   return 0;
 }
 
-void eg2_q8_split(const void* blocks, size_t rows, unsigned k, uint16_t* q, float* d) {
-  const uint8_t* src = static_cast<const uint8_t*>(blocks);
-  const size_t nb = k / 32;
+size_t eg2_q8_tile_bytes(size_t rows, unsigned k) { return (rows + 31) / 32 * (k / 32) * 1024; }
+
+void eg2_q8_pack_rows(const int8_t* q, size_t rows, unsigned k, int8_t* tiles) {
+  const size_t padded = (rows + 31) / 32 * 32;
+  for (size_t r = 0; r < padded; ++r)
+    for (unsigned e = 0; e < k; ++e) tiles[eg2::q8_tile_offset(r, e, k / 32)] = r < rows ? q[r * k + e] : 0;
+}
+
+void eg2_q8_unpack_rows(const int8_t* tiles, size_t rows, unsigned k, int8_t* q) {
   for (size_t r = 0; r < rows; ++r)
-    for (size_t b = 0; b < nb; ++b) {
-      const uint8_t* blk = src + (r * nb + b) * 34;
-      d[r * nb + b] = fp16_to_fp32_host((uint16_t)(blk[0] | (blk[1] << 8)));
-      for (int i = 0; i < 32; ++i) q[r * k + b * 32 + i] = int8_to_fp16_bits((int8_t)blk[2 + i]);
+    for (unsigned e = 0; e < k; ++e) q[r * k + e] = tiles[eg2::q8_tile_offset(r, e, k / 32)];
+}
+
+void eg2_q8_weight_tiles(const void* blocks, size_t rows, unsigned k, int8_t* wq, float* wd) {
+  const uint8_t* src = static_cast<const uint8_t*>(blocks);
+  const unsigned nb = k / 32;
+  const size_t ld = (rows + 31) / 32 * 32;
+  for (size_t r = 0; r < ld; ++r)
+    for (unsigned b = 0; b < nb; ++b) {
+      const uint8_t* blk = r < rows ? src + (r * nb + b) * 34 : nullptr;
+      wd[(size_t)b * ld + r] = blk ? fp16_to_fp32_host((uint16_t)(blk[0] | (blk[1] << 8))) : 0.0f;
+      for (unsigned i = 0; i < 32; ++i)
+        wq[eg2::q8_tile_offset(r, 32 * b + i, nb)] = blk ? (int8_t)blk[2 + i] : 0;
     }
 }
-
-void eg2_q8_fragments(const void* blocks, size_t rows, unsigned k, uint16_t* wf, float* wdf) {
-  const uint8_t* src = static_cast<const uint8_t*>(blocks);
-  const size_t nb = k / 32, tiles = (rows + 31) / 32;
-  for (size_t mt = 0; mt < tiles; ++mt)
-    for (size_t b = 0; b < nb; ++b)
-      for (unsigned lane = 0; lane < 64; ++lane) {
-        const size_t r = mt * 32 + lane % 32, f = (mt * nb + b) * 64 + lane;
-        const uint8_t* blk = r < rows ? src + (r * nb + b) * 34 : nullptr;
-        wdf[f] = blk ? fp16_to_fp32_host((uint16_t)(blk[0] | (blk[1] << 8))) : 0.0f;
-        for (unsigned i = 0; i < 16; ++i)
-          wf[f * 16 + i] = blk ? int8_to_fp16_bits((int8_t)blk[2 + 16 * (lane / 32) + i]) : 0;
-      }
-}
-
-size_t eg2_q8_fragment_halves(size_t rows, unsigned k) { return (rows + 31) / 32 * (k / 32) * 64 * 16; }
 
 void eg2_rope_table(float base, unsigned n_pos, float* table) {
   for (unsigned p = 0; p < n_pos; ++p)

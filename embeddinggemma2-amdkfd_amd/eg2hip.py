@@ -112,12 +112,13 @@ SIGNATURES = {
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
-    "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _u, _vp]),
+    "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
     "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
-    "eg2_q8_split": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
-    "eg2_q8_fragments": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
-    "eg2_q8_fragment_halves": (C.c_size_t, [C.c_size_t, _u]),
+    "eg2_q8_tile_bytes": (C.c_size_t, [C.c_size_t, _u]),
+    "eg2_q8_pack_rows": (None, [_vp, C.c_size_t, _u, _vp]),
+    "eg2_q8_unpack_rows": (None, [_vp, C.c_size_t, _u, _vp]),
+    "eg2_q8_weight_tiles": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
     "eg2_rope_table": (None, [C.c_float, _u, _vp]),
     "eg2_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
     "eg2_gguf_close": (None, [C.POINTER(EiGguf)]),
@@ -274,29 +275,44 @@ def attention_vt_columns(offsets):
     return vcol, max(32, (cols + 31) // 32 * 32)
 
 
-def q8_fragments(blocks_u8, rows, k):
-    """GGUF Q8_0 bytes [rows, k] -> the projection GEMM's fragment-major weights
-    (wf: fp16 integers [ceil(rows/32), k/32, 64, 16], wdf: float32 scales
-    [ceil(rows/32), k/32, 64])."""
+def q8_tile_bytes(rows, k):
+    """Bytes of a Q8_0 row-tile buffer (rows rounded up to 32)."""
+    return lib().eg2_q8_tile_bytes(rows, k)
+
+
+def q8_pack_rows(q):
+    """int8 [rows, k] -> the row-tile layout (flat int8, padding rows zero)."""
+    import numpy as np
+
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    rows, k = q.shape
+    tiles = np.zeros(q8_tile_bytes(rows, k), dtype=np.int8)
+    lib().eg2_q8_pack_rows(q.ctypes.data, rows, k, tiles.ctypes.data)
+    return tiles
+
+
+def q8_unpack_rows(tiles, rows, k):
+    """Row-tile bytes -> int8 [rows, k]."""
+    import numpy as np
+
+    tiles = np.ascontiguousarray(tiles).view(np.int8)
+    assert tiles.size >= q8_tile_bytes(rows, k)
+    q = np.zeros((rows, k), dtype=np.int8)
+    lib().eg2_q8_unpack_rows(tiles.ctypes.data, rows, k, q.ctypes.data)
+    return q
+
+
+def q8_weight_tiles(blocks_u8, rows, k):
+    """GGUF Q8_0 bytes [rows, k] -> the projection GEMM's weight operands
+    (wq: int8 row tiles, flat; wd: float32 block scales [k/32, ldw], ldw =
+    rows rounded up to 32)."""
     import numpy as np
 
     src = np.ascontiguousarray(blocks_u8, dtype=np.uint8)
-    tiles = (rows + 31) // 32
-    wf = np.zeros((tiles, k // 32, 64, 16), dtype=np.float16)
-    wdf = np.zeros((tiles, k // 32, 64), dtype=np.float32)
-    lib().eg2_q8_fragments(src.ctypes.data, rows, k, wf.ctypes.data, wdf.ctypes.data)
-    return wf, wdf
-
-
-def q8_split(blocks_u8, rows, k):
-    """GGUF Q8_0 bytes -> (fp16 integer values [rows, k], float32 scales [rows, k/32])."""
-    import numpy as np
-
-    src = np.ascontiguousarray(blocks_u8, dtype=np.uint8)
-    q = np.zeros((rows, k), dtype=np.float16)
-    d = np.zeros((rows, k // 32), dtype=np.float32)
-    lib().eg2_q8_split(src.ctypes.data, rows, k, q.ctypes.data, d.ctypes.data)
-    return q, d
+    wq = np.zeros(q8_tile_bytes(rows, k), dtype=np.int8)
+    wd = np.zeros((k // 32, (rows + 31) // 32 * 32), dtype=np.float32)
+    lib().eg2_q8_weight_tiles(src.ctypes.data, rows, k, wq.ctypes.data, wd.ctypes.data)
+    return wq, wd
 
 
 class ops:
@@ -381,10 +397,12 @@ class ops:
               name)
 
     @classmethod
-    def gemm_q8(cls, xq, xd, wf, wdf, y, m=None):
-        """y[:, :m] = xq . W^T with xd the activation scales [k/32, ldx] and
-        (wf, wdf) the weights from q8_fragments (m defaults to y's width)."""
-        n, k = xq.shape
+    def gemm_q8(cls, xq, xd, wq, wd, y, m=None):
+        """y[:, :m] = xq . W^T: xq int8 row tiles of y.shape[0] rows with the
+        activation scales xd [k/32, ldx]; (wq, wd) the weights from
+        q8_weight_tiles (m defaults to y's width)."""
+        n = y.shape[0]
+        k = 32 * xd.shape[0]
         m = y.shape[1] if m is None else m
-        check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wf), cls._p(wdf), cls._p(y), n, m, k,
-                                    y.shape[1], cls._stream()), "gemm_q8")
+        check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wq), cls._p(wd), wd.shape[1],
+                                    cls._p(y), n, m, k, y.shape[1], cls._stream()), "gemm_q8")

@@ -5,14 +5,17 @@
  * Device entry points take device pointers, unsigned sizes and a HIP stream
  * (hipStream_t passed as void*, NULL = the null stream). They enqueue work
  * and return 0 or a hipError_t code (eg2_hip_error_string names it); they
- * never synchronise. Q8_0 activations use a split layout: the int8 values
- * stored as fp16 integers [rows][k] (exact) and one float per 32-block
- * holding the value of the block's fp16 scale, stored transposed as
- * [k/32][rows] (the order the projection GEMM reads them in). Q8_0 weights
- * use the fragment-major layout of eg2_q8_fragments. fp16 buffers are passed
- * as uint16_t bit patterns. The attention
- * operands are fp32 values split into fp16 pairs, rows [hi | lo] with
- * hi = fp16(x), lo = fp16(x - hi).
+ * never synchronise. Q8_0 activations and weights use a split layout: the
+ * int8 values in "row tiles" and one float per 32-block holding the value
+ * of the block's fp16 scale, stored transposed as [k/32][ld] (the order
+ * the projection GEMM reads them in). Row tiles are int8
+ * [ceil(rows/32)][k/32][2][32][16]: value e of row r is at byte
+ * ((((r / 32) * (k/32) + e / 32) * 2 + (e / 16) % 2) * 512 + (r % 32) * 16
+ * + e % 16, so each 32 x 32 block is 1 KB in the register order of the int8
+ * MFMA operand (eg2_q8_tile_bytes gives the size; eg2_q8_pack_rows and
+ * eg2_q8_unpack_rows convert from and to row-major int8). fp16 buffers are
+ * passed as uint16_t bit patterns. The attention operands are fp32 values
+ * split into fp16 pairs, rows [hi | lo] with hi = fp16(x), lo = fp16(x - hi).
  *
  * Each entry names the reference function whose semantics it implements
  * (paths relative to vendor/embeddinggemma.c/src/ unless they start with
@@ -37,13 +40,13 @@ extern "C" {
  * GGUF Q8_0 table) fused with kernels.c:139-151 ei_rms_norm_quantize_q8_0
  * (layer-0 attn_norm) into xq/xd. Replaces kernels/eg2.c:36-39 eg2_gather. */
 int eg2_hip_embed_norm_quant(const void *table_q8, const int32_t *ids, unsigned rows, float embed_scale,
-                             const float *norm_w, float eps, float *x, uint16_t *xq, float *xd, void *stream);
+                             const float *norm_w, float eps, float *x, int8_t *xq, float *xd, void *stream);
 
 /* kernels.c:163-188 ei_rms_norm_residual_inplace (x += rms(h)*post_w) then,
  * when next_w != NULL, kernels.c:139-151 on the updated x. Replaces
  * kernels/eg2.c:192-202 eg2_norm_residual + the following eg2_norm. */
 int eg2_hip_residual_norm_quant(float *x, const float *h, const float *post_w, const float *next_w, float eps,
-                                uint16_t *xq, float *xd, unsigned rows, void *stream);
+                                int8_t *xq, float *xd, unsigned rows, void *stream);
 
 /* kernels.c:233-264 ei_qk_norm_rope_qk_inplace on rows of the fused
  * [q 768 | k 256 | v 256] projection; rope_table[pos][0..127] = cos,
@@ -64,12 +67,13 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * wrote must hold finite values, e.g. zeros). The work list `tiles`
  * (device, 4 uint32 per tile, from eg2_attention_tiles) holds *tile_count
  * (device) query tiles; `grid` workgroups stride over it. The fp32 context
- * is quantized to Q8_0 (quants.c:97-177) into cq [rows][768] and cd
- * [24][rows]. A sequence's result does not depend on its place in the wave.
+ * is quantized to Q8_0 (quants.c:97-177) into cq (row tiles, k = 768) and
+ * cd [24][rows]. A sequence's result does not depend on its place in the
+ * wave.
  * Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const int32_t *vcol,
                       const uint32_t *tiles, const uint32_t *tile_count, unsigned grid, unsigned window,
-                      unsigned rows, uint16_t *cq, float *cd, void *stream);
+                      unsigned rows, int8_t *cq, float *cd, void *stream);
 
 /* Host: the query-tile list of a packed wave with sequences
  * [offsets[s], offsets[s+1]) -- up to 16 queries of one sequence per tile as
@@ -85,10 +89,10 @@ size_t eg2_attention_vt_columns(const size_t *offsets, size_t batch, int32_t *vc
 
 /* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
  * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */
-int eg2_hip_gelu_quant(const float *gate_up, uint16_t *gq, float *gd, unsigned rows, void *stream);
+int eg2_hip_gelu_quant(const float *gate_up, int8_t *gq, float *gd, unsigned rows, void *stream);
 
 /* quants.c:97-177 ei_quantize_row_q8_0 on rows of width k (k % 64 == 0). */
-int eg2_hip_quantize_rows(const float *x, unsigned k, uint16_t *q, float *d, unsigned rows, void *stream);
+int eg2_hip_quantize_rows(const float *x, unsigned k, int8_t *q, float *d, unsigned rows, void *stream);
 
 /* kernels.c:158-161 ei_rms_norm_inplace on rows of width 768. */
 int eg2_hip_rms_norm_rows(float *x, const float *w, float eps, unsigned rows, void *stream);
@@ -105,12 +109,13 @@ int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, vo
 
 /* y[n][m] (row stride ldy) = Q8_0 activations [n][k] . Q8_0 weights [m][k]^T
  * with the reference's arithmetic (gemma2.c:120-141): exact integer block
- * dots on MFMA, each scaled ((float)dot * d_w) * d_x and summed in block
- * order in fp32 -- bit-identical to the CPU path. xd holds the activation
- * block scales [k/32][ldx] (ldx >= n); wf/wdf are the weights as written by
- * eg2_q8_fragments. Replaces kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0,
- * k <= 14336. */
-int eg2_hip_gemm_q8(const uint16_t *xq, const float *xd, unsigned ldx, const uint16_t *wf, const float *wdf,
+ * dots on int8 MFMA, each scaled ((float)dot * d_w) * d_x and summed in
+ * block order in fp32 -- bit-identical to the CPU path. xq/wq are row
+ * tiles; xd holds the activation block scales [k/32][ldx] (ldx >= n), wd
+ * the weight block scales [k/32][ldw] (ldw >= m; eg2_q8_weight_tiles writes
+ * both weight arrays). Replaces kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0;
+ * n, m, k and the strides at most 2^24. */
+int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd, unsigned ldw,
                     float *y, unsigned n, unsigned m, unsigned k, unsigned ldy, void *stream);
 
 /* ------------------------------------------------------------ executor phases
@@ -136,20 +141,19 @@ const char *eg2_hip_error_string(int code);
 /* 0 when the current HIP device is a gfx950; otherwise -1 and a reason. */
 int eg2_hip_device_check(char *err, size_t len);
 
-/* GGUF Q8_0 rows (34-byte blocks) -> split layout: q[rows][k] as fp16
- * integer bit patterns, d[rows][k/32] the exact float value of each fp16
- * scale (common.h:17-40). */
-void eg2_q8_split(const void *blocks, size_t rows, unsigned k, uint16_t *q, float *d);
+/* Bytes of a row-tile buffer for `rows` rows of k values (rows rounded up
+ * to 32). */
+size_t eg2_q8_tile_bytes(size_t rows, unsigned k);
 
-/* GGUF Q8_0 rows [rows][k] (34-byte blocks) -> the projection GEMM's
- * fragment-major weight layout: wf [ceil(rows/32)][k/32][64][16] fp16 integer
- * bit patterns, where entry (t, b, lane) holds row 32t + lane % 32, columns
- * 32b + 16 * (lane / 32) .. +15, and wdf [ceil(rows/32)][k/32][64] the float
- * value of that row's block scale. Rows past `rows` are zero.
- * eg2_q8_fragment_halves gives the size of wf in fp16 values (wdf has 1/16
- * of it). */
-void eg2_q8_fragments(const void *blocks, size_t rows, unsigned k, uint16_t *wf, float *wdf);
-size_t eg2_q8_fragment_halves(size_t rows, unsigned k);
+/* Row-major int8 q[rows][k] -> row tiles (padding rows zero), and back. */
+void eg2_q8_pack_rows(const int8_t *q, size_t rows, unsigned k, int8_t *tiles);
+void eg2_q8_unpack_rows(const int8_t *tiles, size_t rows, unsigned k, int8_t *q);
+
+/* GGUF Q8_0 rows [rows][k] (34-byte blocks) -> the projection GEMM's weight
+ * operands: wq, the int8 values as row tiles (eg2_q8_tile_bytes(rows, k)
+ * bytes; padding rows zero), and wd [k/32][ldw], ldw = rows rounded up to
+ * 32, the exact float value of each block's fp16 scale (common.h:17-40). */
+void eg2_q8_weight_tiles(const void *blocks, size_t rows, unsigned k, int8_t *wq, float *wd);
 
 /* RoPE table for positions 0..n_pos-1: row p = [cos(theta_0..127) |
  * sin(theta_0..127)], theta_i = p * powf(base, -2i/256), computed with the

@@ -40,11 +40,16 @@ def split(blocks, k):
     return blocks["qs"].reshape(blocks.shape[0], k), blocks["d"].view(np.float16).astype(np.float32)
 
 
-def qvals(t):
-    """fp16-integer Q8_0 values on the device -> int32 on the host."""
-    a = host(t).astype(np.float32)
-    assert np.array_equal(a, np.round(a)) and np.abs(a).max() <= 128
-    return a.astype(np.int32)
+def qbuf(eg2, rows, k, gpu):
+    """A device buffer for Q8_0 values of `rows` rows of width k (row tiles)."""
+    import torch
+
+    return torch.zeros(eg2.q8_tile_bytes(rows, k), dtype=torch.int8, device=gpu)
+
+
+def qvals(eg2, t, rows, k):
+    """Row-tile Q8_0 values on the device -> int32 [rows, k] on the host."""
+    return eg2.q8_unpack_rows(host(t), rows, k).astype(np.int32)
 
 
 def split_pairs(x):
@@ -62,10 +67,10 @@ def test_quantize_rows_bit_exact(eg2, gpu):
     x[1, :32] = 0.5
     x[1, 32:64] = 63.5
     x[2, ::2] = -x[2, ::2]
-    q, d = empty((96, N_EMBD), torch.float16, gpu), empty((24, 96), torch.float32, gpu)
+    q, d = qbuf(eg2, 96, N_EMBD, gpu), empty((24, 96), torch.float32, gpu)
     eg2.ops.quantize_rows(dev(x, gpu), q, d)
     wq, wd = split(quantize_q8_0(x), N_EMBD)
-    assert np.array_equal(qvals(q), wq)
+    assert np.array_equal(qvals(eg2, q, 96, N_EMBD), wq)
     assert np.array_equal(host(d).T, wd)
 
 
@@ -77,7 +82,7 @@ def test_embed_norm_quant_bit_exact(eg2, gpu):
     ids = RNG.integers(0, vocab, 128).astype(np.int32)
     w = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     scale = float(np.sqrt(np.float32(768)))
-    x, xq, xd = empty((128, N_EMBD), torch.float32, gpu), empty((128, N_EMBD), torch.float16, gpu), \
+    x, xq, xd = empty((128, N_EMBD), torch.float32, gpu), qbuf(eg2, 128, N_EMBD, gpu), \
         empty((24, 128), torch.float32, gpu)
     eg2.ops.embed_norm_quant(dev(table.view(np.uint8), gpu), dev(ids, gpu), scale, dev(w, gpu), 1e-6, x, xq, xd)
     o = oracle()
@@ -89,7 +94,7 @@ def test_embed_norm_quant_bit_exact(eg2, gpu):
     for t in range(128):
         o.or_rms_norm_quantize_q8_0(fptr(want_x[t]), fptr(w), N_EMBD, 1e-6, vptr(blocks[t]))
     wq, wd = split(blocks, N_EMBD)
-    assert np.array_equal(qvals(xq), wq)
+    assert np.array_equal(qvals(eg2, xq, 128, N_EMBD), wq)
     assert np.array_equal(host(xd).T, wd)
 
 
@@ -103,7 +108,7 @@ def test_residual_norm_quant_bit_exact(eg2, gpu, with_next):
     pw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     nw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
     xg = dev(x, gpu)
-    xq, xd = empty((rows, N_EMBD), torch.float16, gpu), empty((24, rows), torch.float32, gpu)
+    xq, xd = qbuf(eg2, rows, N_EMBD, gpu), empty((24, rows), torch.float32, gpu)
     eg2.ops.residual_norm_quant(xg, dev(h, gpu), dev(pw, gpu), dev(nw, gpu) if with_next else None, 1e-6, xq, xd)
     o = oracle()
     want = x.copy()
@@ -114,7 +119,7 @@ def test_residual_norm_quant_bit_exact(eg2, gpu, with_next):
     assert np.array_equal(host(xg), want)
     if with_next:
         wq, wd = split(blocks, N_EMBD)
-        assert np.array_equal(qvals(xq), wq)
+        assert np.array_equal(qvals(eg2, xq, rows, N_EMBD), wq)
         assert np.array_equal(host(xd).T, wd)
 
 
@@ -163,14 +168,14 @@ def test_gelu_quant_matches_up_to_tanh_ulps(eg2, gpu):
     rows = 128
     gate = (RNG.standard_normal((rows, N_FF)) * 2).astype(np.float32)
     up = RNG.standard_normal((rows, N_FF)).astype(np.float32)
-    gq, gd = empty((rows, N_FF), torch.float16, gpu), empty((36, rows), torch.float32, gpu)
+    gq, gd = qbuf(eg2, rows, N_FF, gpu), empty((36, rows), torch.float32, gpu)
     eg2.ops.gelu_quant(dev(np.concatenate([gate, up], 1), gpu), gq, gd)
     o = oracle()
     blocks = np.zeros((rows, 36), dtype=Q8)
     for t in range(rows):
         o.or_gelu_mul_quantize_q8_0(fptr(gate[t]), fptr(up[t]), N_FF, vptr(blocks[t]))
     wq, wd = split(blocks, N_FF)
-    gq, gd = qvals(gq), host(gd).T
+    gq, gd = qvals(eg2, gq, rows, N_FF), host(gd).T
     same_d = gd == wd
     assert same_d.mean() > 0.99
     qd = np.abs(gq.astype(np.int32) - wq).reshape(rows, 36, 32)
@@ -178,17 +183,17 @@ def test_gelu_quant_matches_up_to_tanh_ulps(eg2, gpu):
     assert (qd.max(2) == 0).mean() > 0.98
 
 
-def device_q8(blocks, k, gpu):
-    """Oracle Q8_0 activation blocks -> the kernels' layout (fp16 integers
-    [rows, k] + float scales transposed [k/32, rows])."""
+def device_q8(eg2, blocks, k, gpu):
+    """Oracle Q8_0 activation blocks -> the kernels' layout (int8 row tiles
+    + float scales transposed [k/32, rows])."""
     q, d = split(blocks, k)
-    return dev(q.astype(np.float16), gpu), dev(d.T, gpu)
+    return dev(eg2.q8_pack_rows(q), gpu), dev(d.T, gpu)
 
 
 def device_weights(eg2, blocks, k, gpu):
-    """Oracle Q8_0 weight blocks -> the GEMM's fragment-major layout."""
-    wf, wdf = eg2.q8_fragments(blocks.view(np.uint8), blocks.shape[0], k)
-    return dev(wf, gpu), dev(wdf, gpu)
+    """Oracle Q8_0 weight blocks -> the GEMM's weight operands."""
+    wq, wd = eg2.q8_weight_tiles(blocks.view(np.uint8), blocks.shape[0], k)
+    return dev(wq, gpu), dev(wd, gpu)
 
 
 @pytest.mark.parametrize("n,m,k", [(512, 2304, 768), (2048, 1280, 768), (2048, 768, 1152), (33, 40, 64),
@@ -202,7 +207,7 @@ def test_gemm_q8_bit_exact(eg2, gpu, n, m, k):
     xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
     xb[0, 0]["qs"][:] = -128  # the most negative Q8_0 value round-trips too
     y = empty((n, m), torch.float32, gpu)
-    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_weights(eg2, w, k, gpu), y)
+    eg2.ops.gemm_q8(*device_q8(eg2, xb, k, gpu), *device_weights(eg2, w, k, gpu), y)
     assert np.array_equal(host(y), OL.gemm_q8_0(w, xb))
 
 
@@ -214,7 +219,7 @@ def test_gemm_q8_strided_output(eg2, gpu):
     w = quantize_q8_0((RNG.standard_normal((m, k)) * 0.02).astype(np.float32))
     xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
     y = torch.full((n, 160), 7.0, dtype=torch.float32, device=gpu)
-    eg2.ops.gemm_q8(*device_q8(xb, k, gpu), *device_weights(eg2, w, k, gpu), y, m=m)
+    eg2.ops.gemm_q8(*device_q8(eg2, xb, k, gpu), *device_weights(eg2, w, k, gpu), y, m=m)
     got = host(y)
     assert np.array_equal(got[:, :m], OL.gemm_q8_0(w, xb))
     assert (got[:, m:] == 7.0).all()
@@ -251,11 +256,11 @@ def run_attention(eg2, gpu, q, k, v, offsets, window, fill=0.0):
     import torch
 
     T = q.shape[0]
-    cq, cd = empty((T, N_EMBD), torch.float16, gpu), empty((24, T), torch.float32, gpu)
+    cq, cd = qbuf(eg2, T, N_EMBD, gpu), empty((24, T), torch.float32, gpu)
     vt, vcol = transposed_v(eg2, v, offsets, gpu, fill)
     eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), vt, vcol,
                       offsets, window, cq, cd)
-    return qvals(cq), np.ascontiguousarray(host(cd).T)
+    return qvals(eg2, cq, T, N_EMBD), np.ascontiguousarray(host(cd).T)
 
 
 def attention_double(q, k, v, offsets, window):

@@ -56,11 +56,12 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     lib = eg2.lib()
     inval = 1  # hipErrorInvalidValue
     p = C.c_void_p(16)
-    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 4, 33, 4, None) == inval  # k % 32
-    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 8, 32, 4, None) == inval  # ldy < m
-    assert lib.eg2_hip_gemm_q8(p, p, 3, p, p, p, 4, 4, 32, 4, None) == inval  # ldx < n
-    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, p, 4, 4, 32 * 449, 4, None) == inval  # k above the LDS limit
-    assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, p, 4, 4, 32, 4, None) == inval
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 33, 4, None) == inval  # k % 32
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 8, p, 4, 8, 32, 4, None) == inval  # ldy < m
+    assert lib.eg2_hip_gemm_q8(p, p, 3, p, p, 4, p, 4, 4, 32, 4, None) == inval  # ldx < n
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
+    assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
     assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
     assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, None) == inval
     assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, None) == inval
@@ -110,39 +111,43 @@ def test_rope_table_matches_oracle(eg2, base):
         assert np.array_equal(t[p, 128:], s), p
 
 
-def test_q8_split_is_the_exact_decode(eg2):
+def tile_offset(r, e, k):
+    """Byte offset of value e of row r in a row-tile buffer, written out from
+    the layout's definition: [rows/32][k/32][2][32][16] int8."""
+    return ((((r // 32) * (k // 32) + e // 32) * 2 + (e // 16) % 2) * 32 + r % 32) * 16 + e % 16
+
+
+def test_q8_row_tiles_layout_and_round_trip(eg2):
     rng = np.random.default_rng(0)
-    blocks = quantize_q8_0((rng.standard_normal((10, 96)) * 10.0 ** rng.uniform(-6, 2, (10, 1))).astype(np.float32))
-    blocks[0, 0]["qs"][:4] = [-128, 127, 0, -1]
-    q, d = eg2.q8_split(blocks.view(np.uint8), 10, 96)
-    assert q.dtype == np.float16
-    assert np.array_equal(q.reshape(10, 3, 32).astype(np.int32), blocks["qs"].astype(np.int32))
-    assert np.array_equal(d, blocks["d"].view(np.float16).astype(np.float32))
-    deq = (q.reshape(10, 3, 32).astype(np.float32) * d[:, :, None]).reshape(10, 96)
-    assert np.array_equal(deq, dequantize_q8_0(blocks))
+    for rows, k in [(1, 32), (45, 96), (64, 768), (33, 1152)]:
+        q = rng.integers(-128, 128, (rows, k)).astype(np.int8)
+        tiles = eg2.q8_pack_rows(q)
+        assert tiles.size == eg2.q8_tile_bytes(rows, k) == -(-rows // 32) * (k // 32) * 1024
+        r, e = np.meshgrid(np.arange(rows), np.arange(k), indexing="ij")
+        assert np.array_equal(tiles[tile_offset(r, e, k)], q)
+        covered = np.zeros(tiles.size, bool)
+        covered[tile_offset(r, e, k)] = True
+        assert not tiles[~covered].any()  # padding rows are zero
+        assert np.array_equal(eg2.q8_unpack_rows(tiles, rows, k), q)
 
 
-def test_q8_fragments_layout(eg2):
-    """Fragment-major weights: entry (t, b, lane) = row 32t + lane % 32,
-    columns 32b + 16 * (lane // 32) .. +15 of the block, with the row's
-    block scale; rows past the matrix are zero."""
+def test_q8_weight_tiles_are_the_exact_decode(eg2):
+    """Weights: int8 values in row tiles and the exact float value of each
+    fp16 block scale, transposed [k/32][rows rounded up to 32] (zero past
+    the matrix); value * scale is the reference dequantization."""
     rng = np.random.default_rng(1)
     rows, k = 45, 96
-    blocks = quantize_q8_0((rng.standard_normal((rows, k)) * 0.02).astype(np.float32))
-    wf, wdf = eg2.q8_fragments(blocks.view(np.uint8), rows, k)
-    assert wf.shape == (2, 3, 64, 16) and wdf.shape == (2, 3, 64)
-    assert eg2.lib().eg2_q8_fragment_halves(rows, k) == wf.size
-    q, d = eg2.q8_split(blocks.view(np.uint8), rows, k)
-    for t in range(2):
-        for b in range(3):
-            for lane in range(64):
-                r = 32 * t + lane % 32
-                if r < rows:
-                    c0 = 32 * b + 16 * (lane // 32)
-                    assert np.array_equal(wf[t, b, lane], q[r, c0:c0 + 16])
-                    assert wdf[t, b, lane] == d[r, b]
-                else:
-                    assert not wf[t, b, lane].any() and wdf[t, b, lane] == 0
+    blocks = quantize_q8_0((rng.standard_normal((rows, k)) * 10.0 ** rng.uniform(-6, 2, (rows, 1))).astype(np.float32))
+    blocks[0, 0]["qs"][:4] = [-128, 127, 0, -1]
+    wq, wd = eg2.q8_weight_tiles(blocks.view(np.uint8), rows, k)
+    assert wd.shape == (3, 64)
+    q = eg2.q8_unpack_rows(wq, rows, k)
+    assert np.array_equal(q.reshape(rows, 3, 32), blocks["qs"])
+    assert np.array_equal(wd[:, :rows].T, blocks["d"].view(np.float16).astype(np.float32))
+    assert not wd[:, rows:].any()
+    assert not eg2.q8_unpack_rows(wq, 64, k)[rows:].any()
+    deq = (q.reshape(rows, 3, 32).astype(np.float32) * wd[:, :rows].T[:, :, None]).reshape(rows, k)
+    assert np.array_equal(deq, dequantize_q8_0(blocks))
 
 
 @pytest.fixture(scope="module")
