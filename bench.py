@@ -27,7 +27,9 @@ sys.path.insert(0, ROOT)
 
 TOKENS, SEQS, LAYERS = 2048, 16, 24
 GEMM_N, GEMM_M, GEMM_K = 2048, 2 * 1152, 768
-PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA (the projection GEMMs)
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (attention)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 METRIC = "embedded tokens/s @2048-tok packed waves (1 GPU); Q8_0 GEMM % MFMA peak"
 
 
@@ -50,31 +52,110 @@ def cpu_baseline(path, ids, offsets, threads):
     return TOKENS / dt, dt, out
 
 
-def time_gemm(eg2, torch, steps, warmup):
-    """Average duration of the gate|up projection GEMM (one launch)."""
-    import numpy as np
-
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device="cpu").manual_seed(0)
-    # Q8_0 operands in the kernel layouts: int8 row tiles, block scales
-    # transposed [k/32][rows].
-    xq = torch.randint(-127, 128, (eg2.q8_tile_bytes(GEMM_N, GEMM_K),), generator=g, dtype=torch.int8).to(dev)
-    wq = torch.randint(-127, 128, (eg2.q8_tile_bytes(GEMM_M, GEMM_K),), generator=g, dtype=torch.int8).to(dev)
-    xd = (torch.rand((GEMM_K // 32, GEMM_N), generator=g) * 0.01).to(dev)
-    wd = (torch.rand((GEMM_K // 32, GEMM_M), generator=g) * 0.001).to(dev)
-    y = torch.empty((GEMM_N, GEMM_M), dtype=torch.float32, device=dev)
+def time_launches(torch, fn, steps, warmup):
+    """Average ms per call of fn (kernel launches on torch's current stream,
+    which the operator entry points use), timed with HIP events recorded on
+    that stream."""
     for _ in range(warmup):
-        eg2.ops.gemm_q8(xq, xd, wq, wd, y)
+        fn()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
-        eg2.ops.gemm_q8(xq, xd, wq, wd, y)
+        fn()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / steps
+
+
+def gemm_operands(eg2, torch, n, m, k, g):
+    """Random Q8_0 operands in the kernel layouts: int8 row tiles, block
+    scales transposed [k/32][rows]."""
+    dev = torch.device("cuda:0")
+    xq = torch.randint(-127, 128, (eg2.q8_tile_bytes(n, k),), generator=g, dtype=torch.int8).to(dev)
+    wq = torch.randint(-127, 128, (eg2.q8_tile_bytes(m, k),), generator=g, dtype=torch.int8).to(dev)
+    xd = (torch.rand((k // 32, n), generator=g) * 0.01).to(dev)
+    wd = (torch.rand((k // 32, m), generator=g) * 0.001).to(dev)
+    y = torch.empty((n, m), dtype=torch.float32, device=dev)
+    return xq, xd, wq, wd, y
+
+
+def time_gemm(eg2, torch, steps, warmup):
+    """Average duration of the gate|up projection GEMM (one launch)."""
+    import numpy as np
+
+    g = torch.Generator(device="cpu").manual_seed(0)
+    xq, xd, wq, wd, y = gemm_operands(eg2, torch, GEMM_N, GEMM_M, GEMM_K, g)
+    ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, warmup)
     assert np.isfinite(y[:4, :4].cpu().numpy()).all()
     return ms
+
+
+def kernel_table(eg2, torch, steps):
+    """Every kernel of one 2048-token layer (16 x 128 packing), launched
+    alone on synthetic inputs of its real shape: average us, and the
+    achieved rate against its roofline -- int8 MFMA for the projection
+    GEMMs, fp16 MFMA for attention (algorithmic 3072 * sum L^2 FLOP; the
+    kernel runs 3 split-fp16 passes of it), HBM for the row kernels
+    (algorithmic bytes: each input read once, each output written once)."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(1)
+    T, E, F, D = TOKENS, 768, 1152, 256
+    out = {}
+
+    def rec(name, ms, work, unit, peak):
+        rate = work / (ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
+        out[name] = {"us": round(ms * 1e3, 2), "achieved": round(rate, 1), "unit": unit, "peak": peak,
+                     "frac": round(rate / peak, 4)}
+
+    for name, (m, k) in {"gemm_qkv 2048x1280x768": (1280, E), "gemm_o 2048x768x768": (E, E),
+                         "gemm_gate_up 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
+        xq, xd, wq, wd, y = gemm_operands(eg2, torch, T, m, k, g)
+        ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
+        rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS)
+
+    rnd = lambda *shape: torch.randn(*shape, generator=g).to(dev)
+    w_e, w_d = torch.ones(E, device=dev), torch.ones(D, device=dev)
+    # Row kernels: bytes per token as read + written by each.
+    x, h = rnd(T, E), rnd(T, E) * 0.5
+    xq = torch.zeros(eg2.q8_tile_bytes(T, F), dtype=torch.int8, device=dev)
+    xd = torch.zeros((F // 32, T), device=dev)
+    ms = time_launches(torch, lambda: eg2.ops.residual_norm_quant(x, h, w_e, w_e, 1e-6, xq, xd), steps, 3)
+    rec("residual_norm_quant", ms, T * (3 * 4 * E + E + 4 * E // 32), "GB/s", PEAK_HBM_GBS)
+    gu = rnd(T, 2 * F)
+    ms = time_launches(torch, lambda: eg2.ops.gelu_quant(gu, xq, xd), steps, 3)
+    rec("gelu_quant", ms, T * (4 * 2 * F + F + 4 * F // 32), "GB/s", PEAK_HBM_GBS)
+    vocab = 4096
+    table = np.zeros((vocab, 24, 34), np.uint8)
+    table[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    table[:, :, 2:] = np.random.default_rng(0).integers(0, 256, (vocab, 24, 32))
+    table_d = torch.from_numpy(table.reshape(-1)).to(dev)
+    ids = torch.randint(0, vocab, (T,), generator=g, dtype=torch.int32).to(dev)
+    ms = time_launches(torch, lambda: eg2.ops.embed_norm_quant(table_d, ids, 27.7, w_e, 1e-6, x, xq, xd),
+                       steps, 3)
+    rec("embed_norm_quant", ms, T * (816 + 4 * E + E + 4 * E // 32), "GB/s", PEAK_HBM_GBS)
+    # QK-norm/RoPE and attention on the 16 x 128 packing.
+    offsets = list(range(0, T + 1, T // SEQS))
+    qkv = rnd(T, eg2.QKV_COLS)
+    rope = torch.from_numpy(eg2.rope_table(1e4)).to(dev)
+    pos = torch.tensor([t - (t // 128) * 128 for t in range(T)], dtype=torch.int32, device=dev)
+    vcol_np, ldv = eg2.attention_vt_columns(offsets)
+    vcol = torch.from_numpy(vcol_np).to(dev)
+    qs = torch.zeros((T, 2 * E), dtype=torch.float16, device=dev)
+    ks = torch.zeros((T, 2 * D), dtype=torch.float16, device=dev)
+    vt = torch.zeros((2, D, ldv), dtype=torch.float16, device=dev)
+    ms = time_launches(torch, lambda: eg2.ops.qk_norm_rope(qkv, w_d, w_d, rope, pos, vcol, 1e-6, qs, ks, vt),
+                       steps, 3)
+    rec("qk_norm_rope", ms, T * (4 * (E + 2 * D) + 2 * 2 * (E + 2 * D)), "GB/s", PEAK_HBM_GBS)
+    cq = torch.zeros(eg2.q8_tile_bytes(T, E), dtype=torch.int8, device=dev)
+    cd = torch.zeros((E // 32, T), device=dev)
+    att = eg2.AttentionPlan(offsets, dev)
+    ms = time_launches(torch, lambda: eg2.ops.attention_planned(qs, ks, vt, vcol, att, 0, cq, cd), steps, 3)
+    rec("attention 16x128", ms, 3072.0 * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS)), "TFLOP/s",
+        PEAK_FP16_TFLOPS)
+    return out
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q8_gate_up_2048x2304x768_traffic.md")
@@ -101,14 +182,17 @@ def measured_traffic():
 
 def kernel_only(kind, steps):
     """Counter-collection mode: only the gate|up GEMM, or a plain device copy
-    of COPY_MIB (the calibration kernel for FETCH_SIZE/WRITE_SIZE)."""
+    of COPY_MIB (the calibration kernel for FETCH_SIZE/WRITE_SIZE), or only
+    the per-kernel table of one layer."""
     import torch
 
     import __graft_entry__
 
     eg2 = __graft_entry__._package()
     torch.cuda.set_device(0)
-    if kind == "gate_up":
+    if kind == "table":
+        print(json.dumps(kernel_table(eg2, torch, steps)))
+    elif kind == "gate_up":
         ms = time_gemm(eg2, torch, steps, 2)
         print(json.dumps({"kernel": "gemm_q8 gate|up 2048x2304x768", "avg_us": round(ms * 1e3, 2), "launches": steps + 2}))
     else:
@@ -130,8 +214,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-only", choices=["gate_up", "copy"],
-                    help="run only the dominant GEMM (or the copy calibration kernel) for counter runs")
+    ap.add_argument("--kernel-only", choices=["gate_up", "copy", "table"],
+                    help="run only the dominant GEMM (or the copy calibration kernel) for counter runs, "
+                         "or only the per-kernel table")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has a single MI355X and this path runs "
@@ -188,7 +273,10 @@ def main():
         gemm_ms = time_gemm(eg2, torch, max(20, args.steps), 5)
         flops = 2.0 * GEMM_N * GEMM_M * GEMM_K
         achieved = flops / (gemm_ms / 1e3) / 1e12
-        log(f"gate|up GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} TFLOP/s")
+        log(f"gate|up GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s")
+        kernels = kernel_table(eg2, torch, max(20, args.steps))
+        for name, k in kernels.items():
+            log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak")
 
         cpu = None
         if not args.no_cpu_baseline:
@@ -213,16 +301,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": "int8 x int8 -> fp32 (GEMMs); fp32 (row ops, softmax)",
         "data": "synthetic",
         "config": {"workload": "24-layer Q8_0 EmbeddingGemma-300M-shape encoder forward + dense head, one "
                                "packed wave of 16x128 tokens", "tokens_per_wave": TOKENS, "sequences": SEQS,
                    "layers": LAYERS, "hidden": 768, "ffn": 1152, "heads": "3q/1kv x 256", "weights": "Q8_0",
                    "attention": "full within sequence, RoPE base 1e4"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_q8 gate|up 2048x2304x768",
-                     "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": measured_traffic(),
+        "roofline": {"bound": "mfma", "kernel": "gemm_q8 gate|up 2048x2304x768 (v_mfma_i32_32x32x32_i8; "
+                                                "achieved/peak in T int8 op/s)",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
                      "avg_us": round(gemm_ms * 1e3, 2)},
+        "kernels": kernels,
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),
     }

@@ -39,26 +39,28 @@ __device__ __forceinline__ uint32_t pack_i8x4(int32_t a, int32_t b, int32_t c, i
 // fp32 -> fp16 bits with the reference's rounding (quants.c:13-37): the
 // dropped mantissa bits round half-up in magnitude (not to nearest-even),
 // and any value of 2^16 or more with a nonzero mantissa maps to a NaN.
-__device__ __forceinline__ uint32_t fp32_to_fp16_bits(float f) {
+// Written without branches (every case computed, one selected) so that it
+// costs a few VALU operations inside quantizing epilogues; identical to the
+// branching form for all 2^32 inputs.
+__host__ __device__ inline uint32_t fp32_to_fp16_bits(float f) {
+#ifdef __HIP_DEVICE_COMPILE__
   const uint32_t x = __float_as_uint(f);
+#else
+  uint32_t x;
+  __builtin_memcpy(&x, &f, 4);
+#endif
   const uint32_t sign = (x >> 16) & 0x8000u;
-  uint32_t mant = x & 0x007FFFFFu;
+  const uint32_t mant = x & 0x007FFFFFu;
   const int32_t e = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
-  if (e <= 0) {
-    if (e < -10) return sign;
-    mant |= 0x00800000u;
-    const uint32_t shift = (uint32_t)(14 - e);
-    uint32_t h = sign | (mant >> shift);
-    if ((mant >> (shift - 1u)) & 1u) h++;
-    return h;
-  }
-  if (e >= 31) {
-    if (mant == 0) return sign | 0x7C00u;
-    return sign | 0x7C00u | (mant >> 13) | 1u;
-  }
-  uint32_t h = sign | ((uint32_t)e << 10) | (mant >> 13);
-  if (mant & 0x00001000u) h++;
-  return h;
+  // normal: the rounding carry may step into the exponent (up to 0x7C00)
+  const uint32_t normal = (((uint32_t)e << 10) | (mant >> 13)) + ((mant >> 12) & 1u);
+  // subnormal (-10 <= e <= 0): shift 14 - e in [14, 24]
+  const uint32_t m = mant | 0x00800000u;
+  const uint32_t sh = (uint32_t)(14 - (e < -10 ? -10 : (e > 0 ? 0 : e)));
+  const uint32_t sub = (m >> sh) + ((m >> (sh - 1u)) & 1u);
+  const uint32_t big = 0x7C00u | (mant ? ((mant >> 13) | 1u) : 0u);
+  const uint32_t mag = e >= 31 ? big : (e > 0 ? normal : (e >= -10 ? sub : 0u));
+  return sign | mag;
 }
 
 // Exact fp16 bits -> fp32 (common.h:17-40); the hardware conversion is exact

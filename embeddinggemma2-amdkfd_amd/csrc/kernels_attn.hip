@@ -50,7 +50,6 @@ constexpr int kKvTile = 32;  // keys per LDS stage (one 32-deep MFMA reduction)
 constexpr int kKStage = kKvTile * 2 * kHeadDim * 2;  // [key][hi|lo][256] fp16 = 32 KB
 constexpr int kVStage = 2 * kHeadDim * kKvTile * 2;  // [hi|lo][dim][32 keys] fp16 = 32 KB
 constexpr int kStage = kKStage + kVStage;
-constexpr int kDmaPerStage = kStage / 1024;          // 1 KB DMA instructions per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ floatx4 mfma(const half8& a, const half8& b, const floatx4& c) {
@@ -101,15 +100,20 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       if (t + half + 1 < hi) hi = t + half + 1;
     }
     // Union and intersection of the tile's key ranges (every lane group
-    // holds the same 16 queries).
-    uint32_t kv_lo = active ? lo : 0xFFFFFFFFu, kv_hi = active ? hi : 0u;
-    uint32_t in_lo = active ? lo : 0u, in_hi = active ? hi : 0xFFFFFFFFu;
+    // holds the same 16 queries); without a window both are the sequence.
+    uint32_t kv_lo = seg_lo, kv_hi = seg_hi, in_lo = seg_lo, in_hi = seg_hi;
+    if (window > 0) {
+      kv_lo = active ? lo : 0xFFFFFFFFu;
+      kv_hi = active ? hi : 0u;
+      in_lo = active ? lo : 0u;
+      in_hi = active ? hi : 0xFFFFFFFFu;
 #pragma unroll
-    for (int mk = 8; mk >= 1; mk >>= 1) {
-      kv_lo = min(kv_lo, (uint32_t)__shfl_xor((int)kv_lo, mk, 64));
-      kv_hi = max(kv_hi, (uint32_t)__shfl_xor((int)kv_hi, mk, 64));
-      in_lo = max(in_lo, (uint32_t)__shfl_xor((int)in_lo, mk, 64));
-      in_hi = min(in_hi, (uint32_t)__shfl_xor((int)in_hi, mk, 64));
+      for (int mk = 8; mk >= 1; mk >>= 1) {
+        kv_lo = min(kv_lo, (uint32_t)__shfl_xor((int)kv_lo, mk, 64));
+        kv_hi = max(kv_hi, (uint32_t)__shfl_xor((int)kv_hi, mk, 64));
+        in_lo = max(in_lo, (uint32_t)__shfl_xor((int)in_lo, mk, 64));
+        in_hi = min(in_hi, (uint32_t)__shfl_xor((int)in_hi, mk, 64));
+      }
     }
     kv_lo = __builtin_amdgcn_readfirstlane(kv_lo);
     kv_hi = __builtin_amdgcn_readfirstlane(kv_hi);
@@ -119,26 +123,39 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     const uint32_t k_first = kv_lo >= kv_hi ? kv_hi : seg_lo + ((kv_lo - seg_lo) & ~31u);
     const int col_base = __builtin_amdgcn_readfirstlane(vcol[min(seg_lo, (uint32_t)rows - 1)]) - (int)seg_lo;
 
-    // DMA of key tile k0 into stage s: instructions q = head, head + 3, ...
-    // q < 32: K row of key q; lane L takes half L/32, stored chunk L%32 =
-    // global chunk (L%32) ^ kswz(q). q >= 32: V^T rows 16(q-32)..+15 of half
-    // (q-32)/16; lane L takes dim row L/4, stored chunk L%4 = global chunk
-    // (L%4) ^ vswz(row).
-    auto issue = [&](uint32_t k0, int s) {
-      unsigned char* base = lds + s * kStage;
-      for (int q = head; q < kDmaPerStage; q += 3) {
-        const _Float16* src;
-        if (q < kKvTile) {
-          const uint32_t key = min(k0 + q, (uint32_t)rows - 1);
-          src = ks + (size_t)key * (2 * kHeadDim) + (lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ kswz(q));
-        } else {
-          const int vq = q - kKvTile, hl = vq >> 4, d = 16 * (vq & 15) + (lane >> 2);
-          const int c = (lane & 3) ^ vswz(d);
-          src = vt + ((size_t)hl * kHeadDim + d) * ldv + (col_base + (int)k0) + 8 * c;
-        }
-        dma16(src, base + q * 1024);
-      }
+    // DMA of key tile k0 into stage s, 64 instructions of 1 KB split over
+    // the three waves: wave `head` issues K instruction q and V instruction
+    // q for q = head + 3j < 32 (j = 0..10).
+    // K: row of key q; lane L takes half L/32, stored chunk L%32 = global
+    // chunk (L%32) ^ kswz(q). V: V^T rows 16(q%16)..+15 of half q/16; lane L
+    // takes dim row L/4, stored chunk L%4 = global chunk (L%4) ^ vswz(row).
+    auto dma_k = [&](uint32_t k0, int s, int j) {
+      const int q = head + 3 * j;
+      if (q >= kKvTile) return;
+      const uint32_t key = min(k0 + q, (uint32_t)rows - 1);
+      dma16(ks + (size_t)key * (2 * kHeadDim) + (lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ kswz(q)),
+            lds + s * kStage + q * 1024);
     };
+    auto dma_v = [&](uint32_t k0, int s, int j) {
+      const int q = head + 3 * j;
+      if (q >= kKvTile) return;
+      const int hl = q >> 4, d = 16 * (q & 15) + (lane >> 2), c = (lane & 3) ^ vswz(d);
+      dma16(vt + ((size_t)hl * kHeadDim + d) * ldv + (col_base + (int)k0) + 8 * c,
+            lds + s * kStage + kKStage + q * 1024);
+    };
+    constexpr int kDmaPerWave = (kKvTile + 2) / 3;  // 11
+
+    // Every wave has finished with both stages (previous tile of the grid
+    // stride) before the first DMA overwrites them. The first tile's DMA
+    // then flies while the queries load.
+    __syncthreads();
+    if (k_first < kv_hi) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        dma_k(k_first, 0, j);
+        dma_v(k_first, 0, j);
+      }
+    }
 
     // Q^T operand of the score MFMA: lane holds query t, dims 32s + 8grp .. +7
     // for s = 0..7. Rows of qs are [hi 768 | lo 768].
@@ -155,38 +172,48 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     for (int db = 0; db < 16; ++db) acc[db] = floatx4{};
     float m_run = -INFINITY, l_run = 0.0f;  // running max in log2 units
 
-    // Every wave has finished with both stages (previous tile of the grid
-    // stride) before the first DMA overwrites them.
-    __syncthreads();
-    if (k_first < kv_hi) issue(k_first, 0);
     const int key0 = score_key(0, qi), key1 = score_key(1, qi);
     const int kf0 = kswz(key0), kf1 = kswz(key1);
     int stage = 0;
     for (uint32_t k0 = k_first; k0 < kv_hi; k0 += kKvTile, stage ^= 1) {
-      // This tile's DMA has landed for every wave, and every wave is done
-      // with the other stage, which the next tile's DMA now refills.
+      // This tile's DMA (and the queries) have landed for every wave, and
+      // every wave is done with the other stage, which the next tile's DMA
+      // now refills -- issued in pieces between this tile's MFMAs, so the
+      // memory pipeline's back-pressure overlaps the matrix work.
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if (k0 + kKvTile < kv_hi) issue(k0 + kKvTile, stage ^ 1);
+      const bool more = k0 + kKvTile < kv_hi;
+      const uint32_t k1 = k0 + kKvTile;
       const unsigned char* kst = lds + stage * kStage;
       const unsigned char* vst = kst + kKStage;
 
-      // S^T = K . Q^T, two 16-key blocks.
+      // S^T = K . Q^T, two 16-key blocks; the K fragments of step st + 1
+      // are read from LDS while step st multiplies.
       floatx4 s0 = floatx4{}, s1 = floatx4{};
       const unsigned char* krow0 = kst + key0 * 1024;
       const unsigned char* krow1 = kst + key1 * 1024;
+      half8 kf[2][4];
+      auto load_k = [&](int st, half8 (&f)[4]) {
+        const int c = 4 * st + grp;
+        f[0] = *reinterpret_cast<const half8*>(krow0 + 16 * (c ^ kf0));
+        f[1] = *reinterpret_cast<const half8*>(krow0 + 512 + 16 * (c ^ kf0));
+        f[2] = *reinterpret_cast<const half8*>(krow1 + 16 * (c ^ kf1));
+        f[3] = *reinterpret_cast<const half8*>(krow1 + 512 + 16 * (c ^ kf1));
+      };
+      load_k(0, kf[0]);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const int c = 4 * st + grp;
-        const half8 ah = *reinterpret_cast<const half8*>(krow0 + 16 * (c ^ kf0));
-        const half8 al = *reinterpret_cast<const half8*>(krow0 + 512 + 16 * (c ^ kf0));
-        const half8 bh = *reinterpret_cast<const half8*>(krow1 + 16 * (c ^ kf1));
-        const half8 bl = *reinterpret_cast<const half8*>(krow1 + 512 + 16 * (c ^ kf1));
-        s0 = mfma(ah, qh[st], s0);
-        s0 = mfma(ah, ql[st], s0);
-        s0 = mfma(al, qh[st], s0);
-        s1 = mfma(bh, qh[st], s1);
-        s1 = mfma(bh, ql[st], s1);
-        s1 = mfma(bl, qh[st], s1);
+        const int cur = st & 1;
+        if (st + 1 < 8) load_k(st + 1, kf[cur ^ 1]);
+        s0 = mfma(kf[cur][0], qh[st], s0);
+        s1 = mfma(kf[cur][2], qh[st], s1);
+        s0 = mfma(kf[cur][0], ql[st], s0);
+        s1 = mfma(kf[cur][2], ql[st], s1);
+        s0 = mfma(kf[cur][1], qh[st], s0);
+        s1 = mfma(kf[cur][3], qh[st], s1);
+        if (more) {
+          dma_k(k1, stage ^ 1, st);
+          if (st + 8 < kDmaPerWave) dma_k(k1, stage ^ 1, st + 8);
+        }
       }
       // sc[4kb + v] = 16 x the score of key k0 + 8grp + 4kb + v, taken to
       // log2 units: exp(x) = exp2(x * log2e).
@@ -228,15 +255,34 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 #pragma unroll
       for (int db = 0; db < 16; ++db) acc[db] *= alpha;
 
-      // O^T += V^T . P^T: lane group grp supplies keys 8grp..8grp+7, V^T chunk grp.
+      // O^T += V^T . P^T: lane group grp supplies keys 8grp..8grp+7, V^T chunk
+      // grp. Dimension blocks go in pairs: the V^T fragments of the next pair
+      // are read while this pair multiplies, and each accumulator's three
+      // MFMAs (hi.hi, hi.lo, lo.hi, in that order) alternate with the other's.
+      half8 vf[2][4];
+      auto load_v = [&](int pr, half8 (&f)[4]) {
 #pragma unroll
-      for (int db = 0; db < 16; ++db) {
-        const int d = 16 * db + qi, c = grp ^ vswz(d);
-        const half8 vh = *reinterpret_cast<const half8*>(vst + d * 64 + 16 * c);
-        const half8 vl = *reinterpret_cast<const half8*>(vst + (kHeadDim + d) * 64 + 16 * c);
-        acc[db] = mfma(vh, ph, acc[db]);
-        acc[db] = mfma(vh, pl, acc[db]);
-        acc[db] = mfma(vl, ph, acc[db]);
+        for (int i = 0; i < 2; ++i) {
+          const int d = 16 * (2 * pr + i) + qi, c = grp ^ vswz(d);
+          f[2 * i] = *reinterpret_cast<const half8*>(vst + d * 64 + 16 * c);
+          f[2 * i + 1] = *reinterpret_cast<const half8*>(vst + (kHeadDim + d) * 64 + 16 * c);
+        }
+      };
+      load_v(0, vf[0]);
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) {
+        const int cur = pr & 1, d0 = 2 * pr, d1 = 2 * pr + 1;
+        if (pr + 1 < 8) load_v(pr + 1, vf[cur ^ 1]);
+        acc[d0] = mfma(vf[cur][0], ph, acc[d0]);
+        acc[d1] = mfma(vf[cur][2], ph, acc[d1]);
+        acc[d0] = mfma(vf[cur][0], pl, acc[d0]);
+        acc[d1] = mfma(vf[cur][2], pl, acc[d1]);
+        acc[d0] = mfma(vf[cur][1], ph, acc[d0]);
+        acc[d1] = mfma(vf[cur][3], ph, acc[d1]);
+        if (more) {
+          dma_v(k1, stage ^ 1, pr);
+          if (pr + 8 < kDmaPerWave) dma_v(k1, stage ^ 1, pr + 8);
+        }
       }
     }
 
@@ -244,33 +290,41 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     // acc[db][v] is dim 16db + 4grp + v of query t, so Q8_0 block b (dims
     // 32b..32b+31) sits in acc[2b], acc[2b+1] of the four lane groups. The
     // int8 values go to the row-tile layout of the projection GEMM (4 bytes
-    // per lane and half-block), the scales transposed ([block][row]).
+    // per lane and half-block), the scales transposed ([block][row]). The
+    // eight blocks run phase by phase so their latencies overlap.
+    constexpr int kB = kHeadDim / kQK;
     const float inv_l = 1.0f / l_run;
+    float vals[kB][8], amax[kB];
 #pragma unroll
-    for (int b = 0; b < kHeadDim / kQK; ++b) {
-      float vals[8];
-      float amax = 0.0f;
+    for (int b = 0; b < kB; ++b) {
+      amax[b] = 0.0f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        vals[v] = acc[2 * b][v] * inv_l;
-        vals[4 + v] = acc[2 * b + 1][v] * inv_l;
+        vals[b][v] = acc[2 * b][v] * inv_l;
+        vals[b][4 + v] = acc[2 * b + 1][v] * inv_l;
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(vals[i]));
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-      const float d = amax / 127.0f;
-      const float dq = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
-      const float id = amax == 0.0f ? 0.0f : 1.0f / d;
-      if (!active) continue;
+      for (int i = 0; i < 8; ++i) amax[b] = fmaxf(amax[b], fabsf(vals[b][i]));
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 16, 64));
+#pragma unroll
+    for (int b = 0; b < kB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 32, 64));
+    // Row t of the row tiles: 32-row tile t/32, row t%32; this head's
+    // blocks are 8 head .. 8 head + 7 of the row's 24.
+    int8_t* qrow_out = cq + (size_t)(t >> 5) * (kEmbd / kQK) * 1024 + (size_t)head * kB * 1024 + (t & 31) * 16 + 4 * grp;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const float d = amax[b] / 127.0f;
+      const float id = amax[b] == 0.0f ? 0.0f : 1.0f / d;
       int32_t qv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[i] = amax == 0.0f ? 0 : q8_round(vals[i] * id);
-      const unsigned e = head * kHeadDim + 32 * b + 4 * grp;
-      *reinterpret_cast<uint32_t*>(cq + q8_tile_offset(t, e, kEmbd / kQK)) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
-      *reinterpret_cast<uint32_t*>(cq + q8_tile_offset(t, e + 16, kEmbd / kQK)) =
-          pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
-      if (grp == 0) cd[(size_t)(head * (kHeadDim / kQK) + b) * rows + t] = dq;
+      for (int i = 0; i < 8; ++i) qv[i] = amax[b] == 0.0f ? 0 : q8_round(vals[b][i] * id);
+      if (active) {
+        *reinterpret_cast<uint32_t*>(qrow_out + b * 1024) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
+        *reinterpret_cast<uint32_t*>(qrow_out + b * 1024 + 512) = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
+        if (grp == 0) cd[(size_t)(head * kB + b) * rows + t] = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+      }
     }
   }
   // Drain any DMA still in flight before the workgroup's LDS is released.

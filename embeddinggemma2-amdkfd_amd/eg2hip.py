@@ -315,6 +315,23 @@ def q8_weight_tiles(blocks_u8, rows, k):
     return wq, wd
 
 
+class AttentionPlan:
+    """The attention work list of a packing (eg2_attention_tiles) on the
+    device: 4 uint32 per query tile, then the tile count."""
+
+    def __init__(self, offsets, device):
+        import numpy as np
+        import torch
+
+        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+        tiles = np.zeros(4 * int(offsets[-1]) + 4, dtype=np.uint32)
+        n = lib().eg2_attention_tiles(offs, len(offsets) - 1, tiles.ctypes.data)
+        tiles[-1] = n
+        self.tiles = torch.from_numpy(tiles.view(np.int32)).to(device)
+        self.count_ptr = self.tiles.data_ptr() + 4 * (len(tiles) - 1)
+        self.grid = max(1, (int(offsets[-1]) + 7) // 8)
+
+
 class ops:
     """Operator entry points on torch device tensors (current torch stream)."""
 
@@ -351,19 +368,18 @@ class ops:
     def attention(cls, qs, ks, vt, vcol, offsets, window, cq, cd):
         """Packed attention over sequences [offsets[s], offsets[s+1]); vt and
         vcol as written by qk_norm_rope."""
-        import numpy as np
         import torch
 
-        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
-        tiles = np.zeros(4 * int(offsets[-1]) + 4, dtype=np.uint32)
-        n = lib().eg2_attention_tiles(offs, len(offsets) - 1, tiles.ctypes.data)
-        tiles[-1] = n
-        dev = torch.from_numpy(tiles.view(np.int32)).to(qs.device)
-        grid = max(1, (qs.shape[0] + 7) // 8)
-        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol), cls._p(dev),
-                                      C.c_void_p(dev.data_ptr() + 4 * (len(tiles) - 1)), grid, window, qs.shape[0],
-                                      cls._p(cq), cls._p(cd), cls._stream()), "attention")
-        torch.cuda.current_stream().synchronize()  # keeps `dev` alive until the kernel ran
+        plan = AttentionPlan(offsets, qs.device)
+        cls.attention_planned(qs, ks, vt, vcol, plan, window, cq, cd)
+        torch.cuda.current_stream().synchronize()  # keeps the plan alive until the kernel ran
+
+    @classmethod
+    def attention_planned(cls, qs, ks, vt, vcol, plan, window, cq, cd):
+        """attention() with a prebuilt AttentionPlan (no host work, no sync)."""
+        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol),
+                                      cls._p(plan.tiles), C.c_void_p(plan.count_ptr), plan.grid, window,
+                                      qs.shape[0], cls._p(cq), cls._p(cd), cls._stream()), "attention")
 
     @classmethod
     def gelu_quant(cls, gu, gq, gd):
