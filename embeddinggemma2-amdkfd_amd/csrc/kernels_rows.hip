@@ -4,39 +4,35 @@
 // results are bit-identical to the CPU path for identical inputs (tanhf in
 // the GeGLU kernel is the one libm function evaluated on the device).
 //
-// Work mapping. One 64-lane wave per token row (a 2048-token wave gives two
-// waves per SIMD):
+// Work mapping. One 64-lane wave per 768-wide token row (a 2048-token wave
+// gives two waves per SIMD), so latency, not bandwidth, is what the design
+// fights:
 //  * element-wise work runs one float4 per lane per 256 columns, coalesced,
-//    with the row kept in registers;
+//    with the row kept in registers from load to store;
 //  * the SSE2-order sum of squares (kernels.c:82-94) runs one lane per
 //    chain: lane c owns chain c (the sequential sum of row[8t + c]^2) over
-//    the row staged in LDS, with every read issued before the dependent
-//    additions; every 8-lane group computes the same chains, so every lane
-//    ends with the total;
-//  * Q8_0 quantization splits each 32-value block over P adjacent lanes,
-//    which combine the block maximum with log2(P) shuffles.
-// Rows are staged in LDS with every 32-value block padded to 36 floats so
-// that the per-chain and per-block reads spread over the banks.
+//    the row staged transposed in LDS (24 16-byte reads per lane, all issued
+//    before the dependent additions); every 8-lane group computes the same
+//    chains and combines them with DPP moves, so every lane ends with the
+//    total without an LDS round trip;
+//  * Q8_0 quantization works on the registers: a 32-value block is 8 lanes
+//    x 4 values, its maximum combined by DPP, and each lane stores its 4
+//    int8 values as one 32-bit word of the row tiles.
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
 namespace eg2 {
 
-constexpr int kBlkStride = kQK + 4;                    // padded 32-value block in LDS
-constexpr int kRowFloats = kEmbd / kQK * kBlkStride;   // 864 floats per padded row
 constexpr int kBlocks = kEmbd / kQK;                   // 24 blocks per row
 constexpr int kVec = kEmbd / 256;                      // float4 per lane per row
 
-// LDS index of element e of a padded row.
-__device__ __forceinline__ int pad(int e) { return e + (e / kQK) * (kBlkStride - kQK); }
-
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):
 // the sequential sum over t of x[8t + c]^2, squares rounded then added.
-template <int N, bool PADDED>
+template <int N>
 __device__ __forceinline__ float sse2_chain(const float* row, int c) {
   float v[N / 8];
 #pragma unroll
-  for (int t = 0; t < N / 8; ++t) v[t] = row[PADDED ? pad(8 * t + c) : 8 * t + c];
+  for (int t = 0; t < N / 8; ++t) v[t] = row[8 * t + c];
   float s = 0.0f;
 #pragma unroll
   for (int t = 0; t < N / 8; ++t) {
@@ -59,9 +55,118 @@ __device__ __forceinline__ float sse2_combine(float s) {
   return (v0 + v2) + (v1 + v3);
 }
 
-// SSE2 sum of squares of a padded 768-float LDS row, on every lane.
-__device__ __forceinline__ float row_sum_squares(const float* row) {
-  return sse2_combine(sse2_chain<kEmbd, true>(row, threadIdx.x & 7));
+// ---------------------------------------------------------------- 768-wide rows
+// A 768-float token row is held one float4 per lane per 256 columns (lane L
+// has elements 4L..4L+3 + 256r, r = 0..2). Its SSE2 sum of squares
+// (kernels.c:82-94) needs chain c = the sequential sum over t of
+// row[8t + c]^2: the row is staged transposed in LDS, tr[c][t] = row[8t + c],
+// so lane c reads its 96 values with 24 ds_read_b128. The 104-float pitch
+// puts the eight chain rows 40 banks apart (conflict-free reads) and the
+// two lanes of a pair 32 banks apart (conflict-free transposed writes).
+constexpr int kChain = kEmbd / 8;  // 96
+constexpr int kTPitch = kChain + 8;
+typedef float TRow[kTPitch];
+
+__device__ __forceinline__ void stage_transposed(TRow* tr, const float4 (&v)[kVec]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const float c4[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = 4 * (lane + 64 * r) + k;
+      tr[e & 7][e >> 3] = c4[k];
+    }
+  }
+}
+
+// Chain c of the SSE2 sum of squares from the transposed row, every read
+// issued before the dependent additions.
+__device__ __forceinline__ float transposed_chain(const TRow* tr, int c) {
+  float4 v[kChain / 4];
+#pragma unroll
+  for (int j = 0; j < kChain / 4; ++j) v[j] = *reinterpret_cast<const float4*>(&tr[c][4 * j]);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kChain / 4; ++j) {
+    const float p0 = v[j].x * v[j].x, p1 = v[j].y * v[j].y, p2 = v[j].z * v[j].z, p3 = v[j].w * v[j].w;
+    s = s + p0;
+    s = s + p1;
+    s = s + p2;
+    s = s + p3;
+  }
+  return s;
+}
+
+// DPP moves within 16-lane rows: quad permutation, shift left/right by n
+// lanes. `dpp` writes every lane (lanes shifted in from outside the row
+// read 0 and are not used); `dpp_into` writes only the lanes of the 4-lane
+// banks in BANKS and keeps `old` elsewhere. Choosing lanes by bank mask,
+// not by a select on the lane index, keeps every source lane active: the
+// compiler may turn a select of two DPP results into an EXEC-masked branch,
+// and a DPP move reads 0 from lanes that EXEC disables.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL, int BANKS>
+__device__ __forceinline__ float dpp_into(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, src), CTRL, 0xf, BANKS,
+                                                               false));
+}
+constexpr int kQuad1032 = 0xB1, kQuad2301 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
+constexpr int kQuad0000 = 0x00, kQuad1111 = 0x55, kQuad2222 = 0xAA, kQuad3333 = 0xFF;
+constexpr int kRowShl4 = 0x104, kRowShr4 = 0x114;  // lane i reads lane i + 4 / i - 4
+constexpr int kBanks02 = 0x5, kBanks13 = 0xA;      // lanes 0-3 and 8-11 / 4-7 and 12-15 of a row
+
+// The value of lane i ^ 4: the other 4-lane half of each aligned 8-lane group.
+__device__ __forceinline__ float other_quad(float x) {
+  return dpp_into<kRowShr4, kBanks13>(dpp_into<kRowShl4, kBanks02>(x, x), x);
+}
+
+// sse2_combine with DPP instead of LDS shuffles: lanes 8g..8g+7 hold chains
+// 0..7 (chains 0-3 are the first 4-wide accumulator, 4-7 the second);
+// v[j] = acc0[j] + acc1[j], total (v0 + v2) + (v1 + v3) (kernels.c:35-39),
+// returned to every lane of the group.
+__device__ __forceinline__ float sse2_combine_dpp(float s) {
+  const float v = s + dpp<kRowShl4>(s);  // lanes 0-3 of the group: v[0..3]
+  const float total = (dpp<kQuad0000>(v) + dpp<kQuad2222>(v)) + (dpp<kQuad1111>(v) + dpp<kQuad3333>(v));
+  return dpp_into<kRowShr4, kBanks13>(total, total);  // lanes 4-7 take lanes 0-3's
+}
+
+// Maximum over each aligned group of 8 lanes, on every lane of the group.
+__device__ __forceinline__ float group8_max(float m) {
+  m = fmaxf(m, dpp<kQuad1032>(m));
+  m = fmaxf(m, dpp<kQuad2301>(m));
+  return fmaxf(m, other_quad(m));
+}
+
+// quants.c:97-177 (scalar path) on the row held as float4 per lane: block b
+// (32 values) is lanes 8(b % 8)..+7 of register r = b / 8, four values per
+// lane; the block maximum is combined over those 8 lanes. Each lane stores
+// its 4 int8 values (contiguous in the row-tile layout) for row t of q;
+// lane 8i of the group stores the float value of the fp16 scale at
+// d[b * ld]. v[r] must already hold the values to quantize.
+__device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int t, int8_t* __restrict__ q,
+                                                   float* __restrict__ d, int ld) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const float amax = group8_max(fmaxf(fmaxf(fabsf(v[r].x), fabsf(v[r].y)), fmaxf(fabsf(v[r].z), fabsf(v[r].w))));
+    const float dd = amax / 127.0f;
+    const float id = amax != 0.0f ? 1.0f / dd : 0.0f;
+    const int e = 4 * (lane + 64 * r), b = e / kQK;
+    int32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    if (amax != 0.0f) {
+      q0 = q8_round(v[r].x * id);
+      q1 = q8_round(v[r].y * id);
+      q2 = q8_round(v[r].z * id);
+      q3 = q8_round(v[r].w * id);
+    }
+    *reinterpret_cast<uint32_t*>(q + q8_tile_offset(t, e, kBlocks)) = pack_i8x4(q0, q1, q2, q3);
+    if ((lane & 7) == 0) d[(size_t)b * ld] = fp16_bits_to_fp32(fp32_to_fp16_bits(dd));
+  }
 }
 
 // quants.c:97-177 (scalar path) on one block spread over P adjacent lanes
@@ -97,29 +202,6 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
     *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
 }
 
-// (x*w)*inv on a padded LDS row (kernels.c:124-133, SSE2 branch), quantized
-// to Q8_0 (kernels.c:139-151): lane pairs take the 24 blocks (lanes 48-63
-// repeat the last block and store nothing), each lane one 16-value half.
-// Values go to row t of the row-tile buffer q; block scales are stored
-// transposed, block b of this row at d[b * ld].
-__device__ __forceinline__ void norm_quantize_row(const float* row, const float* __restrict__ w, float inv, int t,
-                                                  int8_t* __restrict__ q, float* __restrict__ d, int ld) {
-  const int lane = threadIdx.x;
-  const int b = min(lane >> 1, kBlocks - 1), part = lane & 1, e0 = b * kQK + part * (kQK / 2);
-  float v[kQK / 2];
-#pragma unroll
-  for (int i = 0; i < kQK / 8; ++i) {
-    const float4 xv = *reinterpret_cast<const float4*>(row + pad(e0) + 4 * i);
-    const float4 wv = *reinterpret_cast<const float4*>(w + e0 + 4 * i);
-    const float p0 = xv.x * wv.x, p1 = xv.y * wv.y, p2 = xv.z * wv.z, p3 = xv.w * wv.w;
-    v[4 * i + 0] = p0 * inv;
-    v[4 * i + 1] = p1 * inv;
-    v[4 * i + 2] = p2 * inv;
-    v[4 * i + 3] = p3 * inv;
-  }
-  quantize_block_part<2>(v, lane < 2 * kBlocks, q + q8_tile_offset(t, e0, kBlocks), d + (size_t)b * ld);
-}
-
 // engine.c:288-295 + kernels.c:139-151 (the first projection's input):
 // x = (fp16(d) * sqrt(768)) * q from the raw GGUF Q8_0 row of token_embd,
 // then the layer-0 attn_norm RMSNorm quantized to Q8_0.
@@ -129,30 +211,39 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
                         int8_t* __restrict__ xq, float* __restrict__ xd) {
   constexpr int kRaw = kBlocks * 34;  // 816 bytes = 51 x 16
   __shared__ __align__(16) uint8_t raw[kRaw];
-  __shared__ __align__(16) float row[kRowFloats];
+  __shared__ __align__(16) float tr[8][kTPitch];
   const int t = blockIdx.x, lane = threadIdx.x;
+  float4 wv[kVec];
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) wv[r] = *reinterpret_cast<const float4*>(norm_w + 4 * (lane + 64 * r));
   // GGUF rows of this tensor are 16-byte aligned: 816 = 16 * 51 and tensor
   // data is 32-byte aligned.
   if (lane < kRaw / 16)
     reinterpret_cast<uint4*>(raw)[lane] = reinterpret_cast<const uint4*>(table + (size_t)ids[t] * kRaw)[lane];
   __syncthreads();
+  float4 v[kVec];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     const uint8_t* blk = raw + (e / kQK) * 34;
     const float dd = fp16_bits_to_fp32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8)) * embed_scale;  // quants.c:67
     const uint8_t* qs = blk + 2 + e % kQK;
-    float4 v;
-    v.x = dd * (float)(int8_t)qs[0];  // quants.c:87
-    v.y = dd * (float)(int8_t)qs[1];
-    v.z = dd * (float)(int8_t)qs[2];
-    v.w = dd * (float)(int8_t)qs[3];
-    *reinterpret_cast<float4*>(&row[pad(e)]) = v;
-    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v;
+    v[r].x = dd * (float)(int8_t)qs[0];  // quants.c:87
+    v[r].y = dd * (float)(int8_t)qs[1];
+    v[r].z = dd * (float)(int8_t)qs[2];
+    v[r].w = dd * (float)(int8_t)qs[3];
+    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v[r];
   }
+  stage_transposed(tr, v);
   __syncthreads();
-  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, norm_w, inv, t, xq, xd + t, (int)gridDim.x);
+  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr, lane & 7)), kEmbd, eps);
+  // (x*w)*inv (kernels.c:124-133, SSE2 branch), then Q8_0 (kernels.c:139-151).
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const float p0 = v[r].x * wv[r].x, p1 = v[r].y * wv[r].y, p2 = v[r].z * wv[r].z, p3 = v[r].w * wv[r].w;
+    v[r] = make_float4(p0 * inv, p1 * inv, p2 * inv, p3 * inv);
+  }
+  quantize_row_lanes(v, t, xq, xd + t, (int)gridDim.x);
 }
 
 // kernels.c:163-188 (SSE2 build: scalar branch, residual += (h*inv)*w), then
@@ -162,34 +253,39 @@ __global__ void __launch_bounds__(64)
 residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, const float* __restrict__ post_w,
                            const float* __restrict__ next_w, float eps, int8_t* __restrict__ xq,
                            float* __restrict__ xd) {
-  __shared__ __align__(16) float row[kRowFloats];
+  __shared__ __align__(16) float tr[2][8][kTPitch];
   const int t = blockIdx.x, lane = threadIdx.x;
-  float4 hv[kVec], xv[kVec], wv[kVec];
+  float4 hv[kVec], xv[kVec], wv[kVec], nv[kVec];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     hv[r] = *reinterpret_cast<const float4*>(h + (size_t)t * kEmbd + e);
     xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + e);
     wv[r] = *reinterpret_cast<const float4*>(post_w + e);
+    if (next_w) nv[r] = *reinterpret_cast<const float4*>(next_w + e);
   }
-#pragma unroll
-  for (int r = 0; r < kVec; ++r) *reinterpret_cast<float4*>(&row[pad(4 * (lane + 64 * r))]) = hv[r];
+  stage_transposed(tr[0], hv);
   __syncthreads();
-  const float inv_h = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  __syncthreads();
+  const float inv_h = rms_inverse(sse2_combine_dpp(transposed_chain(tr[0], lane & 7)), kEmbd, eps);
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     const float a0 = hv[r].x * inv_h, a1 = hv[r].y * inv_h, a2 = hv[r].z * inv_h, a3 = hv[r].w * inv_h;
     const float b0 = a0 * wv[r].x, b1 = a1 * wv[r].y, b2 = a2 * wv[r].z, b3 = a3 * wv[r].w;
-    const float4 v = make_float4(xv[r].x + b0, xv[r].y + b1, xv[r].z + b2, xv[r].w + b3);
-    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v;
-    *reinterpret_cast<float4*>(&row[pad(e)]) = v;
+    xv[r] = make_float4(xv[r].x + b0, xv[r].y + b1, xv[r].z + b2, xv[r].w + b3);
+    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = xv[r];
   }
   if (!next_w) return;
+  stage_transposed(tr[1], xv);
   __syncthreads();
-  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
-  norm_quantize_row(row, next_w, inv, t, xq, xd + t, (int)gridDim.x);
+  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr[1], lane & 7)), kEmbd, eps);
+  // (x*w)*inv (kernels.c:124-133, SSE2 branch), then Q8_0 (kernels.c:139-151).
+#pragma unroll
+  for (int r = 0; r < kVec; ++r) {
+    const float p0 = xv[r].x * nv[r].x, p1 = xv[r].y * nv[r].y, p2 = xv[r].z * nv[r].z, p3 = xv[r].w * nv[r].w;
+    xv[r] = make_float4(p0 * inv, p1 * inv, p2 * inv, p3 * inv);
+  }
+  quantize_row_lanes(xv, t, xq, xd + t, (int)gridDim.x);
 }
 
 // Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
@@ -242,7 +338,7 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
   __syncthreads();
   // lanes 8r..8r+7 run the chains of head row r (r < 4); the rest repeat row 0
   const int hr = (lane >> 3) < kRows ? (lane >> 3) : 0;
-  const float ss = sse2_combine(sse2_chain<kHeadDim, false>(rows[hr], lane & 7));
+  const float ss = sse2_combine(sse2_chain<kHeadDim>(rows[hr], lane & 7));
   float inv[kRows];
 #pragma unroll
   for (int r = 0; r < kRows; ++r) inv[r] = rms_inverse(__shfl(ss, 8 * r, 64), kHeadDim, eps);
@@ -329,16 +425,14 @@ quantize_rows_kernel(const float* __restrict__ x, int k, int8_t* __restrict__ q,
 // kernels.c:153-161 in place on a token row: x = (x*w)*inv.
 __global__ void __launch_bounds__(64)
 rms_norm_rows_kernel(float* __restrict__ x, const float* __restrict__ w, float eps) {
-  __shared__ __align__(16) float row[kRowFloats];
+  __shared__ __align__(16) float tr[8][kTPitch];
   const int t = blockIdx.x, lane = threadIdx.x;
   float4 xv[kVec];
 #pragma unroll
-  for (int r = 0; r < kVec; ++r) {
-    xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + 4 * (lane + 64 * r));
-    *reinterpret_cast<float4*>(&row[pad(4 * (lane + 64 * r))]) = xv[r];
-  }
+  for (int r = 0; r < kVec; ++r) xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + 4 * (lane + 64 * r));
+  stage_transposed(tr, xv);
   __syncthreads();
-  const float inv = rms_inverse(row_sum_squares(row), kEmbd, eps);
+  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr, lane & 7)), kEmbd, eps);
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
@@ -372,7 +466,7 @@ pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets
   acc[e] = sum * scale;
   __syncthreads();
   if (e < 64) {
-    const float ss = sse2_combine(sse2_chain<kEmbd, false>(acc, e & 7));
+    const float ss = sse2_combine(sse2_chain<kEmbd>(acc, e & 7));
     if (e == 0) total = ss;
   }
   __syncthreads();
