@@ -207,6 +207,44 @@ def kernel_only(kind, steps):
 COPY_MIB = 256
 
 
+def config5_stream(vocab, seed=42, n_requests=1000):
+    """The sustained dynamic-batching stream: n_requests requests of U{1..16}
+    texts, token lengths floor(exp(U(ln 4, ln 2048))), ids uniform in the
+    vocabulary, output dimensions cycling 128, 256, 512, 768 per request."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    texts = rng.integers(1, 17, n_requests)
+    n = int(texts.sum())
+    lens = np.clip(np.floor(np.exp(rng.uniform(np.log(4), np.log(2048), n))).astype(np.int64), 4, 2048)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    ids = rng.integers(0, vocab, int(offsets[-1])).astype(np.int32)
+    dims = np.array([128, 256, 512, 768])[np.repeat(np.arange(n_requests), texts) % 4]
+    return ids, offsets, dims
+
+
+def run_stream(eg2, enc, n_requests):
+    """Embeds the config-5 stream twice through eg2_stream_embed (the first
+    pass instantiates one hipGraph per padded wave size) and times the
+    second, end to end: host packing, per-wave uploads, the forwards, the
+    downloads and the Matryoshka prefix normalisation."""
+    ids, offsets, dims = config5_stream(eg2.VOCAB, n_requests=n_requests)
+    out, waves = enc.stream(ids, offsets, dims)
+    t0 = time.perf_counter()
+    out2, waves = enc.stream(ids, offsets, dims)
+    dt = time.perf_counter() - t0
+    import numpy as np
+
+    assert np.array_equal(out, out2)
+    tokens = int(offsets[-1])
+    return {"workload": f"dynamic-batching stream: {n_requests} requests x U{{1..16}} texts, lengths log-uniform "
+                        "[4, 2048], waves <= 2048 tokens / 32 sequences (lookahead, longest first), dims cycling "
+                        "128/256/512/768, seed 42; end to end incl. host packing and PCIe transfers",
+            "requests": n_requests, "texts": int(len(dims)), "tokens": tokens, "waves": int(waves),
+            "seconds": round(dt, 3), "tokens_per_s": round(tokens / dt, 1),
+            "mean_wave_tokens": round(tokens / waves, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +252,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stream-requests", type=int, default=1000,
+                    help="requests in the dynamic-batching stream measurement (0 skips it)")
     ap.add_argument("--kernel-only", choices=["gate_up", "copy", "table"],
                     help="run only the dominant GEMM (or the copy calibration kernel) for counter runs, "
                          "or only the per-kernel table")
@@ -268,6 +308,11 @@ def main():
         for _ in range(n_host):
             enc.batch(ids, offsets)
         host_rate = TOKENS * n_host / (time.perf_counter() - t0)
+        stream = None
+        if args.stream_requests > 0:
+            stream = run_stream(eg2, enc, args.stream_requests)
+            log(f"stream: {stream['tokens']:,} tokens in {stream['waves']} waves, {stream['seconds']:.2f} s, "
+                f"{stream['tokens_per_s']:,.0f} tokens/s")
         enc.close()
 
         gemm_ms = time_gemm(eg2, torch, max(20, args.steps), 5)
@@ -315,6 +360,7 @@ def main():
         "kernels": kernels,
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),
+        "stream": stream,
     }
     print(json.dumps(line), flush=True)
 

@@ -28,13 +28,26 @@ hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
-                            const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
-                            int8_t* cq, float* cd, hipStream_t st);
+                            const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
+                            int8_t* cq, float* cd, float* partials, hipStream_t st);
+hipError_t launch_attention_merge(const uint32_t* merges, const uint32_t* merge_count, int grid, const float* partials,
+                                  int rows, int8_t* cq, float* cd, hipStream_t st);
 
-// Query tiles for launch_attention: up to 16 tokens of one sequence each,
-// {first query, end, sequence start, sequence end}, for the sequences
-// [offsets[s], offsets[s+1]). Returns the tile count (<= offsets[batch]).
-unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles);
+// Work lists of launch_attention / launch_attention_merge for the
+// sequences [offsets[s], offsets[s+1]): per query tile of up to 16 tokens
+// of one sequence, one item (8 uint32: first query, end, sequence start,
+// sequence end, key chunk start, key chunk end, partial slot or
+// 0xFFFFFFFF, 0) per key chunk -- a sequence longer than 256 tokens splits
+// its keys into 256-key chunks whose partial results go to consecutive
+// slots -- and, for split tiles, one merge record (first query, end, first
+// slot, parts). attention_capacity bounds the counts for a wave of
+// `tokens` tokens in at most `batch` sequences.
+struct AttentionCounts {
+  unsigned items, merges, slots;
+};
+AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges);
+AttentionCounts attention_capacity(size_t tokens, size_t batch);
+constexpr size_t kAttentionPartialFloats = 3 * (16 * 64 * 4 + 64 * 2);  // per slot
 
 // V^T column of every token: each sequence starts at a multiple of 32,
 // consecutive tokens take consecutive columns. Returns the column count

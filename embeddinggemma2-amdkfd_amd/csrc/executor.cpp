@@ -18,6 +18,7 @@
 // poisons the context (src/gemma2_kfd.cpp:190-191, 214-215, 270).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -110,13 +111,18 @@ class Backend {
   int8_t *xq_, *cq_, *mid_q_;
   _Float16 *qs_, *ks_, *vt_;
   int32_t *ids_d_, *pos_d_, *vcol_d_;
-  uint32_t *tiles_d_, *off_d_;  // tiles_d_: attention query tiles, then their count
+  // Attention work lists (items, merges) and their counts {items, merges};
+  // partial results of split sequences.
+  uint32_t *items_d_, *merges_d_, *counts_d_, *off_d_;
+  float* partials_;
   // Pinned staging.
   int32_t *ids_h_, *pos_h_, *vcol_h_;
-  uint32_t *tiles_h_, *off_h_;
+  uint32_t *items_h_, *merges_h_, *counts_h_, *off_h_;
+  eg2::AttentionCounts attn_cap_{};
+  bool staged_merge_ = false;
   float* out_h_;
 
-  std::map<unsigned, hipGraphExec_t> graphs_;
+  std::map<unsigned, hipGraphExec_t> graphs_;  // key: 2 * padded rows + (wave has split sequences)
   unsigned staged_tokens_ = 0, staged_rows_ = 0;
   size_t staged_batch_ = 0;
   std::map<std::string, double> timings_;
@@ -143,7 +149,7 @@ class Backend {
   std::vector<uint8_t> q8_rows(const std::string& name, int k, int m) const;
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
   void launch(const char* name, hipError_t e);
-  void record_layers(unsigned rows);
+  void record_layers(unsigned rows, bool merge);
   void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
             hipStream_t s);
   void wait(const char* what);
@@ -335,7 +341,12 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   ids_d_ = dalloc<int32_t>(kCap);
   pos_d_ = dalloc<int32_t>(kCap);
   vcol_d_ = dalloc<int32_t>(kCap);
-  tiles_d_ = dalloc<uint32_t>(4 * kCap + 4);
+  // Capacity for the wave cap plus the padding sequence (rows rounded to 32).
+  attn_cap_ = eg2::attention_capacity(kCap + 32, kCap + 1);
+  items_d_ = dalloc<uint32_t>(8 * (size_t)attn_cap_.items);
+  merges_d_ = dalloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
+  counts_d_ = dalloc<uint32_t>(2);
+  partials_ = dalloc<float>(eg2::kAttentionPartialFloats * std::max(1u, attn_cap_.slots));
   off_d_ = dalloc<uint32_t>(kCap + 1);
   pooled_ = dalloc<float>((size_t)kCap * kEmbd);
   mid_ = dalloc<float>((size_t)kCap * kDenseFF);
@@ -344,7 +355,9 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   ids_h_ = halloc<int32_t>(kCap);
   pos_h_ = halloc<int32_t>(kCap);
   vcol_h_ = halloc<int32_t>(kCap);
-  tiles_h_ = halloc<uint32_t>(4 * kCap + 4);
+  items_h_ = halloc<uint32_t>(8 * (size_t)attn_cap_.items);
+  merges_h_ = halloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
+  counts_h_ = halloc<uint32_t>(2);
   off_h_ = halloc<uint32_t>(kCap + 1);
   out_h_ = halloc<float>((size_t)kCap * kEmbd);
   check(hipDeviceSynchronize(), "upload");
@@ -378,10 +391,11 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
 // then per layer (engine.c:1115-1127 order) QKV GEMM, QK-norm/RoPE,
-// attention (+Q8_0), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM,
-// GeGLU (+Q8_0), down GEMM, residual + next attn_norm (+Q8_0); finally the
+// attention (+Q8_0; with `merge`, the merge of split sequences' key-chunk
+// partials), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM, GeGLU
+// (+Q8_0), down GEMM, residual + next attn_norm (+Q8_0); finally the
 // output_norm per token (the first half of kernels.c:417-427).
-void Backend::record_layers(unsigned rows) {
+void Backend::record_layers(unsigned rows, bool merge) {
   hipStream_t s = stream_;
   const int n = (int)rows;
   launch("embed", eg2::launch_embed_norm_quant(token_embd_, ids_d_, n, std::sqrt((float)kEmbd), layers_[0].attn_norm,
@@ -391,9 +405,11 @@ void Backend::record_layers(unsigned rows) {
     gemm("gemm_qkv", xq_, xd_, L.qkv, qkv_, n, kQKV, s);
     launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, vcol_d_, eps_, qs_, ks_,
                                                     vt_, kVtCols, n, s));
-    launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, tiles_d_, tiles_d_ + 4 * kCap,
-                                              (n + 7) / 8, L.window,
-                                              n, cq_, cd_, s));
+    launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, items_d_, counts_d_, (n + 7) / 8,
+                                              L.window, n, cq_, cd_, partials_, s));
+    if (merge)
+      launch("attention_merge",
+             eg2::launch_attention_merge(merges_d_, counts_d_ + 1, (n + 3) / 4, partials_, n, cq_, cd_, s));
     gemm("gemm_o", cq_, cd_, L.o, h_, n, kEmbd, s);
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
     gemm("gemm_gate_up", xq_, xd_, L.gu, gu_, n, 2 * kFF, s);
@@ -455,12 +471,15 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
     pos_h_[t] = (int32_t)(t - n);
   }
   for (size_t s = 0; s <= batch; ++s) off_h_[s] = (uint32_t)offsets[s];
-  unsigned n_tiles = eg2::build_attention_tiles(offsets, batch, tiles_h_);
-  if (rows > n) {
-    const size_t pad[2] = {n, rows};
-    n_tiles += eg2::build_attention_tiles(pad, 1, tiles_h_ + 4 * n_tiles);
-  }
-  tiles_h_[4 * kCap] = n_tiles;
+  // Attention work lists; the padding rows form one more sequence.
+  std::vector<size_t> all(offsets, offsets + batch + 1);
+  if (rows > n) all.push_back(rows);
+  const eg2::AttentionCounts ac = eg2::build_attention_items(all.data(), all.size() - 1, items_h_, merges_h_);
+  if (ac.items > attn_cap_.items || ac.merges > attn_cap_.merges || ac.slots > attn_cap_.slots)
+    throw std::runtime_error("attention work list exceeds its capacity");
+  counts_h_[0] = ac.items;
+  counts_h_[1] = ac.merges;
+  const bool merge = ac.merges > 0;
   // Transposed-v columns: the padding rows form one more sequence.
   const size_t cols = eg2::build_vt_columns(offsets, batch, vcol_h_);
   for (unsigned t = n; t < rows; ++t) vcol_h_[t] = (int32_t)(cols + (t - n));
@@ -470,15 +489,19 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
   check(hipMemcpyAsync(ids_d_, ids_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
   check(hipMemcpyAsync(pos_d_, pos_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
   check(hipMemcpyAsync(vcol_d_, vcol_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy columns");
-  check(hipMemcpyAsync(tiles_d_, tiles_h_, 4 * n_tiles * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy tiles");
-  check(hipMemcpyAsync(tiles_d_ + 4 * kCap, tiles_h_ + 4 * kCap, sizeof(uint32_t), hipMemcpyHostToDevice, s),
-        "copy tiles");
+  check(hipMemcpyAsync(items_d_, items_h_, 8 * (size_t)ac.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+        "copy attention items");
+  if (merge)
+    check(hipMemcpyAsync(merges_d_, merges_h_, 4 * (size_t)ac.merges * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy attention merges");
+  check(hipMemcpyAsync(counts_d_, counts_h_, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy attention counts");
   check(hipMemcpyAsync(off_d_, off_h_, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy offsets");
-  if (use_graph_ && !profile_ && graphs_.find(rows) == graphs_.end()) {
+  const unsigned key = 2 * rows + (merge ? 1 : 0);
+  if (use_graph_ && !profile_ && graphs_.find(key) == graphs_.end()) {
     hipGraph_t graph = nullptr;
     check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     try {
-      record_layers(rows);
+      record_layers(rows, merge);
     } catch (...) {
       (void)hipStreamEndCapture(s, &graph);
       if (graph) (void)hipGraphDestroy(graph);
@@ -489,8 +512,9 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
     const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     check(e, "hipGraphInstantiate");
-    graphs_.emplace(rows, exec);
+    graphs_.emplace(key, exec);
   }
+  staged_merge_ = merge;
   staged_tokens_ = n;
   staged_rows_ = rows;
   staged_batch_ = batch;
@@ -505,7 +529,7 @@ void Backend::launch_staged(unsigned repeats) {
   poisoned_ = true;
   for (unsigned r = 0; r < repeats; ++r) {
     if (use_graph_ && !profile_) {
-      check(hipGraphLaunch(graphs_.at(staged_rows_), s), "hipGraphLaunch");
+      check(hipGraphLaunch(graphs_.at(2 * staged_rows_ + (staged_merge_ ? 1 : 0)), s), "hipGraphLaunch");
     } else if (profile_) {
       // Per-stage timing needs events around eager launches; the totals are
       // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
@@ -513,7 +537,7 @@ void Backend::launch_staged(unsigned repeats) {
       check(hipEventCreate(&a), "hipEventCreate");
       check(hipEventCreate(&b), "hipEventCreate");
       check(hipEventRecord(a, s), "hipEventRecord");
-      record_layers(staged_rows_);
+      record_layers(staged_rows_, staged_merge_);
       check(hipEventRecord(b, s), "hipEventRecord");
       check(hipEventSynchronize(b), "hipEventSynchronize");
       float ms = 0;
@@ -522,7 +546,7 @@ void Backend::launch_staged(unsigned repeats) {
       (void)hipEventDestroy(a);
       (void)hipEventDestroy(b);
     } else {
-      record_layers(staged_rows_);
+      record_layers(staged_rows_, staged_merge_);
     }
     launch("pool", eg2::launch_pool_l2(x_, off_d_, pooled_, B, s));
     if (dense_) {

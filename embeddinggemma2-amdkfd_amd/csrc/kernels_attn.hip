@@ -37,6 +37,8 @@
 // chosen so that lane group j (lanes 16j..16j+15) ends up holding the
 // probabilities of keys 8j..8j+7: exactly the k-slots it supplies to the
 // P.V MFMA, whose V^T operand is then one aligned 16-byte chunk per lane.
+#include <algorithm>
+
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
@@ -51,6 +53,10 @@ constexpr int kKStage = kKvTile * 2 * kHeadDim * 2;  // [key][hi|lo][256] fp16 =
 constexpr int kVStage = 2 * kHeadDim * kKvTile * 2;  // [hi|lo][dim][32 keys] fp16 = 32 KB
 constexpr int kStage = kKStage + kVStage;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;           // item writes the final context
+constexpr int kPartFloats = 16 * 64 * 4 + 64 * 2;   // per (slot, head): acc in lane order, then (m, l)
+constexpr uint32_t kSplitLen = 256;                // longer sequences split their keys ...
+constexpr uint32_t kChunkKeys = 256;               // ... into chunks of this many keys
 
 __device__ __forceinline__ floatx4 mfma(const half8& a, const half8& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -71,24 +77,76 @@ __device__ __forceinline__ int score_key(int kb, int i) { return 8 * (i >> 2) + 
 __device__ __forceinline__ int kswz(int key) { return (key & 3) | ((key >> 3) << 2); }
 __device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
 
+// Final context of NB Q8_0 blocks of one wave (16 queries x one head):
+// context = acc / l, then Q8_0 per 32 dims (quants.c:97-177). f[2j] and
+// f[2j+1] are the 16-dim MFMA blocks 2(b0+j) and 2(b0+j)+1: lane group grp
+// holds dims 32b + 4grp + v and 32b + 16 + 4grp + v of query t, so a Q8_0
+// block spans the four lane groups. The int8 values go to the row-tile
+// layout of the projection GEMM (4 bytes per lane and half-block), the
+// scales transposed ([block][row]). The blocks run phase by phase so their
+// latencies overlap.
+template <int NB>
+__device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l_run, uint32_t t, bool active,
+                                             int head, int grp, int rows, int b0, int8_t* __restrict__ cq,
+                                             float* __restrict__ cd) {
+  const float inv_l = 1.0f / l_run;
+  float vals[NB][8], amax[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    amax[b] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      vals[b][v] = f[2 * b][v] * inv_l;
+      vals[b][4 + v] = f[2 * b + 1][v] * inv_l;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax[b] = fmaxf(amax[b], fabsf(vals[b][i]));
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 16, 64));
+#pragma unroll
+  for (int b = 0; b < NB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 32, 64));
+  // Row t of the row tiles: 32-row tile t/32, row t%32; this head's
+  // blocks are 8 head .. 8 head + 7 of the row's 24.
+  int8_t* qrow_out = cq + (size_t)(t >> 5) * (kEmbd / kQK) * 1024 + (size_t)(head * 8 + b0) * 1024 + (t & 31) * 16 +
+                     4 * grp;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float d = amax[b] / 127.0f;
+    const float id = amax[b] == 0.0f ? 0.0f : 1.0f / d;
+    int32_t qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[i] = amax[b] == 0.0f ? 0 : q8_round(vals[b][i] * id);
+    if (active) {
+      *reinterpret_cast<uint32_t*>(qrow_out + b * 1024) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
+      *reinterpret_cast<uint32_t*>(qrow_out + b * 1024 + 512) = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
+      if (grp == 0) cd[(size_t)(head * 8 + b0 + b) * rows + t] = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+    }
+  }
+}
+
 __global__ void __launch_bounds__(192)
 attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks, const _Float16* __restrict__ vt,
-                 int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ tiles,
-                 const uint32_t* __restrict__ tile_count, int window, int rows, int8_t* __restrict__ cq,
-                 float* __restrict__ cd) {
+                 int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ items,
+                 const uint32_t* __restrict__ item_count, int window, int rows, int8_t* __restrict__ cq,
+                 float* __restrict__ cd, float* __restrict__ partials) {
   __shared__ __align__(16) unsigned char lds[2 * kStage];
 
   const int tid = threadIdx.x, lane = tid & 63, head = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qi = lane & 15, grp = lane >> 4;
-  const uint32_t count = *tile_count;
-  for (uint32_t tile = blockIdx.x; tile < count; tile += gridDim.x) {
-    // Tile fields are clamped to the wave so a malformed list can never
+  const uint32_t count = *item_count;
+  for (uint32_t item = blockIdx.x; item < count; item += gridDim.x) {
+    // Item fields are clamped to the wave so a malformed list can never
     // address outside the rows (an empty key range yields a non-finite row).
-    const uint4 tl = tiles[tile];
+    const uint4 tl = items[2 * item], kc = items[2 * item + 1];
     const uint32_t seg_hi = min(tl.w, (uint32_t)rows);
     const uint32_t seg_lo = min(tl.z, seg_hi);
     const uint32_t q_end = min(tl.y, (uint32_t)rows);
     const uint32_t q0 = tl.x;
+    // Key chunk of this item ([seg_lo, seg_hi) when unsplit; chunk starts
+    // sit a multiple of 32 keys after seg_lo) and its partial-result slot.
+    const uint32_t c_hi = min(kc.y, seg_hi), c_lo = min(max(kc.x, seg_lo), c_hi);
+    const uint32_t slot = kc.z;
     const bool active = q0 + qi < q_end;
     const uint32_t t = active ? q0 + qi : (q_end > 0 ? q_end - 1 : 0);
 
@@ -115,39 +173,43 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
         in_hi = min(in_hi, (uint32_t)__shfl_xor((int)in_hi, mk, 64));
       }
     }
-    kv_lo = __builtin_amdgcn_readfirstlane(kv_lo);
-    kv_hi = __builtin_amdgcn_readfirstlane(kv_hi);
-    in_lo = __builtin_amdgcn_readfirstlane(in_lo);
-    in_hi = __builtin_amdgcn_readfirstlane(in_hi);
+    kv_lo = __builtin_amdgcn_readfirstlane(max(kv_lo, c_lo));
+    kv_hi = __builtin_amdgcn_readfirstlane(min(kv_hi, c_hi));
+    in_lo = __builtin_amdgcn_readfirstlane(max(in_lo, c_lo));
+    in_hi = __builtin_amdgcn_readfirstlane(min(in_hi, c_hi));
+    lo = max(lo, c_lo);
+    hi = min(hi, c_hi);
     // Key tiles are aligned to the sequence start; so are the V^T columns.
     const uint32_t k_first = kv_lo >= kv_hi ? kv_hi : seg_lo + ((kv_lo - seg_lo) & ~31u);
     const int col_base = __builtin_amdgcn_readfirstlane(vcol[min(seg_lo, (uint32_t)rows - 1)]) - (int)seg_lo;
 
     // DMA of key tile k0 into stage s, 64 instructions of 1 KB split over
     // the three waves: wave `head` issues K instruction q and V instruction
-    // q for q = head + 3j < 32 (j = 0..10).
+    // q for q = min(head + 3j, 31), j = 0..10 (wave 2's last pair repeats
+    // q = 31: the same bytes to the same place). Issued unconditionally --
+    // no branch splits the MFMA loops -- with key rows clamped to the wave.
     // K: row of key q; lane L takes half L/32, stored chunk L%32 = global
     // chunk (L%32) ^ kswz(q). V: V^T rows 16(q%16)..+15 of half q/16; lane L
     // takes dim row L/4, stored chunk L%4 = global chunk (L%4) ^ vswz(row).
     auto dma_k = [&](uint32_t k0, int s, int j) {
-      const int q = head + 3 * j;
-      if (q >= kKvTile) return;
+      const int q = min(head + 3 * j, kKvTile - 1);
       const uint32_t key = min(k0 + q, (uint32_t)rows - 1);
       dma16(ks + (size_t)key * (2 * kHeadDim) + (lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ kswz(q)),
             lds + s * kStage + q * 1024);
     };
     auto dma_v = [&](uint32_t k0, int s, int j) {
-      const int q = head + 3 * j;
-      if (q >= kKvTile) return;
+      const int q = min(head + 3 * j, kKvTile - 1);
       const int hl = q >> 4, d = 16 * (q & 15) + (lane >> 2), c = (lane & 3) ^ vswz(d);
-      dma16(vt + ((size_t)hl * kHeadDim + d) * ldv + (col_base + (int)k0) + 8 * c,
-            lds + s * kStage + kKStage + q * 1024);
+      const int col = min(col_base + (int)k0, ldv - kKvTile);  // the refill past a sequence stays inside vt
+      dma16(vt + ((size_t)hl * kHeadDim + d) * ldv + col + 8 * c, lds + s * kStage + kKStage + q * 1024);
     };
     constexpr int kDmaPerWave = (kKvTile + 2) / 3;  // 11
 
     // Every wave has finished with both stages (previous tile of the grid
-    // stride) before the first DMA overwrites them. The first tile's DMA
-    // then flies while the queries load.
+    // stride), and every DMA it issued -- including the refill of the idle
+    // stage on its last key tile -- has landed, before the first DMA of
+    // this tile overwrites them. That DMA then flies while the queries load.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (k_first < kv_hi) {
 #pragma unroll
@@ -181,7 +243,6 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       // now refills -- issued in pieces between this tile's MFMAs, so the
       // memory pipeline's back-pressure overlaps the matrix work.
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      const bool more = k0 + kKvTile < kv_hi;
       const uint32_t k1 = k0 + kKvTile;
       const unsigned char* kst = lds + stage * kStage;
       const unsigned char* vst = kst + kKStage;
@@ -210,10 +271,10 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
         s1 = mfma(kf[cur][2], ql[st], s1);
         s0 = mfma(kf[cur][1], qh[st], s0);
         s1 = mfma(kf[cur][3], qh[st], s1);
-        if (more) {
-          dma_k(k1, stage ^ 1, st);
-          if (st + 8 < kDmaPerWave) dma_k(k1, stage ^ 1, st + 8);
-        }
+        // The next tile's K rows (on the last tile: a harmless refill of
+        // the idle stage).
+        dma_k(k1, stage ^ 1, st);
+        if (st + 8 < kDmaPerWave) dma_k(k1, stage ^ 1, st + 8);
       }
       // sc[4kb + v] = 16 x the score of key k0 + 8grp + 4kb + v, taken to
       // log2 units: exp(x) = exp2(x * log2e).
@@ -279,70 +340,129 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
         acc[d1] = mfma(vf[cur][2], pl, acc[d1]);
         acc[d0] = mfma(vf[cur][1], ph, acc[d0]);
         acc[d1] = mfma(vf[cur][3], ph, acc[d1]);
-        if (more) {
-          dma_v(k1, stage ^ 1, pr);
-          if (pr + 8 < kDmaPerWave) dma_v(k1, stage ^ 1, pr + 8);
-        }
+        dma_v(k1, stage ^ 1, pr);
+        if (pr + 8 < kDmaPerWave) dma_v(k1, stage ^ 1, pr + 8);
       }
     }
 
-    // Epilogue: context = acc / l, then Q8_0 per 32 dims (quants.c:97-177).
-    // acc[db][v] is dim 16db + 4grp + v of query t, so Q8_0 block b (dims
-    // 32b..32b+31) sits in acc[2b], acc[2b+1] of the four lane groups. The
-    // int8 values go to the row-tile layout of the projection GEMM (4 bytes
-    // per lane and half-block), the scales transposed ([block][row]). The
-    // eight blocks run phase by phase so their latencies overlap.
-    constexpr int kB = kHeadDim / kQK;
-    const float inv_l = 1.0f / l_run;
-    float vals[kB][8], amax[kB];
+    if (slot == kNoSlot) {
+      store_blocks<8>(acc, l_run, t, active, head, grp, rows, 0, cq, cd);
+    } else {
+      // Partial result of this key chunk: the unnormalised context and the
+      // running max / sum, in the lane order of the MFMA layout (16-byte
+      // stores, fully coalesced); attention_merge_kernel combines the parts.
+      float* part = partials + ((size_t)slot * kHeads + head) * kPartFloats;
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      amax[b] = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        vals[b][v] = acc[2 * b][v] * inv_l;
-        vals[b][4 + v] = acc[2 * b + 1][v] * inv_l;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax[b] = fmaxf(amax[b], fabsf(vals[b][i]));
-    }
-#pragma unroll
-    for (int b = 0; b < kB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 16, 64));
-#pragma unroll
-    for (int b = 0; b < kB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 32, 64));
-    // Row t of the row tiles: 32-row tile t/32, row t%32; this head's
-    // blocks are 8 head .. 8 head + 7 of the row's 24.
-    int8_t* qrow_out = cq + (size_t)(t >> 5) * (kEmbd / kQK) * 1024 + (size_t)head * kB * 1024 + (t & 31) * 16 + 4 * grp;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const float d = amax[b] / 127.0f;
-      const float id = amax[b] == 0.0f ? 0.0f : 1.0f / d;
-      int32_t qv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qv[i] = amax[b] == 0.0f ? 0 : q8_round(vals[b][i] * id);
-      if (active) {
-        *reinterpret_cast<uint32_t*>(qrow_out + b * 1024) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
-        *reinterpret_cast<uint32_t*>(qrow_out + b * 1024 + 512) = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
-        if (grp == 0) cd[(size_t)(head * kB + b) * rows + t] = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
-      }
+      for (int db = 0; db < 16; ++db) reinterpret_cast<floatx4*>(part)[db * 64 + lane] = acc[db];
+      reinterpret_cast<float2*>(part + 16 * 64 * 4)[lane] = make_float2(m_run, l_run);
     }
   }
   // Drain any DMA still in flight before the workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-unsigned build_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
-  unsigned n = 0;
-  for (size_t s = 0; s < batch; ++s)
-    for (size_t q = offsets[s]; q < offsets[s + 1]; q += kQTile) {
-      const size_t e = q + kQTile < offsets[s + 1] ? q + kQTile : offsets[s + 1];
-      tiles[4 * n + 0] = (uint32_t)q;
-      tiles[4 * n + 1] = (uint32_t)e;
-      tiles[4 * n + 2] = (uint32_t)offsets[s];
-      tiles[4 * n + 3] = (uint32_t)offsets[s + 1];
-      ++n;
+// Merges the key-chunk partials of split query tiles. One workgroup per
+// (query tile, quarter of the head dimension), one wave per head, lanes in
+// the attention kernel's MFMA layout; a quarter is 4 of the 16 16-dim
+// blocks, i.e. 2 whole Q8_0 blocks, so it quantizes on its own. With m =
+// max over parts of the running maxima (log2 units), l = sum_p l_p
+// 2^(m_p - m) and acc = sum_p acc_p 2^(m_p - m), in part order (a
+// deterministic order that depends only on the sequence), then the same
+// epilogue as an unsplit tile. Every load of a wave is issued before its
+// first use: the (m, l) pairs of all parts, then all parts' 4 x 16 bytes.
+constexpr int kMaxParts = (kCtx + kChunkKeys - 1) / kChunkKeys;  // 8
+__global__ void __launch_bounds__(192)
+attention_merge_kernel(const uint4* __restrict__ merges, const uint32_t* __restrict__ merge_count,
+                       const float* __restrict__ partials, int rows, int8_t* __restrict__ cq,
+                       float* __restrict__ cd) {
+  const int lane = threadIdx.x & 63, head = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qi = lane & 15, grp = lane >> 4;
+  const uint32_t count = 4 * *merge_count;
+  for (uint32_t wi = blockIdx.x; wi < count; wi += gridDim.x) {
+    const uint4 mg = merges[wi >> 2];
+    const int quarter = (int)(wi & 3);
+    const uint32_t q_end = min(mg.y, (uint32_t)rows), q0 = mg.x, first = mg.z;
+    const uint32_t parts = min(mg.w, (uint32_t)kMaxParts);
+    const bool active = q0 + qi < q_end;
+    const uint32_t t = active ? q0 + qi : (q_end > 0 ? q_end - 1 : 0);
+    const float* base = partials + ((size_t)first * kHeads + head) * kPartFloats;
+    const size_t stride = (size_t)kHeads * kPartFloats;  // next part
+    float2 ml[kMaxParts];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p)
+      ml[p] = p < (int)parts ? reinterpret_cast<const float2*>(base + p * stride + 16 * 64 * 4)[lane]
+                             : make_float2(-INFINITY, 0.0f);
+    floatx4 a[kMaxParts][4];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[p][i] = p < (int)parts ? reinterpret_cast<const floatx4*>(base + p * stride)[(4 * quarter + i) * 64 + lane]
+                                 : floatx4{};
+    float m = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) m = fmaxf(m, ml[p].x);
+    floatx4 acc[4] = {floatx4{}, floatx4{}, floatx4{}, floatx4{}};
+    float l = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+      if (p >= (int)parts) break;
+      const float w = ml[p].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[p].x - m);
+      l = l + ml[p].y * w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][v] = acc[i][v] + a[p][i][v] * w;
     }
-  return n;
+    store_blocks<2>(acc, l, t, active, head, grp, rows, 2 * quarter, cq, cd);
+  }
+}
+
+// Key chunks of a sequence of length n: one when n <= kSplitLen, else
+// ceil(n / kChunkKeys). Depends only on n, so a sequence is computed the
+// same way wherever it sits in a wave.
+static size_t key_chunks(size_t n) { return n <= kSplitLen ? 1 : (n + kChunkKeys - 1) / kChunkKeys; }
+
+AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges) {
+  AttentionCounts c{0, 0, 0};
+  for (size_t s = 0; s < batch; ++s) {
+    const size_t lo = offsets[s], hi = offsets[s + 1], chunks = key_chunks(hi - lo);
+    for (size_t q = lo; q < hi; q += kQTile) {
+      const size_t e = q + kQTile < hi ? q + kQTile : hi;
+      if (chunks > 1) {
+        uint32_t* m = merges + 4 * c.merges++;
+        m[0] = (uint32_t)q;
+        m[1] = (uint32_t)e;
+        m[2] = c.slots;
+        m[3] = (uint32_t)chunks;
+      }
+      for (size_t k = 0; k < chunks; ++k) {
+        uint32_t* it = items + 8 * c.items++;
+        it[0] = (uint32_t)q;
+        it[1] = (uint32_t)e;
+        it[2] = (uint32_t)lo;
+        it[3] = (uint32_t)hi;
+        it[4] = (uint32_t)(chunks > 1 ? lo + k * kChunkKeys : lo);
+        it[5] = (uint32_t)(chunks > 1 ? std::min(hi, lo + (k + 1) * kChunkKeys) : hi);
+        it[6] = chunks > 1 ? c.slots++ : kNoSlot;
+        it[7] = 0;
+      }
+    }
+  }
+  return c;
+}
+
+AttentionCounts attention_capacity(size_t tokens, size_t batch) {
+  // Items: at most ceil(n/16) per unsplit sequence (<= n + 15 in total over
+  // a wave... bounded by tokens + batch) and ceil(n/16) ceil(n/256) <= n
+  // for a split one; slots and merges peak when one sequence holds every
+  // token.
+  const size_t tiles = (tokens + kQTile - 1) / kQTile;
+  AttentionCounts c;
+  c.items = (unsigned)(tokens + batch);
+  c.slots = (unsigned)(tokens > kSplitLen ? tiles * key_chunks(tokens) : 0);
+  c.merges = (unsigned)(tokens > kSplitLen ? tiles : 0);
+  return c;
 }
 
 size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
@@ -355,11 +475,19 @@ size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
 }
 
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
-                            const uint32_t* tiles, const uint32_t* tile_count, int grid, int window, int rows,
-                            int8_t* cq, float* cd, hipStream_t st) {
+                            const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
+                            int8_t* cq, float* cd, float* partials, hipStream_t st) {
   if (rows <= 0 || grid <= 0 || ldv <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(192), 0, st, qs, ks, vt, ldv, vcol,
-                     reinterpret_cast<const uint4*>(tiles), tile_count, window, rows, cq, cd);
+                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd, partials);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_merge(const uint32_t* merges, const uint32_t* merge_count, int grid, const float* partials,
+                                  int rows, int8_t* cq, float* cd, hipStream_t st) {
+  if (rows <= 0 || grid <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_merge_kernel, dim3(grid), dim3(192), 0, st, reinterpret_cast<const uint4*>(merges),
+                     merge_count, partials, rows, cq, cd);
   return hipGetLastError();
 }
 

@@ -72,19 +72,32 @@ int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, c
 }
 
 int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const int32_t* vcol,
-                      const uint32_t* tiles, const uint32_t* tile_count, unsigned grid, unsigned window,
-                      unsigned rows, int8_t* cq, float* cd, void* stream) {
-  if (!qs || !ks || !vt || !vcol || !tiles || !tile_count || !cq || !cd || rows == 0 || grid == 0 ||
+                      const uint32_t* items, const uint32_t* item_count, unsigned grid, unsigned window,
+                      unsigned rows, int8_t* cq, float* cd, float* partials, void* stream) {
+  if (!qs || !ks || !vt || !vcol || !items || !item_count || !cq || !cd || rows == 0 || grid == 0 ||
       grid > 65536 || window > 4096u || ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
     return kInvalid;
-  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, vcol, tiles, tile_count, (int)grid,
-                                    (int)window, (int)rows, cq, cd, as_stream(stream)));
+  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, vcol, items, item_count, (int)grid,
+                                    (int)window, (int)rows, cq, cd, partials, as_stream(stream)));
 }
 
-unsigned eg2_attention_tiles(const size_t* offsets, size_t batch, uint32_t* tiles) {
-  if (!offsets || !tiles) return 0;
-  return eg2::build_attention_tiles(offsets, batch, tiles);
+int eg2_hip_attention_merge(const uint32_t* merges, const uint32_t* merge_count, unsigned grid, const float* partials,
+                            unsigned rows, int8_t* cq, float* cd, void* stream) {
+  if (!merges || !merge_count || !partials || !cq || !cd || rows == 0 || grid == 0 || grid > 65536) return kInvalid;
+  return code(eg2::launch_attention_merge(merges, merge_count, (int)grid, partials, (int)rows, cq, cd,
+                                          as_stream(stream)));
 }
+
+unsigned eg2_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges, unsigned* counts) {
+  if (!offsets || !items || !merges || !counts) return 0;
+  const eg2::AttentionCounts c = eg2::build_attention_items(offsets, batch, items, merges);
+  counts[0] = c.items;
+  counts[1] = c.merges;
+  counts[2] = c.slots;
+  return c.items;
+}
+
+size_t eg2_attention_partial_floats(void) { return eg2::kAttentionPartialFloats; }
 
 size_t eg2_attention_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
   if (!offsets || !vcol) return 0;

@@ -1,0 +1,168 @@
+// Deterministic wave packing (the dynamic batcher's fit rules) and the
+// stream runner on top of the executor's C ABI (include/eg2_stream.h).
+#include "eg2_stream.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <list>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "gemma2_kfd.h"
+
+namespace {
+
+constexpr int kEmbd = 768;
+
+bool valid(const eg2_batch_config* c) {
+  return c && c->max_batch_tokens > 0 && c->max_batch_sequence_tokens > 0 && c->max_batch_requests > 0;
+}
+
+// ei_sum_squares, SSE2 branch (kernels.c:82-94): two 4-wide accumulators
+// over a stride of 8, products rounded before each addition, then
+// (v0 + v2) + (v1 + v3) (kernels.c:35-39) and a scalar tail.
+float sum_squares_sse2(const float* x, int n) {
+  float a[4] = {0, 0, 0, 0}, b[4] = {0, 0, 0, 0};
+  int i = 0;
+  for (; i + 7 < n; i += 8)
+    for (int j = 0; j < 4; ++j) {
+      const float p = x[i + j] * x[i + j], q = x[i + 4 + j] * x[i + 4 + j];
+      a[j] = a[j] + p;
+      b[j] = b[j] + q;
+    }
+  float v[4];
+  for (int j = 0; j < 4; ++j) v[j] = a[j] + b[j];
+  float sum = (v[0] + v[2]) + (v[1] + v[3]);
+  for (; i < n; ++i) {
+    const float p = x[i] * x[i];
+    sum = sum + p;
+  }
+  return sum;
+}
+
+}  // namespace
+
+extern "C" void eg2_batch_config_default(eg2_batch_config* cfg) {
+  if (!cfg) return;
+  cfg->max_batch_tokens = 2048;
+  cfg->max_batch_sequence_tokens = 2048;
+  cfg->max_batch_requests = 32;
+  cfg->lookahead = 1;
+  cfg->sort_longest_first = 1;
+}
+
+extern "C" size_t eg2_pack_waves(const size_t* lengths, size_t n, const eg2_batch_config* cfg, size_t* order,
+                                 size_t* wave_end) {
+  if (!lengths || !order || !wave_end || !valid(cfg)) return 0;
+  for (size_t i = 0; i < n; ++i)
+    if (lengths[i] == 0) return 0;
+  const size_t budget = cfg->max_batch_tokens, seq_limit = cfg->max_batch_sequence_tokens;
+  const size_t max_req = cfg->max_batch_requests;
+  const size_t max_scan = max_req <= SIZE_MAX / 8 ? max_req * 8 : SIZE_MAX;  // inference_service.c:415-417
+  std::list<size_t> queue;
+  for (size_t i = 0; i < n; ++i) queue.push_back(i);
+  size_t placed = 0, waves = 0;
+  std::vector<size_t> wave;
+  while (!queue.empty()) {
+    wave.clear();
+    // The head always starts the wave.
+    const size_t head = queue.front();
+    queue.pop_front();
+    wave.push_back(head);
+    size_t total = lengths[head];
+    if (lengths[head] <= seq_limit) {
+      if (cfg->lookahead) {
+        size_t scanned = 0;
+        for (auto it = queue.begin(); it != queue.end() && wave.size() < max_req && scanned < max_scan;) {
+          ++scanned;
+          const size_t len = lengths[*it];
+          if (len <= seq_limit && total + len <= budget) {
+            wave.push_back(*it);
+            total += len;
+            it = queue.erase(it);
+          } else {
+            ++it;
+          }
+        }
+      } else {
+        while (!queue.empty() && wave.size() < max_req) {
+          const size_t len = lengths[queue.front()];
+          if (len > seq_limit || total + len > budget) break;
+          wave.push_back(queue.front());
+          total += len;
+          queue.pop_front();
+        }
+      }
+    }
+    if (cfg->sort_longest_first && wave.size() > 1)
+      std::stable_sort(wave.begin(), wave.end(), [&](size_t a, size_t b) { return lengths[a] > lengths[b]; });
+    for (size_t s : wave) order[placed++] = s;
+    wave_end[waves++] = placed;
+  }
+  return waves;
+}
+
+extern "C" bool eg2_normalize_prefix(float* embedding, unsigned dims) {
+  if (!embedding || (dims != 128 && dims != 256 && dims != 512 && dims != (unsigned)kEmbd)) return false;
+  if (dims < (unsigned)kEmbd) {
+    const float ss = sum_squares_sse2(embedding, (int)dims);
+    if (ss != 0.0f) {
+      const float scale = 1.0f / std::sqrt(ss);
+      for (unsigned i = 0; i < dims; ++i) embedding[i] = embedding[i] * scale;
+    }
+  }
+  return true;
+}
+
+extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* text_offsets, size_t n_texts,
+                                 const unsigned* dims, const eg2_batch_config* cfg, float* out, size_t* n_waves,
+                                 char* err, size_t len) {
+  try {
+    if (!ctx || !ids || !text_offsets || !dims || !out || !valid(cfg) || n_texts == 0)
+      throw std::runtime_error("invalid stream arguments");
+    std::vector<size_t> lengths(n_texts);
+    for (size_t i = 0; i < n_texts; ++i) {
+      if (text_offsets[i + 1] <= text_offsets[i]) throw std::runtime_error("empty or unordered text");
+      if (dims[i] != 128 && dims[i] != 256 && dims[i] != 512 && dims[i] != (unsigned)kEmbd)
+        throw std::runtime_error("unsupported embedding dimensions");
+      lengths[i] = text_offsets[i + 1] - text_offsets[i];
+    }
+    std::vector<size_t> order(n_texts), wave_end(n_texts);
+    const size_t waves = eg2_pack_waves(lengths.data(), n_texts, cfg, order.data(), wave_end.data());
+    if (!waves) throw std::runtime_error("packing failed");
+    std::vector<int32_t> wave_ids;
+    std::vector<size_t> offsets;
+    std::vector<float> wave_out;
+    size_t begin = 0;
+    for (size_t w = 0; w < waves; ++w) {
+      const size_t end = wave_end[w], b = end - begin;
+      wave_ids.clear();
+      offsets.assign(1, 0);
+      for (size_t k = begin; k < end; ++k) {
+        const size_t i = order[k];
+        wave_ids.insert(wave_ids.end(), ids + text_offsets[i], ids + text_offsets[i + 1]);
+        offsets.push_back(wave_ids.size());
+      }
+      wave_out.resize(b * kEmbd);
+      char msg[512] = {0};
+      if (!ei_gemma2_kfd_batch(ctx, wave_ids.data(), offsets.data(), b, wave_out.data(), msg, sizeof msg))
+        throw std::runtime_error(std::string(msg).rfind("HIP: ", 0) == 0 ? std::string(msg).substr(5) : msg);
+      for (size_t k = 0; k < b; ++k) {
+        const size_t i = order[begin + k];
+        float* e = out + i * kEmbd;
+        std::memcpy(e, wave_out.data() + k * kEmbd, kEmbd * sizeof(float));
+        eg2_normalize_prefix(e, dims[i]);
+        std::fill(e + dims[i], e + kEmbd, 0.0f);
+      }
+      begin = end;
+    }
+    if (n_waves) *n_waves = waves;
+    return true;
+  } catch (const std::exception& e) {
+    if (err && len) std::snprintf(err, len, "HIP: %s", e.what());
+    return false;
+  }
+}

@@ -47,6 +47,12 @@ class EiGguf(C.Structure):
                 ("kv", C.POINTER(EiKv)), ("tensors", C.POINTER(EiTensor))]
 
 
+class BatchConfig(C.Structure):
+    """eg2_batch_config (include/eg2_stream.h)."""
+    _fields_ = [("max_batch_tokens", C.c_size_t), ("max_batch_sequence_tokens", C.c_size_t),
+                ("max_batch_requests", C.c_size_t), ("lookahead", C.c_uint), ("sort_longest_first", C.c_uint)]
+
+
 class SynthConfig(C.Structure):
     _fields_ = [("seed", C.c_uint64), ("n_layer", C.c_uint), ("dense_head", C.c_uint), ("weight_std", C.c_float),
                 ("embed_std", C.c_float), ("norm_std", C.c_float), ("rope_base_full", C.c_float),
@@ -96,7 +102,7 @@ class EgSaxpy(C.Structure):
     _fields_ = [("y", _vp), ("x", _vp), ("a", C.c_float), ("n", _u)]
 
 
-# Every symbol declared in include/eg2_hip.h, include/eg2_ops.h and include/gemma2_kfd.h.
+# Every symbol declared in include/eg2_hip.h, eg2_ops.h, eg2_stream.h and gemma2_kfd.h.
 SIGNATURES = {
     "eg2_op_launch": (C.c_int, [C.c_char_p, _vp, C.c_size_t, _u, _u, _u, _vp]),
     "eg2_op_count": (C.c_uint, []),
@@ -104,8 +110,10 @@ SIGNATURES = {
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
-    "eg2_attention_tiles": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_hip_attention_merge": (C.c_int, [_vp, _vp, _u, _vp, _u, _vp, _vp, _vp]),
+    "eg2_attention_items": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp, _vp, _vp]),
+    "eg2_attention_partial_floats": (C.c_size_t, []),
     "eg2_attention_vt_columns": (C.c_size_t, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
@@ -123,6 +131,12 @@ SIGNATURES = {
     "eg2_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
     "eg2_gguf_close": (None, [C.POINTER(EiGguf)]),
     "eg2_synth_write_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthConfig), C.c_char_p, C.c_size_t]),
+    "eg2_batch_config_default": (None, [C.POINTER(BatchConfig)]),
+    "eg2_pack_waves": (C.c_size_t, [C.POINTER(C.c_size_t), C.c_size_t, C.POINTER(BatchConfig), C.POINTER(C.c_size_t),
+                                    C.POINTER(C.c_size_t)]),
+    "eg2_normalize_prefix": (C.c_bool, [_f, C.c_uint]),
+    "eg2_stream_embed": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.POINTER(C.c_uint),
+                                    C.POINTER(BatchConfig), _f, C.POINTER(C.c_size_t), C.c_char_p, C.c_size_t]),
     "ei_gemma2_kfd_create": (C.c_void_p, [C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
     "ei_gemma2_kfd_free": (None, [C.c_void_p]),
     "eg2_kfd_stage": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p, C.c_size_t]),
@@ -242,6 +256,25 @@ class Encoder:
             raise HipError(err.value.decode())
         return out
 
+    def stream(self, ids, text_offsets, dims, cfg=None):
+        """eg2_stream_embed: texts ids[text_offsets[i]:text_offsets[i+1]] with
+        output widths dims[i], packed into waves by the batcher's rules.
+        Returns (float32 [n, 768] with zeros past dims[i], wave count)."""
+        import numpy as np
+
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        n = len(text_offsets) - 1
+        offs = (C.c_size_t * (n + 1))(*[int(o) for o in text_offsets])
+        d = (C.c_uint * n)(*[int(x) for x in dims])
+        cfg = cfg or batch_config()
+        out = np.zeros((n, N_EMBD), dtype=np.float32)
+        waves = C.c_size_t(0)
+        err = C.create_string_buffer(1024)
+        if not lib().eg2_stream_embed(self.ctx, ids.ctypes.data_as(_i32), offs, n, d, C.byref(cfg),
+                                      out.ctypes.data_as(_f), C.byref(waves), err, 1024):
+            raise HipError(err.value.decode())
+        return out, waves.value
+
     def close(self):
         if getattr(self, "ctx", None):
             lib().ei_gemma2_kfd_free(self.ctx)
@@ -254,6 +287,43 @@ class Encoder:
             self.close()
         except Exception:
             pass
+
+
+def batch_config(**overrides):
+    """The launcher's batching settings (eg2_batch_config_default), with overrides."""
+    cfg = BatchConfig()
+    lib().eg2_batch_config_default(C.byref(cfg))
+    for k, v in overrides.items():
+        setattr(cfg, k, v)
+    return cfg
+
+
+def pack_waves(lengths, cfg=None):
+    """eg2_pack_waves: the list of waves, each a list of sequence indices in
+    execution order."""
+    n = len(lengths)
+    arr = (C.c_size_t * max(n, 1))(*[int(x) for x in lengths])
+    order = (C.c_size_t * max(n, 1))()
+    ends = (C.c_size_t * max(n, 1))()
+    cfg = cfg or batch_config()
+    w = lib().eg2_pack_waves(arr, n, C.byref(cfg), order, ends)
+    if n and not w:
+        raise HipError("eg2_pack_waves rejected its arguments")
+    waves, b = [], 0
+    for i in range(w):
+        waves.append(list(order[b:ends[i]]))
+        b = ends[i]
+    return waves
+
+
+def normalize_prefix(embedding, dims):
+    """eg2_normalize_prefix on a copy of a 768-float embedding."""
+    import numpy as np
+
+    e = np.ascontiguousarray(embedding, dtype=np.float32).copy()
+    if not lib().eg2_normalize_prefix(e.ctypes.data_as(_f), dims):
+        raise HipError(f"unsupported dims {dims}")
+    return e
 
 
 def rope_table(base, n_pos=N_CTX):
@@ -315,21 +385,39 @@ def q8_weight_tiles(blocks_u8, rows, k):
     return wq, wd
 
 
+def attention_items(offsets):
+    """(items uint32 [n, 8], merges uint32 [m, 4], slots) of a packing
+    (eg2_attention_items)."""
+    import numpy as np
+
+    offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
+    total, batch = int(offsets[-1]), len(offsets) - 1
+    items = np.zeros((total + batch + 1, 8), dtype=np.uint32)
+    merges = np.zeros(((total + 15) // 16 + 1, 4), dtype=np.uint32)
+    counts = np.zeros(3, dtype=np.uint32)
+    lib().eg2_attention_items(offs, batch, items.ctypes.data, merges.ctypes.data, counts.ctypes.data)
+    return items[:counts[0]], merges[:counts[1]], int(counts[2])
+
+
 class AttentionPlan:
-    """The attention work list of a packing (eg2_attention_tiles) on the
-    device: 4 uint32 per query tile, then the tile count."""
+    """The attention work lists of a packing on the device (items, merges,
+    their counts) and the partial-result buffer of split sequences."""
 
     def __init__(self, offsets, device):
         import numpy as np
         import torch
 
-        offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
-        tiles = np.zeros(4 * int(offsets[-1]) + 4, dtype=np.uint32)
-        n = lib().eg2_attention_tiles(offs, len(offsets) - 1, tiles.ctypes.data)
-        tiles[-1] = n
-        self.tiles = torch.from_numpy(tiles.view(np.int32)).to(device)
-        self.count_ptr = self.tiles.data_ptr() + 4 * (len(tiles) - 1)
+        items, merges, slots = attention_items(offsets)
+        counts = np.array([len(items), len(merges)], dtype=np.uint32)
+        self.items = torch.from_numpy(np.ascontiguousarray(items).view(np.int32).reshape(-1)).to(device)
+        self.merges = torch.from_numpy(np.ascontiguousarray(merges).view(np.int32).reshape(-1).copy()
+                                       if len(merges) else np.zeros(4, np.int32)).to(device)
+        self.counts = torch.from_numpy(counts.view(np.int32)).to(device)
+        self.n_merges = len(merges)
+        self.partials = torch.zeros(max(1, slots) * lib().eg2_attention_partial_floats(), dtype=torch.float32,
+                                    device=device)
         self.grid = max(1, (int(offsets[-1]) + 7) // 8)
+        self.merge_grid = max(1, (int(offsets[-1]) + 3) // 4)
 
 
 class ops:
@@ -377,9 +465,14 @@ class ops:
     @classmethod
     def attention_planned(cls, qs, ks, vt, vcol, plan, window, cq, cd):
         """attention() with a prebuilt AttentionPlan (no host work, no sync)."""
+        rows = qs.shape[0]
         check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol),
-                                      cls._p(plan.tiles), C.c_void_p(plan.count_ptr), plan.grid, window,
-                                      qs.shape[0], cls._p(cq), cls._p(cd), cls._stream()), "attention")
+                                      cls._p(plan.items), cls._p(plan.counts), plan.grid, window, rows, cls._p(cq),
+                                      cls._p(cd), cls._p(plan.partials), cls._stream()), "attention")
+        if plan.n_merges:
+            check(lib().eg2_hip_attention_merge(cls._p(plan.merges), C.c_void_p(plan.counts.data_ptr() + 4),
+                                                plan.merge_grid, cls._p(plan.partials), rows, cls._p(cq), cls._p(cd),
+                                                cls._stream()), "attention_merge")
 
     @classmethod
     def gelu_quant(cls, gu, gq, gd):

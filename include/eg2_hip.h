@@ -64,22 +64,40 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * limited to |t - s| <= window/2 when window > 0; 3 query heads share one KV
  * head, head_dim 256. Inputs are the split q/k rows and the transposed v of
  * eg2_hip_qk_norm_rope (same vt, ldv and vcol; vt columns that no token
- * wrote must hold finite values, e.g. zeros). The work list `tiles`
- * (device, 4 uint32 per tile, from eg2_attention_tiles) holds *tile_count
- * (device) query tiles; `grid` workgroups stride over it. The fp32 context
- * is quantized to Q8_0 (quants.c:97-177) into cq (row tiles, k = 768) and
- * cd [24][rows]. A sequence's result does not depend on its place in the
- * wave.
+ * wrote must hold finite values, e.g. zeros). The work list `items`
+ * (device, 8 uint32 per item, from eg2_attention_items) holds *item_count
+ * (device) items; `grid` workgroups stride over it. An item whose slot is
+ * 0xFFFFFFFF quantizes its fp32 context to Q8_0 (quants.c:97-177) into cq
+ * (row tiles, k = 768) and cd [24][rows]; the items of a sequence longer
+ * than 256 tokens cover 256-key chunks and write partial results to
+ * `partials` (eg2_attention_partial_floats() floats per slot), which
+ * eg2_hip_attention_merge then combines and quantizes. A sequence's result
+ * does not depend on its place in the wave.
  * Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const int32_t *vcol,
-                      const uint32_t *tiles, const uint32_t *tile_count, unsigned grid, unsigned window,
-                      unsigned rows, int8_t *cq, float *cd, void *stream);
+                      const uint32_t *items, const uint32_t *item_count, unsigned grid, unsigned window,
+                      unsigned rows, int8_t *cq, float *cd, float *partials, void *stream);
 
-/* Host: the query-tile list of a packed wave with sequences
- * [offsets[s], offsets[s+1]) -- up to 16 queries of one sequence per tile as
- * {first query, end, sequence start, sequence end}. `tiles` must hold
- * 4 * offsets[batch] entries; returns the tile count. */
-unsigned eg2_attention_tiles(const size_t *offsets, size_t batch, uint32_t *tiles);
+/* Second step of eg2_hip_attention for split sequences: merges the
+ * key-chunk partials of each query tile in `merges` (device, 4 uint32 per
+ * tile: first query, end, first slot, parts; *merge_count of them) and
+ * quantizes the context into cq / cd. Part of the same replacement. */
+int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count, unsigned grid, const float *partials,
+                            unsigned rows, int8_t *cq, float *cd, void *stream);
+
+/* Host: the work lists of a packed wave with sequences [offsets[s],
+ * offsets[s+1]): per query tile of up to 16 tokens one item per key chunk
+ * {first query, end, sequence start, sequence end, chunk start, chunk end,
+ * slot or 0xFFFFFFFF, 0} (a sequence of n > 256 tokens has ceil(n / 256)
+ * chunks, partial slots numbered consecutively; shorter ones one chunk and
+ * no slot), and per split tile one merge record {first query, end, first
+ * slot, parts}. counts[0..2] = items, merges, slots. `items` needs room for
+ * 8 * (offsets[batch] + batch) entries, `merges` for 4 * ceil(offsets[batch]
+ * / 16). Returns the item count. */
+unsigned eg2_attention_items(const size_t *offsets, size_t batch, uint32_t *items, uint32_t *merges, unsigned *counts);
+
+/* Floats of one partial-result slot (3 heads x (16 x 256 + 2 x 64)). */
+size_t eg2_attention_partial_floats(void);
 
 /* Host: the transposed-v column of every token (vcol[offsets[batch]]):
  * each sequence starts at a multiple of 32 and its tokens take consecutive

@@ -322,6 +322,40 @@ def test_attention_packed(eg2, gpu, window):
     assert same.mean() > 0.995
 
 
+@pytest.mark.parametrize("lens", [[1100, 600, 300, 48], [2048]])
+def test_attention_long_sequences_split(eg2, gpu, lens):
+    """Sequences longer than 256 tokens run as 256-key chunks whose partial
+    softmax results are merged: the same float64 bound as the unsplit
+    path, the same agreement with the oracle's quantized context, and a
+    split sequence gives the same bits alone as packed."""
+    rng = np.random.default_rng(sum(lens))
+    T = sum(lens)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    q = (rng.standard_normal((T, N_EMBD)) * 0.0625).astype(np.float32)
+    k = rng.standard_normal((T, HEAD_DIM)).astype(np.float32)
+    v = rng.standard_normal((T, HEAD_DIM)).astype(np.float32)
+    cq, cd = run_attention(eg2, gpu, q, k, v, offsets, 0)
+    exact = attention_double(q, k, v, offsets, 0)
+    tol = 2.0 ** -16 * np.abs(v).max()
+    got = cq.astype(np.float32).reshape(T, 24, 32) * cd[:, :, None]
+    bound = (0.5 + 127 * 2.0 ** -11) * (1 + 2.0 ** -10) * cd[:, :, None] + tol
+    assert (np.abs(got - exact.reshape(T, 24, 32)) <= bound).all()
+    ctx = np.zeros((T, N_EMBD), np.float32)
+    sc = np.zeros(4096, np.float32)
+    for s in range(len(lens)):
+        a, b = int(offsets[s]), int(offsets[s + 1])
+        oracle().or_attention_range(fptr(q[a:b]), fptr(k[a:b]), fptr(v[a:b]), b - a, 0, 0, b - a, fptr(ctx[a:b]),
+                                    fptr(sc))
+    ref = quantize_q8_0(ctx)
+    same = (cq.reshape(T, 24, 32) == ref["qs"]).all(2) & (cd == ref["d"].view(np.float16).astype(np.float32))
+    print(f"identical Q8_0 blocks vs the oracle: {same.mean():.5f}")
+    assert same.mean() > 0.995
+    if len(lens) > 1:
+        a, b = int(offsets[1]), int(offsets[2])
+        sq, sd = run_attention(eg2, gpu, q[a:b], k[a:b], v[a:b], [0, b - a], 0)
+        assert np.array_equal(sq, cq[a:b]) and np.array_equal(sd, cd[a:b])
+
+
 def test_attention_single_token_segments(eg2, gpu):
     """Length-1 sequences attend only to themselves: the context is v
     (to the 22 bits of the split operands), quantized like the reference."""

@@ -1,0 +1,76 @@
+"""The dynamic-batching stream (eg2_stream_embed) on the GPU: texts packed
+into waves by the batcher's rules, each wave through the executor, each
+embedding truncated and prefix-normalised (kernels.c:393-407)."""
+import numpy as np
+import pytest
+
+import gguf_py
+import oracle_lib as OL
+
+pytestmark = pytest.mark.gpu
+DIMS = [128, 256, 512, 768]
+
+
+@pytest.fixture(scope="module")
+def stream_encoder(eg2, gpu, tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("s") / "stream.gguf")
+    eg2.synth_gguf(path, seed=31, n_layer=2, dense_head=True, sliding_window=512, sliding_window_pattern=2,
+                   rope_base_full=1e6, rope_base_swa=1e4, threads=16)
+    enc = eg2.Encoder(path)
+    yield enc, path
+    enc.close()
+
+
+def make_stream(rng, n_texts, max_len):
+    lens = np.floor(np.exp(rng.uniform(np.log(1), np.log(max_len), n_texts))).astype(int)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    ids = rng.integers(0, OL.VOCAB, int(offsets[-1])).astype(np.int32)
+    dims = [DIMS[i % 4] for i in range(n_texts)]
+    return ids, offsets, dims
+
+
+def test_stream_equals_each_text_alone(eg2, stream_encoder):
+    """Packing never changes a sequence's bits, so every stream embedding
+    equals the text run alone, truncated and prefix-normalised."""
+    enc, _ = stream_encoder
+    rng = np.random.default_rng(7)
+    ids, offsets, dims = make_stream(rng, 70, 700)
+    cfg = eg2.batch_config(max_batch_requests=8)
+    out, waves = enc.stream(ids, offsets, dims, cfg)
+    lengths = np.diff(offsets).tolist()
+    assert waves == len(eg2.pack_waves(lengths, cfg)) > 1
+    for i in range(len(dims)):
+        alone = enc.batch(ids[offsets[i]:offsets[i + 1]], [0, lengths[i]])[0]
+        want = eg2.normalize_prefix(alone, dims[i])
+        assert np.array_equal(out[i, :dims[i]], want[:dims[i]]), i
+        assert not out[i, dims[i]:].any()
+        assert abs(np.linalg.norm(out[i, :dims[i]]) - 1) < 1e-5
+
+
+def test_stream_matches_oracle(eg2, stream_encoder):
+    """A small stream against the CPU oracle (cosine >= 0.9999, max-abs <=
+    2e-3 on every truncated, normalised embedding)."""
+    enc, path = stream_encoder
+    rng = np.random.default_rng(8)
+    ids, offsets, dims = make_stream(rng, 12, 120)
+    out, _ = enc.stream(ids, offsets, dims)
+    want = OL.forward(gguf_py.oracle_model(path), ids, offsets.astype(np.uint64), threads=16)
+    for i, d in enumerate(dims):
+        w = want[i].copy()
+        assert OL.oracle().or_normalize_prefix(OL.fptr(w), d) == 1
+        g = out[i, :d]
+        cos = float(g @ w[:d] / np.linalg.norm(g) / np.linalg.norm(w[:d]))
+        assert cos >= 0.9999 and np.abs(g - w[:d]).max() <= 2e-3, (i, cos)
+
+
+def test_stream_rejects_bad_texts(eg2, stream_encoder):
+    enc, _ = stream_encoder
+    with pytest.raises(eg2.HipError, match="dimensions"):
+        enc.stream(np.zeros(4, np.int32), [0, 4], [100])
+    with pytest.raises(eg2.HipError, match="empty"):
+        enc.stream(np.zeros(4, np.int32), [0, 4, 4], [128, 128])
+    with pytest.raises(eg2.HipError, match="out of range"):
+        enc.stream(np.full(4, OL.VOCAB, np.int32), [0, 4], [128])
+    # the context is poisoned only by device failures, not by rejected input
+    out, _ = enc.stream(np.zeros(4, np.int32), [0, 4], [768])
+    assert abs(np.linalg.norm(out[0]) - 1) < 1e-5

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_functions():
     names = set()
-    for h in ("gemma2_kfd.h", "eg2_hip.h", "eg2_ops.h"):
+    for h in ("gemma2_kfd.h", "eg2_hip.h", "eg2_ops.h", "eg2_stream.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b((?:ei|eg2)_[a-z0-9_]+)\s*\(", text):
@@ -62,10 +62,12 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 48, p, p, p, 4, 0, 32, p, p, None) == inval  # ldv % 32
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 48, p, p, p, 4, 0, 32, p, p, p, None) == inval  # ldv % 32
+    assert lib.eg2_hip_attention_merge(p, p, 0, p, 32, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention_merge(p, p, 4, None, 32, p, p, None) == inval
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, p, 1e-6, p, p, p, 40, 4, None) == inval  # ldv % 32
     assert lib.eg2_hip_quantize_rows(p, 96, p, p, 1, None) == inval  # k % 64
     assert lib.eg2_hip_l2_prefix(p, 768, 769, 1, None) == inval
@@ -84,19 +86,37 @@ def test_vt_columns_align_each_sequence(eg2):
     assert ldv == base and ldv <= offs[-1] + 31 * (len(offs) - 1)
 
 
-def test_attention_tiles_cover_each_sequence(eg2):
-    offs = [0, 1, 33, 97, 98, 200]
-    arr = (C.c_size_t * len(offs))(*offs)
-    tiles = np.zeros(4 * 200, np.uint32)
-    n = eg2.lib().eg2_attention_tiles(arr, len(offs) - 1, tiles.ctypes.data)
-    t = tiles[:4 * n].reshape(n, 4)
-    covered = np.zeros(200, int)
-    for q0, q1, lo, hi in t:
-        assert lo <= q0 < q1 <= hi and q1 - q0 <= 16 and (q0 - lo) % 16 == 0
-        assert [lo, hi] in [[offs[s], offs[s + 1]] for s in range(len(offs) - 1)]
-        covered[q0:q1] += 1
-    assert (covered == 1).all()
-    assert n == sum((offs[s + 1] - offs[s] + 15) // 16 for s in range(len(offs) - 1))
+def test_attention_items_cover_each_sequence(eg2):
+    """Every (query, key) pair of a sequence is covered by exactly one item;
+    query tiles are 16 tokens from the sequence start; a sequence longer than
+    256 tokens splits its keys into 256-key chunks (aligned to its start)
+    with consecutive partial slots and one merge record per query tile."""
+    offs = [0, 1, 33, 97, 98, 200, 600, 1100]
+    items, merges, slots = eg2.attention_items(offs)
+    seqs = [(offs[s], offs[s + 1]) for s in range(len(offs) - 1)]
+    covered = {s: np.zeros((hi - lo, hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
+    used_slots = []
+    for q0, q1, lo, hi, k0, k1, slot, zero in items:
+        s = seqs.index((lo, hi))
+        assert lo <= q0 < q1 <= hi and q1 - q0 <= 16 and (q0 - lo) % 16 == 0 and zero == 0
+        assert lo <= k0 < k1 <= hi and (k0 - lo) % 256 == 0
+        n = hi - lo
+        if n <= 256:
+            assert (k0, k1, slot) == (lo, hi, 0xFFFFFFFF)
+        else:
+            assert k1 - k0 == min(256, hi - k0)
+            used_slots.append(int(slot))
+        covered[s][q0 - lo:q1 - lo, k0 - lo:k1 - lo] += 1
+    assert all((c == 1).all() for c in covered.values())
+    assert sorted(used_slots) == list(range(slots))
+    # merges: one per query tile of a split sequence, slots first..first+parts-1
+    split = [(lo, hi) for lo, hi in seqs if hi - lo > 256]
+    assert len(merges) == sum((hi - lo + 15) // 16 for lo, hi in split)
+    for q0, q1, first, parts in merges:
+        lo, hi = next((lo, hi) for lo, hi in split if lo <= q0 < hi)
+        assert parts == (hi - lo + 255) // 256
+        tile_items = [it for it in items if it[0] == q0]
+        assert sorted(int(it[6]) for it in tile_items) == list(range(first, first + parts))
 
 
 @pytest.mark.parametrize("base", [10000.0, 1000000.0])
