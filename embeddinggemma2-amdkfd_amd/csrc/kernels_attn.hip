@@ -313,8 +313,12 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       psum += __shfl_xor(psum, 32, 64);
       l_run = l_run * alpha + psum;
       m_run = m_new;
+      // alpha is exactly 1 in every lane whose maximum did not grow; skip
+      // the rescale when that holds for the whole wave (most tiles).
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-      for (int db = 0; db < 16; ++db) acc[db] *= alpha;
+        for (int db = 0; db < 16; ++db) acc[db] *= alpha;
+      }
 
       // O^T += V^T . P^T: lane group grp supplies keys 8grp..8grp+7, V^T chunk
       // grp. Dimension blocks go in pairs: the V^T fragments of the next pair

@@ -444,8 +444,8 @@ rms_norm_rows_kernel(float* __restrict__ x, const float* __restrict__ w, float e
 
 // kernels.c:417-427 after the per-token RMS (rms_norm_rows_kernel): one
 // workgroup per sequence, one thread per column, sums the normalised rows in
-// token order (loads issued kPoolBatch rows ahead of the additions), scales
-// by 1/n, then L2-normalises in the SSE2 order (kernels.c:393-396).
+// token order (two batches of kPoolBatch rows in flight), scales by 1/n,
+// then L2-normalises in the SSE2 order (kernels.c:393-396).
 constexpr int kPoolBatch = 32;
 __global__ void __launch_bounds__(kEmbd)
 pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets, float* __restrict__ out) {
@@ -453,14 +453,24 @@ pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets
   __shared__ float total;
   const int s = blockIdx.x, e = threadIdx.x;
   const uint32_t lo = offsets[s], hi = offsets[s + 1];
+  // The sum runs in token order; the loads of the next batch are in flight
+  // while the current batch is added.
   float sum = 0.0f;
-  for (uint32_t t = lo; t < hi; t += kPoolBatch) {
-    float v[kPoolBatch];
+  float v[2][kPoolBatch];
+  auto load = [&](float (&b)[kPoolBatch], uint32_t t) {
 #pragma unroll
-    for (int i = 0; i < kPoolBatch; ++i) v[i] = t + i < hi ? x[(size_t)(t + i) * kEmbd + e] : 0.0f;
+    for (int i = 0; i < kPoolBatch; ++i) b[i] = t + i < hi ? x[(size_t)(t + i) * kEmbd + e] : 0.0f;
+  };
+  load(v[0], lo);
+  for (uint32_t t = lo; t < hi; t += 2 * kPoolBatch) {
+    load(v[1], t + kPoolBatch);
 #pragma unroll
     for (int i = 0; i < kPoolBatch; ++i)
-      if (t + i < hi) sum = sum + v[i];
+      if (t + i < hi) sum = sum + v[0][i];
+    load(v[0], t + 2 * kPoolBatch);
+#pragma unroll
+    for (int i = 0; i < kPoolBatch; ++i)
+      if (t + kPoolBatch + i < hi) sum = sum + v[1][i];
   }
   const float scale = 1.0f / (float)(hi - lo);
   acc[e] = sum * scale;
