@@ -37,10 +37,10 @@ hipError_t launch_attention_merge(const uint32_t* merges, const uint32_t* merge_
 // sequences [offsets[s], offsets[s+1]): per query tile of up to 16 tokens
 // of one sequence, one item (8 uint32: first query, end, sequence start,
 // sequence end, key chunk start, key chunk end, partial slot or
-// 0xFFFFFFFF, 0) per key chunk -- a sequence longer than 256 tokens splits
-// its keys into 256-key chunks whose partial results go to consecutive
-// slots -- and, for split tiles, one merge record (first query, end, first
-// slot, parts). attention_capacity bounds the counts for a wave of
+// 0xFFFFFFFF, 0) per key chunk -- a sequence of n > 256 tokens splits its
+// keys into min(ceil(n / 256), 4) chunks of equal size rounded up to 32,
+// whose partial results go to consecutive slots -- and, for split tiles,
+// one merge record (first query, end, first slot, parts). attention_capacity bounds the counts for a wave of
 // `tokens` tokens in at most `batch` sequences.
 struct AttentionCounts {
   unsigned items, merges, slots;

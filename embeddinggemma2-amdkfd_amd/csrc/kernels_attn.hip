@@ -53,17 +53,30 @@ constexpr int kKStage = kKvTile * 2 * kHeadDim * 2;  // [key][hi|lo][256] fp16 =
 constexpr int kVStage = 2 * kHeadDim * kKvTile * 2;  // [hi|lo][dim][32 keys] fp16 = 32 KB
 constexpr int kStage = kKStage + kVStage;
 constexpr float kLog2e = 1.4426950408889634f;
+// A workgroup runs 3 compute waves (one per query head) and 3 more that
+// only move K/V tiles: LDS DMA throughput grows with the number of waves
+// issuing it (measured on this part: 5.1, 9.5 and 14.4 TB/s for 3, 6 and 12
+// waves streaming 64 KB tiles, one workgroup per CU), and the 64 DMA
+// instructions of a tile are spread over all six.
+constexpr int kComputeWaves = kHeads, kWaves = 6;
+constexpr int kDmaPerWave = (kKvTile + kWaves - 1) / kWaves;  // 6 K and 6 V instructions
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;           // item writes the final context
 constexpr int kPartFloats = 16 * 64 * 4 + 64 * 2;   // per (slot, head): acc in lane order, then (m, l)
-constexpr uint32_t kSplitLen = 256;                // longer sequences split their keys ...
-constexpr uint32_t kChunkKeys = 256;               // ... into chunks of this many keys
+constexpr uint32_t kSplitLen = 256;  // longer sequences split their keys into chunks ...
+constexpr uint32_t kMaxChunks = 4;   // ... of at least kSplitLen keys, at most this many
 
 __device__ __forceinline__ floatx4 mfma(const half8& a, const half8& b, const floatx4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// LDS DMA from a wave-uniform global base (SGPR pair) plus a per-lane byte
+// offset, 16 bytes per lane, to the wave-uniform LDS address `lds` (+16
+// bytes per lane), which the instruction takes from M0 (this kernel has no
+// other M0 user). The saddr form keeps one 32-bit offset per lane instead
+// of a 64-bit address.
+__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
 }
 
 // Key fed to row i of key block kb of the score MFMA. Output row r = 4j + v
@@ -125,16 +138,19 @@ __device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l
   }
 }
 
-__global__ void __launch_bounds__(192)
+__global__ void __launch_bounds__(64 * kWaves)
 attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks, const _Float16* __restrict__ vt,
                  int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ items,
                  const uint32_t* __restrict__ item_count, int window, int rows, int8_t* __restrict__ cq,
                  float* __restrict__ cd, float* __restrict__ partials) {
   __shared__ __align__(16) unsigned char lds[2 * kStage];
 
-  const int tid = threadIdx.x, lane = tid & 63, head = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool compute = w < kComputeWaves;
+  const int head = compute ? w : 0;
   const int qi = lane & 15, grp = lane >> 4;
   const uint32_t count = *item_count;
+  const unsigned lds0 = (unsigned)(uintptr_t)lds;
   for (uint32_t item = blockIdx.x; item < count; item += gridDim.x) {
     // Item fields are clamped to the wave so a malformed list can never
     // address outside the rows (an empty key range yields a non-finite row).
@@ -184,26 +200,26 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     const int col_base = __builtin_amdgcn_readfirstlane(vcol[min(seg_lo, (uint32_t)rows - 1)]) - (int)seg_lo;
 
     // DMA of key tile k0 into stage s, 64 instructions of 1 KB split over
-    // the three waves: wave `head` issues K instruction q and V instruction
-    // q for q = min(head + 3j, 31), j = 0..10 (wave 2's last pair repeats
-    // q = 31: the same bytes to the same place). Issued unconditionally --
-    // no branch splits the MFMA loops -- with key rows clamped to the wave.
+    // the six waves: wave w issues K instruction q and V instruction q for
+    // q = min(w + 6j, 31), j = 0..5 (the clamped repeats write the same
+    // bytes to the same place). Issued unconditionally -- no branch splits
+    // the MFMA loops -- with key rows clamped to the wave.
     // K: row of key q; lane L takes half L/32, stored chunk L%32 = global
     // chunk (L%32) ^ kswz(q). V: V^T rows 16(q%16)..+15 of half q/16; lane L
     // takes dim row L/4, stored chunk L%4 = global chunk (L%4) ^ vswz(row).
     auto dma_k = [&](uint32_t k0, int s, int j) {
-      const int q = min(head + 3 * j, kKvTile - 1);
+      const int q = min(w + kWaves * j, kKvTile - 1);
       const uint32_t key = min(k0 + q, (uint32_t)rows - 1);
-      dma16(ks + (size_t)key * (2 * kHeadDim) + (lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ kswz(q)),
-            lds + s * kStage + q * 1024);
+      const unsigned off = 2u * ((lane >> 5) * kHeadDim + 8 * ((lane & 31) ^ kswz(q)));
+      dma16(ks + (size_t)key * (2 * kHeadDim), off, __builtin_amdgcn_readfirstlane(lds0 + s * kStage + q * 1024));
     };
     auto dma_v = [&](uint32_t k0, int s, int j) {
-      const int q = min(head + 3 * j, kKvTile - 1);
+      const int q = min(w + kWaves * j, kKvTile - 1);
       const int hl = q >> 4, d = 16 * (q & 15) + (lane >> 2), c = (lane & 3) ^ vswz(d);
       const int col = min(col_base + (int)k0, ldv - kKvTile);  // the refill past a sequence stays inside vt
-      dma16(vt + ((size_t)hl * kHeadDim + d) * ldv + col + 8 * c, lds + s * kStage + kKStage + q * 1024);
+      const unsigned off = 2u * (unsigned)(((hl * kHeadDim + d) * ldv) + col + 8 * c);
+      dma16(vt, off, __builtin_amdgcn_readfirstlane(lds0 + s * kStage + kKStage + q * 1024));
     };
-    constexpr int kDmaPerWave = (kKvTile + 2) / 3;  // 11
 
     // Every wave has finished with both stages (previous tile of the grid
     // stride), and every DMA it issued -- including the refill of the idle
@@ -222,11 +238,13 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     // Q^T operand of the score MFMA: lane holds query t, dims 32s + 8grp .. +7
     // for s = 0..7. Rows of qs are [hi 768 | lo 768].
     half8 qh[8], ql[8];
-    const _Float16* qrow = qs + (size_t)t * (2 * kEmbd) + head * kHeadDim;
+    if (compute) {
+      const _Float16* qrow = qs + (size_t)t * (2 * kEmbd) + head * kHeadDim;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      qh[s] = *reinterpret_cast<const half8*>(qrow + 32 * s + 8 * grp);
-      ql[s] = *reinterpret_cast<const half8*>(qrow + kEmbd + 32 * s + 8 * grp);
+      for (int s = 0; s < 8; ++s) {
+        qh[s] = *reinterpret_cast<const half8*>(qrow + 32 * s + 8 * grp);
+        ql[s] = *reinterpret_cast<const half8*>(qrow + kEmbd + 32 * s + 8 * grp);
+      }
     }
 
     floatx4 acc[16];
@@ -240,41 +258,39 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     for (uint32_t k0 = k_first; k0 < kv_hi; k0 += kKvTile, stage ^= 1) {
       // This tile's DMA (and the queries) have landed for every wave, and
       // every wave is done with the other stage, which the next tile's DMA
-      // now refills -- issued in pieces between this tile's MFMAs, so the
-      // memory pipeline's back-pressure overlaps the matrix work.
+      // now refills (on the last tile: a harmless refill of the idle stage).
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
       const uint32_t k1 = k0 + kKvTile;
+      if (!compute) {
+#pragma unroll
+        for (int j = 0; j < kDmaPerWave; ++j) {
+          dma_k(k1, stage ^ 1, j);
+          dma_v(k1, stage ^ 1, j);
+        }
+        continue;
+      }
       const unsigned char* kst = lds + stage * kStage;
       const unsigned char* vst = kst + kKStage;
 
-      // S^T = K . Q^T, two 16-key blocks; the K fragments of step st + 1
-      // are read from LDS while step st multiplies.
+      // S^T = K . Q^T, two 16-key blocks; this wave's share of the next
+      // tile's K rows goes out between the MFMAs.
       floatx4 s0 = floatx4{}, s1 = floatx4{};
       const unsigned char* krow0 = kst + key0 * 1024;
       const unsigned char* krow1 = kst + key1 * 1024;
-      half8 kf[2][4];
-      auto load_k = [&](int st, half8 (&f)[4]) {
-        const int c = 4 * st + grp;
-        f[0] = *reinterpret_cast<const half8*>(krow0 + 16 * (c ^ kf0));
-        f[1] = *reinterpret_cast<const half8*>(krow0 + 512 + 16 * (c ^ kf0));
-        f[2] = *reinterpret_cast<const half8*>(krow1 + 16 * (c ^ kf1));
-        f[3] = *reinterpret_cast<const half8*>(krow1 + 512 + 16 * (c ^ kf1));
-      };
-      load_k(0, kf[0]);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const int cur = st & 1;
-        if (st + 1 < 8) load_k(st + 1, kf[cur ^ 1]);
-        s0 = mfma(kf[cur][0], qh[st], s0);
-        s1 = mfma(kf[cur][2], qh[st], s1);
-        s0 = mfma(kf[cur][0], ql[st], s0);
-        s1 = mfma(kf[cur][2], ql[st], s1);
-        s0 = mfma(kf[cur][1], qh[st], s0);
-        s1 = mfma(kf[cur][3], qh[st], s1);
-        // The next tile's K rows (on the last tile: a harmless refill of
-        // the idle stage).
-        dma_k(k1, stage ^ 1, st);
-        if (st + 8 < kDmaPerWave) dma_k(k1, stage ^ 1, st + 8);
+        const int c = 4 * st + grp;
+        const half8 ah = *reinterpret_cast<const half8*>(krow0 + 16 * (c ^ kf0));
+        const half8 al = *reinterpret_cast<const half8*>(krow0 + 512 + 16 * (c ^ kf0));
+        const half8 bh = *reinterpret_cast<const half8*>(krow1 + 16 * (c ^ kf1));
+        const half8 bl = *reinterpret_cast<const half8*>(krow1 + 512 + 16 * (c ^ kf1));
+        s0 = mfma(ah, qh[st], s0);
+        s1 = mfma(bh, qh[st], s1);
+        s0 = mfma(ah, ql[st], s0);
+        s1 = mfma(bh, ql[st], s1);
+        s0 = mfma(al, qh[st], s0);
+        s1 = mfma(bl, qh[st], s1);
+        if (st < kDmaPerWave) dma_k(k1, stage ^ 1, st);
       }
       // sc[4kb + v] = 16 x the score of key k0 + 8grp + 4kb + v, taken to
       // log2 units: exp(x) = exp2(x * log2e).
@@ -321,33 +337,28 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       }
 
       // O^T += V^T . P^T: lane group grp supplies keys 8grp..8grp+7, V^T chunk
-      // grp. Dimension blocks go in pairs: the V^T fragments of the next pair
-      // are read while this pair multiplies, and each accumulator's three
-      // MFMAs (hi.hi, hi.lo, lo.hi, in that order) alternate with the other's.
-      half8 vf[2][4];
-      auto load_v = [&](int pr, half8 (&f)[4]) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int d = 16 * (2 * pr + i) + qi, c = grp ^ vswz(d);
-          f[2 * i] = *reinterpret_cast<const half8*>(vst + d * 64 + 16 * c);
-          f[2 * i + 1] = *reinterpret_cast<const half8*>(vst + (kHeadDim + d) * 64 + 16 * c);
-        }
-      };
-      load_v(0, vf[0]);
+      // grp; each accumulator's three MFMAs (hi.hi, hi.lo, lo.hi, in that
+      // order) alternate with the next block's. This wave's share of the
+      // next tile's V^T rows goes out between them.
 #pragma unroll
       for (int pr = 0; pr < 8; ++pr) {
-        const int cur = pr & 1, d0 = 2 * pr, d1 = 2 * pr + 1;
-        if (pr + 1 < 8) load_v(pr + 1, vf[cur ^ 1]);
-        acc[d0] = mfma(vf[cur][0], ph, acc[d0]);
-        acc[d1] = mfma(vf[cur][2], ph, acc[d1]);
-        acc[d0] = mfma(vf[cur][0], pl, acc[d0]);
-        acc[d1] = mfma(vf[cur][2], pl, acc[d1]);
-        acc[d0] = mfma(vf[cur][1], ph, acc[d0]);
-        acc[d1] = mfma(vf[cur][3], ph, acc[d1]);
-        dma_v(k1, stage ^ 1, pr);
-        if (pr + 8 < kDmaPerWave) dma_v(k1, stage ^ 1, pr + 8);
+        const int d0 = 2 * pr, d1 = 2 * pr + 1;
+        const int e0 = 16 * d0 + qi, e1 = 16 * d1 + qi;
+        const int c0 = grp ^ vswz(e0), c1 = grp ^ vswz(e1);
+        const half8 vh0 = *reinterpret_cast<const half8*>(vst + e0 * 64 + 16 * c0);
+        const half8 vl0 = *reinterpret_cast<const half8*>(vst + (kHeadDim + e0) * 64 + 16 * c0);
+        const half8 vh1 = *reinterpret_cast<const half8*>(vst + e1 * 64 + 16 * c1);
+        const half8 vl1 = *reinterpret_cast<const half8*>(vst + (kHeadDim + e1) * 64 + 16 * c1);
+        acc[d0] = mfma(vh0, ph, acc[d0]);
+        acc[d1] = mfma(vh1, ph, acc[d1]);
+        acc[d0] = mfma(vh0, pl, acc[d0]);
+        acc[d1] = mfma(vh1, pl, acc[d1]);
+        acc[d0] = mfma(vl0, ph, acc[d0]);
+        acc[d1] = mfma(vl1, ph, acc[d1]);
+        if (pr < kDmaPerWave) dma_v(k1, stage ^ 1, pr);
       }
     }
+    if (!compute) continue;
 
     if (slot == kNoSlot) {
       store_blocks<8>(acc, l_run, t, active, head, grp, rows, 0, cq, cd);
@@ -374,7 +385,7 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 // deterministic order that depends only on the sequence), then the same
 // epilogue as an unsplit tile. Every load of a wave is issued before its
 // first use: the (m, l) pairs of all parts, then all parts' 4 x 16 bytes.
-constexpr int kMaxParts = (kCtx + kChunkKeys - 1) / kChunkKeys;  // 8
+constexpr int kMaxParts = kMaxChunks;
 __global__ void __launch_bounds__(192)
 attention_merge_kernel(const uint4* __restrict__ merges, const uint32_t* __restrict__ merge_count,
                        const float* __restrict__ partials, int rows, int8_t* __restrict__ cq,
@@ -423,14 +434,22 @@ attention_merge_kernel(const uint4* __restrict__ merges, const uint32_t* __restr
 }
 
 // Key chunks of a sequence of length n: one when n <= kSplitLen, else
-// ceil(n / kChunkKeys). Depends only on n, so a sequence is computed the
-// same way wherever it sits in a wave.
-static size_t key_chunks(size_t n) { return n <= kSplitLen ? 1 : (n + kChunkKeys - 1) / kChunkKeys; }
+// min(ceil(n / kSplitLen), kMaxChunks) chunks of chunk_keys(n) keys (a
+// multiple of 32, so key tiles stay aligned to the sequence start; the last
+// chunk takes the rest). Both depend only on n, so a sequence is computed
+// the same way wherever it sits in a wave.
+static size_t key_chunks(size_t n) {
+  return n <= kSplitLen ? 1 : std::min<size_t>((n + kSplitLen - 1) / kSplitLen, kMaxChunks);
+}
+static size_t chunk_keys(size_t n) {
+  const size_t c = key_chunks(n), per = (n + c - 1) / c;
+  return (per + kKvTile - 1) / kKvTile * kKvTile;
+}
 
 AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges) {
   AttentionCounts c{0, 0, 0};
   for (size_t s = 0; s < batch; ++s) {
-    const size_t lo = offsets[s], hi = offsets[s + 1], chunks = key_chunks(hi - lo);
+    const size_t lo = offsets[s], hi = offsets[s + 1], chunks = key_chunks(hi - lo), ck = chunk_keys(hi - lo);
     for (size_t q = lo; q < hi; q += kQTile) {
       const size_t e = q + kQTile < hi ? q + kQTile : hi;
       if (chunks > 1) {
@@ -446,8 +465,8 @@ AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint3
         it[1] = (uint32_t)e;
         it[2] = (uint32_t)lo;
         it[3] = (uint32_t)hi;
-        it[4] = (uint32_t)(chunks > 1 ? lo + k * kChunkKeys : lo);
-        it[5] = (uint32_t)(chunks > 1 ? std::min(hi, lo + (k + 1) * kChunkKeys) : hi);
+        it[4] = (uint32_t)(chunks > 1 ? lo + k * ck : lo);
+        it[5] = (uint32_t)(chunks > 1 ? std::min(hi, lo + (k + 1) * ck) : hi);
         it[6] = chunks > 1 ? c.slots++ : kNoSlot;
         it[7] = 0;
       }
@@ -482,7 +501,7 @@ hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float
                             const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
                             int8_t* cq, float* cd, float* partials, hipStream_t st) {
   if (rows <= 0 || grid <= 0 || ldv <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(192), 0, st, qs, ks, vt, ldv, vcol,
+  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(64 * kWaves), 0, st, qs, ks, vt, ldv, vcol,
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd, partials);
   return hipGetLastError();
 }

@@ -88,10 +88,11 @@ int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count,
 /* Host: the work lists of a packed wave with sequences [offsets[s],
  * offsets[s+1]): per query tile of up to 16 tokens one item per key chunk
  * {first query, end, sequence start, sequence end, chunk start, chunk end,
- * slot or 0xFFFFFFFF, 0} (a sequence of n > 256 tokens has ceil(n / 256)
- * chunks, partial slots numbered consecutively; shorter ones one chunk and
- * no slot), and per split tile one merge record {first query, end, first
- * slot, parts}. counts[0..2] = items, merges, slots. `items` needs room for
+ * slot or 0xFFFFFFFF, 0} (a sequence of n > 256 tokens has c = min(ceil(n
+ * / 256), 4) chunks of ceil(n / c) keys rounded up to 32, the last one
+ * taking the rest, partial slots numbered consecutively; shorter ones one
+ * chunk and no slot), and per split tile one merge record {first query,
+ * end, first slot, parts}. counts[0..2] = items, merges, slots. `items` needs room for
  * 8 * (offsets[batch] + batch) entries, `merges` for 4 * ceil(offsets[batch]
  * / 16). Returns the item count. */
 unsigned eg2_attention_items(const size_t *offsets, size_t batch, uint32_t *items, uint32_t *merges, unsigned *counts);

@@ -88,23 +88,26 @@ def test_vt_columns_align_each_sequence(eg2):
 
 def test_attention_items_cover_each_sequence(eg2):
     """Every (query, key) pair of a sequence is covered by exactly one item;
-    query tiles are 16 tokens from the sequence start; a sequence longer than
-    256 tokens splits its keys into 256-key chunks (aligned to its start)
-    with consecutive partial slots and one merge record per query tile."""
-    offs = [0, 1, 33, 97, 98, 200, 600, 1100]
+    query tiles are 16 tokens from the sequence start; a sequence of n > 256
+    tokens splits its keys into c = min(ceil(n / 256), 4) chunks of
+    ceil(n / c) keys rounded up to 32 (aligned to its start) with
+    consecutive partial slots and one merge record per query tile."""
+    offs = [0, 1, 33, 97, 98, 200, 600, 1100, 3150]
     items, merges, slots = eg2.attention_items(offs)
     seqs = [(offs[s], offs[s + 1]) for s in range(len(offs) - 1)]
     covered = {s: np.zeros((hi - lo, hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
     used_slots = []
-    for q0, q1, lo, hi, k0, k1, slot, zero in items:
+    for q0, q1, lo, hi, k0, k1, slot, zero in items.astype(np.int64):
         s = seqs.index((lo, hi))
         assert lo <= q0 < q1 <= hi and q1 - q0 <= 16 and (q0 - lo) % 16 == 0 and zero == 0
-        assert lo <= k0 < k1 <= hi and (k0 - lo) % 256 == 0
         n = hi - lo
+        c = min(-(-n // 256), 4)
+        ck = -(-(-(-n // c)) // 32) * 32
+        assert lo <= k0 < k1 <= hi and (k0 - lo) % ck == 0 and (k0 - lo) % 32 == 0
         if n <= 256:
             assert (k0, k1, slot) == (lo, hi, 0xFFFFFFFF)
         else:
-            assert k1 - k0 == min(256, hi - k0)
+            assert k1 - k0 == min(ck, hi - k0)
             used_slots.append(int(slot))
         covered[s][q0 - lo:q1 - lo, k0 - lo:k1 - lo] += 1
     assert all((c == 1).all() for c in covered.values())
@@ -112,9 +115,9 @@ def test_attention_items_cover_each_sequence(eg2):
     # merges: one per query tile of a split sequence, slots first..first+parts-1
     split = [(lo, hi) for lo, hi in seqs if hi - lo > 256]
     assert len(merges) == sum((hi - lo + 15) // 16 for lo, hi in split)
-    for q0, q1, first, parts in merges:
+    for q0, q1, first, parts in merges.astype(np.int64):
         lo, hi = next((lo, hi) for lo, hi in split if lo <= q0 < hi)
-        assert parts == (hi - lo + 255) // 256
+        assert parts == min((hi - lo + 255) // 256, 4)
         tile_items = [it for it in items if it[0] == q0]
         assert sorted(int(it[6]) for it in tile_items) == list(range(first, first + parts))
 
