@@ -254,6 +254,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stream-requests", type=int, default=1000,
                     help="requests in the dynamic-batching stream measurement (0 skips it)")
+    ap.add_argument("--no-kernel-table", action="store_true",
+                    help="skip the per-kernel table (keeps a kernel trace to the forward and the roofline GEMM)")
     ap.add_argument("--kernel-only", choices=["gate_up", "copy", "table"],
                     help="run only the dominant GEMM (or the copy calibration kernel) for counter runs, "
                          "or only the per-kernel table")
@@ -319,7 +321,7 @@ def main():
         flops = 2.0 * GEMM_N * GEMM_M * GEMM_K
         achieved = flops / (gemm_ms / 1e3) / 1e12
         log(f"gate|up GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s")
-        kernels = kernel_table(eg2, torch, max(20, args.steps))
+        kernels = {} if args.no_kernel_table else kernel_table(eg2, torch, max(20, args.steps))
         for name, k in kernels.items():
             log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak")
 

@@ -69,7 +69,7 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * (device) items; `grid` workgroups stride over it. An item whose slot is
  * 0xFFFFFFFF quantizes its fp32 context to Q8_0 (quants.c:97-177) into cq
  * (row tiles, k = 768) and cd [24][rows]; the items of a sequence longer
- * than 256 tokens cover 256-key chunks and write partial results to
+ * than 256 tokens cover up to four key chunks and write partial results to
  * `partials` (eg2_attention_partial_floats() floats per slot), which
  * eg2_hip_attention_merge then combines and quantizes. A sequence's result
  * does not depend on its place in the wave.
