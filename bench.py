@@ -11,7 +11,8 @@ token ids uniform in [0, 262144), seed 0.
 A step is one forward of that wave with its inputs already resident in HBM
 (ids and packing metadata staged once); value = 2048 tokens / step time.
 The roofline entry times the dominant kernel (the gate|up projection GEMM,
-2048 x 2304 x 768) with HIP events on the stream it runs on. The CPU
+2048 x 2304 x 768, with the GeGLU and its Q8_0 quantization in its
+epilogue) with HIP events on the stream it runs on. The CPU
 baseline is the oracle (the C restatement of the reference CPU path) on the
 same wave, timed on the host's cores.
 """
@@ -80,14 +81,23 @@ def gemm_operands(eg2, torch, n, m, k, g):
     return xq, xd, wq, wd, y
 
 
+def geglu_outputs(eg2, torch, n, ff):
+    """Q8_0 output buffers of the fused gate|up + GeGLU GEMM."""
+    dev = torch.device("cuda:0")
+    return (torch.zeros(eg2.q8_tile_bytes(n, ff), dtype=torch.int8, device=dev),
+            torch.zeros((ff // 32, n), dtype=torch.float32, device=dev))
+
+
 def time_gemm(eg2, torch, steps, warmup):
-    """Average duration of the gate|up projection GEMM (one launch)."""
+    """Average duration of the forward's dominant kernel, the fused gate|up
+    projection GEMM + GeGLU + Q8_0 (one launch)."""
     import numpy as np
 
     g = torch.Generator(device="cpu").manual_seed(0)
-    xq, xd, wq, wd, y = gemm_operands(eg2, torch, GEMM_N, GEMM_M, GEMM_K, g)
-    ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, warmup)
-    assert np.isfinite(y[:4, :4].cpu().numpy()).all()
+    xq, xd, wq, wd, _ = gemm_operands(eg2, torch, GEMM_N, GEMM_M, GEMM_K, g)
+    gq, gd = geglu_outputs(eg2, torch, GEMM_N, GEMM_M // 2)
+    ms = time_launches(torch, lambda: eg2.ops.gemm_q8_geglu(xq, xd, wq, wd, gq, gd, GEMM_N), steps, warmup)
+    assert np.isfinite(gd.cpu().numpy()).all()
     return ms
 
 
@@ -111,9 +121,13 @@ def kernel_table(eg2, torch, steps):
                      "frac": round(rate / peak, 4)}
 
     for name, (m, k) in {"gemm_qkv 2048x1280x768": (1280, E), "gemm_o 2048x768x768": (E, E),
-                         "gemm_gate_up 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
+                         "gemm_gate_up_geglu 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
         xq, xd, wq, wd, y = gemm_operands(eg2, torch, T, m, k, g)
-        ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
+        if "geglu" in name:
+            gq, gd = geglu_outputs(eg2, torch, T, F)
+            ms = time_launches(torch, lambda: eg2.ops.gemm_q8_geglu(xq, xd, wq, wd, gq, gd, T), steps, 3)
+        else:
+            ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
         rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS)
 
     rnd = lambda *shape: torch.randn(*shape, generator=g).to(dev)
@@ -124,9 +138,6 @@ def kernel_table(eg2, torch, steps):
     xd = torch.zeros((F // 32, T), device=dev)
     ms = time_launches(torch, lambda: eg2.ops.residual_norm_quant(x, h, w_e, w_e, 1e-6, xq, xd), steps, 3)
     rec("residual_norm_quant", ms, T * (3 * 4 * E + E + 4 * E // 32), "GB/s", PEAK_HBM_GBS)
-    gu = rnd(T, 2 * F)
-    ms = time_launches(torch, lambda: eg2.ops.gelu_quant(gu, xq, xd), steps, 3)
-    rec("gelu_quant", ms, T * (4 * 2 * F + F + 4 * F // 32), "GB/s", PEAK_HBM_GBS)
     vocab = 4096
     table = np.zeros((vocab, 24, 34), np.uint8)
     table[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
@@ -158,11 +169,11 @@ def kernel_table(eg2, torch, steps):
     return out
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q8_gate_up_2048x2304x768_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q8_geglu_gate_up_2048x2304x768_traffic.md")
 
 
 def measured_traffic():
-    """HBM bytes per launch of the gate|up GEMM from the committed rocprofv3
+    """HBM bytes per launch of the gate|up + GeGLU GEMM from the committed rocprofv3
     counter summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), or
     None when that summary is absent."""
     if not os.path.exists(TRAFFIC_PROFILE):
@@ -181,7 +192,7 @@ def measured_traffic():
 
 
 def kernel_only(kind, steps):
-    """Counter-collection mode: only the gate|up GEMM, or a plain device copy
+    """Counter-collection mode: only the gate|up + GeGLU GEMM, or a plain device copy
     of COPY_MIB (the calibration kernel for FETCH_SIZE/WRITE_SIZE), or only
     the per-kernel table of one layer."""
     import torch
@@ -194,7 +205,7 @@ def kernel_only(kind, steps):
         print(json.dumps(kernel_table(eg2, torch, steps)))
     elif kind == "gate_up":
         ms = time_gemm(eg2, torch, steps, 2)
-        print(json.dumps({"kernel": "gemm_q8 gate|up 2048x2304x768", "avg_us": round(ms * 1e3, 2), "launches": steps + 2}))
+        print(json.dumps({"kernel": "gemm_q8_geglu gate|up 2048x2304x768", "avg_us": round(ms * 1e3, 2), "launches": steps + 2}))
     else:
         src = torch.empty(COPY_MIB << 18, dtype=torch.float32, device="cuda:0").uniform_()
         dst = torch.empty_like(src)
@@ -320,7 +331,7 @@ def main():
         gemm_ms = time_gemm(eg2, torch, max(20, args.steps), 5)
         flops = 2.0 * GEMM_N * GEMM_M * GEMM_K
         achieved = flops / (gemm_ms / 1e3) / 1e12
-        log(f"gate|up GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s")
+        log(f"gate|up + GeGLU GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s")
         kernels = {} if args.no_kernel_table else kernel_table(eg2, torch, max(20, args.steps))
         for name, k in kernels.items():
             log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak")
@@ -354,7 +365,7 @@ def main():
                                "packed wave of 16x128 tokens", "tokens_per_wave": TOKENS, "sequences": SEQS,
                    "layers": LAYERS, "hidden": 768, "ffn": 1152, "heads": "3q/1kv x 256", "weights": "Q8_0",
                    "attention": "full within sequence, RoPE base 1e4"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_q8 gate|up 2048x2304x768 (v_mfma_i32_32x32x32_i8; "
+        "roofline": {"bound": "mfma", "kernel": "gemm_q8_geglu gate|up 2048x2304x768 + GeGLU + Q8_0 (v_mfma_i32_32x32x32_i8; "
                                                 "achieved/peak in T int8 op/s)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),

@@ -105,6 +105,49 @@ __device__ __forceinline__ Q8Lane q8_quantize_lane(float x) {
   return r;
 }
 
+// quants.c:97-177 (scalar path) on one block spread over P adjacent lanes
+// (lanes P*i .. P*i+P-1, all active), each holding N = 32/P consecutive
+// values: amax, d = amax/127 stored as fp16 (round-half-up), id = 1/d,
+// q = roundf(v*id) clamped; an all-zero block stores d = 0 and q = 0. Each
+// lane writes its N int8 values at q (N-byte aligned, consecutive in the
+// row-tile layout since N <= 16); the first lane of the group writes the
+// float value of the stored scale.
+template <int P>
+__device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], bool store, int8_t* __restrict__ q,
+                                                    float* __restrict__ d_out) {
+  constexpr int N = kQK / P;
+  static_assert(N == 8 || N == 16, "8 or 16 values per lane");
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int m = 1; m < P; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  const float d = amax / 127.0f;
+  const float id = amax != 0.0f ? 1.0f / d : 0.0f;
+  if (!store) return;
+  if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+  int32_t qi[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) qi[i] = amax != 0.0f ? q8_round(v[i] * id) : 0;
+  uint32_t w[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) w[i] = pack_i8x4(qi[4 * i], qi[4 * i + 1], qi[4 * i + 2], qi[4 * i + 3]);
+  if constexpr (N == 16)
+    *reinterpret_cast<uint4*>(q) = make_uint4(w[0], w[1], w[2], w[3]);
+  else
+    *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
+}
+
+// kernels.c:367-371 gelu_tanh(g) times u (engine.c's GeGLU), with the
+// device tanhf, in the order written.
+__device__ __forceinline__ float gelu_mul(float g, float u) {
+  const float a = 0.044715f;
+  const float s = 0.79788456080286535587989211986876f;
+  const float inner = s * g * (1.0f + a * g * g);
+  const float gelu = 0.5f * g * (1.0f + tanhf(inner));
+  return gelu * u;
+}
+
 // Sum of squares of an LDS row of n floats (n % 8 == 0) in the reference's
 // SSE2 order (kernels.c:82-94): lane c < 8 runs the sequential chain over
 // x[8t + c] (lanes 0-3 are the first 4-lane accumulator, 4-7 the second),

@@ -27,6 +27,8 @@ hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t
 // xd/wd: their block scales transposed, [k/32][ldx] and [k/32][ldw].
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
+hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
+                                int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st);
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
                             const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
                             int8_t* cq, float* cd, float* partials, hipStream_t st);

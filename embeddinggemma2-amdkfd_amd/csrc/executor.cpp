@@ -5,8 +5,9 @@
 // `gemma-embedding` hyper-parameters and tensors from the caller's ei_gguf
 // (model.c:61-105 names, Q8_0 matrices), repack every matrix once into the
 // projection GEMM's operand layout (the int8 values as row tiles + the
-// block scales transposed, see eg2_q8_weight_tiles), fuse Q|K|V and
-// gate|up into single projections, upload the raw Q8_0
+// block scales transposed, see eg2_q8_weight_tiles), fuse Q|K|V into one
+// projection and gate|up (interleaved in 32-row groups) into the operand of
+// the fused gate|up + GeGLU GEMM, upload the raw Q8_0
 // embedding table, build the RoPE tables on the host, and allocate a
 // 2048-token workspace.
 //
@@ -107,7 +108,7 @@ class Backend {
   bool dense_ = false;
 
   // Workspace for kCap tokens.
-  float *x_, *h_, *qkv_, *gu_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
+  float *x_, *h_, *qkv_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
   int8_t *xq_, *cq_, *mid_q_;
   _Float16 *qs_, *ks_, *vt_;
   int32_t *ids_d_, *pos_d_, *vcol_d_;
@@ -148,6 +149,7 @@ class Backend {
   const float* upload_vector(const std::string& name, int n);
   std::vector<uint8_t> q8_rows(const std::string& name, int k, int m) const;
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
+  DevMat upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k);
   void launch(const char* name, hipError_t e);
   void record_layers(unsigned rows, bool merge);
   void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
@@ -235,6 +237,25 @@ DevMat Backend::upload_q8(const std::vector<const std::vector<uint8_t>*>& parts,
   return mat;
 }
 
+// The gate and up matrices interleaved in 32-row groups, the operand of
+// the fused gate|up + GeGLU GEMM.
+DevMat Backend::upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k) {
+  const size_t ff = gate.size() / ((size_t)(k / 32) * 34);
+  DevMat mat;
+  mat.m = (int)(2 * ff);
+  mat.k = k;
+  mat.ld = mat.m;
+  std::vector<int8_t> q(eg2_q8_tile_bytes(2 * ff, (unsigned)k));
+  std::vector<float> d((size_t)(k / 32) * mat.ld);
+  if (up.size() != gate.size() || eg2_q8_geglu_weight_tiles(gate.data(), up.data(), ff, (unsigned)k, q.data(), d.data()))
+    throw std::runtime_error("ffn_gate / ffn_up shapes");
+  mat.q = dalloc<int8_t>(q.size());
+  mat.d = dalloc<float>(d.size());
+  check(hipMemcpy(mat.q, q.data(), q.size(), hipMemcpyHostToDevice), "upload");
+  check(hipMemcpy(mat.d, d.data(), d.size() * sizeof(float), hipMemcpyHostToDevice), "upload");
+  return mat;
+}
+
 Backend::Backend(const ei_gguf* g) : model_(g) {
   if (!g || !g->tensors) throw std::runtime_error("empty GGUF");
   char why[256];
@@ -298,7 +319,7 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
     auto wo = q8_rows(p + "attn_output.weight", 768, kEmbd);
     L.o = upload_q8({&wo}, 768);
     auto wg = q8_rows(p + "ffn_gate.weight", kEmbd, kFF), wu = q8_rows(p + "ffn_up.weight", kEmbd, kFF);
-    L.gu = upload_q8({&wg, &wu}, kEmbd);
+    L.gu = upload_q8_geglu(wg, wu, kEmbd);
     auto wd = q8_rows(p + "ffn_down.weight", kFF, kEmbd);
     L.down = upload_q8({&wd}, kFF);
     L.attn_norm = upload_vector(p + "attn_norm.weight", kEmbd);
@@ -327,7 +348,6 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   x_ = dalloc<float>((size_t)kCap * kEmbd);
   h_ = dalloc<float>((size_t)kCap * kEmbd);
   qkv_ = dalloc<float>((size_t)kCap * kQKV);
-  gu_ = dalloc<float>((size_t)kCap * 2 * kFF);
   xq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kFF));
   xd_ = dalloc<float>((size_t)kCap * (kFF / 32));
   cq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
@@ -392,8 +412,9 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
 // then per layer (engine.c:1115-1127 order) QKV GEMM, QK-norm/RoPE,
 // attention (+Q8_0; with `merge`, the merge of split sequences' key-chunk
-// partials), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM, GeGLU
-// (+Q8_0), down GEMM, residual + next attn_norm (+Q8_0); finally the
+// partials), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM with the
+// GeGLU (+Q8_0) in its epilogue, down GEMM, residual + next attn_norm
+// (+Q8_0); finally the
 // output_norm per token (the first half of kernels.c:417-427).
 void Backend::record_layers(unsigned rows, bool merge) {
   hipStream_t s = stream_;
@@ -411,9 +432,11 @@ void Backend::record_layers(unsigned rows, bool merge) {
       launch("attention_merge",
              eg2::launch_attention_merge(merges_d_, counts_d_ + 1, (n + 3) / 4, partials_, n, cq_, cd_, s));
     gemm("gemm_o", cq_, cd_, L.o, h_, n, kEmbd, s);
-    launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, xq_, xd_, n, s));
-    gemm("gemm_gate_up", xq_, xd_, L.gu, gu_, n, 2 * kFF, s);
-    launch("gelu", eg2::launch_gelu_quant(gu_, xq_, xd_, n, s));
+    // The FFN input goes to the attention context's buffers (free after the
+    // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.
+    launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, cq_, cd_, n, s));
+    launch("gemm_gate_up_geglu", eg2::launch_gemm_q8_geglu(cq_, cd_, n, L.gu.q, L.gu.d, L.gu.ld, xq_, xd_, n, n, kFF,
+                                                            kEmbd, s));
     gemm("gemm_down", xq_, xd_, L.down, h_, n, kEmbd, s);
     const float* next = il + 1 < layers_.size() ? layers_[il + 1].attn_norm : nullptr;
     launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_ffw, next, eps_, xq_, xd_, n, s));

@@ -100,12 +100,53 @@ __device__ __forceinline__ void scale_accumulate(floatx16& acc, const intx16& bi
   ((acc[V] = acc[V] + t[V]), ...);
 }
 
+constexpr int kGPitch = 40;  // floats per row of the GeGLU epilogue's transposed tile
+
+// GeGLU epilogue (kernels.c:367-391, engine.c's gelu(gate) * up then the
+// Q8_0 quantization of the down projection's input). The weight rows are
+// interleaved in 32-row groups (gate group j, then up group j), so output
+// tile tc holds gate columns 32 tc .. 32 tc + 31 in its waves wc = 0 and
+// the matching up columns in its waves wc = 1, and its 32 GeGLU outputs per
+// row are exactly Q8_0 block tc. The two waves of a row pair swap half of
+// their results through LDS (the gate wave finishes rows 0-15 of the pair,
+// the up wave rows 16-31), transpose them so that four lanes hold one
+// row's block, and quantize with the same code as the standalone GeGLU
+// kernel: the int8 values go to gq in the row-tile layout (nbf blocks per
+// row), the scales to gd[tc * ldg + row].
+__device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int tc, int wr, int wc, int n, int nbf,
+                                               int8_t* __restrict__ gq, float* __restrict__ gd, int ldg) {
+  const int lane = threadIdx.x & 63, g = lane >> 5;
+  // The ring is free once every wave is past its last fragment reads.
+  __syncthreads();
+  float* xch = reinterpret_cast<float*>(gemm_lds) + wr * 1024;                  // [2][8][64]
+  float* tp = reinterpret_cast<float*>(gemm_lds) + 2048 + wr * 32 * kGPitch;  // [32][kGPitch]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xch[(wc * 8 + i) * 64 + lane] = wc ? acc[i] : acc[8 + i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float other = xch[((wc ^ 1) * 8 + i) * 64 + lane];
+    const float gate = wc ? other : acc[i], up = wc ? acc[8 + i] : other;
+    // register v = 8 wc + i of the 32x32 output layout: row 8 (v >> 2) + 4 g + (v & 3), column lane & 31
+    tp[(16 * wc + 8 * (i >> 2) + 4 * g + (i & 3)) * kGPitch + (lane & 31)] = gelu_mul(gate, up);
+  }
+  __syncthreads();
+  const int rr = 16 * wc + (lane >> 2), part = lane & 3;
+  const float4 lo = *reinterpret_cast<const float4*>(tp + rr * kGPitch + 8 * part);
+  const float4 hi = *reinterpret_cast<const float4*>(tp + rr * kGPitch + 8 * part + 4);
+  const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  const int t = 64 * tr + 32 * wr + rr;
+  quantize_block_part<4>(v, t < n, gq + q8_tile_offset(t, 32 * tc + 8 * part, nbf), gd + (size_t)tc * ldg + t);
+}
+
 // TAIL: nb % kStages != 0 (a separate instantiation: the tail code costs
-// registers, and every projection of the model has nb % 4 == 0).
-template <bool TAIL>
+// registers, and every projection of the model has nb % 4 == 0). GEGLU:
+// the epilogue above replaces the fp32 store (y and ldy unused; m = 2 ff).
+template <bool TAIL, bool GEGLU>
 __global__ void __launch_bounds__(256)
 gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx, const int8_t* __restrict__ wq,
-               const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy) {
+               const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy,
+               int8_t* __restrict__ gq, float* __restrict__ gd) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tr_count = (n + 63) / 64, tc_count = (m + 63) / 64, tiles = tr_count * tc_count;
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes one
@@ -203,11 +244,15 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   // The ring's last refills are redundant; they must land before the
   // workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const int col = 64 * tc + 32 * wc + (lane & 31);
+  if constexpr (GEGLU) {
+    geglu_epilogue(acc, tr, tc, wr, wc, n, m / 64, gq, gd, ldy);
+  } else {
+    const int col = 64 * tc + 32 * wc + (lane & 31);
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int row = 64 * tr + 32 * wr + 8 * (v >> 2) + 4 * g + (v & 3);
-    if (row < n && col < m) y[(size_t)row * ldy + col] = acc[v];
+    for (int v = 0; v < 16; ++v) {
+      const int row = 64 * tr + 32 * wr + 8 * (v >> 2) + 4 * g + (v & 3);
+      if (row < n && col < m) y[(size_t)row * ldy + col] = acc[v];
+    }
   }
 }
 
@@ -218,11 +263,29 @@ hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8
   const dim3 grid(((tiles + kXcds - 1) / kXcds) * kXcds);
   const int nb = k / kQK;
   if (nb % kStages == 0)
-    hipLaunchKernelGGL(gemm_q8_kernel<false>, grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd, ldw, y,
-                       n, m, nb, ldy);
+    hipLaunchKernelGGL((gemm_q8_kernel<false, false>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
+                       ldw, y, n, m, nb, ldy, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(gemm_q8_kernel<true>, grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd, ldw, y,
-                       n, m, nb, ldy);
+    hipLaunchKernelGGL((gemm_q8_kernel<true, false>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
+                       ldw, y, n, m, nb, ldy, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
+                                int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st) {
+  const int m = 2 * ff;
+  if (n <= 0 || ff <= 0 || ff % kQK != 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < m || ldg < n)
+    return hipErrorInvalidValue;
+  const int tiles = ((n + 63) / 64) * (m / 64);
+  const dim3 grid(((tiles + kXcds - 1) / kXcds) * kXcds);
+  const int nb = k / kQK;
+  static_assert(2 * 1024 + 2 * 32 * kGPitch <= kStages * kStageBytes / 4, "GeGLU epilogue fits in the ring");
+  if (nb % kStages == 0)
+    hipLaunchKernelGGL((gemm_q8_kernel<false, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
+                       ldw, nullptr, n, m, nb, ldg, gq, gd);
+  else
+    hipLaunchKernelGGL((gemm_q8_kernel<true, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
+                       ldw, nullptr, n, m, nb, ldg, gq, gd);
   return hipGetLastError();
 }
 

@@ -169,39 +169,6 @@ __device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int 
   }
 }
 
-// quants.c:97-177 (scalar path) on one block spread over P adjacent lanes
-// (lanes P*i .. P*i+P-1, all active), each holding N = 32/P consecutive
-// values: amax, d = amax/127 stored as fp16 (round-half-up), id = 1/d,
-// q = roundf(v*id) clamped; an all-zero block stores d = 0 and q = 0. Each
-// lane writes its N int8 values at q (N-byte aligned, consecutive in the
-// row-tile layout since N <= 16); the first lane of the group writes the
-// float value of the stored scale.
-template <int P>
-__device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], bool store, int8_t* __restrict__ q,
-                                                    float* __restrict__ d_out) {
-  constexpr int N = kQK / P;
-  static_assert(N == 8 || N == 16, "8 or 16 values per lane");
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-  for (int m = 1; m < P; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-  const float d = amax / 127.0f;
-  const float id = amax != 0.0f ? 1.0f / d : 0.0f;
-  if (!store) return;
-  if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
-  int32_t qi[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) qi[i] = amax != 0.0f ? q8_round(v[i] * id) : 0;
-  uint32_t w[N / 4];
-#pragma unroll
-  for (int i = 0; i < N / 4; ++i) w[i] = pack_i8x4(qi[4 * i], qi[4 * i + 1], qi[4 * i + 2], qi[4 * i + 3]);
-  if constexpr (N == 16)
-    *reinterpret_cast<uint4*>(q) = make_uint4(w[0], w[1], w[2], w[3]);
-  else
-    *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
-}
-
 // engine.c:288-295 + kernels.c:139-151 (the first projection's input):
 // x = (fp16(d) * sqrt(768)) * q from the raw GGUF Q8_0 row of token_embd,
 // then the layer-0 attn_norm RMSNorm quantized to Q8_0.
@@ -381,8 +348,6 @@ gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* 
   const int t = jb / kB, b = jb - t * kB, e0 = b * kQK + (j & 3) * 8;
   const float* g = gu + (size_t)t * (2 * kFF) + e0;
   const float* u = g + kFF;
-  const float a = 0.044715f;
-  const float s = 0.79788456080286535587989211986876f;
   float v[8];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -391,10 +356,7 @@ gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* 
     const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const float x = gs[c];
-      const float inner = s * x * (1.0f + a * x * x);
-      const float gelu = 0.5f * x * (1.0f + tanhf(inner));
-      v[4 * i + c] = gelu * us[c];
+      v[4 * i + c] = gelu_mul(gs[c], us[c]);
     }
   }
   quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + q8_tile_offset(t, e0, kB), gd + (size_t)b * n_rows + t);

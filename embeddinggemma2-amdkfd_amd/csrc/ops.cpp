@@ -139,6 +139,18 @@ int eg2_hip_gemm_q8(const int8_t* xq, const float* xd, unsigned ldx, const int8_
                                   as_stream(stream)));
 }
 
+int eg2_hip_gemm_q8_geglu(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd,
+                          unsigned ldw, int8_t* gq, float* gd, unsigned ldg, unsigned n, unsigned ff, unsigned k,
+                          void* stream) {
+  constexpr unsigned kMax = 1u << 24;
+  if (!xq || !xd || !wq || !wd || !gq || !gd || n == 0 || ff == 0 || ff % 32 != 0 || k == 0 || k % 32 != 0 ||
+      ldx < n || ldg < n || n > kMax || ff > kMax / 2 || ldw < 2 * ff || k > kMax || ldx > kMax || ldw > kMax ||
+      ldg > kMax)
+    return kInvalid;
+  return code(eg2::launch_gemm_q8_geglu(xq, xd, (int)ldx, wq, wd, (int)ldw, gq, gd, (int)ldg, (int)n, (int)ff, (int)k,
+                                        as_stream(stream)));
+}
+
 const char* eg2_hip_error_string(int c) { return hipGetErrorString((hipError_t)c); }
 
 int eg2_hip_device_check(char* err, size_t len) {
@@ -184,6 +196,18 @@ void eg2_q8_weight_tiles(const void* blocks, size_t rows, unsigned k, int8_t* wq
       for (unsigned i = 0; i < 32; ++i)
         wq[eg2::q8_tile_offset(r, 32 * b + i, nb)] = blk ? (int8_t)blk[2 + i] : 0;
     }
+}
+
+int eg2_q8_geglu_weight_tiles(const void* gate, const void* up, size_t ff, unsigned k, int8_t* wq, float* wd) {
+  if (!gate || !up || !wq || !wd || ff == 0 || ff % 32 != 0 || k == 0 || k % 32 != 0) return -1;
+  const size_t row_bytes = (size_t)(k / 32) * 34, group = 32 * row_bytes;
+  std::vector<uint8_t> rows(2 * ff * row_bytes);
+  for (size_t j = 0; j < ff / 32; ++j) {
+    std::memcpy(rows.data() + (2 * j) * group, static_cast<const uint8_t*>(gate) + j * group, group);
+    std::memcpy(rows.data() + (2 * j + 1) * group, static_cast<const uint8_t*>(up) + j * group, group);
+  }
+  eg2_q8_weight_tiles(rows.data(), 2 * ff, k, wq, wd);
+  return 0;
 }
 
 void eg2_rope_table(float base, unsigned n_pos, float* table) {

@@ -121,12 +121,14 @@ SIGNATURES = {
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _u, _u, _u, _u, _vp]),
+    "eg2_hip_gemm_q8_geglu": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
     "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
     "eg2_q8_tile_bytes": (C.c_size_t, [C.c_size_t, _u]),
     "eg2_q8_pack_rows": (None, [_vp, C.c_size_t, _u, _vp]),
     "eg2_q8_unpack_rows": (None, [_vp, C.c_size_t, _u, _vp]),
     "eg2_q8_weight_tiles": (None, [_vp, C.c_size_t, _u, _vp, _vp]),
+    "eg2_q8_geglu_weight_tiles": (C.c_int, [_vp, _vp, C.c_size_t, _u, _vp, _vp]),
     "eg2_rope_table": (None, [C.c_float, _u, _vp]),
     "eg2_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
     "eg2_gguf_close": (None, [C.POINTER(EiGguf)]),
@@ -385,6 +387,23 @@ def q8_weight_tiles(blocks_u8, rows, k):
     return wq, wd
 
 
+def q8_geglu_weight_tiles(gate_u8, up_u8, ff, k):
+    """GGUF Q8_0 gate and up bytes [ff, k] -> the operands of the fused
+    gate|up + GeGLU GEMM (rows interleaved in 32-row groups; wq int8 row
+    tiles, flat; wd float32 [k/32, 2 ff])."""
+    import numpy as np
+
+    g = np.ascontiguousarray(gate_u8, dtype=np.uint8)
+    u = np.ascontiguousarray(up_u8, dtype=np.uint8)
+    if g.size != ff * (k // 32) * 34 or u.size != g.size:
+        raise ValueError("gate/up must hold ff x k Q8_0 values each")
+    wq = np.zeros(q8_tile_bytes(2 * ff, k), dtype=np.int8)
+    wd = np.zeros((k // 32, 2 * ff), dtype=np.float32)
+    if lib().eg2_q8_geglu_weight_tiles(g.ctypes.data, u.ctypes.data, ff, k, wq.ctypes.data, wd.ctypes.data):
+        raise ValueError("ff and k must be multiples of 32")
+    return wq, wd
+
+
 def attention_items(offsets):
     """(items uint32 [n, 8], merges uint32 [m, 4], slots) of a packing
     (eg2_attention_items)."""
@@ -515,3 +534,14 @@ class ops:
         m = y.shape[1] if m is None else m
         check(lib().eg2_hip_gemm_q8(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wq), cls._p(wd), wd.shape[1],
                                     cls._p(y), n, m, k, y.shape[1], cls._stream()), "gemm_q8")
+
+    @classmethod
+    def gemm_q8_geglu(cls, xq, xd, wq, wd, gq, gd, n):
+        """gq/gd = Q8_0 of gelu(gate) * up for n rows of xq (int8 row tiles,
+        scales xd [k/32, ldx]); (wq, wd) from q8_geglu_weight_tiles; gd is
+        [ff/32, ldg] and gq the row tiles of ff values per row."""
+        k = 32 * xd.shape[0]
+        ff = 32 * gd.shape[0]
+        check(lib().eg2_hip_gemm_q8_geglu(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wq), cls._p(wd), wd.shape[1],
+                                          cls._p(gq), cls._p(gd), gd.shape[1], n, ff, k, cls._stream()),
+              "gemm_q8_geglu")

@@ -137,6 +137,20 @@ int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, vo
 int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd, unsigned ldw,
                     float *y, unsigned n, unsigned m, unsigned k, unsigned ldy, void *stream);
 
+/* The gate and up projections and the GeGLU with its Q8_0 quantization in
+ * one kernel: for rows of Q8_0 activations xq/xd [n][k] and the gate and up
+ * weights interleaved in 32-row groups (eg2_q8_geglu_weight_tiles: ldw >=
+ * 2 ff), computes gate and up exactly as eg2_hip_gemm_q8 does, then
+ * gelu_tanh(gate) * up (kernels.c:367-371) and its Q8_0 blocks
+ * (quants.c:97-177) into gq (row tiles, ff / 32 blocks per row) and gd
+ * [ff/32][ldg] (ldg >= n) -- bit-identical to eg2_hip_gemm_q8 on
+ * [gate | up] followed by eg2_hip_gelu_quant. Replaces the gate and up
+ * eg2_mm* calls and eg2_element mode 1 of kernels/eg2.c (:41-119,
+ * :173-179). ff % 32 == 0, k % 32 == 0; sizes and strides at most 2^24. */
+int eg2_hip_gemm_q8_geglu(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd,
+                          unsigned ldw, int8_t *gq, float *gd, unsigned ldg, unsigned n, unsigned ff, unsigned k,
+                          void *stream);
+
 /* ------------------------------------------------------------ executor phases
  * ei_gemma2_kfd_batch (gemma2_kfd.h) is stage + launch_staged(1) + collect.
  * The phases have no counterpart in the reference; they let a benchmark
@@ -173,6 +187,13 @@ void eg2_q8_unpack_rows(const int8_t *tiles, size_t rows, unsigned k, int8_t *q)
  * bytes; padding rows zero), and wd [k/32][ldw], ldw = rows rounded up to
  * 32, the exact float value of each block's fp16 scale (common.h:17-40). */
 void eg2_q8_weight_tiles(const void *blocks, size_t rows, unsigned k, int8_t *wq, float *wd);
+
+/* GGUF Q8_0 gate and up matrices [ff][k] -> the weight operands of
+ * eg2_hip_gemm_q8_geglu: rows interleaved in 32-row groups (gate rows
+ * 32j..32j+31, then up rows 32j..32j+31, for j = 0 .. ff/32 - 1), then
+ * laid out as eg2_q8_weight_tiles does (2 ff rows, ldw = 2 ff). Returns 0,
+ * or -1 when ff % 32 != 0 or k % 32 != 0 (nothing written). */
+int eg2_q8_geglu_weight_tiles(const void *gate, const void *up, size_t ff, unsigned k, int8_t *wq, float *wd);
 
 /* RoPE table for positions 0..n_pos-1: row p = [cos(theta_0..127) |
  * sin(theta_0..127)], theta_i = p * powf(base, -2i/256), computed with the

@@ -225,6 +225,66 @@ def test_gemm_q8_strided_output(eg2, gpu):
     assert (got[:, m:] == 7.0).all()
 
 
+def run_geglu(eg2, gpu, xb, wg, wu, k, ff, ldg):
+    """The fused gate|up + GeGLU GEMM on oracle Q8_0 blocks; returns
+    (int8 values [n, ff], scales [ff/32, ldg]) with sentinels left in the
+    unwritten scale columns."""
+    import torch
+
+    n = xb.shape[0]
+    wq, wd = eg2.q8_geglu_weight_tiles(wg.view(np.uint8), wu.view(np.uint8), ff, k)
+    gq = qbuf(eg2, n, ff, gpu)
+    gd = torch.full((ff // 32, ldg), -3.0, dtype=torch.float32, device=gpu)
+    eg2.ops.gemm_q8_geglu(*device_q8(eg2, xb, k, gpu), dev(wq, gpu), dev(wd, gpu), gq, gd, n)
+    return qvals(eg2, gq, n, ff), host(gd)
+
+
+@pytest.mark.parametrize("n", [2048, 300, 33, 1])
+def test_gemm_q8_geglu_equals_gemm_then_gelu_quant(eg2, gpu, n):
+    """The fused kernel of the forward (gate|up 2304 x 768 + GeGLU + Q8_0)
+    is bit-identical to the two-kernel path: eg2_hip_gemm_q8 on
+    [gate | up], then eg2_hip_gelu_quant."""
+    import torch
+
+    k, ff = N_EMBD, N_FF
+    wg = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.02).astype(np.float32))
+    wu = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.02).astype(np.float32))
+    xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
+    q, d = run_geglu(eg2, gpu, xb, wg, wu, k, ff, n + 5)
+    y = empty((n, 2 * ff), torch.float32, gpu)
+    eg2.ops.gemm_q8(*device_q8(eg2, xb, k, gpu), *device_weights(eg2, np.concatenate([wg, wu]), k, gpu), y)
+    rq, rd = qbuf(eg2, n, ff, gpu), empty((36, n), torch.float32, gpu)
+    eg2.ops.gelu_quant(y, rq, rd)
+    assert np.array_equal(q, qvals(eg2, rq, n, ff))
+    assert np.array_equal(d[:, :n], host(rd))
+    assert (d[:, n:] == -3.0).all()
+
+
+@pytest.mark.parametrize("n,ff,k", [(64, 32, 32), (100, 96, 160), (65, 1152, 768)])
+def test_gemm_q8_geglu_against_oracle(eg2, gpu, n, ff, k):
+    """Other widths (k = 160: a block count that is not a multiple of the
+    LDS ring depth) against the oracle: the GEMM is exact, so only the
+    device tanhf's last bit separates the results (the tolerance of
+    test_gelu_quant_matches_up_to_tanh_ulps)."""
+    wg = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.05).astype(np.float32))
+    wu = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.05).astype(np.float32))
+    xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
+    q, d = run_geglu(eg2, gpu, xb, wg, wu, k, ff, n)
+    gate, up = OL.gemm_q8_0(wg, xb), OL.gemm_q8_0(wu, xb)
+    o = oracle()
+    nb = ff // 32
+    blocks = np.zeros((n, nb), dtype=Q8)
+    for t in range(n):
+        o.or_gelu_mul_quantize_q8_0(fptr(np.ascontiguousarray(gate[t])), fptr(np.ascontiguousarray(up[t])), ff,
+                                    vptr(blocks[t]))
+    wq, wd = split(blocks, ff)
+    same_d = d.T == wd
+    assert same_d.mean() > 0.99
+    qd = np.abs(q - wq).reshape(n, nb, 32)
+    assert qd[same_d].max() <= 1
+    assert (qd.max(2) == 0).mean() > 0.98
+
+
 def segments_log_uniform(rng, n_seg=16, total=2048, lo=8, hi=512):
     """Sequence lengths ~ exp(U(ln lo, ln hi)), scaled to sum `total`,
     rounded, each clipped to [lo, hi]; the remainder goes to the last one

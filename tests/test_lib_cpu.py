@@ -62,6 +62,14 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
+    # gemm_q8_geglu(xq, xd, ldx, wq, wd, ldw, gq, gd, ldg, n, ff, k)
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 96, p, p, 4, 4, 48, 32, None) == inval  # ff % 32
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 4, 32, 48, None) == inval  # k % 32
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 63, p, p, 4, 4, 32, 32, None) == inval  # ldw < 2 ff
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 3, p, p, 64, p, p, 4, 4, 32, 32, None) == inval  # ldx < n
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 3, 4, 32, 32, None) == inval  # ldg < n
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, None, 4, 4, 32, 32, None) == inval
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 0, 32, 32, None) == inval  # n = 0
     assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, p, None) == inval  # grid 0
     assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, p, None) == inval
     assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, p, None) == inval
@@ -171,6 +179,24 @@ def test_q8_weight_tiles_are_the_exact_decode(eg2):
     assert not eg2.q8_unpack_rows(wq, 64, k)[rows:].any()
     deq = (q.reshape(rows, 3, 32).astype(np.float32) * wd[:, :rows].T[:, :, None]).reshape(rows, k)
     assert np.array_equal(deq, dequantize_q8_0(blocks))
+
+
+def test_q8_geglu_weight_tiles_interleave_gate_and_up(eg2):
+    """The fused gate|up + GeGLU operands are the plain weight tiles of
+    [gate 0-31, up 0-31, gate 32-63, up 32-63, ...]."""
+    rng = np.random.default_rng(2)
+    ff, k = 96, 64
+    gate = quantize_q8_0(rng.standard_normal((ff, k)).astype(np.float32))
+    up = quantize_q8_0((rng.standard_normal((ff, k)) * 3).astype(np.float32))
+    wq, wd = eg2.q8_geglu_weight_tiles(gate.view(np.uint8), up.view(np.uint8), ff, k)
+    order = np.concatenate([np.concatenate([gate[32 * j:32 * j + 32], up[32 * j:32 * j + 32]]) for j in range(ff // 32)])
+    rq, rd = eg2.q8_weight_tiles(order.view(np.uint8), 2 * ff, k)
+    assert np.array_equal(wq, rq) and np.array_equal(wd, rd)
+    q = eg2.q8_unpack_rows(wq, 2 * ff, k).reshape(ff // 32, 2, 32, k)
+    assert np.array_equal(q[1, 0], gate["qs"][32:64].reshape(32, k))
+    assert np.array_equal(q[2, 1], up["qs"][64:96].reshape(32, k))
+    with pytest.raises(ValueError):
+        eg2.q8_geglu_weight_tiles(gate[:40].view(np.uint8), up[:40].view(np.uint8), 40, k)
 
 
 @pytest.fixture(scope="module")
