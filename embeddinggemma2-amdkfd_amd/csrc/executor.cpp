@@ -20,10 +20,12 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <condition_variable>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -77,26 +79,81 @@ struct Layer {
   int window;
 };
 
+// One wave in flight: a stream, the workspace of a 2048-token wave, pinned
+// staging, and the hipGraphs recorded on them. Several lanes share one
+// context's weights, so consecutive waves overlap on the device: one wave's
+// latency-bound kernels (row kernels, attention over few sequences) run
+// beside another wave's GEMMs.
+struct Lane {
+  unsigned index = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mutex;
+  float *x, *h, *qkv, *xd, *cd, *pooled, *mid, *mid_d;
+  int8_t *xq, *cq, *mid_q;
+  _Float16 *qs, *ks, *vt;
+  int32_t *ids_d, *pos_d, *vcol_d;
+  // Attention work lists (items, merges) and their counts {items, merges};
+  // partial results of split sequences.
+  uint32_t *items_d, *merges_d, *counts_d, *off_d;
+  float* partials;
+  // Pinned staging.
+  int32_t *ids_h, *pos_h, *vcol_h;
+  uint32_t *items_h, *merges_h, *counts_h, *off_h;
+  float* out_h;
+  std::map<unsigned, hipGraphExec_t> graphs;  // key: 2 * padded rows + (wave has split sequences)
+  bool staged_merge = false;
+  unsigned staged_tokens = 0, staged_rows = 0;
+  size_t staged_batch = 0;
+  std::map<std::string, double> timings;
+};
+
 class Backend {
  public:
   explicit Backend(const ei_gguf* g);
   ~Backend();
+  // One wave through any free lane: stage, launch, collect. Calls from
+  // several threads run on separate lanes at the same time.
   void batch(const int32_t* ids, const size_t* offsets, size_t batch, float* out);
-  // The three phases of batch(), exposed for measurement: upload one wave's
-  // ids and metadata, enqueue its forward (device-resident, no host copies),
-  // and wait + copy the embeddings back.
-  void stage(const int32_t* ids, const size_t* offsets, size_t batch);
-  void launch_staged(unsigned repeats);
-  void collect(float* out);
-  std::mutex& mutex() { return mutex_; }
+  // The three phases of batch() on one lane, exposed for measurement and
+  // pipelining: upload one wave's ids and metadata, enqueue its forward
+  // (device-resident, no host copies), and wait + copy the embeddings back.
+  // The caller holds the lane's mutex.
+  void stage(Lane& L, const int32_t* ids, const size_t* offsets, size_t batch);
+  void launch_staged(Lane& L, unsigned repeats);
+  void collect(Lane& L, float* out);
+  unsigned lanes() const { return (unsigned)lanes_.size(); }
+  // The pool of lanes not held by a caller: acquire blocks until one is free.
+  unsigned acquire_lane() {
+    std::unique_lock<std::mutex> pool(pool_mutex_);
+    pool_cv_.wait(pool, [&] { return !free_lanes_.empty(); });
+    const unsigned i = free_lanes_.back();
+    free_lanes_.pop_back();
+    return i;
+  }
+  void release_lane(unsigned i) {
+    {
+      std::lock_guard<std::mutex> pool(pool_mutex_);
+      if (i >= lanes_.size() || std::find(free_lanes_.begin(), free_lanes_.end(), i) != free_lanes_.end()) return;
+      free_lanes_.push_back(i);
+    }
+    pool_cv_.notify_one();
+  }
+  Lane& lane(unsigned i) {
+    if (i >= lanes_.size()) throw std::runtime_error("lane index out of range");
+    return *lanes_[i];
+  }
 
  private:
   const ei_gguf* model_;
-  hipStream_t stream_ = nullptr;
   std::vector<void*> dev_allocs_;
   std::vector<void*> host_allocs_;
-  std::mutex mutex_;
-  bool poisoned_ = false;
+  std::vector<std::unique_ptr<Lane>> lanes_;
+  std::mutex pool_mutex_;
+  std::condition_variable pool_cv_;
+  std::vector<unsigned> free_lanes_;
+  // Set by any device-side failure (src/gemma2_kfd.cpp:190-191, 214-215,
+  // 270): every later call fails.
+  std::atomic<bool> failed_{false};
   bool use_graph_ = true;
   bool profile_ = false;
 
@@ -106,27 +163,7 @@ class Backend {
   const float* output_norm_ = nullptr;
   DevMat dense2_, dense3_;
   bool dense_ = false;
-
-  // Workspace for kCap tokens.
-  float *x_, *h_, *qkv_, *xd_, *cd_, *pooled_, *mid_, *mid_d_;
-  int8_t *xq_, *cq_, *mid_q_;
-  _Float16 *qs_, *ks_, *vt_;
-  int32_t *ids_d_, *pos_d_, *vcol_d_;
-  // Attention work lists (items, merges) and their counts {items, merges};
-  // partial results of split sequences.
-  uint32_t *items_d_, *merges_d_, *counts_d_, *off_d_;
-  float* partials_;
-  // Pinned staging.
-  int32_t *ids_h_, *pos_h_, *vcol_h_;
-  uint32_t *items_h_, *merges_h_, *counts_h_, *off_h_;
   eg2::AttentionCounts attn_cap_{};
-  bool staged_merge_ = false;
-  float* out_h_;
-
-  std::map<unsigned, hipGraphExec_t> graphs_;  // key: 2 * padded rows + (wave has split sequences)
-  unsigned staged_tokens_ = 0, staged_rows_ = 0;
-  size_t staged_batch_ = 0;
-  std::map<std::string, double> timings_;
 
   template <class T>
   T* dalloc(size_t n) {
@@ -150,11 +187,22 @@ class Backend {
   std::vector<uint8_t> q8_rows(const std::string& name, int k, int m) const;
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
   DevMat upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k);
+  void alloc_lane(Lane& L);
   void launch(const char* name, hipError_t e);
-  void record_layers(unsigned rows, bool merge);
+  void record_layers(Lane& L, unsigned rows, bool merge);
   void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
             hipStream_t s);
-  void wait(const char* what);
+  void wait(Lane& L, const char* what);
+  // Runs device work; any exception it throws marks the context failed.
+  template <class F>
+  void device_step(F&& f) {
+    try {
+      f();
+    } catch (...) {
+      failed_ = true;
+      throw;
+    }
+  }
 };
 
 const ei_tensor* Backend::tensor(const std::string& name, bool required) const {
@@ -286,8 +334,6 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
   if (swa_period == 0) throw std::runtime_error("sliding_window_pattern must be positive");
   if (swa_window > 2 * kCap) throw std::runtime_error("sliding_window too large");
 
-  check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-
   // RoPE tables, one per distinct base (kernels.c:245-249 values).
   std::vector<float> table((size_t)kCap * kHeadDim);
   std::map<float, const float*> ropes;
@@ -345,41 +391,22 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
     dense_ = true;
   }
 
-  x_ = dalloc<float>((size_t)kCap * kEmbd);
-  h_ = dalloc<float>((size_t)kCap * kEmbd);
-  qkv_ = dalloc<float>((size_t)kCap * kQKV);
-  xq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kFF));
-  xd_ = dalloc<float>((size_t)kCap * (kFF / 32));
-  cq_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
-  cd_ = dalloc<float>((size_t)kCap * (kEmbd / 32));
-  qs_ = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
-  ks_ = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
-  // Columns no token writes are read (masked) by the attention kernel and
-  // must hold finite values: zero the buffer once.
-  vt_ = dalloc<_Float16>((size_t)2 * kHeadDim * kVtCols);
-  check(hipMemset(vt_, 0, (size_t)2 * kHeadDim * kVtCols * sizeof(_Float16)), "hipMemset");
-  ids_d_ = dalloc<int32_t>(kCap);
-  pos_d_ = dalloc<int32_t>(kCap);
-  vcol_d_ = dalloc<int32_t>(kCap);
   // Capacity for the wave cap plus the padding sequence (rows rounded to 32).
   attn_cap_ = eg2::attention_capacity(kCap + 32, kCap + 1);
-  items_d_ = dalloc<uint32_t>(8 * (size_t)attn_cap_.items);
-  merges_d_ = dalloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
-  counts_d_ = dalloc<uint32_t>(2);
-  partials_ = dalloc<float>(eg2::kAttentionPartialFloats * std::max(1u, attn_cap_.slots));
-  off_d_ = dalloc<uint32_t>(kCap + 1);
-  pooled_ = dalloc<float>((size_t)kCap * kEmbd);
-  mid_ = dalloc<float>((size_t)kCap * kDenseFF);
-  mid_q_ = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kDenseFF));
-  mid_d_ = dalloc<float>((size_t)kCap * (kDenseFF / 32));
-  ids_h_ = halloc<int32_t>(kCap);
-  pos_h_ = halloc<int32_t>(kCap);
-  vcol_h_ = halloc<int32_t>(kCap);
-  items_h_ = halloc<uint32_t>(8 * (size_t)attn_cap_.items);
-  merges_h_ = halloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
-  counts_h_ = halloc<uint32_t>(2);
-  off_h_ = halloc<uint32_t>(kCap + 1);
-  out_h_ = halloc<float>((size_t)kCap * kEmbd);
+  // EG2_HIP_LANES (1..8, default 3): waves in flight per context.
+  unsigned n_lanes = 3;
+  if (const char* v = std::getenv("EG2_HIP_LANES")) {
+    char* end = nullptr;
+    const long l = std::strtol(v, &end, 10);
+    if (!*v || *end || l < 1 || l > 8) throw std::runtime_error("EG2_HIP_LANES must be 1..8");
+    n_lanes = (unsigned)l;
+  }
+  for (unsigned i = 0; i < n_lanes; ++i) {
+    lanes_.push_back(std::make_unique<Lane>());
+    lanes_.back()->index = i;
+    alloc_lane(*lanes_.back());
+    free_lanes_.push_back(n_lanes - 1 - i);  // lane 0 is taken first
+  }
   check(hipDeviceSynchronize(), "upload");
 
   size_t bytes = 0;
@@ -390,10 +417,49 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
                layers_.size(), bytes / 1048576.0, emb->n_bytes / 1048576.0, kCap, dense_ ? ", dense head" : "");
 }
 
+void Backend::alloc_lane(Lane& L) {
+  check(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking), "hipStreamCreate");
+  L.x = dalloc<float>((size_t)kCap * kEmbd);
+  L.h = dalloc<float>((size_t)kCap * kEmbd);
+  L.qkv = dalloc<float>((size_t)kCap * kQKV);
+  L.xq = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kFF));
+  L.xd = dalloc<float>((size_t)kCap * (kFF / 32));
+  L.cq = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
+  L.cd = dalloc<float>((size_t)kCap * (kEmbd / 32));
+  L.qs = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
+  L.ks = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
+  // Columns no token writes are read (masked) by the attention kernel and
+  // must hold finite values: zero the buffer once.
+  L.vt = dalloc<_Float16>((size_t)2 * kHeadDim * kVtCols);
+  check(hipMemset(L.vt, 0, (size_t)2 * kHeadDim * kVtCols * sizeof(_Float16)), "hipMemset");
+  L.ids_d = dalloc<int32_t>(kCap);
+  L.pos_d = dalloc<int32_t>(kCap);
+  L.vcol_d = dalloc<int32_t>(kCap);
+  L.items_d = dalloc<uint32_t>(8 * (size_t)attn_cap_.items);
+  L.merges_d = dalloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
+  L.counts_d = dalloc<uint32_t>(2);
+  L.partials = dalloc<float>(eg2::kAttentionPartialFloats * std::max(1u, attn_cap_.slots));
+  L.off_d = dalloc<uint32_t>(kCap + 1);
+  L.pooled = dalloc<float>((size_t)kCap * kEmbd);
+  L.mid = dalloc<float>((size_t)kCap * kDenseFF);
+  L.mid_q = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kDenseFF));
+  L.mid_d = dalloc<float>((size_t)kCap * (kDenseFF / 32));
+  L.ids_h = halloc<int32_t>(kCap);
+  L.pos_h = halloc<int32_t>(kCap);
+  L.vcol_h = halloc<int32_t>(kCap);
+  L.items_h = halloc<uint32_t>(8 * (size_t)attn_cap_.items);
+  L.merges_h = halloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
+  L.counts_h = halloc<uint32_t>(2);
+  L.off_h = halloc<uint32_t>(kCap + 1);
+  L.out_h = halloc<float>((size_t)kCap * kEmbd);
+}
+
 Backend::~Backend() {
-  if (stream_) (void)hipStreamSynchronize(stream_);
-  for (auto& kvp : graphs_) (void)hipGraphExecDestroy(kvp.second);
-  if (stream_) (void)hipStreamDestroy(stream_);
+  for (auto& L : lanes_) {
+    if (L->stream) (void)hipStreamSynchronize(L->stream);
+    for (auto& kvp : L->graphs) (void)hipGraphExecDestroy(kvp.second);
+    if (L->stream) (void)hipStreamDestroy(L->stream);
+  }
   for (void* p : dev_allocs_) (void)hipFree(p);
   for (void* p : host_allocs_) (void)hipHostFree(p);
 }
@@ -416,38 +482,39 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 // GeGLU (+Q8_0) in its epilogue, down GEMM, residual + next attn_norm
 // (+Q8_0); finally the
 // output_norm per token (the first half of kernels.c:417-427).
-void Backend::record_layers(unsigned rows, bool merge) {
-  hipStream_t s = stream_;
+void Backend::record_layers(Lane& ln, unsigned rows, bool merge) {
+  hipStream_t s = ln.stream;
   const int n = (int)rows;
-  launch("embed", eg2::launch_embed_norm_quant(token_embd_, ids_d_, n, std::sqrt((float)kEmbd), layers_[0].attn_norm,
-                                               eps_, x_, xq_, xd_, s));
+  launch("embed", eg2::launch_embed_norm_quant(token_embd_, ln.ids_d, n, std::sqrt((float)kEmbd),
+                                               layers_[0].attn_norm, eps_, ln.x, ln.xq, ln.xd, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
-    gemm("gemm_qkv", xq_, xd_, L.qkv, qkv_, n, kQKV, s);
-    launch("qk_norm_rope", eg2::launch_qk_norm_rope(qkv_, L.q_norm, L.k_norm, L.rope, pos_d_, vcol_d_, eps_, qs_, ks_,
-                                                    vt_, kVtCols, n, s));
-    launch("attention", eg2::launch_attention(qs_, ks_, vt_, kVtCols, vcol_d_, items_d_, counts_d_, (n + 7) / 8,
-                                              L.window, n, cq_, cd_, partials_, s));
+    gemm("gemm_qkv", ln.xq, ln.xd, L.qkv, ln.qkv, n, kQKV, s);
+    launch("qk_norm_rope", eg2::launch_qk_norm_rope(ln.qkv, L.q_norm, L.k_norm, L.rope, ln.pos_d, ln.vcol_d, eps_,
+                                                    ln.qs, ln.ks, ln.vt, kVtCols, n, s));
+    launch("attention", eg2::launch_attention(ln.qs, ln.ks, ln.vt, kVtCols, ln.vcol_d, ln.items_d, ln.counts_d,
+                                              (n + 7) / 8, L.window, n, ln.cq, ln.cd, ln.partials, s));
     if (merge)
-      launch("attention_merge",
-             eg2::launch_attention_merge(merges_d_, counts_d_ + 1, (n + 3) / 4, partials_, n, cq_, cd_, s));
-    gemm("gemm_o", cq_, cd_, L.o, h_, n, kEmbd, s);
+      launch("attention_merge", eg2::launch_attention_merge(ln.merges_d, ln.counts_d + 1, (n + 3) / 4, ln.partials,
+                                                            n, ln.cq, ln.cd, s));
+    gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
     // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.
-    launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_attn, L.ffn_norm, eps_, cq_, cd_, n, s));
-    launch("gemm_gate_up_geglu", eg2::launch_gemm_q8_geglu(cq_, cd_, n, L.gu.q, L.gu.d, L.gu.ld, xq_, xd_, n, n, kFF,
-                                                            kEmbd, s));
-    gemm("gemm_down", xq_, xd_, L.down, h_, n, kEmbd, s);
+    launch("residual",
+           eg2::launch_residual_norm_quant(ln.x, ln.h, L.post_attn, L.ffn_norm, eps_, ln.cq, ln.cd, n, s));
+    launch("gemm_gate_up_geglu", eg2::launch_gemm_q8_geglu(ln.cq, ln.cd, n, L.gu.q, L.gu.d, L.gu.ld, ln.xq, ln.xd, n,
+                                                            n, kFF, kEmbd, s));
+    gemm("gemm_down", ln.xq, ln.xd, L.down, ln.h, n, kEmbd, s);
     const float* next = il + 1 < layers_.size() ? layers_[il + 1].attn_norm : nullptr;
-    launch("residual", eg2::launch_residual_norm_quant(x_, h_, L.post_ffw, next, eps_, xq_, xd_, n, s));
+    launch("residual", eg2::launch_residual_norm_quant(ln.x, ln.h, L.post_ffw, next, eps_, ln.xq, ln.xd, n, s));
   }
-  launch("output_norm", eg2::launch_rms_norm_rows(x_, output_norm_, eps_, n, s));
+  launch("output_norm", eg2::launch_rms_norm_rows(ln.x, output_norm_, eps_, n, s));
 }
 
-void Backend::wait(const char* what) {
+void Backend::wait(Lane& ln, const char* what) {
   const auto start = std::chrono::steady_clock::now();
   for (;;) {
-    const hipError_t e = hipStreamQuery(stream_);
+    const hipError_t e = hipStreamQuery(ln.stream);
     if (e == hipSuccess) return;
     if (e != hipErrorNotReady) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
     if (std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count() > kTimeoutSeconds)
@@ -457,22 +524,29 @@ void Backend::wait(const char* what) {
 }
 
 void Backend::batch(const int32_t* ids, const size_t* offsets, size_t batch, float* out) {
-  std::lock_guard<std::mutex> guard(mutex_);
+  const unsigned idx = acquire_lane();
+  struct Release {
+    Backend* b;
+    unsigned i;
+    ~Release() { b->release_lane(i); }
+  } release{this, idx};
+  Lane& ln = *lanes_[idx];
+  std::lock_guard<std::mutex> guard(ln.mutex);
   const auto t0 = std::chrono::steady_clock::now();
-  stage(ids, offsets, batch);
-  launch_staged(1);
-  collect(out);
+  stage(ln, ids, offsets, batch);
+  launch_staged(ln, 1);
+  collect(ln, out);
   if (profile_) {
     const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    std::fprintf(stderr, "HIP_PROFILE {\"tokens\":%u,\"batch\":%zu,\"wall_ms\":%.3f,\"layers_ms\":%.3f}\n",
-                 staged_tokens_, staged_batch_, ms, timings_["layers"]);
-    timings_.clear();
+    std::fprintf(stderr, "HIP_PROFILE {\"lane\":%u,\"tokens\":%u,\"batch\":%zu,\"wall_ms\":%.3f,\"layers_ms\":%.3f}\n",
+                 ln.index, ln.staged_tokens, ln.staged_batch, ms, ln.timings["layers"]);
+    ln.timings.clear();
   }
 }
 
-void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
-  if (poisoned_) throw std::runtime_error("HIP context failed; restart process before reuse");
-  staged_batch_ = 0;
+void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t batch) {
+  if (failed_) throw std::runtime_error("HIP context failed; restart process before reuse");
+  ln.staged_batch = 0;
   // src/gemma2_kfd.cpp:271-278
   if (!ids || !offsets || !batch || batch > kCap || offsets[0] || offsets[batch] > kCap)
     throw std::runtime_error("HIP batch requires 1..2048 packed tokens and nonempty sequences");
@@ -481,127 +555,137 @@ void Backend::stage(const int32_t* ids, const size_t* offsets, size_t batch) {
   const unsigned n = (unsigned)offsets[batch];
   for (unsigned i = 0; i < n; ++i)
     if (ids[i] < 0 || ids[i] >= kVocab) throw std::runtime_error("token ID out of range");
+  // The lane's pinned staging may still feed its previous wave's copies.
+  device_step([&] { wait(ln, "HIP previous wave"); });
 
   // Metadata; rows [n, rows) form one dummy sequence that is never pooled.
   const unsigned rows = (n + 31) / 32 * 32;
   for (size_t s = 0; s < batch; ++s)
     for (size_t t = offsets[s]; t < offsets[s + 1]; ++t) {
-      ids_h_[t] = ids[t];
-      pos_h_[t] = (int32_t)(t - offsets[s]);
+      ln.ids_h[t] = ids[t];
+      ln.pos_h[t] = (int32_t)(t - offsets[s]);
     }
   for (unsigned t = n; t < rows; ++t) {
-    ids_h_[t] = 0;
-    pos_h_[t] = (int32_t)(t - n);
+    ln.ids_h[t] = 0;
+    ln.pos_h[t] = (int32_t)(t - n);
   }
-  for (size_t s = 0; s <= batch; ++s) off_h_[s] = (uint32_t)offsets[s];
+  for (size_t s = 0; s <= batch; ++s) ln.off_h[s] = (uint32_t)offsets[s];
   // Attention work lists; the padding rows form one more sequence.
   std::vector<size_t> all(offsets, offsets + batch + 1);
   if (rows > n) all.push_back(rows);
-  const eg2::AttentionCounts ac = eg2::build_attention_items(all.data(), all.size() - 1, items_h_, merges_h_);
+  const eg2::AttentionCounts ac = eg2::build_attention_items(all.data(), all.size() - 1, ln.items_h, ln.merges_h);
   if (ac.items > attn_cap_.items || ac.merges > attn_cap_.merges || ac.slots > attn_cap_.slots)
     throw std::runtime_error("attention work list exceeds its capacity");
-  counts_h_[0] = ac.items;
-  counts_h_[1] = ac.merges;
+  ln.counts_h[0] = ac.items;
+  ln.counts_h[1] = ac.merges;
   const bool merge = ac.merges > 0;
   // Transposed-v columns: the padding rows form one more sequence.
-  const size_t cols = eg2::build_vt_columns(offsets, batch, vcol_h_);
-  for (unsigned t = n; t < rows; ++t) vcol_h_[t] = (int32_t)(cols + (t - n));
+  const size_t cols = eg2::build_vt_columns(offsets, batch, ln.vcol_h);
+  for (unsigned t = n; t < rows; ++t) ln.vcol_h[t] = (int32_t)(cols + (t - n));
 
-  poisoned_ = true;  // cleared only when the whole wave completed
-  hipStream_t s = stream_;
-  check(hipMemcpyAsync(ids_d_, ids_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
-  check(hipMemcpyAsync(pos_d_, pos_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
-  check(hipMemcpyAsync(vcol_d_, vcol_h_, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy columns");
-  check(hipMemcpyAsync(items_d_, items_h_, 8 * (size_t)ac.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
-        "copy attention items");
-  if (merge)
-    check(hipMemcpyAsync(merges_d_, merges_h_, 4 * (size_t)ac.merges * sizeof(uint32_t), hipMemcpyHostToDevice, s),
-          "copy attention merges");
-  check(hipMemcpyAsync(counts_d_, counts_h_, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy attention counts");
-  check(hipMemcpyAsync(off_d_, off_h_, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy offsets");
-  const unsigned key = 2 * rows + (merge ? 1 : 0);
-  if (use_graph_ && !profile_ && graphs_.find(key) == graphs_.end()) {
-    hipGraph_t graph = nullptr;
-    check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-    try {
-      record_layers(rows, merge);
-    } catch (...) {
-      (void)hipStreamEndCapture(s, &graph);
-      if (graph) (void)hipGraphDestroy(graph);
-      throw;
+  device_step([&] {
+    hipStream_t s = ln.stream;
+    check(hipMemcpyAsync(ln.ids_d, ln.ids_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
+    check(hipMemcpyAsync(ln.pos_d, ln.pos_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
+    check(hipMemcpyAsync(ln.vcol_d, ln.vcol_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy columns");
+    check(hipMemcpyAsync(ln.items_d, ln.items_h, 8 * (size_t)ac.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy attention items");
+    if (merge)
+      check(hipMemcpyAsync(ln.merges_d, ln.merges_h, 4 * (size_t)ac.merges * sizeof(uint32_t),
+                           hipMemcpyHostToDevice, s),
+            "copy attention merges");
+    check(hipMemcpyAsync(ln.counts_d, ln.counts_h, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy attention counts");
+    check(hipMemcpyAsync(ln.off_d, ln.off_h, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy offsets");
+    const unsigned key = 2 * rows + (merge ? 1 : 0);
+    if (use_graph_ && !profile_ && ln.graphs.find(key) == ln.graphs.end()) {
+      hipGraph_t graph = nullptr;
+      check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        record_layers(ln, rows, merge);
+      } catch (...) {
+        (void)hipStreamEndCapture(s, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+      }
+      check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+      hipGraphExec_t exec = nullptr;
+      const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      check(e, "hipGraphInstantiate");
+      ln.graphs.emplace(key, exec);
     }
-    check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
-    hipGraphExec_t exec = nullptr;
-    const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    check(e, "hipGraphInstantiate");
-    graphs_.emplace(key, exec);
-  }
-  staged_merge_ = merge;
-  staged_tokens_ = n;
-  staged_rows_ = rows;
-  staged_batch_ = batch;
+  });
+  ln.staged_merge = merge;
+  ln.staged_tokens = n;
+  ln.staged_rows = rows;
+  ln.staged_batch = batch;
 }
 
 // Layer stack (graph or eager), then kernels.c:417-427 (mean + L2 per
 // sequence) and the dense head.
-void Backend::launch_staged(unsigned repeats) {
-  if (!staged_batch_) throw std::runtime_error("no staged wave");
-  hipStream_t s = stream_;
-  const int B = (int)staged_batch_;
-  poisoned_ = true;
-  for (unsigned r = 0; r < repeats; ++r) {
-    if (use_graph_ && !profile_) {
-      check(hipGraphLaunch(graphs_.at(2 * staged_rows_ + (staged_merge_ ? 1 : 0)), s), "hipGraphLaunch");
-    } else if (profile_) {
-      // Per-stage timing needs events around eager launches; the totals are
-      // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
-      hipEvent_t a, b;
-      check(hipEventCreate(&a), "hipEventCreate");
-      check(hipEventCreate(&b), "hipEventCreate");
-      check(hipEventRecord(a, s), "hipEventRecord");
-      record_layers(staged_rows_, staged_merge_);
-      check(hipEventRecord(b, s), "hipEventRecord");
-      check(hipEventSynchronize(b), "hipEventSynchronize");
-      float ms = 0;
-      (void)hipEventElapsedTime(&ms, a, b);
-      timings_["layers"] += ms;
-      (void)hipEventDestroy(a);
-      (void)hipEventDestroy(b);
-    } else {
-      record_layers(staged_rows_, staged_merge_);
+void Backend::launch_staged(Lane& ln, unsigned repeats) {
+  if (failed_) throw std::runtime_error("HIP context failed; restart process before reuse");
+  if (!ln.staged_batch) throw std::runtime_error("no staged wave");
+  hipStream_t s = ln.stream;
+  const int B = (int)ln.staged_batch;
+  device_step([&] {
+    for (unsigned r = 0; r < repeats; ++r) {
+      if (use_graph_ && !profile_) {
+        check(hipGraphLaunch(ln.graphs.at(2 * ln.staged_rows + (ln.staged_merge ? 1 : 0)), s), "hipGraphLaunch");
+      } else if (profile_) {
+        // Per-stage timing needs events around eager launches; the totals are
+        // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
+        hipEvent_t a, b;
+        check(hipEventCreate(&a), "hipEventCreate");
+        check(hipEventCreate(&b), "hipEventCreate");
+        check(hipEventRecord(a, s), "hipEventRecord");
+        record_layers(ln, ln.staged_rows, ln.staged_merge);
+        check(hipEventRecord(b, s), "hipEventRecord");
+        check(hipEventSynchronize(b), "hipEventSynchronize");
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, a, b);
+        ln.timings["layers"] += ms;
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+      } else {
+        record_layers(ln, ln.staged_rows, ln.staged_merge);
+      }
+      launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
+      if (dense_) {
+        launch("dense_quant", eg2::launch_quantize_rows(ln.pooled, kEmbd, ln.cq, ln.cd, B, s));
+        gemm("dense_2", ln.cq, ln.cd, dense2_, ln.mid, B, kDenseFF, s);
+        launch("dense_quant", eg2::launch_quantize_rows(ln.mid, kDenseFF, ln.mid_q, ln.mid_d, B, s));
+        gemm("dense_3", ln.mid_q, ln.mid_d, dense3_, ln.pooled, B, kEmbd, s);
+        launch("dense_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+      }
     }
-    launch("pool", eg2::launch_pool_l2(x_, off_d_, pooled_, B, s));
-    if (dense_) {
-      launch("dense_quant", eg2::launch_quantize_rows(pooled_, kEmbd, cq_, cd_, B, s));
-      gemm("dense_2", cq_, cd_, dense2_, mid_, B, kDenseFF, s);
-      launch("dense_quant", eg2::launch_quantize_rows(mid_, kDenseFF, mid_q_, mid_d_, B, s));
-      gemm("dense_3", mid_q_, mid_d_, dense3_, pooled_, B, kEmbd, s);
-      launch("dense_l2", eg2::launch_l2_prefix(pooled_, kEmbd, kEmbd, B, s));
-    }
-  }
+  });
 }
 
-void Backend::collect(float* out) {
-  if (!staged_batch_) throw std::runtime_error("no staged wave");
+void Backend::collect(Lane& ln, float* out) {
+  if (failed_) throw std::runtime_error("HIP context failed; restart process before reuse");
+  if (!ln.staged_batch) throw std::runtime_error("no staged wave");
   if (!out) throw std::runtime_error("null output");
-  const int B = (int)staged_batch_;
-  check(hipMemcpyAsync(out_h_, pooled_, (size_t)B * kEmbd * sizeof(float), hipMemcpyDeviceToHost, stream_),
-        "copy out");
-  wait("HIP wave");
-  poisoned_ = false;
+  const int B = (int)ln.staged_batch;
+  device_step([&] {
+    check(hipMemcpyAsync(ln.out_h, ln.pooled, (size_t)B * kEmbd * sizeof(float), hipMemcpyDeviceToHost, ln.stream),
+          "copy out");
+    wait(ln, "HIP wave");
+  });
 
   // src/gemma2_kfd.cpp:337-343 rejects non-finite or zero embeddings.
   for (int r = 0; r < B; ++r) {
     double ss = 0;
     for (int z = 0; z < kEmbd; ++z) {
-      const float f = out_h_[(size_t)r * kEmbd + z];
+      const float f = ln.out_h[(size_t)r * kEmbd + z];
       if (!std::isfinite(f)) throw std::runtime_error("nonfinite GPU output");
       ss += (double)f * f;
     }
     if (ss <= 0) throw std::runtime_error("zero GPU embedding");
   }
-  std::memcpy(out, out_h_, (size_t)B * kEmbd * sizeof(float));
+  std::memcpy(out, ln.out_h, (size_t)B * kEmbd * sizeof(float));
 }
 
 }  // namespace
@@ -630,42 +714,55 @@ extern "C" bool ei_gemma2_kfd_batch(void* ctx, const int32_t* ids, const size_t*
   }
 }
 
-extern "C" bool eg2_kfd_stage(void* ctx, const int32_t* ids, const size_t* offsets, size_t batch, char* err,
-                              size_t len) {
+namespace {
+// Runs f on lane `lane` of ctx with the lane held; exceptions become
+// "HIP: ..." messages.
+template <class F>
+bool on_lane(void* ctx, unsigned lane, char* err, size_t len, F&& f) {
   try {
     if (!ctx) throw std::runtime_error("empty context");
     Backend* b = static_cast<Backend*>(ctx);
-    std::lock_guard<std::mutex> guard(b->mutex());
-    b->stage(ids, offsets, batch);
+    Lane& ln = b->lane(lane);
+    std::lock_guard<std::mutex> guard(ln.mutex);
+    f(*b, ln);
     return true;
   } catch (const std::exception& e) {
     if (err && len) std::snprintf(err, len, "HIP: %s", e.what());
     return false;
   }
+}
+}  // namespace
+
+extern "C" unsigned eg2_kfd_lanes(void* ctx) { return ctx ? static_cast<Backend*>(ctx)->lanes() : 0; }
+
+extern "C" int eg2_kfd_acquire_lane(void* ctx) { return ctx ? (int)static_cast<Backend*>(ctx)->acquire_lane() : -1; }
+
+extern "C" void eg2_kfd_release_lane(void* ctx, unsigned lane) {
+  if (ctx) static_cast<Backend*>(ctx)->release_lane(lane);
+}
+
+extern "C" bool eg2_kfd_stage_lane(void* ctx, unsigned lane, const int32_t* ids, const size_t* offsets, size_t batch,
+                                   char* err, size_t len) {
+  return on_lane(ctx, lane, err, len, [&](Backend& b, Lane& ln) { b.stage(ln, ids, offsets, batch); });
+}
+
+extern "C" bool eg2_kfd_launch_lane(void* ctx, unsigned lane, unsigned repeats, char* err, size_t len) {
+  return on_lane(ctx, lane, err, len, [&](Backend& b, Lane& ln) { b.launch_staged(ln, repeats); });
+}
+
+extern "C" bool eg2_kfd_collect_lane(void* ctx, unsigned lane, float* out, char* err, size_t len) {
+  return on_lane(ctx, lane, err, len, [&](Backend& b, Lane& ln) { b.collect(ln, out); });
+}
+
+extern "C" bool eg2_kfd_stage(void* ctx, const int32_t* ids, const size_t* offsets, size_t batch, char* err,
+                              size_t len) {
+  return eg2_kfd_stage_lane(ctx, 0, ids, offsets, batch, err, len);
 }
 
 extern "C" bool eg2_kfd_launch_staged(void* ctx, unsigned repeats, char* err, size_t len) {
-  try {
-    if (!ctx) throw std::runtime_error("empty context");
-    Backend* b = static_cast<Backend*>(ctx);
-    std::lock_guard<std::mutex> guard(b->mutex());
-    b->launch_staged(repeats);
-    return true;
-  } catch (const std::exception& e) {
-    if (err && len) std::snprintf(err, len, "HIP: %s", e.what());
-    return false;
-  }
+  return eg2_kfd_launch_lane(ctx, 0, repeats, err, len);
 }
 
 extern "C" bool eg2_kfd_collect(void* ctx, float* out, char* err, size_t len) {
-  try {
-    if (!ctx) throw std::runtime_error("empty context");
-    Backend* b = static_cast<Backend*>(ctx);
-    std::lock_guard<std::mutex> guard(b->mutex());
-    b->collect(out);
-    return true;
-  } catch (const std::exception& e) {
-    if (err && len) std::snprintf(err, len, "HIP: %s", e.what());
-    return false;
-  }
+  return eg2_kfd_collect_lane(ctx, 0, out, err, len);
 }

@@ -11,6 +11,7 @@
 #include <string>
 #include <vector>
 
+#include "eg2_hip.h"
 #include "gemma2_kfd.h"
 
 namespace {
@@ -117,6 +118,25 @@ extern "C" bool eg2_normalize_prefix(float* embedding, unsigned dims) {
   return true;
 }
 
+namespace {
+
+std::string strip_hip(const char* msg) {
+  const std::string m(msg);
+  return m.rfind("HIP: ", 0) == 0 ? m.substr(5) : m;
+}
+
+// Lanes taken from the executor's pool for one stream; returned on every exit.
+struct HeldLanes {
+  void* ctx;
+  std::vector<int> lanes;
+  ~HeldLanes() {
+    for (int l : lanes)
+      if (l >= 0) eg2_kfd_release_lane(ctx, (unsigned)l);
+  }
+};
+
+}  // namespace
+
 extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* text_offsets, size_t n_texts,
                                  const unsigned* dims, const eg2_batch_config* cfg, float* out, size_t* n_waves,
                                  char* err, size_t len) {
@@ -133,12 +153,37 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
     std::vector<size_t> order(n_texts), wave_end(n_texts);
     const size_t waves = eg2_pack_waves(lengths.data(), n_texts, cfg, order.data(), wave_end.data());
     if (!waves) throw std::runtime_error("packing failed");
+
+    // Wave w runs on slot w % L, each slot a lane held for the whole stream;
+    // a slot's previous wave is collected just before the slot is reused,
+    // so up to L waves are in flight.
+    const size_t L = std::min<size_t>(std::max(1u, eg2_kfd_lanes(ctx)), waves);
+    HeldLanes held{ctx, std::vector<int>(L, -1)};
+    std::vector<size_t> pend_begin(L), pend_end(L);
+    std::vector<bool> busy(L, false);
     std::vector<int32_t> wave_ids;
     std::vector<size_t> offsets;
     std::vector<float> wave_out;
+    char msg[512] = {0};
+    auto finish = [&](size_t slot) {
+      const size_t b = pend_end[slot] - pend_begin[slot];
+      wave_out.resize(b * kEmbd);
+      busy[slot] = false;
+      if (!eg2_kfd_collect_lane(ctx, (unsigned)held.lanes[slot], wave_out.data(), msg, sizeof msg))
+        throw std::runtime_error(strip_hip(msg));
+      for (size_t k = 0; k < b; ++k) {
+        const size_t i = order[pend_begin[slot] + k];
+        float* e = out + i * kEmbd;
+        std::memcpy(e, wave_out.data() + k * kEmbd, kEmbd * sizeof(float));
+        eg2_normalize_prefix(e, dims[i]);
+        std::fill(e + dims[i], e + kEmbd, 0.0f);
+      }
+    };
     size_t begin = 0;
     for (size_t w = 0; w < waves; ++w) {
-      const size_t end = wave_end[w], b = end - begin;
+      const size_t slot = w % L, end = wave_end[w];
+      if (held.lanes[slot] < 0) held.lanes[slot] = eg2_kfd_acquire_lane(ctx);
+      if (busy[slot]) finish(slot);
       wave_ids.clear();
       offsets.assign(1, 0);
       for (size_t k = begin; k < end; ++k) {
@@ -146,19 +191,17 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
         wave_ids.insert(wave_ids.end(), ids + text_offsets[i], ids + text_offsets[i + 1]);
         offsets.push_back(wave_ids.size());
       }
-      wave_out.resize(b * kEmbd);
-      char msg[512] = {0};
-      if (!ei_gemma2_kfd_batch(ctx, wave_ids.data(), offsets.data(), b, wave_out.data(), msg, sizeof msg))
-        throw std::runtime_error(std::string(msg).rfind("HIP: ", 0) == 0 ? std::string(msg).substr(5) : msg);
-      for (size_t k = 0; k < b; ++k) {
-        const size_t i = order[begin + k];
-        float* e = out + i * kEmbd;
-        std::memcpy(e, wave_out.data() + k * kEmbd, kEmbd * sizeof(float));
-        eg2_normalize_prefix(e, dims[i]);
-        std::fill(e + dims[i], e + kEmbd, 0.0f);
-      }
+      const unsigned lane = (unsigned)held.lanes[slot];
+      if (!eg2_kfd_stage_lane(ctx, lane, wave_ids.data(), offsets.data(), end - begin, msg, sizeof msg) ||
+          !eg2_kfd_launch_lane(ctx, lane, 1, msg, sizeof msg))
+        throw std::runtime_error(strip_hip(msg));
+      pend_begin[slot] = begin;
+      pend_end[slot] = end;
+      busy[slot] = true;
       begin = end;
     }
+    for (size_t w = waves - L; w < waves; ++w)
+      if (busy[w % L]) finish(w % L);
     if (n_waves) *n_waves = waves;
     return true;
   } catch (const std::exception& e) {

@@ -144,6 +144,13 @@ SIGNATURES = {
     "eg2_kfd_stage": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p, C.c_size_t]),
     "eg2_kfd_launch_staged": (C.c_bool, [C.c_void_p, C.c_uint, C.c_char_p, C.c_size_t]),
     "eg2_kfd_collect": (C.c_bool, [C.c_void_p, _f, C.c_char_p, C.c_size_t]),
+    "eg2_kfd_lanes": (C.c_uint, [C.c_void_p]),
+    "eg2_kfd_acquire_lane": (C.c_int, [C.c_void_p]),
+    "eg2_kfd_release_lane": (None, [C.c_void_p, C.c_uint]),
+    "eg2_kfd_stage_lane": (C.c_bool, [C.c_void_p, C.c_uint, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p,
+                                      C.c_size_t]),
+    "eg2_kfd_launch_lane": (C.c_bool, [C.c_void_p, C.c_uint, C.c_uint, C.c_char_p, C.c_size_t]),
+    "eg2_kfd_collect_lane": (C.c_bool, [C.c_void_p, C.c_uint, _f, C.c_char_p, C.c_size_t]),
     "ei_gemma2_kfd_batch": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, _f, C.c_char_p,
                                        C.c_size_t]),
 }
@@ -233,28 +240,37 @@ class Encoder:
             raise HipError(err.value.decode())
         return out[:batch]
 
-    def stage(self, ids, offsets):
-        """Uploads one wave (eg2_kfd_stage); launch()/collect() then run it."""
+    @property
+    def lanes(self):
+        """Waves the context keeps in flight (eg2_kfd_lanes)."""
+        return lib().eg2_kfd_lanes(self.ctx)
+
+    def stage(self, ids, offsets, lane=0):
+        """Uploads one wave to a lane (eg2_kfd_stage_lane); launch()/collect()
+        with the same lane then run it."""
         import numpy as np
 
-        self._ids = np.ascontiguousarray(ids, dtype=np.int32)
+        if not hasattr(self, "_staged"):
+            self._staged = {}
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
         offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
-        self._batch = len(offsets) - 1
+        batch = len(offsets) - 1
         err = C.create_string_buffer(1024)
-        if not lib().eg2_kfd_stage(self.ctx, self._ids.ctypes.data_as(_i32), offs, self._batch, err, 1024):
+        if not lib().eg2_kfd_stage_lane(self.ctx, lane, ids.ctypes.data_as(_i32), offs, batch, err, 1024):
+            raise HipError(err.value.decode())
+        self._staged[lane] = batch
+
+    def launch(self, repeats=1, lane=0):
+        err = C.create_string_buffer(1024)
+        if not lib().eg2_kfd_launch_lane(self.ctx, lane, repeats, err, 1024):
             raise HipError(err.value.decode())
 
-    def launch(self, repeats=1):
-        err = C.create_string_buffer(1024)
-        if not lib().eg2_kfd_launch_staged(self.ctx, repeats, err, 1024):
-            raise HipError(err.value.decode())
-
-    def collect(self):
+    def collect(self, lane=0):
         import numpy as np
 
-        out = np.zeros((self._batch, N_EMBD), dtype=np.float32)
+        out = np.zeros((self._staged[lane], N_EMBD), dtype=np.float32)
         err = C.create_string_buffer(1024)
-        if not lib().eg2_kfd_collect(self.ctx, out.ctypes.data_as(_f), err, 1024):
+        if not lib().eg2_kfd_collect_lane(self.ctx, lane, out.ctypes.data_as(_f), err, 1024):
             raise HipError(err.value.decode())
         return out
 

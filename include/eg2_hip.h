@@ -152,18 +152,39 @@ int eg2_hip_gemm_q8_geglu(const int8_t *xq, const float *xd, unsigned ldx, const
                           void *stream);
 
 /* ------------------------------------------------------------ executor phases
- * ei_gemma2_kfd_batch (gemma2_kfd.h) is stage + launch_staged(1) + collect.
- * The phases have no counterpart in the reference; they let a benchmark
- * time the device-resident forward apart from the host transfers. Same
- * validation, locking, poisoning and "HIP: ..." error contract as the batch
- * call. */
+ * A context has several lanes (EG2_HIP_LANES, 1..8, default 3): each lane
+ * is a stream with its own 2048-token workspace, pinned staging and
+ * hipGraphs, over the context's one copy of the weights, so waves on
+ * different lanes run on the device at the same time. ei_gemma2_kfd_batch
+ * (gemma2_kfd.h) takes any free lane and runs stage + launch(1) + collect
+ * on it; concurrent calls use separate lanes. The phases below have no
+ * counterpart in the reference; they let a benchmark time the
+ * device-resident forward apart from the host transfers, and a caller keep
+ * several waves in flight. Same validation, poisoning (a device failure on
+ * any lane fails the whole context) and "HIP: ..." error contract as the
+ * batch call; each call holds its lane for its duration. */
 
-/* Validates one wave, uploads its ids and packing metadata, and builds (once
- * per padded wave size) its hipGraph. */
-bool eg2_kfd_stage(void *ctx, const int32_t *ids, const size_t *offsets, size_t batch, char *err, size_t len);
+/* Number of lanes of ctx (0 for NULL). */
+unsigned eg2_kfd_lanes(void *ctx);
+/* Takes a lane from the context's pool of free lanes (blocking until one is
+ * free; ei_gemma2_kfd_batch uses the same pool) and returns its index (-1
+ * for NULL); eg2_kfd_release_lane returns it. A caller that keeps waves in
+ * flight on several lanes holds them this way, so that no concurrent batch
+ * call stages over its pending waves. */
+int eg2_kfd_acquire_lane(void *ctx);
+void eg2_kfd_release_lane(void *ctx, unsigned lane);
+/* Validates one wave, waits until the lane's previous wave is done with its
+ * staging buffers, uploads the ids and packing metadata, and builds (once
+ * per lane and padded wave size) its hipGraph. */
+bool eg2_kfd_stage_lane(void *ctx, unsigned lane, const int32_t *ids, const size_t *offsets, size_t batch, char *err,
+                        size_t len);
 /* Enqueues the staged wave's forward `repeats` times (no host copies, no wait). */
+bool eg2_kfd_launch_lane(void *ctx, unsigned lane, unsigned repeats, char *err, size_t len);
+/* Waits for the lane's wave and copies its [batch][768] embeddings to out. */
+bool eg2_kfd_collect_lane(void *ctx, unsigned lane, float *out, char *err, size_t len);
+/* The same on lane 0. */
+bool eg2_kfd_stage(void *ctx, const int32_t *ids, const size_t *offsets, size_t batch, char *err, size_t len);
 bool eg2_kfd_launch_staged(void *ctx, unsigned repeats, char *err, size_t len);
-/* Waits for the wave and copies its [batch][768] embeddings to out. */
 bool eg2_kfd_collect(void *ctx, float *out, char *err, size_t len);
 
 /* ------------------------------------------------------------ host helpers */

@@ -64,12 +64,14 @@ bool eg2_normalize_prefix(float *embedding, unsigned dims);
 
 /* Embeds a stream of texts: text i is ids[text_offsets[i] ..
  * text_offsets[i+1]) with output width dims[i]. The texts are packed into
- * waves by eg2_pack_waves, each wave runs through ei_gemma2_kfd_batch on
- * ctx (one hipGraph per padded wave size), and each embedding is written
- * to out[i * 768 ..] normalised to its prefix (eg2_normalize_prefix; the
- * values past dims[i] are zeroed). *n_waves (if not NULL) receives the
- * wave count. Returns false and a "HIP: ..." message on any error
- * (invalid text, unsupported dims, executor failure). */
+ * waves by eg2_pack_waves; the waves run on the context's lanes (taken
+ * from its pool, eg2_hip.h), wave w on the (w mod lanes)-th, so that up to
+ * that many waves are in flight, each exactly as ei_gemma2_kfd_batch would
+ * run it (one hipGraph per lane and padded wave size). Each embedding is
+ * written to out[i * 768 ..] normalised to its prefix
+ * (eg2_normalize_prefix; the values past dims[i] are zeroed). *n_waves (if
+ * not NULL) receives the wave count. Returns false and a "HIP: ..." message
+ * on any error (invalid text, unsupported dims, executor failure). */
 bool eg2_stream_embed(void *ctx, const int32_t *ids, const size_t *text_offsets, size_t n_texts, const unsigned *dims,
                       const eg2_batch_config *cfg, float *out, size_t *n_waves, char *err, size_t len);
 

@@ -15,8 +15,9 @@
  *      increasing, 1 <= offsets[batch] <= 2048, batch <= 2048, ids in
  *      [0, 262144). Writes out[batch * 768], each row L2-normalised. Returns
  *      false and writes "HIP: <reason>" on failure; after a device failure
- *      the context is poisoned and every later call fails. Calls are
- *      serialised internally.
+ *      the context is poisoned and every later call fails. Calls from
+ *      several threads are safe: each runs on one of the context's lanes
+ *      (eg2_hip.h), up to that many at the same time.
  */
 #ifndef EG2_KFD_H
 #define EG2_KFD_H

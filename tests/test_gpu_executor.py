@@ -108,6 +108,87 @@ def test_env_flags_are_validated(eg2, small_model):
         del os.environ["EG2_HIP_GRAPH"]
 
 
+def test_env_lanes(eg2, small_model):
+    for bad in ("0", "9", "x", ""):
+        os.environ["EG2_HIP_LANES"] = bad
+        try:
+            with pytest.raises(eg2.HipError, match="EG2_HIP_LANES must be 1..8"):
+                eg2.Encoder(small_model)
+        finally:
+            del os.environ["EG2_HIP_LANES"]
+    os.environ["EG2_HIP_LANES"] = "1"
+    try:
+        one = eg2.Encoder(small_model)
+    finally:
+        del os.environ["EG2_HIP_LANES"]
+    try:
+        assert one.lanes == 1
+        ids = np.arange(50, dtype=np.int32)
+        assert np.isfinite(one.batch(ids, [0, 20, 50])).all()
+    finally:
+        one.close()
+
+
+def waves_for_lanes(n):
+    rng = np.random.default_rng(11)
+    out = []
+    for i in range(n):
+        lens = [[300, 5], [2048], [1, 1, 1, 40], [900, 700, 64], [17]][i % 5]
+        out.append((rng.integers(0, OL.VOCAB, sum(lens)).astype(np.int32), np.concatenate([[0], np.cumsum(lens)])))
+    return out
+
+
+def test_lanes_in_flight_match_one_at_a_time(small_encoder):
+    """Different waves staged on every lane and launched together (up to
+    `lanes` in flight, some twice in a row) give exactly the embeddings each
+    wave gets alone."""
+    L = small_encoder.lanes
+    assert L >= 2
+    waves = waves_for_lanes(L)
+    alone = [small_encoder.batch(ids, offs) for ids, offs in waves]
+    for lane, (ids, offs) in enumerate(waves):
+        small_encoder.stage(ids, offs, lane)
+    for r in range(2):
+        for lane in range(L):
+            small_encoder.launch(1 + r, lane)
+    for lane in range(L):
+        assert np.array_equal(small_encoder.collect(lane), alone[lane])
+    # Restaging a lane whose wave was never collected waits for it first.
+    ids, offs = waves[0]
+    small_encoder.stage(ids, offs, 1)
+    small_encoder.launch(1, 1)
+    small_encoder.stage(waves[1][0], waves[1][1], 1)
+    small_encoder.launch(1, 1)
+    assert np.array_equal(small_encoder.collect(1), alone[1])
+
+
+def test_concurrent_batch_calls(small_encoder):
+    """Threads calling ei_gemma2_kfd_batch at once run on separate lanes;
+    every result equals the one-at-a-time result."""
+    import threading
+
+    waves = waves_for_lanes(6)
+    alone = [small_encoder.batch(ids, offs) for ids, offs in waves]
+    errors = []
+
+    def worker(k):
+        try:
+            for rep in range(3):
+                j = (k + rep) % len(waves)
+                got = small_encoder.batch(*waves[j])
+                if not np.array_equal(got, alone[j]):
+                    errors.append((k, rep, j))
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(5)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors
+
+
 @pytest.fixture(scope="module")
 def full_model(eg2, tmp_path_factory):
     """Config 4: 24 layers, full attention with RoPE base 1e4, dense head."""
