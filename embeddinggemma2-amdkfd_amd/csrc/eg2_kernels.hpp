@@ -49,7 +49,7 @@ struct AttentionCounts {
 };
 AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges);
 AttentionCounts attention_capacity(size_t tokens, size_t batch);
-constexpr size_t kAttentionPartialFloats = 3 * (16 * 64 * 4 + 64 * 2);  // per slot
+constexpr size_t kAttentionPartialFloats = 2 * 3 * (16 * 64 * 4 + 64 * 2);  // per slot: 2 query blocks x 3 heads
 
 // V^T column of every token: each sequence starts at a multiple of 32,
 // consecutive tokens take consecutive columns. Returns the column count

@@ -15,12 +15,15 @@
 // attention. Softmax runs in fp32 (online, one pass over 32-key tiles) in
 // log2 units with the hardware exp2.
 //
-// Work: query tiles of up to 16 tokens of ONE sequence (host-built list:
-// first query, end, sequence start, sequence end); the key tiles of a query
-// tile start at its sequence's first token, so a query's arithmetic depends
-// only on its own sequence and packed and single-sequence calls give
-// bit-identical results. One workgroup per query tile, one wave per query
-// head; the three waves share each 32-key tile of K and V^T in LDS.
+// Work: query tiles of up to 32 tokens of ONE sequence (host-built list:
+// first query, end, sequence start, sequence end, key chunk, partial slot);
+// the query and key tiles of a sequence start at its first token, so a
+// query's arithmetic depends only on its own sequence and packed and
+// single-sequence calls give bit-identical results. One workgroup of six
+// waves per query tile: wave w computes head w % 3 for the 16-query block
+// w / 3; all six share each 32-key tile of K and V^T in LDS, so a K/V byte
+// brought in serves 32 queries of 3 heads. The waves of a second block that
+// a short tile does not have only move data.
 //
 // Data movement: K rows ([hi 256 | lo 256] fp16 per token) and V^T rows
 // (V transposed by the QK-norm/RoPE kernel into [hi|lo][256 dims][column],
@@ -47,21 +50,22 @@ namespace eg2 {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kQTile = 16;   // queries per work tile (one 16x16x32 MFMA column block)
+constexpr int kQBlock = 16;           // queries per wave (one 16x16x32 MFMA column block)
+constexpr int kQTile = 2 * kQBlock;    // queries per work tile (workgroup)
 constexpr int kKvTile = 32;  // keys per LDS stage (one 32-deep MFMA reduction)
 constexpr int kKStage = kKvTile * 2 * kHeadDim * 2;  // [key][hi|lo][256] fp16 = 32 KB
 constexpr int kVStage = 2 * kHeadDim * kKvTile * 2;  // [hi|lo][dim][32 keys] fp16 = 32 KB
 constexpr int kStage = kKStage + kVStage;
 constexpr float kLog2e = 1.4426950408889634f;
-// A workgroup runs 3 compute waves (one per query head) and 3 more that
-// only move K/V tiles: LDS DMA throughput grows with the number of waves
-// issuing it (measured on this part: 5.1, 9.5 and 14.4 TB/s for 3, 6 and 12
-// waves streaming 64 KB tiles, one workgroup per CU), and the 64 DMA
-// instructions of a tile are spread over all six.
-constexpr int kComputeWaves = kHeads, kWaves = 6;
+// A workgroup runs 6 waves, 3 heads x 2 query blocks. All six issue the
+// K/V DMA: its throughput grows with the number of waves issuing it
+// (measured on this part: 5.1, 9.5 and 14.4 TB/s for 3, 6 and 12 waves
+// streaming 64 KB tiles, one workgroup per CU), and the 64 DMA instructions
+// of a tile are spread over all six.
+constexpr int kWaves = 2 * kHeads;
 constexpr int kDmaPerWave = (kKvTile + kWaves - 1) / kWaves;  // 6 K and 6 V instructions
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;           // item writes the final context
-constexpr int kPartFloats = 16 * 64 * 4 + 64 * 2;   // per (slot, head): acc in lane order, then (m, l)
+constexpr int kPartFloats = 16 * 64 * 4 + 64 * 2;   // per (slot, block, head): acc in lane order, then (m, l)
 constexpr uint32_t kSplitLen = 256;  // longer sequences split their keys into chunks ...
 constexpr uint32_t kMaxChunks = 4;   // ... of at least kSplitLen keys, at most this many
 
@@ -146,8 +150,7 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
   __shared__ __align__(16) unsigned char lds[2 * kStage];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool compute = w < kComputeWaves;
-  const int head = compute ? w : 0;
+  const int head = w % kHeads, qb = w / kHeads;
   const int qi = lane & 15, grp = lane >> 4;
   const uint32_t count = *item_count;
   const unsigned lds0 = (unsigned)(uintptr_t)lds;
@@ -163,32 +166,23 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     // sit a multiple of 32 keys after seg_lo) and its partial-result slot.
     const uint32_t c_hi = min(kc.y, seg_hi), c_lo = min(max(kc.x, seg_lo), c_hi);
     const uint32_t slot = kc.z;
-    const bool active = q0 + qi < q_end;
-    const uint32_t t = active ? q0 + qi : (q_end > 0 ? q_end - 1 : 0);
+    // This wave's 16 queries; a block past the tile's end only moves data.
+    const uint32_t qw = q0 + kQBlock * qb;
+    const bool compute = qw < q_end;
+    const bool active = qw + qi < q_end;
+    const uint32_t t = active ? qw + qi : (q_end > 0 ? q_end - 1 : 0);
 
-    // Key range of this lane's query (kernels.c:330-336 in packed coordinates).
-    uint32_t lo = seg_lo, hi = seg_hi;
-    if (window > 0) {
-      const uint32_t half = (uint32_t)(window / 2);
-      if (t > half && t - half > lo) lo = t - half;
-      if (t + half + 1 < hi) hi = t + half + 1;
-    }
-    // Union and intersection of the tile's key ranges (every lane group
-    // holds the same 16 queries); without a window both are the sequence.
-    uint32_t kv_lo = seg_lo, kv_hi = seg_hi, in_lo = seg_lo, in_hi = seg_hi;
-    if (window > 0) {
-      kv_lo = active ? lo : 0xFFFFFFFFu;
-      kv_hi = active ? hi : 0u;
-      in_lo = active ? lo : 0u;
-      in_hi = active ? hi : 0xFFFFFFFFu;
-#pragma unroll
-      for (int mk = 8; mk >= 1; mk >>= 1) {
-        kv_lo = min(kv_lo, (uint32_t)__shfl_xor((int)kv_lo, mk, 64));
-        kv_hi = max(kv_hi, (uint32_t)__shfl_xor((int)kv_hi, mk, 64));
-        in_lo = max(in_lo, (uint32_t)__shfl_xor((int)in_lo, mk, 64));
-        in_hi = min(in_hi, (uint32_t)__shfl_xor((int)in_hi, mk, 64));
-      }
-    }
+    // Key range of query u (kernels.c:330-336 in packed coordinates); both
+    // ends are nondecreasing in u.
+    const uint32_t half = (uint32_t)(window / 2);
+    auto range_lo = [&](uint32_t u) { return window > 0 && u > half && u - half > seg_lo ? u - half : seg_lo; };
+    auto range_hi = [&](uint32_t u) { return window > 0 && u + half + 1 < seg_hi ? u + half + 1 : seg_hi; };
+    uint32_t lo = range_lo(t), hi = range_hi(t);
+    // Union and intersection of the key ranges of the tile's queries
+    // q0 .. q_end - 1 (the same for all six waves); without a window both
+    // are the sequence.
+    const uint32_t q_last = q_end > q0 ? q_end - 1 : q0;
+    uint32_t kv_lo = range_lo(q0), kv_hi = range_hi(q_last), in_lo = range_lo(q_last), in_hi = range_hi(q0);
     kv_lo = __builtin_amdgcn_readfirstlane(max(kv_lo, c_lo));
     kv_hi = __builtin_amdgcn_readfirstlane(min(kv_hi, c_hi));
     in_lo = __builtin_amdgcn_readfirstlane(max(in_lo, c_lo));
@@ -366,7 +360,7 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       // Partial result of this key chunk: the unnormalised context and the
       // running max / sum, in the lane order of the MFMA layout (16-byte
       // stores, fully coalesced); attention_merge_kernel combines the parts.
-      float* part = partials + ((size_t)slot * kHeads + head) * kPartFloats;
+      float* part = partials + (((size_t)slot * 2 + qb) * kHeads + head) * kPartFloats;
 #pragma unroll
       for (int db = 0; db < 16; ++db) reinterpret_cast<floatx4*>(part)[db * 64 + lane] = acc[db];
       reinterpret_cast<float2*>(part + 16 * 64 * 4)[lane] = make_float2(m_run, l_run);
@@ -377,8 +371,8 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 }
 
 // Merges the key-chunk partials of split query tiles. One workgroup per
-// (query tile, quarter of the head dimension), one wave per head, lanes in
-// the attention kernel's MFMA layout; a quarter is 4 of the 16 16-dim
+// (query tile, 16-query block, quarter of the head dimension), one wave per
+// head, lanes in the attention kernel's MFMA layout; a quarter is 4 of the 16 16-dim
 // blocks, i.e. 2 whole Q8_0 blocks, so it quantizes on its own. With m =
 // max over parts of the running maxima (log2 units), l = sum_p l_p
 // 2^(m_p - m) and acc = sum_p acc_p 2^(m_p - m), in part order (a
@@ -392,16 +386,17 @@ attention_merge_kernel(const uint4* __restrict__ merges, const uint32_t* __restr
                        float* __restrict__ cd) {
   const int lane = threadIdx.x & 63, head = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int qi = lane & 15, grp = lane >> 4;
-  const uint32_t count = 4 * *merge_count;
+  const uint32_t count = 8 * *merge_count;
   for (uint32_t wi = blockIdx.x; wi < count; wi += gridDim.x) {
-    const uint4 mg = merges[wi >> 2];
-    const int quarter = (int)(wi & 3);
-    const uint32_t q_end = min(mg.y, (uint32_t)rows), q0 = mg.x, first = mg.z;
+    const uint4 mg = merges[wi >> 3];
+    const int quarter = (int)(wi & 3), qb = (int)((wi >> 2) & 1);
+    const uint32_t q_end = min(mg.y, (uint32_t)rows), qw = mg.x + kQBlock * qb, first = mg.z;
+    if (qw >= q_end) continue;  // a tile with a single 16-query block
     const uint32_t parts = min(mg.w, (uint32_t)kMaxParts);
-    const bool active = q0 + qi < q_end;
-    const uint32_t t = active ? q0 + qi : (q_end > 0 ? q_end - 1 : 0);
-    const float* base = partials + ((size_t)first * kHeads + head) * kPartFloats;
-    const size_t stride = (size_t)kHeads * kPartFloats;  // next part
+    const bool active = qw + qi < q_end;
+    const uint32_t t = active ? qw + qi : q_end - 1;
+    const float* base = partials + (((size_t)first * 2 + qb) * kHeads + head) * kPartFloats;
+    const size_t stride = (size_t)2 * kHeads * kPartFloats;  // next part
     float2 ml[kMaxParts];
 #pragma unroll
     for (int p = 0; p < kMaxParts; ++p)
@@ -476,15 +471,17 @@ AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint3
 }
 
 AttentionCounts attention_capacity(size_t tokens, size_t batch) {
-  // Items: at most ceil(n/16) per unsplit sequence (<= n + 15 in total over
-  // a wave... bounded by tokens + batch) and ceil(n/16) ceil(n/256) <= n
-  // for a split one; slots and merges peak when one sequence holds every
-  // token.
-  const size_t tiles = (tokens + kQTile - 1) / kQTile;
+  // Items: ceil(n/32) c(n) <= n per sequence (c(n) <= 4 chunks, and n > 256
+  // when c(n) > 1), so at most `tokens`; `batch` more keeps room for
+  // rounding. Merges: one per query tile of a split sequence; tiles round
+  // up per sequence, so at most ceil(tokens/32) + (the number of sequences
+  // longer than kSplitLen that fit); slots: at most kMaxChunks per merge.
+  const size_t split_seqs = tokens / (kSplitLen + 1);
+  const size_t tiles = (tokens + kQTile - 1) / kQTile + split_seqs;
   AttentionCounts c;
   c.items = (unsigned)(tokens + batch);
-  c.slots = (unsigned)(tokens > kSplitLen ? tiles * key_chunks(tokens) : 0);
-  c.merges = (unsigned)(tokens > kSplitLen ? tiles : 0);
+  c.merges = (unsigned)(split_seqs ? tiles : 0);
+  c.slots = (unsigned)(split_seqs ? tiles * key_chunks(tokens) : 0);
   return c;
 }
 

@@ -99,6 +99,14 @@ unsigned eg2_attention_items(const size_t* offsets, size_t batch, uint32_t* item
 
 size_t eg2_attention_partial_floats(void) { return eg2::kAttentionPartialFloats; }
 
+void eg2_attention_capacity(size_t tokens, size_t batch, unsigned* counts) {
+  if (!counts) return;
+  const eg2::AttentionCounts c = eg2::attention_capacity(tokens, batch);
+  counts[0] = c.items;
+  counts[1] = c.merges;
+  counts[2] = c.slots;
+}
+
 size_t eg2_attention_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
   if (!offsets || !vcol) return 0;
   return eg2::build_vt_columns(offsets, batch, vcol);

@@ -114,6 +114,7 @@ SIGNATURES = {
     "eg2_hip_attention_merge": (C.c_int, [_vp, _vp, _u, _vp, _u, _vp, _vp, _vp]),
     "eg2_attention_items": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp, _vp, _vp]),
     "eg2_attention_partial_floats": (C.c_size_t, []),
+    "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_uint)]),
     "eg2_attention_vt_columns": (C.c_size_t, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),

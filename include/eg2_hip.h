@@ -86,7 +86,8 @@ int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count,
                             unsigned rows, int8_t *cq, float *cd, void *stream);
 
 /* Host: the work lists of a packed wave with sequences [offsets[s],
- * offsets[s+1]): per query tile of up to 16 tokens one item per key chunk
+ * offsets[s+1]): per query tile of up to 32 tokens (from the sequence
+ * start; one workgroup of the attention kernel) one item per key chunk
  * {first query, end, sequence start, sequence end, chunk start, chunk end,
  * slot or 0xFFFFFFFF, 0} (a sequence of n > 256 tokens has c = min(ceil(n
  * / 256), 4) chunks of ceil(n / c) keys rounded up to 32, the last one
@@ -94,11 +95,18 @@ int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count,
  * chunk and no slot), and per split tile one merge record {first query,
  * end, first slot, parts}. counts[0..2] = items, merges, slots. `items` needs room for
  * 8 * (offsets[batch] + batch) entries, `merges` for 4 * ceil(offsets[batch]
- * / 16). Returns the item count. */
+ * / 32). Returns the item count. */
 unsigned eg2_attention_items(const size_t *offsets, size_t batch, uint32_t *items, uint32_t *merges, unsigned *counts);
 
-/* Floats of one partial-result slot (3 heads x (16 x 256 + 2 x 64)). */
+/* Floats of one partial-result slot (2 blocks of 16 queries x 3 heads x
+ * (16 x 256 + 2 x 64)). */
 size_t eg2_attention_partial_floats(void);
+
+/* Host: counts[0..2] = the most items, merge records and partial slots that
+ * eg2_attention_items can produce for any packing of `tokens` tokens into
+ * at most `batch` sequences (the sizes the executor allocates for a
+ * 2048-token wave plus its padding sequence). */
+void eg2_attention_capacity(size_t tokens, size_t batch, unsigned *counts);
 
 /* Host: the transposed-v column of every token (vcol[offsets[batch]]):
  * each sequence starts at a multiple of 32 and its tokens take consecutive

@@ -96,7 +96,7 @@ def test_vt_columns_align_each_sequence(eg2):
 
 def test_attention_items_cover_each_sequence(eg2):
     """Every (query, key) pair of a sequence is covered by exactly one item;
-    query tiles are 16 tokens from the sequence start; a sequence of n > 256
+    query tiles are 32 tokens from the sequence start; a sequence of n > 256
     tokens splits its keys into c = min(ceil(n / 256), 4) chunks of
     ceil(n / c) keys rounded up to 32 (aligned to its start) with
     consecutive partial slots and one merge record per query tile."""
@@ -107,7 +107,7 @@ def test_attention_items_cover_each_sequence(eg2):
     used_slots = []
     for q0, q1, lo, hi, k0, k1, slot, zero in items.astype(np.int64):
         s = seqs.index((lo, hi))
-        assert lo <= q0 < q1 <= hi and q1 - q0 <= 16 and (q0 - lo) % 16 == 0 and zero == 0
+        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0 and zero == 0
         n = hi - lo
         c = min(-(-n // 256), 4)
         ck = -(-(-(-n // c)) // 32) * 32
@@ -122,12 +122,37 @@ def test_attention_items_cover_each_sequence(eg2):
     assert sorted(used_slots) == list(range(slots))
     # merges: one per query tile of a split sequence, slots first..first+parts-1
     split = [(lo, hi) for lo, hi in seqs if hi - lo > 256]
-    assert len(merges) == sum((hi - lo + 15) // 16 for lo, hi in split)
+    assert len(merges) == sum((hi - lo + 31) // 32 for lo, hi in split)
     for q0, q1, first, parts in merges.astype(np.int64):
         lo, hi = next((lo, hi) for lo, hi in split if lo <= q0 < hi)
         assert parts == min((hi - lo + 255) // 256, 4)
         tile_items = [it for it in items if it[0] == q0]
         assert sorted(int(it[6]) for it in tile_items) == list(range(first, first + parts))
+
+
+def test_attention_capacity_bounds_every_packing(eg2):
+    """The executor sizes its work lists with eg2_attention_capacity(2080,
+    2049) (a 2048-token wave plus a padding sequence of up to 31 rows): no
+    packing may exceed it. Every packing of equal sequences (the per-sequence
+    rounding of tiles and chunks is worst there) and every remainder, each
+    followed by its padding sequence."""
+    import ctypes as C
+
+    cap = (C.c_uint * 3)()
+    eg2.lib().eg2_attention_capacity(2080, 2049, cap)
+    cap = list(cap)
+    worst = [0, 0, 0]
+    for L in range(1, 2049):
+        for total in (2048, 2048 - L // 2, 2017):
+            lens = [L] * (total // L) + ([total % L] if total % L else [])
+            n = sum(lens)
+            pad = (-n) % 32
+            offs = np.concatenate([[0], np.cumsum(lens + ([pad] if pad else []))])
+            items, merges, slots = eg2.attention_items(offs)
+            got = [len(items), len(merges), slots]
+            worst = [max(a, b) for a, b in zip(worst, got)]
+            assert all(g <= c for g, c in zip(got, cap)), (L, total, got, cap)
+    print("worst", worst, "capacity", cap)
 
 
 @pytest.mark.parametrize("base", [10000.0, 1000000.0])
