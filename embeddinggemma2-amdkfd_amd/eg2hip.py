@@ -146,6 +146,11 @@ SIGNATURES = {
     "eg2_kfd_launch_staged": (C.c_bool, [C.c_void_p, C.c_uint, C.c_char_p, C.c_size_t]),
     "eg2_kfd_collect": (C.c_bool, [C.c_void_p, _f, C.c_char_p, C.c_size_t]),
     "eg2_kfd_lanes": (C.c_uint, [C.c_void_p]),
+    "eg2_f32_to_chars": (C.c_size_t, [C.c_char_p, C.c_float]),
+    "eg2_base64_f32": (C.c_size_t, [_f, C.c_size_t, C.c_char_p]),
+    "eg2_embeddings_response_bound": (C.c_size_t, [C.c_size_t, C.c_uint, C.c_size_t]),
+    "eg2_embeddings_response": (C.c_size_t, [_f, C.c_size_t, C.c_uint, C.c_int, C.c_int, C.c_char_p, C.c_size_t,
+                                             C.c_size_t, C.c_char_p, C.c_size_t]),
     "eg2_kfd_acquire_lane": (C.c_int, [C.c_void_p]),
     "eg2_kfd_release_lane": (None, [C.c_void_p, C.c_uint]),
     "eg2_kfd_stage_lane": (C.c_bool, [C.c_void_p, C.c_uint, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p,
@@ -419,6 +424,40 @@ def q8_geglu_weight_tiles(gate_u8, up_u8, ff, k):
     if lib().eg2_q8_geglu_weight_tiles(g.ctypes.data, u.ctypes.data, ff, k, wq.ctypes.data, wd.ctypes.data):
         raise ValueError("ff and k must be multiples of 32")
     return wq, wd
+
+
+def f32_to_chars(value):
+    """eg2_f32_to_chars: the shortest round-trip text of a float32 (None
+    for a non-finite value)."""
+    buf = C.create_string_buffer(32)
+    n = lib().eg2_f32_to_chars(buf, C.c_float(value))
+    return buf.raw[:n].decode() if n else None
+
+
+def base64_f32(values):
+    """eg2_base64_f32 of a float32 array."""
+    import numpy as np
+
+    v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    buf = C.create_string_buffer(4 * ((4 * v.size + 2) // 3) + 1)
+    n = lib().eg2_base64_f32(v.ctypes.data_as(_f), v.size, buf)
+    return buf.raw[:n].decode()
+
+
+def embeddings_response(embeddings, dims, api="ollama", encoding="float", model="", prompt_tokens=0):
+    """eg2_embeddings_response: the response body for [n, 768] embeddings
+    (normalised to their first `dims` values on a copy)."""
+    import numpy as np
+
+    e = np.array(embeddings, dtype=np.float32, copy=True, order="C").reshape(-1, N_EMBD)
+    m = model.encode() if isinstance(model, str) else bytes(model)
+    cap = lib().eg2_embeddings_response_bound(e.shape[0], dims, len(m))
+    buf = C.create_string_buffer(cap + 1)
+    n = lib().eg2_embeddings_response(e.ctypes.data_as(_f), e.shape[0], dims, {"ollama": 0, "openai": 1}[api],
+                                      {"float": 0, "base64": 1}[encoding], m, len(m), prompt_tokens, buf, cap + 1)
+    if n == 0:
+        raise ValueError("embedding response failed (dims, non-finite value)")
+    return buf.raw[:n].decode()
 
 
 def attention_items(offsets):

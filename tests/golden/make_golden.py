@@ -1,7 +1,9 @@
 """Writes tests/golden/reference_vectors.npz: seeded inputs and the outputs of
 the reference's own CPU functions (vendor/embeddinggemma.c/src/quants.c,
 kernels.c and the Q8_0 x Q8_0 `mm` of gemma2.c), compiled from the reference
-tree by oracle/Makefile into oracle/_ref/libref.so.
+tree by oracle/Makefile into oracle/_ref/libref.so; and
+tests/golden/float_text.npz, float32 values and their text by the
+reference's float_format.c.
 
 Run where the reference tree is present:
     make -C oracle ref && python tests/golden/make_golden.py
@@ -138,6 +140,39 @@ def main():
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
+    float_text(r, rng)
+
+
+def float_text(r, rng):
+    """tests/golden/float_text.npz: float32 bit patterns and their text by the
+    reference's ei_f32_to_chars (float_format.c:276-308): specials, binade
+    bottoms and tops, subnormals, powers of ten, random bit patterns and
+    embedding-like values; strings as one byte blob with offsets."""
+    r.ei_f32_to_chars.restype = C.c_size_t
+    r.ei_f32_to_chars.argtypes = [C.c_char_p, C.c_float]
+    special = [0x00000000, 0x80000000, 0x00000001, 0x80000001, 0x007FFFFF, 0x00800000, 0x00800001, 0x7F7FFFFF,
+               0xFF7FFFFF, 0x3F800000, 0x3F7FFFFF, 0x3F800001, 0x4B000000, 0x4B7FFFFF, 0x3DCCCCCD, 0x3E800000]
+    edges = []
+    for ef in range(1, 255, 3):  # binade bottoms and their neighbours
+        base = ef << 23
+        edges += [base, base + 1, base - 1 if ef > 1 else base + 2, base | 0x7FFFFF]
+    tens = np.float32(10.0) ** np.arange(-45, 39, dtype=np.float64)
+    tens = tens[np.isfinite(tens)].astype(np.float32).view(np.uint32).tolist()
+    halves = (np.arange(1, 2000, dtype=np.float32) * np.float32(0.5)).view(np.uint32).tolist()
+    rand_bits = rng.integers(0, 2 ** 32, 12000, dtype=np.uint64).astype(np.uint32).tolist()
+    emb = (rng.standard_normal(12000) / np.sqrt(768)).astype(np.float32).view(np.uint32).tolist()
+    bits = np.array(special + edges + tens + halves + rand_bits + emb, dtype=np.uint32)
+    bits = bits[np.isfinite(bits.view(np.float32))]
+    buf = C.create_string_buffer(64)
+    texts, offs = [], [0]
+    for b in bits:
+        n = r.ei_f32_to_chars(buf, float(np.uint32(b).view(np.float32)))
+        texts.append(buf.raw[:n])
+        offs.append(offs[-1] + n)
+    path = os.path.join(HERE, "float_text.npz")
+    np.savez_compressed(path, bits=bits, text=np.frombuffer(b"".join(texts), np.uint8),
+                        offsets=np.array(offs, np.int64))
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(bits)} values)")
 
 
 if __name__ == "__main__":
