@@ -147,6 +147,12 @@ SIGNATURES = {
     "eg2_kfd_collect": (C.c_bool, [C.c_void_p, _f, C.c_char_p, C.c_size_t]),
     "eg2_kfd_lanes": (C.c_uint, [C.c_void_p]),
     "eg2_f32_to_chars": (C.c_size_t, [C.c_char_p, C.c_float]),
+    "eg2_tokenizer_create": (C.c_void_p, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "eg2_tokenizer_free": (None, [C.c_void_p]),
+    "eg2_tokenizer_text_to_id": (C.c_int32, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "eg2_tokenize": (C.c_size_t, [C.c_void_p, C.c_char_p, C.c_size_t, C.c_bool, C.c_bool, _i32, C.c_size_t]),
+    "eg2_tokenize_batch": (C.c_size_t, [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t), C.c_size_t, C.c_bool,
+                                        C.c_bool, _i32, C.c_size_t, C.POINTER(C.c_size_t), C.c_uint]),
     "eg2_base64_f32": (C.c_size_t, [_f, C.c_size_t, C.c_char_p]),
     "eg2_embeddings_response_bound": (C.c_size_t, [C.c_size_t, C.c_uint, C.c_size_t]),
     "eg2_embeddings_response": (C.c_size_t, [_f, C.c_size_t, C.c_uint, C.c_int, C.c_int, C.c_char_p, C.c_size_t,
@@ -212,6 +218,60 @@ class Gguf:
         if self.g is not None:
             lib().eg2_gguf_close(C.byref(self.g))
             self.g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Tokenizer:
+    """eg2_tokenizer over the tokenizer.ggml.* keys of a GGUF file."""
+
+    def __init__(self, gguf_path):
+        self.gguf = Gguf(gguf_path)
+        err = C.create_string_buffer(512)
+        self.tok = lib().eg2_tokenizer_create(C.byref(self.gguf.g), err, 512)
+        if not self.tok:
+            raise HipError(err.value.decode())
+
+    def encode(self, text, add_special=True, parse_special=False):
+        """Token ids of `text` (bytes or str) as an int32 array."""
+        import numpy as np
+
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = lib().eg2_tokenize(self.tok, b, len(b), add_special, parse_special, None, 0)
+        ids = np.zeros(max(n, 1), np.int32)
+        lib().eg2_tokenize(self.tok, b, len(b), add_special, parse_special, ids.ctypes.data_as(_i32), n)
+        return ids[:n]
+
+    def encode_batch(self, texts, add_special=True, parse_special=False, threads=0):
+        """(ids, offsets) of several texts packed back to back."""
+        import numpy as np
+
+        bs = [t.encode() if isinstance(t, str) else bytes(t) for t in texts]
+        toffs = (C.c_size_t * (len(bs) + 1))(*np.concatenate([[0], np.cumsum([len(b) for b in bs])]).astype(int))
+        joined = b"".join(bs)
+        cap = 4 * len(joined) + 4 * len(bs) + 16
+        ids = np.zeros(cap, np.int32)
+        ioffs = (C.c_size_t * (len(bs) + 1))()
+        n = lib().eg2_tokenize_batch(self.tok, joined, toffs, len(bs), add_special, parse_special,
+                                     ids.ctypes.data_as(_i32), cap, ioffs, threads)
+        if n == (1 << 64) - 1:
+            raise HipError("token capacity exceeded")
+        return ids[:n], np.array(list(ioffs), np.int64)
+
+    def text_to_id(self, text):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        return lib().eg2_tokenizer_text_to_id(self.tok, b, len(b))
+
+    def close(self):
+        if getattr(self, "tok", None):
+            lib().eg2_tokenizer_free(self.tok)
+            self.tok = None
+        if getattr(self, "gguf", None):
+            self.gguf.close()
 
     def __del__(self):
         try:

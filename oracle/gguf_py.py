@@ -92,3 +92,37 @@ def oracle_model(path):
         m["dense_2"] = np.ascontiguousarray(t["dense_2.weight"][2])
         m["dense_3"] = np.ascontiguousarray(t["dense_3.weight"][2])
     return m
+
+
+def write_kv(path, kvs):
+    """GGUF v3 file holding key-values only (no tensors), for the tokenizer's
+    keys. kvs: (key, kind, value) with kind 'str', 'u32', 'bool', 'arr_str'
+    (list of bytes), 'arr_f32' or 'arr_i32'."""
+    out = [struct.pack("<IIQQ", 0x46554747, 3, 0, len(kvs))]
+
+    def s(b):
+        b = b.encode() if isinstance(b, str) else bytes(b)
+        return struct.pack("<Q", len(b)) + b
+
+    for key, kind, val in kvs:
+        out.append(s(key))
+        if kind == "str":
+            out.append(struct.pack("<I", 8) + s(val))
+        elif kind == "u32":
+            out.append(struct.pack("<II", 4, int(val)))
+        elif kind == "bool":
+            out.append(struct.pack("<IB", 7, 1 if val else 0))
+        elif kind == "arr_str":
+            out.append(struct.pack("<IIQ", 9, 8, len(val)) + b"".join(s(v) for v in val))
+        elif kind == "arr_f32":
+            a = np.ascontiguousarray(val, dtype="<f4")
+            out.append(struct.pack("<IIQ", 9, 6, a.size) + a.tobytes())
+        elif kind == "arr_i32":
+            a = np.ascontiguousarray(val, dtype="<i4")
+            out.append(struct.pack("<IIQ", 9, 5, a.size) + a.tobytes())
+        else:
+            raise ValueError(kind)
+    blob = b"".join(out)
+    blob += b"\0" * ((-len(blob)) % 32)
+    with open(path, "wb") as f:
+        f.write(blob)

@@ -37,3 +37,50 @@ void ref_embed_row(const void *table, int vocab, int row, float *out) {
     t.data = table;
     ei_dequantize_row_q8_0_scaled(&t, row, sqrtf((float)EI_N_EMBD), out);
 }
+
+/* The reference tokenizer (tokenizer.c) over the tokenizer keys of a GGUF
+ * file, read as model.c:111-120 reads them; the merge mode when the file
+ * has tokenizer.ggml.merges (the embeddinggemma2 profile). */
+#include "tokenizer.h"
+
+typedef struct {
+    ei_model m;
+    ei_tokenizer tok;
+} ref_tok;
+
+void *ref_tokenizer_open(const char *path) {
+    ref_tok *h = calloc(1, sizeof *h);
+    ei_gguf_open(&h->m.gguf, path);
+    const ei_gguf *g = &h->m.gguf;
+    h->m.embeddinggemma2 = ei_gguf_kv(g, "tokenizer.ggml.merges", false) != NULL;
+    h->m.tok_tokens = ei_gguf_kv(g, "tokenizer.ggml.tokens", true);
+    h->m.tok_scores = ei_gguf_kv(g, "tokenizer.ggml.scores", true);
+    h->m.tok_types = ei_gguf_kv(g, "tokenizer.ggml.token_type", true);
+    h->m.bos_id = (int32_t)ei_gguf_kv_u64(g, "tokenizer.ggml.bos_token_id", 2);
+    h->m.eos_id = (int32_t)ei_gguf_kv_u64(g, "tokenizer.ggml.eos_token_id", 1);
+    h->m.unk_id = (int32_t)ei_gguf_kv_u64(g, "tokenizer.ggml.unknown_token_id", 3);
+    h->m.pad_id = (int32_t)ei_gguf_kv_u64(g, "tokenizer.ggml.padding_token_id", 0);
+    h->m.add_bos = ei_gguf_kv_bool(g, "tokenizer.ggml.add_bos_token", true);
+    h->m.add_eos = ei_gguf_kv_bool(g, "tokenizer.ggml.add_eos_token", false);
+    h->m.add_space_prefix = ei_gguf_kv_bool(g, "tokenizer.ggml.add_space_prefix", true);
+    ei_tokenizer_init(&h->tok, &h->m);
+    return h;
+}
+
+size_t ref_tokenize(void *handle, const char *text, size_t len, int add_special, int parse_special, int32_t *ids,
+                    size_t cap) {
+    ref_tok *h = handle;
+    ei_tokens t;
+    ei_tokenize_spm(&h->tok, text, len, add_special != 0, parse_special != 0, &t);
+    for (size_t i = 0; i < t.n && i < cap; i++) ids[i] = t.ids[i];
+    const size_t n = t.n;
+    ei_tokens_free(&t);
+    return n;
+}
+
+void ref_tokenizer_close(void *handle) {
+    ref_tok *h = handle;
+    ei_tokenizer_free(&h->tok);
+    ei_gguf_close(&h->m.gguf);
+    free(h);
+}

@@ -141,6 +141,160 @@ def main():
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
     float_text(r, rng)
+    tokenizer_vectors(r)
+
+
+SP = "\u2581"
+ALPHABET = list("abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOP0123456789.,;:!?'-()") + ["é", "ü", "中", "文", "😀",
+                                                                                   "\t", "\n", SP]
+COMBOS = [(1, 0), (1, 1), (0, 0), (0, 1)]  # (add_special, parse_special)
+
+
+def synth_vocab(rng, ranked, words):
+    """A seeded SentencePiece-style vocabulary exercising every branch of the
+    reference tokenizer: control / unknown / user-defined specials (one a
+    prefix of another, one empty piece), byte pieces (some bytes only as raw
+    one-byte pieces), single characters (some missing, so they fall back to
+    bytes), corpus substrings with many equal scores, repeated pieces, and
+    in the ranked mode newline pieces and merge rules (repeated ones, and
+    rules whose joined text is not a piece)."""
+    tokens = [b"<pad>", b"<eos>", b"<bos>", b"<unk>", b"<start_of_turn>", b"<end_of_turn>", b"<mask>", b"<start",
+              b""]
+    types = [3, 3, 3, 2, 4, 4, 3, 4, 1]
+    raw_bytes = set(b"abcdefgh")
+    for b in range(256):
+        if b not in raw_bytes:
+            tokens.append(f"<0x{b:02X}>".encode())
+            types.append(6)
+    missing = {"Q", "z", "😀", "文"}
+    singles = [c for c in ALPHABET if c not in missing]
+    tokens += [c.encode() for c in singles]
+    types += [1] * len(singles)
+    subs = set()
+    for w in words:
+        t = SP + w
+        for i in range(len(t)):
+            for j in range(i + 2, min(len(t), i + 6) + 1):
+                if rng.random() < 0.5:
+                    subs.add(t[i:j])
+    subs = sorted(subs)
+    tokens += [x.encode() for x in subs]
+    types += [1] * len(subs)
+    if ranked:
+        tokens += [b"\n", b"\n\n", b"\n\n\n"]
+        types += [1, 1, 1]
+    for i in rng.integers(300, len(tokens), 20):  # repeated pieces: the last id wins
+        tokens.append(tokens[int(i)])
+        types.append(types[int(i)])
+    scores = (-rng.integers(0, 40, len(tokens)) / 4.0).astype(np.float32)
+    scores[:9] = 0.0
+    merges = []
+    if ranked:
+        pieces = set(subs) | set(singles)
+        for x in subs:
+            cut = int(rng.integers(1, len(x)))
+            if x[:cut] in pieces and x[cut:] in pieces:
+                merges.append(f"{x[:cut]} {x[cut:]}".encode())
+        for _ in range(200):  # rules whose joined text is not a piece
+            a, b = rng.choice(singles[:40], 2)
+            merges.append(f"{a} {b}".encode())
+        rng.shuffle(merges)
+        merges += merges[:30]  # repeated rules: the first rank wins
+    return tokens, types, scores, merges
+
+
+def synth_texts(rng, vocab_words):
+    fixed = [b"", b" ", b"a", b"hello world", b"  two  spaces ", b"<bos>x<eos>",
+             b"pre<start_of_turn>mid<end_of_turn>post", b"<start_of", b"<start<start_of_turn>", b"<unk>", b"<mask>",
+             "\u03a9mega \x01 ctrl".encode(), b"\xff\xfe bad utf8 \xc3", "中文 😀 émoji".encode(),
+             b"tab\tand\nnewline\n\n\n x", b"\n\n", "\u2581literal".encode(), b"QzQz zz", b"aaaaaaaaaaaaaaaa",
+             b"abcdefgh hgfedcba"]
+    words = [w for w in "the quick brown fox jumps over lazy dog cafe naive 中文 😀 émoji abc ab ba".split()]
+    chars = ALPHABET + ["Ω", "\x01", " "]
+    out = list(fixed)
+    for i in range(260):
+        parts = []
+        for _ in range(int(rng.integers(1, 25))):
+            u = rng.random()
+            if u < 0.6:
+                parts.append(str(rng.choice(words)))
+            elif u < 0.85:
+                parts.append("".join(rng.choice(chars, size=rng.integers(1, 6))))
+            elif u < 0.95:
+                parts.append(str(rng.choice(["<bos>", "<eos>", "<unk>", "<mask>", "<start_of_turn>", "<start"])))
+            else:
+                parts.append("\n" * int(rng.integers(1, 4)))
+        sep = [" ", "  ", "", "\t"]
+        out.append("".join(p + str(rng.choice(sep, p=[0.7, 0.1, 0.15, 0.05])) for p in parts).encode())
+    for i in range(120):  # texts of the vocabularies' own words: long merges
+        out.append(" ".join(str(w) for w in rng.choice(vocab_words, size=rng.integers(1, 30))).encode())
+    out.append(" ".join(str(rng.choice(words)) for _ in range(900)).encode())  # a long text
+    return out
+
+
+def blob(items):
+    offs = np.concatenate([[0], np.cumsum([len(x) for x in items])]).astype(np.int64)
+    return np.frombuffer(b"".join(items), np.uint8) if offs[-1] else np.zeros(0, np.uint8), offs
+
+
+def tokenizer_vectors(r):
+    """tests/golden/tokenizer_vectors.npz: three synthetic vocabularies (the
+    vocabulary and model flags as data), seeded texts, and the ids the
+    reference's tokenizer.c gives each text under each (add_special,
+    parse_special) pair."""
+    import tempfile
+
+    import gguf_py
+
+    r.ref_tokenizer_open.restype = C.c_void_p
+    r.ref_tokenizer_open.argtypes = [C.c_char_p]
+    r.ref_tokenize.restype = C.c_size_t
+    r.ref_tokenize.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t, C.c_int, C.c_int, C.POINTER(C.c_int32),
+                               C.c_size_t]
+    r.ref_tokenizer_close.argtypes = [C.c_void_p]
+    rng = np.random.default_rng(20260201)
+    letters = list("abcdefghijklmnopqrstuvwxyzABCDE") + ["é", "ü", "中"]
+    words = ["".join(rng.choice(letters, size=rng.integers(1, 8))) for _ in range(300)]
+    texts = synth_texts(rng, words)
+    out = {}
+    out["text"], out["text_offsets"] = blob(texts)
+    configs = {"spm": dict(ranked=False, bos=2, eos=1, add_bos=True, add_eos=False, prefix=True),
+               "spm_eos": dict(ranked=False, bos=4, eos=6, add_bos=False, add_eos=True, prefix=False),
+               "ranked": dict(ranked=True, bos=2, eos=1, add_bos=True, add_eos=True, prefix=True)}
+    for name, c in configs.items():
+        tokens, types, scores, merges = synth_vocab(rng, c["ranked"], words)
+        kvs = [("tokenizer.ggml.model", "str", "llama"), ("tokenizer.ggml.tokens", "arr_str", tokens),
+               ("tokenizer.ggml.scores", "arr_f32", scores), ("tokenizer.ggml.token_type", "arr_i32", types),
+               ("tokenizer.ggml.bos_token_id", "u32", c["bos"]), ("tokenizer.ggml.eos_token_id", "u32", c["eos"]),
+               ("tokenizer.ggml.add_bos_token", "bool", c["add_bos"]),
+               ("tokenizer.ggml.add_eos_token", "bool", c["add_eos"]),
+               ("tokenizer.ggml.add_space_prefix", "bool", c["prefix"])]
+        if merges:
+            kvs.append(("tokenizer.ggml.merges", "arr_str", merges))
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "tok.gguf")
+            gguf_py.write_kv(path, kvs)
+            h = r.ref_tokenizer_open(path.encode())
+            ids, offs = [], [0]
+            buf = (C.c_int32 * 65536)()
+            for t in texts:
+                for add_special, parse_special in COMBOS:
+                    n = r.ref_tokenize(h, t, len(t), add_special, parse_special, buf, 65536)
+                    assert n <= 65536
+                    ids.extend(buf[:n])
+                    offs.append(offs[-1] + n)
+            r.ref_tokenizer_close(h)
+        out[f"{name}_tokens"], out[f"{name}_token_offsets"] = blob(tokens)
+        out[f"{name}_types"] = np.array(types, np.int32)
+        out[f"{name}_scores"] = scores
+        out[f"{name}_merges"], out[f"{name}_merge_offsets"] = blob(merges)
+        out[f"{name}_flags"] = np.array([c["bos"], c["eos"], c["add_bos"], c["add_eos"], c["prefix"]], np.int32)
+        out[f"{name}_ids"] = np.array(ids, np.int32)
+        out[f"{name}_id_offsets"] = np.array(offs, np.int64)
+    path = os.path.join(HERE, "tokenizer_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(texts)} texts x {len(COMBOS)} flag pairs x "
+          f"{len(configs)} vocabularies)")
 
 
 def float_text(r, rng):
