@@ -123,7 +123,7 @@ def kernel_table(eg2, torch, steps):
         out[name] = {"us": round(ms * 1e3, 2), "achieved": round(rate, 1), "unit": unit, "peak": peak,
                      "frac": round(rate / peak, 4)}
 
-    for name, (m, k) in {"gemm_qkv 2048x1280x768": (1280, E), "gemm_o 2048x768x768": (E, E),
+    for name, (m, k) in {"gemm_o 2048x768x768": (E, E),
                          "gemm_gate_up_geglu 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
         xq, xd, wq, wd, y = gemm_operands(eg2, torch, T, m, k, g)
         if "geglu" in name:
@@ -150,9 +150,8 @@ def kernel_table(eg2, torch, steps):
     ms = time_launches(torch, lambda: eg2.ops.embed_norm_quant(table_d, ids, 27.7, w_e, 1e-6, x, xq, xd),
                        steps, 3)
     rec("embed_norm_quant", ms, T * (816 + 4 * E + E + 4 * E // 32), "GB/s", PEAK_HBM_GBS)
-    # QK-norm/RoPE and attention on the 16 x 128 packing.
+    # QKV projection with QK-norm/RoPE, and attention, on the 16 x 128 packing.
     offsets = list(range(0, T + 1, T // SEQS))
-    qkv = rnd(T, eg2.QKV_COLS)
     rope = torch.from_numpy(eg2.rope_table(1e4)).to(dev)
     pos = torch.tensor([t - (t // 128) * 128 for t in range(T)], dtype=torch.int32, device=dev)
     vcol_np, ldv = eg2.attention_vt_columns(offsets)
@@ -160,9 +159,10 @@ def kernel_table(eg2, torch, steps):
     qs = torch.zeros((T, 2 * E), dtype=torch.float16, device=dev)
     ks = torch.zeros((T, 2 * D), dtype=torch.float16, device=dev)
     vt = torch.zeros((2, D, ldv), dtype=torch.float16, device=dev)
-    ms = time_launches(torch, lambda: eg2.ops.qk_norm_rope(qkv, w_d, w_d, rope, pos, vcol, 1e-6, qs, ks, vt),
-                       steps, 3)
-    rec("qk_norm_rope", ms, T * (4 * (E + 2 * D) + 2 * 2 * (E + 2 * D)), "GB/s", PEAK_HBM_GBS)
+    xq, xd, wq, wd, _ = gemm_operands(eg2, torch, T, eg2.QKV_COLS, E, g)
+    ms = time_launches(torch, lambda: eg2.ops.gemm_q8_qkv_rope(xq, xd, wq, wd, T, w_d, w_d, rope, pos, vcol, 1e-6,
+                                                               qs, ks, vt), steps, 3)
+    rec("gemm_qkv_rope 2048x1280x768", ms, 2.0 * T * eg2.QKV_COLS * E, "TFLOP/s", PEAK_INT8_TOPS)
     cq = torch.zeros(eg2.q8_tile_bytes(T, E), dtype=torch.int8, device=dev)
     cd = torch.zeros((E // 32, T), device=dev)
     att = eg2.AttentionPlan(offsets, dev)

@@ -148,6 +148,43 @@ __device__ __forceinline__ float gelu_mul(float g, float u) {
   return gelu * u;
 }
 
+// Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):
+// the sequential sum over t of x[8t + c]^2, squares rounded then added.
+template <int N>
+__device__ __forceinline__ float sse2_chain(const float* row, int c) {
+  float v[N / 8];
+#pragma unroll
+  for (int t = 0; t < N / 8; ++t) v[t] = row[8 * t + c];
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < N / 8; ++t) {
+    const float p = v[t] * v[t];
+    s = s + p;
+  }
+  return s;
+}
+
+// Horizontal step of the SSE2 sum for the 8-lane group holding chains 0..7
+// (chains 0-3 are the first 4-wide accumulator, 4-7 the second):
+// v[j] = acc0[j] + acc1[j], total (v0 + v2) + (v1 + v3) (kernels.c:35-39).
+// Every lane of the group receives the total. All 64 lanes must call it.
+__device__ __forceinline__ float sse2_combine(float s) {
+  const int lane = threadIdx.x & 63, base = lane & ~7;
+  const float up = __shfl(s, base + ((lane + 4) & 7), 64);
+  const float v = s + up;
+  const float v0 = __shfl(v, base, 64), v1 = __shfl(v, base + 1, 64);
+  const float v2 = __shfl(v, base + 2, 64), v3 = __shfl(v, base + 3, 64);
+  return (v0 + v2) + (v1 + v3);
+}
+
+// Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
+// exact in fp32, so hi + lo carries 22 of the 24 significand bits.
+__device__ __forceinline__ void store_split(_Float16* row, int width, int i, float x) {
+  const _Float16 h = (_Float16)x;
+  row[i] = h;
+  row[width + i] = (_Float16)(x - (float)h);
+}
+
 // Sum of squares of an LDS row of n floats (n % 8 == 0) in the reference's
 // SSE2 order (kernels.c:82-94): lane c < 8 runs the sequential chain over
 // x[8t + c] (lanes 0-3 are the first 4-lane accumulator, 4-7 the second),

@@ -27,6 +27,10 @@ hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t
 // xd/wd: their block scales transposed, [k/32][ldx] and [k/32][ldw].
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
+hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd,
+                                   int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
+                                   const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
+                                   _Float16* vt, int ldv, hipStream_t st);
 hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                                 int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st);
 hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,

@@ -88,7 +88,7 @@ struct Lane {
   unsigned index = 0;
   hipStream_t stream = nullptr;
   std::mutex mutex;
-  float *x, *h, *qkv, *xd, *cd, *pooled, *mid, *mid_d;
+  float *x, *h, *xd, *cd, *pooled, *mid, *mid_d;
   int8_t *xq, *cq, *mid_q;
   _Float16 *qs, *ks, *vt;
   int32_t *ids_d, *pos_d, *vcol_d;
@@ -421,7 +421,6 @@ void Backend::alloc_lane(Lane& L) {
   check(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking), "hipStreamCreate");
   L.x = dalloc<float>((size_t)kCap * kEmbd);
   L.h = dalloc<float>((size_t)kCap * kEmbd);
-  L.qkv = dalloc<float>((size_t)kCap * kQKV);
   L.xq = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kFF));
   L.xd = dalloc<float>((size_t)kCap * (kFF / 32));
   L.cq = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
@@ -476,7 +475,7 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 }
 
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
-// then per layer (engine.c:1115-1127 order) QKV GEMM, QK-norm/RoPE,
+// then per layer (engine.c:1115-1127 order) QKV GEMM with QK-norm/RoPE,
 // attention (+Q8_0; with `merge`, the merge of split sequences' key-chunk
 // partials), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM with the
 // GeGLU (+Q8_0) in its epilogue, down GEMM, residual + next attn_norm
@@ -489,9 +488,11 @@ void Backend::record_layers(Lane& ln, unsigned rows, bool merge) {
                                                layers_[0].attn_norm, eps_, ln.x, ln.xq, ln.xd, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
-    gemm("gemm_qkv", ln.xq, ln.xd, L.qkv, ln.qkv, n, kQKV, s);
-    launch("qk_norm_rope", eg2::launch_qk_norm_rope(ln.qkv, L.q_norm, L.k_norm, L.rope, ln.pos_d, ln.vcol_d, eps_,
-                                                    ln.qs, ln.ks, ln.vt, kVtCols, n, s));
+    // Q|K|V projection with QK-norm / RoPE in its epilogue: the split q/k
+    // rows and the transposed v for attention, no fp32 projection in HBM.
+    launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
+                                                         L.q_norm, L.k_norm, L.rope, ln.pos_d, ln.vcol_d, eps_,
+                                                         ln.qs, ln.ks, ln.vt, kVtCols, s));
     launch("attention", eg2::launch_attention(ln.qs, ln.ks, ln.vt, kVtCols, ln.vcol_d, ln.items_d, ln.counts_d,
                                               (n + 7) / 8, L.window, n, ln.cq, ln.cd, ln.partials, s));
     if (merge)

@@ -109,11 +109,11 @@ __device__ __forceinline__ void scale_accumulate(floatx16& acc, const intx16& bi
 struct XcdRegions {
   int cparts, rows, cols;  // column parts; row and column tiles per region
 };
-__host__ __device__ inline XcdRegions xcd_regions(int n, int m) {
-  const int tr_count = (n + 63) / 64, tc_count = (m + 63) / 64;
+__host__ __device__ inline XcdRegions xcd_split(int tr_count, int tc_count) {
   const int rparts = tr_count >= 2 ? 2 : 1, cparts = kXcds / rparts;
   return {cparts, (tr_count + rparts - 1) / rparts, (tc_count + cparts - 1) / cparts};
 }
+__host__ __device__ inline XcdRegions xcd_regions(int n, int m) { return xcd_split((n + 63) / 64, (m + 63) / 64); }
 __host__ inline dim3 gemm_grid(int n, int m) {
   const XcdRegions reg = xcd_regions(n, m);
   return dim3(kXcds * reg.rows * reg.cols);
@@ -303,6 +303,211 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
   else
     hipLaunchKernelGGL((gemm_q8_kernel<true, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
                        ldw, nullptr, n, m, nb, ldg, gq, gd);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The Q|K|V projection with the QK-norm / RoPE epilogue (kernels.c:233-264 on
+// each token of the projection's output): a workgroup of 8 waves computes 32
+// token rows x one 256-wide head (head hc of [q0 q1 q2 | k | v]), wave w the
+// 32 x 32 piece at columns 32 w, with the block loop of gemm_q8_kernel (so
+// the projection's fp32 values are bit-identical to it). The epilogue puts
+// the tile in LDS and, for q and k heads, runs each row's SSE2-order sum of
+// squares (waves 0-3, 8 lanes per row), then (x*w)*inv, the NeoX rotation of
+// pairs (d, d+128) with the host cos/sin row of the token's position, the
+// 1/16 scale of q, and writes the split fp16 pairs the attention kernel
+// reads -- the operations and order of the standalone qk_norm_rope kernel.
+// The v head is written transposed, vt[hi|lo][dim][vcol[t]]. The fp32
+// projection never reaches HBM.
+constexpr int kQkvTiles = 9;                      // A | B0 .. B7 per stage
+constexpr int kQDxOff = kQkvTiles * kTile;        // 64 floats (rows 0-31 used)
+constexpr int kQDwOff = kQDxOff + 64 * 4;         // 256 floats
+constexpr int kQStageBytes = kQDwOff + 256 * 4;
+constexpr int kRowPitch = kHeadDim + 8;  // floats per token row of the epilogue tile (8 banks apart)
+constexpr int kQkvHeads = kQKVCols / kHeadDim;  // 5
+
+template <bool TAIL>
+__global__ void __launch_bounds__(512)
+gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx,
+                        const int8_t* __restrict__ wq, const float* __restrict__ wd, int ldw, int n, int nb,
+                        const float* __restrict__ q_w, const float* __restrict__ k_w, const float* __restrict__ rope,
+                        const int32_t* __restrict__ pos, const int32_t* __restrict__ vcol, float eps,
+                        _Float16* __restrict__ qs, _Float16* __restrict__ ks, _Float16* __restrict__ vt, int ldv) {
+  __shared__ float invs[32];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
+  const int x = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
+  const int r0 = (x / reg.cparts) * reg.rows, c0 = (x % reg.cparts) * reg.cols;
+  const int rows_here = min(reg.rows, (n + 31) / 32 - r0), cols_here = min(reg.cols, kQkvHeads - c0);
+  if (rows_here <= 0 || cols_here <= 0 || i >= rows_here * cols_here) return;
+  const int tr = r0 + i % rows_here, hc = c0 + i / rows_here;
+
+  // DMA, the same three transfers for every wave (no branch in the loop):
+  // weight tile 8 hc + w of the block; a quarter of the activation tile
+  // (waves 0-3) or of the head's 256 weight scales (waves 4-7), 4 bytes a
+  // lane; and the activation scales of the tile's rows (identical data in
+  // every wave; lanes 32-63 repeat rows 0-31).
+  const int8_t* tbase = wq + (size_t)(8 * hc + w) * nb * kTile;
+  const unsigned lds0 = (unsigned)(uintptr_t)gemm_lds;
+  const unsigned t_lds = lds0 + kTile * (1 + w);
+  const bool aq = w < 4;
+  const char* q_base = aq ? reinterpret_cast<const char*>(xq + (size_t)tr * nb * kTile) + 256 * w
+                          : reinterpret_cast<const char*>(wd + 256 * hc + 64 * (w - 4));
+  const size_t q_step = aq ? (size_t)kTile : (size_t)ldw * 4;  // bytes per block
+  const unsigned q_lds = lds0 + (aq ? 256 * w : kQDwOff + 256 * (w - 4));
+  const unsigned x_off = 4u * (unsigned)min(32 * tr + (lane & 31), n - 1);
+  auto issue = [&](int slot, int kb) {
+    kb = min(kb, nb - 1);
+    const unsigned st = slot * kQStageBytes;
+    dma16(tbase + (size_t)kb * kTile, 16u * lane, __builtin_amdgcn_readfirstlane(t_lds + st));
+    dma4(q_base + kb * q_step, 4u * lane, __builtin_amdgcn_readfirstlane(q_lds + st));
+    dma4(xd + (size_t)kb * ldx, x_off, __builtin_amdgcn_readfirstlane(lds0 + st + kQDxOff));
+  };
+
+  const int g = lane >> 5;
+  const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
+  const unsigned char* a_p = gemm_lds + 16 * lane;
+  const unsigned char* b_p = gemm_lds + kTile * (1 + w) + 16 * lane;
+  const unsigned char* dx_p = gemm_lds + kQDxOff + 4 * srow;
+  const unsigned char* dw_p = gemm_lds + kQDwOff + 4 * (32 * w + (lane & 31));
+  intx16 magic = (intx16)(kMagicBits);
+  asm volatile("" : "+v"(magic));
+  struct Frag {
+    intx4 a, b;
+    float dx, dw;
+  };
+  auto frag = [&](int slot) {
+    Frag f;
+    f.a = *reinterpret_cast<const intx4*>(a_p + slot * kQStageBytes);
+    f.b = *reinterpret_cast<const intx4*>(b_p + slot * kQStageBytes);
+    f.dx = *reinterpret_cast<const float*>(dx_p + slot * kQStageBytes);
+    f.dw = *reinterpret_cast<const float*>(dw_p + slot * kQStageBytes);
+    return f;
+  };
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue(s, s);
+  wait_barrier<3 * (kStages - 2)>();
+  Frag f[2];
+  intx16 d[2];
+  f[0] = frag(0);
+  d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[0].a, f[0].b, magic, 0, 0, 0);
+  floatx16 acc = floatx16{};
+  auto step = [&](int j, int kb) {
+    const int cur = j & 1, nxt = cur ^ 1;
+    issue((j + kStages - 1) % kStages, kb + kStages - 1);
+    wait_barrier<3 * (kStages - 2)>();
+    f[nxt] = frag((j + 1) % kStages);
+    d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
+    scale_accumulate(acc, d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+  };
+  int kb0 = 0;
+  for (; kb0 + kStages <= nb; kb0 += kStages) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) step(j, kb0 + j);
+  }
+  if constexpr (TAIL) {
+#pragma unroll
+    for (int j = 0; j < kStages - 1; ++j)
+      if (kb0 + j < nb) step(j, kb0 + j);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // The epilogue's global inputs go out now, so their latency overlaps the
+  // tile's trip through LDS and the sums of squares: the cos/sin and norm
+  // weights of this wave's rows 4w..4w+3 (q, k), or the v columns.
+  constexpr int half = kHeadDim / 2;
+  const bool is_v = hc == kHeads + 1;
+  const float* wgt = hc < kHeads ? q_w : k_w;
+  float cs_r[4][4], w_r[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    w_r[2 * j] = wgt[lane + 64 * j];
+    w_r[2 * j + 1] = wgt[lane + 64 * j + half];
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int t = min(32 * tr + 4 * w + rr, n - 1);
+    const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      cs_r[rr][2 * j] = cs[lane + 64 * j];
+      cs_r[rr][2 * j + 1] = cs[half + lane + 64 * j];
+    }
+  }
+  const int v_col = vcol[min(32 * tr + (lane & 31), n - 1)];
+  __syncthreads();  // the ring becomes the epilogue tile
+
+  float* tile = reinterpret_cast<float*>(gemm_lds);  // [32][kRowPitch]
+#pragma unroll
+  for (int v = 0; v < 16; ++v) tile[(8 * (v >> 2) + 4 * g + (v & 3)) * kRowPitch + 32 * w + (lane & 31)] = acc[v];
+  __syncthreads();
+  if (is_v) {
+    // v: transposed split pairs; lanes 0-31 take 32 tokens of dim e, lanes
+    // 32-63 of dim e + 1.
+    const int tl = lane & 31, t = 32 * tr + tl;
+    if (t < n) {
+      _Float16* col = vt + v_col;
+#pragma unroll 2
+      for (int p = 0; p < 16; ++p) {
+        const int e = 32 * w + 2 * p + g;
+        const float val = tile[tl * kRowPitch + e];
+        const _Float16 h = (_Float16)val;
+        col[(size_t)e * ldv] = h;
+        col[(size_t)(kHeadDim + e) * ldv] = (_Float16)(val - (float)h);
+      }
+    }
+    return;
+  }
+  // kernels.c:233-264 for q head hc (hc < 3) or k (hc == 3).
+  if (w < 4) {
+    const int row = 8 * w + (lane >> 3);
+    const float ss = sse2_combine(sse2_chain<kHeadDim>(tile + row * kRowPitch, lane & 7));
+    if ((lane & 7) == 0) invs[row] = rms_inverse(ss, kHeadDim, eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int row = 4 * w + rr, t = 32 * tr + row;
+    if (t >= n) break;
+    const float inv = invs[row];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int dd = lane + 64 * j;
+      const float c = cs_r[rr][2 * j], s = cs_r[rr][2 * j + 1];
+      const float x0 = tile[row * kRowPitch + dd] * w_r[2 * j] * inv;
+      const float x1 = tile[row * kRowPitch + dd + half] * w_r[2 * j + 1] * inv;
+      const float a0 = x0 * c, a1 = x1 * s;
+      const float b0 = x0 * s, b1 = x1 * c;
+      float lo = a0 - a1, hi = b0 + b1;
+      if (hc < kHeads) {
+        lo = lo * 0.0625f;
+        hi = hi * 0.0625f;
+        _Float16* qrow = qs + (size_t)t * 2 * kEmbd;
+        store_split(qrow, kEmbd, hc * kHeadDim + dd, lo * 16.0f);
+        store_split(qrow, kEmbd, hc * kHeadDim + dd + half, hi * 16.0f);
+      } else {
+        _Float16* krow = ks + (size_t)t * 2 * kHeadDim;
+        store_split(krow, kHeadDim, dd, lo);
+        store_split(krow, kHeadDim, dd + half, hi);
+      }
+    }
+  }
+}
+
+hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd,
+                                   int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
+                                   const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
+                                   _Float16* vt, int ldv, hipStream_t st) {
+  if (n <= 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < kQKVCols || ldv <= 0) return hipErrorInvalidValue;
+  static_assert(32 * kRowPitch * 4 <= kStages * kQStageBytes, "the epilogue tile fits in the ring");
+  const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
+  const dim3 grid(kXcds * reg.rows * reg.cols);
+  const int nb = k / kQK;
+  if (nb % kStages == 0)
+    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<false>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
+                       wd, ldw, n, nb, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv);
+  else
+    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<true>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
+                       wd, ldw, n, nb, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv);
   return hipGetLastError();
 }
 

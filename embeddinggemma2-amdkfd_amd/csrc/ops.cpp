@@ -147,6 +147,19 @@ int eg2_hip_gemm_q8(const int8_t* xq, const float* xd, unsigned ldx, const int8_
                                   as_stream(stream)));
 }
 
+int eg2_hip_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd,
+                             unsigned ldw, unsigned n, unsigned k, const float* q_w, const float* k_w,
+                             const float* rope_table, const int32_t* pos, const int32_t* vcol, float eps,
+                             uint16_t* qs, uint16_t* ks, uint16_t* vt, unsigned ldv, void* stream) {
+  constexpr unsigned kMax = 1u << 24;
+  if (!xq || !xd || !wq || !wd || !q_w || !k_w || !rope_table || !pos || !vcol || !qs || !ks || !vt || n == 0 ||
+      k == 0 || k % 32 != 0 || ldx < n || ldw < 1280 || n > kMax || k > kMax || ldx > kMax || ldw > kMax ||
+      ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
+    return kInvalid;
+  return code(eg2::launch_gemm_q8_qkv_rope(xq, xd, (int)ldx, wq, wd, (int)ldw, (int)n, (int)k, q_w, k_w, rope_table,
+                                           pos, vcol, eps, h16(qs), h16(ks), h16(vt), (int)ldv, as_stream(stream)));
+}
+
 int eg2_hip_gemm_q8_geglu(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd,
                           unsigned ldw, int8_t* gq, float* gd, unsigned ldg, unsigned n, unsigned ff, unsigned k,
                           void* stream) {

@@ -123,6 +123,8 @@ SIGNATURES = {
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8_geglu": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _u, _vp]),
+    "eg2_hip_gemm_q8_qkv_rope": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp, _vp, C.c_float,
+                                           _vp, _vp, _vp, _u, _vp]),
     "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
     "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
     "eg2_q8_tile_bytes": (C.c_size_t, [C.c_size_t, _u]),
@@ -586,6 +588,15 @@ class ops:
         check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos),
                                          cls._p(vcol), eps, cls._p(qh), cls._p(kh), cls._p(vt), vt.shape[2],
                                          qkv.shape[0], cls._stream()), "qk_norm_rope")
+
+    @classmethod
+    def gemm_q8_qkv_rope(cls, xq, xd, wq, wd, n, q_w, k_w, table, pos, vcol, eps, qh, kh, vt):
+        """The QKV projection of n rows (xq/xd as for gemm_q8, weights of the
+        [q|k|v] concatenation) followed by qk_norm_rope, in one kernel."""
+        check(lib().eg2_hip_gemm_q8_qkv_rope(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wq), cls._p(wd),
+                                             wd.shape[1], n, 32 * xd.shape[0], cls._p(q_w), cls._p(k_w),
+                                             cls._p(table), cls._p(pos), cls._p(vcol), eps, cls._p(qh), cls._p(kh),
+                                             cls._p(vt), vt.shape[2], cls._stream()), "gemm_q8_qkv_rope")
 
     @classmethod
     def attention(cls, qs, ks, vt, vcol, offsets, window, cq, cd):

@@ -145,6 +145,19 @@ int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, vo
 int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd, unsigned ldw,
                     float *y, unsigned n, unsigned m, unsigned k, unsigned ldy, void *stream);
 
+/* The fused Q|K|V projection with its QK-norm / RoPE in one kernel: for
+ * n rows of Q8_0 activations xq/xd [n][k] and the [q 768 | k 256 | v 256]
+ * weights (eg2_q8_weight_tiles of the concatenated matrices, ldw >= 1280),
+ * the projection exactly as eg2_hip_gemm_q8 computes it, then exactly what
+ * eg2_hip_qk_norm_rope does with it (same q_w, k_w, rope_table, pos, vcol,
+ * eps, outputs and ldv) -- bit-identical to the two calls, without the fp32
+ * projection in memory. Replaces the Q/K/V eg2_mm* calls and eg2_norm_rope
+ * of kernels/eg2.c (:41-119, :204-217). k % 32 == 0; ldv % 32 == 0. */
+int eg2_hip_gemm_q8_qkv_rope(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd,
+                             unsigned ldw, unsigned n, unsigned k, const float *q_w, const float *k_w,
+                             const float *rope_table, const int32_t *pos, const int32_t *vcol, float eps,
+                             uint16_t *qs, uint16_t *ks, uint16_t *vt, unsigned ldv, void *stream);
+
 /* The gate and up projections and the GeGLU with its Q8_0 quantization in
  * one kernel: for rows of Q8_0 activations xq/xd [n][k] and the gate and up
  * weights interleaved in 32-row groups (eg2_q8_geglu_weight_tiles: ldw >=

@@ -285,6 +285,41 @@ def test_gemm_q8_geglu_against_oracle(eg2, gpu, n, ff, k):
     assert (qd.max(2) == 0).mean() > 0.98
 
 
+@pytest.mark.parametrize("lens", [[128] * 16, [40, 260], [33], [1, 1, 5], [2048]])
+def test_gemm_q8_qkv_rope_equals_gemm_then_qk_norm_rope(eg2, gpu, lens):
+    """The fused QKV projection + QK-norm/RoPE of the forward is
+    bit-identical to eg2_hip_gemm_q8 on [q|k|v] then eg2_hip_qk_norm_rope:
+    q and k split pairs, and v transposed at each token's column (columns
+    no token writes stay untouched)."""
+    import torch
+
+    k = N_EMBD
+    n = int(sum(lens))
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    w = quantize_q8_0((RNG.standard_normal((eg2.QKV_COLS, k)) * 0.05).astype(np.float32))
+    xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
+    xq, xd = device_q8(eg2, xb, k, gpu)
+    wq, wd = device_weights(eg2, w, k, gpu)
+    qw, kw = ((1 + 0.1 * RNG.standard_normal(HEAD_DIM)).astype(np.float32) for _ in range(2))
+    pos = np.concatenate([np.arange(l) for l in lens]).astype(np.int32)
+    table = dev(eg2.rope_table(1e4), gpu)
+    vcol, ldv = eg2.attention_vt_columns(offsets)
+    args = (dev(qw, gpu), dev(kw, gpu), table, dev(pos, gpu), dev(vcol, gpu), 1e-6)
+    outs = []
+    for fused in (False, True):
+        qs, ks = (torch.full((n, 2 * c), 7.0, dtype=torch.float16, device=gpu) for c in (N_EMBD, HEAD_DIM))
+        vt = torch.full((2, HEAD_DIM, ldv), 7.0, dtype=torch.float16, device=gpu)
+        if fused:
+            eg2.ops.gemm_q8_qkv_rope(xq, xd, wq, wd, n, *args, qs, ks, vt)
+        else:
+            y = empty((n, eg2.QKV_COLS), torch.float32, gpu)
+            eg2.ops.gemm_q8(xq, xd, wq, wd, y)
+            eg2.ops.qk_norm_rope(y, *args, qs, ks, vt)
+        outs.append([host(t).view(np.uint16) for t in (qs, ks, vt)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+
+
 def segments_log_uniform(rng, n_seg=16, total=2048, lo=8, hi=512):
     """Sequence lengths ~ exp(U(ln lo, ln hi)), scaled to sum `total`,
     rounded, each clipped to [lo, hi]; the remainder goes to the last one

@@ -62,6 +62,13 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
+    # gemm_q8_qkv_rope(xq, xd, ldx, wq, wd, ldw, n, k, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv)
+    f = C.c_float(1e-6)
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 48, p, p, p, p, p, f, p, p, p, 64, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1279, 4, 32, p, p, p, p, p, f, p, p, p, 64, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 3, p, p, 1280, 4, 32, p, p, p, p, p, f, p, p, p, 64, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, p, p, f, p, p, p, 48, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, None, p, f, p, p, p, 64, None) == inval
     # gemm_q8_geglu(xq, xd, ldx, wq, wd, ldw, gq, gd, ldg, n, ff, k)
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 96, p, p, 4, 4, 48, 32, None) == inval  # ff % 32
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 4, 32, 48, None) == inval  # k % 32
