@@ -126,29 +126,35 @@ constexpr int kGPitch = 40;  // floats per row of the GeGLU epilogue's transpose
 // interleaved in 32-row groups (gate group j, then up group j), so output
 // tile tc holds gate columns 32 tc .. 32 tc + 31 in its waves wc = 0 and
 // the matching up columns in its waves wc = 1, and its 32 GeGLU outputs per
-// row are exactly Q8_0 block tc. The two waves of a row pair swap half of
-// their results through LDS (the gate wave finishes rows 0-15 of the pair,
-// the up wave rows 16-31), transpose them so that four lanes hold one
-// row's block, and quantize with the same code as the standalone GeGLU
-// kernel: the int8 values go to gq in the row-tile layout (nbf blocks per
+// row are exactly Q8_0 block tc. The two waves of a row pair swap their
+// results through LDS (the gate wave finishes rows 0-15 of the pair, the
+// up wave rows 16-31), transpose them so that four lanes hold one row's
+// block, and quantize with the same code as the standalone GeGLU kernel: the int8 values go to gq in the row-tile layout (nbf blocks per
 // row), the scales to gd[tc * ldg + row].
 __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int tc, int wr, int wc, int n, int nbf,
                                                int8_t* __restrict__ gq, float* __restrict__ gd, int ldg) {
   const int lane = threadIdx.x & 63, g = lane >> 5;
   // The ring is free once every wave is past its last fragment reads.
   __syncthreads();
-  float* xch = reinterpret_cast<float*>(gemm_lds) + wr * 1024;                  // [2][8][64]
-  float* tp = reinterpret_cast<float*>(gemm_lds) + 2048 + wr * 32 * kGPitch;  // [32][kGPitch]
+  // Every wave puts all 16 of its registers in LDS ([2 wc][16 v][64 lanes]
+  // per row pair) and reads back the gate and up values of its own half by
+  // address, so no register is selected at run time.
+  float* xch = reinterpret_cast<float*>(gemm_lds) + wr * 2048;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) xch[(wc * 8 + i) * 64 + lane] = wc ? acc[i] : acc[8 + i];
+  for (int v = 0; v < 16; ++v) xch[(wc * 16 + v) * 64 + lane] = acc[v];
   __syncthreads();
+  float gv[8], uv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float other = xch[((wc ^ 1) * 8 + i) * 64 + lane];
-    const float gate = wc ? other : acc[i], up = wc ? acc[8 + i] : other;
-    // register v = 8 wc + i of the 32x32 output layout: row 8 (v >> 2) + 4 g + (v & 3), column lane & 31
-    tp[(16 * wc + 8 * (i >> 2) + 4 * g + (i & 3)) * kGPitch + (lane & 31)] = gelu_mul(gate, up);
+    gv[i] = xch[(8 * wc + i) * 64 + lane];
+    uv[i] = xch[(16 + 8 * wc + i) * 64 + lane];
   }
+  __syncthreads();  // the exchange area becomes the transposed tile
+  float* tp = reinterpret_cast<float*>(gemm_lds) + wr * 32 * kGPitch;  // [32][kGPitch]
+  // register v = 8 wc + i of the 32x32 output layout: row 8 (v >> 2) + 4 g + (v & 3), column lane & 31
+  float* trow = tp + (16 * wc + 4 * g) * kGPitch + (lane & 31);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) trow[(8 * (i >> 2) + (i & 3)) * kGPitch] = gelu_mul(gv[i], uv[i]);
   __syncthreads();
   const int rr = 16 * wc + (lane >> 2), part = lane & 3;
   const float4 lo = *reinterpret_cast<const float4*>(tp + rr * kGPitch + 8 * part);
@@ -296,7 +302,8 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
     return hipErrorInvalidValue;
   const dim3 grid = gemm_grid(n, m);
   const int nb = k / kQK;
-  static_assert(2 * 1024 + 2 * 32 * kGPitch <= kStages * kStageBytes / 4, "GeGLU epilogue fits in the ring");
+  static_assert(2 * 2048 <= kStages * kStageBytes / 4 && 2 * 32 * kGPitch <= kStages * kStageBytes / 4,
+                "the GeGLU epilogue fits in the ring");
   if (nb % kStages == 0)
     hipLaunchKernelGGL((gemm_q8_kernel<false, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
                        ldw, nullptr, n, m, nb, ldg, gq, gd);
