@@ -166,7 +166,7 @@ def kernel_table(eg2, torch, steps):
     cq = torch.zeros(eg2.q8_tile_bytes(T, E), dtype=torch.int8, device=dev)
     cd = torch.zeros((E // 32, T), device=dev)
     att = eg2.AttentionPlan(offsets, dev)
-    ms = time_launches(torch, lambda: eg2.ops.attention_planned(qs, ks, vt, vcol, att, 0, cq, cd), steps, 3)
+    ms = time_launches(torch, lambda: eg2.ops.attention_planned(qs, ks, vt, att, 0, cq, cd), steps, 3)
     rec("attention 16x128", ms, 3072.0 * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS)), "TFLOP/s",
         PEAK_FP16_TFLOPS)
     return out

@@ -33,9 +33,9 @@ hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, c
                                    _Float16* vt, int ldv, hipStream_t st);
 hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                                 int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st);
-hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
-                            const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
-                            int8_t* cq, float* cd, float* partials, hipStream_t st);
+hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const uint32_t* items,
+                            const uint32_t* item_count, int grid, int window, int rows, int8_t* cq, float* cd,
+                            float* partials, hipStream_t st);
 hipError_t launch_attention_merge(const uint32_t* merges, const uint32_t* merge_count, int grid, const float* partials,
                                   int rows, int8_t* cq, float* cd, hipStream_t st);
 

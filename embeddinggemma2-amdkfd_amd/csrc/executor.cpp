@@ -493,7 +493,7 @@ void Backend::record_layers(Lane& ln, unsigned rows, bool merge) {
     launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
                                                          L.q_norm, L.k_norm, L.rope, ln.pos_d, ln.vcol_d, eps_,
                                                          ln.qs, ln.ks, ln.vt, kVtCols, s));
-    launch("attention", eg2::launch_attention(ln.qs, ln.ks, ln.vt, kVtCols, ln.vcol_d, ln.items_d, ln.counts_d,
+    launch("attention", eg2::launch_attention(ln.qs, ln.ks, ln.vt, kVtCols, ln.items_d, ln.counts_d,
                                               (n + 7) / 8, L.window, n, ln.cq, ln.cd, ln.partials, s));
     if (merge)
       launch("attention_merge", eg2::launch_attention_merge(ln.merges_d, ln.counts_d + 1, (n + 3) / 4, ln.partials,

@@ -144,7 +144,7 @@ __device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l
 
 __global__ void __launch_bounds__(64 * kWaves)
 attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ ks, const _Float16* __restrict__ vt,
-                 int ldv, const int32_t* __restrict__ vcol, const uint4* __restrict__ items,
+                 int ldv, const uint4* __restrict__ items,
                  const uint32_t* __restrict__ item_count, int window, int rows, int8_t* __restrict__ cq,
                  float* __restrict__ cd, float* __restrict__ partials) {
   __shared__ __align__(16) unsigned char lds[2 * kStage];
@@ -191,7 +191,9 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     hi = min(hi, c_hi);
     // Key tiles are aligned to the sequence start; so are the V^T columns.
     const uint32_t k_first = kv_lo >= kv_hi ? kv_hi : seg_lo + ((kv_lo - seg_lo) & ~31u);
-    const int col_base = __builtin_amdgcn_readfirstlane(vcol[min(seg_lo, (uint32_t)rows - 1)]) - (int)seg_lo;
+    // V^T column of key u: the sequence's first column (from the item, so
+    // the first V DMA does not wait on a second dependent load) + u - seg_lo.
+    const int col_base = (int)kc.w - (int)seg_lo;
 
     // DMA of key tile k0 into stage s, 64 instructions of 1 KB split over
     // the six waves: wave w issues K instruction q and V instruction q for
@@ -210,7 +212,7 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     auto dma_v = [&](uint32_t k0, int s, int j) {
       const int q = min(w + kWaves * j, kKvTile - 1);
       const int hl = q >> 4, d = 16 * (q & 15) + (lane >> 2), c = (lane & 3) ^ vswz(d);
-      const int col = min(col_base + (int)k0, ldv - kKvTile);  // the refill past a sequence stays inside vt
+      const int col = max(0, min(col_base + (int)k0, ldv - kKvTile));  // the refill past a sequence stays inside vt
       const unsigned off = 2u * (unsigned)(((hl * kHeadDim + d) * ldv) + col + 8 * c);
       dma16(vt, off, __builtin_amdgcn_readfirstlane(lds0 + s * kStage + kKStage + q * 1024));
     };
@@ -443,6 +445,7 @@ static size_t chunk_keys(size_t n) {
 
 AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges) {
   AttentionCounts c{0, 0, 0};
+  size_t col = 0;  // first V^T column of sequence s, as build_vt_columns lays them out
   for (size_t s = 0; s < batch; ++s) {
     const size_t lo = offsets[s], hi = offsets[s + 1], chunks = key_chunks(hi - lo), ck = chunk_keys(hi - lo);
     for (size_t q = lo; q < hi; q += kQTile) {
@@ -463,9 +466,10 @@ AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint3
         it[4] = (uint32_t)(chunks > 1 ? lo + k * ck : lo);
         it[5] = (uint32_t)(chunks > 1 ? std::min(hi, lo + (k + 1) * ck) : hi);
         it[6] = chunks > 1 ? c.slots++ : kNoSlot;
-        it[7] = 0;
+        it[7] = (uint32_t)col;
       }
     }
+    col += (hi - lo + 31) / 32 * 32;
   }
   return c;
 }
@@ -494,11 +498,10 @@ size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
   return base;
 }
 
-hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const int32_t* vcol,
-                            const uint32_t* items, const uint32_t* item_count, int grid, int window, int rows,
-                            int8_t* cq, float* cd, float* partials, hipStream_t st) {
+hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const uint32_t* items,
+                            const uint32_t* item_count, int grid, int window, int rows, int8_t* cq, float* cd, float* partials, hipStream_t st) {
   if (rows <= 0 || grid <= 0 || ldv <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(64 * kWaves), 0, st, qs, ks, vt, ldv, vcol,
+  hipLaunchKernelGGL(attention_kernel, dim3(grid), dim3(64 * kWaves), 0, st, qs, ks, vt, ldv,
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd, partials);
   return hipGetLastError();
 }

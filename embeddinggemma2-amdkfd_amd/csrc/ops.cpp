@@ -71,13 +71,13 @@ int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, c
                                        (int)ldv, (int)rows, as_stream(stream)));
 }
 
-int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const int32_t* vcol,
-                      const uint32_t* items, const uint32_t* item_count, unsigned grid, unsigned window,
-                      unsigned rows, int8_t* cq, float* cd, float* partials, void* stream) {
-  if (!qs || !ks || !vt || !vcol || !items || !item_count || !cq || !cd || rows == 0 || grid == 0 ||
+int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const uint32_t* items,
+                      const uint32_t* item_count, unsigned grid, unsigned window, unsigned rows, int8_t* cq, float* cd,
+                      float* partials, void* stream) {
+  if (!qs || !ks || !vt || !items || !item_count || !cq || !cd || rows == 0 || grid == 0 ||
       grid > 65536 || window > 4096u || ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
     return kInvalid;
-  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, vcol, items, item_count, (int)grid,
+  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, items, item_count, (int)grid,
                                     (int)window, (int)rows, cq, cd, partials, as_stream(stream)));
 }
 

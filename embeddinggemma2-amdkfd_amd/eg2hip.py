@@ -110,7 +110,7 @@ SIGNATURES = {
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
     "eg2_hip_attention_merge": (C.c_int, [_vp, _vp, _u, _vp, _u, _vp, _vp, _vp]),
     "eg2_attention_items": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp, _vp, _vp]),
     "eg2_attention_partial_floats": (C.c_size_t, []),
@@ -599,20 +599,20 @@ class ops:
                                              cls._p(vt), vt.shape[2], cls._stream()), "gemm_q8_qkv_rope")
 
     @classmethod
-    def attention(cls, qs, ks, vt, vcol, offsets, window, cq, cd):
-        """Packed attention over sequences [offsets[s], offsets[s+1]); vt and
-        vcol as written by qk_norm_rope."""
+    def attention(cls, qs, ks, vt, offsets, window, cq, cd):
+        """Packed attention over sequences [offsets[s], offsets[s+1]); vt as
+        qk_norm_rope writes it at the columns of attention_vt_columns."""
         import torch
 
         plan = AttentionPlan(offsets, qs.device)
-        cls.attention_planned(qs, ks, vt, vcol, plan, window, cq, cd)
+        cls.attention_planned(qs, ks, vt, plan, window, cq, cd)
         torch.cuda.current_stream().synchronize()  # keeps the plan alive until the kernel ran
 
     @classmethod
-    def attention_planned(cls, qs, ks, vt, vcol, plan, window, cq, cd):
+    def attention_planned(cls, qs, ks, vt, plan, window, cq, cd):
         """attention() with a prebuilt AttentionPlan (no host work, no sync)."""
         rows = qs.shape[0]
-        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2], cls._p(vcol),
+        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2],
                                       cls._p(plan.items), cls._p(plan.counts), plan.grid, window, rows, cls._p(cq),
                                       cls._p(cd), cls._p(plan.partials), cls._stream()), "attention")
         if plan.n_merges:

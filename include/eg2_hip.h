@@ -63,8 +63,9 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * (engine.c:850-873): each token attends to the keys of its own sequence,
  * limited to |t - s| <= window/2 when window > 0; 3 query heads share one KV
  * head, head_dim 256. Inputs are the split q/k rows and the transposed v of
- * eg2_hip_qk_norm_rope (same vt, ldv and vcol; vt columns that no token
- * wrote must hold finite values, e.g. zeros). The work list `items`
+ * eg2_hip_qk_norm_rope (same vt and ldv, its vcol laid out by
+ * eg2_attention_vt_columns; vt columns that no token wrote must hold finite
+ * values, e.g. zeros). The work list `items`
  * (device, 8 uint32 per item, from eg2_attention_items) holds *item_count
  * (device) items; `grid` workgroups stride over it. An item whose slot is
  * 0xFFFFFFFF quantizes its fp32 context to Q8_0 (quants.c:97-177) into cq
@@ -74,9 +75,9 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * eg2_hip_attention_merge then combines and quantizes. A sequence's result
  * does not depend on its place in the wave.
  * Replaces kernels/eg2.c:145-170 eg2_attention256. */
-int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const int32_t *vcol,
-                      const uint32_t *items, const uint32_t *item_count, unsigned grid, unsigned window,
-                      unsigned rows, int8_t *cq, float *cd, float *partials, void *stream);
+int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const uint32_t *items,
+                      const uint32_t *item_count, unsigned grid, unsigned window, unsigned rows, int8_t *cq,
+                      float *cd, float *partials, void *stream);
 
 /* Second step of eg2_hip_attention for split sequences: merges the
  * key-chunk partials of each query tile in `merges` (device, 4 uint32 per
@@ -89,7 +90,8 @@ int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count,
  * offsets[s+1]): per query tile of up to 32 tokens (from the sequence
  * start; one workgroup of the attention kernel) one item per key chunk
  * {first query, end, sequence start, sequence end, chunk start, chunk end,
- * slot or 0xFFFFFFFF, 0} (a sequence of n > 256 tokens has c = min(ceil(n
+ * slot or 0xFFFFFFFF, the sequence's first vt column as
+ * eg2_attention_vt_columns places it} (a sequence of n > 256 tokens has c = min(ceil(n
  * / 256), 4) chunks of ceil(n / c) keys rounded up to 32, the last one
  * taking the rest, partial slots numbered consecutively; shorter ones one
  * chunk and no slot), and per split tile one merge record {first query,

@@ -352,9 +352,9 @@ def run_attention(eg2, gpu, q, k, v, offsets, window, fill=0.0):
 
     T = q.shape[0]
     cq, cd = qbuf(eg2, T, N_EMBD, gpu), empty((24, T), torch.float32, gpu)
-    vt, vcol = transposed_v(eg2, v, offsets, gpu, fill)
-    eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), vt, vcol,
-                      offsets, window, cq, cd)
+    vt, _ = transposed_v(eg2, v, offsets, gpu, fill)
+    eg2.ops.attention(dev(split_pairs(q * np.float32(16)), gpu), dev(split_pairs(k), gpu), vt, offsets, window, cq,
+                      cd)
     return qvals(eg2, cq, T, N_EMBD), np.ascontiguousarray(host(cd).T)
 
 

@@ -77,10 +77,10 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 3, 4, 32, 32, None) == inval  # ldg < n
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, None, 4, 4, 32, 32, None) == inval
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 0, 32, 32, None) == inval  # n = 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 0, 0, 32, p, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, p, 4, 99999, 32, p, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 64, p, None, p, 4, 0, 32, p, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 48, p, p, p, 4, 0, 32, p, p, p, None) == inval  # ldv % 32
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, 0, 0, 32, p, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, 64, p, p, 4, 99999, 32, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, None, p, 4, 0, 32, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 48, p, p, 4, 0, 32, p, p, p, None) == inval  # ldv % 32
     assert lib.eg2_hip_attention_merge(p, p, 0, p, 32, p, p, None) == inval  # grid 0
     assert lib.eg2_hip_attention_merge(p, p, 4, None, 32, p, p, None) == inval
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, p, 1e-6, p, p, p, 40, 4, None) == inval  # ldv % 32
@@ -106,15 +106,17 @@ def test_attention_items_cover_each_sequence(eg2):
     query tiles are 32 tokens from the sequence start; a sequence of n > 256
     tokens splits its keys into c = min(ceil(n / 256), 4) chunks of
     ceil(n / c) keys rounded up to 32 (aligned to its start) with
-    consecutive partial slots and one merge record per query tile."""
+    consecutive partial slots and one merge record per query tile; the last
+    field is the V^T column of the sequence's first token."""
     offs = [0, 1, 33, 97, 98, 200, 600, 1100, 3150]
     items, merges, slots = eg2.attention_items(offs)
+    vcol, _ = eg2.attention_vt_columns(offs)
     seqs = [(offs[s], offs[s + 1]) for s in range(len(offs) - 1)]
     covered = {s: np.zeros((hi - lo, hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
     used_slots = []
-    for q0, q1, lo, hi, k0, k1, slot, zero in items.astype(np.int64):
+    for q0, q1, lo, hi, k0, k1, slot, col in items.astype(np.int64):
         s = seqs.index((lo, hi))
-        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0 and zero == 0
+        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0 and col == vcol[lo]
         n = hi - lo
         c = min(-(-n // 256), 4)
         ck = -(-(-(-n // c)) // 32) * 32
