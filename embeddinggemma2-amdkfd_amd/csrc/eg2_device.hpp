@@ -70,11 +70,36 @@ __device__ __forceinline__ float fp16_bits_to_fp32(uint32_t h) {
 }
 
 // Round-half-away-from-zero like C roundf, clamped to int8 (quants.c:169-174).
+// roundf(v) == truncf(v + copysignf(0.5 - 2^-25, v)) for every finite float
+// (checked over all 2^32 bit patterns): adding the largest float below 0.5
+// carries into the next integer exactly when |frac(v)| >= 0.5, and the
+// conversion truncates (saturating; NaN converts to 0). Four VALU
+// instructions instead of the eight of truncf/compare/select.
 __device__ __forceinline__ int32_t q8_round(float v) {
-  int32_t q = (int32_t)__builtin_roundf(v);
+  int32_t q = (int32_t)(v + __builtin_copysignf(0x1.fffffep-2f, v));
   q = q < -128 ? -128 : q;
   q = q > 127 ? 127 : q;
   return q;
+}
+
+// v combined (op: max or +) with its copies in lanes l ^ 16 and l ^ 32,
+// i.e. over the four 16-lane rows, on the VALU: v_permlane16_swap and
+// v_permlane32_swap of v with itself leave v of lane l and of its partner in
+// the two results (in an order that differs between the rows, so op must
+// be commutative; + of two floats is). Same values as two __shfl_xor steps
+// (16, then 32) without the LDS round trips.
+template <typename Op>
+__device__ __forceinline__ float rows4_reduce(float v, Op op) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_max(float v) {
+  return rows4_reduce(v, [](float x, float y) { return fmaxf(x, y); });
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+  return rows4_reduce(v, [](float x, float y) { return x + y; });
 }
 
 // Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
@@ -128,7 +153,7 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
   if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
   int32_t qi[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) qi[i] = amax != 0.0f ? q8_round(v[i] * id) : 0;
+  for (int i = 0; i < N; ++i) qi[i] = q8_round(v[i] * id);  // id = 0 for an all-zero block
   uint32_t w[N / 4];
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) w[i] = pack_i8x4(qi[4 * i], qi[4 * i + 1], qi[4 * i + 2], qi[4 * i + 3]);

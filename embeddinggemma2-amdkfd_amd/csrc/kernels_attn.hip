@@ -41,6 +41,8 @@
 // probabilities of keys 8j..8j+7: exactly the k-slots it supplies to the
 // P.V MFMA, whose V^T operand is then one aligned 16-byte chunk per lane.
 #include <algorithm>
+#include <cfloat>
+#include <type_traits>
 
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
@@ -87,12 +89,26 @@ __device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned l
 // of a 16x16 block lands in lane group j (lanes 16j..16j+15) as register v,
 // so this order gives lane group j the keys 8j..8j+7 -- the k-slots it
 // supplies to the P.V MFMA.
-__device__ __forceinline__ int score_key(int kb, int i) { return 8 * (i >> 2) + 4 * kb + (i & 3); }
+__host__ __device__ constexpr int score_key(int kb, int i) { return 8 * (i >> 2) + 4 * kb + (i & 3); }
 // Chunk swizzles. K rows (32 chunks of 16 bytes per half): XOR with a key
 // hash that is distinct over the 16 keys one score block reads. V^T rows
 // (4 chunks): the GEMM's pattern, distinct over 4 rows 64 bytes apart.
-__device__ __forceinline__ int kswz(int key) { return (key & 3) | ((key >> 3) << 2); }
-__device__ __forceinline__ int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+__host__ __device__ constexpr int kswz(int key) { return (key & 3) | ((key >> 3) << 2); }
+__host__ __device__ constexpr int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+// What the kernel's precomputed fragment offsets rely on: the second score
+// block's key is the first's + 4 with the same K swizzle (below 16), and
+// the V^T swizzle of dim row 16 d + q depends on d only through d & 1.
+constexpr bool fragment_offsets_hold() {
+  for (int q = 0; q < 16; ++q) {
+    if (score_key(1, q) != score_key(0, q) + 4 || kswz(score_key(1, q)) != kswz(score_key(0, q)) ||
+        kswz(score_key(0, q)) >= 16)
+      return false;
+    for (int d = 0; d < 16; ++d)
+      if (vswz(16 * d + q) != vswz(16 * (d & 1) + q)) return false;
+  }
+  return true;
+}
+static_assert(fragment_offsets_hold(), "attention fragment offsets");
 
 // Final context of NB Q8_0 blocks of one wave (16 queries x one head):
 // context = acc / l, then Q8_0 per 32 dims (quants.c:97-177). f[2j] and
@@ -120,9 +136,7 @@ __device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l
     for (int i = 0; i < 8; ++i) amax[b] = fmaxf(amax[b], fabsf(vals[b][i]));
   }
 #pragma unroll
-  for (int b = 0; b < NB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 16, 64));
-#pragma unroll
-  for (int b = 0; b < NB; ++b) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], 32, 64));
+  for (int b = 0; b < NB; ++b) amax[b] = rows4_max(amax[b]);
   // Row t of the row tiles: 32-row tile t/32, row t%32; this head's
   // blocks are 8 head .. 8 head + 7 of the row's 24.
   int8_t* qrow_out = cq + (size_t)(t >> 5) * (kEmbd / kQK) * 1024 + (size_t)(head * 8 + b0) * 1024 + (t & 31) * 16 +
@@ -133,7 +147,7 @@ __device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l
     const float id = amax[b] == 0.0f ? 0.0f : 1.0f / d;
     int32_t qv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qv[i] = amax[b] == 0.0f ? 0 : q8_round(vals[b][i] * id);
+    for (int i = 0; i < 8; ++i) qv[i] = q8_round(vals[b][i] * id);  // id = 0 for an all-zero block
     if (active) {
       *reinterpret_cast<uint32_t*>(qrow_out + b * 1024) = pack_i8x4(qv[0], qv[1], qv[2], qv[3]);
       *reinterpret_cast<uint32_t*>(qrow_out + b * 1024 + 512) = pack_i8x4(qv[4], qv[5], qv[6], qv[7]);
@@ -246,12 +260,30 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     floatx4 acc[16];
 #pragma unroll
     for (int db = 0; db < 16; ++db) acc[db] = floatx4{};
-    float m_run = -INFINITY, l_run = 0.0f;  // running max in log2 units
+    // Running max in log2 units; -FLT_MAX (not -inf) until a key is in
+    // range, so exp2 of a masked score (-inf) minus it is 0 and exp2 of it
+    // minus a real maximum is 0, with no test.
+    float m_run = -FLT_MAX, l_run = 0.0f;
 
-    const int key0 = score_key(0, qi), key1 = score_key(1, qi);
-    const int kf0 = kswz(key0), kf1 = kswz(key1);
-    int stage = 0;
-    for (uint32_t k0 = k_first; k0 < kv_hi; k0 += kKvTile, stage ^= 1) {
+    // Lane-varying LDS byte offsets of the fragment reads, fixed for the
+    // item; the stage and the MFMA step only add immediates. K: key row
+    // key0 (key1 = key0 + 4 has the same swizzle, 4 KB further), chunk
+    // (4 st + grp) ^ kf = 4 (st ^ (kf >> 2)) + (grp ^ (kf & 3)), and
+    // st ^ (kf >> 2) = (st & 4) + ((st & 3) ^ (kf >> 2)) for kf < 16.
+    // V^T: dim row e = 16 d + qi, chunk grp ^ vswz(e), where vswz(e)
+    // depends on d only through d & 1.
+    const int key0 = score_key(0, qi), kf = kswz(key0);
+    int kofs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kofs[j] = key0 * 1024 + 64 * (j ^ (kf >> 2)) + 16 * (grp ^ (kf & 3));
+    int vofs[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) vofs[p] = kKStage + 64 * qi + 16 * (grp ^ vswz(16 * p + qi));
+
+    // One 32-key tile in LDS stage S (a compile-time constant, so every
+    // fragment address is a per-item register plus an immediate).
+    auto key_tile = [&](uint32_t k0, auto stage_tag) {
+      constexpr int S = decltype(stage_tag)::value;
       // This tile's DMA (and the queries) have landed for every wave, and
       // every wave is done with the other stage, which the next tile's DMA
       // now refills (on the last tile: a harmless refill of the idle stage).
@@ -260,33 +292,30 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       if (!compute) {
 #pragma unroll
         for (int j = 0; j < kDmaPerWave; ++j) {
-          dma_k(k1, stage ^ 1, j);
-          dma_v(k1, stage ^ 1, j);
+          dma_k(k1, S ^ 1, j);
+          dma_v(k1, S ^ 1, j);
         }
-        continue;
+        return;
       }
-      const unsigned char* kst = lds + stage * kStage;
-      const unsigned char* vst = kst + kKStage;
+      const unsigned char* st_base = lds + S * kStage;
 
       // S^T = K . Q^T, two 16-key blocks; this wave's share of the next
       // tile's K rows goes out between the MFMAs.
       floatx4 s0 = floatx4{}, s1 = floatx4{};
-      const unsigned char* krow0 = kst + key0 * 1024;
-      const unsigned char* krow1 = kst + key1 * 1024;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const int c = 4 * st + grp;
-        const half8 ah = *reinterpret_cast<const half8*>(krow0 + 16 * (c ^ kf0));
-        const half8 al = *reinterpret_cast<const half8*>(krow0 + 512 + 16 * (c ^ kf0));
-        const half8 bh = *reinterpret_cast<const half8*>(krow1 + 16 * (c ^ kf1));
-        const half8 bl = *reinterpret_cast<const half8*>(krow1 + 512 + 16 * (c ^ kf1));
+        const unsigned char* krow = st_base + kofs[st & 3] + 256 * (st >> 2);
+        const half8 ah = *reinterpret_cast<const half8*>(krow);
+        const half8 al = *reinterpret_cast<const half8*>(krow + 512);
+        const half8 bh = *reinterpret_cast<const half8*>(krow + 4096);
+        const half8 bl = *reinterpret_cast<const half8*>(krow + 4096 + 512);
         s0 = mfma(ah, qh[st], s0);
         s1 = mfma(bh, qh[st], s1);
         s0 = mfma(ah, ql[st], s0);
         s1 = mfma(bh, ql[st], s1);
         s0 = mfma(al, qh[st], s0);
         s1 = mfma(bl, qh[st], s1);
-        if (st < kDmaPerWave) dma_k(k1, stage ^ 1, st);
+        if (st < kDmaPerWave) dma_k(k1, S ^ 1, st);
       }
       // sc[4kb + v] = 16 x the score of key k0 + 8grp + 4kb + v, taken to
       // log2 units: exp(x) = exp2(x * log2e).
@@ -307,27 +336,24 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       float mt = sc[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) mt = fmaxf(mt, sc[i]);
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float m_new = fmaxf(m_run, rows4_max(mt));
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       float psum = 0.0f;
       half8 ph, pl;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p = sc[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[i] - m_new);
+        const float p = __builtin_amdgcn_exp2f(sc[i] - m_new);
         psum += p;
         const _Float16 h = (_Float16)p;
         ph[i] = h;
         pl[i] = (_Float16)(p - (float)h);
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l_run = l_run * alpha + psum;
+      l_run = l_run * alpha + rows4_sum(psum);
       m_run = m_new;
       // alpha is exactly 1 in every lane whose maximum did not grow; skip
-      // the rescale when that holds for the whole wave (most tiles).
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+      // the rescale when that holds for the whole wave (most tiles), and on
+      // the first tile, where acc is still zero.
+      if (k0 != k_first && __builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
         for (int db = 0; db < 16; ++db) acc[db] *= alpha;
       }
@@ -339,20 +365,27 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 #pragma unroll
       for (int pr = 0; pr < 8; ++pr) {
         const int d0 = 2 * pr, d1 = 2 * pr + 1;
-        const int e0 = 16 * d0 + qi, e1 = 16 * d1 + qi;
-        const int c0 = grp ^ vswz(e0), c1 = grp ^ vswz(e1);
-        const half8 vh0 = *reinterpret_cast<const half8*>(vst + e0 * 64 + 16 * c0);
-        const half8 vl0 = *reinterpret_cast<const half8*>(vst + (kHeadDim + e0) * 64 + 16 * c0);
-        const half8 vh1 = *reinterpret_cast<const half8*>(vst + e1 * 64 + 16 * c1);
-        const half8 vl1 = *reinterpret_cast<const half8*>(vst + (kHeadDim + e1) * 64 + 16 * c1);
+        const unsigned char* v0 = st_base + vofs[0] + 1024 * d0;
+        const unsigned char* v1 = st_base + vofs[1] + 1024 * d1;
+        const half8 vh0 = *reinterpret_cast<const half8*>(v0);
+        const half8 vl0 = *reinterpret_cast<const half8*>(v0 + kHeadDim * 64);
+        const half8 vh1 = *reinterpret_cast<const half8*>(v1);
+        const half8 vl1 = *reinterpret_cast<const half8*>(v1 + kHeadDim * 64);
         acc[d0] = mfma(vh0, ph, acc[d0]);
         acc[d1] = mfma(vh1, ph, acc[d1]);
         acc[d0] = mfma(vh0, pl, acc[d0]);
         acc[d1] = mfma(vh1, pl, acc[d1]);
         acc[d0] = mfma(vl0, ph, acc[d0]);
         acc[d1] = mfma(vl1, ph, acc[d1]);
-        if (pr < kDmaPerWave) dma_v(k1, stage ^ 1, pr);
+        if (pr < kDmaPerWave) dma_v(k1, S ^ 1, pr);
       }
+    };
+    // Key tiles alternate between the two stages, starting in stage 0.
+    for (uint32_t k0 = k_first; k0 < kv_hi;) {
+      key_tile(k0, std::integral_constant<int, 0>{});
+      if ((k0 += kKvTile) >= kv_hi) break;
+      key_tile(k0, std::integral_constant<int, 1>{});
+      k0 += kKvTile;
     }
     if (!compute) continue;
 

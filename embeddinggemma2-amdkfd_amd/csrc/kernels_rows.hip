@@ -128,13 +128,9 @@ __device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int 
     const float dd = amax / 127.0f;
     const float id = amax != 0.0f ? 1.0f / dd : 0.0f;
     const int e = 4 * (lane + 64 * r), b = e / kQK;
-    int32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-    if (amax != 0.0f) {
-      q0 = q8_round(v[r].x * id);
-      q1 = q8_round(v[r].y * id);
-      q2 = q8_round(v[r].z * id);
-      q3 = q8_round(v[r].w * id);
-    }
+    // id = 0 for an all-zero block, whose values then quantize to 0.
+    const int32_t q0 = q8_round(v[r].x * id), q1 = q8_round(v[r].y * id), q2 = q8_round(v[r].z * id),
+                  q3 = q8_round(v[r].w * id);
     *reinterpret_cast<uint32_t*>(q + q8_tile_offset(t, e, kBlocks)) = pack_i8x4(q0, q1, q2, q3);
     if ((lane & 7) == 0) d[(size_t)b * ld] = fp16_bits_to_fp32(fp32_to_fp16_bits(dd));
   }
