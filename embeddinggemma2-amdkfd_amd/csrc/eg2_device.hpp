@@ -163,14 +163,25 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
     *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
 }
 
-// kernels.c:367-371 gelu_tanh(g) times u (engine.c's GeGLU), with the
-// device tanhf, in the order written.
+// kernels.c:367-371 gelu_tanh(g) = 0.5 g (1 + tanh(z)), z = s g (1 + a g^2)
+// (the inner term in the order written), times u (engine.c's GeGLU),
+// evaluated as g / (1 + exp(-2 z)): the same function, since
+// 0.5 (1 + tanh z) = 1 / (1 + e^(-2z)), in a dozen instructions instead of
+// a tanhf. 1 + e^(-2z) is formed without cancellation, so the result is
+// within a few ulps of the exact value everywhere (the reference's fp32
+// 1 + tanhf(z) loses relative accuracy as z goes negative); below
+// z = -9, where the reference's tanhf(z) is exactly -1, it is exactly 0.
 __device__ __forceinline__ float gelu_mul(float g, float u) {
   const float a = 0.044715f;
   const float s = 0.79788456080286535587989211986876f;
   const float inner = s * g * (1.0f + a * g * g);
-  const float gelu = 0.5f * g * (1.0f + tanhf(inner));
-  return gelu * u;
+  // e^(-2z) = 2^(-2 log2(e) z), the exponent capped so the sum stays finite.
+  const float e = __builtin_amdgcn_exp2f(fminf(inner * -2.8853900817779268f, 126.0f));
+  const float den = 1.0f + e;
+  float r = __builtin_amdgcn_rcpf(den);
+  r = __builtin_fmaf(__builtin_fmaf(-den, r, 1.0f), r, r);  // Newton step: 1/den to about half an ulp
+  r = inner < -9.0f ? 0.0f : r;
+  return (g * r) * u;
 }
 
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):

@@ -1,8 +1,8 @@
 // Row kernels of the packed encoder forward. They are HBM-bound; each one
 // fuses the element-wise work between two GEMMs so a token row is read and
 // written once, and each reproduces the reference's operation order, so its
-// results are bit-identical to the CPU path for identical inputs (tanhf in
-// the GeGLU kernel is the one libm function evaluated on the device).
+// results are bit-identical to the CPU path for identical inputs (the GeGLU
+// kernel's GELU, evaluated through exp2 instead of tanhf, is the exception).
 //
 // Work mapping. One 64-lane wave per 768-wide token row (a 2048-token wave
 // gives two waves per SIMD), so latency, not bandwidth, is what the design
