@@ -92,9 +92,13 @@ __device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned l
 __host__ __device__ constexpr int score_key(int kb, int i) { return 8 * (i >> 2) + 4 * kb + (i & 3); }
 // Chunk swizzles. K rows (32 chunks of 16 bytes per half): XOR with a key
 // hash that is distinct over the 16 keys one score block reads. V^T rows
-// (4 chunks): the GEMM's pattern, distinct over 4 rows 64 bytes apart.
+// (4 chunks of a 64-byte row): XOR with (row >> 1) & 3. Both were chosen by
+// measurement (SQ_LDS_BANK_CONFLICT over the fragment read patterns on
+// this part): the V^T pattern must differ between rows 2i and 2i + 1 --
+// an XOR of ((row >> 1) ^ (row >> 3)) & 3, distinct over every 4 rows 64
+// bytes apart, still cost 4 conflict cycles per ds_read_b128.
 __host__ __device__ constexpr int kswz(int key) { return (key & 3) | ((key >> 3) << 2); }
-__host__ __device__ constexpr int vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+__host__ __device__ constexpr int vswz(int d) { return (d >> 1) & 3; }
 // What the kernel's precomputed fragment offsets rely on: the second score
 // block's key is the first's + 4 with the same K swizzle (below 16), and
 // the V^T swizzle of dim row 16 d + q depends on d only through d & 1.
