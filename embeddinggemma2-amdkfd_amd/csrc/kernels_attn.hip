@@ -303,24 +303,56 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       }
       const unsigned char* st_base = lds + S * kStage;
 
+      // Fragment reads run one MFMA step ahead of their use (two register
+      // sets), so the LDS latency overlaps the previous step's MFMAs.
+      struct KFrag {
+        half8 ah, al, bh, bl;  // key rows key0 / key0 + 4, hi and lo halves
+      };
+      auto kfrag = [&](int st) {
+        const unsigned char* krow = st_base + kofs[st & 3] + 256 * (st >> 2);
+        KFrag f;
+        f.ah = *reinterpret_cast<const half8*>(krow);
+        f.al = *reinterpret_cast<const half8*>(krow + 512);
+        f.bh = *reinterpret_cast<const half8*>(krow + 4096);
+        f.bl = *reinterpret_cast<const half8*>(krow + 4096 + 512);
+        return f;
+      };
+      struct VFrag {
+        half8 h0, l0, h1, l1;  // V^T rows of 16-dim blocks 2 pr and 2 pr + 1
+      };
+      auto vfrag = [&](int pr) {
+        const unsigned char* v0 = st_base + vofs[0] + 1024 * (2 * pr);
+        const unsigned char* v1 = st_base + vofs[1] + 1024 * (2 * pr + 1);
+        VFrag f;
+        f.h0 = *reinterpret_cast<const half8*>(v0);
+        f.l0 = *reinterpret_cast<const half8*>(v0 + kHeadDim * 64);
+        f.h1 = *reinterpret_cast<const half8*>(v1);
+        f.l1 = *reinterpret_cast<const half8*>(v1 + kHeadDim * 64);
+        return f;
+      };
+
       // S^T = K . Q^T, two 16-key blocks; this wave's share of the next
       // tile's K rows goes out between the MFMAs.
       floatx4 s0 = floatx4{}, s1 = floatx4{};
+      KFrag kfr[2];
+      kfr[0] = kfrag(0);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const unsigned char* krow = st_base + kofs[st & 3] + 256 * (st >> 2);
-        const half8 ah = *reinterpret_cast<const half8*>(krow);
-        const half8 al = *reinterpret_cast<const half8*>(krow + 512);
-        const half8 bh = *reinterpret_cast<const half8*>(krow + 4096);
-        const half8 bl = *reinterpret_cast<const half8*>(krow + 4096 + 512);
-        s0 = mfma(ah, qh[st], s0);
-        s1 = mfma(bh, qh[st], s1);
-        s0 = mfma(ah, ql[st], s0);
-        s1 = mfma(bh, ql[st], s1);
-        s0 = mfma(al, qh[st], s0);
-        s1 = mfma(bl, qh[st], s1);
+        if (st + 1 < 8) kfr[(st + 1) & 1] = kfrag(st + 1);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above this step's MFMAs
+        const KFrag& f = kfr[st & 1];
+        s0 = mfma(f.ah, qh[st], s0);
+        s1 = mfma(f.bh, qh[st], s1);
+        s0 = mfma(f.ah, ql[st], s0);
+        s1 = mfma(f.bh, ql[st], s1);
+        s0 = mfma(f.al, qh[st], s0);
+        s1 = mfma(f.bl, qh[st], s1);
         if (st < kDmaPerWave) dma_k(k1, S ^ 1, st);
       }
+      // The first V^T fragments go out before the softmax.
+      VFrag vfr[2];
+      vfr[0] = vfrag(0);
+      __builtin_amdgcn_sched_barrier(0);
       // sc[4kb + v] = 16 x the score of key k0 + 8grp + 4kb + v, taken to
       // log2 units: exp(x) = exp2(x * log2e).
       float sc[8];
@@ -369,18 +401,15 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
 #pragma unroll
       for (int pr = 0; pr < 8; ++pr) {
         const int d0 = 2 * pr, d1 = 2 * pr + 1;
-        const unsigned char* v0 = st_base + vofs[0] + 1024 * d0;
-        const unsigned char* v1 = st_base + vofs[1] + 1024 * d1;
-        const half8 vh0 = *reinterpret_cast<const half8*>(v0);
-        const half8 vl0 = *reinterpret_cast<const half8*>(v0 + kHeadDim * 64);
-        const half8 vh1 = *reinterpret_cast<const half8*>(v1);
-        const half8 vl1 = *reinterpret_cast<const half8*>(v1 + kHeadDim * 64);
-        acc[d0] = mfma(vh0, ph, acc[d0]);
-        acc[d1] = mfma(vh1, ph, acc[d1]);
-        acc[d0] = mfma(vh0, pl, acc[d0]);
-        acc[d1] = mfma(vh1, pl, acc[d1]);
-        acc[d0] = mfma(vl0, ph, acc[d0]);
-        acc[d1] = mfma(vl1, ph, acc[d1]);
+        if (pr + 1 < 8) vfr[(pr + 1) & 1] = vfrag(pr + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const VFrag& f = vfr[pr & 1];
+        acc[d0] = mfma(f.h0, ph, acc[d0]);
+        acc[d1] = mfma(f.h1, ph, acc[d1]);
+        acc[d0] = mfma(f.h0, pl, acc[d0]);
+        acc[d1] = mfma(f.h1, pl, acc[d1]);
+        acc[d0] = mfma(f.l0, ph, acc[d0]);
+        acc[d1] = mfma(f.l1, ph, acc[d1]);
         if (pr < kDmaPerWave) dma_v(k1, S ^ 1, pr);
       }
     };
