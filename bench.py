@@ -15,7 +15,10 @@ a serving loop keeps them; value = 2048 tokens / (timed seconds / steps).
 The latency of one wave alone is reported beside it.
 The roofline entry times the dominant kernel (the gate|up projection GEMM,
 2048 x 2304 x 768, with the GeGLU and its Q8_0 quantization in its
-epilogue) with HIP events on the stream it runs on. The CPU
+epilogue) with HIP events on the stream it runs on; beside the int8 MFMA
+roofline it reports the floor the exact Q8_0 scaling puts on the VALU
+(3 fp32 operations per output per 32-block), which is what bounds the
+kernel. The CPU
 baseline is the oracle (the C restatement of the reference CPU path) on the
 same wave, timed on the host's cores.
 """
@@ -34,6 +37,10 @@ GEMM_N, GEMM_M, GEMM_K = 2048, 2 * 1152, 768
 PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA (the projection GEMMs)
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (attention)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# The exact Q8_0 scaling is 3 fp32 VALU operations per output per 32-block;
+# a wave64 fp32 VALU instruction occupies a SIMD for 4 cycles (no packed
+# fp32 here), 1024 SIMDs at the 2.4 GHz peak engine clock.
+VALU_WAVE_INSTR_PER_US = 1024 * 2400.0 / 4
 METRIC = "embedded tokens/s @2048-tok packed waves (1 GPU); Q8_0 GEMM % MFMA peak"
 
 
@@ -363,7 +370,10 @@ def main():
         gemm_ms = time_gemm(eg2, torch, max(20, args.steps), 5)
         flops = 2.0 * GEMM_N * GEMM_M * GEMM_K
         achieved = flops / (gemm_ms / 1e3) / 1e12
-        log(f"gate|up + GeGLU GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s")
+        scaling_instr = GEMM_N * GEMM_M * (GEMM_K // 32) * 3 // 64
+        valu_floor_us = scaling_instr / VALU_WAVE_INSTR_PER_US
+        log(f"gate|up + GeGLU GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s; exact-scaling VALU floor "
+            f"{valu_floor_us:.2f} us ({100 * valu_floor_us / (gemm_ms * 1e3):.0f}% of the kernel's time)")
         kernels = {} if args.no_kernel_table else kernel_table(eg2, torch, max(20, args.steps))
         for name, k in kernels.items():
             log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak")
@@ -401,7 +411,11 @@ def main():
                                                 "achieved/peak in T int8 op/s)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
-                     "avg_us": round(gemm_ms * 1e3, 2)},
+                     "avg_us": round(gemm_ms * 1e3, 2),
+                     "valu_floor": {"wave_instructions": scaling_instr, "floor_us": round(valu_floor_us, 2),
+                                    "frac": round(valu_floor_us / (gemm_ms * 1e3), 4),
+                                    "what": "exact per-block scaling only: 3 fp32 VALU ops per output per "
+                                            "32-block at 4 cycles per wave64 instruction on 1024 SIMDs, 2.4 GHz"}},
         "kernels": kernels,
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),
