@@ -238,16 +238,10 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
     // Every wave has finished with both stages (previous tile of the grid
     // stride), and every DMA it issued -- including the refill of the idle
     // stage on its last key tile -- has landed, before the first DMA of
-    // this tile overwrites them. That DMA then flies while the queries load.
+    // this tile overwrites them: each wave drains its own DMA, then issues
+    // its query loads, then meets the others at a plain s_barrier (no
+    // memory wait, so the query loads fly across it).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (k_first < kv_hi) {
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        dma_k(k_first, 0, j);
-        dma_v(k_first, 0, j);
-      }
-    }
 
     // Q^T operand of the score MFMA: lane holds query t, dims 32s + 8grp .. +7
     // for s = 0..7. Rows of qs are [hi 768 | lo 768].
@@ -258,6 +252,14 @@ attention_kernel(const _Float16* __restrict__ qs, const _Float16* __restrict__ k
       for (int s = 0; s < 8; ++s) {
         qh[s] = *reinterpret_cast<const half8*>(qrow + 32 * s + 8 * grp);
         ql[s] = *reinterpret_cast<const half8*>(qrow + kEmbd + 32 * s + 8 * grp);
+      }
+    }
+    __builtin_amdgcn_s_barrier();
+    if (k_first < kv_hi) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        dma_k(k_first, 0, j);
+        dma_v(k_first, 0, j);
       }
     }
 
