@@ -69,6 +69,16 @@ __device__ __forceinline__ float fp16_bits_to_fp32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// The Q8_0 scale amax / 127 (quants.c:97-177), correctly rounded like the
+// IEEE division, in three instructions: q = amax * RN(1/127), then one FMA
+// correction with the exact remainder amax - 127 q. Equal to amax / 127.0f
+// for every non-negative finite float (checked over all of them).
+__device__ __forceinline__ float div127(float amax) {
+  constexpr float r = 1.0f / 127.0f;
+  const float q = amax * r;
+  return __builtin_fmaf(__builtin_fmaf(-q, 127.0f, amax), r, q);
+}
+
 // Round-half-away-from-zero like C roundf, clamped to int8 (quants.c:169-174).
 // roundf(v) == truncf(v + copysignf(0.5 - 2^-25, v)) for every finite float
 // (checked over all 2^32 bit patterns): adding the largest float below 0.5
@@ -118,7 +128,7 @@ struct Q8Lane {
 };
 __device__ __forceinline__ Q8Lane q8_quantize_lane(float x) {
   const float amax = half_wave_max(fabsf(x));
-  const float d = amax / 127.0f;
+  const float d = div127(amax);
   Q8Lane r;
   r.d = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
   if (amax == 0.0f) {
@@ -147,7 +157,7 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
   for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
 #pragma unroll
   for (int m = 1; m < P; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-  const float d = amax / 127.0f;
+  const float d = div127(amax);
   const float id = amax != 0.0f ? 1.0f / d : 0.0f;
   if (!store) return;
   if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));

@@ -147,7 +147,7 @@ __device__ __forceinline__ void store_blocks(const floatx4 (&f)[2 * NB], float l
                      4 * grp;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    const float d = amax[b] / 127.0f;
+    const float d = div127(amax[b]);
     const float id = amax[b] == 0.0f ? 0.0f : 1.0f / d;
     int32_t qv[8];
 #pragma unroll

@@ -125,7 +125,7 @@ __device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int 
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const float amax = group8_max(fmaxf(fmaxf(fabsf(v[r].x), fabsf(v[r].y)), fmaxf(fabsf(v[r].z), fabsf(v[r].w))));
-    const float dd = amax / 127.0f;
+    const float dd = div127(amax);
     const float id = amax != 0.0f ? 1.0f / dd : 0.0f;
     const int e = 4 * (lane + 64 * r), b = e / kQK;
     // id = 0 for an all-zero block, whose values then quantize to 0.

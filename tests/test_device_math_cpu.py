@@ -5,12 +5,22 @@ instead of library calls (CPU only; the GPU tests check the kernels).
   truncf(v + copysignf(0.5 - 2^-25, v)); the two agree on every finite
   float (an exhaustive 2^32 sweep was run when the identity was adopted;
   this test covers every float in [-256, 256] plus random bit patterns).
+- Q8_0 scale (eg2_device.hpp div127): amax / 127 as amax * RN(1/127)
+  plus one FMA correction equals the IEEE quotient (exhaustive sweep when
+  adopted; here every float in [0.5, 1024) and a stride over all of them,
+  in C so that fmaf is the real fused operation).
 - GELU (eg2_device.hpp gelu_mul): 0.5 g (1 + tanh z) evaluated as
   g / (1 + e^(-2z)); same function, and in fp32 (with correctly rounded
   exp and reciprocal standing in for the hardware's) within a few ulps of
   the exact value where the reference's fp32 form is itself accurate.
 """
+import os
+import shutil
+import subprocess
+import tempfile
+
 import numpy as np
+import pytest
 
 F = np.float32
 HALF_MINUS = np.nextafter(F(0.5), F(0))  # 0x1.fffffep-2
@@ -81,3 +91,37 @@ def test_gelu_sigmoid_form_fp32_accuracy():
     assert err[inner >= -0.5].max() <= 3
     assert err[(inner >= -9) & (np.abs(exact) > 1e-30)].max() <= 20
     assert (got[inner < -9] == 0).all()
+
+
+DIV127_C = r"""
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+static int check(uint32_t u) {
+  float a; memcpy(&a, &u, 4);
+  const float r = 1.0f / 127.0f;
+  volatile float want = a / 127.0f;
+  float q = a * r;
+  float got = fmaf(fmaf(-q, 127.0f, a), r, q);
+  return memcmp(&got, (const void*)&want, 4) != 0;
+}
+int main(int argc, char** argv) {
+  uint64_t bad = 0;
+  for (uint64_t u = 0x3F000000u; u < 0x44800000u; ++u) bad += check((uint32_t)u);  /* [0.5, 1024) */
+  for (uint64_t u = 0; u < 0x7F800000u; u += 7) bad += check((uint32_t)u);           /* all, stride 7 */
+  printf("%llu\n", (unsigned long long)bad);
+  return bad != 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_div127_fma_correction_is_the_ieee_quotient():
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "div127.c"), os.path.join(d, "div127")
+        open(src, "w").write(DIV127_C)
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm"], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+        assert out.returncode == 0 and out.stdout.strip() == "0", out.stdout
