@@ -22,6 +22,7 @@ hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, h
 hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st);
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);
 hipError_t launch_pool_l2(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st);
+hipError_t launch_pool_mean(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st);
 hipError_t launch_l2_prefix(float* x, int width, int dims, int rows, hipStream_t st);
 // xq/wq: int8 row tiles of the activations [n][k] and weights [m][k];
 // xd/wd: their block scales transposed, [k/32][ldx] and [k/32][ldw].

@@ -45,6 +45,7 @@ constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:2
 // Transposed-v columns: every sequence (and the padding sequence) starts at
 // a multiple of 32, so at most kCap + 31 * (kCap + 1) columns, rounded to 32.
 constexpr unsigned kVtCols = (kCap + 31 * (kCap + 1) + 31) / 32 * 32;
+constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
 constexpr double kTimeoutSeconds = 30.0;  // src/gemma2_kfd.cpp:21
@@ -102,7 +103,7 @@ struct Lane {
   float* out_h;
   std::map<unsigned, hipGraphExec_t> graphs;  // key: 2 * padded rows + (wave has split sequences)
   bool staged_merge = false;
-  unsigned staged_tokens = 0, staged_rows = 0;
+  unsigned staged_tokens = 0, staged_rows = 0, staged_longest = 0;
   size_t staged_batch = 0;
   std::map<std::string, double> timings;
 };
@@ -551,8 +552,11 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
   // src/gemma2_kfd.cpp:271-278
   if (!ids || !offsets || !batch || batch > kCap || offsets[0] || offsets[batch] > kCap)
     throw std::runtime_error("HIP batch requires 1..2048 packed tokens and nonempty sequences");
-  for (size_t s = 0; s < batch; ++s)
+  unsigned longest = 0;
+  for (size_t s = 0; s < batch; ++s) {
     if (offsets[s + 1] <= offsets[s]) throw std::runtime_error("invalid HIP sequence offsets");
+    longest = std::max(longest, (unsigned)(offsets[s + 1] - offsets[s]));
+  }
   const unsigned n = (unsigned)offsets[batch];
   for (unsigned i = 0; i < n; ++i)
     if (ids[i] < 0 || ids[i] >= kVocab) throw std::runtime_error("token ID out of range");
@@ -622,6 +626,7 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
   ln.staged_tokens = n;
   ln.staged_rows = rows;
   ln.staged_batch = batch;
+  ln.staged_longest = longest;
 }
 
 // Layer stack (graph or eager), then kernels.c:417-427 (mean + L2 per
@@ -653,7 +658,15 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
       } else {
         record_layers(ln, ln.staged_rows, ln.staged_merge);
       }
-      launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
+      // One workgroup per sequence reads it through one CU; past 256 tokens
+      // the mean spreads over 12 workgroups per sequence and the L2 follows
+      // (the same result, bit for bit).
+      if (ln.staged_longest > kPoolSplitLen) {
+        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
+        launch("pool_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+      } else {
+        launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
+      }
       if (dense_) {
         launch("dense_quant", eg2::launch_quantize_rows(ln.pooled, kEmbd, ln.cq, ln.cd, B, s));
         gemm("dense_2", ln.cq, ln.cd, dense2_, ln.mid, B, kDenseFF, s);

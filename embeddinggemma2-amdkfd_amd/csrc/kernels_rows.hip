@@ -368,14 +368,10 @@ rms_norm_rows_kernel(float* __restrict__ x, const float* __restrict__ w, float e
 // token order (two batches of kPoolBatch rows in flight), scales by 1/n,
 // then L2-normalises in the SSE2 order (kernels.c:393-396).
 constexpr int kPoolBatch = 32;
-__global__ void __launch_bounds__(kEmbd)
-pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets, float* __restrict__ out) {
-  __shared__ float acc[kEmbd];
-  __shared__ float total;
-  const int s = blockIdx.x, e = threadIdx.x;
-  const uint32_t lo = offsets[s], hi = offsets[s + 1];
-  // The sum runs in token order; the loads of the next batch are in flight
-  // while the current batch is added.
+
+// Column e of rows [lo, hi) summed in token order; the loads of the next
+// batch of rows are in flight while the current batch is added.
+__device__ __forceinline__ float column_sum(const float* __restrict__ x, uint32_t lo, uint32_t hi, int e) {
   float sum = 0.0f;
   float v[2][kPoolBatch];
   auto load = [&](float (&b)[kPoolBatch], uint32_t t) {
@@ -393,6 +389,16 @@ pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets
     for (int i = 0; i < kPoolBatch; ++i)
       if (t + kPoolBatch + i < hi) sum = sum + v[1][i];
   }
+  return sum;
+}
+
+__global__ void __launch_bounds__(kEmbd)
+pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets, float* __restrict__ out) {
+  __shared__ float acc[kEmbd];
+  __shared__ float total;
+  const int s = blockIdx.x, e = threadIdx.x;
+  const uint32_t lo = offsets[s], hi = offsets[s + 1];
+  const float sum = column_sum(x, lo, hi, e);
   const float scale = 1.0f / (float)(hi - lo);
   acc[e] = sum * scale;
   __syncthreads();
@@ -403,6 +409,20 @@ pool_l2_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets
   __syncthreads();
   const float ss = total;
   out[(size_t)s * kEmbd + e] = ss != 0.0f ? acc[e] * (1.0f / __builtin_sqrtf(ss)) : acc[e];
+}
+
+// The mean of pool_l2_kernel alone, one workgroup per (sequence, 64
+// columns): a sequence's rows are read by 12 CUs instead of one, which is
+// what bounds pool_l2_kernel on long sequences. Followed by
+// l2_prefix_kernel over the full width (the same arithmetic as the second
+// half of pool_l2_kernel), the result is pool_l2_kernel's bit for bit.
+__global__ void __launch_bounds__(64)
+pool_mean_kernel(const float* __restrict__ x, const uint32_t* __restrict__ offsets, float* __restrict__ out) {
+  const int s = blockIdx.x, e = 64 * blockIdx.y + threadIdx.x;
+  const uint32_t lo = offsets[s], hi = offsets[s + 1];
+  const float sum = column_sum(x, lo, hi, e);
+  const float scale = 1.0f / (float)(hi - lo);
+  out[(size_t)s * kEmbd + e] = sum * scale;
 }
 
 // kernels.c:393-396 on the first `dims` elements of rows of width `width`
@@ -469,6 +489,11 @@ hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, h
 
 hipError_t launch_pool_l2(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st) {
   hipLaunchKernelGGL(pool_l2_kernel, dim3(batch), dim3(kEmbd), 0, st, x, offsets, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pool_mean(const float* x, const uint32_t* offsets, float* out, int batch, hipStream_t st) {
+  hipLaunchKernelGGL(pool_mean_kernel, dim3(batch, kEmbd / 64), dim3(64), 0, st, x, offsets, out);
   return hipGetLastError();
 }
 

@@ -132,6 +132,11 @@ int eg2_hip_pool_l2(const float* x, const uint32_t* offsets, float* out, unsigne
   return code(eg2::launch_pool_l2(x, offsets, out, (int)batch, as_stream(stream)));
 }
 
+int eg2_hip_pool_mean(const float* x, const uint32_t* offsets, float* out, unsigned batch, void* stream) {
+  if (!x || !offsets || !out || batch == 0 || batch > 65535) return kInvalid;
+  return code(eg2::launch_pool_mean(x, offsets, out, (int)batch, as_stream(stream)));
+}
+
 int eg2_hip_l2_prefix(float* x, unsigned width, unsigned dims, unsigned rows, void* stream) {
   if (!x || rows == 0 || dims == 0 || dims > width || dims % 8 != 0 || dims > 8192) return kInvalid;
   return code(eg2::launch_l2_prefix(x, (int)width, (int)dims, (int)rows, as_stream(stream)));

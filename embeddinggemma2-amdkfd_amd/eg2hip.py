@@ -120,6 +120,7 @@ SIGNATURES = {
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_pool_mean": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8_geglu": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _u, _vp]),
@@ -638,6 +639,11 @@ class ops:
     def pool_l2(cls, x, offsets, out):
         check(lib().eg2_hip_pool_l2(cls._p(x), cls._p(offsets), cls._p(out), out.shape[0], cls._stream()),
               "pool_l2")
+
+    @classmethod
+    def pool_mean(cls, x, offsets, out):
+        check(lib().eg2_hip_pool_mean(cls._p(x), cls._p(offsets), cls._p(out), out.shape[0], cls._stream()),
+              "pool_mean")
 
     @classmethod
     def l2_prefix(cls, x, dims):

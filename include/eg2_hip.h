@@ -132,6 +132,13 @@ int eg2_hip_rms_norm_rows(float *x, const float *w, float eps, unsigned rows, vo
  * src/gemma2_kfd.cpp:337-343. */
 int eg2_hip_pool_l2(const float *x, const uint32_t *offsets, float *out, unsigned batch, void *stream);
 
+/* The mean of eg2_hip_pool_l2 alone (out = [batch][768], the same
+ * token-order sums), spread over 12 workgroups per sequence so that a long
+ * sequence is read by 12 CUs; eg2_hip_l2_prefix(out, 768, 768, batch) then
+ * completes eg2_hip_pool_l2 bit for bit. The executor takes this form for
+ * waves holding a sequence longer than 256 tokens. batch <= 65535. */
+int eg2_hip_pool_mean(const float *x, const uint32_t *offsets, float *out, unsigned batch, void *stream);
+
 /* kernels.c:393-407 ei_l2_normalize / ei_embedding_normalize_prefix on the
  * first `dims` entries of rows of width `width` (dims % 8 == 0). */
 int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, void *stream);

@@ -519,6 +519,34 @@ def test_pool_and_l2_bit_exact(eg2, gpu):
     assert np.array_equal(host(out), want)
 
 
+@pytest.mark.parametrize("lens", [[2048], [1, 700, 300, 1047], [257, 5, 33], [1]])
+def test_pool_mean_then_l2_equals_pool_l2(eg2, gpu, lens):
+    """The column-split mean (12 workgroups per sequence, the executor's
+    form for waves with a sequence over 256 tokens) followed by the
+    full-width L2 is eg2_hip_pool_l2 bit for bit, and both match the
+    oracle's mean + L2."""
+    import torch
+
+    T = sum(lens)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    x = (RNG.standard_normal((T, N_EMBD)) * 4).astype(np.float32)
+    xg, og = dev(x, gpu), dev(offsets, gpu)
+    one = empty((len(lens), N_EMBD), torch.float32, gpu)
+    eg2.ops.pool_l2(xg, og, one)
+    two = empty((len(lens), N_EMBD), torch.float32, gpu)
+    eg2.ops.pool_mean(xg, og, two)
+    mean = host(two).copy()
+    eg2.ops.l2_prefix(two, N_EMBD)
+    assert np.array_equal(host(one), host(two))
+    # the mean half alone: token-order float32 sums scaled by 1/n
+    for s in range(len(lens)):
+        a, b = offsets[s], offsets[s + 1]
+        acc = np.zeros(N_EMBD, np.float32)
+        for t in range(a, b):
+            acc = (acc + x[t]).astype(np.float32)
+        assert np.array_equal(mean[s], (acc * (np.float32(1) / np.float32(b - a))).astype(np.float32))
+
+
 @pytest.mark.parametrize("dims", [128, 256, 512, 768])
 def test_l2_prefix_bit_exact(eg2, gpu, dims):
     e = RNG.standard_normal((20, N_EMBD)).astype(np.float32)

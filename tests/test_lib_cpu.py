@@ -88,6 +88,8 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_l2_prefix(p, 768, 769, 1, None) == inval
     assert lib.eg2_hip_l2_prefix(p, 768, 100, 1, None) == inval
     assert lib.eg2_hip_pool_l2(p, p, p, 0, None) == inval
+    assert lib.eg2_hip_pool_mean(p, p, p, 0, None) == inval
+    assert lib.eg2_hip_pool_mean(p, p, p, 65536, None) == inval
 
 
 def test_vt_columns_align_each_sequence(eg2):
