@@ -228,10 +228,11 @@ def kernel_only(kind, steps):
 COPY_MIB = 256
 
 
-def config5_stream(vocab, seed=42, n_requests=1000):
+def config5_stream(vocab, seed=42, n_requests=1000, with_requests=False):
     """The sustained dynamic-batching stream: n_requests requests of U{1..16}
     texts, token lengths floor(exp(U(ln 4, ln 2048))), ids uniform in the
-    vocabulary, output dimensions cycling 128, 256, 512, 768 per request."""
+    vocabulary, output dimensions cycling 128, 256, 512, 768 per request.
+    with_requests adds the texts-per-request counts."""
     import numpy as np
 
     rng = np.random.default_rng(seed)
@@ -241,6 +242,8 @@ def config5_stream(vocab, seed=42, n_requests=1000):
     offsets = np.concatenate([[0], np.cumsum(lens)])
     ids = rng.integers(0, vocab, int(offsets[-1])).astype(np.int32)
     dims = np.array([128, 256, 512, 768])[np.repeat(np.arange(n_requests), texts) % 4]
+    if with_requests:
+        return ids, offsets, dims, texts
     return ids, offsets, dims
 
 

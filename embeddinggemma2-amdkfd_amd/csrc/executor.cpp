@@ -67,6 +67,120 @@ bool env_flag(const char* name, bool dflt) {
   return v[0] == '1';
 }
 
+const ei_tensor* find_tensor(const ei_gguf* g, const std::string& name) {
+  for (uint64_t i = 0; i < g->n_tensors; ++i)
+    if (str_eq(g->tensors[i].name, name.c_str())) return &g->tensors[i];
+  return nullptr;
+}
+
+// A tensor of `type` with shape [ne0, ne1] (ne[2] = ne[3] = 1) whose byte
+// count is exactly what that shape takes, with its data present
+// (model.c:79-105 names; model.c:93-99 checks type and shape). Every tensor
+// the executor uploads goes through this check first, so no upload or
+// kernel reads past a tensor whose record disagrees with its shape.
+const ei_tensor* checked_tensor(const ei_gguf* g, const std::string& name, uint32_t type, uint64_t ne0, uint64_t ne1,
+                                bool required = true) {
+  const ei_tensor* t = find_tensor(g, name);
+  if (!t) {
+    if (required) throw std::runtime_error("missing tensor: " + name);
+    return nullptr;
+  }
+  const uint64_t want_bytes = type == EI_T_Q8_0 ? ne1 * (ne0 / 32) * 34 : ne0 * ne1 * 4;
+  const bool ok_type = t->type == type && (type == EI_T_Q8_0 || type == EI_T_F32);
+  if (!ok_type || (type == EI_T_Q8_0 && ne0 % 32 != 0))
+    throw std::runtime_error("unexpected type: " + name + (type == EI_T_Q8_0 ? " (need Q8_0)" : " (need F32)"));
+  if (t->n_dims < 1 || t->n_dims > 4 || t->ne[0] != ne0 || t->ne[1] != ne1 || t->ne[2] != 1 || t->ne[3] != 1)
+    throw std::runtime_error("unexpected shape: " + name + " (need [" + std::to_string(ne0) + ", " +
+                             std::to_string(ne1) + "])");
+  if (t->n_bytes != want_bytes || !t->data) throw std::runtime_error("unexpected byte count: " + name);
+  return t;
+}
+
+const ei_kv* find_kv(const ei_gguf* g, const char* key) {
+  for (uint64_t i = 0; i < g->n_kv; ++i)
+    if (str_eq(g->kv[i].key, key)) return &g->kv[i];
+  return nullptr;
+}
+
+// model.c:71-77 read these through ei_gguf_kv_f64/_u64, which take the
+// normalised union member (gguf.c:46-61); an integer-typed key read as a
+// float (or the reverse) is converted here instead of reinterpreted.
+double kv_f64(const ei_gguf* g, const char* key, double dflt) {
+  const ei_kv* k = find_kv(g, key);
+  if (!k) return dflt;
+  switch (k->type) {
+    case EI_GGUF_F32:
+    case EI_GGUF_F64: return k->v.f64;
+    case EI_GGUF_I8: case EI_GGUF_I16: case EI_GGUF_I32: case EI_GGUF_I64: return (double)k->v.i64;
+    case EI_GGUF_U8: case EI_GGUF_U16: case EI_GGUF_U32: case EI_GGUF_U64: return (double)k->v.u64;
+    default: throw std::runtime_error(std::string("GGUF key is not numeric: ") + key);
+  }
+}
+
+uint64_t kv_u64(const ei_gguf* g, const char* key, uint64_t dflt) {
+  const ei_kv* k = find_kv(g, key);
+  if (!k) return dflt;
+  switch (k->type) {
+    case EI_GGUF_U8: case EI_GGUF_U16: case EI_GGUF_U32: case EI_GGUF_U64: return k->v.u64;
+    case EI_GGUF_I8: case EI_GGUF_I16: case EI_GGUF_I32: case EI_GGUF_I64:
+      if (k->v.i64 < 0) throw std::runtime_error(std::string("negative GGUF key: ") + key);
+      return (uint64_t)k->v.i64;
+    default: throw std::runtime_error(std::string("GGUF key is not an integer: ") + key);
+  }
+}
+
+// Everything the executor reads from the model, checked on the host before
+// any device call: the architecture, the hyper-parameters this build's
+// kernels are specialised for (model.c:61-77), and the type, shape and byte
+// count of every tensor (model.c:79-105, plus the optional dense_2 /
+// dense_3 of EXTRACTION.md:178-181). Returns the layer count.
+uint64_t validate_model(const ei_gguf* g) {
+  if (!g || !g->tensors) throw std::runtime_error("empty GGUF");
+  const ei_kv* arch = find_kv(g, "general.architecture");
+  if (!arch || arch->type != EI_GGUF_STRING || !str_eq(arch->v.s, "gemma-embedding"))
+    throw std::runtime_error("expected a gemma-embedding GGUF");
+  auto hp = [&](const char* key, uint64_t want) {
+    if (kv_u64(g, key, 0) != want) throw std::runtime_error(std::string("unsupported hyper-parameter ") + key);
+  };
+  hp("gemma-embedding.embedding_length", kEmbd);
+  hp("gemma-embedding.feed_forward_length", kFF);
+  hp("gemma-embedding.attention.head_count", 3);
+  hp("gemma-embedding.attention.head_count_kv", 1);
+  hp("gemma-embedding.attention.key_length", kHeadDim);
+  hp("gemma-embedding.attention.value_length", kHeadDim);
+  const uint64_t n_layer = kv_u64(g, "gemma-embedding.block_count", 0);
+  if (n_layer < 1 || n_layer > 64) throw std::runtime_error("block_count must be 1..64");
+  (void)kv_f64(g, "gemma-embedding.attention.layer_norm_rms_epsilon", 1e-6);
+  (void)kv_f64(g, "gemma-embedding.rope.freq_base", 1000000.0);
+  (void)kv_f64(g, "gemma-embedding.rope.freq_base_swa", 10000.0);
+  if (kv_u64(g, "gemma-embedding.attention.sliding_window_pattern", 6) == 0)
+    throw std::runtime_error("sliding_window_pattern must be positive");
+  if (kv_u64(g, "gemma-embedding.attention.sliding_window", 512) > 2 * kCap)
+    throw std::runtime_error("sliding_window too large");
+
+  const ei_tensor* emb = checked_tensor(g, "token_embd.weight", EI_T_Q8_0, kEmbd, kVocab);
+  if (reinterpret_cast<uintptr_t>(emb->data) % 2 != 0) throw std::runtime_error("token_embd.weight misaligned");
+  checked_tensor(g, "output_norm.weight", EI_T_F32, kEmbd, 1);
+  for (uint64_t il = 0; il < n_layer; ++il) {
+    const std::string p = "blk." + std::to_string(il) + ".";
+    checked_tensor(g, p + "attn_q.weight", EI_T_Q8_0, kEmbd, 768);
+    checked_tensor(g, p + "attn_k.weight", EI_T_Q8_0, kEmbd, 256);
+    checked_tensor(g, p + "attn_v.weight", EI_T_Q8_0, kEmbd, 256);
+    checked_tensor(g, p + "attn_output.weight", EI_T_Q8_0, 768, kEmbd);
+    checked_tensor(g, p + "ffn_gate.weight", EI_T_Q8_0, kEmbd, kFF);
+    checked_tensor(g, p + "ffn_up.weight", EI_T_Q8_0, kEmbd, kFF);
+    checked_tensor(g, p + "ffn_down.weight", EI_T_Q8_0, kFF, kEmbd);
+    for (const char* v : {"attn_norm.weight", "post_attention_norm.weight", "ffn_norm.weight", "post_ffw_norm.weight"})
+      checked_tensor(g, p + v, EI_T_F32, kEmbd, 1);
+    checked_tensor(g, p + "attn_q_norm.weight", EI_T_F32, kHeadDim, 1);
+    checked_tensor(g, p + "attn_k_norm.weight", EI_T_F32, kHeadDim, 1);
+  }
+  const ei_tensor* d2 = checked_tensor(g, "dense_2.weight", EI_T_Q8_0, kEmbd, kDenseFF, false);
+  const ei_tensor* d3 = checked_tensor(g, "dense_3.weight", EI_T_Q8_0, kDenseFF, kEmbd, false);
+  if ((d2 == nullptr) != (d3 == nullptr)) throw std::runtime_error("dense_2/dense_3 must be both present or absent");
+  return n_layer;
+}
+
 struct DevMat {
   int8_t* q = nullptr;  // row tiles
   float* d = nullptr;   // block scales [k/32][ld]
@@ -131,6 +245,13 @@ class Backend {
     free_lanes_.pop_back();
     return i;
   }
+  // Takes lane i itself from the pool, blocking until it is free.
+  void acquire_lane(unsigned i) {
+    if (i >= lanes_.size()) throw std::runtime_error("lane index out of range");
+    std::unique_lock<std::mutex> pool(pool_mutex_);
+    pool_cv_.wait(pool, [&] { return std::find(free_lanes_.begin(), free_lanes_.end(), i) != free_lanes_.end(); });
+    free_lanes_.erase(std::find(free_lanes_.begin(), free_lanes_.end(), i));
+  }
   void release_lane(unsigned i) {
     {
       std::lock_guard<std::mutex> pool(pool_mutex_);
@@ -143,6 +264,14 @@ class Backend {
     if (i >= lanes_.size()) throw std::runtime_error("lane index out of range");
     return *lanes_[i];
   }
+  // Lane 0 taken from the pool by eg2_kfd_stage and held until
+  // eg2_kfd_collect returns it, so that no concurrent batch call stages
+  // over the wave in between.
+  std::mutex lane0_mutex;
+  bool lane0_held = false;
+  // Test hook: the next device wait reports a failure as a failing HIP
+  // call would, from the host, with no device fault involved.
+  std::atomic<bool> inject_failure{false};
 
  private:
   const ei_gguf* model_;
@@ -180,10 +309,6 @@ class Backend {
     host_allocs_.push_back(p);
     return static_cast<T*>(p);
   }
-  const ei_tensor* tensor(const std::string& name, bool required = true) const;
-  const ei_kv* kv(const char* key) const;
-  double kv_f64(const char* key, double dflt) const;
-  uint64_t kv_u64(const char* key, uint64_t dflt) const;
   const float* upload_vector(const std::string& name, int n);
   std::vector<uint8_t> q8_rows(const std::string& name, int k, int m) const;
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
@@ -206,50 +331,8 @@ class Backend {
   }
 };
 
-const ei_tensor* Backend::tensor(const std::string& name, bool required) const {
-  for (uint64_t i = 0; i < model_->n_tensors; ++i)
-    if (str_eq(model_->tensors[i].name, name.c_str())) return &model_->tensors[i];
-  if (required) throw std::runtime_error("missing tensor: " + name);
-  return nullptr;
-}
-
-const ei_kv* Backend::kv(const char* key) const {
-  for (uint64_t i = 0; i < model_->n_kv; ++i)
-    if (str_eq(model_->kv[i].key, key)) return &model_->kv[i];
-  return nullptr;
-}
-
-// model.c:71-77 read these through ei_gguf_kv_f64/_u64, which take the
-// normalised union member (gguf.c:46-61); an integer-typed key read as a
-// float (or the reverse) is converted here instead of reinterpreted.
-double Backend::kv_f64(const char* key, double dflt) const {
-  const ei_kv* k = kv(key);
-  if (!k) return dflt;
-  switch (k->type) {
-    case EI_GGUF_F32:
-    case EI_GGUF_F64: return k->v.f64;
-    case EI_GGUF_I8: case EI_GGUF_I16: case EI_GGUF_I32: case EI_GGUF_I64: return (double)k->v.i64;
-    case EI_GGUF_U8: case EI_GGUF_U16: case EI_GGUF_U32: case EI_GGUF_U64: return (double)k->v.u64;
-    default: throw std::runtime_error(std::string("GGUF key is not numeric: ") + key);
-  }
-}
-
-uint64_t Backend::kv_u64(const char* key, uint64_t dflt) const {
-  const ei_kv* k = kv(key);
-  if (!k) return dflt;
-  switch (k->type) {
-    case EI_GGUF_U8: case EI_GGUF_U16: case EI_GGUF_U32: case EI_GGUF_U64: return k->v.u64;
-    case EI_GGUF_I8: case EI_GGUF_I16: case EI_GGUF_I32: case EI_GGUF_I64:
-      if (k->v.i64 < 0) throw std::runtime_error(std::string("negative GGUF key: ") + key);
-      return (uint64_t)k->v.i64;
-    default: throw std::runtime_error(std::string("GGUF key is not an integer: ") + key);
-  }
-}
-
 const float* Backend::upload_vector(const std::string& name, int n) {
-  const ei_tensor* t = tensor(name);
-  if (t->type != EI_T_F32 || t->ne[0] != (uint64_t)n || t->ne[1] != 1)
-    throw std::runtime_error("norm requires F32[" + std::to_string(n) + "]: " + name);
+  const ei_tensor* t = checked_tensor(model_, name, EI_T_F32, (uint64_t)n, 1);
   float* d = dalloc<float>(n);
   check(hipMemcpy(d, t->data, n * sizeof(float), hipMemcpyHostToDevice), "upload");
   return d;
@@ -257,13 +340,9 @@ const float* Backend::upload_vector(const std::string& name, int n) {
 
 // Raw Q8_0 rows of a [k, m] (ne[0] = k) matrix, validated (model.c:93-99 with Q8_0).
 std::vector<uint8_t> Backend::q8_rows(const std::string& name, int k, int m) const {
-  const ei_tensor* t = tensor(name);
-  if (t->type != EI_T_Q8_0) throw std::runtime_error("matrix must be Q8_0: " + name);
-  if (t->ne[0] != (uint64_t)k || t->ne[1] != (uint64_t)m || t->ne[2] != 1 || t->ne[3] != 1)
-    throw std::runtime_error("unexpected shape: " + name);
-  const size_t bytes = (size_t)m * (k / 32) * 34;
+  const ei_tensor* t = checked_tensor(model_, name, EI_T_Q8_0, (uint64_t)k, (uint64_t)m);
   const uint8_t* p = static_cast<const uint8_t*>(t->data);
-  return std::vector<uint8_t>(p, p + bytes);
+  return std::vector<uint8_t>(p, p + t->n_bytes);
 }
 
 // Concatenates matrices along the output dimension and uploads them in the
@@ -306,34 +385,19 @@ DevMat Backend::upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vec
 }
 
 Backend::Backend(const ei_gguf* g) : model_(g) {
-  if (!g || !g->tensors) throw std::runtime_error("empty GGUF");
+  // The whole model is checked before the first device call.
+  const uint64_t n_layer = validate_model(g);
+  use_graph_ = env_flag("EG2_HIP_GRAPH", true);
+  profile_ = env_flag("EG2_HIP_PROFILE", false);
   char why[256];
   if (eg2_hip_device_check(why, sizeof why) != 0)
     throw std::runtime_error(std::string("supported HIP device not found (gfx950): ") + why);
-  use_graph_ = env_flag("EG2_HIP_GRAPH", true);
-  profile_ = env_flag("EG2_HIP_PROFILE", false);
 
-  const ei_kv* arch = kv("general.architecture");
-  if (!arch || arch->type != EI_GGUF_STRING || !str_eq(arch->v.s, "gemma-embedding"))
-    throw std::runtime_error("expected a gemma-embedding GGUF");
-  auto hp = [&](const char* key, uint64_t want) {
-    if (kv_u64(key, 0) != want) throw std::runtime_error(std::string("unsupported hyper-parameter ") + key);
-  };
-  hp("gemma-embedding.embedding_length", kEmbd);
-  hp("gemma-embedding.feed_forward_length", kFF);
-  hp("gemma-embedding.attention.head_count", 3);
-  hp("gemma-embedding.attention.head_count_kv", 1);
-  hp("gemma-embedding.attention.key_length", kHeadDim);
-  hp("gemma-embedding.attention.value_length", kHeadDim);
-  const uint64_t n_layer = kv_u64("gemma-embedding.block_count", 0);
-  if (n_layer < 1 || n_layer > 64) throw std::runtime_error("block_count must be 1..64");
-  eps_ = (float)kv_f64("gemma-embedding.attention.layer_norm_rms_epsilon", 1e-6);
-  const float base_full = (float)kv_f64("gemma-embedding.rope.freq_base", 1000000.0);
-  const float base_swa = (float)kv_f64("gemma-embedding.rope.freq_base_swa", 10000.0);
-  const uint64_t swa_window = kv_u64("gemma-embedding.attention.sliding_window", 512);
-  const uint64_t swa_period = kv_u64("gemma-embedding.attention.sliding_window_pattern", 6);
-  if (swa_period == 0) throw std::runtime_error("sliding_window_pattern must be positive");
-  if (swa_window > 2 * kCap) throw std::runtime_error("sliding_window too large");
+  eps_ = (float)kv_f64(g, "gemma-embedding.attention.layer_norm_rms_epsilon", 1e-6);
+  const float base_full = (float)kv_f64(g, "gemma-embedding.rope.freq_base", 1000000.0);
+  const float base_swa = (float)kv_f64(g, "gemma-embedding.rope.freq_base_swa", 10000.0);
+  const uint64_t swa_window = kv_u64(g, "gemma-embedding.attention.sliding_window", 512);
+  const uint64_t swa_period = kv_u64(g, "gemma-embedding.attention.sliding_window_pattern", 6);
 
   // RoPE tables, one per distinct base (kernels.c:245-249 values).
   std::vector<float> table((size_t)kCap * kHeadDim);
@@ -346,10 +410,7 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
     ropes[base] = d;
   }
 
-  const ei_tensor* emb = tensor("token_embd.weight");
-  if (emb->type != EI_T_Q8_0 || emb->ne[0] != (uint64_t)kEmbd || emb->ne[1] != (uint64_t)kVocab)
-    throw std::runtime_error("token_embd.weight must be Q8_0 [768, 262144]");
-  if (reinterpret_cast<uintptr_t>(emb->data) % 2 != 0) throw std::runtime_error("token_embd.weight misaligned");
+  const ei_tensor* emb = checked_tensor(g, "token_embd.weight", EI_T_Q8_0, kEmbd, kVocab);
   {
     uint8_t* d = dalloc<uint8_t>(emb->n_bytes);
     check(hipMemcpy(d, emb->data, emb->n_bytes, hipMemcpyHostToDevice), "upload");
@@ -382,10 +443,7 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
     layers_.push_back(L);
   }
   // Optional dense head (EXTRACTION.md:178-181: dense_2 {768, 3072}, dense_3 {3072, 768}).
-  const ei_tensor* d2 = tensor("dense_2.weight", false);
-  const ei_tensor* d3 = tensor("dense_3.weight", false);
-  if ((d2 == nullptr) != (d3 == nullptr)) throw std::runtime_error("dense_2/dense_3 must be both present or absent");
-  if (d2) {
+  if (find_tensor(g, "dense_2.weight")) {
     auto a = q8_rows("dense_2.weight", kEmbd, kDenseFF), b = q8_rows("dense_3.weight", kDenseFF, kEmbd);
     dense2_ = upload_q8({&a}, kEmbd);
     dense3_ = upload_q8({&b}, kDenseFF);
@@ -515,6 +573,7 @@ void Backend::record_layers(Lane& ln, unsigned rows, bool merge) {
 
 void Backend::wait(Lane& ln, const char* what) {
   const auto start = std::chrono::steady_clock::now();
+  if (inject_failure.exchange(false)) throw std::runtime_error(std::string(what) + ": injected HIP failure");
   for (;;) {
     const hipError_t e = hipStreamQuery(ln.stream);
     if (e == hipSuccess) return;
@@ -658,21 +717,24 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
       } else {
         record_layers(ln, ln.staged_rows, ln.staged_merge);
       }
-      // One workgroup per sequence reads it through one CU; past 256 tokens
-      // the mean spreads over 12 workgroups per sequence and the L2 follows
-      // (the same result, bit for bit).
-      if (ln.staged_longest > kPoolSplitLen) {
-        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
-        launch("pool_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
-      } else {
-        launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
-      }
       if (dense_) {
+        // EXTRACTION.md:178-181: dense_2 then dense_3 on the mean pool
+        // (kernels.c:417-425 without its L2), each input Q8_0-quantized,
+        // then the L2 of kernels.c:393-396.
+        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
         launch("dense_quant", eg2::launch_quantize_rows(ln.pooled, kEmbd, ln.cq, ln.cd, B, s));
         gemm("dense_2", ln.cq, ln.cd, dense2_, ln.mid, B, kDenseFF, s);
         launch("dense_quant", eg2::launch_quantize_rows(ln.mid, kDenseFF, ln.mid_q, ln.mid_d, B, s));
         gemm("dense_3", ln.mid_q, ln.mid_d, dense3_, ln.pooled, B, kEmbd, s);
         launch("dense_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+      } else if (ln.staged_longest > kPoolSplitLen) {
+        // One workgroup per sequence reads it through one CU; past 256
+        // tokens the mean spreads over 12 workgroups per sequence and the
+        // L2 follows (the same result, bit for bit).
+        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
+        launch("pool_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+      } else {
+        launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
       }
     }
   });
@@ -768,15 +830,61 @@ extern "C" bool eg2_kfd_collect_lane(void* ctx, unsigned lane, float* out, char*
   return on_lane(ctx, lane, err, len, [&](Backend& b, Lane& ln) { b.collect(ln, out); });
 }
 
+// Lane 0 through the pool: eg2_kfd_stage takes it (unless a wave staged
+// by it is still uncollected) and keeps it after a successful stage;
+// eg2_kfd_collect gives it back.
 extern "C" bool eg2_kfd_stage(void* ctx, const int32_t* ids, const size_t* offsets, size_t batch, char* err,
                               size_t len) {
-  return eg2_kfd_stage_lane(ctx, 0, ids, offsets, batch, err, len);
+  if (!ctx) return eg2_kfd_stage_lane(ctx, 0, ids, offsets, batch, err, len);
+  Backend* b = static_cast<Backend*>(ctx);
+  std::lock_guard<std::mutex> g(b->lane0_mutex);
+  const bool took = !b->lane0_held;
+  if (took) b->acquire_lane(0u);
+  const bool ok = eg2_kfd_stage_lane(ctx, 0, ids, offsets, batch, err, len);
+  if (ok) {
+    b->lane0_held = true;
+  } else if (took) {
+    b->release_lane(0);
+  }
+  return ok;
 }
 
 extern "C" bool eg2_kfd_launch_staged(void* ctx, unsigned repeats, char* err, size_t len) {
+  if (ctx) {
+    Backend* b = static_cast<Backend*>(ctx);
+    std::lock_guard<std::mutex> g(b->lane0_mutex);
+    if (!b->lane0_held) {
+      if (err && len) std::snprintf(err, len, "HIP: no staged wave (eg2_kfd_stage first)");
+      return false;
+    }
+  }
   return eg2_kfd_launch_lane(ctx, 0, repeats, err, len);
 }
 
 extern "C" bool eg2_kfd_collect(void* ctx, float* out, char* err, size_t len) {
-  return eg2_kfd_collect_lane(ctx, 0, out, err, len);
+  if (!ctx) return eg2_kfd_collect_lane(ctx, 0, out, err, len);
+  Backend* b = static_cast<Backend*>(ctx);
+  std::lock_guard<std::mutex> g(b->lane0_mutex);
+  if (!b->lane0_held) {
+    if (err && len) std::snprintf(err, len, "HIP: no staged wave (eg2_kfd_stage first)");
+    return false;
+  }
+  const bool ok = eg2_kfd_collect_lane(ctx, 0, out, err, len);
+  b->lane0_held = false;
+  b->release_lane(0);
+  return ok;
+}
+
+extern "C" void eg2_kfd_inject_failure(void* ctx) {
+  if (ctx) static_cast<Backend*>(ctx)->inject_failure = true;
+}
+
+extern "C" bool eg2_kfd_validate_gguf(const ei_gguf* g, char* err, size_t len) {
+  try {
+    validate_model(g);
+    return true;
+  } catch (const std::exception& e) {
+    if (err && len) std::snprintf(err, len, "HIP: %s", e.what());
+    return false;
+  }
 }

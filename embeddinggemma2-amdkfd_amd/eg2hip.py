@@ -149,6 +149,8 @@ SIGNATURES = {
     "eg2_kfd_launch_staged": (C.c_bool, [C.c_void_p, C.c_uint, C.c_char_p, C.c_size_t]),
     "eg2_kfd_collect": (C.c_bool, [C.c_void_p, _f, C.c_char_p, C.c_size_t]),
     "eg2_kfd_lanes": (C.c_uint, [C.c_void_p]),
+    "eg2_kfd_validate_gguf": (C.c_bool, [C.POINTER(EiGguf), C.c_char_p, C.c_size_t]),
+    "eg2_kfd_inject_failure": (None, [C.c_void_p]),
     "eg2_f32_to_chars": (C.c_size_t, [C.c_char_p, C.c_float]),
     "eg2_tokenizer_create": (C.c_void_p, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "eg2_tokenizer_free": (None, [C.c_void_p]),
@@ -227,6 +229,14 @@ class Gguf:
             self.close()
         except Exception:
             pass
+
+
+def validate_gguf(gguf):
+    """eg2_kfd_validate_gguf on an open Gguf: None, or the rejection message."""
+    err = C.create_string_buffer(512)
+    if lib().eg2_kfd_validate_gguf(C.byref(gguf.g), err, 512):
+        return None
+    return err.value.decode()
 
 
 class Tokenizer:

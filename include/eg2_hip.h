@@ -212,10 +212,29 @@ bool eg2_kfd_stage_lane(void *ctx, unsigned lane, const int32_t *ids, const size
 bool eg2_kfd_launch_lane(void *ctx, unsigned lane, unsigned repeats, char *err, size_t len);
 /* Waits for the lane's wave and copies its [batch][768] embeddings to out. */
 bool eg2_kfd_collect_lane(void *ctx, unsigned lane, float *out, char *err, size_t len);
-/* The same on lane 0. */
+/* The same on lane 0, which eg2_kfd_stage takes from the pool (waiting
+ * while a batch call holds it) and keeps until eg2_kfd_collect hands it
+ * back; launch and collect without a staged wave fail. */
 bool eg2_kfd_stage(void *ctx, const int32_t *ids, const size_t *offsets, size_t batch, char *err, size_t len);
 bool eg2_kfd_launch_staged(void *ctx, unsigned repeats, char *err, size_t len);
 bool eg2_kfd_collect(void *ctx, float *out, char *err, size_t len);
+
+/* Test hook with no reference counterpart: the context's next device wait
+ * (every batch, stage and collect waits on its lane's stream) reports a
+ * failure exactly as a failing HIP call does -- the call returns false with
+ * "HIP: ... injected HIP failure" and the context is poisoned, so every
+ * later call fails with "restart process" (src/gemma2_kfd.cpp:190-191,
+ * 214-215, 270). Raised on the host: no device fault is involved. */
+void eg2_kfd_inject_failure(void *ctx);
+
+/* The model checks of ei_gemma2_kfd_create alone, on the host with no
+ * device call: the gemma-embedding architecture and hyper-parameters
+ * (model.c:61-77), and every tensor the executor reads with its type, its
+ * [ne0, ne1, 1, 1] shape and exactly the byte count that shape takes
+ * (model.c:79-105, Q8_0 matrices; optional dense_2 / dense_3). create runs
+ * the same checks before its first device call. Returns false and
+ * "HIP: <what>" in err for a model it would reject. */
+bool eg2_kfd_validate_gguf(const ei_gguf *g, char *err, size_t len);
 
 /* ------------------------------------------------------------ host helpers */
 

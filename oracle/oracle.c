@@ -300,9 +300,9 @@ int or_normalize_prefix(float *embedding, int32_t dimensions) {
     return 1;
 }
 
-/* kernels.c:417-427: per-token RMS (in place), token-ordered sum, times
- * 1/n, then L2. */
-void or_mean_pool_rms_l2(float *x, int32_t n_tokens, const float *w, float eps, float *out) {
+/* kernels.c:417-425: per-token RMS (in place), token-ordered sum, times
+ * 1/n -- the mean pool without the L2 of :426. */
+void or_mean_pool_rms(float *x, int32_t n_tokens, const float *w, float eps, float *out) {
     memset(out, 0, sizeof(float) * OR_N_EMBD);
     for (int32_t t = 0; t < n_tokens; t++) {
         float *row = x + (size_t)t * OR_N_EMBD;
@@ -311,6 +311,11 @@ void or_mean_pool_rms_l2(float *x, int32_t n_tokens, const float *w, float eps, 
     }
     const float scale = 1.0f / (float)n_tokens;
     for (int32_t i = 0; i < OR_N_EMBD; i++) out[i] *= scale;
+}
+
+/* kernels.c:417-427: the mean pool above, then L2. */
+void or_mean_pool_rms_l2(float *x, int32_t n_tokens, const float *w, float eps, float *out) {
+    or_mean_pool_rms(x, n_tokens, w, eps, out);
     or_l2_normalize(out, OR_N_EMBD);
 }
 
@@ -555,10 +560,12 @@ void or_input_embeddings(const or_model *m, const int32_t *ids, int32_t n_tokens
 }
 
 /* engine.c:1021-1138 (validation :1024-1041, positions :1099-1104, layers
- * :1115-1127, pooling :1129-1135). The dense head after pooling has no
- * reference implementation (EXTRACTION.md:178-181): it is the pinned Q8_0
- * GEMM applied twice (activations Q8_0-quantized like every other
- * projection input), then the L2 of kernels.c:393-396. */
+ * :1115-1127, pooling :1129-1135). The dense head has no reference
+ * implementation; EXTRACTION.md:178-181 places it after the mean pool and
+ * before normalisation: dense_2 then dense_3, no biases, no activation. It
+ * is the pinned Q8_0 GEMM applied twice to the (un-normalised) mean, each
+ * input Q8_0-quantized like every other projection input, then the L2 of
+ * kernels.c:393-396. Without the head the pool is kernels.c:417-427 as is. */
 int or_forward(const or_model *m, const int32_t *ids, const size_t *offsets, size_t batch,
                float *out, int32_t threads) {
     if (!ids || !offsets || !out || batch == 0 || offsets[0] != 0) return -1;
@@ -577,10 +584,16 @@ int or_forward(const or_model *m, const int32_t *ids, const size_t *offsets, siz
     or_input_embeddings(m, ids, T, x);
     for (int32_t il = 0; il < m->n_layer; il++)
         or_layer_forward(&m->layers[il], m->eps, x, positions, offsets, batch, threads);
-    for (size_t s = 0; s < batch; s++)
-        or_mean_pool_rms_l2(x + offsets[s] * OR_N_EMBD, (int32_t)(offsets[s + 1] - offsets[s]),
-                            m->output_norm, m->eps, out + s * OR_N_EMBD);
-    if (m->dense_2 && m->dense_3) {
+    const int dense = m->dense_2 && m->dense_3;
+    for (size_t s = 0; s < batch; s++) {
+        float *xs = x + offsets[s] * OR_N_EMBD;
+        const int32_t n = (int32_t)(offsets[s + 1] - offsets[s]);
+        if (dense)
+            or_mean_pool_rms(xs, n, m->output_norm, m->eps, out + s * OR_N_EMBD);
+        else
+            or_mean_pool_rms_l2(xs, n, m->output_norm, m->eps, out + s * OR_N_EMBD);
+    }
+    if (dense) {
         const int32_t B = (int32_t)batch;
         or_block_q8_0 *pq = malloc(sizeof(or_block_q8_0) * (size_t)B * (OR_DENSE_FF / OR_QK));
         float *mid = malloc(sizeof(float) * (size_t)B * OR_DENSE_FF);

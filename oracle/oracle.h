@@ -24,9 +24,13 @@
  *       double-precision brute-force layer on tiny inputs (tolerance).
  *   or_op_mm (the operator-level fp32 projection): the exact-arithmetic
  *       cases of tests/kernels.cpp:57-80 and a float64 brute force.
- *   Dense head (dense_2, dense_3): parity unpinned by reference code (the
- *       reference describes it in EXTRACTION.md:178-181 but never
- *       implements it); pinned only by composing the pinned GEMM.
+ *   Dense head (dense_2, dense_3 on the mean pool, then L2): the reference
+ *       describes it (EXTRACTION.md:178-181) but never implements it; its
+ *       composition is pinned by a float64 brute force on tiny models that
+ *       rejects planted mistakes (L2 before the head, the middle activation
+ *       not re-quantized, an activation between the layers, a transposed
+ *       weight), including a scale case where normalising first changes
+ *       the quantized input (tests/test_oracle_math.py).
  */
 #ifndef EG_ORACLE_H
 #define EG_ORACLE_H
@@ -76,6 +80,7 @@ float or_gelu_tanh(float x);
 void or_gelu_mul_quantize_q8_0(const float *gate, const float *up, int32_t n, or_block_q8_0 *out);
 void or_l2_normalize(float *x, int32_t n);
 int or_normalize_prefix(float *embedding, int32_t dimensions);
+void or_mean_pool_rms(float *x, int32_t n_tokens, const float *w, float eps, float *out);
 void or_mean_pool_rms_l2(float *x, int32_t n_tokens, const float *w, float eps, float *out);
 
 /* y[t*m + r] = sum_p float(dot_p) * d_w * d_x over the K/32 blocks, in block

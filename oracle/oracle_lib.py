@@ -54,6 +54,7 @@ def _load_oracle():
         "or_gelu_mul_quantize_q8_0": (None, [_f, _f, C.c_int32, _vp]),
         "or_l2_normalize": (None, [_f, C.c_int32]),
         "or_normalize_prefix": (C.c_int, [_f, C.c_int32]),
+        "or_mean_pool_rms": (None, [_f, C.c_int32, _f, C.c_float, _f]),
         "or_mean_pool_rms_l2": (None, [_f, C.c_int32, _f, C.c_float, _f]),
         "or_gemm_q8_0": (None, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, _f, C.c_int32]),
         "or_op_mm": (None, [_f, _f, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f]),

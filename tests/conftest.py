@@ -40,3 +40,13 @@ def gpu(eg2):
     if eg2.lib().eg2_hip_device_check(err, 256) != 0:
         pytest.fail("device check failed: " + err.value.decode())
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def full_model(eg2, tmp_path_factory):
+    """The 24-layer model of the 16x128 benchmark wave: seed 0, full
+    attention with RoPE base 1e4, dense head (written once per session)."""
+    path = str(tmp_path_factory.mktemp("full") / "full.gguf")
+    eg2.synth_gguf(path, seed=0, n_layer=24, dense_head=True, sliding_window=0, rope_base_full=1e4,
+                   rope_base_swa=1e4, threads=16)
+    return path

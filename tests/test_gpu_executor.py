@@ -99,6 +99,31 @@ def test_invalid_batches_fail_without_poisoning(eg2, small_encoder):
     assert np.isfinite(out).all()
 
 
+def test_injected_hip_failure_poisons_the_context(eg2, small_model):
+    """A failing HIP call (forced from the host by the test hook, no device
+    fault) makes the call return false with a "HIP:" message, and every later
+    call on the context fails until it is recreated (src/gemma2_kfd.cpp:190-191,
+    214-215, 270)."""
+    enc = eg2.Encoder(small_model)
+    try:
+        ids = np.arange(40, dtype=np.int32)
+        good = enc.batch(ids, [0, 40])
+        eg2.lib().eg2_kfd_inject_failure(enc.ctx)
+        with pytest.raises(eg2.HipError, match=r"^HIP: .*injected HIP failure"):
+            enc.batch(ids, [0, 40])
+        for call in (lambda: enc.batch(ids, [0, 40]), lambda: enc.stage(ids, [0, 40], 1),
+                     lambda: enc.stream(ids, [0, 40], [768])):
+            with pytest.raises(eg2.HipError, match="restart process"):
+                call()
+    finally:
+        enc.close()
+    fresh = eg2.Encoder(small_model)
+    try:
+        assert np.array_equal(fresh.batch(ids, [0, 40]), good)
+    finally:
+        fresh.close()
+
+
 def test_env_flags_are_validated(eg2, small_model):
     os.environ["EG2_HIP_GRAPH"] = "yes"
     try:
@@ -187,15 +212,6 @@ def test_concurrent_batch_calls(small_encoder):
     for t in threads:
         t.join()
     assert not errors
-
-
-@pytest.fixture(scope="module")
-def full_model(eg2, tmp_path_factory):
-    """Config 4: 24 layers, full attention with RoPE base 1e4, dense head."""
-    path = str(tmp_path_factory.mktemp("full") / "full.gguf")
-    eg2.synth_gguf(path, seed=0, n_layer=24, dense_head=True, sliding_window=0, rope_base_full=1e4,
-                   rope_base_swa=1e4, threads=16)
-    return path
 
 
 def test_full_model_16x128_parity(eg2, gpu, full_model):

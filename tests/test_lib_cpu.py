@@ -309,6 +309,53 @@ def test_executor_create_reports_missing_device(eg2, small_gguf):
         eg2.Encoder(small_gguf)
 
 
+def _tensor(g, name):
+    for i in range(g.g.n_tensors):
+        t = g.g.tensors[i]
+        if C.string_at(t.name.str, t.name.len).decode() == name:
+            return t
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name,change,msg", [
+    # n_dims 3 with ne[2] = 0: a zero byte count that passes the reader's
+    # bounds check but would make the embedding gather read past the upload.
+    ("token_embd.weight", dict(n_dims=3, ne2=0, n_bytes=0), "unexpected shape: token_embd.weight"),
+    ("output_norm.weight", dict(n_bytes=256), "unexpected byte count: output_norm.weight"),
+    ("blk.0.attn_norm.weight", dict(n_dims=3, ne2=2, n_bytes=768 * 4 * 2), "unexpected shape: blk.0.attn_norm"),
+    ("blk.1.attn_q_norm.weight", dict(ne0=128, n_bytes=512), "unexpected shape: blk.1.attn_q_norm"),
+    ("blk.1.ffn_down.weight", dict(type=0), "unexpected type: blk.1.ffn_down.weight"),
+    ("blk.0.attn_q.weight", dict(n_bytes=768 * 24 * 34 - 34), "unexpected byte count: blk.0.attn_q.weight"),
+    ("blk.0.attn_k.weight", dict(ne3=0), "unexpected shape: blk.0.attn_k.weight"),
+    ("blk.1.ffn_up.weight", dict(rename=True), "missing tensor: blk.1.ffn_up.weight"),
+    ("dense_3.weight", dict(rename=True), "dense_2/dense_3 must be both present or absent"),
+])
+def test_model_validation_rejects_malformed_tensor_records(eg2, small_gguf, name, change, msg):
+    """Every tensor record the executor reads is checked for type, shape and
+    exact byte count on the host, before create makes any device call."""
+    g = eg2.Gguf(small_gguf)
+    try:
+        assert eg2.validate_gguf(g) is None
+        t = _tensor(g, name)
+        if change.get("rename"):
+            t.name.len = 3  # a different name
+        for f in ("n_dims", "type", "n_bytes"):
+            if f in change:
+                setattr(t, f, change[f])
+        for i in range(4):
+            if f"ne{i}" in change:
+                t.ne[i] = change[f"ne{i}"]
+        got = eg2.validate_gguf(g)
+        assert got is not None and got.startswith("HIP: ") and msg in got, got
+        # create reports the same rejection: the checks run before the
+        # device is touched (here, before finding there is none).
+        err = C.create_string_buffer(512)
+        assert not eg2.lib().ei_gemma2_kfd_create(C.byref(g.g), err, 512)
+        assert msg in err.value.decode()
+    finally:
+        g.close()
+
+
 REFERENCE_OPERATORS = {"eg2_saxpy", "eg2_gather", "eg2_mm", "eg2_mm64", "eg2_mm64x64", "eg2_mmstep8", "eg2_norm",
                        "eg2_rope", "eg2_attention256", "eg2_attention512", "eg2_element", "eg2_pool",
                        "eg2_norm_residual", "eg2_norm_rope"}  # kernels/eg2.c

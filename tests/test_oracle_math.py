@@ -327,3 +327,107 @@ def test_op_mm_is_the_sequential_fma_chain():
             assert got[r, c] == acc, (r, c)
             unfused_differs |= bool(plain != acc)
     assert unfused_differs
+
+
+# ------------------------------------------------------------------ dense head
+
+
+def _gelu64(g):
+    return 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3)))
+
+
+def _head_double(rows, offsets, out_w, d2, d3, l2_first=False, requant_mid=True, act=False, transpose_d2=False):
+    """EXTRACTION.md:178-181 in float64: per token rms(x, output_norm), the
+    mean over the sequence, then dense_2 and dense_3 (no bias), then L2. The
+    inputs of both dense projections are Q8_0-quantized with the oracle's
+    quantizer (the reference quantizes every projection input, gemma2.c:142-153);
+    the keyword arguments plant plausible mistakes."""
+    W2 = dequantize_q8_0(d2).astype(np.float64)
+    if transpose_d2:  # the [768, 3072] GGUF shape read with its dimensions swapped
+        W2 = W2.reshape(N_EMBD, OL.DENSE_FF).T
+    W3 = dequantize_q8_0(d3).astype(np.float64)
+    out = []
+    for s in range(len(offsets) - 1):
+        x = rows[offsets[s]:offsets[s + 1]].astype(np.float64)
+        r = x * out_w / np.sqrt((x ** 2).mean(1, keepdims=True) + 1e-6)
+        p = r.mean(0)
+        if l2_first:
+            p = p / np.linalg.norm(p)
+        pq = dequantize_q8_0(quantize_q8_0(p.astype(np.float32))).astype(np.float64)
+        mid = W2 @ pq
+        if act:
+            mid = _gelu64(mid)
+        if requant_mid:
+            mid = dequantize_q8_0(quantize_q8_0(mid.astype(np.float32))).astype(np.float64)
+        o = W3 @ mid
+        out.append(o / np.linalg.norm(o))
+    return np.array(out)
+
+
+def _head_model(seed, norm_scale):
+    """A model with no layers (embedding -> pooling -> dense head) whose used
+    embedding rows are random."""
+    rng = np.random.default_rng(seed)
+    lens = [5, 1, 12]
+    ids = rng.integers(0, OL.VOCAB, sum(lens)).astype(np.int32)
+    table = np.zeros((OL.VOCAB, N_EMBD // 32), dtype=Q8)
+    u = np.unique(ids)
+    table[u] = quantize_q8_0((rng.standard_normal((len(u), N_EMBD)) * 0.05).astype(np.float32))
+    out_w = ((1 + 0.3 * rng.standard_normal(N_EMBD)) * norm_scale).astype(np.float32)
+    d2 = quantize_q8_0((rng.standard_normal((OL.DENSE_FF, N_EMBD)) * 0.02).astype(np.float32))
+    d3 = quantize_q8_0((rng.standard_normal((N_EMBD, OL.DENSE_FF)) * 0.02).astype(np.float32))
+    model = dict(token_embd=table, output_norm=out_w, dense_2=d2, dense_3=d3, layers=[])
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    rows = dequantize_q8_0(table[ids]) * np.float32(np.sqrt(N_EMBD))
+    return model, ids, offsets, rows
+
+
+@pytest.fixture(scope="module")
+def head_cases():
+    # norm_scale 1e-5 puts the pooled values' Q8_0 scales in the fp16
+    # subnormal range, where normalising first changes the quantized input.
+    return {scale: _head_model(17, scale) for scale in (1.0, 1e-5)}
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e-5])
+def test_dense_head_matches_double_composition(head_cases, scale):
+    model, ids, offsets, rows = head_cases[scale]
+    got = OL.forward(model, ids, offsets, threads=4)
+    want = _head_double(rows, offsets.astype(np.int64), model["output_norm"], model["dense_2"], model["dense_3"])
+    assert _cos(got, want).min() > 0.999999
+    assert np.abs(got - want).max() < 2e-6
+
+
+def test_dense_head_check_rejects_planted_mistakes(head_cases):
+    """The composition check has teeth: each plausible mistake misses its
+    tolerance by a wide margin."""
+    model, ids, offsets, rows = head_cases[1.0]
+    got = OL.forward(model, ids, offsets, threads=4)
+    args = (rows, offsets.astype(np.int64), model["output_norm"], model["dense_2"], model["dense_3"])
+    for kw in (dict(requant_mid=False), dict(act=True), dict(transpose_d2=True), dict(l2_first=True)):
+        bad = _head_double(*args, **kw)
+        assert np.abs(got - bad).max() > 1e-4, kw
+    # Normalising before the head changes only the quantization of the
+    # head's input (Q8_0's fp16 scale rounding is not scale-equivariant);
+    # where its block scales fall in the fp16 subnormal range the change is
+    # large.
+    model, ids, offsets, rows = head_cases[1e-5]
+    got = OL.forward(model, ids, offsets, threads=4)
+    bad = _head_double(rows, offsets.astype(np.int64), model["output_norm"], model["dense_2"], model["dense_3"],
+                       l2_first=True)
+    assert np.abs(got - bad).max() > 1e-2
+
+
+def test_mean_pool_without_l2_is_the_scaled_mean():
+    x = (RNG.standard_normal((9, N_EMBD)) * 2).astype(np.float32)
+    w = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
+    mean = np.zeros(N_EMBD, np.float32)
+    oracle().or_mean_pool_rms(fptr(x.copy()), 9, fptr(w), 1e-6, fptr(mean))
+    xd = x.astype(np.float64)
+    want = (xd * w / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6)).mean(0)
+    assert np.abs(mean - want).max() < 1e-6 * np.abs(want).max()
+    l2 = np.zeros(N_EMBD, np.float32)
+    oracle().or_mean_pool_rms_l2(fptr(x.copy()), 9, fptr(w), 1e-6, fptr(l2))
+    m2 = mean.copy()
+    oracle().or_l2_normalize(fptr(m2), N_EMBD)
+    assert np.array_equal(l2, m2)
