@@ -10,6 +10,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "eg2_libm.hpp"
+
 namespace eg2 {
 
 constexpr int kEmbd = 768;      // model.h:9
@@ -173,25 +175,14 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
     *reinterpret_cast<uint2*>(q) = make_uint2(w[0], w[1]);
 }
 
-// kernels.c:367-371 gelu_tanh(g) = 0.5 g (1 + tanh(z)), z = s g (1 + a g^2)
-// (the inner term in the order written), times u (engine.c's GeGLU),
-// evaluated as g / (1 + exp(-2 z)): the same function, since
-// 0.5 (1 + tanh z) = 1 / (1 + e^(-2z)), in a dozen instructions instead of
-// a tanhf. 1 + e^(-2z) is formed without cancellation, so the result is
-// within a few ulps of the exact value everywhere (the reference's fp32
-// 1 + tanhf(z) loses relative accuracy as z goes negative); below
-// z = -9, where the reference's tanhf(z) is exactly -1, it is exactly 0.
+// kernels.c:367-371 gelu_tanh(g) = 0.5 g (1 + tanhf(z)), z = s g (1 + a g^2),
+// times u (engine.c's GeGLU), each operation in the reference's order with
+// the host libm's own tanhf (eg2_libm.hpp): bit-identical to the CPU path.
 __device__ __forceinline__ float gelu_mul(float g, float u) {
   const float a = 0.044715f;
   const float s = 0.79788456080286535587989211986876f;
   const float inner = s * g * (1.0f + a * g * g);
-  // e^(-2z) = 2^(-2 log2(e) z), the exponent capped so the sum stays finite.
-  const float e = __builtin_amdgcn_exp2f(fminf(inner * -2.8853900817779268f, 126.0f));
-  const float den = 1.0f + e;
-  float r = __builtin_amdgcn_rcpf(den);
-  r = __builtin_fmaf(__builtin_fmaf(-den, r, 1.0f), r, r);  // Newton step: 1/den to about half an ulp
-  r = inner < -9.0f ? 0.0f : r;
-  return (g * r) * u;
+  return 0.5f * g * (1.0f + libm::tanhf(inner)) * u;
 }
 
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):
@@ -221,14 +212,6 @@ __device__ __forceinline__ float sse2_combine(float s) {
   const float v0 = __shfl(v, base, 64), v1 = __shfl(v, base + 1, 64);
   const float v2 = __shfl(v, base + 2, 64), v3 = __shfl(v, base + 3, 64);
   return (v0 + v2) + (v1 + v3);
-}
-
-// Writes x as the fp16 pair (hi, lo) = (fp16(x), fp16(x - hi)); x - hi is
-// exact in fp32, so hi + lo carries 22 of the 24 significand bits.
-__device__ __forceinline__ void store_split(_Float16* row, int width, int i, float x) {
-  const _Float16 h = (_Float16)x;
-  row[i] = h;
-  row[width + i] = (_Float16)(x - (float)h);
 }
 
 // Sum of squares of an LDS row of n floats (n % 8 == 0) in the reference's

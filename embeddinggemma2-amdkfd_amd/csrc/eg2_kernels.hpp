@@ -15,9 +15,12 @@ hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int
                                    hipStream_t st);
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
                                       float eps, int8_t* xq, float* xd, int rows, hipStream_t st);
+// QK-norm / RoPE on rows of the fused projection [q0 q1 q2 | k | v]
+// (kQKVCols fp32 each): q heads and k normalised and rotated, q scaled by
+// 1/16, v copied; in place when out == qkv.
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
-                               const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
-                               _Float16* vt, int ldv, int rows, hipStream_t st);
+                               const int32_t* pos, float eps, float* out, int rows, hipStream_t st);
+hipError_t launch_libm_eval(const float* x, unsigned n, float* e, float* t, hipStream_t st);
 hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, hipStream_t st);
 hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st);
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);
@@ -30,35 +33,36 @@ hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8
                           float* y, int n, int m, int k, int ldy, hipStream_t st);
 hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd,
                                    int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
-                                   const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
-                                   _Float16* vt, int ldv, hipStream_t st);
+                                   const int32_t* pos, float eps, float* out, hipStream_t st);
 hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                                 int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st);
-hipError_t launch_attention(const _Float16* qs, const _Float16* ks, const _Float16* vt, int ldv, const uint32_t* items,
-                            const uint32_t* item_count, int grid, int window, int rows, int8_t* cq, float* cd,
-                            float* partials, hipStream_t st);
-hipError_t launch_attention_merge(const uint32_t* merges, const uint32_t* merge_count, int grid, const float* partials,
-                                  int rows, int8_t* cq, float* cd, hipStream_t st);
 
-// Work lists of launch_attention / launch_attention_merge for the
-// sequences [offsets[s], offsets[s+1]): per query tile of up to 16 tokens
-// of one sequence, one item (8 uint32: first query, end, sequence start,
-// sequence end, key chunk start, key chunk end, partial slot or
-// 0xFFFFFFFF, 0) per key chunk -- a sequence of n > 256 tokens splits its
-// keys into min(ceil(n / 256), 4) chunks of equal size rounded up to 32,
-// whose partial results go to consecutive slots -- and, for split tiles,
-// one merge record (first query, end, first slot, parts). attention_capacity bounds the counts for a wave of
-// `tokens` tokens in at most `batch` sequences.
+// Attention over the rows [q0 q1 q2 | k | v] of a packed wave, bit-exact
+// with the reference (see kernels_attn.hip): the scores of the work items
+// (8 uint32 each: sequence start, sequence end, first key of a 64-key
+// block, first query, end of the queries, the sequence's first score
+// index, 0, 0; *item_count of them, `grid` workgroups striding over them)
+// into `scores`, then per token (tok: 4 uint32 each: sequence start, end,
+// first score index, 0) the context, quantized to Q8_0 into cq (row tiles,
+// k = 768) and cd [24][rows]. rows % 4 == 0.
+hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
+                            const uint32_t* tok, int window, int rows, float* scores, int8_t* cq, float* cd,
+                            hipStream_t st);
+
+// Work items and token records of launch_attention for the sequences
+// [offsets[s], offsets[s+1]): a sequence of n tokens has ceil(n / 64) key
+// blocks times ceil(n / q(n)) query chunks (q(n) = 8, 16 or 32 as n grows)
+// and 3 n^2 scores. attention_counts gives the counts of a packing;
+// build_attention_plan writes the lists when they fit `cap` (else returns
+// false having written nothing) and reports the counts in *used;
+// attention_capacity bounds the counts of any packing of `tokens` tokens
+// into at most `batch` sequences.
 struct AttentionCounts {
-  unsigned items, merges, slots;
+  size_t items, score_floats;
 };
-AttentionCounts build_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges);
+AttentionCounts attention_counts(const size_t* offsets, size_t batch);
+bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCounts& cap, uint32_t* items,
+                          uint32_t* tok, AttentionCounts* used);
 AttentionCounts attention_capacity(size_t tokens, size_t batch);
-constexpr size_t kAttentionPartialFloats = 2 * 3 * (16 * 64 * 4 + 64 * 2);  // per slot: 2 query blocks x 3 heads
-
-// V^T column of every token: each sequence starts at a multiple of 32,
-// consecutive tokens take consecutive columns. Returns the column count
-// used (sequences rounded up to 32 tokens each).
-size_t build_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol);
 
 }  // namespace eg2

@@ -42,9 +42,7 @@
 namespace {
 
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
-// Transposed-v columns: every sequence (and the padding sequence) starts at
-// a multiple of 32, so at most kCap + 31 * (kCap + 1) columns, rounded to 32.
-constexpr unsigned kVtCols = (kCap + 31 * (kCap + 1) + 31) / 32 * 32;
+constexpr int kScoreGrid = 512;  // workgroups of the attention scores kernel (two per CU), striding over its items
 constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
@@ -205,18 +203,17 @@ struct Lane {
   std::mutex mutex;
   float *x, *h, *xd, *cd, *pooled, *mid, *mid_d;
   int8_t *xq, *cq, *mid_q;
-  _Float16 *qs, *ks, *vt;
-  int32_t *ids_d, *pos_d, *vcol_d;
-  // Attention work lists (items, merges) and their counts {items, merges};
-  // partial results of split sequences.
-  uint32_t *items_d, *merges_d, *counts_d, *off_d;
-  float* partials;
+  float* qkv;     // [rows][q0 q1 q2 | k | v] after QK-norm / RoPE
+  float* scores;  // attention scores scratch, 3 n^2 per sequence of n tokens
+  int32_t *ids_d, *pos_d;
+  // Attention plan: the scores kernel's work items and their count, one
+  // record per token.
+  uint32_t *items_d, *count_d, *tok_d, *off_d;
   // Pinned staging.
-  int32_t *ids_h, *pos_h, *vcol_h;
-  uint32_t *items_h, *merges_h, *counts_h, *off_h;
+  int32_t *ids_h, *pos_h;
+  uint32_t *items_h, *count_h, *tok_h, *off_h;
   float* out_h;
-  std::map<unsigned, hipGraphExec_t> graphs;  // key: 2 * padded rows + (wave has split sequences)
-  bool staged_merge = false;
+  std::map<unsigned, hipGraphExec_t> graphs;  // key: padded rows
   unsigned staged_tokens = 0, staged_rows = 0, staged_longest = 0;
   size_t staged_batch = 0;
   std::map<std::string, double> timings;
@@ -315,7 +312,7 @@ class Backend {
   DevMat upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k);
   void alloc_lane(Lane& L);
   void launch(const char* name, hipError_t e);
-  void record_layers(Lane& L, unsigned rows, bool merge);
+  void record_layers(Lane& L, unsigned rows);
   void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
             hipStream_t s);
   void wait(Lane& L, const char* what);
@@ -484,19 +481,13 @@ void Backend::alloc_lane(Lane& L) {
   L.xd = dalloc<float>((size_t)kCap * (kFF / 32));
   L.cq = dalloc<int8_t>(eg2_q8_tile_bytes(kCap, kEmbd));
   L.cd = dalloc<float>((size_t)kCap * (kEmbd / 32));
-  L.qs = dalloc<_Float16>((size_t)kCap * 2 * kEmbd);
-  L.ks = dalloc<_Float16>((size_t)kCap * 2 * kHeadDim);
-  // Columns no token writes are read (masked) by the attention kernel and
-  // must hold finite values: zero the buffer once.
-  L.vt = dalloc<_Float16>((size_t)2 * kHeadDim * kVtCols);
-  check(hipMemset(L.vt, 0, (size_t)2 * kHeadDim * kVtCols * sizeof(_Float16)), "hipMemset");
+  L.qkv = dalloc<float>((size_t)kCap * kQKV);
+  L.scores = dalloc<float>(attn_cap_.score_floats);
   L.ids_d = dalloc<int32_t>(kCap);
   L.pos_d = dalloc<int32_t>(kCap);
-  L.vcol_d = dalloc<int32_t>(kCap);
-  L.items_d = dalloc<uint32_t>(8 * (size_t)attn_cap_.items);
-  L.merges_d = dalloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
-  L.counts_d = dalloc<uint32_t>(2);
-  L.partials = dalloc<float>(eg2::kAttentionPartialFloats * std::max(1u, attn_cap_.slots));
+  L.items_d = dalloc<uint32_t>(8 * attn_cap_.items);
+  L.count_d = dalloc<uint32_t>(1);
+  L.tok_d = dalloc<uint32_t>(4 * (size_t)kCap);
   L.off_d = dalloc<uint32_t>(kCap + 1);
   L.pooled = dalloc<float>((size_t)kCap * kEmbd);
   L.mid = dalloc<float>((size_t)kCap * kDenseFF);
@@ -504,10 +495,9 @@ void Backend::alloc_lane(Lane& L) {
   L.mid_d = dalloc<float>((size_t)kCap * (kDenseFF / 32));
   L.ids_h = halloc<int32_t>(kCap);
   L.pos_h = halloc<int32_t>(kCap);
-  L.vcol_h = halloc<int32_t>(kCap);
-  L.items_h = halloc<uint32_t>(8 * (size_t)attn_cap_.items);
-  L.merges_h = halloc<uint32_t>(4 * (size_t)std::max(1u, attn_cap_.merges));
-  L.counts_h = halloc<uint32_t>(2);
+  L.items_h = halloc<uint32_t>(8 * attn_cap_.items);
+  L.count_h = halloc<uint32_t>(1);
+  L.tok_h = halloc<uint32_t>(4 * (size_t)kCap);
   L.off_h = halloc<uint32_t>(kCap + 1);
   L.out_h = halloc<float>((size_t)kCap * kEmbd);
 }
@@ -535,28 +525,23 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
 // then per layer (engine.c:1115-1127 order) QKV GEMM with QK-norm/RoPE,
-// attention (+Q8_0; with `merge`, the merge of split sequences' key-chunk
-// partials), O GEMM, residual + ffn_norm (+Q8_0), gate|up GEMM with the
-// GeGLU (+Q8_0) in its epilogue, down GEMM, residual + next attn_norm
-// (+Q8_0); finally the
-// output_norm per token (the first half of kernels.c:417-427).
-void Backend::record_layers(Lane& ln, unsigned rows, bool merge) {
+// attention (scores, then the context and its Q8_0), O GEMM, residual +
+// ffn_norm (+Q8_0), gate|up GEMM with the GeGLU (+Q8_0) in its epilogue,
+// down GEMM, residual + next attn_norm (+Q8_0); finally the output_norm per
+// token (the first half of kernels.c:417-427).
+void Backend::record_layers(Lane& ln, unsigned rows) {
   hipStream_t s = ln.stream;
   const int n = (int)rows;
   launch("embed", eg2::launch_embed_norm_quant(token_embd_, ln.ids_d, n, std::sqrt((float)kEmbd),
                                                layers_[0].attn_norm, eps_, ln.x, ln.xq, ln.xd, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
-    // Q|K|V projection with QK-norm / RoPE in its epilogue: the split q/k
-    // rows and the transposed v for attention, no fp32 projection in HBM.
+    // Q|K|V projection with QK-norm / RoPE in its epilogue: the attention
+    // operand rows, no unnormalised projection in HBM.
     launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
-                                                         L.q_norm, L.k_norm, L.rope, ln.pos_d, ln.vcol_d, eps_,
-                                                         ln.qs, ln.ks, ln.vt, kVtCols, s));
-    launch("attention", eg2::launch_attention(ln.qs, ln.ks, ln.vt, kVtCols, ln.items_d, ln.counts_d,
-                                              (n + 7) / 8, L.window, n, ln.cq, ln.cd, ln.partials, s));
-    if (merge)
-      launch("attention_merge", eg2::launch_attention_merge(ln.merges_d, ln.counts_d + 1, (n + 3) / 4, ln.partials,
-                                                            n, ln.cq, ln.cd, s));
+                                                         L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
+    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, kScoreGrid, ln.tok_d, L.window, n,
+                                              ln.scores, ln.cq, ln.cd, s));
     gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
     // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.
@@ -634,40 +619,32 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
     ln.pos_h[t] = (int32_t)(t - n);
   }
   for (size_t s = 0; s <= batch; ++s) ln.off_h[s] = (uint32_t)offsets[s];
-  // Attention work lists; the padding rows form one more sequence.
+  // The attention plan; the padding rows form one more sequence. Its counts
+  // are checked against the allocation before anything is written.
   std::vector<size_t> all(offsets, offsets + batch + 1);
   if (rows > n) all.push_back(rows);
-  const eg2::AttentionCounts ac = eg2::build_attention_items(all.data(), all.size() - 1, ln.items_h, ln.merges_h);
-  if (ac.items > attn_cap_.items || ac.merges > attn_cap_.merges || ac.slots > attn_cap_.slots)
+  eg2::AttentionCounts used{0, 0};
+  if (!eg2::build_attention_plan(all.data(), all.size() - 1, attn_cap_, ln.items_h, ln.tok_h, &used))
     throw std::runtime_error("attention work list exceeds its capacity");
-  ln.counts_h[0] = ac.items;
-  ln.counts_h[1] = ac.merges;
-  const bool merge = ac.merges > 0;
-  // Transposed-v columns: the padding rows form one more sequence.
-  const size_t cols = eg2::build_vt_columns(offsets, batch, ln.vcol_h);
-  for (unsigned t = n; t < rows; ++t) ln.vcol_h[t] = (int32_t)(cols + (t - n));
+  ln.count_h[0] = (uint32_t)used.items;
 
   device_step([&] {
     hipStream_t s = ln.stream;
     check(hipMemcpyAsync(ln.ids_d, ln.ids_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy ids");
     check(hipMemcpyAsync(ln.pos_d, ln.pos_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
-    check(hipMemcpyAsync(ln.vcol_d, ln.vcol_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy columns");
-    check(hipMemcpyAsync(ln.items_d, ln.items_h, 8 * (size_t)ac.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+    check(hipMemcpyAsync(ln.items_d, ln.items_h, 8 * used.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
           "copy attention items");
-    if (merge)
-      check(hipMemcpyAsync(ln.merges_d, ln.merges_h, 4 * (size_t)ac.merges * sizeof(uint32_t),
-                           hipMemcpyHostToDevice, s),
-            "copy attention merges");
-    check(hipMemcpyAsync(ln.counts_d, ln.counts_h, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, s),
-          "copy attention counts");
+    check(hipMemcpyAsync(ln.count_d, ln.count_h, sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy attention count");
+    check(hipMemcpyAsync(ln.tok_d, ln.tok_h, 4 * (size_t)rows * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy token records");
     check(hipMemcpyAsync(ln.off_d, ln.off_h, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
           "copy offsets");
-    const unsigned key = 2 * rows + (merge ? 1 : 0);
+    const unsigned key = rows;
     if (use_graph_ && !profile_ && ln.graphs.find(key) == ln.graphs.end()) {
       hipGraph_t graph = nullptr;
       check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
       try {
-        record_layers(ln, rows, merge);
+        record_layers(ln, rows);
       } catch (...) {
         (void)hipStreamEndCapture(s, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -681,7 +658,6 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
       ln.graphs.emplace(key, exec);
     }
   });
-  ln.staged_merge = merge;
   ln.staged_tokens = n;
   ln.staged_rows = rows;
   ln.staged_batch = batch;
@@ -698,7 +674,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
   device_step([&] {
     for (unsigned r = 0; r < repeats; ++r) {
       if (use_graph_ && !profile_) {
-        check(hipGraphLaunch(ln.graphs.at(2 * ln.staged_rows + (ln.staged_merge ? 1 : 0)), s), "hipGraphLaunch");
+        check(hipGraphLaunch(ln.graphs.at(ln.staged_rows), s), "hipGraphLaunch");
       } else if (profile_) {
         // Per-stage timing needs events around eager launches; the totals are
         // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
@@ -706,7 +682,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
         check(hipEventCreate(&a), "hipEventCreate");
         check(hipEventCreate(&b), "hipEventCreate");
         check(hipEventRecord(a, s), "hipEventRecord");
-        record_layers(ln, ln.staged_rows, ln.staged_merge);
+        record_layers(ln, ln.staged_rows);
         check(hipEventRecord(b, s), "hipEventRecord");
         check(hipEventSynchronize(b), "hipEventSynchronize");
         float ms = 0;
@@ -715,7 +691,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
         (void)hipEventDestroy(a);
         (void)hipEventDestroy(b);
       } else {
-        record_layers(ln, ln.staged_rows, ln.staged_merge);
+        record_layers(ln, ln.staged_rows);
       }
       if (dense_) {
         // EXTRACTION.md:178-181: dense_2 then dense_3 on the mean pool

@@ -322,10 +322,10 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // the tile in LDS and, for q and k heads, runs each row's SSE2-order sum of
 // squares (waves 0-3, 8 lanes per row), then (x*w)*inv, the NeoX rotation of
 // pairs (d, d+128) with the host cos/sin row of the token's position, the
-// 1/16 scale of q, and writes the split fp16 pairs the attention kernel
-// reads -- the operations and order of the standalone qk_norm_rope kernel.
-// The v head is written transposed, vt[hi|lo][dim][vcol[t]]. The fp32
-// projection never reaches HBM.
+// 1/16 scale of q -- the operations and order of the standalone
+// qk_norm_rope kernel -- and writes the rows [q0 q1 q2 | k | v] attention
+// reads; the v head is the projection itself. The unnormalised projection
+// never reaches HBM.
 constexpr int kQkvTiles = 9;                      // A | B0 .. B7 per stage
 constexpr int kQDxOff = kQkvTiles * kTile;        // 64 floats (rows 0-31 used)
 constexpr int kQDwOff = kQDxOff + 64 * 4;         // 256 floats
@@ -338,8 +338,7 @@ __global__ void __launch_bounds__(512)
 gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx,
                         const int8_t* __restrict__ wq, const float* __restrict__ wd, int ldw, int n, int nb,
                         const float* __restrict__ q_w, const float* __restrict__ k_w, const float* __restrict__ rope,
-                        const int32_t* __restrict__ pos, const int32_t* __restrict__ vcol, float eps,
-                        _Float16* __restrict__ qs, _Float16* __restrict__ ks, _Float16* __restrict__ vt, int ldv) {
+                        const int32_t* __restrict__ pos, float eps, float* __restrict__ out) {
   __shared__ float invs[32];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
@@ -440,7 +439,6 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
       cs_r[rr][2 * j + 1] = cs[half + lane + 64 * j];
     }
   }
-  const int v_col = vcol[min(32 * tr + (lane & 31), n - 1)];
   __syncthreads();  // the ring becomes the epilogue tile
 
   float* tile = reinterpret_cast<float*>(gemm_lds);  // [32][kRowPitch]
@@ -448,19 +446,13 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
   for (int v = 0; v < 16; ++v) tile[(8 * (v >> 2) + 4 * g + (v & 3)) * kRowPitch + 32 * w + (lane & 31)] = acc[v];
   __syncthreads();
   if (is_v) {
-    // v: transposed split pairs; lanes 0-31 take 32 tokens of dim e, lanes
-    // 32-63 of dim e + 1.
-    const int tl = lane & 31, t = 32 * tr + tl;
-    if (t < n) {
-      _Float16* col = vt + v_col;
-#pragma unroll 2
-      for (int p = 0; p < 16; ++p) {
-        const int e = 32 * w + 2 * p + g;
-        const float val = tile[tl * kRowPitch + e];
-        const _Float16 h = (_Float16)val;
-        col[(size_t)e * ldv] = h;
-        col[(size_t)(kHeadDim + e) * ldv] = (_Float16)(val - (float)h);
-      }
+    // v: the projection as it is; wave w copies rows 4w .. 4w + 3.
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int row = 4 * w + rr, t = 32 * tr + row;
+      if (t >= n) break;
+      float* vrow = out + (size_t)t * kQKVCols + kHeads * kHeadDim + kHeadDim;
+      *reinterpret_cast<float4*>(vrow + 4 * lane) = *reinterpret_cast<const float4*>(tile + row * kRowPitch + 4 * lane);
     }
     return;
   }
@@ -488,33 +480,28 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
       if (hc < kHeads) {
         lo = lo * 0.0625f;
         hi = hi * 0.0625f;
-        _Float16* qrow = qs + (size_t)t * 2 * kEmbd;
-        store_split(qrow, kEmbd, hc * kHeadDim + dd, lo * 16.0f);
-        store_split(qrow, kEmbd, hc * kHeadDim + dd + half, hi * 16.0f);
-      } else {
-        _Float16* krow = ks + (size_t)t * 2 * kHeadDim;
-        store_split(krow, kHeadDim, dd, lo);
-        store_split(krow, kHeadDim, dd + half, hi);
       }
+      float* orow = out + (size_t)t * kQKVCols + hc * kHeadDim;
+      orow[dd] = lo;
+      orow[dd + half] = hi;
     }
   }
 }
 
 hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd,
                                    int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
-                                   const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
-                                   _Float16* vt, int ldv, hipStream_t st) {
-  if (n <= 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < kQKVCols || ldv <= 0) return hipErrorInvalidValue;
+                                   const int32_t* pos, float eps, float* out, hipStream_t st) {
+  if (n <= 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < kQKVCols) return hipErrorInvalidValue;
   static_assert(32 * kRowPitch * 4 <= kStages * kQStageBytes, "the epilogue tile fits in the ring");
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
   const dim3 grid(kXcds * reg.rows * reg.cols);
   const int nb = k / kQK;
   if (nb % kStages == 0)
     hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<false>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
-                       wd, ldw, n, nb, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv);
+                       wd, ldw, n, nb, q_w, k_w, rope, pos, eps, out);
   else
     hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<true>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
-                       wd, ldw, n, nb, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv);
+                       wd, ldw, n, nb, q_w, k_w, rope, pos, eps, out);
   return hipGetLastError();
 }
 

@@ -18,6 +18,8 @@
 //  * Q8_0 quantization works on the registers: a 32-value block is 8 lanes
 //    x 4 values, its maximum combined by DPP, and each lane stores its 4
 //    int8 values as one 32-bit word of the row tiles.
+#include <algorithm>
+
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
 
@@ -228,21 +230,18 @@ constexpr int kHeadStride = kHeadDim + 8;  // LDS row of one head: 8 banks apart
 // [q0 q1 q2 | k | v] (fp32, kQKVCols wide): per-head RMS with the weight
 // applied before the inverse, NeoX rotation of pairs (d, d+128) with the
 // host-built cos/sin row of this token's position, Q scaled by 0.0625 after
-// rotation. The fp32 results (bit-identical to the reference) are written as
-// split fp16 pairs for the attention kernel: q and k as rows [hi | lo] (q
-// times 16, exact, to keep its low half clear of fp16 subnormals), v
-// transposed as vt[hi|lo][dim][vcol[t]] so that a 32-key tile of a sequence
-// is one contiguous 64-byte run per dimension.
+// rotation; v unchanged. The results (bit-identical to the reference) go to
+// the same layout in `out`, which may be `qkv` itself: the row is read in
+// full before any of it is written.
 __global__ void __launch_bounds__(64)
-qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w, const float* __restrict__ k_w,
-                    const float* __restrict__ rope, const int32_t* __restrict__ pos,
-                    const int32_t* __restrict__ vcol, float eps, _Float16* __restrict__ qs,
-                    _Float16* __restrict__ ks, _Float16* __restrict__ vt, int ldv) {
+qk_norm_rope_kernel(const float* qkv, const float* __restrict__ q_w, const float* __restrict__ k_w,
+                    const float* __restrict__ rope, const int32_t* __restrict__ pos, float eps, float* out) {
   constexpr int kRows = kHeads + 1;  // q heads, then k
   constexpr int half = kHeadDim / 2;
   __shared__ __align__(16) float rows[kRows][kHeadStride];
   const int t = blockIdx.x, lane = threadIdx.x;
   const float* src = qkv + (size_t)t * kQKVCols;
+  float* dst = out + (size_t)t * kQKVCols;
   const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
   const float c0 = cs[lane], c1 = cs[lane + 64], s0 = cs[half + lane], s1 = cs[half + lane + 64];
 #pragma unroll
@@ -251,17 +250,8 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
     *reinterpret_cast<float4*>(&rows[e / kHeadDim][e % kHeadDim]) = *reinterpret_cast<const float4*>(src + e);
   }
   const float4 v = *reinterpret_cast<const float4*>(src + kRows * kHeadDim + 4 * lane);
-  {
-    const float vv[4] = {v.x, v.y, v.z, v.w};
-    _Float16* vcol_ptr = vt + vcol[t];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const _Float16 h = (_Float16)vv[i];
-      vcol_ptr[(size_t)(4 * lane + i) * ldv] = h;
-      vcol_ptr[(size_t)(kHeadDim + 4 * lane + i) * ldv] = (_Float16)(vv[i] - (float)h);
-    }
-  }
   __syncthreads();
+  *reinterpret_cast<float4*>(dst + kRows * kHeadDim + 4 * lane) = v;
   // lanes 8r..8r+7 run the chains of head row r (r < 4); the rest repeat row 0
   const int hr = (lane >> 3) < kRows ? (lane >> 3) : 0;
   const float ss = sse2_combine(sse2_chain<kHeadDim>(rows[hr], lane & 7));
@@ -283,14 +273,9 @@ qk_norm_rope_kernel(const float* __restrict__ qkv, const float* __restrict__ q_w
       if (hd < kHeads) {
         lo = lo * 0.0625f;
         hi = hi * 0.0625f;
-        _Float16* row = qs + (size_t)t * 2 * kEmbd;
-        store_split(row, kEmbd, hd * kHeadDim + d, lo * 16.0f);
-        store_split(row, kEmbd, hd * kHeadDim + d + half, hi * 16.0f);
-      } else {
-        _Float16* row = ks + (size_t)t * 2 * kHeadDim;
-        store_split(row, kHeadDim, d, lo);
-        store_split(row, kHeadDim, d + half, hi);
       }
+      dst[hd * kHeadDim + d] = lo;
+      dst[hd * kHeadDim + d + half] = hi;
     }
   }
 }
@@ -462,11 +447,26 @@ hipError_t launch_residual_norm_quant(float* x, const float* h, const float* pos
   return hipGetLastError();
 }
 
+// The restated libm functions (eg2_libm.hpp) on n floats, for comparison
+// with the host's: e[i] = expf(x[i]), t[i] = tanhf(x[i]).
+__global__ void __launch_bounds__(256)
+libm_eval_kernel(const float* __restrict__ x, unsigned n, float* __restrict__ e, float* __restrict__ t) {
+  for (unsigned i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    e[i] = libm::expf(x[i]);
+    t[i] = libm::tanhf(x[i]);
+  }
+}
+
+hipError_t launch_libm_eval(const float* x, unsigned n, float* e, float* t, hipStream_t st) {
+  if (n == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(libm_eval_kernel, dim3(std::min(4096u, (n + 255) / 256)), dim3(256), 0, st, x, n, e, t);
+  return hipGetLastError();
+}
+
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
-                               const int32_t* pos, const int32_t* vcol, float eps, _Float16* qs, _Float16* ks,
-                               _Float16* vt, int ldv, int rows, hipStream_t st) {
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, vcol, eps, qs, ks,
-                     vt, ldv);
+                               const int32_t* pos, float eps, float* out, int rows, hipStream_t st) {
+  if (rows <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(rows), dim3(64), 0, st, qkv, q_w, k_w, rope, pos, eps, out);
   return hipGetLastError();
 }
 

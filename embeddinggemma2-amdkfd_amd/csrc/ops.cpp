@@ -12,8 +12,6 @@
 
 namespace {
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
-_Float16* h16(uint16_t* p) { return reinterpret_cast<_Float16*>(p); }
-const _Float16* h16(const uint16_t* p) { return reinterpret_cast<const _Float16*>(p); }
 
 int code(hipError_t e) { return (int)e; }
 constexpr int kInvalid = (int)hipErrorInvalidValue;
@@ -62,54 +60,44 @@ int eg2_hip_residual_norm_quant(float* x, const float* h, const float* post_w, c
 }
 
 int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope_table,
-                         const int32_t* pos, const int32_t* vcol, float eps, uint16_t* qs, uint16_t* ks, uint16_t* vt,
-                         unsigned ldv, unsigned rows, void* stream) {
-  if (!qkv || !q_w || !k_w || !rope_table || !pos || !vcol || !qs || !ks || !vt || rows == 0 || ldv == 0 ||
-      ldv % 32 != 0 || ldv > (1u << 20))
+                         const int32_t* pos, float eps, float* out, unsigned rows, void* stream) {
+  if (!qkv || !q_w || !k_w || !rope_table || !pos || !out || rows == 0) return kInvalid;
+  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, eps, out, (int)rows, as_stream(stream)));
+}
+
+int eg2_hip_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, unsigned grid,
+                      const uint32_t* tok, unsigned window, unsigned rows, float* scores, int8_t* cq, float* cd,
+                      void* stream) {
+  if (!qkv || !items || !item_count || !tok || !scores || !cq || !cd || rows == 0 || rows % 4 != 0 ||
+      rows > (1u << 24) || grid == 0 || grid > 65536 || window > 4096u)
     return kInvalid;
-  return code(eg2::launch_qk_norm_rope(qkv, q_w, k_w, rope_table, pos, vcol, eps, h16(qs), h16(ks), h16(vt),
-                                       (int)ldv, (int)rows, as_stream(stream)));
+  return code(eg2::launch_attention(qkv, items, item_count, (int)grid, tok, (int)window, (int)rows, scores, cq, cd,
+                                    as_stream(stream)));
 }
 
-int eg2_hip_attention(const uint16_t* qs, const uint16_t* ks, const uint16_t* vt, unsigned ldv, const uint32_t* items,
-                      const uint32_t* item_count, unsigned grid, unsigned window, unsigned rows, int8_t* cq, float* cd,
-                      float* partials, void* stream) {
-  if (!qs || !ks || !vt || !items || !item_count || !cq || !cd || rows == 0 || grid == 0 ||
-      grid > 65536 || window > 4096u || ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
-    return kInvalid;
-  return code(eg2::launch_attention(h16(qs), h16(ks), h16(vt), (int)ldv, items, item_count, (int)grid,
-                                    (int)window, (int)rows, cq, cd, partials, as_stream(stream)));
+int eg2_attention_plan(const size_t* offsets, size_t batch, size_t items_cap, size_t scores_cap, uint32_t* items,
+                       uint32_t* tok, size_t* counts) {
+  if (!offsets || !items || !tok || !counts) return -1;
+  for (size_t s = 0; s < batch; ++s)
+    if (offsets[s + 1] < offsets[s] || offsets[s + 1] > (1u << 24)) return -1;
+  eg2::AttentionCounts used{0, 0};
+  const bool ok = eg2::build_attention_plan(offsets, batch, eg2::AttentionCounts{items_cap, scores_cap}, items, tok,
+                                            &used);
+  counts[0] = used.items;
+  counts[1] = used.score_floats;
+  return ok ? 0 : -1;
 }
 
-int eg2_hip_attention_merge(const uint32_t* merges, const uint32_t* merge_count, unsigned grid, const float* partials,
-                            unsigned rows, int8_t* cq, float* cd, void* stream) {
-  if (!merges || !merge_count || !partials || !cq || !cd || rows == 0 || grid == 0 || grid > 65536) return kInvalid;
-  return code(eg2::launch_attention_merge(merges, merge_count, (int)grid, partials, (int)rows, cq, cd,
-                                          as_stream(stream)));
-}
-
-unsigned eg2_attention_items(const size_t* offsets, size_t batch, uint32_t* items, uint32_t* merges, unsigned* counts) {
-  if (!offsets || !items || !merges || !counts) return 0;
-  const eg2::AttentionCounts c = eg2::build_attention_items(offsets, batch, items, merges);
-  counts[0] = c.items;
-  counts[1] = c.merges;
-  counts[2] = c.slots;
-  return c.items;
-}
-
-size_t eg2_attention_partial_floats(void) { return eg2::kAttentionPartialFloats; }
-
-void eg2_attention_capacity(size_t tokens, size_t batch, unsigned* counts) {
+void eg2_attention_capacity(size_t tokens, size_t batch, size_t* counts) {
   if (!counts) return;
   const eg2::AttentionCounts c = eg2::attention_capacity(tokens, batch);
   counts[0] = c.items;
-  counts[1] = c.merges;
-  counts[2] = c.slots;
+  counts[1] = c.score_floats;
 }
 
-size_t eg2_attention_vt_columns(const size_t* offsets, size_t batch, int32_t* vcol) {
-  if (!offsets || !vcol) return 0;
-  return eg2::build_vt_columns(offsets, batch, vcol);
+int eg2_hip_libm_eval(const float* x, unsigned n, float* expf_out, float* tanhf_out, void* stream) {
+  if (!x || !expf_out || !tanhf_out || n == 0) return kInvalid;
+  return code(eg2::launch_libm_eval(x, n, expf_out, tanhf_out, as_stream(stream)));
 }
 
 int eg2_hip_gelu_quant(const float* gate_up, int8_t* gq, float* gd, unsigned rows, void* stream) {
@@ -154,15 +142,13 @@ int eg2_hip_gemm_q8(const int8_t* xq, const float* xd, unsigned ldx, const int8_
 
 int eg2_hip_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd,
                              unsigned ldw, unsigned n, unsigned k, const float* q_w, const float* k_w,
-                             const float* rope_table, const int32_t* pos, const int32_t* vcol, float eps,
-                             uint16_t* qs, uint16_t* ks, uint16_t* vt, unsigned ldv, void* stream) {
+                             const float* rope_table, const int32_t* pos, float eps, float* out, void* stream) {
   constexpr unsigned kMax = 1u << 24;
-  if (!xq || !xd || !wq || !wd || !q_w || !k_w || !rope_table || !pos || !vcol || !qs || !ks || !vt || n == 0 ||
-      k == 0 || k % 32 != 0 || ldx < n || ldw < 1280 || n > kMax || k > kMax || ldx > kMax || ldw > kMax ||
-      ldv == 0 || ldv % 32 != 0 || ldv > (1u << 20))
+  if (!xq || !xd || !wq || !wd || !q_w || !k_w || !rope_table || !pos || !out || n == 0 || k == 0 || k % 32 != 0 ||
+      ldx < n || ldw < 1280 || n > kMax || k > kMax || ldx > kMax || ldw > kMax)
     return kInvalid;
   return code(eg2::launch_gemm_q8_qkv_rope(xq, xd, (int)ldx, wq, wd, (int)ldw, (int)n, (int)k, q_w, k_w, rope_table,
-                                           pos, vcol, eps, h16(qs), h16(ks), h16(vt), (int)ldv, as_stream(stream)));
+                                           pos, eps, out, as_stream(stream)));
 }
 
 int eg2_hip_gemm_q8_geglu(const int8_t* xq, const float* xd, unsigned ldx, const int8_t* wq, const float* wd,

@@ -109,14 +109,13 @@ SIGNATURES = {
     "eg2_op_name": (C.c_char_p, [_u]),
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
-    "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _u, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
-    "eg2_hip_attention_merge": (C.c_int, [_vp, _vp, _u, _vp, _u, _vp, _vp, _vp]),
-    "eg2_attention_items": (C.c_uint, [C.POINTER(C.c_size_t), C.c_size_t, _vp, _vp, _vp]),
-    "eg2_attention_partial_floats": (C.c_size_t, []),
-    "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_uint)]),
-    "eg2_attention_vt_columns": (C.c_size_t, [C.POINTER(C.c_size_t), C.c_size_t, _vp]),
+    "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_attention_plan": (C.c_int, [C.POINTER(C.c_size_t), C.c_size_t, C.c_size_t, C.c_size_t, _vp, _vp,
+                                     C.POINTER(C.c_size_t)]),
+    "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_libm_eval": (C.c_int, [_vp, _u, _vp, _vp, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
@@ -124,8 +123,8 @@ SIGNATURES = {
     "eg2_hip_l2_prefix": (C.c_int, [_vp, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _u, _u, _u, _u, _vp]),
     "eg2_hip_gemm_q8_geglu": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _vp, _vp, _u, _u, _u, _u, _vp]),
-    "eg2_hip_gemm_q8_qkv_rope": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp, _vp, C.c_float,
-                                           _vp, _vp, _vp, _u, _vp]),
+    "eg2_hip_gemm_q8_qkv_rope": (C.c_int, [_vp, _vp, _u, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp, C.c_float, _vp,
+                                           _vp]),
     "eg2_hip_error_string": (C.c_char_p, [C.c_int]),
     "eg2_hip_device_check": (C.c_int, [C.c_char_p, C.c_size_t]),
     "eg2_q8_tile_bytes": (C.c_size_t, [C.c_size_t, _u]),
@@ -431,17 +430,6 @@ def rope_table(base, n_pos=N_CTX):
     return t
 
 
-def attention_vt_columns(offsets):
-    """(vcol int32 [offsets[-1]], ldv): the transposed-v column of every token
-    and a row pitch (multiple of 32) that holds them."""
-    import numpy as np
-
-    offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
-    vcol = np.zeros(max(1, int(offsets[-1])), dtype=np.int32)
-    cols = lib().eg2_attention_vt_columns(offs, len(offsets) - 1, vcol.ctypes.data)
-    return vcol, max(32, (cols + 31) // 32 * 32)
-
-
 def q8_tile_bytes(rows, k):
     """Bytes of a Q8_0 row-tile buffer (rows rounded up to 32)."""
     return lib().eg2_q8_tile_bytes(rows, k)
@@ -533,39 +521,50 @@ def embeddings_response(embeddings, dims, api="ollama", encoding="float", model=
     return buf.raw[:n].decode()
 
 
-def attention_items(offsets):
-    """(items uint32 [n, 8], merges uint32 [m, 4], slots) of a packing
-    (eg2_attention_items)."""
+def attention_capacity(tokens, batch):
+    """(items, score floats): eg2_attention_capacity."""
+    counts = (C.c_size_t * 2)()
+    lib().eg2_attention_capacity(tokens, batch, counts)
+    return int(counts[0]), int(counts[1])
+
+
+def attention_plan(offsets, rows=None):
+    """(items uint32 [n, 8], tok uint32 [rows, 4], score floats) of the
+    sequences [offsets[s], offsets[s+1]) (eg2_attention_plan); rows defaults
+    to offsets[-1], and every row must belong to a sequence."""
     import numpy as np
 
     offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
     total, batch = int(offsets[-1]), len(offsets) - 1
-    items = np.zeros((total + batch + 1, 8), dtype=np.uint32)
-    merges = np.zeros(((total + 15) // 16 + 1, 4), dtype=np.uint32)
-    counts = np.zeros(3, dtype=np.uint32)
-    lib().eg2_attention_items(offs, batch, items.ctypes.data, merges.ctypes.data, counts.ctypes.data)
-    return items[:counts[0]], merges[:counts[1]], int(counts[2])
+    rows = total if rows is None else rows
+    cap_items, cap_scores = attention_capacity(max(total, 1), max(batch, 1))
+    items = np.zeros((cap_items, 8), dtype=np.uint32)
+    tok = np.zeros((max(rows, total, 1), 4), dtype=np.uint32)
+    counts = (C.c_size_t * 2)()
+    rc = lib().eg2_attention_plan(offs, batch, cap_items, cap_scores, items.ctypes.data, tok.ctypes.data, counts)
+    if rc != 0:
+        raise HipError("attention plan exceeds its capacity")
+    return items[:counts[0]], tok[:rows], int(counts[1])
 
 
 class AttentionPlan:
-    """The attention work lists of a packing on the device (items, merges,
-    their counts) and the partial-result buffer of split sequences."""
+    """The attention plan of a packing on the device (work items, their
+    count, token records) and its scores scratch."""
 
-    def __init__(self, offsets, device):
+    GRID = 512  # scores workgroups striding over the items (the executor's choice)
+
+    def __init__(self, offsets, device, rows=None):
         import numpy as np
         import torch
 
-        items, merges, slots = attention_items(offsets)
-        counts = np.array([len(items), len(merges)], dtype=np.uint32)
-        self.items = torch.from_numpy(np.ascontiguousarray(items).view(np.int32).reshape(-1)).to(device)
-        self.merges = torch.from_numpy(np.ascontiguousarray(merges).view(np.int32).reshape(-1).copy()
-                                       if len(merges) else np.zeros(4, np.int32)).to(device)
-        self.counts = torch.from_numpy(counts.view(np.int32)).to(device)
-        self.n_merges = len(merges)
-        self.partials = torch.zeros(max(1, slots) * lib().eg2_attention_partial_floats(), dtype=torch.float32,
-                                    device=device)
-        self.grid = max(1, (int(offsets[-1]) + 7) // 8)
-        self.merge_grid = max(1, (int(offsets[-1]) + 3) // 4)
+        items, tok, score_floats = attention_plan(offsets, rows)
+        self.n_items = len(items)
+        self.items = torch.from_numpy(np.ascontiguousarray(items).view(np.int32).reshape(-1).copy()
+                                      if len(items) else np.zeros(8, np.int32)).to(device)
+        self.count = torch.tensor([len(items)], dtype=torch.int32, device=device)
+        self.tok = torch.from_numpy(np.ascontiguousarray(tok).view(np.int32).reshape(-1).copy()).to(device)
+        self.scores = torch.zeros(max(1, score_floats), dtype=torch.float32, device=device)
+        self.rows = tok.shape[0]
 
 
 class ops:
@@ -594,42 +593,38 @@ class ops:
               "residual_norm_quant")
 
     @classmethod
-    def qk_norm_rope(cls, qkv, q_w, k_w, table, pos, vcol, eps, qh, kh, vt):
-        """vt: [2, 256, ldv] transposed v, written at columns vcol (attention_vt_columns)."""
-        check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos),
-                                         cls._p(vcol), eps, cls._p(qh), cls._p(kh), cls._p(vt), vt.shape[2],
-                                         qkv.shape[0], cls._stream()), "qk_norm_rope")
+    def qk_norm_rope(cls, qkv, q_w, k_w, table, pos, eps, out):
+        """Rows [q0 q1 q2 | k | v] of qkv normalised / rotated into out (may be qkv)."""
+        check(lib().eg2_hip_qk_norm_rope(cls._p(qkv), cls._p(q_w), cls._p(k_w), cls._p(table), cls._p(pos), eps,
+                                         cls._p(out), qkv.shape[0], cls._stream()), "qk_norm_rope")
 
     @classmethod
-    def gemm_q8_qkv_rope(cls, xq, xd, wq, wd, n, q_w, k_w, table, pos, vcol, eps, qh, kh, vt):
+    def gemm_q8_qkv_rope(cls, xq, xd, wq, wd, n, q_w, k_w, table, pos, eps, out):
         """The QKV projection of n rows (xq/xd as for gemm_q8, weights of the
-        [q|k|v] concatenation) followed by qk_norm_rope, in one kernel."""
+        [q|k|v] concatenation) followed by qk_norm_rope, in one kernel, into
+        out [n, 1280]."""
         check(lib().eg2_hip_gemm_q8_qkv_rope(cls._p(xq), cls._p(xd), xd.shape[1], cls._p(wq), cls._p(wd),
                                              wd.shape[1], n, 32 * xd.shape[0], cls._p(q_w), cls._p(k_w),
-                                             cls._p(table), cls._p(pos), cls._p(vcol), eps, cls._p(qh), cls._p(kh),
-                                             cls._p(vt), vt.shape[2], cls._stream()), "gemm_q8_qkv_rope")
+                                             cls._p(table), cls._p(pos), eps, cls._p(out), cls._stream()),
+              "gemm_q8_qkv_rope")
 
     @classmethod
-    def attention(cls, qs, ks, vt, offsets, window, cq, cd):
-        """Packed attention over sequences [offsets[s], offsets[s+1]); vt as
-        qk_norm_rope writes it at the columns of attention_vt_columns."""
+    def attention(cls, qkv, offsets, window, cq, cd):
+        """Packed attention over sequences [offsets[s], offsets[s+1]) of the
+        rows [q0 q1 q2 | k | v] of qkv (rows a multiple of 4 covered by the
+        sequences), the context quantized into cq / cd."""
         import torch
 
-        plan = AttentionPlan(offsets, qs.device)
-        cls.attention_planned(qs, ks, vt, plan, window, cq, cd)
-        torch.cuda.current_stream().synchronize()  # keeps the plan alive until the kernel ran
+        plan = AttentionPlan(offsets, qkv.device, qkv.shape[0])
+        cls.attention_planned(qkv, plan, window, cq, cd)
+        torch.cuda.current_stream().synchronize()  # keeps the plan alive until the kernels ran
 
     @classmethod
-    def attention_planned(cls, qs, ks, vt, plan, window, cq, cd):
+    def attention_planned(cls, qkv, plan, window, cq, cd):
         """attention() with a prebuilt AttentionPlan (no host work, no sync)."""
-        rows = qs.shape[0]
-        check(lib().eg2_hip_attention(cls._p(qs), cls._p(ks), cls._p(vt), vt.shape[2],
-                                      cls._p(plan.items), cls._p(plan.counts), plan.grid, window, rows, cls._p(cq),
-                                      cls._p(cd), cls._p(plan.partials), cls._stream()), "attention")
-        if plan.n_merges:
-            check(lib().eg2_hip_attention_merge(cls._p(plan.merges), C.c_void_p(plan.counts.data_ptr() + 4),
-                                                plan.merge_grid, cls._p(plan.partials), rows, cls._p(cq), cls._p(cd),
-                                                cls._stream()), "attention_merge")
+        check(lib().eg2_hip_attention(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID,
+                                      cls._p(plan.tok), window, qkv.shape[0], cls._p(plan.scores), cls._p(cq),
+                                      cls._p(cd), cls._stream()), "attention")
 
     @classmethod
     def gelu_quant(cls, gu, gq, gd):

@@ -13,9 +13,8 @@
  * ((((r / 32) * (k/32) + e / 32) * 2 + (e / 16) % 2) * 512 + (r % 32) * 16
  * + e % 16, so each 32 x 32 block is 1 KB in the register order of the int8
  * MFMA operand (eg2_q8_tile_bytes gives the size; eg2_q8_pack_rows and
- * eg2_q8_unpack_rows convert from and to row-major int8). fp16 buffers are
- * passed as uint16_t bit patterns. The attention operands are fp32 values
- * split into fp16 pairs, rows [hi | lo] with hi = fp16(x), lo = fp16(x - hi).
+ * eg2_q8_unpack_rows convert from and to row-major int8). The attention
+ * operands are the fp32 rows [q0 q1 q2 | k | v] of the fused projection.
  *
  * Each entry names the reference function whose semantics it implements
  * (paths relative to vendor/embeddinggemma.c/src/ unless they start with
@@ -49,72 +48,57 @@ int eg2_hip_residual_norm_quant(float *x, const float *h, const float *post_w, c
                                 int8_t *xq, float *xd, unsigned rows, void *stream);
 
 /* kernels.c:233-264 ei_qk_norm_rope_qk_inplace on rows of the fused
- * [q 768 | k 256 | v 256] projection; rope_table[pos][0..127] = cos,
- * [128..255] = sin (eg2_rope_table). The fp32 results are written as split
- * fp16 values: qs [rows][2][768] holding 16*q (q includes the 0.0625 scale),
- * ks [rows][2][256], and v (unchanged) transposed into vt [2][256][ldv] at
- * column vcol[t] (eg2_attention_vt_columns). ldv % 32 == 0.
- * Replaces kernels/eg2.c:204-217 eg2_norm_rope. */
+ * projection [q0 q1 q2 | k | v] (1280 fp32 per token): each q head and k
+ * normalised and rotated with rope_table[pos[t]] ([0..127] = cos, [128..255]
+ * = sin; eg2_rope_table), q scaled by 0.0625 after rotation, v unchanged;
+ * the results, bit-identical to the reference, in the same layout in out,
+ * which may be qkv itself. Replaces kernels/eg2.c:204-217 eg2_norm_rope. */
 int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, const float *rope_table,
-                         const int32_t *pos, const int32_t *vcol, float eps, uint16_t *qs, uint16_t *ks, uint16_t *vt,
-                         unsigned ldv, unsigned rows, void *stream);
+                         const int32_t *pos, float eps, float *out, unsigned rows, void *stream);
 
 /* kernels.c:324-360 ei_attention_mha_range over packed sequences
- * (engine.c:850-873): each token attends to the keys of its own sequence,
- * limited to |t - s| <= window/2 when window > 0; 3 query heads share one KV
- * head, head_dim 256. Inputs are the split q/k rows and the transposed v of
- * eg2_hip_qk_norm_rope (same vt and ldv, its vcol laid out by
- * eg2_attention_vt_columns; vt columns that no token wrote must hold finite
- * values, e.g. zeros). The work list `items`
- * (device, 8 uint32 per item, from eg2_attention_items) holds *item_count
- * (device) items; `grid` workgroups stride over it. An item whose slot is
- * 0xFFFFFFFF quantizes its fp32 context to Q8_0 (quants.c:97-177) into cq
- * (row tiles, k = 768) and cd [24][rows]; the items of a sequence longer
- * than 256 tokens cover up to four key chunks and write partial results to
- * `partials` (eg2_attention_partial_floats() floats per slot), which
- * eg2_hip_attention_merge then combines and quantizes. A sequence's result
- * does not depend on its place in the wave.
- * Replaces kernels/eg2.c:145-170 eg2_attention256. */
-int eg2_hip_attention(const uint16_t *qs, const uint16_t *ks, const uint16_t *vt, unsigned ldv, const uint32_t *items,
-                      const uint32_t *item_count, unsigned grid, unsigned window, unsigned rows, int8_t *cq,
-                      float *cd, float *partials, void *stream);
+ * (engine.c:850-873), bit-identical to the reference: each token attends to
+ * the keys of its own sequence, limited to |t - s| <= window/2 when window >
+ * 0; 3 query heads share one KV head, head_dim 256; scores in the
+ * reference's dot order (the SSE2 ei_dot_f32), expf as the host libm
+ * computes it, the sequential sum and context accumulation in key order;
+ * the context row is then quantized to Q8_0 (quants.c:97-177) into cq (row
+ * tiles, k = 768) and cd [24][rows]. qkv: rows of [q0 q1 q2 | k | v] as
+ * eg2_hip_qk_norm_rope leaves them. items / tok: the plan of
+ * eg2_attention_plan on the device (*item_count items; `grid` workgroups
+ * stride over them; tok holds one record for each of the `rows` rows, so
+ * every row must belong to a planned sequence, e.g. a padding one).
+ * scores: scratch of at least the plan's score count (counts[1]) floats.
+ * rows % 4 == 0. A sequence's result does not depend on its place in the
+ * wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
+int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
+                      const uint32_t *tok, unsigned window, unsigned rows, float *scores, int8_t *cq, float *cd,
+                      void *stream);
 
-/* Second step of eg2_hip_attention for split sequences: merges the
- * key-chunk partials of each query tile in `merges` (device, 4 uint32 per
- * tile: first query, end, first slot, parts; *merge_count of them) and
- * quantizes the context into cq / cd. Part of the same replacement. */
-int eg2_hip_attention_merge(const uint32_t *merges, const uint32_t *merge_count, unsigned grid, const float *partials,
-                            unsigned rows, int8_t *cq, float *cd, void *stream);
+/* Host: the plan of eg2_hip_attention for the sequences [offsets[s],
+ * offsets[s+1]): the scores kernel's work items (8 uint32 each: sequence
+ * start, end, first key of a 64-key block, first query, end of the
+ * queries, the sequence's first score index, 0, 0) and one token record
+ * per token (4 uint32: sequence start, end, first score index, 0) at
+ * tok[4 t]. counts[0] = items, counts[1] = score floats (3 n^2 per sequence
+ * of n tokens). Writes the lists and returns 0 when they fit items_cap
+ * items and scores_cap score floats; otherwise writes nothing and returns
+ * -1 (counts still report the need). */
+int eg2_attention_plan(const size_t *offsets, size_t batch, size_t items_cap, size_t scores_cap, uint32_t *items,
+                       uint32_t *tok, size_t *counts);
 
-/* Host: the work lists of a packed wave with sequences [offsets[s],
- * offsets[s+1]): per query tile of up to 32 tokens (from the sequence
- * start; one workgroup of the attention kernel) one item per key chunk
- * {first query, end, sequence start, sequence end, chunk start, chunk end,
- * slot or 0xFFFFFFFF, the sequence's first vt column as
- * eg2_attention_vt_columns places it} (a sequence of n > 256 tokens has c = min(ceil(n
- * / 256), 4) chunks of ceil(n / c) keys rounded up to 32, the last one
- * taking the rest, partial slots numbered consecutively; shorter ones one
- * chunk and no slot), and per split tile one merge record {first query,
- * end, first slot, parts}. counts[0..2] = items, merges, slots. `items` needs room for
- * 8 * (offsets[batch] + batch) entries, `merges` for 4 * ceil(offsets[batch]
- * / 32). Returns the item count. */
-unsigned eg2_attention_items(const size_t *offsets, size_t batch, uint32_t *items, uint32_t *merges, unsigned *counts);
+/* Host: counts[0..1] = the most items and score floats eg2_attention_plan
+ * can need for any packing of `tokens` tokens into at most `batch`
+ * sequences (the sizes the executor allocates for a 2048-token wave plus
+ * its padding sequence). */
+void eg2_attention_capacity(size_t tokens, size_t batch, size_t *counts);
 
-/* Floats of one partial-result slot (2 blocks of 16 queries x 3 heads x
- * (16 x 256 + 2 x 64)). */
-size_t eg2_attention_partial_floats(void);
-
-/* Host: counts[0..2] = the most items, merge records and partial slots that
- * eg2_attention_items can produce for any packing of `tokens` tokens into
- * at most `batch` sequences (the sizes the executor allocates for a
- * 2048-token wave plus its padding sequence). */
-void eg2_attention_capacity(size_t tokens, size_t batch, unsigned *counts);
-
-/* Host: the transposed-v column of every token (vcol[offsets[batch]]):
- * each sequence starts at a multiple of 32 and its tokens take consecutive
- * columns. Returns the columns used, at most offsets[batch] + 31 * batch;
- * vt needs ldv >= that, rounded up to 32. */
-size_t eg2_attention_vt_columns(const size_t *offsets, size_t batch, int32_t *vcol);
+/* The host libm functions the reference path calls (glibc's expf for the
+ * softmax, kernels.c:348, and tanhf for the GELU, kernels.c:370) as this
+ * library restates them on the device: expf_out[i] = expf(x[i]),
+ * tanhf_out[i] = tanhf(x[i]) for n floats, bit-identical to the host's for
+ * every input. For tests that compare the two. */
+int eg2_hip_libm_eval(const float *x, unsigned n, float *expf_out, float *tanhf_out, void *stream);
 
 /* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
  * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */
@@ -158,14 +142,13 @@ int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, unsigned ldx, const int8_
  * n rows of Q8_0 activations xq/xd [n][k] and the [q 768 | k 256 | v 256]
  * weights (eg2_q8_weight_tiles of the concatenated matrices, ldw >= 1280),
  * the projection exactly as eg2_hip_gemm_q8 computes it, then exactly what
- * eg2_hip_qk_norm_rope does with it (same q_w, k_w, rope_table, pos, vcol,
- * eps, outputs and ldv) -- bit-identical to the two calls, without the fp32
- * projection in memory. Replaces the Q/K/V eg2_mm* calls and eg2_norm_rope
- * of kernels/eg2.c (:41-119, :204-217). k % 32 == 0; ldv % 32 == 0. */
+ * eg2_hip_qk_norm_rope does with it (same q_w, k_w, rope_table, pos, eps),
+ * into out [n][1280] -- bit-identical to the two calls, without the
+ * unnormalised projection in memory. Replaces the Q/K/V eg2_mm* calls and
+ * eg2_norm_rope of kernels/eg2.c (:41-119, :204-217). k % 32 == 0. */
 int eg2_hip_gemm_q8_qkv_rope(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd,
                              unsigned ldw, unsigned n, unsigned k, const float *q_w, const float *k_w,
-                             const float *rope_table, const int32_t *pos, const int32_t *vcol, float eps,
-                             uint16_t *qs, uint16_t *ks, uint16_t *vt, unsigned ldv, void *stream);
+                             const float *rope_table, const int32_t *pos, float eps, float *out, void *stream);
 
 /* The gate and up projections and the GeGLU with its Q8_0 quantization in
  * one kernel: for rows of Q8_0 activations xq/xd [n][k] and the gate and up

@@ -630,3 +630,13 @@ void or_op_mm(const float *x, const float *w, uint32_t n, uint32_t k, uint32_t m
         }
     }
 }
+
+/* The host libm's expf and tanhf over an array (the functions the
+ * reference calls at kernels.c:348 and :370), for comparing a device
+ * restatement with them. */
+void or_libm_eval(const float *x, size_t n, float *expf_out, float *tanhf_out) {
+    for (size_t i = 0; i < n; i++) {
+        expf_out[i] = expf(x[i]);
+        tanhf_out[i] = tanhf(x[i]);
+    }
+}

@@ -130,6 +130,9 @@ void or_input_embeddings(const or_model *m, const int32_t *ids, int32_t n_tokens
 int or_forward(const or_model *m, const int32_t *ids, const size_t *offsets, size_t batch,
                float *out, int32_t threads);
 
+/* Host libm expf / tanhf over n floats. */
+void or_libm_eval(const float *x, size_t n, float *expf_out, float *tanhf_out);
+
 #ifdef __cplusplus
 }
 #endif

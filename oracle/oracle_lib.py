@@ -60,6 +60,7 @@ def _load_oracle():
         "or_op_mm": (None, [_f, _f, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f]),
         "or_layer_forward": (None, [_vp, C.c_float, _f, _i32, _vp, C.c_size_t, C.c_int32]),
         "or_forward": (C.c_int, [_vp, _i32, _vp, C.c_size_t, _f, C.c_int32]),
+        "or_libm_eval": (None, [_f, C.c_size_t, _f, _f]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -137,6 +138,14 @@ def dequantize_q8_0(blocks):
     d = d.reshape(blocks.shape)
     q = blocks["qs"].astype(np.float32)
     return (q * d[..., None]).reshape(blocks.shape[:-1] + (blocks.shape[-1] * QK,))
+
+
+def host_libm(name, x):
+    """The host libm's expf or tanhf of every element of x (float32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    e, t = np.empty_like(x), np.empty_like(x)
+    oracle().or_libm_eval(fptr(x), x.size, fptr(e), fptr(t))
+    return {"expf": e, "tanhf": t}[name]
 
 
 def op_mm(x, w, step):

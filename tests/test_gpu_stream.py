@@ -48,8 +48,9 @@ def test_stream_equals_each_text_alone(eg2, stream_encoder):
 
 
 def test_stream_matches_oracle(eg2, stream_encoder):
-    """A small stream against the CPU oracle (cosine >= 0.9999, max-abs <=
-    2e-3 on every truncated, normalised embedding)."""
+    """A small stream against the CPU oracle: every truncated, normalised
+    embedding within cosine >= 0.9999 and max-abs <= 2e-3, and equal bit for
+    bit."""
     enc, path = stream_encoder
     rng = np.random.default_rng(8)
     ids, offsets, dims = make_stream(rng, 12, 120)
@@ -61,6 +62,7 @@ def test_stream_matches_oracle(eg2, stream_encoder):
         g = out[i, :d]
         cos = float(g @ w[:d] / np.linalg.norm(g) / np.linalg.norm(w[:d]))
         assert cos >= 0.9999 and np.abs(g - w[:d]).max() <= 2e-3, (i, cos)
+        assert np.array_equal(g, w[:d]), i
 
 
 def test_stream_rejects_bad_texts(eg2, stream_encoder):

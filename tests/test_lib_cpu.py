@@ -62,13 +62,13 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
-    # gemm_q8_qkv_rope(xq, xd, ldx, wq, wd, ldw, n, k, q_w, k_w, rope, pos, vcol, eps, qs, ks, vt, ldv)
+    # gemm_q8_qkv_rope(xq, xd, ldx, wq, wd, ldw, n, k, q_w, k_w, rope, pos, eps, out)
     f = C.c_float(1e-6)
-    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 48, p, p, p, p, p, f, p, p, p, 64, None) == inval
-    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1279, 4, 32, p, p, p, p, p, f, p, p, p, 64, None) == inval
-    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 3, p, p, 1280, 4, 32, p, p, p, p, p, f, p, p, p, 64, None) == inval
-    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, p, p, f, p, p, p, 48, None) == inval
-    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, None, p, f, p, p, p, 64, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 48, p, p, p, p, f, p, None) == inval  # k % 32
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1279, 4, 32, p, p, p, p, f, p, None) == inval  # ldw
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 3, p, p, 1280, 4, 32, p, p, p, p, f, p, None) == inval  # ldx < n
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, None, f, p, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, p, f, None, None) == inval
     # gemm_q8_geglu(xq, xd, ldx, wq, wd, ldw, gq, gd, ldg, n, ff, k)
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 96, p, p, 4, 4, 48, 32, None) == inval  # ff % 32
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 4, 32, 48, None) == inval  # k % 32
@@ -77,13 +77,15 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 3, 4, 32, 32, None) == inval  # ldg < n
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, None, 4, 4, 32, 32, None) == inval
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 0, 32, 32, None) == inval  # n = 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, 0, 0, 32, p, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, p, 4, 99999, 32, p, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 64, None, p, 4, 0, 32, p, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 48, p, p, 4, 0, 32, p, p, p, None) == inval  # ldv % 32
-    assert lib.eg2_hip_attention_merge(p, p, 0, p, 32, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention_merge(p, p, 4, None, 32, p, p, None) == inval
-    assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, p, 1e-6, p, p, p, 40, 4, None) == inval  # ldv % 32
+    # attention(qkv, items, item_count, grid, tok, window, rows, scores, cq, cd)
+    assert lib.eg2_hip_attention(p, p, p, 0, p, 0, 32, p, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 99999, 32, p, p, p, None) == inval  # window
+    assert lib.eg2_hip_attention(p, p, p, 64, None, 0, 32, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 30, p, p, p, None) == inval  # rows % 4
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, None, p, p, None) == inval  # no scratch
+    assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, None, 4, None) == inval
+    assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, p, 0, None) == inval
+    assert lib.eg2_hip_libm_eval(p, 0, p, p, None) == inval
     assert lib.eg2_hip_quantize_rows(p, 96, p, p, 1, None) == inval  # k % 64
     assert lib.eg2_hip_l2_prefix(p, 768, 769, 1, None) == inval
     assert lib.eg2_hip_l2_prefix(p, 768, 100, 1, None) == inval
@@ -92,75 +94,65 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_pool_mean(p, p, p, 65536, None) == inval
 
 
-def test_vt_columns_align_each_sequence(eg2):
-    offs = [0, 1, 33, 97, 98, 200]
-    vcol, ldv = eg2.attention_vt_columns(offs)
-    base = 0
-    for s in range(len(offs) - 1):
-        n = offs[s + 1] - offs[s]
-        assert list(vcol[offs[s]:offs[s + 1]]) == list(range(base, base + n))
-        base += (n + 31) // 32 * 32
-    assert ldv == base and ldv <= offs[-1] + 31 * (len(offs) - 1)
-
-
-def test_attention_items_cover_each_sequence(eg2):
-    """Every (query, key) pair of a sequence is covered by exactly one item;
-    query tiles are 32 tokens from the sequence start; a sequence of n > 256
-    tokens splits its keys into c = min(ceil(n / 256), 4) chunks of
-    ceil(n / c) keys rounded up to 32 (aligned to its start) with
-    consecutive partial slots and one merge record per query tile; the last
-    field is the V^T column of the sequence's first token."""
+def test_attention_plan_covers_each_sequence(eg2):
+    """Every (query, key) pair of each sequence is covered by exactly one
+    scores item (64-key blocks from the sequence start, query chunks of 8,
+    16 or 32 tokens by length); each sequence's scores take 3 n^2 floats
+    after the previous ones; every token's record names its sequence and
+    that first score index."""
     offs = [0, 1, 33, 97, 98, 200, 600, 1100, 3150]
-    items, merges, slots = eg2.attention_items(offs)
-    vcol, _ = eg2.attention_vt_columns(offs)
+    items, tok, score_floats = eg2.attention_plan(offs)
     seqs = [(offs[s], offs[s + 1]) for s in range(len(offs) - 1)]
+    base = np.concatenate([[0], np.cumsum([3 * (b - a) ** 2 for a, b in seqs])])
+    assert score_floats == base[-1]
     covered = {s: np.zeros((hi - lo, hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
-    used_slots = []
-    for q0, q1, lo, hi, k0, k1, slot, col in items.astype(np.int64):
+    for lo, hi, k0, q0, q1, sb, z0, z1 in items.astype(np.int64):
         s = seqs.index((lo, hi))
-        assert lo <= q0 < q1 <= hi and q1 - q0 <= 32 and (q0 - lo) % 32 == 0 and col == vcol[lo]
         n = hi - lo
-        c = min(-(-n // 256), 4)
-        ck = -(-(-(-n // c)) // 32) * 32
-        assert lo <= k0 < k1 <= hi and (k0 - lo) % ck == 0 and (k0 - lo) % 32 == 0
-        if n <= 256:
-            assert (k0, k1, slot) == (lo, hi, 0xFFFFFFFF)
-        else:
-            assert k1 - k0 == min(ck, hi - k0)
-            used_slots.append(int(slot))
-        covered[s][q0 - lo:q1 - lo, k0 - lo:k1 - lo] += 1
-    assert all((c == 1).all() for c in covered.values())
-    assert sorted(used_slots) == list(range(slots))
-    # merges: one per query tile of a split sequence, slots first..first+parts-1
-    split = [(lo, hi) for lo, hi in seqs if hi - lo > 256]
-    assert len(merges) == sum((hi - lo + 31) // 32 for lo, hi in split)
-    for q0, q1, first, parts in merges.astype(np.int64):
-        lo, hi = next((lo, hi) for lo, hi in split if lo <= q0 < hi)
-        assert parts == min((hi - lo + 255) // 256, 4)
-        tile_items = [it for it in items if it[0] == q0]
-        assert sorted(int(it[6]) for it in tile_items) == list(range(first, first + parts))
+        qc = 8 if n <= 128 else (16 if n <= 512 else 32)
+        assert sb == base[s] and z0 == z1 == 0
+        assert lo <= k0 < hi and (k0 - lo) % 64 == 0
+        assert lo <= q0 < q1 <= hi and (q0 - lo) % qc == 0 and q1 == min(hi, q0 + qc)
+        covered[s][q0 - lo:q1 - lo, k0 - lo:min(hi, k0 + 64) - lo] += 1
+    for s in covered:
+        assert (covered[s] == 1).all(), s
+    for s, (lo, hi) in enumerate(seqs):
+        assert (tok[lo:hi] == [lo, hi, base[s], 0]).all()
+
+
+def test_attention_plan_checks_capacity_before_writing(eg2):
+    """A plan that does not fit the given capacity is rejected with nothing
+    written (the counts still report the need)."""
+    import ctypes as C
+
+    offs = [0, 700, 1500]
+    need_items = len(eg2.attention_plan(offs)[0])
+    arr = (C.c_size_t * 3)(*offs)
+    items = np.full((need_items, 8), 7, np.uint32)
+    tok = np.full((1500, 4), 7, np.uint32)
+    counts = (C.c_size_t * 2)()
+    for cap_items, cap_scores in ((need_items - 1, 1 << 30), (need_items, 3 * (700 ** 2 + 800 ** 2) - 1)):
+        rc = eg2.lib().eg2_attention_plan(arr, 2, cap_items, cap_scores, items.ctypes.data, tok.ctypes.data, counts)
+        assert rc == -1 and list(counts) == [need_items, 3 * (700 ** 2 + 800 ** 2)]
+        assert (items == 7).all() and (tok == 7).all()
 
 
 def test_attention_capacity_bounds_every_packing(eg2):
-    """The executor sizes its work lists with eg2_attention_capacity(2080,
-    2049) (a 2048-token wave plus a padding sequence of up to 31 rows): no
-    packing may exceed it. Every packing of equal sequences (the per-sequence
-    rounding of tiles and chunks is worst there) and every remainder, each
+    """The executor sizes its plan with eg2_attention_capacity(2080, 2049)
+    (a 2048-token wave plus a padding sequence of up to 31 rows): no packing
+    may exceed it. Every packing of equal sequences (the per-sequence
+    rounding of blocks and chunks is worst there) and every remainder, each
     followed by its padding sequence."""
-    import ctypes as C
-
-    cap = (C.c_uint * 3)()
-    eg2.lib().eg2_attention_capacity(2080, 2049, cap)
-    cap = list(cap)
-    worst = [0, 0, 0]
+    cap = eg2.attention_capacity(2080, 2049)
+    worst = [0, 0]
     for L in range(1, 2049):
         for total in (2048, 2048 - L // 2, 2017):
             lens = [L] * (total // L) + ([total % L] if total % L else [])
             n = sum(lens)
             pad = (-n) % 32
             offs = np.concatenate([[0], np.cumsum(lens + ([pad] if pad else []))])
-            items, merges, slots = eg2.attention_items(offs)
-            got = [len(items), len(merges), slots]
+            items, _, score_floats = eg2.attention_plan(offs)
+            got = [len(items), score_floats]
             worst = [max(a, b) for a, b in zip(worst, got)]
             assert all(g <= c for g, c in zip(got, cap)), (L, total, got, cap)
     print("worst", worst, "capacity", cap)
