@@ -177,12 +177,13 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
 
 // kernels.c:367-371 gelu_tanh(g) = 0.5 g (1 + tanhf(z)), z = s g (1 + a g^2),
 // times u (engine.c's GeGLU), each operation in the reference's order with
-// the host libm's own tanhf (eg2_libm.hpp): bit-identical to the CPU path.
+// the host libm's own tanhf (eg2_libm.hpp, its branch-free form, since the
+// lanes of a wave take different cases): bit-identical to the CPU path.
 __device__ __forceinline__ float gelu_mul(float g, float u) {
   const float a = 0.044715f;
   const float s = 0.79788456080286535587989211986876f;
   const float inner = s * g * (1.0f + a * g * g);
-  return 0.5f * g * (1.0f + libm::tanhf(inner)) * u;
+  return 0.5f * g * (1.0f + libm::tanhf_flat(inner)) * u;
 }
 
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):

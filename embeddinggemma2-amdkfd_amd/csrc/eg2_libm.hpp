@@ -147,6 +147,58 @@ __host__ __device__ inline float tanhf(float x) {
   return (int32_t)jx >= 0 ? z : -z;
 }
 
+// The same function as tanhf, for finite x, written without branches so
+// that a wave whose lanes fall in different cases runs one path: every case
+// of expm1f's reconstruction is computed and the lane's own selected. The
+// arithmetic of each case is fdlibm's unchanged. The argument reduction is
+// shared: fdlibm's k = 0 (no reduction, c = 0) and k = +-1 (x -+ ln2_hi,
+// lo = +-ln2_lo) cases are its general formula hi = x - k ln2_hi,
+// lo = k ln2_lo at k = 0 and +-1 (both products exact), so only the choice
+// of k differs between them. Inside tanhf expm1f sees 2|x| >= 2 or
+// -2|x| in (-2, 0), which keeps it off its overflow and saturation cases.
+__host__ __device__ inline float tanhf_flat(float x) {
+  const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+  const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
+              Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+  const uint32_t jx = fbits(x), ix = jx & 0x7fffffffu;
+  const bool big = ix >= 0x3f800000u;  // |x| >= 1: expm1f(2|x|), else expm1f(-2|x|)
+  const float ax = __builtin_fabsf(x);
+  const float a = big ? 2.0f * ax : -2.0f * ax;  // expm1f's argument
+  const uint32_t ha = fbits(a) & 0x7fffffffu;
+  // k: 0 for |a| <= 0.5 ln2, +-1 below 1.5 ln2, else the rounded a / ln2.
+  const int32_t kr = (int32_t)(invln2 * a + (big ? 0.5f : -0.5f));
+  const int32_t k = ha <= 0x3eb17218u ? 0 : (ha < 0x3F851592u ? (big ? 1 : -1) : kr);
+  const float t = (float)k;
+  const float hi = a - t * ln2_hi, lo = t * ln2_lo;
+  const float r = hi - lo;
+  const float c = (hi - r) - lo;
+  const bool tiny = ha < 0x33000000u;  // |a| < 2^-25: expm1f(a) = a
+  const float hfx = 0.5f * r;
+  const float hxs = r * hfx;
+  const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  const float tt = 3.0f - r1 * hfx;
+  const float e0 = hxs * ((r1 - tt) / (6.0f - r * tt));
+  float e = r * (e0 - c) - c;
+  e -= hxs;
+  // The reconstructions, k = 0, -1, 1, |k| large, 2 <= k < 23, 23 <= k <= 56.
+  const float v0 = r - (r * e0 - hxs);
+  const float vm1 = 0.5f * (r - e) - 0.5f;
+  const float vp1 = r < -0.25f ? -2.0f * (e - (r + 0.5f)) : 1.0f + 2.0f * (r - e);
+  const uint32_t kbits = (uint32_t)k << 23;
+  const float vout = ffrom(fbits(1.0f - (e - r)) + kbits) - 1.0f;
+  const int32_t kc = k < 1 ? 1 : (k > 31 ? 31 : k);  // shift counts kept in range; used only where k fits
+  const float vlow = ffrom(fbits(ffrom(0x3f800000u - (0x1000000u >> kc)) - (e - r)) + kbits);
+  const float vmid = ffrom(fbits((r - (e + ffrom((uint32_t)(0x7f - (k > 56 ? 56 : k)) << 23))) + 1.0f) + kbits);
+  float em1 = k == 0 ? v0 : (k == -1 ? vm1 : (k == 1 ? vp1 : ((k <= -2 || k > 56) ? vout : (k < 23 ? vlow : vmid))));
+  em1 = tiny ? a : em1;
+  // tanhf's tail: one division, 2 / (t + 2) or -t / (t + 2).
+  const float q = (big ? 2.0f : -em1) / (em1 + 2.0f);
+  float z = big ? 1.0f - q : q;
+  z = ix >= 0x41b00000u ? 1.0f - 1.0e-30f : z;  // |x| >= 22
+  z = ix < 0x24000000u ? x * (1.0f + x) : z;    // |x| < 2^-55 (and 0): tanhf keeps x's sign itself
+  return ix < 0x24000000u ? z : ((int32_t)jx >= 0 ? z : -z);
+}
+
 // 2^(i/32) for i = 0..31 as double bit patterns, minus i << 47 (the
 // exponent of 2^(k/32) is added back from k); each entry is the double
 // nearest 2^(i/32).

@@ -51,7 +51,7 @@ namespace eg2 {
 
 constexpr int kKeyBlock = 64;          // keys of a scores work item, one per lane
 constexpr int kKPitch = kHeadDim + 4;  // floats per LDS K row: 4 banks apart, so 8 lanes' b128 reads cover all 32
-constexpr int kPairs = 4;              // (token, head) pairs per pass of a scores wave
+constexpr int kPairs = 2;              // (token, head) pairs per pass of a scores wave
 constexpr int kLd = kQKVCols;          // floats per operand row [q0 q1 q2 | k | v]
 constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 
@@ -123,18 +123,52 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
       for (int i = 0; i < kPairs; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-#pragma unroll 4
-      for (int s = 0; s < kHeadDim / 4; ++s) {
-        const float4 k4 = *reinterpret_cast<const float4*>(krow + 4 * s);
+      // q in chunks of 2 steps (8 floats per pair), wave-uniform scalar
+      // loads, two chunks in registers: chunk c + 1 is requested after
+      // chunk c has arrived and before chunk c is used, so its latency
+      // overlaps chunk c's arithmetic. (Scalar loads return out of order:
+      // any wait for one is a wait for all, hence the explicit order.)
+      constexpr int kQ = 8, kChunks = kHeadDim / kQ;
+      float qa[kPairs][kQ], qb[kPairs][kQ];
+      auto load_q = [&](float (&dst)[kPairs][kQ], int c) {
 #pragma unroll
-        for (int i = 0; i < kPairs; ++i) {
-          const float4 q4 = *reinterpret_cast<const float4*>(qrow[i] + 4 * s);
-          const float p0 = q4.x * k4.x, p1 = q4.y * k4.y, p2 = q4.z * k4.z, p3 = q4.w * k4.w;
-          acc[i][0] = acc[i][0] + p0;
-          acc[i][1] = acc[i][1] + p1;
-          acc[i][2] = acc[i][2] + p2;
-          acc[i][3] = acc[i][3] + p3;
+        for (int i = 0; i < kPairs; ++i)
+#pragma unroll
+          for (int e = 0; e < kQ; e += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(qrow[i] + kQ * c + e);
+            dst[i][e] = v.x;
+            dst[i][e + 1] = v.y;
+            dst[i][e + 2] = v.z;
+            dst[i][e + 3] = v.w;
+          }
+      };
+      auto chunk = [&](const float (&q)[kPairs][kQ], int c) {
+#pragma unroll
+        for (int s = 0; s < kQ / 4; ++s) {
+          const float4 k4 = *reinterpret_cast<const float4*>(krow + kQ * c + 4 * s);
+#pragma unroll
+          for (int i = 0; i < kPairs; ++i) {
+            const float p0 = q[i][4 * s] * k4.x, p1 = q[i][4 * s + 1] * k4.y;
+            const float p2 = q[i][4 * s + 2] * k4.z, p3 = q[i][4 * s + 3] * k4.w;
+            acc[i][0] = acc[i][0] + p0;
+            acc[i][1] = acc[i][1] + p1;
+            acc[i][2] = acc[i][2] + p2;
+            acc[i][3] = acc[i][3] + p3;
+          }
         }
+      };
+      load_q(qa, 0);
+      for (int c = 0; c < kChunks; c += 2) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): chunk c (and earlier LDS reads) have arrived
+        __builtin_amdgcn_sched_barrier(0);
+        load_q(qb, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        chunk(qa, c);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // chunk c + 1
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 2 < kChunks) load_q(qa, c + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        chunk(qb, c + 1);
       }
 #pragma unroll
       for (int i = 0; i < kPairs; ++i) {
@@ -247,19 +281,34 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     wave_lds_sync();
     const int n = (int)min(64u, last - c0);
     const float* vrow = vcol + (size_t)c0 * kLd;
-#pragma unroll 4
-    for (int j = 0; j < n; ++j) {
-      const float4 s4 = *reinterpret_cast<const float4*>(sbuf[w][j]);
-      const float4 v4 = *reinterpret_cast<const float4*>(vrow + (size_t)j * kLd);
-      const float s[kHeads] = {s4.x, s4.y, s4.z};
+    // The V rows of 8 keys are in flight while the previous 8 are used
+    // (rows past the chunk's end repeat its last one and are not used).
+    constexpr int kAhead = 8;
+    float4 vq[kAhead];
 #pragma unroll
-      for (int h = 0; h < kHeads; ++h) {
-        const float a0 = s[h] * v4.x, a1 = s[h] * v4.y, a2 = s[h] * v4.z, a3 = s[h] * v4.w;
-        acc[h][0] = acc[h][0] + a0;
-        acc[h][1] = acc[h][1] + a1;
-        acc[h][2] = acc[h][2] + a2;
-        acc[h][3] = acc[h][3] + a3;
+    for (int j = 0; j < kAhead; ++j) vq[j] = *reinterpret_cast<const float4*>(vrow + (size_t)min(j, n - 1) * kLd);
+    for (int j0 = 0; j0 < n; j0 += kAhead) {
+      float4 vn[kAhead];
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j)
+        vn[j] = *reinterpret_cast<const float4*>(vrow + (size_t)min(j0 + kAhead + j, n - 1) * kLd);
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) {
+        if (j0 + j >= n) break;  // uniform
+        const float4 s4 = *reinterpret_cast<const float4*>(sbuf[w][j0 + j]);
+        const float4 v4 = vq[j];
+        const float s[kHeads] = {s4.x, s4.y, s4.z};
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h) {
+          const float a0 = s[h] * v4.x, a1 = s[h] * v4.y, a2 = s[h] * v4.z, a3 = s[h] * v4.w;
+          acc[h][0] = acc[h][0] + a0;
+          acc[h][1] = acc[h][1] + a1;
+          acc[h][2] = acc[h][2] + a2;
+          acc[h][3] = acc[h][3] + a3;
+        }
       }
+#pragma unroll
+      for (int j = 0; j < kAhead; ++j) vq[j] = vn[j];
     }
     wave_lds_sync();
   }

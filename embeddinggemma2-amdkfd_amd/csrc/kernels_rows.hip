@@ -448,12 +448,13 @@ hipError_t launch_residual_norm_quant(float* x, const float* h, const float* pos
 }
 
 // The restated libm functions (eg2_libm.hpp) on n floats, for comparison
-// with the host's: e[i] = expf(x[i]), t[i] = tanhf(x[i]).
+// with the host's: e[i] = expf(x[i]), t[i] = tanhf(x[i]) in the branch-free
+// form the GELU uses.
 __global__ void __launch_bounds__(256)
 libm_eval_kernel(const float* __restrict__ x, unsigned n, float* __restrict__ e, float* __restrict__ t) {
   for (unsigned i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
     e[i] = libm::expf(x[i]);
-    t[i] = libm::tanhf(x[i]);
+    t[i] = libm::tanhf_flat(x[i]);
   }
 }
 

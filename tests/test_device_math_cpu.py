@@ -10,7 +10,8 @@ instead of library calls (CPU only; the GPU tests check the kernels).
   adopted; here every float in [0.5, 1024) and a stride over all of them,
   in C so that fmaf is the real fused operation).
 - The host libm's expf and tanhf restated (eg2_libm.hpp: fdlibm's tanhf
-  and expm1f, the table method of glibc's expf): the header, built for the
+  and expm1f, and tanhf's branch-free form, the table method of glibc's
+  expf): the header, built for the
   host with g++, equals the host's libm on every 61st float bit pattern
   and every 7th in the GELU's and the softmax's working ranges (an
   exhaustive 2^32 sweep of all three functions was run when they were
@@ -113,6 +114,7 @@ static unsigned long long sweep(uint64_t lo, uint64_t hi, uint64_t stride) {
         const float x = ffrom((uint32_t)u);
         if (std::isnan(x)) continue;
         bad[i] += fbits(::tanhf(x)) != fbits(eg2::libm::tanhf(x));
+        if (std::isfinite(x)) bad[i] += fbits(::tanhf(x)) != fbits(eg2::libm::tanhf_flat(x));
         bad[i] += fbits(::expm1f(x)) != fbits(eg2::libm::expm1f(x));
         bad[i] += fbits(::expf(x)) != fbits(eg2::libm::expf(x));
       }
