@@ -2,7 +2,7 @@
 // pointers; row counts are token rows of the packed wave. Q8_0 activations
 // are int8 row tiles (q8_tile_offset; buffers hold the rows rounded up to
 // 32) plus one float scale per 32-block stored transposed, [k/32][rows];
-// attention operands are split fp16 rows [hi | lo].
+// attention reads fp32 rows [q0 q1 q2 | k | v].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -64,5 +64,16 @@ AttentionCounts attention_counts(const size_t* offsets, size_t batch);
 bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCounts& cap, uint32_t* items,
                           uint32_t* tok, AttentionCounts* used);
 AttentionCounts attention_capacity(size_t tokens, size_t batch);
+
+// Workgroups of the scores kernel (two per CU), striding over the items.
+constexpr int kAttentionScoreGrid = 512;
+
+// launch_attention with the plan built on the device from the device
+// sequence bounds offsets[0..batch] (offsets[0] read as 0, offsets[batch]
+// as rows, the rest clamped into a non-decreasing list) and the plan and
+// scores kept in a static per-device array: no allocation. rows <= 2048,
+// rows % 4 == 0, batch <= 4096. Calls overlapping on one device race.
+hipError_t launch_attention_static(const float* qkv, const uint32_t* offsets, int batch, int window, int rows,
+                                   int8_t* cq, float* cd, hipStream_t st);
 
 }  // namespace eg2

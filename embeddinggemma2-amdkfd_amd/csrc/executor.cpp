@@ -42,7 +42,6 @@
 namespace {
 
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
-constexpr int kScoreGrid = 512;  // workgroups of the attention scores kernel (two per CU), striding over its items
 constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
@@ -540,7 +539,7 @@ void Backend::record_layers(Lane& ln, unsigned rows) {
     // operand rows, no unnormalised projection in HBM.
     launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
                                                          L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
-    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, kScoreGrid, ln.tok_d, L.window, n,
+    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionScoreGrid, ln.tok_d, L.window, n,
                                               ln.scores, ln.cq, ln.cd, s));
     gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the

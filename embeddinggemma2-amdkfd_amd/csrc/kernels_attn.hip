@@ -42,6 +42,7 @@
 // A sequence's keys, scores and context depend only on its own tokens, so
 // packing never changes a bit.
 #include <algorithm>
+#include <mutex>
 
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
@@ -58,7 +59,7 @@ constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 // Query tokens per scores work item: longer sequences take more queries per
 // staged K block (fewer restagings); shorter ones fewer (more items to
 // spread over the CUs). A function of the length alone.
-static inline size_t query_chunk(size_t len) { return len <= 128 ? 8 : (len <= 512 ? 16 : 32); }
+__host__ __device__ inline size_t query_chunk(size_t len) { return len <= 128 ? 8 : (len <= 512 ? 16 : 32); }
 
 // Key range of query token t in its sequence [lo, hi) (kernels.c:330-336
 // in packed coordinates): the sequence, or |t - kt| <= window/2.
@@ -397,6 +398,171 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
   hipLaunchKernelGGL(attention_context_kernel, dim3(rows / 4), dim3(256), 0, st, qkv, scores,
                      reinterpret_cast<const uint4*>(tok), window, rows, cq, cd);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- allocation-free form
+//
+// launch_attention_static keeps its plan and scores in `scratch`, a
+// file-scope device array (one copy per GPU, alive until the process
+// ends), and builds the plan on the device from device offsets, so a call
+// allocates nothing. Layout: [item count | pad to 256 B][token records,
+// 16 B x kStaticRows][work items, 32 B x kStaticItems][scores, 3 x
+// kStaticRows^2 floats]. Any packing of at most kStaticRows rows into at
+// most kStaticBatch sequences fits (the bounds of attention_capacity).
+// Nothing in it has to start at zero: the plan kernel writes the count and
+// every record the other two kernels read, and the context kernel reads
+// only scores the scores kernel wrote in the same call. Calls that overlap
+// on one GPU share the array and race.
+
+constexpr size_t kStaticRows = 2048, kStaticBatch = 4096;
+constexpr size_t kStaticItems = kStaticRows * kStaticRows / 512 + 9 * kStaticRows / 64 + kStaticBatch + 1;
+constexpr size_t kStaticTokOff = 256;
+constexpr size_t kStaticItemsOff = kStaticTokOff + 16 * kStaticRows;
+constexpr size_t kStaticScoresOff = (kStaticItemsOff + 32 * kStaticItems + 255) / 256 * 256;
+constexpr size_t kStaticBytes = kStaticScoresOff + sizeof(float) * 3 * kStaticRows * kStaticRows;
+static_assert(kStaticItemsOff % 256 == 0, "sections stay 256-byte aligned");
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+constexpr int kPlanThreads = 1024;
+
+// Exclusive prefix (sum or max) of one value per thread over the workgroup,
+// Hillis-Steele through `tmp` (kPlanThreads entries); `total` gets the
+// reduction of all values.
+template <bool MAX>
+__device__ uint32_t plan_scan(uint32_t v, uint32_t* tmp, uint32_t& total) {
+  const int tid = threadIdx.x;
+  tmp[tid] = v;
+  __syncthreads();
+  for (int d = 1; d < kPlanThreads; d <<= 1) {
+    const uint32_t o = tid >= d ? tmp[tid - d] : 0u;
+    __syncthreads();
+    if (tid >= d) tmp[tid] = MAX ? max(tmp[tid], o) : tmp[tid] + o;
+    __syncthreads();
+  }
+  const uint32_t excl = MAX ? (tid > 0 ? tmp[tid - 1] : 0u) : tmp[tid] - v;
+  total = tmp[kPlanThreads - 1];
+  __syncthreads();  // tmp is free for the next scan
+  return excl;
+}
+
+// Last index i in [0, n] with a[i] <= x for non-decreasing a with a[0] <= x.
+__device__ __forceinline__ int last_le(const uint32_t* a, int n, uint32_t x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a[mid] <= x) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// The plan of build_attention_plan, on the device, in the same order. The
+// offsets are read as sequence bounds with offsets[0] taken as 0,
+// offsets[batch] as rows, each bound clamped to rows and raised to the one
+// before it, so every row belongs to exactly one sequence and no record
+// can address outside the rows or the scores section whatever the offsets
+// hold. One workgroup of kPlanThreads; batch <= kStaticBatch.
+__global__ void __launch_bounds__(kPlanThreads)
+attention_plan_kernel(const uint32_t* __restrict__ offsets, int batch, int rows, uint32_t* __restrict__ count,
+                      uint4* __restrict__ tok, uint4* __restrict__ items) {
+  __shared__ uint32_t bound[kStaticBatch + 1], first_item[kStaticBatch + 1], first_score[kStaticBatch + 1];
+  __shared__ uint32_t tmp[kPlanThreads];
+  const int tid = threadIdx.x;
+  const int nb = batch + 1, seg = (nb + kPlanThreads - 1) / kPlanThreads;
+  const int b0 = min(tid * seg, nb), b1 = min(b0 + seg, nb);
+  // Bounds: clamp, then the running maximum over the whole list.
+  uint32_t run = 0;
+  for (int i = b0; i < b1; ++i) {
+    const uint32_t v = i == 0 ? 0u : (i == batch ? (uint32_t)rows : min(offsets[i], (uint32_t)rows));
+    run = max(run, v);
+    bound[i] = run;
+  }
+  uint32_t unused;
+  const uint32_t before = plan_scan<true>(b1 > b0 ? run : 0u, tmp, unused);
+  for (int i = b0; i < b1; ++i) bound[i] = max(bound[i], before);
+  __syncthreads();
+  // Items and score floats per sequence, and their exclusive prefixes.
+  const int s0 = min(tid * seg, batch), s1 = min(s0 + seg, batch);
+  uint32_t ni = 0, ns = 0;
+  for (int s = s0; s < s1; ++s) {
+    const uint32_t len = bound[s + 1] - bound[s], qc = (uint32_t)query_chunk(len);
+    first_item[s] = ni;
+    first_score[s] = ns;
+    ni += (len + kKeyBlock - 1) / kKeyBlock * ((len + qc - 1) / qc);
+    ns += 3 * len * len;
+  }
+  uint32_t total_items, total_scores;
+  const uint32_t ibase = plan_scan<false>(ni, tmp, total_items);
+  const uint32_t sbase = plan_scan<false>(ns, tmp, total_scores);
+  for (int s = s0; s < s1; ++s) {
+    first_item[s] += ibase;
+    first_score[s] += sbase;
+  }
+  if (tid == 0) {
+    first_item[batch] = total_items;
+    first_score[batch] = total_scores;
+    *count = total_items;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < total_items; i += kPlanThreads) {
+    const int s = last_le(first_item, batch, i);  // a sequence with items has first_item[s] < first_item[s + 1]
+    const uint32_t lo = bound[s], hi = bound[s + 1], len = hi - lo, qc = (uint32_t)query_chunk(len);
+    const uint32_t nq = (len + qc - 1) / qc, local = i - first_item[s];
+    const uint32_t k0 = lo + kKeyBlock * (local / nq), q = lo + qc * (local % nq);
+    items[2 * i] = make_uint4(lo, hi, k0, q);
+    items[2 * i + 1] = make_uint4(min(hi, q + qc), first_score[s], 0u, 0u);
+  }
+  for (uint32_t t = tid; t < (uint32_t)rows; t += kPlanThreads) {
+    const int s = last_le(bound, batch, t);  // bound[s] <= t < bound[s + 1]
+    tok[t] = make_uint4(bound[s], bound[s + 1], first_score[s], 0u);
+  }
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up once per
+// device. (The array's name in host code is not a device address.)
+hipError_t static_scratch(unsigned char** out) {
+  static std::mutex mu;
+  static void* ptr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    ptr[dev] = p;
+  }
+  *out = static_cast<unsigned char*>(ptr[dev]);
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_attention_static(const float* qkv, const uint32_t* offsets, int batch, int window, int rows,
+                                   int8_t* cq, float* cd, hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || (size_t)rows > kStaticRows || batch <= 0 || (size_t)batch > kStaticBatch ||
+      window < 0)
+    return hipErrorInvalidValue;
+  unsigned char* base = nullptr;
+  hipError_t e = static_scratch(&base);
+  if (e != hipSuccess) return e;
+  uint32_t* count = reinterpret_cast<uint32_t*>(base);
+  uint32_t* tok = reinterpret_cast<uint32_t*>(base + kStaticTokOff);
+  uint32_t* items = reinterpret_cast<uint32_t*>(base + kStaticItemsOff);
+  float* scores = reinterpret_cast<float*>(base + kStaticScoresOff);
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, batch, rows, count,
+                     reinterpret_cast<uint4*>(tok), reinterpret_cast<uint4*>(items));
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_attention(qkv, items, count, kAttentionScoreGrid, tok, window, rows, scores, cq, cd, st);
 }
 
 }  // namespace eg2

@@ -75,6 +75,15 @@ int eg2_hip_attention(const float* qkv, const uint32_t* items, const uint32_t* i
                                     as_stream(stream)));
 }
 
+int eg2_hip_attention_static(const float* qkv, const uint32_t* offsets, unsigned batch, unsigned window,
+                             unsigned rows, int8_t* cq, float* cd, void* stream) {
+  if (!qkv || !offsets || !cq || !cd || rows == 0 || rows % 4 != 0 || rows > EG2_ATTENTION_STATIC_ROWS ||
+      batch == 0 || batch > EG2_ATTENTION_STATIC_BATCH || window > 4096u)
+    return kInvalid;
+  return code(eg2::launch_attention_static(qkv, offsets, (int)batch, (int)window, (int)rows, cq, cd,
+                                           as_stream(stream)));
+}
+
 int eg2_attention_plan(const size_t* offsets, size_t batch, size_t items_cap, size_t scores_cap, uint32_t* items,
                        uint32_t* tok, size_t* counts) {
   if (!offsets || !items || !tok || !counts) return -1;

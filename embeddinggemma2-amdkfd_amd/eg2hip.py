@@ -111,6 +111,7 @@ SIGNATURES = {
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u, _vp]),
     "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_hip_attention_static": (C.c_int, [_vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
     "eg2_attention_plan": (C.c_int, [C.POINTER(C.c_size_t), C.c_size_t, C.c_size_t, C.c_size_t, _vp, _vp,
                                      C.POINTER(C.c_size_t)]),
     "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -625,6 +626,20 @@ class ops:
         check(lib().eg2_hip_attention(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID,
                                       cls._p(plan.tok), window, qkv.shape[0], cls._p(plan.scores), cls._p(cq),
                                       cls._p(cd), cls._stream()), "attention")
+
+    STATIC_ROWS, STATIC_BATCH = 2048, 4096  # EG2_ATTENTION_STATIC_ROWS / _BATCH
+
+    @classmethod
+    def attention_static(cls, qkv, offsets_d, window, cq, cd):
+        """attention() through the allocation-free entry point: offsets_d is
+        a device uint32/int32 tensor of the batch + 1 sequence bounds; the
+        plan is built on the device into the library's static array."""
+        rows, batch = qkv.shape[0], offsets_d.numel() - 1
+        if rows > cls.STATIC_ROWS or batch > cls.STATIC_BATCH or batch < 1 or rows % 4:
+            raise ValueError(f"attention_static: rows {rows} (at most {cls.STATIC_ROWS}, a multiple of 4) and "
+                             f"batch {batch} (1 to {cls.STATIC_BATCH}) exceed the static scratch's limits")
+        check(lib().eg2_hip_attention_static(cls._p(qkv), cls._p(offsets_d), batch, window, rows, cls._p(cq),
+                                             cls._p(cd), cls._stream()), "attention_static")
 
     @classmethod
     def gelu_quant(cls, gu, gq, gd):

@@ -75,6 +75,25 @@ int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *i
                       const uint32_t *tok, unsigned window, unsigned rows, float *scores, int8_t *cq, float *cd,
                       void *stream);
 
+/* eg2_hip_attention without allocation. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc). The work plan is built on the device from the device
+ * sequence bounds offsets[0..batch] (uint32; offsets[0] is read as 0 and
+ * offsets[batch] as rows, every row must belong to a sequence, e.g. a
+ * padding one), and the plan and scores live in a static array of this
+ * library, one per GPU, of 48.4 MiB, held until the process ends. The
+ * call allocates nothing; it rejects (hipErrorInvalidValue, nothing
+ * launched) rows above EG2_ATTENTION_STATIC_ROWS, batch above
+ * EG2_ATTENTION_STATIC_BATCH or rows % 4 != 0. The stream must belong to
+ * the current device. Calls overlapping on one GPU share its array and
+ * race; calls in one stream are ordered. Results are bit-identical to
+ * eg2_hip_attention's. */
+#define EG2_ATTENTION_STATIC_ROWS 2048u
+#define EG2_ATTENTION_STATIC_BATCH 4096u
+int eg2_hip_attention_static(const float *qkv, const uint32_t *offsets, unsigned batch, unsigned window,
+                             unsigned rows, int8_t *cq, float *cd, void *stream);
+
 /* Host: the plan of eg2_hip_attention for the sequences [offsets[s],
  * offsets[s+1]): the scores kernel's work items (8 uint32 each: sequence
  * start, end, first key of a 64-key block, first query, end of the
