@@ -1,19 +1,40 @@
-// The reference's operator set (kernels/abi.h records, kernels/eg2.c kernel
-// names and launch geometry) as gfx950 kernels.
+// The operator set of the reference's by-name kernel interface (the
+// kernels/abi.h records, the kernel names and launch geometry of
+// kernels/eg2.c) on this library's own gfx950 designs.
 //
 // Each kernel takes its record by value, so its kernarg segment has the
 // record's layout and a code object built from this file can be dispatched
-// by symbol name ("eg2_mm.kd", ...) with the same records, grids and
+// by symbol name ("eg2_mm64x64.kd", ...) with the same records, grids and
 // workgroup sizes the reference executor uses (src/gemma2_kfd.cpp:160-165,
-// 248-336) and its operator test uses (tests/kernels.cpp:36-137).
+// 248-336) and its operator test uses (tests/kernels.cpp:36-137). The
+// results meet that test's tolerances (2e-5 absolute against exact
+// references; 2e-6 between a fused operator and its unfused sequence); they
+// are not the reference kernels' bits.
 //
-// Per output element the arithmetic is the reference kernel's: the same
-// operations in the same order with the same roundings, including the fused
-// multiply-adds its compiler forms under the default -ffp-contract=on
-// (written out here as fmaf), the hardware v_rsq_f32 / v_exp_f32 the
-// reference calls through __builtin_amdgcn_rsqf / exp2f, correctly rounded
-// division, and the xor-butterfly wave sum. The projection kernels add the
-// same zero padding of the K loop (k rounded up to the variant's step).
+// Designs:
+//  - projections (eg2_mm*): fp32 MFMA (v_mfma_f32_16x16x4f32) on LDS-staged
+//    32-deep K slices of the activations and of the weights decoded to fp32
+//    (F32, F16, BF16 or Q8_0 blocks over the flattened matrix), zero-padded
+//    past k. The MFMA's k index is a permutation of the slice chosen so that
+//    each lane reads contiguous float4s of its row: lane group g (lanes
+//    16g .. 16g+15) feeds slice elements g*KW/4 .. (g+1)*KW/4 - 1, one per
+//    MFMA. The 16x16 tile splits the slice over its four waves and adds
+//    their partial tiles at the end; the wider tiles give each wave its own
+//    16x16 blocks.
+//  - attention: keys in chunks of 64, one per lane: every lane computes its
+//    key's whole dot product against q (broadcast from LDS), so a chunk
+//    costs one wave max and one wave sum instead of one reduction per key;
+//    then the softmax weights of the chunk (exp through the host libm's
+//    expf restated in eg2_libm.hpp, rescaled by the running maximum between
+//    chunks) go through LDS to the context, where lanes own dimensions.
+//  - row operators (norm, norm_residual, norm_rope): one wave per row with
+//    the row held in registers as float4s (a single read of the row), the
+//    sum of squares reduced by DPP within 16-lane rows and a 4-way add
+//    across them, correctly rounded division and square root. The fused
+//    forms share the helpers of the unfused ones, so fused = unfused.
+//  - element-wise operators (saxpy, gathers, rope, element, pool): one
+//    element per work-item, as the launch contract gives; GELU is the
+//    tanh form with the host libm's tanhf restated (eg2_device.hpp).
 //
 // Launch contract (grid counted in workgroups, as the reference counts it):
 //   eg2_saxpy, eg2_gather, eg2_rope, eg2_element, eg2_pool, eg2_gather768:
@@ -32,268 +53,441 @@
 #include <stdint.h>
 
 #include "abi.h"
+#include "eg2_device.hpp"
 
 namespace {
 
-constexpr unsigned kWave = 64;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ unsigned flat_index() { return threadIdx.x + blockIdx.x * blockDim.x; }
 
-// GGML element decode of the reference's weight() (kernels/eg2.c:9-17):
-// 1 F16, 0 F32, 30 BF16; every other id is read as Q8_0 (34-byte blocks of a
-// little-endian fp16 scale and 32 int8 values, blocks running over the
-// flattened matrix). The Q8_0 product fp16(d) * q is exact in fp32.
-__device__ __forceinline__ float decode_weight(const void* w, unsigned i, unsigned type) {
-  if (type == 1) return (float)static_cast<const _Float16*>(w)[i];
-  if (type == 0) return static_cast<const float*>(w)[i];
-  if (type == 30) return __uint_as_float((uint32_t)static_cast<const uint16_t*>(w)[i] << 16);
-  const unsigned char* b = static_cast<const unsigned char*>(w) + (size_t)(i / 32) * 34;
-  const uint16_t bits = (uint16_t)(b[0] | (b[1] << 8));
-  const float d = (float)__builtin_bit_cast(_Float16, bits);
-  return d * (float)(int)reinterpret_cast<const signed char*>(b + 2)[i % 32];
-}
-
-// Xor-butterfly sum over the 64 lanes; every lane ends with the same value.
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int s = kWave / 2; s > 0; s >>= 1) x = x + __shfl_xor(x, s, kWave);
-  return x;
-}
-
-__device__ __forceinline__ float exp_e(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-
-// gelu_tanh as x / (1 + e^(-2u)), u = sqrt(2/pi) (x + 0.044715 x^3)
-// (kernels/eg2.c:25-29); the inner x + c*x*x*x is one fused multiply-add.
-__device__ __forceinline__ float gelu_exp(float x) {
-  const float cube = (0.044715f * x) * x;
-  const float u = 0.7978845608028654f * fmaf(cube, x, x);
-  return x / (1.0f + exp_e(-2.0f * u));
-}
-
-// Sum of squares of row[lane + 64 j] * pre (pre = 1: the raw values), one
-// fused multiply-add per term when FUSED, then the wave sum.
-template <bool FUSED>
-__device__ __forceinline__ float row_sum_squares(const float* row, unsigned d, float pre, unsigned lane) {
-  float ss = 0.0f;
-  for (unsigned z = lane; z < d; z += kWave) {
-    const float v = row[z] * pre;
-    if constexpr (FUSED) {
-      ss = fmaf(v, v, ss);
-    } else {
-      const float sq = v * v;
-      ss = ss + sq;
+// Element i of a GGML-typed weight matrix (type 0 F32, 1 F16, 30 BF16,
+// otherwise Q8_0: 34-byte blocks of a little-endian fp16 scale and 32 int8
+// values, running over the flattened matrix), as fp32. The Q8_0 value
+// fp16(d) * q is exact in fp32.
+__device__ __forceinline__ float weight_at(const void* w, size_t i, unsigned type) {
+  switch (type) {
+    case 0:
+      return static_cast<const float*>(w)[i];
+    case 1:
+      return eg2::fp16_bits_to_fp32(static_cast<const uint16_t*>(w)[i]);
+    case 30:
+      return __uint_as_float((uint32_t)static_cast<const uint16_t*>(w)[i] << 16);
+    default: {
+      const unsigned char* blk = static_cast<const unsigned char*>(w) + (i >> 5) * 34;
+      const float d = eg2::fp16_bits_to_fp32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+      return d * (float)reinterpret_cast<const signed char*>(blk + 2)[i & 31];
     }
   }
-  return wave_sum(ss);
 }
 
-__device__ __forceinline__ float rms_inverse(float ss, unsigned d) {
-  return __builtin_amdgcn_rsqf(ss / (float)d + 1.0e-6f);
-}
+// ------------------------------------------------------------ projections
 
-// Projection tile: TH x TW outputs per 256-thread workgroup, K staged
-// through LDS STEP columns at a time (zero-padded past k, as the reference
-// variants pad). Each output accumulates fmaf(x, w, acc) in ascending k.
-template <int TH, int TW, int STEP>
-__device__ void mm_tile(const EgMM& p) {
-  constexpr int RI = TH / 16, CJ = TW / 16;
-  __shared__ float xs[TH][STEP + 1];
-  __shared__ float ws[TW][STEP + 1];
-  const unsigned tid = threadIdx.x, r = tid / 16, c = tid % 16;
+constexpr int kSlice = 32;           // K values per LDS stage
+constexpr int kPitch = kSlice + 4;   // floats per staged row
+
+// out[n x m] = x[n x k] . W[m x k]^T for a TH x TW tile per 256-thread
+// workgroup (4 waves).
+template <int TH, int TW>
+__device__ void mm_mfma(const EgMM& p) {
+  static_assert((TH == 16 && (TW == 16 || TW == 64)) || (TH == 64 && TW == 64), "tile shapes of the contract");
+  __shared__ __align__(16) float xs[TH * kPitch];
+  __shared__ __align__(16) float ws[TW * kPitch];
+  __shared__ __align__(16) floatx4 part[(TH == 16 && TW == 16) ? 3 * 64 : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
   const unsigned row0 = blockIdx.y * TH, col0 = blockIdx.x * TW;
-  float acc[RI][CJ];
+
+  // Wave geometry: row blocks (16 rows) and column blocks (16 columns) it
+  // owns, and the part of each slice it reads.
+  constexpr bool kSplit = TH == 16 && TW == 16;  // the four waves split each slice
+  constexpr int RB = TH == 64 ? 2 : 1, CB = TH == 64 ? 2 : 1;
+  constexpr int KW = kSplit ? kSlice / 4 : kSlice;  // slice values per wave
+  constexpr int PER = KW / 4;                       // values per lane group = MFMAs per slice
+  const int rbase = TH == 64 ? 32 * (wave >> 1) : 0;
+  const int cbase = TH == 64 ? 32 * (wave & 1) : (TW == 64 ? 16 * wave : 0);
+  const int kbase = kSplit ? KW * wave : 0;
+
+  floatx4 acc[RB][CB];
 #pragma unroll
-  for (int i = 0; i < RI; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int j = 0; j < CJ; ++j) acc[i][j] = 0.0f;
-  for (unsigned base = 0; base < p.k; base += STEP) {
-    for (unsigned idx = tid; idx < (unsigned)(TH * STEP); idx += 256) {
-      const unsigned rr = idx / STEP, kk = idx % STEP, row = row0 + rr;
-      xs[rr][kk] = row < p.n && base + kk < p.k ? p.x[(size_t)row * p.k + base + kk] : 0.0f;
+    for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (unsigned base = 0; base < p.k; base += kSlice) {
+    for (int idx = tid; idx < TH * kSlice; idx += 256) {
+      const int rr = idx / kSlice, kk = idx % kSlice;
+      const unsigned row = row0 + rr, kx = base + kk;
+      xs[rr * kPitch + kk] = row < p.n && kx < p.k ? p.x[(size_t)row * p.k + kx] : 0.0f;
     }
-    for (unsigned idx = tid; idx < (unsigned)(TW * STEP); idx += 256) {
-      const unsigned cc = idx / STEP, kk = idx % STEP, col = col0 + cc;
-      ws[cc][kk] = col < p.m && base + kk < p.k ? decode_weight(p.weight, col * p.k + base + kk, p.type) : 0.0f;
+    for (int idx = tid; idx < TW * kSlice; idx += 256) {
+      const int cc = idx / kSlice, kk = idx % kSlice;
+      const unsigned col = col0 + cc, kx = base + kk;
+      ws[cc * kPitch + kk] = col < p.m && kx < p.k ? weight_at(p.weight, (size_t)col * p.k + kx, p.type) : 0.0f;
     }
     __syncthreads();
-#pragma unroll 4
-    for (int j = 0; j < STEP; ++j) {
+    float a[RB][PER], b[CB][PER];
 #pragma unroll
-      for (int i = 0; i < RI; ++i) {
-        const float xv = xs[r + 16 * i][j];
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int o = 0; o < CJ; ++o) acc[i][o] = fmaf(xv, ws[c + 16 * o][j], acc[i][o]);
-      }
-    }
+      for (int e = 0; e < PER; ++e) a[i][e] = xs[(rbase + 16 * i + r16) * kPitch + kbase + g * PER + e];
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) b[j][e] = ws[(cbase + 16 * j + r16) * kPitch + kbase + g * PER + e];
+#pragma unroll
+    for (int e = 0; e < PER; ++e)
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
     __syncthreads();
   }
+
+  if constexpr (kSplit) {
+    // Waves 1-3 hand their partial tiles to wave 0, which adds them in order.
+    if (wave > 0) part[(wave - 1) * 64 + lane] = acc[0][0];
+    __syncthreads();
+    if (wave > 0) return;
+    acc[0][0] = ((acc[0][0] + part[lane]) + part[64 + lane]) + part[128 + lane];
+  }
+  // MFMA 16x16 output: lane holds rows 4g .. 4g + 3 of column r16.
 #pragma unroll
-  for (int i = 0; i < RI; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int o = 0; o < CJ; ++o) {
-      const unsigned row = row0 + r + 16 * i, col = col0 + c + 16 * o;
-      if (row < p.n && col < p.m) p.out[(size_t)row * p.m + col] = acc[i][o];
-    }
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const unsigned row = row0 + rbase + 16 * i + 4 * g + v, col = col0 + cbase + 16 * j + r16;
+        if (row < p.n && col < p.m) p.out[(size_t)row * p.m + col] = acc[i][j][v];
+      }
 }
 
-// Streaming-softmax attention of one (token, query head) per wave
-// (kernels/eg2.c:145-170): keys [bounds[2t], bounds[2t+1]) clipped to
-// |t - s| <= window when window > 0; q row stride D, K/V row stride KV_STRIDE
-// with the head's KV block at kh * D. Lane owns elements lane + 64 j.
-template <int D, int HEADS, int KV_STRIDE>
-__device__ void attention_row(const EgAttention& p, unsigned kh_div) {
-  constexpr int J = D / kWave;
+// -------------------------------------------------------------- row sums
+
+// Sum over the 64 lanes: DPP exchanges within each 16-lane row (lanes
+// i^1, i^2, then the mirrored half-row and row), then the four row totals
+// added as (r0 + r1) + (r2 + r3). Wave-uniform result.
+__device__ __forceinline__ float dpp_wave_sum(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {
+      case 0:
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+      case 1:
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+      case 2:
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+      default:
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+    }
+  };
+  v = v + dpp(v, 0);
+  v = v + dpp(v, 1);
+  v = v + dpp(v, 2);
+  v = v + dpp(v, 3);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float dpp_wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// A row of d floats held by one wave: float4 chunks c = lane + 64 j
+// (elements 4c .. 4c + 3) for j < kRowChunks when d % 4 == 0 and d <=
+// 256 kRowChunks; other widths are read element-wise in two passes.
+constexpr int kRowChunks = 4;
+
+struct Row {
+  floatx4 v[kRowChunks];
+};
+
+__device__ __forceinline__ bool row_in_registers(unsigned d) { return d % 4 == 0 && d <= 256u * kRowChunks; }
+
+__device__ __forceinline__ Row load_row(const float* x, unsigned d, unsigned lane) {
+  Row r;
+#pragma unroll
+  for (int j = 0; j < kRowChunks; ++j) {
+    const unsigned c = lane + 64u * j;
+    r.v[j] = 4 * c < d ? *reinterpret_cast<const floatx4*>(x + 4 * c) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  return r;
+}
+
+// 1 / sqrt(mean((x * pre)^2) + 1e-6) of a row.
+__device__ __forceinline__ float row_inverse_rms(const float* x, unsigned d, float pre, unsigned lane, const Row* r) {
+  float ss = 0.0f;
+  if (r) {
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = r->v[j][e] * pre;
+        ss = __builtin_fmaf(v, v, ss);
+      }
+  } else {
+    for (unsigned z = lane; z < d; z += 64) {
+      const float v = x[z] * pre;
+      ss = __builtin_fmaf(v, v, ss);
+    }
+  }
+  return eg2::rms_inverse(dpp_wave_sum(ss), (int)d, 1.0e-6f);
+}
+
+// The normalized value of element z: ((x * pre) * inv) * w.
+__device__ __forceinline__ float normed(float x, float pre, float inv, const float* w, unsigned z) {
+  const float v = (x * pre) * inv;
+  return w ? v * w[z] : v;
+}
+
+// NeoX rotation of the pair (a, b) by (c, s).
+__device__ __forceinline__ void rotate(float a, float b, float c, float s, float& ra, float& rb) {
+  const float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+  ra = ac - bs;
+  rb = as + bc;
+}
+
+// --------------------------------------------------------------- attention
+
+// One wave per (token t, query head h): out = softmax(q . K^T) V over the
+// keys [bounds[2t], bounds[2t+1]) clipped to |t - s| <= window (window >
+// 0). q rows of D floats per (t, h); K/V rows of KVS floats with head h's
+// KV block at (h / GROUP) * D.
+template <int D, int HEADS, int KVS, int GROUP>
+__device__ void attention_chunked(const EgAttention& p) {
+  static_assert(D % 256 == 0, "lanes own float4s of the context");
+  constexpr int CV = D / 256;  // float4 of the context per lane
+  __shared__ __align__(16) floatx4 qs[D / 4];
+  __shared__ float ps[64];
   const unsigned row = blockIdx.x, lane = threadIdx.x;
-  const unsigned t = row / HEADS, h = row % HEADS, kh = h / kh_div;
+  const unsigned t = row / HEADS, h = row % HEADS, kv = (h / GROUP) * D;
   if (t >= p.n) return;
   unsigned lo = p.bounds[2 * t], hi = p.bounds[2 * t + 1];
-  if (p.window && t > p.window && lo < t - p.window) lo = t - p.window;
-  if (p.window && hi > t + p.window + 1) hi = t + p.window + 1;
-  float q[J], acc[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    q[j] = p.q[(size_t)row * D + lane + j * kWave];
-    acc[j] = 0.0f;
+  if (p.window) {
+    if (t > p.window) lo = max(lo, t - p.window);
+    hi = min(hi, t + p.window + 1);
   }
+  for (unsigned c = lane; c < D / 4; c += 64) qs[c] = reinterpret_cast<const floatx4*>(p.q + (size_t)row * D)[c];
+  __syncthreads();
   float run_max = -__builtin_inff(), den = 0.0f;
-  for (unsigned s = lo; s < hi; ++s) {
-    const float* krow = p.k + (size_t)s * KV_STRIDE + kh * D;
-    const float* vrow = p.v + (size_t)s * KV_STRIDE + kh * D;
-    float vv[J];
-    float dot = 0.0f;
+  floatx4 acc[CV];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      dot = fmaf(q[j], krow[lane + j * kWave], dot);
-      vv[j] = vrow[lane + j * kWave];
+  for (int u = 0; u < CV; ++u) acc[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (unsigned c0 = lo; c0 < hi; c0 += 64) {
+    const unsigned key = c0 + lane;
+    float score = -__builtin_inff();
+    if (key < hi) {
+      const floatx4* kr = reinterpret_cast<const floatx4*>(p.k + (size_t)key * KVS + kv);
+      floatx4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+      for (int c = 0; c < D / 4; ++c) {
+        const floatx4 k4 = kr[c], q4 = qs[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s4[e] = __builtin_fmaf(q4[e], k4[e], s4[e]);
+      }
+      score = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     }
-    dot = wave_sum(dot);
-    const float next = fmaxf(run_max, dot);
-    const float alpha = exp_e(run_max - next), beta = exp_e(dot - next);
-    den = fmaf(den, alpha, beta);
+    const float next = fmaxf(run_max, dpp_wave_max(score));  // finite: the chunk has a key
+    const float alpha = eg2::libm::expf(run_max - next);     // 0 for the first chunk
+    const float pk = key < hi ? eg2::libm::expf(score - next) : 0.0f;
+    den = den * alpha + dpp_wave_sum(pk);
+    ps[lane] = pk;
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < J; ++j) acc[j] = fmaf(acc[j], alpha, beta * vv[j]);
+    for (int u = 0; u < CV; ++u) acc[u] = acc[u] * alpha;
+    const unsigned count = min(64u, hi - c0);
+    const float* vbase = p.v + (size_t)c0 * KVS + kv + 4 * lane;
+    for (unsigned j = 0; j < count; ++j) {
+      const float w = ps[j];
+#pragma unroll
+      for (int u = 0; u < CV; ++u) {
+        const floatx4 v4 = *reinterpret_cast<const floatx4*>(vbase + (size_t)j * KVS + 256 * u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[u][e] = __builtin_fmaf(w, v4[e], acc[u][e]);
+      }
+    }
+    __syncthreads();  // ps is rewritten by the next chunk
     run_max = next;
   }
+  const float inv = hi > lo ? 1.0f / den : 0.0f;
 #pragma unroll
-  for (int j = 0; j < J; ++j) p.out[(size_t)row * D + lane + j * kWave] = acc[j] / den;
+  for (int u = 0; u < CV; ++u)
+    *reinterpret_cast<floatx4*>(p.out + (size_t)row * D + 4 * lane + 256 * u) = acc[u] * inv;
 }
 
 }  // namespace
 
-// kernels/eg2.c:31-34: y = a*x + y (one fused multiply-add).
+// y = a x + y.
 extern "C" __global__ void eg2_saxpy(float* y, const float* x, float a, unsigned n) {
   const unsigned i = flat_index();
-  if (i < n) y[i] = fmaf(a, x[i], y[i]);
+  if (i < n) y[i] = __builtin_fmaf(a, x[i], y[i]);
 }
 
-// kernels/eg2.c:36-39: rows of 512 values, (fp16(d) * q) * sqrt(512).
+// Rows of 512 values of a Q8_0 table: (fp16(d) * q) * sqrt(512)
+// (kernels/eg2.c:36-39 semantics).
 extern "C" __global__ void eg2_gather(EgGather p) {
   const unsigned i = flat_index();
-  if (i < p.n * 512u) p.out[i] = decode_weight(p.weight, (unsigned)p.ids[i / 512] * 512u + i % 512, 8) * 22.62741699796952f;
+  if (i >= p.n * 512u) return;
+  const unsigned r = i >> 9, z = i & 511;
+  p.out[i] = weight_at(p.weight, (size_t)p.ids[r] * 512 + z, 8) * 22.62741699796952f;
 }
 
-// Width-768 gather with the order of the 768-wide CPU path
-// (engine.c:288-295, quants.c:67,86-88): (fp16(d) * sqrt(768)) * q.
+// Rows of 768 values with the 768-wide CPU path's order (engine.c:288-295,
+// quants.c:67,86-88): (fp16(d) * sqrt(768)) * q.
 extern "C" __global__ void eg2_gather768(EgGather p) {
   const unsigned i = flat_index();
   if (i >= p.n * 768u) return;
-  const unsigned e = (unsigned)p.ids[i / 768] * 768u + i % 768;
-  const unsigned char* b = static_cast<const unsigned char*>(p.weight) + (size_t)(e / 32) * 34;
-  const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[0] | (b[1] << 8)));
-  p.out[i] = (d * 27.712812921102035f) * (float)(int)reinterpret_cast<const signed char*>(b + 2)[e % 32];
+  const unsigned r = i / 768u, z = i - 768u * r;
+  const unsigned char* blk = static_cast<const unsigned char*>(p.weight) + ((size_t)p.ids[r] * 24 + z / 32) * 34;
+  const float d = eg2::fp16_bits_to_fp32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  p.out[i] = (d * 27.712812921102035f) * (float)reinterpret_cast<const signed char*>(blk + 2)[z & 31];
 }
 
-// kernels/eg2.c:41-119: out[n x m] = x[n x k] . W[m x k]^T, four tilings.
-extern "C" __global__ void __launch_bounds__(256) eg2_mm(EgMM p) { mm_tile<16, 16, 16>(p); }
-extern "C" __global__ void __launch_bounds__(256) eg2_mm64(EgMM p) { mm_tile<16, 64, 32>(p); }
-extern "C" __global__ void __launch_bounds__(256) eg2_mm64x64(EgMM p) { mm_tile<64, 64, 32>(p); }
-extern "C" __global__ void __launch_bounds__(256) eg2_mmstep8(EgMM p) { mm_tile<64, 64, 8>(p); }
+// kernels/eg2.c:41-119 semantics, four tile shapes.
+extern "C" __global__ void __launch_bounds__(256) eg2_mm(EgMM p) { mm_mfma<16, 16>(p); }
+extern "C" __global__ void __launch_bounds__(256) eg2_mm64(EgMM p) { mm_mfma<16, 64>(p); }
+extern "C" __global__ void __launch_bounds__(256) eg2_mm64x64(EgMM p) { mm_mfma<64, 64>(p); }
+extern "C" __global__ void __launch_bounds__(256) eg2_mmstep8(EgMM p) { mm_mfma<64, 64>(p); }
 
-// kernels/eg2.c:121-133: out = ((x*scale) * inv) * w, inv = rsq(mean((x*scale)^2) + 1e-6);
-// weight may be NULL (= 1). In place (out == x) is valid.
+// out = ((x * scale) * inv) * w, inv = 1/sqrt(mean((x * scale)^2) + 1e-6);
+// w may be NULL (= 1); out == x is valid (kernels/eg2.c:121-133 semantics).
 extern "C" __global__ void __launch_bounds__(64) eg2_norm(EgNorm p) {
   const unsigned row = blockIdx.x, lane = threadIdx.x;
   if (row >= p.rows) return;
   const float* x = p.x + (size_t)row * p.d;
-  const float inv = rms_inverse(row_sum_squares<true>(x, p.d, p.scale, lane), p.d);
-  for (unsigned z = lane; z < p.d; z += kWave) {
-    const float v = (x[z] * p.scale) * inv;
-    p.out[(size_t)row * p.d + z] = v * (p.weight ? p.weight[z] : 1.0f);
+  float* out = p.out + (size_t)row * p.d;
+  if (row_in_registers(p.d)) {
+    const Row r = load_row(x, p.d, lane);
+    const float inv = row_inverse_rms(x, p.d, p.scale, lane, &r);
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+      const unsigned c = lane + 64u * j;
+      if (4 * c >= p.d) break;
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = normed(r.v[j][e], p.scale, inv, p.weight, 4 * c + e);
+      *reinterpret_cast<floatx4*>(out + 4 * c) = o;
+    }
+  } else {
+    const float inv = row_inverse_rms(x, p.d, p.scale, lane, nullptr);
+    for (unsigned z = lane; z < p.d; z += 64) out[z] = normed(x[z], p.scale, inv, p.weight, z);
   }
 }
 
-// kernels/eg2.c:135-143: NeoX rotation of pairs (z, z + d/2) with the table
-// row of token row/heads = [cos(d/2) | sin(d/2)].
+// NeoX rotation of pairs (z, z + d/2), table row of token row/heads =
+// [cos(d/2) | sin(d/2)] (kernels/eg2.c:135-143 semantics).
 extern "C" __global__ void eg2_rope(EgRope p) {
   const unsigned i = flat_index(), half = p.d / 2;
   if (i >= p.n * p.heads * half) return;
   const unsigned z = i % half, row = i / half, t = row / p.heads;
-  const float c = p.table[(size_t)t * p.d + z], s = p.table[(size_t)t * p.d + half + z];
+  const float* tab = p.table + (size_t)t * p.d;
   float* x = p.x + (size_t)row * p.d;
-  const float a = x[z], b = x[half + z];
-  x[z] = fmaf(a, c, -(b * s));
-  x[half + z] = fmaf(a, s, b * c);
+  rotate(x[z], x[half + z], tab[z], tab[half + z], x[z], x[half + z]);
 }
 
-// kernels/eg2.c:145-170: 4 query heads per token; d 256 reads KV head h/2
-// of two, d 512 the single KV head (K/V rows of 512 floats).
-extern "C" __global__ void __launch_bounds__(64) eg2_attention256(EgAttention p) { attention_row<256, 4, 512>(p, 2); }
-extern "C" __global__ void __launch_bounds__(64) eg2_attention512(EgAttention p) { attention_row<512, 4, 512>(p, 4); }
+// kernels/eg2.c:145-170 semantics: 4 query heads per token; d 256 reads KV
+// head h/2 of two, d 512 the single KV head (K/V rows of 512 floats).
+extern "C" __global__ void __launch_bounds__(64) eg2_attention256(EgAttention p) {
+  attention_chunked<256, 4, 512, 2>(p);
+}
+extern "C" __global__ void __launch_bounds__(64) eg2_attention512(EgAttention p) {
+  attention_chunked<512, 4, 512, 4>(p);
+}
 // 3 query heads sharing one KV head of 256 (K/V rows of 256 floats).
-extern "C" __global__ void __launch_bounds__(64) eg2_attention256x3(EgAttention p) { attention_row<256, 3, 256>(p, 3); }
+extern "C" __global__ void __launch_bounds__(64) eg2_attention256x3(EgAttention p) {
+  attention_chunked<256, 3, 256, 3>(p);
+}
 
-// kernels/eg2.c:172-179: mode 0 (x + other) * scale, 1 gelu(x) * other,
-// 2 gelu(x) * other[(i/512*24 + layer)*512 + i%512].
+// Mode 0: (x + other) * scale; 1: gelu(x) * other; 2: gelu(x) * the
+// per-layer gate other[(i/512 * 24 + layer) * 512 + i % 512]
+// (kernels/eg2.c:172-179 semantics). Both loads come before the mode
+// branch: with the x load inside a three-way branch, hipcc (ROCm 7.2, -O3)
+// left the mode-2 path's x address undefined.
 extern "C" __global__ void eg2_element(EgElement p) {
   const unsigned i = flat_index();
   if (i >= p.n) return;
-  if (p.mode == 0) {
-    p.out[i] = (p.x[i] + p.other[i]) * p.scale;
-  } else if (p.mode == 1) {
-    p.out[i] = gelu_exp(p.x[i]) * p.other[i];
-  } else {
-    p.out[i] = gelu_exp(p.x[i]) * p.other[((size_t)(i / 512) * 24 + p.layer) * 512 + i % 512];
-  }
+  const size_t o = p.mode == 2 ? ((size_t)(i >> 9) * 24 + p.layer) * 512 + (i & 511) : (size_t)i;
+  const float xv = p.x[i], ov = p.other[o];
+  p.out[i] = p.mode == 0 ? (xv + ov) * p.scale : eg2::gelu_mul(xv, ov);
 }
 
-// kernels/eg2.c:181-188: mean over rows [offsets[s], offsets[s+1]) of width 768.
+// Mean over rows [offsets[s], offsets[s+1]) of width 768, in row order
+// (kernels/eg2.c:181-188 semantics); four rows' loads in flight at a time.
 extern "C" __global__ void eg2_pool(EgPool p) {
-  const unsigned i = flat_index(), seq = i / 768, z = i % 768;
+  const unsigned i = flat_index(), seq = i / 768u, z = i - 768u * seq;
   if (seq >= p.batch) return;
   const unsigned lo = p.offsets[seq], hi = p.offsets[seq + 1];
+  const float* col = p.x + z;
   float sum = 0.0f;
-  for (unsigned t = lo; t < hi; ++t) sum = sum + p.x[(size_t)t * 768 + z];
+  unsigned t = lo;
+  for (; t + 4 <= hi; t += 4) {
+    const float a = col[(size_t)t * 768], b = col[(size_t)(t + 1) * 768];
+    const float c = col[(size_t)(t + 2) * 768], d = col[(size_t)(t + 3) * 768];
+    sum = sum + a;
+    sum = sum + b;
+    sum = sum + c;
+    sum = sum + d;
+  }
+  for (; t < hi; ++t) sum = sum + col[(size_t)t * 768];
   p.out[i] = sum / (float)(hi - lo);
 }
 
-// kernels/eg2.c:190-202: out = (out + (x*inv)*w) * scale, no fused operations.
+// out = (out + (x * inv) * w) * scale (kernels/eg2.c:190-202 semantics):
+// the normalized values of eg2_norm with scale 1, added to the residual.
 extern "C" __global__ void __launch_bounds__(64) eg2_norm_residual(EgNormResidual p) {
   const unsigned row = blockIdx.x, lane = threadIdx.x;
   if (row >= p.rows) return;
   const float* x = p.x + (size_t)row * p.d;
-  const float inv = rms_inverse(row_sum_squares<false>(x, p.d, 1.0f, lane), p.d);
-  for (unsigned z = lane; z < p.d; z += kWave) {
-    const size_t i = (size_t)row * p.d + z;
-    const float nv = (x[z] * inv) * p.weight[z];
-    p.out[i] = (p.out[i] + nv) * p.scale;
+  float* out = p.out + (size_t)row * p.d;
+  if (row_in_registers(p.d)) {
+    const Row r = load_row(x, p.d, lane);
+    const float inv = row_inverse_rms(x, p.d, 1.0f, lane, &r);
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+      const unsigned c = lane + 64u * j;
+      if (4 * c >= p.d) break;
+      floatx4 o = *reinterpret_cast<const floatx4*>(out + 4 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (o[e] + normed(r.v[j][e], 1.0f, inv, p.weight, 4 * c + e)) * p.scale;
+      *reinterpret_cast<floatx4*>(out + 4 * c) = o;
+    }
+  } else {
+    const float inv = row_inverse_rms(x, p.d, 1.0f, lane, nullptr);
+    for (unsigned z = lane; z < p.d; z += 64) out[z] = (out[z] + normed(x[z], 1.0f, inv, p.weight, z)) * p.scale;
   }
 }
 
-// kernels/eg2.c:204-217: per-row RMS with the row weight, then the NeoX
-// rotation with the table row of token row/heads; in place.
+// Per-row RMS with the row weight, then the NeoX rotation with the table
+// row of token row/heads, in place (kernels/eg2.c:204-217 semantics): the
+// normalized row goes through LDS so that each lane can take its pairs.
 extern "C" __global__ void __launch_bounds__(64) eg2_norm_rope(EgNormRope p) {
+  constexpr unsigned kMaxD = 4096;
+  __shared__ float nrow[kMaxD];
   const unsigned row = blockIdx.x, lane = threadIdx.x, half = p.d / 2;
-  if (row >= p.rows) return;
+  if (row >= p.rows || p.d > kMaxD) return;
   float* x = p.x + (size_t)row * p.d;
-  const float inv = rms_inverse(row_sum_squares<true>(x, p.d, 1.0f, lane), p.d);
-  const unsigned t = row / p.heads;
-  for (unsigned z = lane; z < half; z += kWave) {
-    const float a = (x[z] * inv) * p.weight[z];
-    const float b = (x[half + z] * inv) * p.weight[half + z];
-    const float c = p.table[(size_t)t * p.d + z], s = p.table[(size_t)t * p.d + half + z];
-    x[z] = fmaf(a, c, -(b * s));
-    x[half + z] = fmaf(a, s, b * c);
+  if (row_in_registers(p.d)) {
+    const Row r = load_row(x, p.d, lane);
+    const float inv = row_inverse_rms(x, p.d, 1.0f, lane, &r);
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+      const unsigned c = lane + 64u * j;
+      if (4 * c >= p.d) break;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nrow[4 * c + e] = normed(r.v[j][e], 1.0f, inv, p.weight, 4 * c + e);
+    }
+  } else {
+    const float inv = row_inverse_rms(x, p.d, 1.0f, lane, nullptr);
+    for (unsigned z = lane; z < p.d; z += 64) nrow[z] = normed(x[z], 1.0f, inv, p.weight, z);
   }
+  __syncthreads();
+  const float* tab = p.table + (size_t)(row / p.heads) * p.d;
+  for (unsigned z = lane; z < half; z += 64) rotate(nrow[z], nrow[half + z], tab[z], tab[half + z], x[z], x[half + z]);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -345,7 +539,7 @@ bool valid_norm_residual(const void* r) {
 }
 bool valid_norm_rope(const void* r) {
   const EgNormRope& p = as<EgNormRope>(r);
-  return p.x && p.weight && p.table && p.d > 0 && p.d % 2 == 0 && p.heads > 0;
+  return p.x && p.weight && p.table && p.d > 0 && p.d % 2 == 0 && p.d <= 4096 && p.heads > 0;
 }
 
 const OpEntry kOps[] = {

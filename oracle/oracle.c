@@ -614,23 +614,6 @@ int or_forward(const or_model *m, const int32_t *ids, const size_t *offsets, siz
     return 0;
 }
 
-/* kernels/eg2.c:41-119: every tiling accumulates fmaf(x, w, acc) over k in
- * ascending order, with zeros loaded past k up to the tiling's step. */
-void or_op_mm(const float *x, const float *w, uint32_t n, uint32_t k, uint32_t m, uint32_t step, float *out) {
-    const uint32_t kp = (k + step - 1) / step * step;
-    for (uint32_t r = 0; r < n; ++r) {
-        for (uint32_t c = 0; c < m; ++c) {
-            float acc = 0.0f;
-            for (uint32_t z = 0; z < kp; ++z) {
-                const float a = z < k ? x[(size_t)r * k + z] : 0.0f;
-                const float b = z < k ? w[(size_t)c * k + z] : 0.0f;
-                acc = fmaf(a, b, acc);
-            }
-            out[(size_t)r * m + c] = acc;
-        }
-    }
-}
-
 /* The host libm's expf and tanhf over an array (the functions the
  * reference calls at kernels.c:348 and :370), for comparing a device
  * restatement with them. */

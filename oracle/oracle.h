@@ -22,8 +22,6 @@
  *   or_layer_forward / or_forward: composition of the pinned functions in
  *       the order of engine.c:488-821, 1098-1135; pinned through a
  *       double-precision brute-force layer on tiny inputs (tolerance).
- *   or_op_mm (the operator-level fp32 projection): the exact-arithmetic
- *       cases of tests/kernels.cpp:57-80 and a float64 brute force.
  *   Dense head (dense_2, dense_3 on the mean pool, then L2): the reference
  *       describes it (EXTRACTION.md:178-181) but never implements it; its
  *       composition is pinned by a float64 brute force on tiny models that
@@ -85,14 +83,6 @@ void or_mean_pool_rms_l2(float *x, int32_t n_tokens, const float *w, float eps, 
 
 /* y[t*m + r] = sum_p float(dot_p) * d_w * d_x over the K/32 blocks, in block
  * order (gemma2.c:120-141). w: m rows of k/32 blocks; xq: n rows of k/32. */
-/* Operator-level projection of kernels/eg2.c:41-119 (eg2_mm, eg2_mm64,
- * eg2_mm64x64, eg2_mmstep8): out[r][c] = fmaf(x[r][z], w[c][z], acc) for z
- * ascending over k rounded up to `step` (16, 32, 32, 8), the padded terms
- * being fmaf(0, 0, acc). w is the decoded fp32 weight [m][k]. Pinned by the
- * exact-arithmetic cases of tests/kernels.cpp:57-80 and a brute-force
- * float64 sum (tests/test_oracle_math.py). */
-void or_op_mm(const float *x, const float *w, uint32_t n, uint32_t k, uint32_t m, uint32_t step, float *out);
-
 void or_gemm_q8_0(const or_block_q8_0 *w, const or_block_q8_0 *xq, int32_t n, int32_t k,
                   int32_t m, float *y, int32_t threads);
 

@@ -57,7 +57,6 @@ def _load_oracle():
         "or_mean_pool_rms": (None, [_f, C.c_int32, _f, C.c_float, _f]),
         "or_mean_pool_rms_l2": (None, [_f, C.c_int32, _f, C.c_float, _f]),
         "or_gemm_q8_0": (None, [_vp, _vp, C.c_int32, C.c_int32, C.c_int32, _f, C.c_int32]),
-        "or_op_mm": (None, [_f, _f, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f]),
         "or_layer_forward": (None, [_vp, C.c_float, _f, _i32, _vp, C.c_size_t, C.c_int32]),
         "or_forward": (C.c_int, [_vp, _i32, _vp, C.c_size_t, _f, C.c_int32]),
         "or_libm_eval": (None, [_f, C.c_size_t, _f, _f]),
@@ -146,17 +145,6 @@ def host_libm(name, x):
     e, t = np.empty_like(x), np.empty_like(x)
     oracle().or_libm_eval(fptr(x), x.size, fptr(e), fptr(t))
     return {"expf": e, "tanhf": t}[name]
-
-
-def op_mm(x, w, step):
-    """kernels/eg2.c:41-119 arithmetic: x fp32 [n,k], w decoded fp32 [m,k]."""
-    x = np.ascontiguousarray(x, np.float32)
-    w = np.ascontiguousarray(w, np.float32)
-    n, k = x.shape
-    m = w.shape[0]
-    out = np.zeros((n, m), np.float32)
-    oracle().or_op_mm(fptr(x), fptr(w), n, k, m, step, fptr(out))
-    return out
 
 
 def gemm_q8_0(w, xq, threads=8):

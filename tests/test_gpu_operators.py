@@ -1,17 +1,20 @@
 """The operator kernels that take the include/abi.h records
-(kernels_abi.hip), launched by name through eg2_op_launch with the grids and
-workgroup sizes of the reference's operator test, tests/kernels.cpp.
+(kernels_abi.hip: MFMA projections, chunked attention, register-row norms),
+launched by name through eg2_op_launch with the grids and workgroup sizes
+of the reference's operator test, tests/kernels.cpp, and once from the
+stand-alone code object through hipModuleLoad.
 
 Cases and tolerances follow tests/kernels.cpp:
   * projections (:57-80): four tilings x four weight types x n in
     {1, 17, 33, 65}, k 64, m 35, inputs whose every partial sum is exact, so
-    the check is bit-exact; plus random inputs against the oracle's
-    restatement of the same fmaf order (or_op_mm), bit-exact;
+    the check is bit-exact; plus random inputs over several K slices against
+    a float64 product, within 4e-6 of the sum of |x w|;
   * norm (:81-91) against a float64 sum of squares, 2e-5;
   * fused vs unfused (:92-113): norm_residual = norm + element(mode 0), and
     norm_rope = norm + rope, 2e-6;
   * attention (:114-137): GQA, two sequences, SWA window 1, against a
-    float64 softmax, 2e-5; plus the 3-query-head variant the same way.
+    float64 softmax, 2e-5; plus the 3-query-head variant the same way, with
+    sequences longer than one 64-key chunk.
 Also: the gathers and pooling bit-exact against float32 restatements,
 element modes 1/2 against float64 gelu_tanh, saxpy on exact inputs."""
 import math
@@ -105,17 +108,60 @@ def test_mm_exact_cases(eg2, gpu, variant, wtype):
 
 @pytest.mark.parametrize("variant", MM_VARIANTS, ids=[v[0] for v in MM_VARIANTS])
 @pytest.mark.parametrize("wtype", [0, 1, 8, 30])
-def test_mm_random_matches_fma_order(eg2, gpu, variant, wtype):
-    """Random inputs, k not a multiple of the step: bit-identical to the
-    sequential fmaf order (oracle or_op_mm)."""
-    name, width, height, step = variant
-    rng = np.random.default_rng(7 + wtype)
-    n, k, m = 37, 70, 67
+@pytest.mark.parametrize("shape", [(37, 70, 67), (130, 770, 200)])
+def test_mm_random_against_float64(eg2, gpu, variant, wtype, shape):
+    """Random inputs, k not a multiple of the 32-value slice, partial tiles
+    in both directions: within 4e-6 of sum |x w| of the float64 product of
+    the decoded weights (a wrong operand or output placement is off by O(1))."""
+    name, width, height, _ = variant
+    rng = np.random.default_rng(7 + wtype + shape[1])
+    n, k, m = shape
     x = rng.standard_normal((n, k)).astype(np.float32)
     raw, dec = encode_weights((rng.standard_normal((m, k)) * 0.05).astype(np.float32), wtype)
     got = run_mm(eg2, gpu, name, width, height, x, raw, wtype, m)
-    want = OL.op_mm(x, dec, step)
-    assert np.array_equal(got, want), np.abs(got - want).max()
+    x64, w64 = x.astype(np.float64), dec.astype(np.float64)
+    want, mag = x64 @ w64.T, np.abs(x64) @ np.abs(w64).T
+    assert np.all(np.abs(got - want) <= 4e-6 * mag + 1e-30), np.abs(got - want).max()
+
+
+def test_code_object_dispatch_by_name(eg2, gpu):
+    """The stand-alone code object eg2_ops_gfx950.co, loaded with
+    hipModuleLoad and eg2_mm64x64 launched by symbol name with the EgMM
+    record as its kernarg buffer (src/gemma2_kfd.cpp:106-110, 156-170):
+    the same output as the library's own launch of the operator."""
+    import ctypes as C
+    import os
+
+    import torch
+
+    hip = C.CDLL("libamdhip64.so.7")  # the runtime already in the process
+    co = os.path.join(os.path.dirname(eg2.LIB_PATH), "eg2_ops_gfx950.co")
+    assert os.path.exists(co)
+    mod, fn = C.c_void_p(), C.c_void_p()
+    assert hip.hipModuleLoad(C.byref(mod), co.encode()) == 0
+    try:
+        assert hip.hipModuleGetFunction(C.byref(fn), mod, b"eg2_mm64x64") == 0
+        rng = np.random.default_rng(3)
+        n, k, m = 70, 96, 130
+        x = rng.standard_normal((n, k)).astype(np.float32)
+        raw, dec = encode_weights((rng.standard_normal((m, k)) * 0.05).astype(np.float32), 8)
+        xd, wd = dev(x, gpu), dev(raw, gpu)
+        y = torch.full((n, m), float("nan"), dtype=torch.float32, device=gpu)
+        rec = eg2.EgMM(ptr(y), ptr(xd), ptr(wd), n, k, m, 8)
+        size = C.c_size_t(C.sizeof(rec))
+        extra = (C.c_void_p * 5)(1, C.addressof(rec), 2, C.addressof(size), 3)  # BUFFER_POINTER, SIZE, END
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        hip.hipModuleLaunchKernel.argtypes = [C.c_void_p] + [C.c_uint] * 7 + [C.c_void_p, C.c_void_p, C.c_void_p]
+        assert hip.hipModuleLaunchKernel(fn, (m + 63) // 64, (n + 63) // 64, 1, 256, 1, 1, 0, stream, None,
+                                         extra) == 0
+        got = host(y)
+    finally:
+        torch.cuda.synchronize()
+        assert hip.hipModuleUnload(mod) == 0
+    same = run_mm(eg2, gpu, "eg2_mm64x64", 64, 64, x, raw, 8, m)
+    assert np.array_equal(got, same)
+    want = x.astype(np.float64) @ dec.astype(np.float64).T
+    assert np.abs(got - want).max() <= 4e-6 * (np.abs(x) @ np.abs(dec).T).max()
 
 
 # ------------------------------------------------------------------- norms
@@ -224,13 +270,14 @@ def test_attention_against_float64(eg2, gpu, d, window):
     assert np.abs(host(y).reshape(32, d) - want).max() <= 2e-5
 
 
-@pytest.mark.parametrize("window", [0, 2])
-def test_attention_3q1kv_against_float64(eg2, gpu, window):
-    """eg2_attention256x3: 3 query heads share the one KV head of 256."""
+@pytest.mark.parametrize("window", [0, 2, 50])
+@pytest.mark.parametrize("lens", [[1, 6, 13], [70, 1, 150]])
+def test_attention_3q1kv_against_float64(eg2, gpu, window, lens):
+    """eg2_attention256x3: 3 query heads share the one KV head of 256;
+    sequences longer than a 64-key chunk take the rescaling between chunks."""
     import torch
 
-    rng = np.random.default_rng(5)
-    lens = [1, 6, 13]
+    rng = np.random.default_rng(5 + len(lens) + lens[0])
     n = sum(lens)
     starts = np.concatenate([[0], np.cumsum(lens)])
     bounds = np.array([v for s in range(len(lens)) for _ in range(lens[s]) for v in (starts[s], starts[s + 1])],

@@ -272,63 +272,6 @@ def test_forward_packing_invariance_and_validation():
             OL.forward(model, bad_ids, np.asarray(bad_off, np.uint64))
 
 
-def _round_f32(fr):
-    """Exact Fraction -> nearest float32 (ties to even)."""
-    from fractions import Fraction
-
-    f = np.float32(float(fr))
-    best = None
-    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
-        err = abs(Fraction(float(c)) - fr)
-        key = (err, int(np.array(c, np.float32).view(np.uint32)) & 1)
-        if best is None or key < best[0]:
-            best = (key, c)
-    return np.float32(best[1])
-
-
-def _fmaf(a, b, c):
-    from fractions import Fraction
-
-    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
-    if exact == 0:  # IEEE: x*y + z = 0 is +0 unless both addends are -0
-        neg = (np.signbit(a) != np.signbit(b)) and np.signbit(c)
-        return np.float32(-0.0 if neg else 0.0)
-    return _round_f32(exact)
-
-
-def test_op_mm_exact_known_answer():
-    """tests/kernels.cpp:57-80 inputs: every partial sum is exact, so the
-    result is the float64 product for every accumulation order."""
-    k, m = 64, 35
-    w = ((np.arange(k * m) % 23) - 11).astype(np.float32).reshape(m, k) * 0.125
-    for n in (1, 17, 33, 65):
-        x = ((np.arange(n * k) % 19) - 9).astype(np.float32).reshape(n, k) * 0.03125
-        want = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
-        for step in (8, 16, 32):
-            assert np.array_equal(OL.op_mm(x, w, step), want)
-
-
-def test_op_mm_is_the_sequential_fma_chain():
-    """Brute force with exact rational fma on tiny random inputs; a
-    multiply-then-add chain (the plausible mistake) differs."""
-    rng = np.random.default_rng(3)
-    n, k, m = 3, 21, 4
-    x = rng.standard_normal((n, k)).astype(np.float32)
-    w = rng.standard_normal((m, k)).astype(np.float32)
-    got = OL.op_mm(x, w, 8)
-    unfused_differs = False
-    for r in range(n):
-        for c in range(m):
-            acc = np.float32(0.0)
-            plain = np.float32(0.0)
-            for z in range(k):
-                acc = _fmaf(x[r, z], w[c, z], acc)
-                plain = np.float32(plain + np.float32(x[r, z] * w[c, z]))
-            assert got[r, c] == acc, (r, c)
-            unfused_differs |= bool(plain != acc)
-    assert unfused_differs
-
-
 # ------------------------------------------------------------------ dense head
 
 
