@@ -38,41 +38,47 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
                                 int8_t* gq, float* gd, int ldg, int n, int ff, int k, hipStream_t st);
 
 // Attention over the rows [q0 q1 q2 | k | v] of a packed wave, bit-exact
-// with the reference (see kernels_attn.hip): the scores of the work items
-// (8 uint32 each: sequence start, sequence end, first key of a 64-key
-// block, first query, end of the queries, the sequence's first score
-// index, 0, 0; *item_count of them, `grid` workgroups striding over them)
-// into `scores`, then per token (tok: 4 uint32 each: sequence start, end,
-// first score index, 0) the context, quantized to Q8_0 into cq (row tiles,
-// k = 768) and cd [24][rows]. rows % 4 == 0.
+// with the reference (see kernels_attn.hip). `items` holds item_count[0]
+// score items (8 uint32: sequence start, end, first key of a 32-key
+// block, first pair, end of the pairs, the sequence's first score index,
+// 0, 0) followed by item_count[1] context items (sequence start, end,
+// first pair of a 64-pair block, end of the pairs, first score index, 0,
+// 0, 0); a pair is 3 (token - start) + head. tok: one record per row (4
+// uint32: sequence start, end, first score index, 0). `grid` workgroups
+// stride over each item list. scores: the plan's score floats (the 1/sum
+// of each (token, head) at [3 t + h], then a row of ceil4(n) scores per
+// pair of each sequence of n tokens). The context is quantized to Q8_0
+// into cq (row tiles, k = 768) and cd [24][rows]. rows % 4 == 0.
 hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
                             const uint32_t* tok, int window, int rows, float* scores, int8_t* cq, float* cd,
                             hipStream_t st);
 
-// Work items and token records of launch_attention for the sequences
-// [offsets[s], offsets[s+1]): a sequence of n tokens has ceil(n / 64) key
-// blocks times ceil(n / q(n)) query chunks (q(n) = 8, 16 or 32 as n grows)
-// and 3 n^2 scores. attention_counts gives the counts of a packing;
-// build_attention_plan writes the lists when they fit `cap` (else returns
-// false having written nothing) and reports the counts in *used;
-// attention_capacity bounds the counts of any packing of `tokens` tokens
-// into at most `batch` sequences.
+// The plan of launch_attention for the sequences [offsets[s], offsets[s+1])
+// (rows = offsets[batch]): a sequence of n tokens has ceil(n/32) key
+// blocks times ceil(3n/32) pair blocks of score items, ceil(3n/64)
+// context items and 3 n ceil4(n) score floats, after the 1/sum area of
+// ceil4(3 rows). attention_counts gives the counts of a packing
+// (items = both kinds); build_attention_plan writes the lists when they
+// fit `cap` (else returns false having written nothing) and reports the
+// counts in *used; attention_capacity bounds the counts of any packing of
+// `tokens` tokens into at most `batch` sequences.
 struct AttentionCounts {
-  size_t items, score_floats;
+  size_t items, score_floats, score_items;
 };
 AttentionCounts attention_counts(const size_t* offsets, size_t batch);
 bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCounts& cap, uint32_t* items,
                           uint32_t* tok, AttentionCounts* used);
 AttentionCounts attention_capacity(size_t tokens, size_t batch);
 
-// Workgroups of the scores kernel (two per CU), striding over the items.
-constexpr int kAttentionScoreGrid = 512;
+// Workgroups of the scores and context kernels (four per CU), striding
+// over their items.
+constexpr int kAttentionGrid = 1024;
 
 // launch_attention with the plan built on the device from the device
 // sequence bounds offsets[0..batch] (offsets[0] read as 0, offsets[batch]
 // as rows, the rest clamped into a non-decreasing list) and the plan and
 // scores kept in a static per-device array: no allocation. rows <= 2048,
-// rows % 4 == 0, batch <= 4096. Calls overlapping on one device race.
+// rows % 4 == 0, batch <= 2048. Calls overlapping on one device race.
 hipError_t launch_attention_static(const float* qkv, const uint32_t* offsets, int batch, int window, int rows,
                                    int8_t* cq, float* cd, hipStream_t st);
 

@@ -203,9 +203,9 @@ struct Lane {
   float *x, *h, *xd, *cd, *pooled, *mid, *mid_d;
   int8_t *xq, *cq, *mid_q;
   float* qkv;     // [rows][q0 q1 q2 | k | v] after QK-norm / RoPE
-  float* scores;  // attention scores scratch, 3 n^2 per sequence of n tokens
+  float* scores;  // attention scratch: 1/sum per (token, head), then a score row per (token, head)
   int32_t *ids_d, *pos_d;
-  // Attention plan: the scores kernel's work items and their count, one
+  // Attention plan: score and context work items, their two counts, one
   // record per token.
   uint32_t *items_d, *count_d, *tok_d, *off_d;
   // Pinned staging.
@@ -485,7 +485,7 @@ void Backend::alloc_lane(Lane& L) {
   L.ids_d = dalloc<int32_t>(kCap);
   L.pos_d = dalloc<int32_t>(kCap);
   L.items_d = dalloc<uint32_t>(8 * attn_cap_.items);
-  L.count_d = dalloc<uint32_t>(1);
+  L.count_d = dalloc<uint32_t>(2);
   L.tok_d = dalloc<uint32_t>(4 * (size_t)kCap);
   L.off_d = dalloc<uint32_t>(kCap + 1);
   L.pooled = dalloc<float>((size_t)kCap * kEmbd);
@@ -495,7 +495,7 @@ void Backend::alloc_lane(Lane& L) {
   L.ids_h = halloc<int32_t>(kCap);
   L.pos_h = halloc<int32_t>(kCap);
   L.items_h = halloc<uint32_t>(8 * attn_cap_.items);
-  L.count_h = halloc<uint32_t>(1);
+  L.count_h = halloc<uint32_t>(2);
   L.tok_h = halloc<uint32_t>(4 * (size_t)kCap);
   L.off_h = halloc<uint32_t>(kCap + 1);
   L.out_h = halloc<float>((size_t)kCap * kEmbd);
@@ -539,7 +539,7 @@ void Backend::record_layers(Lane& ln, unsigned rows) {
     // operand rows, no unnormalised projection in HBM.
     launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
                                                          L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
-    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionScoreGrid, ln.tok_d, L.window, n,
+    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid, ln.tok_d, L.window, n,
                                               ln.scores, ln.cq, ln.cd, s));
     gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
@@ -622,10 +622,11 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
   // are checked against the allocation before anything is written.
   std::vector<size_t> all(offsets, offsets + batch + 1);
   if (rows > n) all.push_back(rows);
-  eg2::AttentionCounts used{0, 0};
+  eg2::AttentionCounts used{0, 0, 0};
   if (!eg2::build_attention_plan(all.data(), all.size() - 1, attn_cap_, ln.items_h, ln.tok_h, &used))
     throw std::runtime_error("attention work list exceeds its capacity");
-  ln.count_h[0] = (uint32_t)used.items;
+  ln.count_h[0] = (uint32_t)used.score_items;
+  ln.count_h[1] = (uint32_t)(used.items - used.score_items);
 
   device_step([&] {
     hipStream_t s = ln.stream;
@@ -633,7 +634,8 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
     check(hipMemcpyAsync(ln.pos_d, ln.pos_h, rows * sizeof(int32_t), hipMemcpyHostToDevice, s), "copy positions");
     check(hipMemcpyAsync(ln.items_d, ln.items_h, 8 * used.items * sizeof(uint32_t), hipMemcpyHostToDevice, s),
           "copy attention items");
-    check(hipMemcpyAsync(ln.count_d, ln.count_h, sizeof(uint32_t), hipMemcpyHostToDevice, s), "copy attention count");
+    check(hipMemcpyAsync(ln.count_d, ln.count_h, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+          "copy attention counts");
     check(hipMemcpyAsync(ln.tok_d, ln.tok_h, 4 * (size_t)rows * sizeof(uint32_t), hipMemcpyHostToDevice, s),
           "copy token records");
     check(hipMemcpyAsync(ln.off_d, ln.off_h, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s),

@@ -17,28 +17,39 @@
 // in that order; expf is the host libm's own algorithm (eg2_libm.hpp).
 // A last-bit difference here would become a different Q8_0 quantum, and
 // through the 24 quantized layers a different embedding, so the kernels
-// reproduce the order exactly: on the VALU, since no matrix instruction
-// rounds each product before adding it.
+// reproduce the order exactly.
+//
+// Products on the matrix cores. An fp32 MFMA with a zero accumulator and
+// one product per output (v_mfma_f32_16x16x1_4b_f32) returns each product
+// rounded once, exactly as the VALU multiply does (checked on 12 million
+// random pairs including subnormal results); the ordered additions stay on
+// the VALU. That halves the VALU work of both products (q.k and p.v).
 //
 // Operands: the rows [q0 q1 q2 | k | v] (1280 fp32) that QK-norm/RoPE
-// leaves, one per token (q already scaled by 1/16).
+// leaves, one per token (q already scaled by 1/16). A (token t, head h)
+// pair of a sequence starting at lo is numbered 3 (t - lo) + h.
 //
-// Two kernels:
-//  - attention_scores_kernel: work items of (sequence, 64 keys, a chunk of
-//    its queries). The workgroup stages the 64 K rows in LDS (one per lane,
-//    rows 260 floats apart so the lanes' 16-byte reads fall in distinct
-//    banks); each wave takes 4 (token, head) pairs at a time, whose q values
-//    are wave-uniform scalar loads, and runs the 4 chains of each of the 4
-//    dot products per lane: 32 multiplies and adds per 4 dimensions. The
-//    scores go to a scratch buffer, one row of the sequence's length per
-//    (token, head).
-//  - attention_context_kernel: one wave per token, its 3 heads. The row
-//    maxima; then per 64-key chunk every lane's expf of its key (for all 3
-//    heads) into LDS, and lanes 0-2 add their head's chunk to its sum in key
-//    order; 1/sum; then the chunk's scales p * (1/sum) into LDS and, key by
-//    key, the lanes' 4 dimensions of each head's context (12 multiplies and
-//    adds per key and lane, the V row read once for the 3 heads). The Q8_0
-//    epilogue quantizes 32-dimension blocks over 8 lanes.
+// Three kernels:
+//  - attention_scores_kernel: work items of (sequence, 32 keys, 32 pairs).
+//    The workgroup stages the q rows of its pairs and the k rows of its
+//    keys in LDS, 128 dimensions at a time, reordered so that chain c's
+//    values (dimensions c, c + 4, ...) are contiguous. Each wave owns 16
+//    pairs x 16 keys; per 4 dimensions one 4-block MFMA whose block c
+//    multiplies chain c (lane group c feeds chain c's q and k values), and
+//    each lane adds its 16 products to its 4 pairs' 4 chain sums. The
+//    scores go to a scratch row per pair (row length rounded up to 4).
+//  - attention_softmax_kernel: one wave per (token, head): the row
+//    maximum; then per 64-key chunk every lane's expf of its key, written
+//    back over the score, and lane 0 adds the chunk to the sum in key
+//    order; 1/sum per (token, head) into the scratch's head.
+//  - attention_context_kernel: work items of (sequence, 64 pairs), each
+//    taken by 4 workgroups of 64 dimensions. Per 64-key chunk the
+//    workgroup stages w = p * (1/sum) for its pairs (0 for keys outside a
+//    pair's window, which adds +0 and changes no sum) and the chunk's v
+//    values in LDS; per key each wave issues one 4-block MFMA (block b =
+//    16 pairs, columns = its 16 dimensions) and adds the 16 products to its
+//    accumulators, in key order. The Q8_0 epilogue quantizes 32-value
+//    blocks over lane pairs.
 // A sequence's keys, scores and context depend only on its own tokens, so
 // packing never changes a bit.
 #include <algorithm>
@@ -50,16 +61,22 @@
 
 namespace eg2 {
 
-constexpr int kKeyBlock = 64;          // keys of a scores work item, one per lane
-constexpr int kKPitch = kHeadDim + 4;  // floats per LDS K row: 4 banks apart, so 8 lanes' b128 reads cover all 32
-constexpr int kPairs = 2;              // (token, head) pairs per pass of a scores wave
-constexpr int kLd = kQKVCols;          // floats per operand row [q0 q1 q2 | k | v]
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kLd = kQKVCols;  // floats per operand row [q0 q1 q2 | k | v]
 constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 
-// Query tokens per scores work item: longer sequences take more queries per
-// staged K block (fewer restagings); shorter ones fewer (more items to
-// spread over the CUs). A function of the length alone.
-__host__ __device__ inline size_t query_chunk(size_t len) { return len <= 128 ? 8 : (len <= 512 ? 16 : 32); }
+constexpr int kSKeys = 32, kSPairs = 32;  // scores workgroup tile
+constexpr int kSDims = 128;               // dimensions staged at a time
+constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apart
+constexpr int kCPairs = 64, kCDims = 64;  // context workgroup tile
+constexpr int kCKeys = 64;                // keys per staged chunk
+constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
+
+// Floats of a sequence's score row (its length rounded up to 4, so that
+// rows are 16-byte aligned), and of the 1/sum area at the scratch's head.
+__host__ __device__ inline uint32_t score_pitch(uint32_t len) { return (len + 3u) & ~3u; }
+__host__ __device__ inline size_t inv_floats(size_t rows) { return (3 * rows + 3) & ~(size_t)3; }
 
 // Key range of query token t in its sequence [lo, hi) (kernels.c:330-336
 // in packed coordinates): the sequence, or |t - kt| <= window/2.
@@ -70,122 +87,116 @@ __host__ __device__ inline void key_range(uint32_t t, uint32_t lo, uint32_t hi, 
   last = window > 0 && t + half + 1 < hi ? t + half + 1 : hi;
 }
 
+// ----------------------------------------------------------------- scores
+
+// 16 values of dimensions d0 .. d0 + 15 (d0 = 128 part + 16 grp), loaded,
+// then stored to the chain-major staged row: chain c's values (d0 + c,
+// d0 + 4 + c, ...) at [32 c + 4 grp .. 32 c + 4 grp + 3].
+struct Stage16 {
+  float4 a, b, c, d;
+};
+__device__ __forceinline__ Stage16 load16(const float* __restrict__ src) {
+  return {*reinterpret_cast<const float4*>(src), *reinterpret_cast<const float4*>(src + 4),
+          *reinterpret_cast<const float4*>(src + 8), *reinterpret_cast<const float4*>(src + 12)};
+}
+__device__ __forceinline__ void store16(const Stage16& v, float* row, int grp) {
+  *reinterpret_cast<float4*>(row + 0 * 32 + 4 * grp) = make_float4(v.a.x, v.b.x, v.c.x, v.d.x);
+  *reinterpret_cast<float4*>(row + 1 * 32 + 4 * grp) = make_float4(v.a.y, v.b.y, v.c.y, v.d.y);
+  *reinterpret_cast<float4*>(row + 2 * 32 + 4 * grp) = make_float4(v.a.z, v.b.z, v.c.z, v.d.z);
+  *reinterpret_cast<float4*>(row + 3 * 32 + 4 * grp) = make_float4(v.a.w, v.b.w, v.c.w, v.d.w);
+}
+
 __global__ void __launch_bounds__(256)
 attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__ items,
                         const uint32_t* __restrict__ item_count, int window, int rows,
                         float* __restrict__ scores) {
-  __shared__ __align__(16) float kblk[kKeyBlock * kKPitch];
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t count = *item_count;
+  __shared__ __align__(16) float qs[kSPairs * kSPitch];
+  __shared__ __align__(16) float ks[kSKeys * kSPitch];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int pr = 16 * (w >> 1), kr = 16 * (w & 1);  // the wave's 16 pairs and 16 keys in the tile
+  const int srow = tid >> 3, grp = tid & 7;          // staging: row and 16-dimension group
+  const uint32_t count = item_count[0];
+  const floatx16 zero = {};
   for (uint32_t item = blockIdx.x; item < count; item += gridDim.x) {
     // Item fields clamped to the wave, so a malformed list cannot address
     // outside the rows.
     const uint4 a = items[2 * item], b = items[2 * item + 1];
-    const uint32_t hi = min(a.y, (uint32_t)rows), lo = min(a.x, hi);
-    const uint32_t key0 = a.z, q1 = min(b.x, hi), q0 = max(min(a.w, q1), lo);
-    const uint32_t len = hi - lo;
+    const uint32_t hi = min(a.y, (uint32_t)rows), lo = min(a.x, hi), len = hi - lo;
+    const uint32_t key0 = a.z, pair1 = min(b.x, 3 * len), pair0 = a.w;
+    if (len == 0 || key0 < lo || key0 >= hi || pair0 >= pair1) continue;  // uniform over the workgroup
     const size_t sbase = b.y;
-    if (len == 0 || key0 < lo || key0 >= hi) continue;  // uniform over the workgroup
-    __syncthreads();  // the previous item's K rows are no longer read
-    // K rows key0 .. key0 + 63 (clamped to the sequence's last), 16 float4
-    // per thread, 64 threads per row.
-#pragma unroll
-    for (int j = 0; j < kKeyBlock * kHeadDim / 4 / 256; ++j) {
-      const int idx = tid + 256 * j, r = idx >> 6, c4 = idx & 63;
-      const uint32_t key = min(key0 + (uint32_t)r, hi - 1);
-      *reinterpret_cast<float4*>(kblk + r * kKPitch + 4 * c4) =
-          *reinterpret_cast<const float4*>(qkv + (size_t)key * kLd + kKOff + 4 * c4);
+    const uint32_t pitch = score_pitch(len);
+    if (window > 0) {  // skip a tile with no (pair, key) inside the window
+      const int half = window / 2;
+      const int tmin = (int)(lo + pair0 / 3), tmax = (int)(lo + (pair1 - 1) / 3);
+      const int kmin = (int)key0, kmax = (int)min(key0 + kSKeys, hi) - 1;
+      if (kmax < tmin - half || kmin > tmax + half) continue;
     }
-    __syncthreads();
-    const float* krow = kblk + lane * kKPitch;
-    const uint32_t key = key0 + lane;
-    const uint32_t pairs = 3 * (q1 - q0);
-    for (uint32_t g = (uint32_t)w; kPairs * g < pairs; g += 4) {
-      uint32_t t[kPairs], h[kPairs];
-      bool in[kPairs];
-      bool any = false;
+    float acc[4][4];  // [chain][pair 4g + r]
 #pragma unroll
-      for (int i = 0; i < kPairs; ++i) {
-        const uint32_t c = min(kPairs * g + i, pairs - 1);  // past the end: repeats the last pair, not stored
-        t[i] = q0 + c / 3;
-        h[i] = c % 3;
-        uint32_t first, last;
-        key_range(t[i], lo, hi, window, first, last);
-        in[i] = kPairs * g + i < pairs && key >= first && key < last;
-        any |= in[i];
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[c][r] = 0.0f;
+    // Staging sources: this thread's pair row and key row (clamped; the
+    // rows past the tile's end are computed and not stored).
+    const uint32_t spair = min(pair0 + (uint32_t)srow, pair1 - 1), skey = min(key0 + (uint32_t)srow, hi - 1);
+    const float* qsrc = qkv + (size_t)(lo + spair / 3) * kLd + (spair % 3) * kHeadDim;
+    const float* ksrc = qkv + (size_t)skey * kLd + kKOff;
+    // The second half's values are loaded while the first half computes.
+    Stage16 qn = load16(qsrc + 16 * grp), kn = load16(ksrc + 16 * grp);
+#pragma unroll 1
+    for (int part = 0; part < kHeadDim / kSDims; ++part) {
+      __syncthreads();  // the previous half's (or item's) rows are no longer read
+      store16(qn, qs + srow * kSPitch, grp);
+      store16(kn, ks + srow * kSPitch, grp);
+      __syncthreads();
+      if (part + 1 < kHeadDim / kSDims) {
+        qn = load16(qsrc + (part + 1) * kSDims + 16 * grp);
+        kn = load16(ksrc + (part + 1) * kSDims + 16 * grp);
       }
-      if (!__builtin_amdgcn_ballot_w64(any)) continue;  // no key of the block in range for these pairs
-      const float* qrow[kPairs];
+      const float* qa = qs + (pr + r16) * kSPitch + 32 * g;
+      const float* kb = ks + (kr + r16) * kSPitch + 32 * g;
+      // Per 4 steps: the 4 MFMAs into separate registers, then their adds
+      // (the adds of one overlap the next ones' execution), with the next
+      // 4 steps' operands read from LDS before the adds.
+      float4 q4 = *reinterpret_cast<const float4*>(qa), k4 = *reinterpret_cast<const float4*>(kb);
 #pragma unroll
-      for (int i = 0; i < kPairs; ++i) qrow[i] = qkv + (size_t)t[i] * kLd + h[i] * kHeadDim;
-      // kernels.c:289-294: chain j accumulates q[4s + j] * k[4s + j], s = 0..63.
-      float acc[kPairs][4];
+      for (int s = 0; s < kSDims / 4; s += 4) {
+        const float qv[4] = {q4.x, q4.y, q4.z, q4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
+        floatx16 prod[4];
 #pragma unroll
-      for (int i = 0; i < kPairs; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-      // q in chunks of 2 steps (8 floats per pair), wave-uniform scalar
-      // loads, two chunks in registers: chunk c + 1 is requested after
-      // chunk c has arrived and before chunk c is used, so its latency
-      // overlaps chunk c's arithmetic. (Scalar loads return out of order:
-      // any wait for one is a wait for all, hence the explicit order.)
-      constexpr int kQ = 8, kChunks = kHeadDim / kQ;
-      float qa[kPairs][kQ], qb[kPairs][kQ];
-      auto load_q = [&](float (&dst)[kPairs][kQ], int c) {
-#pragma unroll
-        for (int i = 0; i < kPairs; ++i)
-#pragma unroll
-          for (int e = 0; e < kQ; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(qrow[i] + kQ * c + e);
-            dst[i][e] = v.x;
-            dst[i][e + 1] = v.y;
-            dst[i][e + 2] = v.z;
-            dst[i][e + 3] = v.w;
-          }
-      };
-      auto chunk = [&](const float (&q)[kPairs][kQ], int c) {
-#pragma unroll
-        for (int s = 0; s < kQ / 4; ++s) {
-          const float4 k4 = *reinterpret_cast<const float4*>(krow + kQ * c + 4 * s);
-#pragma unroll
-          for (int i = 0; i < kPairs; ++i) {
-            const float p0 = q[i][4 * s] * k4.x, p1 = q[i][4 * s + 1] * k4.y;
-            const float p2 = q[i][4 * s + 2] * k4.z, p3 = q[i][4 * s + 3] * k4.w;
-            acc[i][0] = acc[i][0] + p0;
-            acc[i][1] = acc[i][1] + p1;
-            acc[i][2] = acc[i][2] + p2;
-            acc[i][3] = acc[i][3] + p3;
-          }
+        for (int e = 0; e < 4; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
+          prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e], kv[e], zero, 0, 0, 0);
+        if (s + 4 < kSDims / 4) {
+          q4 = *reinterpret_cast<const float4*>(qa + s + 4);
+          k4 = *reinterpret_cast<const float4*>(kb + s + 4);
         }
-      };
-      load_q(qa, 0);
-      for (int c = 0; c < kChunks; c += 2) {
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): chunk c (and earlier LDS reads) have arrived
         __builtin_amdgcn_sched_barrier(0);
-        load_q(qb, c + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        chunk(qa, c);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // chunk c + 1
-        __builtin_amdgcn_sched_barrier(0);
-        if (c + 2 < kChunks) load_q(qa, c + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        chunk(qb, c + 1);
-      }
 #pragma unroll
-      for (int i = 0; i < kPairs; ++i) {
-        const float score = (acc[i][0] + acc[i][2]) + (acc[i][1] + acc[i][3]);
-        if (in[i]) scores[sbase + ((size_t)3 * (t[i] - lo) + h[i]) * len + (key - lo)] = score;
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    const uint32_t key = key0 + kr + r16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t pair = pair0 + pr + 4 * g + r;
+      const float score = (acc[0][r] + acc[2][r]) + (acc[1][r] + acc[3][r]);
+      if (pair < pair1 && key < hi) {
+        uint32_t first, last;
+        key_range(lo + pair / 3, lo, hi, window, first, last);
+        if (key >= first && key < last) scores[sbase + (size_t)pair * pitch + (key - lo)] = score;
       }
     }
   }
 }
 
-// Lanes l ^ 1, l ^ 2, l ^ 4 combined with l: the maximum over each 8-lane group.
-__device__ __forceinline__ float group8_max(float v) {
-#pragma unroll
-  for (int m = 1; m < 8; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
+// ---------------------------------------------------------------- softmax
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -200,51 +211,49 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One wave per (token, head) pair: the row maximum, then per 64-key chunk
+// every lane's p = expf(score - m) written back over the score and, in
+// key order, added by lane 0 to the sum; 1/sum to the scratch's head.
 __global__ void __launch_bounds__(256)
-attention_context_kernel(const float* __restrict__ qkv, const float* __restrict__ scores,
-                         const uint4* __restrict__ tok, int window, int rows, int8_t* __restrict__ cq,
-                         float* __restrict__ cd) {
+attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
-  __shared__ __align__(16) float pbuf[4][kHeads][64];  // per wave: a chunk's p values, per head
-  __shared__ __align__(16) float sbuf[4][64][4];       // per wave: a chunk's scales, [key][head]
+  __shared__ __align__(16) float pbuf[4][64];  // per wave: a chunk's p values
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
   __syncthreads();
-  const uint32_t t = 4 * blockIdx.x + w;
+  const uint32_t pair = 4 * blockIdx.x + w, t = pair / 3, h = pair % 3;
   if (t >= (uint32_t)rows) return;
   const uint4 meta = tok[t];
   const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
   if (t < lo || t >= hi) return;  // a malformed entry: nothing is written for this token
-  const uint32_t len = hi - lo;
   uint32_t first, last;
   key_range(t, lo, hi, window, first, last);
-  // Score rows of (t, h); key kt is at srow[h][kt - lo].
-  const float* srow[kHeads];
-#pragma unroll
-  for (int h = 0; h < kHeads; ++h) srow[h] = scores + meta.z + ((size_t)3 * (t - lo) + h) * len;
+  float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
 
-  // The row maxima (order-free).
-  float m[kHeads];
-#pragma unroll
-  for (int h = 0; h < kHeads; ++h) m[h] = -__builtin_inff();
-  for (uint32_t kt = first + lane; kt < last; kt += 64)
-#pragma unroll
-    for (int h = 0; h < kHeads; ++h) m[h] = fmaxf(m[h], srow[h][kt - lo]);
-#pragma unroll
-  for (int h = 0; h < kHeads; ++h) m[h] = wave_max(m[h]);
+  // The row maximum (order-free), four loads in flight per lane.
+  float m = -__builtin_inff();
+  uint32_t kt = first + lane;
+  for (; kt + 192 < last; kt += 256) {
+    const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
+    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+  }
+  for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
+  m = wave_max(m);
 
-  // sum = p[first] + p[first + 1] + ... in key order: each chunk's p values
-  // are computed by all lanes, then lane h adds its head's in order.
+  // p and the sum = p[first] + p[first + 1] + ... in key order.
   float sum = 0.0f;
   for (uint32_t c0 = first; c0 < last; c0 += 64) {
-    const uint32_t kt = c0 + lane;
-#pragma unroll
-    for (int h = 0; h < kHeads; ++h)
-      pbuf[w][h][lane] = kt < last ? libm::expf_tab(srow[h][kt - lo] - m[h], tab) : 0.0f;
+    const uint32_t k = c0 + lane;
+    float p = 0.0f;
+    if (k < last) {
+      p = libm::expf_tab(srow[k - lo] - m, tab);
+      srow[k - lo] = p;
+    }
+    pbuf[w][lane] = p;
     wave_lds_sync();
-    if (lane < kHeads) {
+    if (lane == 0) {
       const int n = (int)min(64u, last - c0);
-      const float* pr = pbuf[w][lane];
+      const float* pr = pbuf[w];
       int j = 0;
       for (; j + 4 <= n; j += 4) {
         const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
@@ -257,91 +266,170 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     }
     wave_lds_sync();
   }
-  const float inv_lane = 1.0f / sum;
-  float inv[kHeads];
-#pragma unroll
-  for (int h = 0; h < kHeads; ++h) inv[h] = __shfl(inv_lane, h, 64);
+  if (lane == 0) scores[3 * (size_t)t + h] = 1.0f / sum;
+}
 
-  // out = sum over kt in order of (p[kt] * inv) * v[kt]; lane l owns
-  // dimensions 4l .. 4l + 3 of each head.
-  float acc[kHeads][4];
-#pragma unroll
-  for (int h = 0; h < kHeads; ++h)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) acc[h][d] = 0.0f;
-  const float* vcol = qkv + kVOff + 4 * lane;
-  for (uint32_t c0 = first; c0 < last; c0 += 64) {
-    const uint32_t kt = c0 + lane;
-    float sc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int h = 0; h < kHeads; ++h) {
-      const float p = kt < last ? libm::expf_tab(srow[h][kt - lo] - m[h], tab) : 0.0f;
-      sc[h] = p * inv[h];
+// ---------------------------------------------------------------- context
+
+__global__ void __launch_bounds__(256)
+attention_context_kernel(const float* __restrict__ qkv, const float* __restrict__ scores,
+                         const uint4* __restrict__ items, const uint32_t* __restrict__ item_count, int window,
+                         int rows, int8_t* __restrict__ cq, float* __restrict__ cd) {
+  __shared__ __align__(16) float wl[kCKeys * kCPitchW];  // [key][pair]: w = p * (1/sum), 0 outside the window
+  __shared__ __align__(16) float vl[kCKeys * kCPitchV];  // [key][dimension]
+  __shared__ uint32_t range[kCPairs][2];                  // each pair's key range
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const uint4* citems = items + 2 * (size_t)item_count[0];  // the context items follow the score items
+  const uint32_t count = 4 * item_count[1];
+  const floatx16 zero = {};
+  for (uint32_t work = blockIdx.x; work < count; work += gridDim.x) {
+    const uint4 a = citems[2 * (work >> 2)], b = citems[2 * (work >> 2) + 1];
+    const uint32_t hi = min(a.y, (uint32_t)rows), lo = min(a.x, hi), len = hi - lo;
+    const uint32_t pair1 = min(a.w, 3 * len), pair0 = a.z;
+    if (len == 0 || pair0 >= pair1) continue;  // uniform
+    const size_t sbase = b.x;
+    const uint32_t pitch = score_pitch(len);
+    const int dblk = (int)(work & 3) * kCDims;  // the workgroup's 64 dimensions of each head
+    __syncthreads();  // the previous item's ranges and tile are no longer read
+    if (tid < kCPairs) {
+      const uint32_t pair = min(pair0 + (uint32_t)tid, pair1 - 1);
+      uint32_t first, last;
+      key_range(lo + pair / 3, lo, hi, window, first, last);
+      range[tid][0] = first;
+      range[tid][1] = last;
     }
-    *reinterpret_cast<float4*>(sbuf[w][lane]) = make_float4(sc[0], sc[1], sc[2], sc[3]);
-    wave_lds_sync();
-    const int n = (int)min(64u, last - c0);
-    const float* vrow = vcol + (size_t)c0 * kLd;
-    // The V rows of 8 keys are in flight while the previous 8 are used
-    // (rows past the chunk's end repeat its last one and are not used).
-    constexpr int kAhead = 8;
-    float4 vq[kAhead];
+    __syncthreads();
+    // Keys the tile's pairs need (ranges grow with the token), from a
+    // multiple of 4 past lo so that the float4 reads of the rows align.
+    const uint32_t kfirst = lo + ((range[0][0] - lo) & ~3u);
+    const uint32_t klast = range[min(pair1 - pair0, (uint32_t)kCPairs) - 1][1];
+    float acc[16];
 #pragma unroll
-    for (int j = 0; j < kAhead; ++j) vq[j] = *reinterpret_cast<const float4*>(vrow + (size_t)min(j, n - 1) * kLd);
-    for (int j0 = 0; j0 < n; j0 += kAhead) {
-      float4 vn[kAhead];
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    // Staging roles: w by (pair = lane, the 16 keys of quarter w); v by
+    // (key = tid / 4, 16 dimensions of quarter tid % 4).
+    const uint32_t wp = (uint32_t)lane;
+    const uint32_t wpair = min(pair0 + wp, pair1 - 1);
+    const float winv = scores[3 * (size_t)(lo + wpair / 3) + wpair % 3];
+    const float* wsrc = scores + sbase + (size_t)wpair * pitch;
+    const uint32_t wfirst = range[wp][0], wlast = pair0 + wp < pair1 ? range[wp][1] : wfirst;
+    const uint32_t vk = (uint32_t)tid >> 2, vq = 16 * (tid & 3);
+    for (uint32_t c0 = kfirst; c0 < klast; c0 += kCKeys) {
+      __syncthreads();  // the previous chunk is no longer read
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j)
-        vn[j] = *reinterpret_cast<const float4*>(vrow + (size_t)min(j0 + kAhead + j, n - 1) * kLd);
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const uint32_t k4 = c0 + 16 * w + 4 * j4;  // 4 keys, 16-byte aligned in the row
+        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (k4 - lo < pitch) p4 = *reinterpret_cast<const float4*>(wsrc + (k4 - lo));
+        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) {
-        if (j0 + j >= n) break;  // uniform
-        const float4 s4 = *reinterpret_cast<const float4*>(sbuf[w][j0 + j]);
-        const float4 v4 = vq[j];
-        const float s[kHeads] = {s4.x, s4.y, s4.z};
-#pragma unroll
-        for (int h = 0; h < kHeads; ++h) {
-          const float a0 = s[h] * v4.x, a1 = s[h] * v4.y, a2 = s[h] * v4.z, a3 = s[h] * v4.w;
-          acc[h][0] = acc[h][0] + a0;
-          acc[h][1] = acc[h][1] + a1;
-          acc[h][2] = acc[h][2] + a2;
-          acc[h][3] = acc[h][3] + a3;
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t kt = k4 + e;
+          const float wv = pv[e] * winv;
+          wl[(16 * w + 4 * j4 + e) * kCPitchW + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
         }
       }
+      {
+        const uint32_t kt = c0 + vk;
+        float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0, v2 = v0, v3 = v0;
+        if (kt < hi) {
+          const float* src = qkv + (size_t)kt * kLd + kVOff + dblk + vq;
+          v0 = *reinterpret_cast<const float4*>(src);
+          v1 = *reinterpret_cast<const float4*>(src + 4);
+          v2 = *reinterpret_cast<const float4*>(src + 8);
+          v3 = *reinterpret_cast<const float4*>(src + 12);
+        }
+        float* dst = vl + vk * kCPitchV + vq;
+        *reinterpret_cast<float4*>(dst) = v0;
+        *reinterpret_cast<float4*>(dst + 4) = v1;
+        *reinterpret_cast<float4*>(dst + 8) = v2;
+        *reinterpret_cast<float4*>(dst + 12) = v3;
+      }
+      __syncthreads();
+      // Keys in groups of 4 (a group's keys past klast carry w = 0 for every
+      // pair and add +0): the group's 4 MFMAs into separate registers, the
+      // next group's operands read from LDS, then the adds in key order.
+      const int n4 = (int)((min((uint32_t)kCKeys, klast - c0) + 3) & ~3u);
+      const float* wa = wl + lane;
+      const float* vb = vl + 16 * w + r16;
+      float an[4], bn[4];
 #pragma unroll
-      for (int j = 0; j < kAhead; ++j) vq[j] = vn[j];
+      for (int e = 0; e < 4; ++e) {
+        an[e] = wa[e * kCPitchW];
+        bn[e] = vb[e * kCPitchV];
+      }
+      for (int j = 0; j < n4; j += 4) {
+        floatx16 prod[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)  // block b: pairs 16b .. 16b + 15 (rows) x the wave's 16 dimensions
+          prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(an[e], bn[e], zero, 0, 0, 0);
+        if (j + 4 < n4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            an[e] = wa[(j + 4 + e) * kCPitchW];
+            bn[e] = vb[(j + 4 + e) * kCPitchV];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[v] = acc[v] + prod[e][v];
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    wave_lds_sync();
-  }
-
-  // Q8_0 of the context row (quants.c:97-177): block b of head h is
-  // dimensions 32b .. 32b + 31, held by lanes 8b .. 8b + 7; the int8 values
-  // go to the row-tile layout (24 blocks per row), the scales to cd[block][row].
+    // Lane holds dimension dblk + 16 w + r16 of pairs 16 (v/4) + 4 g + v%4.
+    // Through LDS to [pair][64 dimensions], then Q8_0 over lane pairs.
+    __syncthreads();
+    float* tile = wl;  // 64 x kCPitchW floats
 #pragma unroll
-  for (int h = 0; h < kHeads; ++h) {
-    float amax = 0.0f;
+    for (int v = 0; v < 16; ++v) tile[(16 * (v >> 2) + 4 * g + (v & 3)) * kCPitchW + 16 * w + r16] = acc[v];
+    __syncthreads();
+    const uint32_t qp = (uint32_t)tid >> 2, qb = (tid >> 1) & 1, qh = tid & 1;  // pair, 32-block, half
+    float vals[16];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) amax = fmaxf(amax, fabsf(acc[h][d]));
-    amax = group8_max(amax);
-    const float dq = div127(amax);
-    const float id = amax != 0.0f ? 1.0f / dq : 0.0f;  // quants.c: an all-zero block stores zeros
-    const int e = h * kHeadDim + 4 * lane;
-    *reinterpret_cast<uint32_t*>(cq + q8_tile_offset(t, (unsigned)e, kEmbd / kQK)) =
-        pack_i8x4(q8_round(acc[h][0] * id), q8_round(acc[h][1] * id), q8_round(acc[h][2] * id),
-                  q8_round(acc[h][3] * id));
-    if ((lane & 7) == 0) cd[(size_t)(e / kQK) * rows + t] = fp16_bits_to_fp32(fp32_to_fp16_bits(dq));
+    for (int i = 0; i < 16; i += 4) {
+      const float4 x4 = *reinterpret_cast<const float4*>(tile + qp * kCPitchW + 32 * qb + 16 * qh + i);
+      vals[i] = x4.x;
+      vals[i + 1] = x4.y;
+      vals[i + 2] = x4.z;
+      vals[i + 3] = x4.w;
+    }
+    const uint32_t pair = min(pair0 + qp, pair1 - 1);
+    const uint32_t t = lo + pair / 3, h = pair % 3;
+    const unsigned e = h * kHeadDim + (unsigned)dblk + 32 * qb + 16 * qh;
+    quantize_block_part<2>(vals, pair0 + qp < pair1, cq + q8_tile_offset(t, e, kEmbd / kQK),
+                           cd + (size_t)(e / kQK) * rows + t);
   }
 }
 
 // ---------------------------------------------------------------- host side
 
+namespace {
+
+// Per-sequence counts of the plan.
+struct SeqPlan {
+  size_t score_items, context_items, score_floats;
+};
+__host__ __device__ inline SeqPlan seq_plan(size_t len) {
+  const size_t pairs = 3 * len;
+  return {(len + kSKeys - 1) / kSKeys * ((pairs + kSPairs - 1) / kSPairs), (pairs + kCPairs - 1) / kCPairs,
+          pairs * score_pitch((uint32_t)len)};
+}
+
+}  // namespace
+
 AttentionCounts attention_counts(const size_t* offsets, size_t batch) {
-  AttentionCounts c{0, 0};
+  AttentionCounts c{0, inv_floats(batch ? offsets[batch] : 0), 0};
+  size_t ctx = 0;
   for (size_t s = 0; s < batch; ++s) {
-    const size_t len = offsets[s + 1] - offsets[s];
-    c.items += (len + kKeyBlock - 1) / kKeyBlock * ((len + query_chunk(len) - 1) / query_chunk(len));
-    c.score_floats += 3 * len * len;
+    const SeqPlan p = seq_plan(offsets[s + 1] - offsets[s]);
+    c.score_items += p.score_items;
+    ctx += p.context_items;
+    c.score_floats += p.score_floats;
   }
+  c.items = c.score_items + ctx;
   return c;
 }
 
@@ -350,40 +438,51 @@ bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCo
   const AttentionCounts need = attention_counts(offsets, batch);
   if (used) *used = need;
   if (need.items > cap.items || need.score_floats > cap.score_floats) return false;
-  size_t n = 0, sbase = 0;
+  size_t ns = 0, nc = need.score_items, sbase = inv_floats(batch ? offsets[batch] : 0);
   for (size_t s = 0; s < batch; ++s) {
-    const size_t lo = offsets[s], hi = offsets[s + 1], len = hi - lo, qc = query_chunk(len);
-    for (size_t k0 = lo; k0 < hi; k0 += kKeyBlock)
-      for (size_t q = lo; q < hi; q += qc) {
-        uint32_t* it = items + 8 * n++;
+    const size_t lo = offsets[s], hi = offsets[s + 1], len = hi - lo, pairs = 3 * len;
+    for (size_t k0 = lo; k0 < hi; k0 += kSKeys)
+      for (size_t p0 = 0; p0 < pairs; p0 += kSPairs) {
+        uint32_t* it = items + 8 * ns++;
         it[0] = (uint32_t)lo;
         it[1] = (uint32_t)hi;
         it[2] = (uint32_t)k0;
-        it[3] = (uint32_t)q;
-        it[4] = (uint32_t)std::min(hi, q + qc);
+        it[3] = (uint32_t)p0;
+        it[4] = (uint32_t)std::min(pairs, p0 + kSPairs);
         it[5] = (uint32_t)sbase;
-        it[6] = 0;
-        it[7] = 0;
+        it[6] = it[7] = 0;
       }
+    for (size_t p0 = 0; p0 < pairs; p0 += kCPairs) {
+      uint32_t* it = items + 8 * nc++;
+      it[0] = (uint32_t)lo;
+      it[1] = (uint32_t)hi;
+      it[2] = (uint32_t)p0;
+      it[3] = (uint32_t)std::min(pairs, p0 + kCPairs);
+      it[4] = (uint32_t)sbase;
+      it[5] = it[6] = it[7] = 0;
+    }
     for (size_t t = lo; t < hi; ++t) {
       tok[4 * t] = (uint32_t)lo;
       tok[4 * t + 1] = (uint32_t)hi;
       tok[4 * t + 2] = (uint32_t)sbase;
       tok[4 * t + 3] = 0;
     }
-    sbase += 3 * len * len;
+    sbase += seq_plan(len).score_floats;
   }
   return true;
 }
 
 AttentionCounts attention_capacity(size_t tokens, size_t batch) {
-  // Items of a sequence of n tokens: ceil(n/64) ceil(n/qc(n)) <= (n/64 + 1)
-  // (n/8 + 1) = n^2/512 + n (1/64 + 1/8) + 1; over sequences with sum n <=
-  // tokens and at most `batch` of them, at most tokens^2/512 + 9 tokens/64 +
-  // batch. Scores: 3 n^2 per sequence, at most 3 tokens^2.
+  // Per sequence of n tokens: ceil(n/32) ceil(3n/32) <= (n/32 + 1)(3n/32 +
+  // 1) = 3n^2/1024 + n/8 + 1 score items and ceil(3n/64) <= 3n/64 + 1
+  // context items; over sequences with sum n <= tokens, at most `batch` of
+  // them: 3 tokens^2/1024 + 11 tokens/64 + 2 batch. Score floats: 3n
+  // (n + 3) per sequence, at most 3 tokens^2 + 9 tokens, plus the 1/sum
+  // area of 3 tokens rounded up to 4.
   AttentionCounts c;
-  c.items = tokens * tokens / 512 + 9 * tokens / 64 + batch + 1;
-  c.score_floats = 3 * tokens * tokens;
+  c.items = 3 * tokens * tokens / 1024 + 11 * tokens / 64 + 2 * batch + 2;
+  c.score_floats = 3 * tokens * tokens + 12 * tokens + 4;
+  c.score_items = 0;
   return c;
 }
 
@@ -395,8 +494,12 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, scores);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attention_context_kernel, dim3(rows / 4), dim3(256), 0, st, qkv, scores,
-                     reinterpret_cast<const uint4*>(tok), window, rows, cq, cd);
+  hipLaunchKernelGGL(attention_softmax_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
+                     reinterpret_cast<const uint4*>(tok), window, rows);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attention_context_kernel, dim3(grid), dim3(256), 0, st, qkv, scores,
+                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd);
   return hipGetLastError();
 }
 
@@ -405,21 +508,22 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
 // launch_attention_static keeps its plan and scores in `scratch`, a
 // file-scope device array (one copy per GPU, alive until the process
 // ends), and builds the plan on the device from device offsets, so a call
-// allocates nothing. Layout: [item count | pad to 256 B][token records,
-// 16 B x kStaticRows][work items, 32 B x kStaticItems][scores, 3 x
-// kStaticRows^2 floats]. Any packing of at most kStaticRows rows into at
-// most kStaticBatch sequences fits (the bounds of attention_capacity).
-// Nothing in it has to start at zero: the plan kernel writes the count and
-// every record the other two kernels read, and the context kernel reads
-// only scores the scores kernel wrote in the same call. Calls that overlap
-// on one GPU share the array and race.
+// allocates nothing. Layout: [item counts | pad to 256 B][token records,
+// 16 B x kStaticRows][work items, 32 B x kStaticItems][scores]. Any packing
+// of at most kStaticRows rows into at most kStaticBatch sequences fits
+// (the bounds of attention_capacity). Nothing in it has to start at zero:
+// the plan kernel writes the counts and every record the other kernels
+// read, the softmax kernel every 1/sum the context kernel reads, and the
+// softmax and context kernels use only scores written in the same call.
+// Calls that overlap on one GPU share the array and race.
 
-constexpr size_t kStaticRows = 2048, kStaticBatch = 4096;
-constexpr size_t kStaticItems = kStaticRows * kStaticRows / 512 + 9 * kStaticRows / 64 + kStaticBatch + 1;
+constexpr size_t kStaticRows = 2048, kStaticBatch = 2048;
+constexpr size_t kStaticItems = 3 * kStaticRows * kStaticRows / 1024 + 11 * kStaticRows / 64 + 2 * kStaticBatch + 2;
+constexpr size_t kStaticScoreFloats = 3 * kStaticRows * kStaticRows + 12 * kStaticRows + 4;
 constexpr size_t kStaticTokOff = 256;
 constexpr size_t kStaticItemsOff = kStaticTokOff + 16 * kStaticRows;
 constexpr size_t kStaticScoresOff = (kStaticItemsOff + 32 * kStaticItems + 255) / 256 * 256;
-constexpr size_t kStaticBytes = kStaticScoresOff + sizeof(float) * 3 * kStaticRows * kStaticRows;
+constexpr size_t kStaticBytes = kStaticScoresOff + sizeof(float) * kStaticScoreFloats;
 static_assert(kStaticItemsOff % 256 == 0, "sections stay 256-byte aligned");
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
@@ -464,9 +568,10 @@ __device__ __forceinline__ int last_le(const uint32_t* a, int n, uint32_t x) {
 // can address outside the rows or the scores section whatever the offsets
 // hold. One workgroup of kPlanThreads; batch <= kStaticBatch.
 __global__ void __launch_bounds__(kPlanThreads)
-attention_plan_kernel(const uint32_t* __restrict__ offsets, int batch, int rows, uint32_t* __restrict__ count,
+attention_plan_kernel(const uint32_t* __restrict__ offsets, int batch, int rows, uint32_t* __restrict__ counts,
                       uint4* __restrict__ tok, uint4* __restrict__ items) {
-  __shared__ uint32_t bound[kStaticBatch + 1], first_item[kStaticBatch + 1], first_score[kStaticBatch + 1];
+  __shared__ uint32_t bound[kStaticBatch + 1], first_sitem[kStaticBatch + 1], first_citem[kStaticBatch + 1];
+  __shared__ uint32_t first_score[kStaticBatch + 1];
   __shared__ uint32_t tmp[kPlanThreads];
   const int tid = threadIdx.x;
   const int nb = batch + 1, seg = (nb + kPlanThreads - 1) / kPlanThreads;
@@ -484,34 +589,48 @@ attention_plan_kernel(const uint32_t* __restrict__ offsets, int batch, int rows,
   __syncthreads();
   // Items and score floats per sequence, and their exclusive prefixes.
   const int s0 = min(tid * seg, batch), s1 = min(s0 + seg, batch);
-  uint32_t ni = 0, ns = 0;
+  uint32_t ni = 0, nc = 0, ns = 0;
   for (int s = s0; s < s1; ++s) {
-    const uint32_t len = bound[s + 1] - bound[s], qc = (uint32_t)query_chunk(len);
-    first_item[s] = ni;
+    const SeqPlan p = seq_plan(bound[s + 1] - bound[s]);
+    first_sitem[s] = ni;
+    first_citem[s] = nc;
     first_score[s] = ns;
-    ni += (len + kKeyBlock - 1) / kKeyBlock * ((len + qc - 1) / qc);
-    ns += 3 * len * len;
+    ni += (uint32_t)p.score_items;
+    nc += (uint32_t)p.context_items;
+    ns += (uint32_t)p.score_floats;
   }
-  uint32_t total_items, total_scores;
-  const uint32_t ibase = plan_scan<false>(ni, tmp, total_items);
+  uint32_t total_sitems, total_citems, total_scores;
+  const uint32_t ibase = plan_scan<false>(ni, tmp, total_sitems);
+  const uint32_t cbase = plan_scan<false>(nc, tmp, total_citems);
   const uint32_t sbase = plan_scan<false>(ns, tmp, total_scores);
+  const uint32_t score0 = (uint32_t)inv_floats((size_t)rows);
   for (int s = s0; s < s1; ++s) {
-    first_item[s] += ibase;
-    first_score[s] += sbase;
+    first_sitem[s] += ibase;
+    first_citem[s] += cbase;
+    first_score[s] += sbase + score0;
   }
   if (tid == 0) {
-    first_item[batch] = total_items;
-    first_score[batch] = total_scores;
-    *count = total_items;
+    first_sitem[batch] = total_sitems;
+    first_citem[batch] = total_citems;
+    first_score[batch] = total_scores + score0;
+    counts[0] = total_sitems;
+    counts[1] = total_citems;
   }
   __syncthreads();
-  for (uint32_t i = tid; i < total_items; i += kPlanThreads) {
-    const int s = last_le(first_item, batch, i);  // a sequence with items has first_item[s] < first_item[s + 1]
-    const uint32_t lo = bound[s], hi = bound[s + 1], len = hi - lo, qc = (uint32_t)query_chunk(len);
-    const uint32_t nq = (len + qc - 1) / qc, local = i - first_item[s];
-    const uint32_t k0 = lo + kKeyBlock * (local / nq), q = lo + qc * (local % nq);
-    items[2 * i] = make_uint4(lo, hi, k0, q);
-    items[2 * i + 1] = make_uint4(min(hi, q + qc), first_score[s], 0u, 0u);
+  for (uint32_t i = tid; i < total_sitems; i += kPlanThreads) {
+    const int s = last_le(first_sitem, batch, i);  // a sequence with items has first_sitem[s] < first_sitem[s + 1]
+    const uint32_t lo = bound[s], hi = bound[s + 1], pairs = 3 * (hi - lo);
+    const uint32_t np = (pairs + kSPairs - 1) / kSPairs, local = i - first_sitem[s];
+    const uint32_t k0 = lo + kSKeys * (local / np), p0 = kSPairs * (local % np);
+    items[2 * i] = make_uint4(lo, hi, k0, p0);
+    items[2 * i + 1] = make_uint4(min(pairs, p0 + kSPairs), first_score[s], 0u, 0u);
+  }
+  for (uint32_t i = tid; i < total_citems; i += kPlanThreads) {
+    const int s = last_le(first_citem, batch, i);
+    const uint32_t lo = bound[s], hi = bound[s + 1], pairs = 3 * (hi - lo);
+    const uint32_t p0 = kCPairs * (i - first_citem[s]);
+    items[2 * (total_sitems + i)] = make_uint4(lo, hi, p0, min(pairs, p0 + kCPairs));
+    items[2 * (total_sitems + i) + 1] = make_uint4(first_score[s], 0u, 0u, 0u);
   }
   for (uint32_t t = tid; t < (uint32_t)rows; t += kPlanThreads) {
     const int s = last_le(bound, batch, t);  // bound[s] <= t < bound[s + 1]
@@ -554,15 +673,15 @@ hipError_t launch_attention_static(const float* qkv, const uint32_t* offsets, in
   unsigned char* base = nullptr;
   hipError_t e = static_scratch(&base);
   if (e != hipSuccess) return e;
-  uint32_t* count = reinterpret_cast<uint32_t*>(base);
+  uint32_t* counts = reinterpret_cast<uint32_t*>(base);
   uint32_t* tok = reinterpret_cast<uint32_t*>(base + kStaticTokOff);
   uint32_t* items = reinterpret_cast<uint32_t*>(base + kStaticItemsOff);
   float* scores = reinterpret_cast<float*>(base + kStaticScoresOff);
-  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, batch, rows, count,
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, offsets, batch, rows, counts,
                      reinterpret_cast<uint4*>(tok), reinterpret_cast<uint4*>(items));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_attention(qkv, items, count, kAttentionScoreGrid, tok, window, rows, scores, cq, cd, st);
+  return launch_attention(qkv, items, counts, kAttentionGrid, tok, window, rows, scores, cq, cd, st);
 }
 
 }  // namespace eg2

@@ -89,11 +89,12 @@ int eg2_attention_plan(const size_t* offsets, size_t batch, size_t items_cap, si
   if (!offsets || !items || !tok || !counts) return -1;
   for (size_t s = 0; s < batch; ++s)
     if (offsets[s + 1] < offsets[s] || offsets[s + 1] > (1u << 24)) return -1;
-  eg2::AttentionCounts used{0, 0};
-  const bool ok = eg2::build_attention_plan(offsets, batch, eg2::AttentionCounts{items_cap, scores_cap}, items, tok,
-                                            &used);
+  eg2::AttentionCounts used{0, 0, 0};
+  const bool ok = eg2::build_attention_plan(offsets, batch, eg2::AttentionCounts{items_cap, scores_cap, 0}, items,
+                                            tok, &used);
   counts[0] = used.items;
   counts[1] = used.score_floats;
+  counts[2] = used.score_items;
   return ok ? 0 : -1;
 }
 

@@ -530,9 +530,10 @@ def attention_capacity(tokens, batch):
 
 
 def attention_plan(offsets, rows=None):
-    """(items uint32 [n, 8], tok uint32 [rows, 4], score floats) of the
-    sequences [offsets[s], offsets[s+1]) (eg2_attention_plan); rows defaults
-    to offsets[-1], and every row must belong to a sequence."""
+    """(items uint32 [n, 8], tok uint32 [rows, 4], score floats, score item
+    count) of the sequences [offsets[s], offsets[s+1]) (eg2_attention_plan):
+    the score items, then the context items; rows defaults to offsets[-1],
+    and every row must belong to a sequence."""
     import numpy as np
 
     offs = (C.c_size_t * len(offsets))(*[int(o) for o in offsets])
@@ -541,28 +542,28 @@ def attention_plan(offsets, rows=None):
     cap_items, cap_scores = attention_capacity(max(total, 1), max(batch, 1))
     items = np.zeros((cap_items, 8), dtype=np.uint32)
     tok = np.zeros((max(rows, total, 1), 4), dtype=np.uint32)
-    counts = (C.c_size_t * 2)()
+    counts = (C.c_size_t * 3)()
     rc = lib().eg2_attention_plan(offs, batch, cap_items, cap_scores, items.ctypes.data, tok.ctypes.data, counts)
     if rc != 0:
         raise HipError("attention plan exceeds its capacity")
-    return items[:counts[0]], tok[:rows], int(counts[1])
+    return items[:counts[0]], tok[:rows], int(counts[1]), int(counts[2])
 
 
 class AttentionPlan:
-    """The attention plan of a packing on the device (work items, their
-    count, token records) and its scores scratch."""
+    """The attention plan of a packing on the device (work items, their two
+    counts, token records) and its scores scratch."""
 
-    GRID = 512  # scores workgroups striding over the items (the executor's choice)
+    GRID = 1024  # workgroups striding over each item list (the executor's choice)
 
     def __init__(self, offsets, device, rows=None):
         import numpy as np
         import torch
 
-        items, tok, score_floats = attention_plan(offsets, rows)
+        items, tok, score_floats, score_items = attention_plan(offsets, rows)
         self.n_items = len(items)
         self.items = torch.from_numpy(np.ascontiguousarray(items).view(np.int32).reshape(-1).copy()
                                       if len(items) else np.zeros(8, np.int32)).to(device)
-        self.count = torch.tensor([len(items)], dtype=torch.int32, device=device)
+        self.count = torch.tensor([score_items, len(items) - score_items], dtype=torch.int32, device=device)
         self.tok = torch.from_numpy(np.ascontiguousarray(tok).view(np.int32).reshape(-1).copy()).to(device)
         self.scores = torch.zeros(max(1, score_floats), dtype=torch.float32, device=device)
         self.rows = tok.shape[0]
@@ -627,7 +628,7 @@ class ops:
                                       cls._p(plan.tok), window, qkv.shape[0], cls._p(plan.scores), cls._p(cq),
                                       cls._p(cd), cls._stream()), "attention")
 
-    STATIC_ROWS, STATIC_BATCH = 2048, 4096  # EG2_ATTENTION_STATIC_ROWS / _BATCH
+    STATIC_ROWS, STATIC_BATCH = 2048, 2048  # EG2_ATTENTION_STATIC_ROWS / _BATCH
 
     @classmethod
     def attention_static(cls, qkv, offsets_d, window, cq, cd):

@@ -61,16 +61,18 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * the keys of its own sequence, limited to |t - s| <= window/2 when window >
  * 0; 3 query heads share one KV head, head_dim 256; scores in the
  * reference's dot order (the SSE2 ei_dot_f32), expf as the host libm
- * computes it, the sequential sum and context accumulation in key order;
- * the context row is then quantized to Q8_0 (quants.c:97-177) into cq (row
- * tiles, k = 768) and cd [24][rows]. qkv: rows of [q0 q1 q2 | k | v] as
+ * computes it, the sequential sum and context accumulation in key order
+ * (products on fp32 MFMA, each rounded once as a multiply); the context
+ * row is then quantized to Q8_0 (quants.c:97-177) into cq (row tiles, k =
+ * 768) and cd [24][rows]. qkv: rows of [q0 q1 q2 | k | v] as
  * eg2_hip_qk_norm_rope leaves them. items / tok: the plan of
- * eg2_attention_plan on the device (*item_count items; `grid` workgroups
- * stride over them; tok holds one record for each of the `rows` rows, so
- * every row must belong to a planned sequence, e.g. a padding one).
- * scores: scratch of at least the plan's score count (counts[1]) floats.
- * rows % 4 == 0. A sequence's result does not depend on its place in the
- * wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
+ * eg2_attention_plan on the device; item_count: 2 uint32 on the device,
+ * the score items (first in `items`) and the context items after them;
+ * `grid` workgroups stride over each list; tok holds one record for each
+ * of the `rows` rows, so every row must belong to a planned sequence, e.g.
+ * a padding one. scores: scratch of at least the plan's score floats
+ * (counts[1]). rows % 4 == 0. A sequence's result does not depend on its
+ * place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
                       const uint32_t *tok, unsigned window, unsigned rows, float *scores, int8_t *cq, float *cd,
                       void *stream);
@@ -82,7 +84,7 @@ int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *i
  * sequence bounds offsets[0..batch] (uint32; offsets[0] is read as 0 and
  * offsets[batch] as rows, every row must belong to a sequence, e.g. a
  * padding one), and the plan and scores live in a static array of this
- * library, one per GPU, of 48.4 MiB, held until the process ends. The
+ * library, one per GPU, of 48.6 MiB, held until the process ends. The
  * call allocates nothing; it rejects (hipErrorInvalidValue, nothing
  * launched) rows above EG2_ATTENTION_STATIC_ROWS, batch above
  * EG2_ATTENTION_STATIC_BATCH or rows % 4 != 0. The stream must belong to
@@ -90,19 +92,21 @@ int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *i
  * race; calls in one stream are ordered. Results are bit-identical to
  * eg2_hip_attention's. */
 #define EG2_ATTENTION_STATIC_ROWS 2048u
-#define EG2_ATTENTION_STATIC_BATCH 4096u
+#define EG2_ATTENTION_STATIC_BATCH 2048u
 int eg2_hip_attention_static(const float *qkv, const uint32_t *offsets, unsigned batch, unsigned window,
                              unsigned rows, int8_t *cq, float *cd, void *stream);
 
 /* Host: the plan of eg2_hip_attention for the sequences [offsets[s],
- * offsets[s+1]): the scores kernel's work items (8 uint32 each: sequence
- * start, end, first key of a 64-key block, first query, end of the
- * queries, the sequence's first score index, 0, 0) and one token record
- * per token (4 uint32: sequence start, end, first score index, 0) at
- * tok[4 t]. counts[0] = items, counts[1] = score floats (3 n^2 per sequence
- * of n tokens). Writes the lists and returns 0 when they fit items_cap
- * items and scores_cap score floats; otherwise writes nothing and returns
- * -1 (counts still report the need). */
+ * offsets[s+1]) (rows = offsets[batch]): the score items of every
+ * sequence (per sequence of n tokens, ceil(n/32) key blocks x ceil(3n/32)
+ * pair blocks), then its context items (ceil(3n/64) pair blocks), 8
+ * uint32 each as eg2_hip_attention reads them, and one token record per
+ * token (4 uint32: sequence start, end, first score index, 0) at tok[4 t].
+ * counts[0] = items of both kinds, counts[1] = score floats (ceil4(3 rows)
+ * for the 1/sum values, then 3 n ceil4(n) per sequence), counts[2] = score
+ * items. Writes the lists and returns 0 when they fit items_cap items and
+ * scores_cap score floats; otherwise writes nothing and returns -1 (counts
+ * still report the need). */
 int eg2_attention_plan(const size_t *offsets, size_t batch, size_t items_cap, size_t scores_cap, uint32_t *items,
                        uint32_t *tok, size_t *counts);
 

@@ -95,27 +95,39 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
 
 
 def test_attention_plan_covers_each_sequence(eg2):
-    """Every (query, key) pair of each sequence is covered by exactly one
-    scores item (64-key blocks from the sequence start, query chunks of 8,
-    16 or 32 tokens by length); each sequence's scores take 3 n^2 floats
+    """Every (pair, key) of each sequence (pair = 3 (token - start) + head)
+    is covered by exactly one score item (32-key blocks from the sequence
+    start times 32-pair blocks), every pair by exactly one context item
+    (64-pair blocks), the score items coming first; the 1/sum area takes
+    ceil4(3 rows) floats, then each sequence's scores 3 n ceil4(n) floats
     after the previous ones; every token's record names its sequence and
     that first score index."""
     offs = [0, 1, 33, 97, 98, 200, 600, 1100, 3150]
-    items, tok, score_floats = eg2.attention_plan(offs)
+    items, tok, score_floats, n_score = eg2.attention_plan(offs)
     seqs = [(offs[s], offs[s + 1]) for s in range(len(offs) - 1)]
-    base = np.concatenate([[0], np.cumsum([3 * (b - a) ** 2 for a, b in seqs])])
+    c4 = lambda n: (n + 3) // 4 * 4  # noqa: E731
+    base = np.concatenate([[c4(3 * offs[-1])],
+                           c4(3 * offs[-1]) + np.cumsum([3 * (b - a) * c4(b - a) for a, b in seqs])])
     assert score_floats == base[-1]
-    covered = {s: np.zeros((hi - lo, hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
-    for lo, hi, k0, q0, q1, sb, z0, z1 in items.astype(np.int64):
+    covered = {s: np.zeros((3 * (hi - lo), hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
+    ctx = {s: np.zeros(3 * (hi - lo), int) for s, (lo, hi) in enumerate(seqs)}
+    for i, (lo, hi, f2, f3, f4, f5, f6, f7) in enumerate(items.astype(np.int64)):
         s = seqs.index((lo, hi))
         n = hi - lo
-        qc = 8 if n <= 128 else (16 if n <= 512 else 32)
-        assert sb == base[s] and z0 == z1 == 0
-        assert lo <= k0 < hi and (k0 - lo) % 64 == 0
-        assert lo <= q0 < q1 <= hi and (q0 - lo) % qc == 0 and q1 == min(hi, q0 + qc)
-        covered[s][q0 - lo:q1 - lo, k0 - lo:min(hi, k0 + 64) - lo] += 1
+        if i < n_score:
+            k0, p0, p1, sb = f2, f3, f4, f5
+            assert sb == base[s] and f6 == f7 == 0
+            assert lo <= k0 < hi and (k0 - lo) % 32 == 0
+            assert 0 <= p0 < p1 <= 3 * n and p0 % 32 == 0 and p1 == min(3 * n, p0 + 32)
+            covered[s][p0:p1, k0 - lo:min(hi, k0 + 32) - lo] += 1
+        else:
+            p0, p1, sb = f2, f3, f4
+            assert sb == base[s] and f5 == f6 == f7 == 0
+            assert p0 % 64 == 0 and p1 == min(3 * n, p0 + 64)
+            ctx[s][p0:p1] += 1
     for s in covered:
         assert (covered[s] == 1).all(), s
+        assert (ctx[s] == 1).all(), s
     for s, (lo, hi) in enumerate(seqs):
         assert (tok[lo:hi] == [lo, hi, base[s], 0]).all()
 
@@ -126,14 +138,16 @@ def test_attention_plan_checks_capacity_before_writing(eg2):
     import ctypes as C
 
     offs = [0, 700, 1500]
-    need_items = len(eg2.attention_plan(offs)[0])
+    items0, _, need_scores, n_score = eg2.attention_plan(offs)
+    need_items = len(items0)
+    assert need_scores == 4500 + 3 * (700 * 700 + 800 * 800)
     arr = (C.c_size_t * 3)(*offs)
     items = np.full((need_items, 8), 7, np.uint32)
     tok = np.full((1500, 4), 7, np.uint32)
-    counts = (C.c_size_t * 2)()
-    for cap_items, cap_scores in ((need_items - 1, 1 << 30), (need_items, 3 * (700 ** 2 + 800 ** 2) - 1)):
+    counts = (C.c_size_t * 3)()
+    for cap_items, cap_scores in ((need_items - 1, 1 << 30), (need_items, need_scores - 1)):
         rc = eg2.lib().eg2_attention_plan(arr, 2, cap_items, cap_scores, items.ctypes.data, tok.ctypes.data, counts)
-        assert rc == -1 and list(counts) == [need_items, 3 * (700 ** 2 + 800 ** 2)]
+        assert rc == -1 and list(counts) == [need_items, need_scores, n_score]
         assert (items == 7).all() and (tok == 7).all()
 
 
@@ -141,8 +155,8 @@ def test_attention_capacity_bounds_every_packing(eg2):
     """The executor sizes its plan with eg2_attention_capacity(2080, 2049)
     (a 2048-token wave plus a padding sequence of up to 31 rows): no packing
     may exceed it. Every packing of equal sequences (the per-sequence
-    rounding of blocks and chunks is worst there) and every remainder, each
-    followed by its padding sequence."""
+    rounding of blocks is worst there) and every remainder, each followed by
+    its padding sequence."""
     cap = eg2.attention_capacity(2080, 2049)
     worst = [0, 0]
     for L in range(1, 2049):
@@ -151,7 +165,7 @@ def test_attention_capacity_bounds_every_packing(eg2):
             n = sum(lens)
             pad = (-n) % 32
             offs = np.concatenate([[0], np.cumsum(lens + ([pad] if pad else []))])
-            items, _, score_floats = eg2.attention_plan(offs)
+            items, _, score_floats, _ = eg2.attention_plan(offs)
             got = [len(items), score_floats]
             worst = [max(a, b) for a, b in zip(worst, got)]
             assert all(g <= c for g, c in zip(got, cap)), (L, total, got, cap)

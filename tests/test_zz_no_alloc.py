@@ -93,7 +93,7 @@ def test_static_attention_rejects_sizes_beyond_its_array(eg2, gpu):
     lib, s = eg2.lib(), C.c_void_p(torch.cuda.current_stream().cuda_stream)
     invalid = 1  # hipErrorInvalidValue
     assert lib.eg2_hip_attention_static(p(qkv), p(offs), 1, 0, rows, p(cq), p(cd), s) == invalid
-    assert lib.eg2_hip_attention_static(p(qkv), p(offs), 4097, 0, 2048, p(cq), p(cd), s) == invalid
+    assert lib.eg2_hip_attention_static(p(qkv), p(offs), 2049, 0, 2048, p(cq), p(cd), s) == invalid
     assert lib.eg2_hip_attention_static(p(qkv), p(offs), 1, 0, 2046, p(cq), p(cd), s) == invalid
     assert lib.eg2_hip_attention_static(p(qkv), p(offs), 0, 0, 2048, p(cq), p(cd), s) == invalid
     torch.cuda.synchronize()
