@@ -29,8 +29,10 @@
 // 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Per block, the
 // four operand tiles and the 64 + 64 scales go by DMA into a 4-stage LDS
 // ring (each wave moves one tile and one scale vector), two blocks in
-// flight beyond the one being read; the MFMA of block kb + 1 is issued
-// before the scaling of block kb. In the MFMA 32x32 output layout a lane
+// flight beyond the one being read. After each barrier the fragments of
+// block kb + 1 are requested from LDS, the two multiply phases of block
+// kb's scaling cover their latency, then the MFMA of block kb + 1 is
+// issued and block kb's adds follow. In the MFMA 32x32 output layout a lane
 // holds one column and 16 rows; each row's activation scale reaches it
 // through a DPP row broadcast folded into the multiply.
 #include <utility>
@@ -83,20 +85,24 @@ __device__ __forceinline__ float row_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + V, 0xf, 0xf, true));
 }
 
-// acc[v] += ((dot[v] * d_w) * d_x(row v)) from the biased MFMA result; the
+// t[v] = (dot[v] * d_w) * d_x(row v) from the biased MFMA result; the
 // lane's 16 output rows take their activation scales from lanes 0..15 of
-// its 16-lane row. The three phases are kept apart so 16 independent
-// operations separate each dependent pair.
+// its 16-lane row. The two phases are kept apart so 16 independent
+// operations separate each dependent pair; accumulate_products then adds
+// t to acc (the third phase), after the next block's MFMA is issued.
 template <int... V>
-__device__ __forceinline__ void scale_accumulate(floatx16& acc, const intx16& biased, float dw, float dxv,
-                                                 std::integer_sequence<int, V...>) {
+__device__ __forceinline__ floatx16 scale_products(const intx16& biased, float dw, float dxv,
+                                                   std::integer_sequence<int, V...>) {
   const float bias = dw * -kMagic;
   const floatx16 f = __builtin_bit_cast(floatx16, biased);
   floatx16 t;
   ((t[V] = __builtin_fmaf(f[V], dw, bias)), ...);
   __builtin_amdgcn_sched_barrier(0);
   ((t[V] = t[V] * row_bcast<V>(dxv)), ...);
-  __builtin_amdgcn_sched_barrier(0);
+  return t;
+}
+template <int... V>
+__device__ __forceinline__ void accumulate_products(floatx16& acc, const floatx16& t, std::integer_sequence<int, V...>) {
   ((acc[V] = acc[V] + t[V]), ...);
 }
 
@@ -249,10 +255,17 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   auto step = [&](int j, int kb) {
     const int cur = j & 1, nxt = cur ^ 1;
     issue((j + kStages - 1) % kStages, kb + kStages - 1);
+    // The barrier's wait is asm the compiler does not see; marking these
+    // registers redefined here puts its own wait for their loads before
+    // the barrier, not after the next fragment reads.
+    asm volatile("" : "+v"(f[cur].dx), "+v"(f[cur].dw));
     wait_barrier<2 * (kStages - 2)>();
     f[nxt] = frag((j + 1) % kStages);
+    const floatx16 t = scale_products(d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+    __builtin_amdgcn_sched_barrier(0);
     d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
-    scale_accumulate(acc, d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+    __builtin_amdgcn_sched_barrier(0);
+    accumulate_products(acc, t, std::make_integer_sequence<int, 16>{});
   };
   int kb0 = 0;
   for (; kb0 + kStages <= nb; kb0 += kStages) {
@@ -401,10 +414,17 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
   auto step = [&](int j, int kb) {
     const int cur = j & 1, nxt = cur ^ 1;
     issue((j + kStages - 1) % kStages, kb + kStages - 1);
+    // The barrier's wait is asm the compiler does not see; marking these
+    // registers redefined here puts its own wait for their loads before
+    // the barrier, not after the next fragment reads.
+    asm volatile("" : "+v"(f[cur].dx), "+v"(f[cur].dw));
     wait_barrier<3 * (kStages - 2)>();
     f[nxt] = frag((j + 1) % kStages);
+    const floatx16 t = scale_products(d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+    __builtin_amdgcn_sched_barrier(0);
     d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
-    scale_accumulate(acc, d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+    __builtin_amdgcn_sched_barrier(0);
+    accumulate_products(acc, t, std::make_integer_sequence<int, 16>{});
   };
   int kb0 = 0;
   for (; kb0 + kStages <= nb; kb0 += kStages) {
