@@ -148,14 +148,18 @@ __host__ __device__ inline float tanhf(float x) {
 }
 
 // The same function as tanhf, for finite x, written without branches so
-// that a wave whose lanes fall in different cases runs one path: every case
-// of expm1f's reconstruction is computed and the lane's own selected. The
-// arithmetic of each case is fdlibm's unchanged. The argument reduction is
-// shared: fdlibm's k = 0 (no reduction, c = 0) and k = +-1 (x -+ ln2_hi,
-// lo = +-ln2_lo) cases are its general formula hi = x - k ln2_hi,
-// lo = k ln2_lo at k = 0 and +-1 (both products exact), so only the choice
-// of k differs between them. Inside tanhf expm1f sees 2|x| >= 2 or
-// -2|x| in (-2, 0), which keeps it off its overflow and saturation cases.
+// that a wave whose lanes fall in different cases runs one path. Inside
+// tanhf, expm1f sees a = 2|x| >= 2 or a = -2|x| in (-2, 0], so of its
+// reconstructions only these occur: k = 0, k = -1, k <= -2 ("1 - (e - r)",
+// scaled, minus 1), 2 <= k <= 22 ("(1 - 2^-k) - (e - r)", scaled) and
+// 23 <= k ("r - (e + 2^-k) + 1", scaled). The k <= -2 and the 2..22 cases
+// share "T - (e - r)" and the scaling, T = 1 or 1 - 2^-k. For k > 56,
+// where fdlibm uses the k <= -2 form, |x| > 19.6 and tanhf is 1 either
+// way (2 / (t + 2) is below half an ulp of 1 once |x| > 9.02), so the 23 <=
+// k form serves. The argument reduction is shared: fdlibm's k = 0 (no
+// reduction, c = 0) and k = -1 (x + ln2_hi, lo = -ln2_lo) cases are its
+// general formula hi = x - k ln2_hi, lo = k ln2_lo at those k (both
+// products exact). Each operation is fdlibm's, in its order.
 __host__ __device__ inline float tanhf_flat(float x) {
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
   const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
@@ -165,14 +169,14 @@ __host__ __device__ inline float tanhf_flat(float x) {
   const float ax = __builtin_fabsf(x);
   const float a = big ? 2.0f * ax : -2.0f * ax;  // expm1f's argument
   const uint32_t ha = fbits(a) & 0x7fffffffu;
-  // k: 0 for |a| <= 0.5 ln2, +-1 below 1.5 ln2, else the rounded a / ln2.
+  // k: 0 for |a| <= 0.5 ln2, -1 below 1.5 ln2 (a >= 2 never is), else the
+  // rounded a / ln2.
   const int32_t kr = (int32_t)(invln2 * a + (big ? 0.5f : -0.5f));
-  const int32_t k = ha <= 0x3eb17218u ? 0 : (ha < 0x3F851592u ? (big ? 1 : -1) : kr);
+  const int32_t k = ha <= 0x3eb17218u ? 0 : (ha < 0x3F851592u ? -1 : kr);
   const float t = (float)k;
   const float hi = a - t * ln2_hi, lo = t * ln2_lo;
   const float r = hi - lo;
   const float c = (hi - r) - lo;
-  const bool tiny = ha < 0x33000000u;  // |a| < 2^-25: expm1f(a) = a
   const float hfx = 0.5f * r;
   const float hxs = r * hfx;
   const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
@@ -180,17 +184,23 @@ __host__ __device__ inline float tanhf_flat(float x) {
   const float e0 = hxs * ((r1 - tt) / (6.0f - r * tt));
   float e = r * (e0 - c) - c;
   e -= hxs;
-  // The reconstructions, k = 0, -1, 1, |k| large, 2 <= k < 23, 23 <= k <= 56.
-  const float v0 = r - (r * e0 - hxs);
-  const float vm1 = 0.5f * (r - e) - 0.5f;
-  const float vp1 = r < -0.25f ? -2.0f * (e - (r + 0.5f)) : 1.0f + 2.0f * (r - e);
   const uint32_t kbits = (uint32_t)k << 23;
-  const float vout = ffrom(fbits(1.0f - (e - r)) + kbits) - 1.0f;
-  const int32_t kc = k < 1 ? 1 : (k > 31 ? 31 : k);  // shift counts kept in range; used only where k fits
-  const float vlow = ffrom(fbits(ffrom(0x3f800000u - (0x1000000u >> kc)) - (e - r)) + kbits);
-  const float vmid = ffrom(fbits((r - (e + ffrom((uint32_t)(0x7f - (k > 56 ? 56 : k)) << 23))) + 1.0f) + kbits);
-  float em1 = k == 0 ? v0 : (k == -1 ? vm1 : (k == 1 ? vp1 : ((k <= -2 || k > 56) ? vout : (k < 23 ? vlow : vmid))));
-  em1 = tiny ? a : em1;
+  const float v0 = r - (r * e0 - hxs);          // k = 0
+  const float vm1 = 0.5f * (r - e) - 0.5f;      // k = -1
+  const int32_t kl = k < 1 ? 1 : (k > 22 ? 22 : k);
+  const float T = k < 0 ? 1.0f : ffrom(0x3f800000u - (0x1000000u >> kl));
+  const float w = ffrom(fbits(T - (e - r)) + kbits);
+  const float vlo = k < 0 ? w - 1.0f : w;       // k <= -2, or 2 <= k <= 22
+  const int32_t kh = k < 23 ? 23 : (k > 126 ? 126 : k);
+  const float vhi = ffrom(fbits((r - (e + ffrom((uint32_t)(0x7f - kh) << 23))) + 1.0f) + kbits);  // k >= 23
+#ifdef __HIP_DEVICE_COMPILE__
+  // All four are computed for every lane (the compiler would otherwise
+  // turn the selection below into branches, which a divergent wave runs
+  // one after the other).
+  asm volatile("" ::"v"(v0), "v"(vm1), "v"(vlo), "v"(vhi));
+#endif
+  float em1 = k == 0 ? v0 : (k == -1 ? vm1 : (k >= 23 ? vhi : vlo));
+  em1 = ha < 0x33000000u ? a : em1;  // |a| < 2^-25: expm1f(a) = a
   // tanhf's tail: one division, 2 / (t + 2) or -t / (t + 2).
   const float q = (big ? 2.0f : -em1) / (em1 + 2.0f);
   float z = big ? 1.0f - q : q;
