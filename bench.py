@@ -18,7 +18,8 @@ The roofline entry times the dominant kernel (the gate|up projection GEMM,
 epilogue) with HIP events on the stream it runs on; beside the int8 MFMA
 roofline it reports the floor the exact Q8_0 scaling puts on the VALU
 (3 fp32 operations per output per 32-block), which is what bounds the
-kernel. The CPU
+kernel, and the share of the int8 MFMA peak the kernel would reach at that
+floor (about 17%: bit-exact scaling caps MFMA use there). The CPU
 baseline is the oracle (the C restatement of the reference CPU path) on the
 same wave, timed on the host's cores.
 """
@@ -35,15 +36,14 @@ sys.path.insert(0, ROOT)
 TOKENS, SEQS, LAYERS = 2048, 16, 24
 GEMM_N, GEMM_M, GEMM_K = 2048, 2 * 1152, 768
 PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA (the projection GEMMs)
-# Attention's exact-order arithmetic runs on the VALU as separate fp32
-# multiplies and adds (no FMA, no packed fp32): 16 lanes per SIMD, 1024
-# SIMDs at 2.4 GHz = 39.3 T operations/s, the peak its FLOP count is held to.
+# The VALU: 16 lanes per SIMD, 1024 SIMDs at 2.4 GHz = 39.3 T fp32
+# operations/s without packed fp32 (not used here); a wave64 instruction
+# occupies its SIMD for 4 cycles. Exact attention adds its products (made
+# on fp32 MFMA) one rounded VALU add at a time: its floor is those adds.
 PEAK_VALU_TOPS = 1024 * 16 * 2.4e9 / 1e12
 HEAD_DIM = 256
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
-# The exact Q8_0 scaling is 3 fp32 VALU operations per output per 32-block;
-# a wave64 fp32 VALU instruction occupies a SIMD for 4 cycles (no packed
-# fp32 here), 1024 SIMDs at the 2.4 GHz peak engine clock.
+# The exact Q8_0 scaling is 3 fp32 VALU operations per output per 32-block.
 VALU_WAVE_INSTR_PER_US = 1024 * 2400.0 / 4
 METRIC = "embedded tokens/s @2048-tok packed waves (1 GPU); Q8_0 GEMM % MFMA peak"
 
@@ -151,11 +151,13 @@ def time_gemm(eg2, torch, steps, warmup):
 
 def kernel_table(eg2, torch, steps):
     """Every kernel of one 2048-token layer (16 x 128 packing), launched
-    alone on synthetic inputs of its real shape: average us, and the
-    achieved rate against its roofline -- int8 MFMA for the projection
-    GEMMs, fp16 MFMA for attention (algorithmic 3072 * sum L^2 FLOP; the
-    kernel runs 3 split-fp16 passes of it), HBM for the row kernels
-    (algorithmic bytes: each input read once, each output written once)."""
+    alone on synthetic inputs of its real shape, back to back: average us
+    per launch (each includes the fixed cost of a launch), and the achieved
+    rate against its roofline -- int8 MFMA for the projection GEMMs with
+    the floor their exact scaling puts on the VALU (3 fp32 operations per
+    output per 32-block), the VALU adds for attention (its products run on
+    fp32 MFMA), HBM for the row kernels (algorithmic bytes: each input read
+    once, each output written once)."""
     import numpy as np
 
     dev = torch.device("cuda:0")
@@ -163,10 +165,17 @@ def kernel_table(eg2, torch, steps):
     T, E, F, D = TOKENS, 768, 1152, 256
     out = {}
 
-    def rec(name, ms, work, unit, peak):
+    def rec(name, ms, work, unit, peak, valu_instr=None):
         rate = work / (ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
         out[name] = {"us": round(ms * 1e3, 2), "achieved": round(rate, 1), "unit": unit, "peak": peak,
                      "frac": round(rate / peak, 4)}
+        if valu_instr is not None:
+            floor = valu_instr / VALU_WAVE_INSTR_PER_US
+            out[name]["valu_floor_us"] = round(floor, 2)
+            out[name]["valu_floor_frac"] = round(floor / (ms * 1e3), 4)
+
+    def scaling_instr(m, k):
+        return T * m * (k // 32) * 3 // 64
 
     for name, (m, k) in {"gemm_o 2048x768x768": (E, E),
                          "gemm_gate_up_geglu 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
@@ -176,7 +185,7 @@ def kernel_table(eg2, torch, steps):
             ms = time_launches(torch, lambda: eg2.ops.gemm_q8_geglu(xq, xd, wq, wd, gq, gd, T), steps, 3)
         else:
             ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
-        rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS)
+        rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS, scaling_instr(m, k))
 
     rnd = lambda *shape: torch.randn(*shape, generator=g).to(dev)
     w_e, w_d = torch.ones(E, device=dev), torch.ones(D, device=dev)
@@ -203,7 +212,8 @@ def kernel_table(eg2, torch, steps):
     xq, xd, wq, wd, _ = gemm_operands(eg2, torch, T, eg2.QKV_COLS, E, g)
     ms = time_launches(torch, lambda: eg2.ops.gemm_q8_qkv_rope(xq, xd, wq, wd, T, w_d, w_d, rope, pos, 1e-6, qkv),
                        steps, 3)
-    rec("gemm_qkv_rope 2048x1280x768", ms, 2.0 * T * eg2.QKV_COLS * E, "TFLOP/s", PEAK_INT8_TOPS)
+    rec("gemm_qkv_rope 2048x1280x768", ms, 2.0 * T * eg2.QKV_COLS * E, "TFLOP/s", PEAK_INT8_TOPS,
+        scaling_instr(eg2.QKV_COLS, E))
     # Attention on realistic operands: the QKV rows of unit-scale activations.
     qkv.copy_(torch.randn((T, eg2.QKV_COLS), generator=g).to(dev))
     eg2.ops.qk_norm_rope(qkv, w_d, w_d, rope, pos, 1e-6, qkv)
@@ -211,13 +221,12 @@ def kernel_table(eg2, torch, steps):
     cd = torch.zeros((E // 32, T), device=dev)
     att = eg2.AttentionPlan(offsets, dev)
     ms = time_launches(torch, lambda: eg2.ops.attention_planned(qkv, att, 0, cq, cd), steps, 3)
-    # Exact (reference-order) attention runs on the VALU: 2 fp32 operations
-    # (multiply, add) per dimension per (query, key, head) for the scores
-    # and again for the context.
-    pairs = 3.0 * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS))
-    rec("attention 16x128", ms, 3072.0 * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS)), "TFLOP/s",
-        PEAK_VALU_TOPS)
-    out["attention 16x128"]["valu_floor_us"] = round(pairs * 4 * HEAD_DIM / (VALU_WAVE_INSTR_PER_US * 64), 2)
+    # Exact (reference-order) attention: every product on fp32 MFMA, every
+    # addition a rounded VALU add -- one per dimension per (query, key,
+    # head) for the scores and again for the context; the rate below counts
+    # those adds against the VALU peak.
+    adds = 2.0 * 3 * HEAD_DIM * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS))
+    rec("attention 16x128", ms, adds, "TFLOP/s", PEAK_VALU_TOPS, adds / 64)
     return out
 
 
@@ -425,7 +434,8 @@ def main():
             f"{valu_floor_us:.2f} us ({100 * valu_floor_us / (gemm_ms * 1e3):.0f}% of the kernel's time)")
         kernels = {} if args.no_kernel_table else kernel_table(eg2, torch, max(20, args.steps))
         for name, k in kernels.items():
-            log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak")
+            floor = f"  VALU floor {k['valu_floor_us']:.2f} us ({100 * k['valu_floor_frac']:.0f}%)" if "valu_floor_us" in k else ""
+            log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak{floor}")
 
         cpu = None
         if not args.no_cpu_baseline:
@@ -455,9 +465,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 x int8 -> int32 -> fp32 (Q8_0 GEMMs, exact); attention on fp16 MFMA with fp32 operands "
-                 "split into fp16 hi+lo pairs (3 passes, ~2^-21 relative per product), fp32 accumulation and "
-                 "softmax; fp32 row ops",
+        "dtype": "int8 x int8 -> int32 -> fp32 (Q8_0 GEMMs); fp32 attention (products on fp32 MFMA, each "
+                 "rounded once as a multiply; adds, softmax and expf in the reference's order); fp32 row ops -- "
+                 "every kernel bit-identical to the reference CPU path",
         "data": "synthetic",
         "config": {"workload": "24-layer Q8_0 EmbeddingGemma-300M-shape encoder forward + dense head, one "
                                "packed wave of 16x128 tokens", "tokens_per_wave": TOKENS, "sequences": SEQS,
@@ -471,7 +481,8 @@ def main():
                      "valu_floor": {"wave_instructions": scaling_instr, "floor_us": round(valu_floor_us, 2),
                                     "frac": round(valu_floor_us / (gemm_ms * 1e3), 4),
                                     "what": "exact per-block scaling only: 3 fp32 VALU ops per output per "
-                                            "32-block at 4 cycles per wave64 instruction on 1024 SIMDs, 2.4 GHz"}},
+                                            "32-block at 4 cycles per wave64 instruction on 1024 SIMDs, 2.4 GHz"},
+                     "mfma_cap_at_valu_floor": round(flops / (valu_floor_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)},
         "kernels": kernels,
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),

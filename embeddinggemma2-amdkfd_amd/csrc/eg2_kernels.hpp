@@ -48,10 +48,12 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // stride over each item list. scores: the plan's score floats (the 1/sum
 // of each (token, head) at [3 t + h], then a row of ceil4(n) scores per
 // pair of each sequence of n tokens). The context is quantized to Q8_0
-// into cq (row tiles, k = 768) and cd [24][rows]. rows % 4 == 0.
+// into cq (row tiles, k = 768) and cd [24][rows]. rows % 4 == 0. longest:
+// the longest sequence of the packing, which picks the softmax's kernel
+// form (0 = not known: the form for any length); the results are the same.
 hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
-                            const uint32_t* tok, int window, int rows, float* scores, int8_t* cq, float* cd,
-                            hipStream_t st);
+                            const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
+                            float* cd, hipStream_t st);
 
 // The plan of launch_attention for the sequences [offsets[s], offsets[s+1])
 // (rows = offsets[batch]): a sequence of n tokens has ceil(n/32) key

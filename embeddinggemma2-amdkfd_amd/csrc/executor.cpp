@@ -43,6 +43,12 @@ namespace {
 
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
 constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
+// The attention's softmax takes one of two equivalent kernel forms by the
+// wave's longest sequence (up to 512 tokens: one kernel); a graph is kept
+// per padded row count and form.
+constexpr unsigned kShortSoftmaxLen = 512;
+inline unsigned attention_form(unsigned longest) { return longest <= kShortSoftmaxLen ? kShortSoftmaxLen : 0; }
+inline unsigned graph_key(unsigned rows, unsigned longest) { return 2 * rows + (longest <= kShortSoftmaxLen ? 1 : 0); }
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
 constexpr double kTimeoutSeconds = 30.0;  // src/gemma2_kfd.cpp:21
@@ -212,7 +218,7 @@ struct Lane {
   int32_t *ids_h, *pos_h;
   uint32_t *items_h, *count_h, *tok_h, *off_h;
   float* out_h;
-  std::map<unsigned, hipGraphExec_t> graphs;  // key: padded rows
+  std::map<unsigned, hipGraphExec_t> graphs;  // key: graph_key(padded rows, longest sequence)
   unsigned staged_tokens = 0, staged_rows = 0, staged_longest = 0;
   size_t staged_batch = 0;
   std::map<std::string, double> timings;
@@ -311,7 +317,7 @@ class Backend {
   DevMat upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k);
   void alloc_lane(Lane& L);
   void launch(const char* name, hipError_t e);
-  void record_layers(Lane& L, unsigned rows);
+  void record_layers(Lane& L, unsigned rows, unsigned longest);
   void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
             hipStream_t s);
   void wait(Lane& L, const char* what);
@@ -528,7 +534,7 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 // ffn_norm (+Q8_0), gate|up GEMM with the GeGLU (+Q8_0) in its epilogue,
 // down GEMM, residual + next attn_norm (+Q8_0); finally the output_norm per
 // token (the first half of kernels.c:417-427).
-void Backend::record_layers(Lane& ln, unsigned rows) {
+void Backend::record_layers(Lane& ln, unsigned rows, unsigned longest) {
   hipStream_t s = ln.stream;
   const int n = (int)rows;
   launch("embed", eg2::launch_embed_norm_quant(token_embd_, ln.ids_d, n, std::sqrt((float)kEmbd),
@@ -540,7 +546,7 @@ void Backend::record_layers(Lane& ln, unsigned rows) {
     launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
                                                          L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
     launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid, ln.tok_d, L.window, n,
-                                              ln.scores, ln.cq, ln.cd, s));
+                                              (int)longest, ln.scores, ln.cq, ln.cd, s));
     gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
     // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.
@@ -640,12 +646,12 @@ void Backend::stage(Lane& ln, const int32_t* ids, const size_t* offsets, size_t 
           "copy token records");
     check(hipMemcpyAsync(ln.off_d, ln.off_h, (batch + 1) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
           "copy offsets");
-    const unsigned key = rows;
+    const unsigned key = graph_key(rows, longest);
     if (use_graph_ && !profile_ && ln.graphs.find(key) == ln.graphs.end()) {
       hipGraph_t graph = nullptr;
       check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
       try {
-        record_layers(ln, rows);
+        record_layers(ln, rows, attention_form(longest));
       } catch (...) {
         (void)hipStreamEndCapture(s, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -675,7 +681,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
   device_step([&] {
     for (unsigned r = 0; r < repeats; ++r) {
       if (use_graph_ && !profile_) {
-        check(hipGraphLaunch(ln.graphs.at(ln.staged_rows), s), "hipGraphLaunch");
+        check(hipGraphLaunch(ln.graphs.at(graph_key(ln.staged_rows, ln.staged_longest)), s), "hipGraphLaunch");
       } else if (profile_) {
         // Per-stage timing needs events around eager launches; the totals are
         // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
@@ -683,7 +689,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
         check(hipEventCreate(&a), "hipEventCreate");
         check(hipEventCreate(&b), "hipEventCreate");
         check(hipEventRecord(a, s), "hipEventRecord");
-        record_layers(ln, ln.staged_rows);
+        record_layers(ln, ln.staged_rows, attention_form(ln.staged_longest));
         check(hipEventRecord(b, s), "hipEventRecord");
         check(hipEventSynchronize(b), "hipEventSynchronize");
         float ms = 0;
@@ -692,7 +698,7 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
         (void)hipEventDestroy(a);
         (void)hipEventDestroy(b);
       } else {
-        record_layers(ln, ln.staged_rows);
+        record_layers(ln, ln.staged_rows, attention_form(ln.staged_longest));
       }
       if (dense_) {
         // EXTRACTION.md:178-181: dense_2 then dense_3 on the mean pool

@@ -29,7 +29,7 @@
 // leaves, one per token (q already scaled by 1/16). A (token t, head h)
 // pair of a sequence starting at lo is numbered 3 (t - lo) + h.
 //
-// Three kernels:
+// The kernels:
 //  - attention_scores_kernel: work items of (sequence, 32 keys, 32 pairs).
 //    The workgroup stages the q rows of its pairs and the k rows of its
 //    keys in LDS, 128 dimensions at a time, reordered so that chain c's
@@ -38,10 +38,15 @@
 //    multiplies chain c (lane group c feeds chain c's q and k values), and
 //    each lane adds its 16 products to its 4 pairs' 4 chain sums. The
 //    scores go to a scratch row per pair (row length rounded up to 4).
-//  - attention_softmax_kernel: one wave per (token, head): the row
-//    maximum; then per 64-key chunk every lane's expf of its key, written
-//    back over the score, and lane 0 adds the chunk to the sum in key
-//    order; 1/sum per (token, head) into the scratch's head.
+//  - attention_exp_kernel: one wave per (token, head): the row maximum,
+//    then every lane's expf of its keys, written back over the scores.
+//  - attention_sum_kernel: one lane per (token, head): the sum of its p
+//    row in key order (a serial chain, so 16 pairs share a wave's
+//    instructions), 1/sum into the scratch's head.
+//  - attention_softmax_kernel: the two above in one, for waves whose
+//    sequences are at most kShortSoftmax tokens: lane 0 of the pair's wave
+//    adds the chunk's p values, which costs little for short rows and
+//    saves a launch.
 //  - attention_context_kernel: work items of (sequence, 64 pairs), each
 //    taken by 4 workgroups of 64 dimensions. Per 64-key chunk the
 //    workgroup stages w = p * (1/sum) for its pairs (0 for keys outside a
@@ -72,6 +77,7 @@ constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apar
 constexpr int kCPairs = 64, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
+constexpr int kShortSoftmax = 512;        // longest sequence for the one-kernel softmax
 
 // Floats of a sequence's score row (its length rounded up to 4, so that
 // rows are 16-byte aligned), and of the 1/sum area at the scratch's head.
@@ -211,9 +217,13 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One wave per (token, head) pair: the row maximum, then per 64-key chunk
-// every lane's p = expf(score - m) written back over the score and, in
-// key order, added by lane 0 to the sum; 1/sum to the scratch's head.
+// The softmax in one kernel, for waves whose sequences are short: one wave
+// per (token, head) pair, the row maximum, then per 64-key chunk every
+// lane's p = expf(score - m) written back over the score and, in key
+// order, added by lane 0 to the sum; 1/sum into the scratch's head. The
+// same operations in the same order as attention_exp_kernel followed by
+// attention_sum_kernel, which long rows take instead (their serial sums
+// would occupy one lane of a wave per key).
 __global__ void __launch_bounds__(256)
 attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
@@ -229,8 +239,6 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   uint32_t first, last;
   key_range(t, lo, hi, window, first, last);
   float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
-
-  // The row maximum (order-free), four loads in flight per lane.
   float m = -__builtin_inff();
   uint32_t kt = first + lane;
   for (; kt + 192 < last; kt += 256) {
@@ -239,8 +247,6 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   }
   for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
   m = wave_max(m);
-
-  // p and the sum = p[first] + p[first + 1] + ... in key order.
   float sum = 0.0f;
   for (uint32_t c0 = first; c0 < last; c0 += 64) {
     const uint32_t k = c0 + lane;
@@ -267,6 +273,94 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
     wave_lds_sync();
   }
   if (lane == 0) scores[3 * (size_t)t + h] = 1.0f / sum;
+}
+
+// One wave per (token, head) pair: the row maximum (order-free), then
+// every lane's p = expf(score - m) for its keys, written back over the
+// scores. The sums come in attention_sum_kernel.
+__global__ void __launch_bounds__(256)
+attention_exp_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
+  __shared__ uint64_t tab[32];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
+  __syncthreads();
+  const uint32_t pair = 4 * blockIdx.x + w, t = pair / 3, h = pair % 3;
+  if (t >= (uint32_t)rows) return;
+  const uint4 meta = tok[t];
+  const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
+  if (t < lo || t >= hi) return;  // a malformed entry: nothing is written for this token
+  uint32_t first, last;
+  key_range(t, lo, hi, window, first, last);
+  float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
+  float m = -__builtin_inff();
+  uint32_t kt = first + lane;
+  for (; kt + 192 < last; kt += 256) {
+    const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
+    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+  }
+  for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
+  m = wave_max(m);
+  for (uint32_t k = first + lane; k < last; k += 64) srow[k - lo] = libm::expf_tab(srow[k - lo] - m, tab);
+}
+
+// sum = p[first] + p[first + 1] + ... in key order for each (token, head)
+// pair, then 1/sum into the scratch's head at [3 t + h]. The sum is a
+// serial chain, so a lane takes a whole pair: lanes 0-15 of each wave,
+// 16 pairs per wave (more waves to overlap the row reads than 64 pairs
+// per wave would give), the row read in batches of 32 keys with the next
+// three batches in flight while the current one is added.
+constexpr int kSumPairsPerWave = 16;
+constexpr int kSumBatch = 8;  // float4 per batch
+constexpr int kSumRing = 4;   // batches in the ring
+
+__global__ void __launch_bounds__(256)
+attention_sum_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane >= kSumPairsPerWave) return;
+  const uint32_t pair = (blockIdx.x * 4 + w) * kSumPairsPerWave + lane, t = pair / 3, h = pair % 3;
+  if (t >= (uint32_t)rows) return;
+  const uint4 meta = tok[t];
+  const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
+  if (t < lo || t >= hi) return;
+  uint32_t first, last;
+  key_range(t, lo, hi, window, first, last);
+  const float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
+  uint32_t k = first - lo;
+  const uint32_t end = last - lo;
+  float sum = 0.0f;
+  for (; (k & 3) != 0 && k < end; ++k) sum = sum + srow[k];  // up to the row's next 16-byte boundary
+  const uint32_t n4 = (end - k) / 4;                         // whole float4 of the row from k
+  const float4* r4 = reinterpret_cast<const float4*>(srow + k);
+  // A ring of kSumRing batches: batch i is added while batches i + 1 ..
+  // i + kSumRing - 1 are in flight.
+  float4 ring[kSumRing][kSumBatch];
+  auto load = [&](float4 (&dst)[kSumBatch], uint32_t j0) {
+#pragma unroll
+    for (int j = 0; j < kSumBatch; ++j) dst[j] = r4[min(j0 + j, n4 - 1)];
+  };
+  if (n4 > 0) {
+#pragma unroll
+    for (int b = 0; b < kSumRing - 1; ++b) load(ring[b], b * kSumBatch);
+  }
+  for (uint32_t j0 = 0; j0 < n4; j0 += kSumRing * kSumBatch) {
+#pragma unroll
+    for (int b = 0; b < kSumRing; ++b) {
+      const uint32_t jb = j0 + b * kSumBatch;
+      if (jb >= n4) break;
+      load(ring[(b + kSumRing - 1) % kSumRing], jb + (kSumRing - 1) * kSumBatch);
+#pragma unroll
+      for (int j = 0; j < kSumBatch; ++j) {
+        if (jb + j < n4) {
+          sum = sum + ring[b][j].x;
+          sum = sum + ring[b][j].y;
+          sum = sum + ring[b][j].z;
+          sum = sum + ring[b][j].w;
+        }
+      }
+    }
+  }
+  for (k += 4 * n4; k < end; ++k) sum = sum + srow[k];
+  scores[3 * (size_t)t + h] = 1.0f / sum;
 }
 
 // ---------------------------------------------------------------- context
@@ -315,38 +409,41 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     const float* wsrc = scores + sbase + (size_t)wpair * pitch;
     const uint32_t wfirst = range[wp][0], wlast = pair0 + wp < pair1 ? range[wp][1] : wfirst;
     const uint32_t vk = (uint32_t)tid >> 2, vq = 16 * (tid & 3);
+    // A chunk's staging values (this thread's 16 p values and 16 v values)
+    // are loaded while the previous chunk is computed.
+    float4 pw[4], pv[4];
+    auto load_chunk = [&](uint32_t c0) {
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const uint32_t k4 = c0 + 16 * w + 4 * j4;  // 4 keys, 16-byte aligned in the row
+        pw[j4] = k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+      const uint32_t kt = c0 + vk;
+      const float* src = qkv + (size_t)min(kt, hi - 1) * kLd + kVOff + dblk + vq;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pv[j] = kt < hi ? *reinterpret_cast<const float4*>(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    if (kfirst < klast) load_chunk(kfirst);
     for (uint32_t c0 = kfirst; c0 < klast; c0 += kCKeys) {
       __syncthreads();  // the previous chunk is no longer read
 #pragma unroll
       for (int j4 = 0; j4 < 4; ++j4) {
-        const uint32_t k4 = c0 + 16 * w + 4 * j4;  // 4 keys, 16-byte aligned in the row
-        float4 p4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (k4 - lo < pitch) p4 = *reinterpret_cast<const float4*>(wsrc + (k4 - lo));
-        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+        const float pr[4] = {pw[j4].x, pw[j4].y, pw[j4].z, pw[j4].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t kt = k4 + e;
-          const float wv = pv[e] * winv;
+          const uint32_t kt = c0 + 16 * w + 4 * j4 + e;
+          const float wv = pr[e] * winv;
           wl[(16 * w + 4 * j4 + e) * kCPitchW + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
         }
       }
       {
-        const uint32_t kt = c0 + vk;
-        float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0, v2 = v0, v3 = v0;
-        if (kt < hi) {
-          const float* src = qkv + (size_t)kt * kLd + kVOff + dblk + vq;
-          v0 = *reinterpret_cast<const float4*>(src);
-          v1 = *reinterpret_cast<const float4*>(src + 4);
-          v2 = *reinterpret_cast<const float4*>(src + 8);
-          v3 = *reinterpret_cast<const float4*>(src + 12);
-        }
         float* dst = vl + vk * kCPitchV + vq;
-        *reinterpret_cast<float4*>(dst) = v0;
-        *reinterpret_cast<float4*>(dst + 4) = v1;
-        *reinterpret_cast<float4*>(dst + 8) = v2;
-        *reinterpret_cast<float4*>(dst + 12) = v3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(dst + 4 * j) = pv[j];
       }
       __syncthreads();
+      if (c0 + kCKeys < klast) load_chunk(c0 + kCKeys);
       // Keys in groups of 4 (a group's keys past klast carry w = 0 for every
       // pair and add +0): the group's 4 MFMAs into separate registers, the
       // next group's operands read from LDS, then the adds in key order.
@@ -487,15 +584,24 @@ AttentionCounts attention_capacity(size_t tokens, size_t batch) {
 }
 
 hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
-                            const uint32_t* tok, int window, int rows, float* scores, int8_t* cq, float* cd,
-                            hipStream_t st) {
-  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0) return hipErrorInvalidValue;
+                            const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
+                            float* cd, hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_scores_kernel, dim3(grid), dim3(256), 0, st, qkv,
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, scores);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attention_softmax_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
-                     reinterpret_cast<const uint4*>(tok), window, rows);
+  if (longest > 0 && longest <= kShortSoftmax) {
+    hipLaunchKernelGGL(attention_softmax_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
+                       reinterpret_cast<const uint4*>(tok), window, rows);
+  } else {
+    hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
+                       reinterpret_cast<const uint4*>(tok), window, rows);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_sum_kernel, dim3((3 * rows + 4 * kSumPairsPerWave - 1) / (4 * kSumPairsPerWave)),
+                       dim3(256), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attention_context_kernel, dim3(grid), dim3(256), 0, st, qkv, scores,
@@ -513,8 +619,8 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
 // of at most kStaticRows rows into at most kStaticBatch sequences fits
 // (the bounds of attention_capacity). Nothing in it has to start at zero:
 // the plan kernel writes the counts and every record the other kernels
-// read, the softmax kernel every 1/sum the context kernel reads, and the
-// softmax and context kernels use only scores written in the same call.
+// read, the sum kernel every 1/sum the context kernel reads, and the
+// exp, sum and context kernels use only scores written in the same call.
 // Calls that overlap on one GPU share the array and race.
 
 constexpr size_t kStaticRows = 2048, kStaticBatch = 2048;
@@ -681,7 +787,7 @@ hipError_t launch_attention_static(const float* qkv, const uint32_t* offsets, in
                      reinterpret_cast<uint4*>(tok), reinterpret_cast<uint4*>(items));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_attention(qkv, items, counts, kAttentionGrid, tok, window, rows, scores, cq, cd, st);
+  return launch_attention(qkv, items, counts, kAttentionGrid, tok, window, rows, 0, scores, cq, cd, st);
 }
 
 }  // namespace eg2

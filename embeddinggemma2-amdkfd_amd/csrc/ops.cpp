@@ -66,13 +66,13 @@ int eg2_hip_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, c
 }
 
 int eg2_hip_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, unsigned grid,
-                      const uint32_t* tok, unsigned window, unsigned rows, float* scores, int8_t* cq, float* cd,
-                      void* stream) {
+                      const uint32_t* tok, unsigned window, unsigned rows, unsigned longest, float* scores, int8_t* cq,
+                      float* cd, void* stream) {
   if (!qkv || !items || !item_count || !tok || !scores || !cq || !cd || rows == 0 || rows % 4 != 0 ||
-      rows > (1u << 24) || grid == 0 || grid > 65536 || window > 4096u)
+      rows > (1u << 24) || grid == 0 || grid > 65536 || window > 4096u || longest > rows)
     return kInvalid;
-  return code(eg2::launch_attention(qkv, items, item_count, (int)grid, tok, (int)window, (int)rows, scores, cq, cd,
-                                    as_stream(stream)));
+  return code(eg2::launch_attention(qkv, items, item_count, (int)grid, tok, (int)window, (int)rows, (int)longest,
+                                    scores, cq, cd, as_stream(stream)));
 }
 
 int eg2_hip_attention_static(const float* qkv, const uint32_t* offsets, unsigned batch, unsigned window,

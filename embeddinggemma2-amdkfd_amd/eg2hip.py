@@ -110,7 +110,7 @@ SIGNATURES = {
     "eg2_hip_embed_norm_quant": (C.c_int, [_vp, _vp, _u, C.c_float, _vp, C.c_float, _vp, _vp, _vp, _vp]),
     "eg2_hip_residual_norm_quant": (C.c_int, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _u, _vp]),
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u, _vp]),
-    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
     "eg2_hip_attention_static": (C.c_int, [_vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
     "eg2_attention_plan": (C.c_int, [C.POINTER(C.c_size_t), C.c_size_t, C.c_size_t, C.c_size_t, _vp, _vp,
                                      C.POINTER(C.c_size_t)]),
@@ -567,6 +567,7 @@ class AttentionPlan:
         self.tok = torch.from_numpy(np.ascontiguousarray(tok).view(np.int32).reshape(-1).copy()).to(device)
         self.scores = torch.zeros(max(1, score_floats), dtype=torch.float32, device=device)
         self.rows = tok.shape[0]
+        self.longest = max(int(offsets[i + 1]) - int(offsets[i]) for i in range(len(offsets) - 1))
 
 
 class ops:
@@ -622,11 +623,14 @@ class ops:
         torch.cuda.current_stream().synchronize()  # keeps the plan alive until the kernels ran
 
     @classmethod
-    def attention_planned(cls, qkv, plan, window, cq, cd):
-        """attention() with a prebuilt AttentionPlan (no host work, no sync)."""
+    def attention_planned(cls, qkv, plan, window, cq, cd, longest=None):
+        """attention() with a prebuilt AttentionPlan (no host work, no sync);
+        longest overrides the plan's longest sequence (0 = the softmax form
+        for any length)."""
         check(lib().eg2_hip_attention(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID,
-                                      cls._p(plan.tok), window, qkv.shape[0], cls._p(plan.scores), cls._p(cq),
-                                      cls._p(cd), cls._stream()), "attention")
+                                      cls._p(plan.tok), window, qkv.shape[0],
+                                      plan.longest if longest is None else longest, cls._p(plan.scores),
+                                      cls._p(cq), cls._p(cd), cls._stream()), "attention")
 
     STATIC_ROWS, STATIC_BATCH = 2048, 2048  # EG2_ATTENTION_STATIC_ROWS / _BATCH
 

@@ -71,11 +71,13 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * `grid` workgroups stride over each list; tok holds one record for each
  * of the `rows` rows, so every row must belong to a planned sequence, e.g.
  * a padding one. scores: scratch of at least the plan's score floats
- * (counts[1]). rows % 4 == 0. A sequence's result does not depend on its
- * place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
+ * (counts[1]). rows % 4 == 0. longest: the longest sequence of the
+ * packing (it picks one of two equivalent softmax kernel forms; 0 = not
+ * known, valid for any packing). A sequence's result does not depend on
+ * its place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
-                      const uint32_t *tok, unsigned window, unsigned rows, float *scores, int8_t *cq, float *cd,
-                      void *stream);
+                      const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores, int8_t *cq,
+                      float *cd, void *stream);
 
 /* eg2_hip_attention without allocation. It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code

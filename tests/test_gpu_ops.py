@@ -334,10 +334,11 @@ def segments_log_uniform(rng, n_seg=16, total=2048, lo=8, hi=512):
     return lens
 
 
-def run_attention(eg2, gpu, q, k, v, offsets, window, scratch_fill=0.0):
+def run_attention(eg2, gpu, q, k, v, offsets, window, scratch_fill=0.0, longest=None):
     """The device attention of rows [q | k | v] packed as `offsets` (rows
     padded to a multiple of 4 by one more sequence): (int8 [T, 768], scales
-    [T, 24]) of the quantized context."""
+    [T, 24]) of the quantized context. longest: the softmax form override
+    (None: the plan's longest sequence; 0: the form for any length)."""
     import torch
 
     T = q.shape[0]
@@ -348,7 +349,7 @@ def run_attention(eg2, gpu, q, k, v, offsets, window, scratch_fill=0.0):
     cq, cd = qbuf(eg2, rows, N_EMBD, gpu), empty((24, rows), torch.float32, gpu)
     plan = eg2.AttentionPlan(offs, gpu, rows)
     plan.scores.fill_(scratch_fill)
-    eg2.ops.attention_planned(dev(qkv, gpu), plan, window, cq, cd)
+    eg2.ops.attention_planned(dev(qkv, gpu), plan, window, cq, cd, longest)
     return qvals(eg2, cq, rows, N_EMBD)[:T], np.ascontiguousarray(host(cd).T)[:T]
 
 
@@ -451,6 +452,21 @@ def test_attention_independent_of_packing(eg2, gpu, window):
         a, b = offsets[s], offsets[s + 1]
         sq, sd = run_attention(eg2, gpu, q[a:b], k[a:b], v[a:b], [0, b - a], window)
         assert np.array_equal(sq, cq[a:b]) and np.array_equal(sd, cd[a:b])
+
+
+@pytest.mark.parametrize("window", [0, 64])
+def test_attention_softmax_forms_agree(eg2, gpu, window):
+    """The one-kernel softmax (waves of sequences up to 512 tokens) and the
+    exp + serial-sum pair (any length) give the same bits."""
+    rng = np.random.default_rng(10)
+    lens = [1, 130, 512, 7, 300]
+    T = sum(lens)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    q, k, v = qkv_inputs(rng, T)
+    short = run_attention(eg2, gpu, q, k, v, offsets, window)
+    split = run_attention(eg2, gpu, q, k, v, offsets, window, longest=0)
+    assert np.array_equal(short[0], split[0]) and np.array_equal(bits(short[1]), bits(split[1]))
+    assert_attention_bit_exact(*short, oracle_attention(q, k, v, offsets, window))
 
 
 def test_attention_reads_only_scores_it_wrote(eg2, gpu):

@@ -77,12 +77,13 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 3, 4, 32, 32, None) == inval  # ldg < n
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, None, 4, 4, 32, 32, None) == inval
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 0, 32, 32, None) == inval  # n = 0
-    # attention(qkv, items, item_count, grid, tok, window, rows, scores, cq, cd)
-    assert lib.eg2_hip_attention(p, p, p, 0, p, 0, 32, p, p, p, None) == inval  # grid 0
-    assert lib.eg2_hip_attention(p, p, p, 64, p, 99999, 32, p, p, p, None) == inval  # window
-    assert lib.eg2_hip_attention(p, p, p, 64, None, 0, 32, p, p, p, None) == inval
-    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 30, p, p, p, None) == inval  # rows % 4
-    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, None, p, p, None) == inval  # no scratch
+    # attention(qkv, items, item_count, grid, tok, window, rows, longest, scores, cq, cd)
+    assert lib.eg2_hip_attention(p, p, p, 0, p, 0, 32, 0, p, p, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 99999, 32, 0, p, p, p, None) == inval  # window
+    assert lib.eg2_hip_attention(p, p, p, 64, None, 0, 32, 0, p, p, p, None) == inval
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 30, 0, p, p, p, None) == inval  # rows % 4
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, 0, None, p, p, None) == inval  # no scratch
+    assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, 33, p, p, p, None) == inval  # longest > rows
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, None, 4, None) == inval
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, p, 0, None) == inval
     assert lib.eg2_hip_libm_eval(p, 0, p, p, None) == inval
