@@ -35,6 +35,12 @@ def golden():
 
 
 def make_tokenizer(eg2, g, name, path):
+    make_tokenizer_file(g, name, path)
+    return eg2.Tokenizer(path)
+
+
+def make_tokenizer_file(g, name, path):
+    """Writes vocabulary `name` of the fixture as a GGUF file of tokenizer keys."""
     bos, eos, add_bos, add_eos, prefix = (int(x) for x in g[f"{name}_flags"])
     kvs = [("tokenizer.ggml.model", "str", "llama"),
            ("tokenizer.ggml.tokens", "arr_str", unblob(g[f"{name}_tokens"], g[f"{name}_token_offsets"])),
@@ -47,7 +53,6 @@ def make_tokenizer(eg2, g, name, path):
     if merges:
         kvs.append(("tokenizer.ggml.merges", "arr_str", merges))
     gguf_py.write_kv(path, kvs)
-    return eg2.Tokenizer(path)
 
 
 @pytest.mark.parametrize("name", ["spm", "spm_eos", "ranked"])
