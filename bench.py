@@ -33,6 +33,16 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# The serving configuration: at least 8 hardware queues per process (the
+# HIP runtime reads this when it initialises, before torch touches the
+# GPU), so each of the executor's four lanes runs on a queue of its own;
+# with the runtime's default of 4 the executor keeps three lanes.
+try:
+    _queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+except ValueError:
+    _queues = 4
+os.environ["GPU_MAX_HW_QUEUES"] = str(max(_queues, 8))
+
 TOKENS, SEQS, LAYERS = 2048, 16, 24
 GEMM_N, GEMM_M, GEMM_K = 2048, 2 * 1152, 768
 PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA (the projection GEMMs)
@@ -472,7 +482,8 @@ def main():
         "config": {"workload": "24-layer Q8_0 EmbeddingGemma-300M-shape encoder forward + dense head, one "
                                "packed wave of 16x128 tokens", "tokens_per_wave": TOKENS, "sequences": SEQS,
                    "layers": LAYERS, "hidden": 768, "ffn": 1152, "heads": "3q/1kv x 256", "weights": "Q8_0",
-                   "attention": "full within sequence, RoPE base 1e4", "lanes": lanes},
+                   "attention": "full within sequence, RoPE base 1e4", "lanes": lanes,
+                   "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"])},
         "roofline": {"bound": "mfma", "kernel": "gemm_q8_geglu gate|up 2048x2304x768 + GeGLU + Q8_0 (v_mfma_i32_32x32x32_i8; "
                                                 "achieved/peak in T int8 op/s)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",

@@ -454,8 +454,19 @@ Backend::Backend(const ei_gguf* g) : model_(g) {
 
   // Capacity for the wave cap plus the padding sequence (rows rounded to 32).
   attn_cap_ = eg2::attention_capacity(kCap + 32, kCap + 1);
-  // EG2_HIP_LANES (1..8, default 3): waves in flight per context.
+  // EG2_HIP_LANES (1..8): waves in flight per context. The default gives
+  // each lane a hardware queue of its own next to the queue of the null
+  // stream: the HIP runtime opens GPU_MAX_HW_QUEUES queues per process (4
+  // when unset) and streams beyond that share queues, which serialises
+  // their kernels. So min(4, queues - 1) lanes: 3 with the runtime's
+  // default, 4 with 5 or more queues (more lanes than 4 measured slower:
+  // their working sets no longer stay in the Infinity Cache).
   unsigned n_lanes = 3;
+  if (const char* q = std::getenv("GPU_MAX_HW_QUEUES")) {
+    char* end = nullptr;
+    const long n = std::strtol(q, &end, 10);
+    if (*q && !*end && n >= 2) n_lanes = (unsigned)std::min(4L, n - 1);
+  }
   if (const char* v = std::getenv("EG2_HIP_LANES")) {
     char* end = nullptr;
     const long l = std::strtol(v, &end, 10);

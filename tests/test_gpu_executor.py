@@ -155,6 +155,24 @@ def test_env_lanes(eg2, small_model):
         assert np.isfinite(one.batch(ids, [0, 20, 50])).all()
     finally:
         one.close()
+    # default: one lane per hardware queue beside the null stream's, at most 4
+    saved = os.environ.pop("GPU_MAX_HW_QUEUES", None)
+    try:
+        for queues, want in ((None, 3), ("2", 1), ("4", 3), ("5", 4), ("8", 4), ("32", 4), ("x", 3)):
+            if queues is None:
+                os.environ.pop("GPU_MAX_HW_QUEUES", None)
+            else:
+                os.environ["GPU_MAX_HW_QUEUES"] = queues
+            enc = eg2.Encoder(small_model)
+            try:
+                assert enc.lanes == want, (queues, enc.lanes)
+            finally:
+                enc.close()
+    finally:
+        if saved is None:
+            os.environ.pop("GPU_MAX_HW_QUEUES", None)
+        else:
+            os.environ["GPU_MAX_HW_QUEUES"] = saved
 
 
 def waves_for_lanes(n):
