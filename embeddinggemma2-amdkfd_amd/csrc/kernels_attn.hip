@@ -44,9 +44,9 @@
 //    row in key order (a serial chain, so 16 pairs share a wave's
 //    instructions), 1/sum into the scratch's head.
 //  - attention_softmax_kernel: the two above in one, for waves whose
-//    sequences are at most kShortSoftmax tokens: lane 0 of the pair's wave
-//    adds the chunk's p values, which costs little for short rows and
-//    saves a launch.
+//    sequences are at most kShortSoftmax tokens: a workgroup of 16 waves
+//    (pairs) keeps their p rows in LDS, and lanes 0-15 of its first wave
+//    add them, one pair each, which saves a launch.
 //  - attention_context_kernel: work items of (sequence, 64 pairs), each
 //    taken by 4 workgroups of 64 dimensions. Per 64-key chunk the
 //    workgroup stages w = p * (1/sum) for its pairs (0 for keys outside a
@@ -210,69 +210,72 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// LDS writes of this wave are visible to its other lanes' later reads.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // The softmax in one kernel, for waves whose sequences are short: one wave
-// per (token, head) pair, the row maximum, then per 64-key chunk every
-// lane's p = expf(score - m) written back over the score and, in key
-// order, added by lane 0 to the sum; 1/sum into the scratch's head. The
-// same operations in the same order as attention_exp_kernel followed by
-// attention_sum_kernel, which long rows take instead (their serial sums
-// would occupy one lane of a wave per key).
-__global__ void __launch_bounds__(256)
+// per (token, head) pair takes the row maximum, then every lane's
+// p = expf(score - m) for its keys, written back over the scores and into
+// the pair's LDS row; then lane i of the first wave adds pair i's p values
+// in key order (a serial chain: 16 pairs share each add instruction) and
+// writes 1/sum into the scratch's head. The same operations in the same
+// order as attention_exp_kernel followed by attention_sum_kernel, which
+// long rows take instead (their rows would not fit the LDS).
+constexpr int kSmWaves = 16;  // pairs (waves) per workgroup
+constexpr int kSmPitch = kShortSoftmax + 4;
+
+__global__ void __launch_bounds__(64 * kSmWaves)
 attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
-  __shared__ __align__(16) float pbuf[4][64];  // per wave: a chunk's p values
+  __shared__ __align__(16) float prow[kSmWaves][kSmPitch];  // each pair's p values from its first key
+  __shared__ uint32_t plen[kSmWaves];                        // and their count (0: no such pair)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
   __syncthreads();
-  const uint32_t pair = 4 * blockIdx.x + w, t = pair / 3, h = pair % 3;
-  if (t >= (uint32_t)rows) return;
-  const uint4 meta = tok[t];
-  const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
-  if (t < lo || t >= hi) return;  // a malformed entry: nothing is written for this token
-  uint32_t first, last;
-  key_range(t, lo, hi, window, first, last);
-  float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
-  float m = -__builtin_inff();
-  uint32_t kt = first + lane;
-  for (; kt + 192 < last; kt += 256) {
-    const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
-    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
-  }
-  for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
-  m = wave_max(m);
-  float sum = 0.0f;
-  for (uint32_t c0 = first; c0 < last; c0 += 64) {
-    const uint32_t k = c0 + lane;
-    float p = 0.0f;
-    if (k < last) {
-      p = libm::expf_tab(srow[k - lo] - m, tab);
-      srow[k - lo] = p;
+  const uint32_t pair = kSmWaves * blockIdx.x + w, t = pair / 3, h = pair % 3;
+  uint32_t n = 0;
+  if (t < (uint32_t)rows) {
+    const uint4 meta = tok[t];
+    const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
+    // a malformed entry (t outside its sequence, or a row longer than the
+    // LDS row): nothing is written for this token
+    if (t >= lo && t < hi && hi - lo <= (uint32_t)kShortSoftmax) {
+      uint32_t first, last;
+      key_range(t, lo, hi, window, first, last);
+      float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
+      float m = -__builtin_inff();
+      uint32_t kt = first + lane;
+      for (; kt + 192 < last; kt += 256) {
+        const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
+        m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+      }
+      for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
+      m = wave_max(m);
+      for (uint32_t k = first + lane; k < last; k += 64) {
+        const float p = libm::expf_tab(srow[k - lo] - m, tab);
+        srow[k - lo] = p;
+        prow[w][k - first] = p;
+      }
+      n = last - first;
     }
-    pbuf[w][lane] = p;
-    wave_lds_sync();
-    if (lane == 0) {
-      const int n = (int)min(64u, last - c0);
-      const float* pr = pbuf[w];
-      int j = 0;
-      for (; j + 4 <= n; j += 4) {
+  }
+  if (lane == 0) plen[w] = n;
+  __syncthreads();
+  if (w == 0 && lane < kSmWaves) {
+    const uint32_t cnt = plen[lane];
+    const uint32_t own = kSmWaves * blockIdx.x + lane;
+    if (cnt > 0) {
+      const float* pr = prow[lane];
+      float sum = 0.0f;
+      uint32_t j = 0;
+      for (; j + 4 <= cnt; j += 4) {
         const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
         sum = sum + p4.x;
         sum = sum + p4.y;
         sum = sum + p4.z;
         sum = sum + p4.w;
       }
-      for (; j < n; ++j) sum = sum + pr[j];
+      for (; j < cnt; ++j) sum = sum + pr[j];
+      scores[3 * (size_t)(own / 3) + own % 3] = 1.0f / sum;
     }
-    wave_lds_sync();
   }
-  if (lane == 0) scores[3 * (size_t)t + h] = 1.0f / sum;
 }
 
 // One wave per (token, head) pair: the row maximum (order-free), then
@@ -592,8 +595,8 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (longest > 0 && longest <= kShortSoftmax) {
-    hipLaunchKernelGGL(attention_softmax_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
-                       reinterpret_cast<const uint4*>(tok), window, rows);
+    hipLaunchKernelGGL(attention_softmax_kernel, dim3((3 * rows + kSmWaves - 1) / kSmWaves), dim3(64 * kSmWaves), 0,
+                       st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
   } else {
     hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
                        reinterpret_cast<const uint4*>(tok), window, rows);
