@@ -106,18 +106,26 @@ __device__ __forceinline__ void accumulate_products(floatx16& acc, const floatx1
   ((acc[V] = acc[V] + t[V]), ...);
 }
 
-// The 64 x 64 tiles of an n x m output split into 8 regions, one per XCD:
-// the row tiles in 2 parts (1 when there is a single row tile) and the
-// column tiles in 8 / that many, so that an XCD's L2 fetches half of the
-// activation rows and a quarter of the weight columns instead of all rows
-// and an eighth of the columns (11 MB instead of 16 MB for gate|up at
-// 2048 rows).
+// The output tiles split into 8 regions, one per XCD: the row tiles in
+// rparts parts and the column tiles in 8 / rparts, rparts chosen so that the
+// fullest region holds the fewest tiles (the kernel lasts as long as its
+// busiest XCD), ties going to 2 row parts, then 4, 8, 1. With 2 row parts an
+// XCD's L2 fetches half of the activation rows and a quarter of the weight
+// columns instead of all rows and an eighth of the columns (11 MB instead
+// of 16 MB for gate|up at 2048 rows); the Q|K|V projection's 5 head columns
+// split evenly only over 8 row parts (40 tiles per XCD at 2048 rows, where
+// 2 row parts would give two XCDs nothing and two half the others' 64).
 struct XcdRegions {
   int cparts, rows, cols;  // column parts; row and column tiles per region
 };
 __host__ __device__ inline XcdRegions xcd_split(int tr_count, int tc_count) {
-  const int rparts = tr_count >= 2 ? 2 : 1, cparts = kXcds / rparts;
-  return {cparts, (tr_count + rparts - 1) / rparts, (tc_count + cparts - 1) / cparts};
+  XcdRegions best{0, 0, 0};
+  for (int rparts : {2, 4, 8, 1}) {
+    const int cparts = kXcds / rparts;
+    const XcdRegions r{cparts, (tr_count + rparts - 1) / rparts, (tc_count + cparts - 1) / cparts};
+    if (best.cparts == 0 || r.rows * r.cols < best.rows * best.cols) best = r;
+  }
+  return best;
 }
 __host__ __device__ inline XcdRegions xcd_regions(int n, int m) { return xcd_split((n + 63) / 64, (m + 63) / 64); }
 __host__ inline dim3 gemm_grid(int n, int m) {
