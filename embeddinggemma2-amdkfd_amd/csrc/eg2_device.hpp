@@ -94,6 +94,16 @@ __device__ __forceinline__ int32_t q8_round(float v) {
   return q;
 }
 
+// The quantized value q = (int)roundf(v * id), clamped (quants.c:169-174),
+// including the x86 conversion the reference runs on: cvttss2si turns NaN
+// and out-of-range values into INT_MIN, which the clamp makes -128. Within a
+// block that only happens when 1 / d overflows (d = amax / 127 below 2^-128,
+// a block of subnormal-sized values), where every v * id is +-inf or, for
+// v = 0, NaN: every value of such a block quantizes to -128.
+__device__ __forceinline__ int32_t q8_value(float v, float id) {
+  return id > 3.40282347e38f ? -128 : q8_round(v * id);
+}
+
 // v combined (op: max or +) with its copies in lanes l ^ 16 and l ^ 32,
 // i.e. over the four 16-lane rows, on the VALU: v_permlane16_swap and
 // v_permlane32_swap of v with itself leave v of lane l and of its partner in
@@ -137,7 +147,7 @@ __device__ __forceinline__ Q8Lane q8_quantize_lane(float x) {
     r.q = 0;
   } else {
     const float id = 1.0f / d;
-    r.q = q8_round(x * id);
+    r.q = q8_value(x, id);
   }
   return r;
 }
@@ -165,7 +175,7 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
   if ((threadIdx.x & (P - 1)) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
   int32_t qi[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) qi[i] = q8_round(v[i] * id);  // id = 0 for an all-zero block
+  for (int i = 0; i < N; ++i) qi[i] = q8_value(v[i], id);  // id = 0 for an all-zero block
   uint32_t w[N / 4];
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) w[i] = pack_i8x4(qi[4 * i], qi[4 * i + 1], qi[4 * i + 2], qi[4 * i + 3]);
@@ -179,11 +189,110 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[kQK / P], b
 // times u (engine.c's GeGLU), each operation in the reference's order with
 // the host libm's own tanhf (eg2_libm.hpp, its branch-free form, since the
 // lanes of a wave take different cases): bit-identical to the CPU path.
+constexpr float kGeluA = 0.044715f;
+constexpr float kGeluS = 0.79788456080286535587989211986876f;
+__device__ __forceinline__ float gelu_inner(float g) { return kGeluS * g * (1.0f + kGeluA * g * g); }
 __device__ __forceinline__ float gelu_mul(float g, float u) {
-  const float a = 0.044715f;
-  const float s = 0.79788456080286535587989211986876f;
-  const float inner = s * g * (1.0f + a * g * g);
-  return 0.5f * g * (1.0f + libm::tanhf_flat(inner)) * u;
+  return 0.5f * g * (1.0f + libm::tanhf_flat(gelu_inner(g))) * u;
+}
+
+// A cheap tanh: 1 - 2 / (1 + 2^(2x log2 e)) by the hardware exp2 and
+// reciprocal. |tanh_approx(x) - tanhf(x)| <= 2^-22 for every finite float x,
+// tanhf being the host libm's (as restated in eg2_libm.hpp): the maximum over
+// all 2^32 inputs, measured on the device (4 units of 2^-24, at x =
+// -1.87318516); a GPU test repeats the exhaustive check against
+// kTanhApproxBound, twice that.
+__device__ __forceinline__ float tanh_approx(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
+constexpr float kTanhApproxBound = 0x1p-21f;
+
+// The GeGLU of one 32-value block and its Q8_0 quantization (quants.c:97-177,
+// scalar path), the block spread over 4 adjacent lanes with 8 (gate, up)
+// pairs each, with the results of gelu_mul then quantize_block_part<4> bit
+// for bit but without evaluating the exact tanhf for most values:
+//  1. A = ((0.5 g)(1 + tanh_approx(z))) u for each value, and a bound on
+//     |A - gelu_mul(g, u)|: with |tanh_approx - tanhf| <= eta, one rounding
+//     each of 1 + tanh, 0.5 g (1 + tanh) and the product with u gives
+//     |A - exact| <= |0.5 g u| (eta + 2^-23) + 2^-22.9 |A| (plus a few
+//     subnormal units); the bound used, |0.5 g u| (2^-21 + 2^-22) +
+//     2^-21 |A| + 2^-146, is that with room to spare for its own fp32
+//     evaluation.
+//  2. The block maximum needs exact values: every value whose |A| + bound
+//     reaches max(|A| - bound) over the block may be the largest, so those
+//     (usually one) are evaluated exactly; amax, the fp16 scale d and 1/d
+//     follow from them as in the quantizer.
+//  3. q = roundf(v / d) of any other value is decided by its interval
+//     [A - bound', A + bound'] (bound' adds the rounding of A -/+ bound):
+//     v -> roundf(RN(v id)) is monotone, so equal q at both ends is the q of
+//     the exact value; the rare value whose interval straddles a rounding
+//     boundary is evaluated exactly.
+// The exact evaluations run as passes over the wave in which each lane
+// takes one of its pending values, as many passes as the lane with the most.
+__device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const float (&u)[8], bool store,
+                                                     int8_t* __restrict__ q, float* __restrict__ d_out) {
+  float a[8], bound[8];
+  float mlo = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float h = 0.5f * g[i];
+    const float t = 1.0f + tanh_approx(gelu_inner(g[i]));
+    a[i] = h * t * u[i];
+    bound[i] = fabsf(h * u[i]) * (kTanhApproxBound + 0x1p-22f) + fabsf(a[i]) * 0x1p-21f + 0x1p-146f;
+    mlo = fmaxf(mlo, fabsf(a[i]) - bound[i]);
+  }
+  mlo = fmaxf(mlo, __shfl_xor(mlo, 1, 64));
+  mlo = fmaxf(mlo, __shfl_xor(mlo, 2, 64));
+  // A non-finite approximation (or bound) fails every comparison: such a
+  // value is evaluated exactly.
+  uint32_t pending = 0, cand = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool maybe_max = !(fabsf(a[i]) + bound[i] < mlo);
+    cand |= maybe_max ? 1u << i : 0u;
+  }
+  pending = cand;
+  auto exact_passes = [&]() {
+    while (__ballot(pending != 0)) {
+      const int k = pending ? __builtin_ctz(pending) : 0;
+      float gk = g[0], uk = u[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        gk = k == i ? g[i] : gk;
+        uk = k == i ? u[i] : uk;
+      }
+      const float x = gelu_mul(gk, uk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = (pending & (1u << i)) && k == i ? x : a[i];
+      pending &= pending - 1;
+    }
+  };
+  exact_passes();  // a[] now exact for the candidates
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, cand & (1u << i) ? fabsf(a[i]) : 0.0f);
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float d = div127(amax);
+  const float id = amax != 0.0f ? 1.0f / d : 0.0f;
+  int32_t qi[8];
+  uint32_t exact = cand;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float b2 = bound[i] + fabsf(a[i]) * 0x1p-22f + 0x1p-146f;
+    const int32_t lo = q8_value(a[i] - b2, id), hi = q8_value(a[i] + b2, id);
+    qi[i] = lo;
+    if (!(cand & (1u << i)) && lo != hi) pending |= 1u << i;
+  }
+  exact |= pending;
+  exact_passes();  // a[] now exact for the undecided values too
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (exact & (1u << i)) qi[i] = q8_value(a[i], id);
+  if (!store) return;
+  if ((threadIdx.x & 3) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
+  *reinterpret_cast<uint2*>(q) = make_uint2(pack_i8x4(qi[0], qi[1], qi[2], qi[3]), pack_i8x4(qi[4], qi[5], qi[6], qi[7]));
 }
 
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):

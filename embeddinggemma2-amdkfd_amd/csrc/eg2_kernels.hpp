@@ -21,6 +21,9 @@ hipError_t launch_residual_norm_quant(float* x, const float* h, const float* pos
 hipError_t launch_qk_norm_rope(const float* qkv, const float* q_w, const float* k_w, const float* rope,
                                const int32_t* pos, float eps, float* out, int rows, hipStream_t st);
 hipError_t launch_libm_eval(const float* x, unsigned n, float* e, float* t, hipStream_t st);
+// *out (a zeroed uint32) := the bits of max |tanh_approx(x) - tanhf(x)| over
+// every finite float x (an exhaustive sweep of the 2^32 bit patterns).
+hipError_t launch_tanh_approx_error(uint32_t* out, hipStream_t st);
 hipError_t launch_gelu_quant(const float* gu, int8_t* gq, float* gd, int rows, hipStream_t st);
 hipError_t launch_quantize_rows(const float* x, int k, int8_t* q, float* d, int rows, hipStream_t st);
 hipError_t launch_rms_norm_rows(float* x, const float* w, float eps, int rows, hipStream_t st);

@@ -35,6 +35,7 @@
 // issued and block kb's adds follow. In the MFMA 32x32 output layout a lane
 // holds one column and 16 rows; each row's activation scale reaches it
 // through a DPP row broadcast folded into the multiply.
+#include <algorithm>
 #include <utility>
 
 #include "eg2_device.hpp"
@@ -142,9 +143,10 @@ constexpr int kGPitch = 40;  // floats per row of the GeGLU epilogue's transpose
 // the matching up columns in its waves wc = 1, and its 32 GeGLU outputs per
 // row are exactly Q8_0 block tc. The two waves of a row pair swap their
 // results through LDS (the gate wave finishes rows 0-15 of the pair, the
-// up wave rows 16-31), transpose them so that four lanes hold one row's
-// block, and quantize with the same code as the standalone GeGLU kernel: the int8 values go to gq in the row-tile layout (nbf blocks per
-// row), the scales to gd[tc * ldg + row].
+// up wave rows 16-31), transpose the gate and up values so that four lanes
+// hold one row's block, and run the standalone GeGLU kernel's code
+// (geglu_quantize_part4): the int8 values go to gq in the row-tile layout
+// (nbf blocks per row), the scales to gd[tc * ldg + row].
 __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int tc, int wr, int wc, int n, int nbf,
                                                int8_t* __restrict__ gq, float* __restrict__ gd, int ldg) {
   const int lane = threadIdx.x & 63, g = lane >> 5;
@@ -163,19 +165,28 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
     gv[i] = xch[(8 * wc + i) * 64 + lane];
     uv[i] = xch[(16 + 8 * wc + i) * 64 + lane];
   }
-  __syncthreads();  // the exchange area becomes the transposed tile
-  float* tp = reinterpret_cast<float*>(gemm_lds) + wr * 32 * kGPitch;  // [32][kGPitch]
+  __syncthreads();  // the exchange area becomes the transposed gate and up tiles
+  float* tg = reinterpret_cast<float*>(gemm_lds) + wr * 2 * 32 * kGPitch;  // [32][kGPitch] gate, then up
+  float* tu = tg + 32 * kGPitch;
   // register v = 8 wc + i of the 32x32 output layout: row 8 (v >> 2) + 4 g + (v & 3), column lane & 31
-  float* trow = tp + (16 * wc + 4 * g) * kGPitch + (lane & 31);
+  const int trow = (16 * wc + 4 * g) * kGPitch + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) trow[(8 * (i >> 2) + (i & 3)) * kGPitch] = gelu_mul(gv[i], uv[i]);
+  for (int i = 0; i < 8; ++i) {
+    tg[trow + (8 * (i >> 2) + (i & 3)) * kGPitch] = gv[i];
+    tu[trow + (8 * (i >> 2) + (i & 3)) * kGPitch] = uv[i];
+  }
   __syncthreads();
   const int rr = 16 * wc + (lane >> 2), part = lane & 3;
-  const float4 lo = *reinterpret_cast<const float4*>(tp + rr * kGPitch + 8 * part);
-  const float4 hi = *reinterpret_cast<const float4*>(tp + rr * kGPitch + 8 * part + 4);
-  const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  float gs[8], us[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float4 g4 = *reinterpret_cast<const float4*>(tg + rr * kGPitch + 8 * part + 4 * h);
+    const float4 u4 = *reinterpret_cast<const float4*>(tu + rr * kGPitch + 8 * part + 4 * h);
+    gs[4 * h] = g4.x, gs[4 * h + 1] = g4.y, gs[4 * h + 2] = g4.z, gs[4 * h + 3] = g4.w;
+    us[4 * h] = u4.x, us[4 * h + 1] = u4.y, us[4 * h + 2] = u4.z, us[4 * h + 3] = u4.w;
+  }
   const int t = 64 * tr + 32 * wr + rr;
-  quantize_block_part<4>(v, t < n, gq + q8_tile_offset(t, 32 * tc + 8 * part, nbf), gd + (size_t)tc * ldg + t);
+  geglu_quantize_part4(gs, us, t < n, gq + q8_tile_offset(t, 32 * tc + 8 * part, nbf), gd + (size_t)tc * ldg + t);
 }
 
 // TAIL: nb % kStages != 0 (a separate instantiation: the tail code costs
@@ -323,14 +334,15 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
     return hipErrorInvalidValue;
   const dim3 grid = gemm_grid(n, m);
   const int nb = k / kQK;
-  static_assert(2 * 2048 <= kStages * kStageBytes / 4 && 2 * 32 * kGPitch <= kStages * kStageBytes / 4,
-                "the GeGLU epilogue fits in the ring");
+  // LDS: the ring, or the epilogue's exchange area and its gate and up tiles
+  constexpr size_t lds = std::max<size_t>(kStages * kStageBytes, 2 * 2 * 32 * kGPitch * sizeof(float));
+  static_assert(2 * 2048 * sizeof(float) <= lds, "the GeGLU exchange fits");
   if (nb % kStages == 0)
-    hipLaunchKernelGGL((gemm_q8_kernel<false, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
-                       ldw, nullptr, n, m, nb, ldg, gq, gd);
+    hipLaunchKernelGGL((gemm_q8_kernel<false, true>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m,
+                       nb, ldg, gq, gd);
   else
-    hipLaunchKernelGGL((gemm_q8_kernel<true, true>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
-                       ldw, nullptr, n, m, nb, ldg, gq, gd);
+    hipLaunchKernelGGL((gemm_q8_kernel<true, true>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m,
+                       nb, ldg, gq, gd);
   return hipGetLastError();
 }
 

@@ -131,8 +131,8 @@ __device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int 
     const float id = amax != 0.0f ? 1.0f / dd : 0.0f;
     const int e = 4 * (lane + 64 * r), b = e / kQK;
     // id = 0 for an all-zero block, whose values then quantize to 0.
-    const int32_t q0 = q8_round(v[r].x * id), q1 = q8_round(v[r].y * id), q2 = q8_round(v[r].z * id),
-                  q3 = q8_round(v[r].w * id);
+    const int32_t q0 = q8_value(v[r].x, id), q1 = q8_value(v[r].y, id), q2 = q8_value(v[r].z, id),
+                  q3 = q8_value(v[r].w, id);
     *reinterpret_cast<uint32_t*>(q + q8_tile_offset(t, e, kBlocks)) = pack_i8x4(q0, q1, q2, q3);
     if ((lane & 7) == 0) d[(size_t)b * ld] = fp16_bits_to_fp32(fp32_to_fp16_bits(dd));
   }
@@ -281,8 +281,9 @@ qk_norm_rope_kernel(const float* qkv, const float* __restrict__ q_w, const float
 }
 
 // kernels.c:367-371 and :373-391: gelu_tanh(gate) * up, quantized to Q8_0,
-// each 32-value block over 4 lanes (8 values each), values in the row-tile
-// layout, block scales transposed ([block][row]).
+// each 32-value block over 4 lanes (8 values each; geglu_quantize_part4,
+// which evaluates the exact tanhf only where the Q8_0 result depends on
+// it), values in the row-tile layout, block scales transposed ([block][row]).
 // gu rows hold [gate 0..1151 | up 0..1151].
 __global__ void __launch_bounds__(256)
 gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* __restrict__ gd, int n_rows) {
@@ -292,18 +293,15 @@ gelu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ gq, float* 
   const int t = jb / kB, b = jb - t * kB, e0 = b * kQK + (j & 3) * 8;
   const float* g = gu + (size_t)t * (2 * kFF) + e0;
   const float* u = g + kFF;
-  float v[8];
+  float gs[8], us[8];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float4 g4 = *reinterpret_cast<const float4*>(g + 4 * i);
     const float4 u4 = *reinterpret_cast<const float4*>(u + 4 * i);
-    const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      v[4 * i + c] = gelu_mul(gs[c], us[c]);
-    }
+    gs[4 * i] = g4.x, gs[4 * i + 1] = g4.y, gs[4 * i + 2] = g4.z, gs[4 * i + 3] = g4.w;
+    us[4 * i] = u4.x, us[4 * i + 1] = u4.y, us[4 * i + 2] = u4.z, us[4 * i + 3] = u4.w;
   }
-  quantize_block_part<4>(v, (j >> 2) < n_rows * kB, gq + q8_tile_offset(t, e0, kB), gd + (size_t)b * n_rows + t);
+  geglu_quantize_part4(gs, us, (j >> 2) < n_rows * kB, gq + q8_tile_offset(t, e0, kB), gd + (size_t)b * n_rows + t);
 }
 
 // quants.c:97-177 on rows of width k (k % 32 == 0), each block over 4 lanes;
@@ -461,6 +459,27 @@ libm_eval_kernel(const float* __restrict__ x, unsigned n, float* __restrict__ e,
 hipError_t launch_libm_eval(const float* x, unsigned n, float* e, float* t, hipStream_t st) {
   if (n == 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(libm_eval_kernel, dim3(std::min(4096u, (n + 255) / 256)), dim3(256), 0, st, x, n, e, t);
+  return hipGetLastError();
+}
+
+// max over every finite float x of |tanh_approx(x) - tanhf(x)| (the restated
+// host tanhf), as the bit pattern of the float, reduced by an atomic max (the
+// bit patterns of non-negative floats order as the floats do). *out must
+// start at 0.
+__global__ void __launch_bounds__(256) tanh_approx_error_kernel(uint32_t* __restrict__ out) {
+  const uint64_t threads = (uint64_t)gridDim.x * 256, per = (1ull << 32) / threads;
+  const uint64_t first = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * per;
+  float worst = 0.0f;
+  for (uint64_t i = 0; i < per; ++i) {
+    const float x = __uint_as_float((uint32_t)(first + i));
+    if (!(fabsf(x) <= 3.40282347e38f)) continue;  // NaN or infinite
+    worst = fmaxf(worst, fabsf(tanh_approx(x) - libm::tanhf_flat(x)));
+  }
+  atomicMax(out, __float_as_uint(worst));
+}
+
+hipError_t launch_tanh_approx_error(uint32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(tanh_approx_error_kernel, dim3(16384), dim3(256), 0, st, out);  // 2^32 / (16384 * 256) each
   return hipGetLastError();
 }
 

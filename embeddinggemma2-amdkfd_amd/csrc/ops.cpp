@@ -110,6 +110,11 @@ int eg2_hip_libm_eval(const float* x, unsigned n, float* expf_out, float* tanhf_
   return code(eg2::launch_libm_eval(x, n, expf_out, tanhf_out, as_stream(stream)));
 }
 
+int eg2_hip_tanh_approx_error(uint32_t* out, void* stream) {
+  if (!out) return kInvalid;
+  return code(eg2::launch_tanh_approx_error(out, as_stream(stream)));
+}
+
 int eg2_hip_gelu_quant(const float* gate_up, int8_t* gq, float* gd, unsigned rows, void* stream) {
   if (!gate_up || !gq || !gd || rows == 0) return kInvalid;
   return code(eg2::launch_gelu_quant(gate_up, gq, gd, (int)rows, as_stream(stream)));

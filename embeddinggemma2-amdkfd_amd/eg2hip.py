@@ -117,6 +117,7 @@ SIGNATURES = {
     "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]),
     "eg2_hip_gelu_quant": (C.c_int, [_vp, _vp, _vp, _u, _vp]),
     "eg2_hip_libm_eval": (C.c_int, [_vp, _u, _vp, _vp, _vp]),
+    "eg2_hip_tanh_approx_error": (C.c_int, [_vp, _vp]),
     "eg2_hip_quantize_rows": (C.c_int, [_vp, _u, _vp, _vp, _u, _vp]),
     "eg2_hip_rms_norm_rows": (C.c_int, [_vp, _vp, C.c_float, _u, _vp]),
     "eg2_hip_pool_l2": (C.c_int, [_vp, _vp, _vp, _u, _vp]),

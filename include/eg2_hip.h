@@ -125,6 +125,14 @@ void eg2_attention_capacity(size_t tokens, size_t batch, size_t *counts);
  * every input. For tests that compare the two. */
 int eg2_hip_libm_eval(const float *x, unsigned n, float *expf_out, float *tanhf_out, void *stream);
 
+/* The GeGLU kernels evaluate the exact tanhf only where a Q8_0 result depends
+ * on it, and an approximation (hardware exp2 and reciprocal) with a proven
+ * error bound elsewhere. This sweeps every finite float x on the device and
+ * leaves in *out (a device uint32 that must start at 0) the bits of
+ * max |approximation(x) - tanhf(x)|, which the kernels assume is at most
+ * 2^-21. For the test that asserts it. */
+int eg2_hip_tanh_approx_error(uint32_t *out, void *stream);
+
 /* kernels.c:367-391 ei_gelu_mul_quantize_q8_0 on rows [gate 1152 | up 1152].
  * Replaces kernels/eg2.c:173-179 eg2_element mode 1. */
 int eg2_hip_gelu_quant(const float *gate_up, int8_t *gq, float *gd, unsigned rows, void *stream);
