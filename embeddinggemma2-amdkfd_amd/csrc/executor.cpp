@@ -247,6 +247,14 @@ class Backend {
     free_lanes_.pop_back();
     return i;
   }
+  // A free lane from the pool, or -1 when every lane is taken (no wait).
+  int try_acquire_lane() {
+    std::lock_guard<std::mutex> pool(pool_mutex_);
+    if (free_lanes_.empty()) return -1;
+    const unsigned i = free_lanes_.back();
+    free_lanes_.pop_back();
+    return (int)i;
+  }
   // Takes lane i itself from the pool, blocking until it is free.
   void acquire_lane(unsigned i) {
     if (i >= lanes_.size()) throw std::runtime_error("lane index out of range");
@@ -806,6 +814,10 @@ bool on_lane(void* ctx, unsigned lane, char* err, size_t len, F&& f) {
 extern "C" unsigned eg2_kfd_lanes(void* ctx) { return ctx ? static_cast<Backend*>(ctx)->lanes() : 0; }
 
 extern "C" int eg2_kfd_acquire_lane(void* ctx) { return ctx ? (int)static_cast<Backend*>(ctx)->acquire_lane() : -1; }
+
+extern "C" int eg2_kfd_try_acquire_lane(void* ctx) {
+  return ctx ? static_cast<Backend*>(ctx)->try_acquire_lane() : -1;
+}
 
 extern "C" void eg2_kfd_release_lane(void* ctx, unsigned lane) {
   if (ctx) static_cast<Backend*>(ctx)->release_lane(lane);

@@ -156,9 +156,20 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
 
     // Wave w runs on slot w % L, each slot a lane held for the whole stream;
     // a slot's previous wave is collected just before the slot is reused,
-    // so up to L waves are in flight.
-    const size_t L = std::min<size_t>(std::max(1u, eg2_kfd_lanes(ctx)), waves);
-    HeldLanes held{ctx, std::vector<int>(L, -1)};
+    // so up to L waves are in flight. The lanes are taken before the first
+    // wave: one waiting for a free lane (nothing is held yet), the others
+    // only if free at once, so that a stream never waits while holding
+    // lanes (concurrent streams could otherwise each hold some lanes and
+    // wait for the others' forever). L is the number taken.
+    const size_t want = std::min<size_t>(std::max(1u, eg2_kfd_lanes(ctx)), waves);
+    HeldLanes held{ctx, {}};
+    held.lanes.push_back(eg2_kfd_acquire_lane(ctx));
+    while (held.lanes.size() < want) {
+      const int l = eg2_kfd_try_acquire_lane(ctx);
+      if (l < 0) break;
+      held.lanes.push_back(l);
+    }
+    const size_t L = held.lanes.size();
     std::vector<size_t> pend_begin(L), pend_end(L);
     std::vector<bool> busy(L, false);
     std::vector<int32_t> wave_ids;
@@ -182,7 +193,6 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
     size_t begin = 0;
     for (size_t w = 0; w < waves; ++w) {
       const size_t slot = w % L, end = wave_end[w];
-      if (held.lanes[slot] < 0) held.lanes[slot] = eg2_kfd_acquire_lane(ctx);
       if (busy[slot]) finish(slot);
       wave_ids.clear();
       offsets.assign(1, 0);

@@ -164,6 +164,7 @@ SIGNATURES = {
     "eg2_embeddings_response": (C.c_size_t, [_f, C.c_size_t, C.c_uint, C.c_int, C.c_int, C.c_char_p, C.c_size_t,
                                              C.c_size_t, C.c_char_p, C.c_size_t]),
     "eg2_kfd_acquire_lane": (C.c_int, [C.c_void_p]),
+    "eg2_kfd_try_acquire_lane": (C.c_int, [C.c_void_p]),
     "eg2_kfd_release_lane": (None, [C.c_void_p, C.c_uint]),
     "eg2_kfd_stage_lane": (C.c_bool, [C.c_void_p, C.c_uint, _i32, C.POINTER(C.c_size_t), C.c_size_t, C.c_char_p,
                                       C.c_size_t]),

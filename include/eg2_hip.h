@@ -220,6 +220,11 @@ unsigned eg2_kfd_lanes(void *ctx);
  * flight on several lanes holds them this way, so that no concurrent batch
  * call stages over its pending waves. */
 int eg2_kfd_acquire_lane(void *ctx);
+/* Takes a free lane from the pool without waiting: its index, or -1 when
+ * every lane is taken (or ctx is NULL). A caller that already holds a lane
+ * takes more this way, never by eg2_kfd_acquire_lane: two callers that
+ * each hold lanes and wait for more would wait for each other forever. */
+int eg2_kfd_try_acquire_lane(void *ctx);
 void eg2_kfd_release_lane(void *ctx, unsigned lane);
 /* Validates one wave, waits until the lane's previous wave is done with its
  * staging buffers, uploads the ids and packing metadata, and builds (once

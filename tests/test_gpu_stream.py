@@ -76,3 +76,46 @@ def test_stream_rejects_bad_texts(eg2, stream_encoder):
     # the context is poisoned only by device failures, not by rejected input
     out, _ = enc.stream(np.zeros(4, np.int32), [0, 4], [768])
     assert abs(np.linalg.norm(out[0]) - 1) < 1e-5
+
+
+def test_concurrent_streams_and_batches(eg2, stream_encoder):
+    """Streams of many waves and batch calls from several threads at once on
+    one context: each stream takes one lane waiting and the others only if
+    free, so no thread waits while holding lanes another one waits for;
+    every result equals the one-at-a-time result."""
+    import threading
+
+    enc, _ = stream_encoder
+    rng = np.random.default_rng(9)
+    streams = [make_stream(rng, 40, 600) for _ in range(3)]
+    cfg = eg2.batch_config(max_batch_requests=4)
+    alone = [enc.stream(ids, offs, dims, cfg)[0] for ids, offs, dims in streams]
+    ids_b, offs_b, _ = streams[0]
+    batch_alone = enc.batch(ids_b[:offs_b[5]], offs_b[:6])
+    errors = []
+
+    def run_stream(k):
+        try:
+            for _ in range(2):
+                got, waves = enc.stream(*streams[k], cfg)
+                if waves < enc.lanes or not np.array_equal(got, alone[k]):
+                    errors.append(("stream", k, waves))
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    def run_batches():
+        try:
+            for _ in range(6):
+                if not np.array_equal(enc.batch(ids_b[:offs_b[5]], offs_b[:6]), batch_alone):
+                    errors.append("batch")
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=run_stream, args=(k,)) for k in range(3)]
+    threads += [threading.Thread(target=run_batches) for _ in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=90)
+    assert not any(t.is_alive() for t in threads), "a thread did not finish"
+    assert not errors, errors
