@@ -144,3 +144,113 @@ def test_tokenized_texts_through_the_executor(eg2, gpu, tmp_path_factory):
     print(json.dumps({"tokenized_wave": {"texts": n, "tokens": int(wave_offs[-1]), "min_cos": c, "max_abs": a}}))
     assert c >= COS_MIN and a <= MAX_ABS
     assert np.array_equal(got, want)
+
+
+def test_requests_against_the_http_parity_contract(eg2, gpu, tmp_path_factory):
+    """The checks of the reference's tests/http_parity.py:15-107 on the
+    request path without its HTTP transport, as the server's handle_embed
+    runs it (server.c:1029-1210): the texts of a request tokenized by
+    eg2_tokenize_batch, embedded 768 wide by eg2_stream_embed (the service
+    hands the server full embeddings), and the OpenAI response body written
+    by eg2_embeddings_response (prefix L2 to `dimensions`, float text or
+    base64), then parsed as JSON. Where http_parity.py compares the GPU
+    server with the CPU server by cosine >= 0.99, the body here is compared
+    byte for byte with the body written from the oracle's embeddings;
+    batch = solo, reversed order and concurrent requests are asserted bit
+    for bit (the script: cosine >= 0.99999)."""
+    import base64
+    import math
+    import struct
+    import threading
+
+    from test_tokenizer_cpu import GOLDEN, make_tokenizer
+
+    g = np.load(GOLDEN)
+    d = tmp_path_factory.mktemp("req")
+    tok = make_tokenizer(eg2, g, "spm", str(d / "spm.gguf"))
+    path = str(d / "model.gguf")
+    eg2.synth_gguf(path, seed=43, n_layer=2, dense_head=True, sliding_window=512, sliding_window_pattern=2,
+                   rope_base_full=1e6, rope_base_swa=1e4, threads=16)
+    model = gguf_py.oracle_model(path)
+    enc = eg2.Encoder(path)
+    lock = threading.Lock()  # the tokenizer handle is used from one thread at a time
+
+    def embed(texts, dims=768, encoding="float", oracle=False):
+        """One request: (response body, prompt tokens); raises on a rejected request."""
+        raw = [t.encode() for t in ([texts] if isinstance(texts, str) else texts)]
+        with lock:
+            ids, offs = tok.encode_batch(raw, True, False, 4)
+        if oracle:
+            e = oracle_waves(model, ids, offs)
+        else:
+            e, _ = enc.stream(ids, offs, [768] * len(raw))
+        body = eg2.embeddings_response(e, dims, api="openai", encoding=encoding, model="embeddinggemma-2",
+                                       prompt_tokens=int(offs[-1]))
+        return body, int(offs[-1])
+
+    def request(texts, dims=768, encoding="float"):
+        """http_parity.py:15-34 on the parsed body."""
+        body, tokens = embed(texts, dims, encoding)
+        obj = json.loads(body)
+        assert obj["object"] == "list"
+        assert obj["usage"]["total_tokens"] == obj["usage"]["prompt_tokens"] == tokens > 0
+        vectors = []
+        for i, item in enumerate(obj["data"]):
+            assert item["index"] == i and item["object"] == "embedding"
+            v = item["embedding"]
+            if encoding == "base64":
+                v = struct.unpack("<" + "f" * dims, base64.b64decode(v, validate=True))
+            assert len(v) == dims and all(math.isfinite(x) for x in v)
+            assert abs(math.sqrt(sum(x * x for x in v)) - 1) < 1e-4
+            vectors.append(np.array(v, np.float32))
+        assert len(vectors) == (1 if isinstance(texts, str) else len(texts))
+        return np.stack(vectors), body
+
+    try:
+        texts = ["", "hello world", "检索增强生成与向量数据库。", "a " * 37,
+                 "query: How does a GPU execute a kernel?", "emoji: 🌍 café\nsecond line"]
+        # http_parity.py --long: a sequence past 1024 tokens, within one wave
+        reps = 1030
+        while len(tok.encode(("boundary " * reps).encode(), True, False)) > 2000:
+            reps -= 40
+        long_texts = ["boundary " * reps, "short unrelated sequence"]
+        assert len(tok.encode(long_texts[0].encode(), True, False)) > 1024
+        wide = [f"wide item {j}: " + "word " * (27 + j % 7) for j in range(16)]
+        for group in (texts, long_texts, wide):
+            got, body = request(group)
+            assert body == embed(group, oracle=True)[0]  # the CPU side, byte for byte
+            for text, vector in zip(group, got):
+                assert np.array_equal(request(text)[0][0], vector)
+            rev, _ = request(list(reversed(group)))
+            assert np.array_equal(rev[::-1], got)
+        for dim in (128, 256, 512, 768):
+            f, _ = request("format test", dim)
+            b, _ = request("format test", dim, "base64")
+            assert np.array_equal(f, b)
+        full, _ = request(texts)
+        results, errors = [None] * len(texts), []
+
+        def one(i):
+            try:
+                results[i] = request(texts[i])[0][0]
+            except Exception as e:  # reported below
+                errors.append(repr(e))
+
+        threads = [threading.Thread(target=one, args=(i,)) for i in range(len(texts))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=90)
+        assert not errors and all(r is not None for r in results), errors
+        assert all(np.array_equal(r, v) for r, v in zip(results, full))
+        # invalid requests: no input, unsupported dimensions, a text over 2048 tokens
+        with pytest.raises(eg2.HipError, match="invalid"):
+            embed([])
+        with pytest.raises(ValueError, match="dims"):
+            embed("test", 17)
+        with pytest.raises(eg2.HipError, match="1..2048"):
+            embed("word " * 2100)
+        request("still healthy after validation failures")
+    finally:
+        enc.close()
+        tok.close()
