@@ -182,46 +182,78 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
   quantize_row_lanes(v, t, xq, xd + t, (int)gridDim.x);
 }
 
+// Eight token rows per workgroup (one wave each) share the SSE2 chains: each
+// wave stages its row transposed, then wave 0 runs all 64 chains (lane
+// 8 k + c: chain c of token k) and combines each token's eight with DPP,
+// so the 96-step chains issue once per eight tokens instead of once per
+// token. A token's rows start 4 floats past the previous token's (its 8
+// chain rows span 8 x kTPitch + 4 floats), so the 16 rows read in one LDS
+// cycle fall in distinct banks.
+constexpr int kRowsPerGroup = 8;
+constexpr int kTokStride = 8 * kTPitch + 4;  // floats per token in the staging area
+
+__device__ __forceinline__ float* token_rows(float* tr, int k) { return tr + k * kTokStride; }
+
+// Wave 0: inv[k] = rms_inverse of token k's staged row, k = 0..7.
+__device__ __forceinline__ void group_rms_inverse(float* tr, float* inv, float eps) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  const TRow* rows = reinterpret_cast<const TRow*>(token_rows(tr, lane >> 3));
+  const float r = rms_inverse(sse2_combine_dpp(transposed_chain(rows, lane & 7)), kEmbd, eps);
+  if ((lane & 7) == 0) inv[lane >> 3] = r;
+}
+
 // kernels.c:163-188 (SSE2 build: scalar branch, residual += (h*inv)*w), then
 // kernels.c:139-151 with the next norm weight on the updated residual. With
-// next_w == nullptr only the residual update runs.
-__global__ void __launch_bounds__(64)
+// next_w == nullptr only the residual update runs. Rows past `rows` in the
+// last workgroup load nothing and store nothing; their waves still join
+// every barrier.
+__global__ void __launch_bounds__(64 * kRowsPerGroup)
 residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, const float* __restrict__ post_w,
                            const float* __restrict__ next_w, float eps, int8_t* __restrict__ xq,
-                           float* __restrict__ xd) {
-  __shared__ __align__(16) float tr[2][8][kTPitch];
-  const int t = blockIdx.x, lane = threadIdx.x;
+                           float* __restrict__ xd, int rows) {
+  __shared__ __align__(16) float tr[kRowsPerGroup * kTokStride];
+  __shared__ float inv_s[2][kRowsPerGroup];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kRowsPerGroup + w;
+  const bool live = t < rows;
   float4 hv[kVec], xv[kVec], wv[kVec], nv[kVec];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
-    hv[r] = *reinterpret_cast<const float4*>(h + (size_t)t * kEmbd + e);
-    xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + e);
+    hv[r] = live ? *reinterpret_cast<const float4*>(h + (size_t)t * kEmbd + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    xv[r] = live ? *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     wv[r] = *reinterpret_cast<const float4*>(post_w + e);
     if (next_w) nv[r] = *reinterpret_cast<const float4*>(next_w + e);
   }
-  stage_transposed(tr[0], hv);
+  float* mine = token_rows(tr, w);
+  stage_transposed(reinterpret_cast<TRow*>(mine), hv);
   __syncthreads();
-  const float inv_h = rms_inverse(sse2_combine_dpp(transposed_chain(tr[0], lane & 7)), kEmbd, eps);
+  group_rms_inverse(tr, inv_s[0], eps);
+  __syncthreads();
+  const float inv_h = inv_s[0][w];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     const float a0 = hv[r].x * inv_h, a1 = hv[r].y * inv_h, a2 = hv[r].z * inv_h, a3 = hv[r].w * inv_h;
     const float b0 = a0 * wv[r].x, b1 = a1 * wv[r].y, b2 = a2 * wv[r].z, b3 = a3 * wv[r].w;
     xv[r] = make_float4(xv[r].x + b0, xv[r].y + b1, xv[r].z + b2, xv[r].w + b3);
-    *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = xv[r];
+    if (live) *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = xv[r];
   }
-  if (!next_w) return;
-  stage_transposed(tr[1], xv);
+  if (!next_w) return;  // uniform over the grid
+  // Wave 0 read every token's rows before the barrier above.
+  stage_transposed(reinterpret_cast<TRow*>(mine), xv);
   __syncthreads();
-  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr[1], lane & 7)), kEmbd, eps);
+  group_rms_inverse(tr, inv_s[1], eps);
+  __syncthreads();
+  const float inv = inv_s[1][w];
   // (x*w)*inv (kernels.c:124-133, SSE2 branch), then Q8_0 (kernels.c:139-151).
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const float p0 = xv[r].x * nv[r].x, p1 = xv[r].y * nv[r].y, p2 = xv[r].z * nv[r].z, p3 = xv[r].w * nv[r].w;
     xv[r] = make_float4(p0 * inv, p1 * inv, p2 * inv, p3 * inv);
   }
-  quantize_row_lanes(xv, t, xq, xd + t, (int)gridDim.x);
+  if (live) quantize_row_lanes(xv, t, xq, xd + t, rows);
 }
 
 constexpr int kHeadStride = kHeadDim + 8;  // LDS row of one head: 8 banks apart
@@ -441,7 +473,8 @@ hipError_t launch_embed_norm_quant(const uint8_t* table, const int32_t* ids, int
 
 hipError_t launch_residual_norm_quant(float* x, const float* h, const float* post_w, const float* next_w,
                                       float eps, int8_t* xq, float* xd, int rows, hipStream_t st) {
-  hipLaunchKernelGGL(residual_norm_quant_kernel, dim3(rows), dim3(64), 0, st, x, h, post_w, next_w, eps, xq, xd);
+  hipLaunchKernelGGL(residual_norm_quant_kernel, dim3((rows + kRowsPerGroup - 1) / kRowsPerGroup),
+                     dim3(64 * kRowsPerGroup), 0, st, x, h, post_w, next_w, eps, xq, xd, rows);
   return hipGetLastError();
 }
 

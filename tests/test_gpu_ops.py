@@ -96,11 +96,11 @@ def test_embed_norm_quant_bit_exact(eg2, gpu):
     assert np.array_equal(host(xd).T, wd)
 
 
-@pytest.mark.parametrize("with_next", [True, False])
-def test_residual_norm_quant_bit_exact(eg2, gpu, with_next):
+@pytest.mark.parametrize("with_next,rows", [(True, 64), (False, 64), (True, 37), (False, 5)])
+def test_residual_norm_quant_bit_exact(eg2, gpu, with_next, rows):
+    """Rows go 8 to a workgroup; 37 and 5 leave a partial last group."""
     import torch
 
-    rows = 64
     x = (RNG.standard_normal((rows, N_EMBD)) * 5).astype(np.float32)
     h = (RNG.standard_normal((rows, N_EMBD)) * 0.7).astype(np.float32)
     pw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
