@@ -208,28 +208,67 @@ __device__ __forceinline__ float tanh_approx(float x) {
 }
 constexpr float kTanhApproxBound = 0x1p-21f;
 
+// Maximum over each aligned quad of lanes (4i .. 4i+3), on every lane of it,
+// by two DPP quad permutations (all 64 lanes must be active).
+__device__ __forceinline__ float quad_max(float m) {
+  m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0xB1, 0xf, 0xf, true)));
+  return fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0x4E, 0xf, 0xf, true)));
+}
+
+// Exact GeGLU values (gelu_mul) of the pending values of each lane (bit i of
+// pending = value i), one per pass over the wave, as many passes as the lane
+// with the most. Q = false stores them in a[]; Q = true stores their
+// quantized values q8_value(., id) in qi[].
+template <bool Q>
+__device__ __forceinline__ void geglu_exact_passes(const float (&g)[8], const float (&u)[8], uint32_t pending, float id,
+                                                   float (&a)[8], int32_t (&qi)[8]) {
+  while (__ballot(pending != 0)) {
+    const int k = pending ? __builtin_ctz(pending) : 0;
+    float gk = g[0], uk = u[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      gk = k == i ? g[i] : gk;
+      uk = k == i ? u[i] : uk;
+    }
+    const float x = gelu_mul(gk, uk);
+    if constexpr (Q) {
+      const int32_t qx = q8_value(x, id);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qi[i] = (pending & (1u << i)) && k == i ? qx : qi[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = (pending & (1u << i)) && k == i ? x : a[i];
+    }
+    pending &= pending - 1;
+  }
+}
+
 // The GeGLU of one 32-value block and its Q8_0 quantization (quants.c:97-177,
 // scalar path), the block spread over 4 adjacent lanes with 8 (gate, up)
 // pairs each, with the results of gelu_mul then quantize_block_part<4> bit
 // for bit but without evaluating the exact tanhf for most values:
-//  1. A = ((0.5 g)(1 + tanh_approx(z))) u for each value, and a bound on
+//  1. A = ((0.5 g)(1 + tanh_approx(z))) u for each value, and a bound B on
 //     |A - gelu_mul(g, u)|: with |tanh_approx - tanhf| <= eta, one rounding
 //     each of 1 + tanh, 0.5 g (1 + tanh) and the product with u gives
 //     |A - exact| <= |0.5 g u| (eta + 2^-23) + 2^-22.9 |A| (plus a few
 //     subnormal units); the bound used, |0.5 g u| (2^-21 + 2^-22) +
-//     2^-21 |A| + 2^-146, is that with room to spare for its own fp32
-//     evaluation.
-//  2. The block maximum needs exact values: every value whose |A| + bound
-//     reaches max(|A| - bound) over the block may be the largest, so those
+//     2^-21 |A| + 2^-146, is at least twice that: room for its own fp32
+//     evaluation and for the roundings in step 3.
+//  2. The block maximum needs exact values: every value whose |A| + B
+//     reaches max(|A| - B) over the block may be the largest, so those
 //     (usually one) are evaluated exactly; amax, the fp16 scale d and 1/d
 //     follow from them as in the quantizer.
-//  3. q = roundf(v / d) of any other value is decided by its interval
-//     [A - bound', A + bound'] (bound' adds the rounding of A -/+ bound):
-//     v -> roundf(RN(v id)) is monotone, so equal q at both ends is the q of
-//     the exact value; the rare value whose interval straddles a rounding
-//     boundary is evaluated exactly.
-// The exact evaluations run as passes over the wave in which each lane
-// takes one of its pending values, as many passes as the lane with the most.
+//  3. q = roundf(RN(v id)) of any other value is decided from y = RN(A id):
+//     the exact value's product lies within B id of A id, which lies within
+//     half an ulp of y, and roundf changes only at half-integers, so when y
+//     is farther from the nearest half-integer h than B id plus the
+//     roundings of y and of a product near h (2 ulp(y) for |y| >= 1/4,
+//     at most |y| 2^-22; the test adds |y| 2^-21, and below 1/4 the
+//     distance exceeds 1/4), the exact value's q is roundf(y); the distance
+//     |(|y| - trunc|y|) - 1/2| is exact in fp32 for |y| >= 1/4. The rare
+//     value closer than that (or non-finite) is evaluated exactly. A block whose
+//     1/d overflows quantizes to -128 throughout (q8_value) and needs no
+//     decision.
 __device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const float (&u)[8], bool store,
                                                      int8_t* __restrict__ q, float* __restrict__ d_out) {
   float a[8], bound[8];
@@ -239,57 +278,35 @@ __device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const 
     const float h = 0.5f * g[i];
     const float t = 1.0f + tanh_approx(gelu_inner(g[i]));
     a[i] = h * t * u[i];
-    bound[i] = fabsf(h * u[i]) * (kTanhApproxBound + 0x1p-22f) + fabsf(a[i]) * 0x1p-21f + 0x1p-146f;
+    bound[i] = __builtin_fmaf(fabsf(h * u[i]), kTanhApproxBound + 0x1p-22f, __builtin_fmaf(fabsf(a[i]), 0x1p-21f, 0x1p-146f));
     mlo = fmaxf(mlo, fabsf(a[i]) - bound[i]);
   }
-  mlo = fmaxf(mlo, __shfl_xor(mlo, 1, 64));
-  mlo = fmaxf(mlo, __shfl_xor(mlo, 2, 64));
+  mlo = quad_max(mlo);
   // A non-finite approximation (or bound) fails every comparison: such a
   // value is evaluated exactly.
-  uint32_t pending = 0, cand = 0;
+  uint32_t cand = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bool maybe_max = !(fabsf(a[i]) + bound[i] < mlo);
-    cand |= maybe_max ? 1u << i : 0u;
-  }
-  pending = cand;
-  auto exact_passes = [&]() {
-    while (__ballot(pending != 0)) {
-      const int k = pending ? __builtin_ctz(pending) : 0;
-      float gk = g[0], uk = u[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) {
-        gk = k == i ? g[i] : gk;
-        uk = k == i ? u[i] : uk;
-      }
-      const float x = gelu_mul(gk, uk);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = (pending & (1u << i)) && k == i ? x : a[i];
-      pending &= pending - 1;
-    }
-  };
-  exact_passes();  // a[] now exact for the candidates
+  for (int i = 0; i < 8; ++i) cand |= !(fabsf(a[i]) + bound[i] < mlo) ? 1u << i : 0u;
+  int32_t qi[8];
+  geglu_exact_passes<false>(g, u, cand, 0.0f, a, qi);  // a[] now exact for the candidates
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, cand & (1u << i) ? fabsf(a[i]) : 0.0f);
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = quad_max(amax);
   const float d = div127(amax);
   const float id = amax != 0.0f ? 1.0f / d : 0.0f;
-  int32_t qi[8];
-  uint32_t exact = cand;
+  const bool id_over = id > 3.40282347e38f;
+  uint32_t undecided = 0;  // built without branches: every value is tested
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float b2 = bound[i] + fabsf(a[i]) * 0x1p-22f + 0x1p-146f;
-    const int32_t lo = q8_value(a[i] - b2, id), hi = q8_value(a[i] + b2, id);
-    qi[i] = lo;
-    if (!(cand & (1u << i)) && lo != hi) pending |= 1u << i;
+    const float y = a[i] * id, ay = fabsf(y);
+    qi[i] = id_over ? -128 : q8_round(y);
+    const float dist = fabsf((ay - truncf(ay)) - 0.5f);
+    const float margin = __builtin_fmaf(bound[i], id, ay * 0x1p-21f);
+    undecided |= dist > margin ? 0u : 1u << i;
   }
-  exact |= pending;
-  exact_passes();  // a[] now exact for the undecided values too
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (exact & (1u << i)) qi[i] = q8_value(a[i], id);
+  undecided = id_over ? 0u : undecided & ~cand;
+  geglu_exact_passes<true>(g, u, undecided, id, a, qi);
   if (!store) return;
   if ((threadIdx.x & 3) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
   *reinterpret_cast<uint2*>(q) = make_uint2(pack_i8x4(qi[0], qi[1], qi[2], qi[3]), pack_i8x4(qi[4], qi[5], qi[6], qi[7]));
