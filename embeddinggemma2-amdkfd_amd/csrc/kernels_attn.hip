@@ -47,14 +47,15 @@
 //    sequences are at most kShortSoftmax tokens: a workgroup of 16 waves
 //    (pairs) keeps their p rows in LDS, and lanes 0-15 of its first wave
 //    add them, one pair each, which saves a launch.
-//  - attention_context_kernel: work items of (sequence, 64 pairs), each
-//    taken by 4 workgroups of 64 dimensions. Per 64-key chunk the
-//    workgroup stages w = p * (1/sum) for its pairs (0 for keys outside a
-//    pair's window, which adds +0 and changes no sum) and the chunk's v
-//    values in LDS; per key each wave issues one 4-block MFMA (block b =
-//    16 pairs, columns = its 16 dimensions) and adds the 16 products to its
-//    accumulators, in key order. The Q8_0 epilogue quantizes 32-value
-//    blocks over lane pairs.
+//  - attention_context_kernel: work items of (sequence, 32 pairs), each
+//    taken by 4 workgroups of 64 dimensions (768 workgroups for a wave of
+//    16 x 128 tokens or for one 2048-token sequence: three per CU). Per
+//    64-key chunk the workgroup stages w = p * (1/sum) for its pairs (0 for
+//    keys outside a pair's window, which adds +0 and changes no sum) and the
+//    chunk's v values in LDS; per 2 keys each wave issues one 4-block MFMA
+//    (block b = pairs 16 (b % 2) .. + 15 of key b / 2, columns = its 16
+//    dimensions) and adds the products to its 8 accumulators, in key order.
+//    The Q8_0 epilogue quantizes 32-value blocks over 4 lanes.
 // A sequence's keys, scores and context depend only on its own tokens, so
 // packing never changes a bit.
 #include <algorithm>
@@ -74,10 +75,19 @@ constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 constexpr int kSKeys = 32, kSPairs = 32;  // scores workgroup tile
 constexpr int kSDims = 128;               // dimensions staged at a time
 constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apart
-constexpr int kCPairs = 64, kCDims = 64;  // context workgroup tile
+constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
 constexpr int kShortSoftmax = 512;        // longest sequence for the one-kernel softmax
+
+// Work items of any packing of `tokens` rows into at most `batch`
+// sequences: per sequence of n tokens, ceil(n/32) ceil(3n/32) <= 3n^2/1024
+// + n/8 + 1 score items (32 x 32 tiles) and ceil(3n/kCPairs) <= 3n/kCPairs
+// + 1 context items; summed over sequences with sum n <= tokens.
+constexpr size_t item_bound(size_t tokens, size_t batch) {
+  static_assert(kSKeys == 32 && kSPairs == 32, "the score-item bound assumes 32 x 32 tiles");
+  return 3 * tokens * tokens / 1024 + tokens / 8 + 3 * tokens / kCPairs + 2 * batch + 2;
+}
 
 // Floats of a sequence's score row (its length rounded up to 4, so that
 // rows are 16-byte aligned), and of the 1/sum area at the scratch's head.
@@ -401,24 +411,24 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     // multiple of 4 past lo so that the float4 reads of the rows align.
     const uint32_t kfirst = lo + ((range[0][0] - lo) & ~3u);
     const uint32_t klast = range[min(pair1 - pair0, (uint32_t)kCPairs) - 1][1];
-    float acc[16];
+    float acc[8];  // pairs 16 (v / 4) + 4 g + v % 4, dimension dblk + 16 w + r16
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    // Staging roles: w by (pair = lane, the 16 keys of quarter w); v by
-    // (key = tid / 4, 16 dimensions of quarter tid % 4).
-    const uint32_t wp = (uint32_t)lane;
+    for (int v = 0; v < 8; ++v) acc[v] = 0.0f;
+    // Staging roles: w by (pair = tid % 32, the 8 keys 8 (tid / 32) ..);
+    // v by (key = tid / 4, 16 dimensions of quarter tid % 4).
+    const uint32_t wp = (uint32_t)tid & (kCPairs - 1), wk = 8 * ((uint32_t)tid / kCPairs);
     const uint32_t wpair = min(pair0 + wp, pair1 - 1);
     const float winv = scores[3 * (size_t)(lo + wpair / 3) + wpair % 3];
     const float* wsrc = scores + sbase + (size_t)wpair * pitch;
     const uint32_t wfirst = range[wp][0], wlast = pair0 + wp < pair1 ? range[wp][1] : wfirst;
     const uint32_t vk = (uint32_t)tid >> 2, vq = 16 * (tid & 3);
-    // A chunk's staging values (this thread's 16 p values and 16 v values)
+    // A chunk's staging values (this thread's 8 p values and 16 v values)
     // are loaded while the previous chunk is computed.
-    float4 pw[4], pv[4];
+    float4 pw[2], pv[4];
     auto load_chunk = [&](uint32_t c0) {
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const uint32_t k4 = c0 + 16 * w + 4 * j4;  // 4 keys, 16-byte aligned in the row
+      for (int j4 = 0; j4 < 2; ++j4) {
+        const uint32_t k4 = c0 + wk + 4 * j4;  // 4 keys, 16-byte aligned in the row
         pw[j4] = k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
       const uint32_t kt = c0 + vk;
@@ -431,13 +441,13 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     for (uint32_t c0 = kfirst; c0 < klast; c0 += kCKeys) {
       __syncthreads();  // the previous chunk is no longer read
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
+      for (int j4 = 0; j4 < 2; ++j4) {
         const float pr[4] = {pw[j4].x, pw[j4].y, pw[j4].z, pw[j4].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t kt = c0 + 16 * w + 4 * j4 + e;
+          const uint32_t kt = c0 + wk + 4 * j4 + e;
           const float wv = pr[e] * winv;
-          wl[(16 * w + 4 * j4 + e) * kCPitchW + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
+          wl[(wk + 4 * j4 + e) * kCPitchW + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
         }
       }
       {
@@ -447,50 +457,54 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
       }
       __syncthreads();
       if (c0 + kCKeys < klast) load_chunk(c0 + kCKeys);
-      // Keys in groups of 4 (a group's keys past klast carry w = 0 for every
-      // pair and add +0): the group's 4 MFMAs into separate registers, the
-      // next group's operands read from LDS, then the adds in key order.
-      const int n4 = (int)((min((uint32_t)kCKeys, klast - c0) + 3) & ~3u);
-      const float* wa = wl + lane;
-      const float* vb = vl + 16 * w + r16;
+      // Keys in groups of 8 (keys past klast carry w = 0 for every pair and
+      // add +0): per 2 keys one MFMA whose block b holds pairs 16 (b % 2) ..
+      // + 15 (rows) x the wave's 16 dimensions for key 2 i + b / 2; the
+      // group's 4 MFMAs into separate registers, the next group's operands
+      // read from LDS, then the adds in key order.
+      const int n8 = (int)((min((uint32_t)kCKeys, klast - c0) + 7) & ~7u);
+      const float* wa = wl + (g >> 1) * kCPitchW + 16 * (g & 1) + r16;
+      const float* vb = vl + (g >> 1) * kCPitchV + 16 * w + r16;
       float an[4], bn[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        an[e] = wa[e * kCPitchW];
-        bn[e] = vb[e * kCPitchV];
+        an[e] = wa[2 * e * kCPitchW];
+        bn[e] = vb[2 * e * kCPitchV];
       }
-      for (int j = 0; j < n4; j += 4) {
+      for (int j = 0; j < n8; j += 8) {
         floatx16 prod[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)  // block b: pairs 16b .. 16b + 15 (rows) x the wave's 16 dimensions
+        for (int e = 0; e < 4; ++e)  // keys j + 2 e, j + 2 e + 1
           prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(an[e], bn[e], zero, 0, 0, 0);
-        if (j + 4 < n4) {
+        if (j + 8 < n8) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            an[e] = wa[(j + 4 + e) * kCPitchW];
-            bn[e] = vb[(j + 4 + e) * kCPitchV];
+            an[e] = wa[(j + 8 + 2 * e) * kCPitchW];
+            bn[e] = vb[(j + 8 + 2 * e) * kCPitchV];
           }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[v] = acc[v] + prod[e][v];
+          for (int kk = 0; kk < 2; ++kk)  // key j + 2 e + kk: blocks 2 kk, 2 kk + 1
+#pragma unroll
+            for (int v = 0; v < 8; ++v) acc[v] = acc[v] + prod[e][8 * kk + v];
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // Lane holds dimension dblk + 16 w + r16 of pairs 16 (v/4) + 4 g + v%4.
-    // Through LDS to [pair][64 dimensions], then Q8_0 over lane pairs.
+    // Through LDS to [pair][64 dimensions], then Q8_0: block (32 values) of
+    // 4 lanes x 8 values.
     __syncthreads();
-    float* tile = wl;  // 64 x kCPitchW floats
+    float* tile = wl;  // kCPairs x kCPitchV floats
 #pragma unroll
-    for (int v = 0; v < 16; ++v) tile[(16 * (v >> 2) + 4 * g + (v & 3)) * kCPitchW + 16 * w + r16] = acc[v];
+    for (int v = 0; v < 8; ++v) tile[(16 * (v >> 2) + 4 * g + (v & 3)) * kCPitchV + 16 * w + r16] = acc[v];
     __syncthreads();
-    const uint32_t qp = (uint32_t)tid >> 2, qb = (tid >> 1) & 1, qh = tid & 1;  // pair, 32-block, half
-    float vals[16];
+    const uint32_t qp = (uint32_t)tid >> 3, qb = ((uint32_t)tid >> 2) & 1, part = (uint32_t)tid & 3;
+    float vals[8];
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      const float4 x4 = *reinterpret_cast<const float4*>(tile + qp * kCPitchW + 32 * qb + 16 * qh + i);
+    for (int i = 0; i < 8; i += 4) {
+      const float4 x4 = *reinterpret_cast<const float4*>(tile + qp * kCPitchV + 32 * qb + 8 * part + i);
       vals[i] = x4.x;
       vals[i + 1] = x4.y;
       vals[i + 2] = x4.z;
@@ -498,8 +512,8 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     }
     const uint32_t pair = min(pair0 + qp, pair1 - 1);
     const uint32_t t = lo + pair / 3, h = pair % 3;
-    const unsigned e = h * kHeadDim + (unsigned)dblk + 32 * qb + 16 * qh;
-    quantize_block_part<2>(vals, pair0 + qp < pair1, cq + q8_tile_offset(t, e, kEmbd / kQK),
+    const unsigned e = h * kHeadDim + (unsigned)dblk + 32 * qb + 8 * part;
+    quantize_block_part<4>(vals, pair0 + qp < pair1, cq + q8_tile_offset(t, e, kEmbd / kQK),
                            cd + (size_t)(e / kQK) * rows + t);
   }
 }
@@ -573,14 +587,10 @@ bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCo
 }
 
 AttentionCounts attention_capacity(size_t tokens, size_t batch) {
-  // Per sequence of n tokens: ceil(n/32) ceil(3n/32) <= (n/32 + 1)(3n/32 +
-  // 1) = 3n^2/1024 + n/8 + 1 score items and ceil(3n/64) <= 3n/64 + 1
-  // context items; over sequences with sum n <= tokens, at most `batch` of
-  // them: 3 tokens^2/1024 + 11 tokens/64 + 2 batch. Score floats: 3n
-  // (n + 3) per sequence, at most 3 tokens^2 + 9 tokens, plus the 1/sum
-  // area of 3 tokens rounded up to 4.
+  // Score floats: 3n (n + 3) per sequence, at most 3 tokens^2 + 9 tokens,
+  // plus the 1/sum area of 3 tokens rounded up to 4.
   AttentionCounts c;
-  c.items = 3 * tokens * tokens / 1024 + 11 * tokens / 64 + 2 * batch + 2;
+  c.items = item_bound(tokens, batch);
   c.score_floats = 3 * tokens * tokens + 12 * tokens + 4;
   c.score_items = 0;
   return c;
@@ -627,7 +637,7 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
 // Calls that overlap on one GPU share the array and race.
 
 constexpr size_t kStaticRows = 2048, kStaticBatch = 2048;
-constexpr size_t kStaticItems = 3 * kStaticRows * kStaticRows / 1024 + 11 * kStaticRows / 64 + 2 * kStaticBatch + 2;
+constexpr size_t kStaticItems = item_bound(kStaticRows, kStaticBatch);
 constexpr size_t kStaticScoreFloats = 3 * kStaticRows * kStaticRows + 12 * kStaticRows + 4;
 constexpr size_t kStaticTokOff = 256;
 constexpr size_t kStaticItemsOff = kStaticTokOff + 16 * kStaticRows;

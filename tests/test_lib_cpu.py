@@ -99,7 +99,7 @@ def test_attention_plan_covers_each_sequence(eg2):
     """Every (pair, key) of each sequence (pair = 3 (token - start) + head)
     is covered by exactly one score item (32-key blocks from the sequence
     start times 32-pair blocks), every pair by exactly one context item
-    (64-pair blocks), the score items coming first; the 1/sum area takes
+    (32-pair blocks), the score items coming first; the 1/sum area takes
     ceil4(3 rows) floats, then each sequence's scores 3 n ceil4(n) floats
     after the previous ones; every token's record names its sequence and
     that first score index."""
@@ -124,7 +124,7 @@ def test_attention_plan_covers_each_sequence(eg2):
         else:
             p0, p1, sb = f2, f3, f4
             assert sb == base[s] and f5 == f6 == f7 == 0
-            assert p0 % 64 == 0 and p1 == min(3 * n, p0 + 64)
+            assert p0 % 32 == 0 and p1 == min(3 * n, p0 + 32)
             ctx[s][p0:p1] += 1
     for s in covered:
         assert (covered[s] == 1).all(), s
