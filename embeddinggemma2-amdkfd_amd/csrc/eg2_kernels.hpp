@@ -45,7 +45,7 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // score items (8 uint32: sequence start, end, first key of a 32-key
 // block, first pair, end of the pairs, the sequence's first score index,
 // 0, 0) followed by item_count[1] context items (sequence start, end,
-// first pair of a 64-pair block, end of the pairs, first score index, 0,
+// first pair of a 32-pair block, end of the pairs, first score index, 0,
 // 0, 0); a pair is 3 (token - start) + head. tok: one record per row (4
 // uint32: sequence start, end, first score index, 0). `grid` workgroups
 // stride over each item list. scores: the plan's score floats (the 1/sum

@@ -10,11 +10,14 @@
 //  * element-wise work runs one float4 per lane per 256 columns, coalesced,
 //    with the row kept in registers from load to store;
 //  * the SSE2-order sum of squares (kernels.c:82-94) runs one lane per
-//    chain: lane c owns chain c (the sequential sum of row[8t + c]^2) over
+//    chain: a lane owns chain c (the sequential sum of row[8t + c]^2) over
 //    the row staged transposed in LDS (24 16-byte reads per lane, all issued
-//    before the dependent additions); every 8-lane group computes the same
-//    chains and combines them with DPP moves, so every lane ends with the
-//    total without an LDS round trip;
+//    before the dependent additions), and an 8-lane group combines a row's
+//    eight chains with DPP moves. The residual kernel stages eight rows per
+//    workgroup and its first wave runs all 64 chains (8 rows x 8 chains);
+//    the embedding kernel's single wave runs its row's chains in every
+//    8-lane group, so every lane ends with the total without an LDS round
+//    trip;
 //  * Q8_0 quantization works on the registers: a 32-value block is 8 lanes
 //    x 4 values, its maximum combined by DPP, and each lane stores its 4
 //    int8 values as one 32-bit word of the row tiles.
