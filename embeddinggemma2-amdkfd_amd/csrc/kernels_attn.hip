@@ -37,7 +37,9 @@
 //    pairs x 16 keys; per 4 dimensions one 4-block MFMA whose block c
 //    multiplies chain c (lane group c feeds chain c's q and k values), and
 //    each lane adds its 16 products to its 4 pairs' 4 chain sums. The
-//    scores go to a scratch row per pair (row length rounded up to 4).
+//    scores go to a scratch row per pair (row length rounded up to 4). A
+//    workgroup takes items in turn and loads the next item's first half
+//    while its current item's second half computes.
 //  - attention_exp_kernel: one wave per (token, head): the row maximum,
 //    then every lane's expf of its keys, written back over the scores.
 //  - attention_sum_kernel: one lane per (token, head): the sum of its p
@@ -122,45 +124,132 @@ __device__ __forceinline__ void store16(const Stage16& v, float* row, int grp) {
   *reinterpret_cast<float4*>(row + 3 * 32 + 4 * grp) = make_float4(v.a.w, v.b.w, v.c.w, v.d.w);
 }
 
+// One staged half (kSDims dimensions) of the wave's 16 pairs x 16 keys:
+// per 4 steps the 4 MFMAs into separate registers, then their adds (the
+// adds of one overlap the next ones' execution), with the next 4 steps'
+// operands read from LDS before the adds.
+__device__ __forceinline__ void scores_half(const float* qa, const float* kb, float (&acc)[4][4]) {
+  const floatx16 zero = {};
+  float4 q4 = *reinterpret_cast<const float4*>(qa), k4 = *reinterpret_cast<const float4*>(kb);
+#pragma unroll
+  for (int s = 0; s < kSDims / 4; s += 4) {
+    const float qv[4] = {q4.x, q4.y, q4.z, q4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
+    floatx16 prod[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
+      prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e], kv[e], zero, 0, 0, 0);
+    if (s + 4 < kSDims / 4) {
+      q4 = *reinterpret_cast<const float4*>(qa + s + 4);
+      k4 = *reinterpret_cast<const float4*>(kb + s + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The wave's 16 x 16 scores ((chain 0 + chain 2) + (chain 1 + chain 3),
+// kernels.c:35-39) for the (pair, key)s inside the pair's window.
+__device__ __forceinline__ void store_scores(const float (&acc)[4][4], uint32_t lo, uint32_t hi, uint32_t key0,
+                                             uint32_t pair0, uint32_t pair1, size_t sbase, int window, int pr,
+                                             int kr, int g, int r16, float* __restrict__ scores) {
+  const uint32_t pitch = score_pitch(hi - lo);
+  const uint32_t key = key0 + kr + r16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t pair = pair0 + pr + 4 * g + r;
+    const float score = (acc[0][r] + acc[2][r]) + (acc[1][r] + acc[3][r]);
+    if (pair < pair1 && key < hi) {
+      uint32_t first, last;
+      key_range(lo + pair / 3, lo, hi, window, first, last);
+      if (key >= first && key < last) scores[sbase + (size_t)pair * pitch + (key - lo)] = score;
+    }
+  }
+}
+
+// A score item's tile, its fields clamped to the wave (so a malformed list
+// cannot address outside the rows); valid is 0 for an empty or malformed
+// item and for a tile with no (pair, key) inside the window.
+struct ScoreTile {  // all 32-bit fields: no padding bytes for a copy to carry
+  uint32_t lo, hi, key0, pair0, pair1, sbase, valid;
+};
+__device__ __forceinline__ ScoreTile score_tile(const uint4* __restrict__ items, uint32_t item, int window,
+                                                int rows) {
+  const uint4 a = items[2 * item], b = items[2 * item + 1];
+  ScoreTile t;
+  t.hi = min(a.y, (uint32_t)rows);
+  t.lo = min(a.x, t.hi);
+  const uint32_t len = t.hi - t.lo;
+  t.key0 = a.z;
+  t.pair1 = min(b.x, 3 * len);
+  t.pair0 = a.w;
+  t.sbase = b.y;
+  t.valid = len != 0 && t.key0 >= t.lo && t.key0 < t.hi && t.pair0 < t.pair1 ? 1u : 0u;
+  if (t.valid && window > 0) {
+    const int half = window / 2;
+    const int tmin = (int)(t.lo + t.pair0 / 3), tmax = (int)(t.lo + (t.pair1 - 1) / 3);
+    const int kmin = (int)t.key0, kmax = (int)min(t.key0 + kSKeys, t.hi) - 1;
+    t.valid = kmax < tmin - half || kmin > tmax + half ? 0u : 1u;
+  }
+  return t;
+}
+
+// Offsets in qkv of staging row srow's pair row and key row of tile t
+// (clamped; the rows past the tile's end are computed and not stored).
+__device__ __forceinline__ void score_sources(const ScoreTile& t, int srow, size_t& qoff, size_t& koff) {
+  const uint32_t spair = min(t.pair0 + (uint32_t)srow, t.pair1 - 1), skey = min(t.key0 + (uint32_t)srow, t.hi - 1);
+  qoff = (size_t)(t.lo + spair / 3) * kLd + (spair % 3) * kHeadDim;
+  koff = (size_t)skey * kLd + kKOff;
+}
+
+// The first item from `item` on (stride gridDim.x) that has work, its tile
+// in t; count when none is left. Uniform over the workgroup.
+__device__ __forceinline__ uint32_t next_score_item(const uint4* __restrict__ items, uint32_t item, uint32_t count,
+                                                    int window, int rows, ScoreTile& t) {
+  for (; item < count; item += gridDim.x) {
+    t = score_tile(items, item, window, rows);
+    if (t.valid) break;
+  }
+  return item;
+}
+
+// The workgroup takes items in turn (grid-stride); each half's values are
+// loaded while the previous half computes: the second half's during the
+// first, the next item's first half during the second.
 __global__ void __launch_bounds__(256)
 attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__ items,
-                        const uint32_t* __restrict__ item_count, int window, int rows,
-                        float* __restrict__ scores) {
+                                 const uint32_t* __restrict__ item_count, int window, int rows,
+                                 float* __restrict__ scores) {
   __shared__ __align__(16) float qs[kSPairs * kSPitch];
   __shared__ __align__(16) float ks[kSKeys * kSPitch];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
-  const int pr = 16 * (w >> 1), kr = 16 * (w & 1);  // the wave's 16 pairs and 16 keys in the tile
-  const int srow = tid >> 3, grp = tid & 7;          // staging: row and 16-dimension group
+  const int pr = 16 * (w >> 1), kr = 16 * (w & 1);
+  const int srow = tid >> 3, grp = tid & 7;
   const uint32_t count = item_count[0];
-  const floatx16 zero = {};
-  for (uint32_t item = blockIdx.x; item < count; item += gridDim.x) {
-    // Item fields clamped to the wave, so a malformed list cannot address
-    // outside the rows.
-    const uint4 a = items[2 * item], b = items[2 * item + 1];
-    const uint32_t hi = min(a.y, (uint32_t)rows), lo = min(a.x, hi), len = hi - lo;
-    const uint32_t key0 = a.z, pair1 = min(b.x, 3 * len), pair0 = a.w;
-    if (len == 0 || key0 < lo || key0 >= hi || pair0 >= pair1) continue;  // uniform over the workgroup
-    const size_t sbase = b.y;
-    const uint32_t pitch = score_pitch(len);
-    if (window > 0) {  // skip a tile with no (pair, key) inside the window
-      const int half = window / 2;
-      const int tmin = (int)(lo + pair0 / 3), tmax = (int)(lo + (pair1 - 1) / 3);
-      const int kmin = (int)key0, kmax = (int)min(key0 + kSKeys, hi) - 1;
-      if (kmax < tmin - half || kmin > tmax + half) continue;
-    }
-    float acc[4][4];  // [chain][pair 4g + r]
+  ScoreTile t;
+  uint32_t item = next_score_item(items, blockIdx.x, count, window, rows, t);
+  size_t qoff = 0, koff = 0;
+  Stage16 qn, kn;
+  if (item < count) {
+    score_sources(t, srow, qoff, koff);
+    qn = load16(qkv + qoff + 16 * grp);
+    kn = load16(qkv + koff + 16 * grp);
+  }
+  while (item < count) {
+    float acc[4][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[c][r] = 0.0f;
-    // Staging sources: this thread's pair row and key row (clamped; the
-    // rows past the tile's end are computed and not stored).
-    const uint32_t spair = min(pair0 + (uint32_t)srow, pair1 - 1), skey = min(key0 + (uint32_t)srow, hi - 1);
-    const float* qsrc = qkv + (size_t)(lo + spair / 3) * kLd + (spair % 3) * kHeadDim;
-    const float* ksrc = qkv + (size_t)skey * kLd + kKOff;
-    // The second half's values are loaded while the first half computes.
-    Stage16 qn = load16(qsrc + 16 * grp), kn = load16(ksrc + 16 * grp);
+    ScoreTile nt = t;
+    uint32_t nitem = count;
+    size_t nqoff = qoff, nkoff = koff;
 #pragma unroll 1
     for (int part = 0; part < kHeadDim / kSDims; ++part) {
       __syncthreads();  // the previous half's (or item's) rows are no longer read
@@ -168,47 +257,23 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
       store16(kn, ks + srow * kSPitch, grp);
       __syncthreads();
       if (part + 1 < kHeadDim / kSDims) {
-        qn = load16(qsrc + (part + 1) * kSDims + 16 * grp);
-        kn = load16(ksrc + (part + 1) * kSDims + 16 * grp);
-      }
-      const float* qa = qs + (pr + r16) * kSPitch + 32 * g;
-      const float* kb = ks + (kr + r16) * kSPitch + 32 * g;
-      // Per 4 steps: the 4 MFMAs into separate registers, then their adds
-      // (the adds of one overlap the next ones' execution), with the next
-      // 4 steps' operands read from LDS before the adds.
-      float4 q4 = *reinterpret_cast<const float4*>(qa), k4 = *reinterpret_cast<const float4*>(kb);
-#pragma unroll
-      for (int s = 0; s < kSDims / 4; s += 4) {
-        const float qv[4] = {q4.x, q4.y, q4.z, q4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
-        floatx16 prod[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
-          prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e], kv[e], zero, 0, 0, 0);
-        if (s + 4 < kSDims / 4) {
-          q4 = *reinterpret_cast<const float4*>(qa + s + 4);
-          k4 = *reinterpret_cast<const float4*>(kb + s + 4);
+        qn = load16(qkv + qoff + (part + 1) * kSDims + 16 * grp);
+        kn = load16(qkv + koff + (part + 1) * kSDims + 16 * grp);
+      } else {
+        nitem = next_score_item(items, item + gridDim.x, count, window, rows, nt);
+        if (nitem < count) {
+          score_sources(nt, srow, nqoff, nkoff);
+          qn = load16(qkv + nqoff + 16 * grp);
+          kn = load16(qkv + nkoff + 16 * grp);
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
-        __builtin_amdgcn_sched_barrier(0);
       }
+      scores_half(qs + (pr + r16) * kSPitch + 32 * g, ks + (kr + r16) * kSPitch + 32 * g, acc);
     }
-    const uint32_t key = key0 + kr + r16;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t pair = pair0 + pr + 4 * g + r;
-      const float score = (acc[0][r] + acc[2][r]) + (acc[1][r] + acc[3][r]);
-      if (pair < pair1 && key < hi) {
-        uint32_t first, last;
-        key_range(lo + pair / 3, lo, hi, window, first, last);
-        if (key >= first && key < last) scores[sbase + (size_t)pair * pitch + (key - lo)] = score;
-      }
-    }
+    store_scores(acc, t.lo, t.hi, t.key0, t.pair0, t.pair1, t.sbase, window, pr, kr, g, r16, scores);
+    item = nitem;
+    t = nt;
+    qoff = nqoff;
+    koff = nkoff;
   }
 }
 
