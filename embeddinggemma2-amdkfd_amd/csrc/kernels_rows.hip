@@ -35,19 +35,21 @@ constexpr int kVec = kEmbd / 256;                      // float4 per lane per ro
 // A 768-float token row is held one float4 per lane per 256 columns (lane L
 // has elements 4L..4L+3 + 256r, r = 0..2). Its SSE2 sum of squares
 // (kernels.c:82-94) needs chain c = the sequential sum over t of
-// row[8t + c]^2: the row is staged transposed in LDS, tr[c][t] = row[8t + c],
-// so lane c reads its 96 values with 24 ds_read_b128. The 104-float pitch
+// row[8t + c]^2: the row's squares (each rounded, as the reference's) are
+// staged transposed in LDS, tr[c][t] = row[8t + c]^2, by every lane of the
+// row, so the lane that runs chain c reads its 96 squares with 24
+// ds_read_b128 and only adds. The 104-float pitch
 // puts the eight chain rows 40 banks apart (conflict-free reads) and the
 // two lanes of a pair 32 banks apart (conflict-free transposed writes).
 constexpr int kChain = kEmbd / 8;  // 96
 constexpr int kTPitch = kChain + 8;
 typedef float TRow[kTPitch];
 
-__device__ __forceinline__ void stage_transposed(TRow* tr, const float4 (&v)[kVec]) {
+__device__ __forceinline__ void stage_squares(TRow* tr, const float4 (&v)[kVec]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
-    const float c4[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+    const float c4[4] = {v[r].x * v[r].x, v[r].y * v[r].y, v[r].z * v[r].z, v[r].w * v[r].w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int e = 4 * (lane + 64 * r) + k;
@@ -56,20 +58,19 @@ __device__ __forceinline__ void stage_transposed(TRow* tr, const float4 (&v)[kVe
   }
 }
 
-// Chain c of the SSE2 sum of squares from the transposed row, every read
+// Chain c of the SSE2 sum of squares from the staged squares, every read
 // issued before the dependent additions.
-__device__ __forceinline__ float transposed_chain(const TRow* tr, int c) {
+__device__ __forceinline__ float squares_chain(const TRow* tr, int c) {
   float4 v[kChain / 4];
 #pragma unroll
   for (int j = 0; j < kChain / 4; ++j) v[j] = *reinterpret_cast<const float4*>(&tr[c][4 * j]);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < kChain / 4; ++j) {
-    const float p0 = v[j].x * v[j].x, p1 = v[j].y * v[j].y, p2 = v[j].z * v[j].z, p3 = v[j].w * v[j].w;
-    s = s + p0;
-    s = s + p1;
-    s = s + p2;
-    s = s + p3;
+    s = s + v[j].x;
+    s = s + v[j].y;
+    s = s + v[j].z;
+    s = s + v[j].w;
   }
   return s;
 }
@@ -173,9 +174,9 @@ embed_norm_quant_kernel(const uint8_t* __restrict__ table, const int32_t* __rest
     v[r].w = dd * (float)(int8_t)qs[3];
     *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = v[r];
   }
-  stage_transposed(tr, v);
+  stage_squares(tr, v);
   __syncthreads();
-  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr, lane & 7)), kEmbd, eps);
+  const float inv = rms_inverse(sse2_combine_dpp(squares_chain(tr, lane & 7)), kEmbd, eps);
   // (x*w)*inv (kernels.c:124-133, SSE2 branch), then Q8_0 (kernels.c:139-151).
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
@@ -202,7 +203,7 @@ __device__ __forceinline__ void group_rms_inverse(float* tr, float* inv, float e
   if (threadIdx.x >= 64) return;
   const int lane = threadIdx.x;
   const TRow* rows = reinterpret_cast<const TRow*>(token_rows(tr, lane >> 3));
-  const float r = rms_inverse(sse2_combine_dpp(transposed_chain(rows, lane & 7)), kEmbd, eps);
+  const float r = rms_inverse(sse2_combine_dpp(squares_chain(rows, lane & 7)), kEmbd, eps);
   if ((lane & 7) == 0) inv[lane >> 3] = r;
 }
 
@@ -230,7 +231,7 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
     if (next_w) nv[r] = *reinterpret_cast<const float4*>(next_w + e);
   }
   float* mine = token_rows(tr, w);
-  stage_transposed(reinterpret_cast<TRow*>(mine), hv);
+  stage_squares(reinterpret_cast<TRow*>(mine), hv);
   __syncthreads();
   group_rms_inverse(tr, inv_s[0], eps);
   __syncthreads();
@@ -245,7 +246,7 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   }
   if (!next_w) return;  // uniform over the grid
   // Wave 0 read every token's rows before the barrier above.
-  stage_transposed(reinterpret_cast<TRow*>(mine), xv);
+  stage_squares(reinterpret_cast<TRow*>(mine), xv);
   __syncthreads();
   group_rms_inverse(tr, inv_s[1], eps);
   __syncthreads();
@@ -369,9 +370,9 @@ rms_norm_rows_kernel(float* __restrict__ x, const float* __restrict__ w, float e
   float4 xv[kVec];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) xv[r] = *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + 4 * (lane + 64 * r));
-  stage_transposed(tr, xv);
+  stage_squares(tr, xv);
   __syncthreads();
-  const float inv = rms_inverse(sse2_combine_dpp(transposed_chain(tr, lane & 7)), kEmbd, eps);
+  const float inv = rms_inverse(sse2_combine_dpp(squares_chain(tr, lane & 7)), kEmbd, eps);
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
