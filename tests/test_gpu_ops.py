@@ -283,6 +283,33 @@ def test_gemm_q8_bit_exact(eg2, gpu, n, m, k):
     assert np.array_equal(host(y), OL.gemm_q8_0(w, xb))
 
 
+def test_gemm_q8_extreme_block_dots(eg2, gpu):
+    """Block dots at both ends of their range (all -128 x -128 = +2^19, and
+    -128 x 127 = -16256 x 32) and scales across the fp16 range, subnormal
+    to the largest (outputs from 1e-9 to 1e16): the biased accumulator
+    keeps every dot exact (1.5 2^23 + dot stays in [2^23, 2^24)), and the
+    outputs are the oracle's bit for bit."""
+    import torch
+
+    n, m, k = 64, 96, 768
+    w = quantize_q8_0((RNG.standard_normal((m, k)) * 0.02).astype(np.float32))
+    xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
+    w["qs"][: m // 2] = -128
+    w["qs"][m // 2:m // 2 + 8] = 127
+    xb["qs"][: n // 2] = -128
+    scales = np.array([6.0e-8, 6.1e-5, 1.0, 0.0039, 1024.0, 65504.0], np.float16)
+    w["d"] = scales[RNG.integers(0, len(scales), w["d"].shape)].view(np.uint16)
+    xb["d"] = scales[RNG.integers(0, len(scales), xb["d"].shape)].view(np.uint16)
+    w["d"][-8:] = scales[0].view(np.uint16)  # rows and columns of the smallest scale only
+    xb["d"][-8:] = scales[0].view(np.uint16)
+    y = empty((n, m), torch.float32, gpu)
+    eg2.ops.gemm_q8(*device_q8(eg2, xb, k, gpu), *device_weights(eg2, w, k, gpu), y)
+    want = OL.gemm_q8_0(w, xb)
+    assert np.array_equal(bits(host(y)), bits(want))
+    mag = np.abs(want[want != 0])
+    assert mag.max() > 1e15 and mag.min() < 1e-6
+
+
 def test_gemm_q8_strided_output(eg2, gpu):
     """ldy > m writes into a wider row (the fused-projection layout)."""
     import torch
