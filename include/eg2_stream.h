@@ -64,10 +64,13 @@ bool eg2_normalize_prefix(float *embedding, unsigned dims);
 
 /* Embeds a stream of texts: text i is ids[text_offsets[i] ..
  * text_offsets[i+1]) with output width dims[i]. The texts are packed into
- * waves by eg2_pack_waves; the waves run on the context's lanes (taken
- * from its pool, eg2_hip.h), wave w on the (w mod lanes)-th, so that up to
- * that many waves are in flight, each exactly as ei_gemma2_kfd_batch would
- * run it (one hipGraph per lane and padded wave size). Each embedding is
+ * waves by eg2_pack_waves; the waves run on lanes taken from the context's
+ * pool (eg2_hip.h) before the first wave: one, waited for, and as many more
+ * as are free at that moment, up to the context's lane count (so that
+ * concurrent callers never wait for each other's lanes). Wave w runs on the
+ * (w mod taken)-th, so that up to that many waves are in flight, each
+ * exactly as ei_gemma2_kfd_batch would run it (one hipGraph per lane and
+ * padded wave size). Each embedding is
  * written to out[i * 768 ..] normalised to its prefix
  * (eg2_normalize_prefix; the values past dims[i] are zeroed). *n_waves (if
  * not NULL) receives the wave count. Returns false and a "HIP: ..." message
