@@ -11,9 +11,9 @@
 //    with the row kept in registers from load to store;
 //  * the SSE2-order sum of squares (kernels.c:82-94) runs one lane per
 //    chain: a lane owns chain c (the sequential sum of row[8t + c]^2) over
-//    the row staged transposed in LDS (24 16-byte reads per lane, all issued
-//    before the dependent additions), and an 8-lane group combines a row's
-//    eight chains with DPP moves. The residual kernel stages eight rows per
+//    the row staged transposed in LDS (24 16-byte reads per lane, in three
+//    groups of eight issued before their dependent additions), and an 8-lane
+//    group combines a row's eight chains with DPP moves. The residual kernel stages eight rows per
 //    workgroup and its first wave runs all 64 chains (8 rows x 8 chains);
 //    the embedding kernel's single wave runs its row's chains in every
 //    8-lane group, so every lane ends with the total without an LDS round
@@ -58,19 +58,25 @@ __device__ __forceinline__ void stage_squares(TRow* tr, const float4 (&v)[kVec])
   }
 }
 
-// Chain c of the SSE2 sum of squares from the staged squares, every read
-// issued before the dependent additions.
+// Chain c of the SSE2 sum of squares from the staged squares, read in three
+// groups of eight float4, each group's reads issued before its additions.
+// The rolled outer loop keeps 32 registers of reads in flight, not 96: the
+// residual kernel's register count (and so how many of its waves fit beside
+// other streams' kernels on a CU) is set by this chain.
 __device__ __forceinline__ float squares_chain(const TRow* tr, int c) {
-  float4 v[kChain / 4];
-#pragma unroll
-  for (int j = 0; j < kChain / 4; ++j) v[j] = *reinterpret_cast<const float4*>(&tr[c][4 * j]);
   float s = 0.0f;
+#pragma unroll 1
+  for (int g = 0; g < kChain / 32; ++g) {
+    float4 v[8];
 #pragma unroll
-  for (int j = 0; j < kChain / 4; ++j) {
-    s = s + v[j].x;
-    s = s + v[j].y;
-    s = s + v[j].z;
-    s = s + v[j].w;
+    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(&tr[c][32 * g + 4 * j]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s = s + v[j].x;
+      s = s + v[j].y;
+      s = s + v[j].z;
+      s = s + v[j].w;
+    }
   }
   return s;
 }
@@ -211,24 +217,30 @@ __device__ __forceinline__ void group_rms_inverse(float* tr, float* inv, float e
 // kernels.c:139-151 with the next norm weight on the updated residual. With
 // next_w == nullptr only the residual update runs. Rows past `rows` in the
 // last workgroup load nothing and store nothing; their waves still join
-// every barrier.
+// every barrier. The two norm weight vectors are staged once per workgroup
+// in LDS (threads 0-191 and 192-383, one float4 each) rather than held in
+// every wave's registers.
 __global__ void __launch_bounds__(64 * kRowsPerGroup)
 residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, const float* __restrict__ post_w,
                            const float* __restrict__ next_w, float eps, int8_t* __restrict__ xq,
                            float* __restrict__ xd, int rows) {
   __shared__ __align__(16) float tr[kRowsPerGroup * kTokStride];
   __shared__ float inv_s[2][kRowsPerGroup];
+  __shared__ float4 wl[2][kEmbd / 4];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kRowsPerGroup + w;
   const bool live = t < rows;
-  float4 hv[kVec], xv[kVec], wv[kVec], nv[kVec];
+  if (threadIdx.x < kEmbd / 4) {
+    wl[0][threadIdx.x] = reinterpret_cast<const float4*>(post_w)[threadIdx.x];
+  } else if (threadIdx.x < kEmbd / 2 && next_w) {
+    wl[1][threadIdx.x - kEmbd / 4] = reinterpret_cast<const float4*>(next_w)[threadIdx.x - kEmbd / 4];
+  }
+  float4 hv[kVec], xv[kVec];
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     hv[r] = live ? *reinterpret_cast<const float4*>(h + (size_t)t * kEmbd + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     xv[r] = live ? *reinterpret_cast<const float4*>(x + (size_t)t * kEmbd + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    wv[r] = *reinterpret_cast<const float4*>(post_w + e);
-    if (next_w) nv[r] = *reinterpret_cast<const float4*>(next_w + e);
   }
   float* mine = token_rows(tr, w);
   stage_squares(reinterpret_cast<TRow*>(mine), hv);
@@ -240,7 +252,8 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   for (int r = 0; r < kVec; ++r) {
     const int e = 4 * (lane + 64 * r);
     const float a0 = hv[r].x * inv_h, a1 = hv[r].y * inv_h, a2 = hv[r].z * inv_h, a3 = hv[r].w * inv_h;
-    const float b0 = a0 * wv[r].x, b1 = a1 * wv[r].y, b2 = a2 * wv[r].z, b3 = a3 * wv[r].w;
+    const float4 wr = wl[0][lane + 64 * r];
+    const float b0 = a0 * wr.x, b1 = a1 * wr.y, b2 = a2 * wr.z, b3 = a3 * wr.w;
     xv[r] = make_float4(xv[r].x + b0, xv[r].y + b1, xv[r].z + b2, xv[r].w + b3);
     if (live) *reinterpret_cast<float4*>(x + (size_t)t * kEmbd + e) = xv[r];
   }
@@ -254,7 +267,8 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   // (x*w)*inv (kernels.c:124-133, SSE2 branch), then Q8_0 (kernels.c:139-151).
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
-    const float p0 = xv[r].x * nv[r].x, p1 = xv[r].y * nv[r].y, p2 = xv[r].z * nv[r].z, p3 = xv[r].w * nv[r].w;
+    const float4 nr = wl[1][lane + 64 * r];
+    const float p0 = xv[r].x * nr.x, p1 = xv[r].y * nr.y, p2 = xv[r].z * nr.z, p3 = xv[r].w * nr.w;
     xv[r] = make_float4(p0 * inv, p1 * inv, p2 * inv, p3 * inv);
   }
   if (live) quantize_row_lanes(xv, t, xq, xd + t, rows);
