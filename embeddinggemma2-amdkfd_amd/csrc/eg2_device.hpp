@@ -269,9 +269,11 @@ __device__ __forceinline__ void geglu_exact_passes(const float (&g)[8], const fl
 //     value closer than that (or non-finite) is evaluated exactly. A block whose
 //     1/d overflows quantizes to -128 throughout (q8_value) and needs no
 //     decision.
-__device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const float (&u)[8], bool store,
-                                                     int8_t* __restrict__ q, float* __restrict__ d_out) {
-  float a[8], bound[8];
+// Steps 1 and 2's candidate test of geglu_quantize_part4: the approximations
+// a[], their bounds, and the candidate bits (every block has one: the value
+// with the largest |A| - B passes the test).
+__device__ __forceinline__ uint32_t geglu_approx_part4(const float (&g)[8], const float (&u)[8], float (&a)[8],
+                                                       float (&bound)[8]) {
   float mlo = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -287,8 +289,15 @@ __device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const 
   uint32_t cand = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) cand |= !(fabsf(a[i]) + bound[i] < mlo) ? 1u << i : 0u;
+  return cand;
+}
+
+// Steps 2 (from the exact candidates in a[]) and 3 of geglu_quantize_part4,
+// and the stores.
+__device__ __forceinline__ void geglu_decide_part4(const float (&g)[8], const float (&u)[8], const float (&bound)[8],
+                                                   uint32_t cand, float (&a)[8], bool store, int8_t* __restrict__ q,
+                                                   float* __restrict__ d_out) {
   int32_t qi[8];
-  geglu_exact_passes<false>(g, u, cand, 0.0f, a, qi);  // a[] now exact for the candidates
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, cand & (1u << i) ? fabsf(a[i]) : 0.0f);
@@ -310,6 +319,15 @@ __device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const 
   if (!store) return;
   if ((threadIdx.x & 3) == 0) *d_out = fp16_bits_to_fp32(fp32_to_fp16_bits(d));
   *reinterpret_cast<uint2*>(q) = make_uint2(pack_i8x4(qi[0], qi[1], qi[2], qi[3]), pack_i8x4(qi[4], qi[5], qi[6], qi[7]));
+}
+
+__device__ __forceinline__ void geglu_quantize_part4(const float (&g)[8], const float (&u)[8], bool store,
+                                                     int8_t* __restrict__ q, float* __restrict__ d_out) {
+  float a[8], bound[8];
+  const uint32_t cand = geglu_approx_part4(g, u, a, bound);
+  int32_t unused[8];
+  geglu_exact_passes<false>(g, u, cand, 0.0f, a, unused);  // a[] now exact for the candidates
+  geglu_decide_part4(g, u, bound, cand, a, store, q, d_out);
 }
 
 // Chain c of the SSE2 sum of squares of an n-float row (kernels.c:82-94):

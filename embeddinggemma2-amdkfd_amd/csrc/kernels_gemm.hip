@@ -147,6 +147,52 @@ constexpr int kGPitch = 40;  // floats per row of the GeGLU epilogue's transpose
 // hold one row's block, and run the standalone GeGLU kernel's code
 // (geglu_quantize_part4): the int8 values go to gq in the row-tile layout
 // (nbf blocks per row), the scales to gd[tc * ldg + row].
+// Minimum over each aligned quad of lanes, on every lane of it (all 64 lanes
+// active).
+__device__ __forceinline__ uint32_t quad_min_u32(uint32_t m) {
+  m = min(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0xB1, 0xf, 0xf, true));
+  return min(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0x4E, 0xf, 0xf, true));
+}
+
+// The exact GeGLU values of the workgroup's block-maximum candidates
+// (geglu_quantize_part4, step 2) in one pass of one wave instead of one per
+// wave: the workgroup's 4 waves hold 64 blocks (a quad of lanes each), and
+// each block's first candidate -- the lowest one of the quad's lowest lane
+// that has any; every block has one -- goes to LDS slot 16 w + quad; wave 0
+// evaluates slot `lane` with gelu_mul, and the owner takes the value back
+// into a[]. A block's other candidates (values within their bounds of its
+// largest: rare) take the per-wave passes, which run only when some lane
+// has one. All 256 threads must call it.
+__device__ __forceinline__ void geglu_block_candidates(const float (&g)[8], const float (&u)[8], uint32_t cand,
+                                                       float (&a)[8]) {
+  __shared__ float slot_g[64], slot_u[64], slot_x[64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t own = cand ? ((uint32_t)(lane & 3) << 3) | (uint32_t)__builtin_ctz(cand) : 0xffu;
+  const uint32_t key = quad_min_u32(own);
+  const bool owner = (int)(key >> 3) == (lane & 3);
+  const int k = (int)(key & 7), s = 16 * w + (lane >> 2);
+  if (owner) {
+    float gk = g[0], uk = u[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      gk = k == i ? g[i] : gk;
+      uk = k == i ? u[i] : uk;
+    }
+    slot_g[s] = gk;
+    slot_u[s] = uk;
+  }
+  __syncthreads();
+  if (w == 0) slot_x[lane] = gelu_mul(slot_g[lane], slot_u[lane]);
+  __syncthreads();
+  if (owner) {
+    const float x = slot_x[s];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = k == i ? x : a[i];
+  }
+  int32_t unused[8];
+  geglu_exact_passes<false>(g, u, owner ? cand & ~(1u << k) : cand, 0.0f, a, unused);
+}
+
 __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int tc, int wr, int wc, int n, int nbf,
                                                int8_t* __restrict__ gq, float* __restrict__ gd, int ldg) {
   const int lane = threadIdx.x & 63, g = lane >> 5;
@@ -186,7 +232,11 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
     us[4 * h] = u4.x, us[4 * h + 1] = u4.y, us[4 * h + 2] = u4.z, us[4 * h + 3] = u4.w;
   }
   const int t = 64 * tr + 32 * wr + rr;
-  geglu_quantize_part4(gs, us, t < n, gq + q8_tile_offset(t, 32 * tc + 8 * part, nbf), gd + (size_t)tc * ldg + t);
+  float a[8], bound[8];
+  const uint32_t cand = geglu_approx_part4(gs, us, a, bound);
+  geglu_block_candidates(gs, us, cand, a);  // a[] now exact for the candidates
+  geglu_decide_part4(gs, us, bound, cand, a, t < n, gq + q8_tile_offset(t, 32 * tc + 8 * part, nbf),
+                     gd + (size_t)tc * ldg + t);
 }
 
 // TAIL: nb % kStages != 0 (a separate instantiation: the tail code costs
