@@ -13,8 +13,9 @@
 //    chain: a lane owns chain c (the sequential sum of row[8t + c]^2) over
 //    the row staged transposed in LDS (24 16-byte reads per lane, in three
 //    groups of eight issued before their dependent additions), and an 8-lane
-//    group combines a row's eight chains with DPP moves. The residual kernel stages eight rows per
-//    workgroup and its first wave runs all 64 chains (8 rows x 8 chains);
+//    group combines a row's eight chains with DPP moves. The residual kernel
+//    stages eight rows per workgroup and its first wave runs all 64 chains
+//    (8 rows x 8 chains);
 //    the embedding kernel's single wave runs its row's chains in every
 //    8-lane group, so every lane ends with the total without an LDS round
 //    trip;
@@ -127,24 +128,39 @@ __device__ __forceinline__ float group8_max(float m) {
 
 // quants.c:97-177 (scalar path) on the row held as float4 per lane: block b
 // (32 values) is lanes 8(b % 8)..+7 of register r = b / 8, four values per
-// lane; the block maximum is combined over those 8 lanes. Each lane stores
-// its 4 int8 values (contiguous in the row-tile layout) for row t of q;
-// lane 8i of the group stores the float value of the fp16 scale at
-// d[b * ld]. v[r] must already hold the values to quantize.
+// lane; the block maximum is combined over those 8 lanes. A group's three
+// blocks get their scale computed once each: lane 8i + r takes block
+// (r, i)'s maximum, computes d = amax / 127, 1/d and the fp16 scale, and
+// stores the latter's float value at d[b * ld]; the group's lanes take the
+// three 1/d back by swizzle broadcasts (an LDS-unit permute, no VALU work).
+// Each lane stores its 4 int8 values (contiguous in the row-tile layout)
+// for row t of q. v[r] must already hold the values to quantize; all 64
+// lanes must be active.
+template <int R>
+__device__ __forceinline__ float group8_lane(float x) {
+  // ds_swizzle bitmask mode within 32 lanes: source lane (lane & 0x18) | R
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x18 | (R << 5)));
+}
 __device__ __forceinline__ void quantize_row_lanes(const float4 (&v)[kVec], int t, int8_t* __restrict__ q,
                                                    float* __restrict__ d, int ld) {
-  const int lane = threadIdx.x & 63;
+  static_assert(kVec == 3, "three blocks per 8-lane group");
+  const int lane = threadIdx.x & 63, r8 = lane & 7;
+  float amax[kVec];
+#pragma unroll
+  for (int r = 0; r < kVec; ++r)
+    amax[r] = group8_max(fmaxf(fmaxf(fabsf(v[r].x), fabsf(v[r].y)), fmaxf(fabsf(v[r].z), fabsf(v[r].w))));
+  const float am = r8 == 0 ? amax[0] : (r8 == 1 ? amax[1] : amax[2]);  // lanes 8i + 3 .. 7: block 2 again, unused
+  const float dd = div127(am);
+  const float id_own = am != 0.0f ? 1.0f / dd : 0.0f;  // 0 for an all-zero block, whose values quantize to 0
+  if (r8 < kVec) d[(size_t)((lane >> 3) + 8 * r8) * ld] = fp16_bits_to_fp32(fp32_to_fp16_bits(dd));
+  const float ids[kVec] = {group8_lane<0>(id_own), group8_lane<1>(id_own), group8_lane<2>(id_own)};
 #pragma unroll
   for (int r = 0; r < kVec; ++r) {
-    const float amax = group8_max(fmaxf(fmaxf(fabsf(v[r].x), fabsf(v[r].y)), fmaxf(fabsf(v[r].z), fabsf(v[r].w))));
-    const float dd = div127(amax);
-    const float id = amax != 0.0f ? 1.0f / dd : 0.0f;
-    const int e = 4 * (lane + 64 * r), b = e / kQK;
-    // id = 0 for an all-zero block, whose values then quantize to 0.
+    const float id = ids[r];
+    const int e = 4 * (lane + 64 * r);
     const int32_t q0 = q8_value(v[r].x, id), q1 = q8_value(v[r].y, id), q2 = q8_value(v[r].z, id),
                   q3 = q8_value(v[r].w, id);
     *reinterpret_cast<uint32_t*>(q + q8_tile_offset(t, e, kBlocks)) = pack_i8x4(q0, q1, q2, q3);
-    if ((lane & 7) == 0) d[(size_t)b * ld] = fp16_bits_to_fp32(fp32_to_fp16_bits(dd));
   }
 }
 
