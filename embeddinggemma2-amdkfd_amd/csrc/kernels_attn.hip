@@ -57,10 +57,10 @@
 //    chunk's v values in LDS (a chunk inside every pair's window, the usual
 //    case, skips those bounds and the zero fill of rows past the sequence:
 //    about 56 fewer VALU instructions per chunk and wave); per 2 keys each
-//    wave issues one 4-block MFMA
-//    (block b = pairs 16 (b % 2) .. + 15 of key b / 2, columns = its 16
-//    dimensions) and adds the products to its 8 accumulators, in key order.
-//    The Q8_0 epilogue quantizes 32-value blocks over 4 lanes.
+//    wave issues one 4-block MFMA (block b = pairs 16 (b % 2) .. + 15 of key
+//    b / 2, columns = its 16 dimensions) and adds the products to its 8
+//    accumulators, in key order. The Q8_0 epilogue quantizes 32-value
+//    blocks over 4 lanes.
 // A sequence's keys, scores and context depend only on its own tokens, so
 // packing never changes a bit.
 #include <algorithm>
@@ -302,6 +302,7 @@ constexpr int kSmPitch = kShortSoftmax + 4;
 __global__ void __launch_bounds__(64 * kSmWaves)
 attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
+  __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
   __shared__ __align__(16) float prow[kSmWaves][kSmPitch];  // each pair's p values from its first key
   __shared__ uint32_t plen[kSmWaves];                        // and their count (0: no such pair)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -243,6 +243,11 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   __shared__ __align__(16) float tr[kRowsPerGroup * kTokStride];
   __shared__ float inv_s[2][kRowsPerGroup];
   __shared__ float4 wl[2][kEmbd / 4];
+  // Highest issue priority on its SIMDs: this short, latency-bound kernel
+  // (loads, two serial chains, stores) sits on each wave's critical path
+  // and shares the SIMDs with other streams' GEMM and attention waves,
+  // whose throughput-bound work fills the gaps it leaves.
+  __builtin_amdgcn_s_setprio(3);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kRowsPerGroup + w;
   const bool live = t < rows;
