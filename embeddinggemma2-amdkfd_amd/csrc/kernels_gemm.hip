@@ -248,6 +248,9 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
                const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy,
                int8_t* __restrict__ gq, float* __restrict__ gd) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Issue priority 1: above the attention kernels (0), below the short
+  // latency-bound row kernels (3), when other streams share the SIMDs.
+  __builtin_amdgcn_s_setprio(1);
   // XCD-aware order: workgroup b runs on XCD b % 8, which takes one region
   // of the tile grid (column-group major inside it).
   const XcdRegions reg = xcd_regions(n, m);
@@ -424,6 +427,9 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
                         const int32_t* __restrict__ pos, float eps, float* __restrict__ out) {
   __shared__ float invs[32];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Issue priority 1: above the attention kernels (0), below the short
+  // latency-bound row kernels (3), when other streams share the SIMDs.
+  __builtin_amdgcn_s_setprio(1);
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
   const int x = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
   const int r0 = (x / reg.cparts) * reg.rows, c0 = (x % reg.cparts) * reg.cols;
