@@ -38,8 +38,9 @@
 //    multiplies chain c (lane group c feeds chain c's q and k values), and
 //    each lane adds its 16 products to its 4 pairs' 4 chain sums. The
 //    scores go to a scratch row per pair (row length rounded up to 4). A
-//    workgroup takes items in turn and loads the next item's first half
-//    while its current item's second half computes.
+//    workgroup takes items in turn (the workgroups of an XCD, a contiguous
+//    eighth of the list) and loads the next item's first half while its
+//    current item's second half computes.
 //  - attention_exp_kernel: one wave per (token, head): the row maximum,
 //    then every lane's expf of its keys, written back over the scores.
 //  - attention_sum_kernel: one lane per (token, head): the sum of its p
@@ -84,6 +85,7 @@ constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
 constexpr int kShortSoftmax = 512;        // longest sequence for the one-kernel softmax
+constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
 
 // Work items of any packing of `tokens` rows into at most `batch`
 // sequences: per sequence of n tokens, ceil(n/32) ceil(3n/32) <= 3n^2/1024
@@ -210,11 +212,11 @@ __device__ __forceinline__ void score_sources(const ScoreTile& t, int srow, size
   koff = (size_t)skey * kLd + kKOff;
 }
 
-// The first item from `item` on (stride gridDim.x) that has work, its tile
-// in t; count when none is left. Uniform over the workgroup.
+// The first item from `item` on (stride `stride`) below `count` that has
+// work, its tile in t; count when none is left. Uniform over the workgroup.
 __device__ __forceinline__ uint32_t next_score_item(const uint4* __restrict__ items, uint32_t item, uint32_t count,
-                                                    int window, int rows, ScoreTile& t) {
-  for (; item < count; item += gridDim.x) {
+                                                    uint32_t stride, int window, int rows, ScoreTile& t) {
+  for (; item < count; item += stride) {
     t = score_tile(items, item, window, rows);
     if (t.valid) break;
   }
@@ -234,9 +236,17 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
   const int g = lane >> 4, r16 = lane & 15;
   const int pr = 16 * (w >> 1), kr = 16 * (w & 1);
   const int srow = tid >> 3, grp = tid & 7;
-  const uint32_t count = item_count[0];
+  // XCD-aware order (a grid that is a multiple of 8): workgroup b runs on
+  // XCD b % 8, which takes the contiguous eighth of the item list, so an
+  // XCD's L2 holds the rows of few sequences; any other grid strides over
+  // the whole list.
+  const bool by_xcd = gridDim.x % kXcdCount == 0;
+  const uint32_t total = item_count[0], xcd = blockIdx.x % kXcdCount;
+  const uint32_t count = by_xcd ? total * (xcd + 1) / kXcdCount : total;
+  const uint32_t stride = by_xcd ? gridDim.x / kXcdCount : gridDim.x;
   ScoreTile t;
-  uint32_t item = next_score_item(items, blockIdx.x, count, window, rows, t);
+  uint32_t item = next_score_item(items, by_xcd ? total * xcd / kXcdCount + blockIdx.x / kXcdCount : blockIdx.x,
+                                  count, stride, window, rows, t);
   size_t qoff = 0, koff = 0;
   Stage16 qn, kn;
   if (item < count) {
@@ -263,7 +273,7 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
         qn = load16(qkv + qoff + (part + 1) * kSDims + 16 * grp);
         kn = load16(qkv + koff + (part + 1) * kSDims + 16 * grp);
       } else {
-        nitem = next_score_item(items, item + gridDim.x, count, window, rows, nt);
+        nitem = next_score_item(items, item + stride, count, stride, window, rows, nt);
         if (nitem < count) {
           score_sources(nt, srow, nqoff, nkoff);
           qn = load16(qkv + nqoff + 16 * grp);
@@ -450,16 +460,25 @@ attention_sum_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, 
 __global__ void __launch_bounds__(256)
 attention_context_kernel(const float* __restrict__ qkv, const float* __restrict__ scores,
                          const uint4* __restrict__ items, const uint32_t* __restrict__ item_count, int window,
-                         int rows, int8_t* __restrict__ cq, float* __restrict__ cd) {
+                         int rows, int8_t* __restrict__ cq, float* __restrict__ cd, int xcd_order) {
   __shared__ __align__(16) float wl[kCKeys * kCPitchW];  // [key][pair]: w = p * (1/sum), 0 outside the window
   __shared__ __align__(16) float vl[kCKeys * kCPitchV];  // [key][dimension]
   __shared__ uint32_t range[kCPairs][2];                  // each pair's key range
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const uint4* citems = items + 2 * (size_t)item_count[0];  // the context items follow the score items
-  const uint32_t count = 4 * item_count[1];
+  // XCD-aware order as in the scores kernel when xcd_order is set (waves
+  // of sequences up to 512 tokens): XCD b % 8 takes the contiguous eighth
+  // of the work (items x 4 dimension quarters). Waves with longer
+  // sequences keep the plain stride, which spreads an item's four
+  // quarters over four XCDs (measured faster for them).
+  const bool by_xcd = xcd_order && gridDim.x % kXcdCount == 0;
+  const uint32_t total = 4 * item_count[1], xcd = blockIdx.x % kXcdCount;
+  const uint32_t count = by_xcd ? total * (xcd + 1) / kXcdCount : total;
+  const uint32_t stride = by_xcd ? gridDim.x / kXcdCount : gridDim.x;
   const floatx16 zero = {};
-  for (uint32_t work = blockIdx.x; work < count; work += gridDim.x) {
+  for (uint32_t work = by_xcd ? total * xcd / kXcdCount + blockIdx.x / kXcdCount : blockIdx.x; work < count;
+       work += stride) {
     const uint4 a = citems[2 * (work >> 2)], b = citems[2 * (work >> 2) + 1];
     const uint32_t hi = min(a.y, (uint32_t)rows), lo = min(a.x, hi), len = hi - lo;
     const uint32_t pair1 = min(a.w, 3 * len), pair0 = a.z;
@@ -712,7 +731,8 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attention_context_kernel, dim3(grid), dim3(256), 0, st, qkv, scores,
-                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd);
+                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd,
+                     longest > 0 && longest <= kShortSoftmax ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -551,6 +551,33 @@ def test_attention_softmax_forms_agree(eg2, gpu, window):
     assert_attention_bit_exact(*short, oracle_attention(q, k, v, offsets, window))
 
 
+@pytest.mark.parametrize("lens", [[128] * 8 + [60, 4], [700, 5, 300, 39]])
+def test_attention_any_grid_same_bits(eg2, gpu, lens):
+    """The workgroups take the items XCD by XCD (a contiguous eighth each)
+    when the grid is a multiple of 8 and stride over the whole list
+    otherwise; a small grid walks many items per workgroup. Grids 8, 61, 1
+    and 1024 give the same bits, for short waves (the context kernel in XCD
+    order too) and long ones."""
+    import torch
+
+    rng = np.random.default_rng(14 + len(lens))
+    T = sum(lens)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    q, k, v = qkv_inputs(rng, T)
+    ref = run_attention(eg2, gpu, q, k, v, offsets, 0)
+    rows = (T + 3) // 4 * 4
+    offs = list(offsets) + ([rows] if rows > T else [])
+    qkv = np.zeros((rows, eg2.QKV_COLS), np.float32)
+    qkv[:T] = np.concatenate([q, k, v], axis=1)
+    for grid in (8, 61, 1):
+        plan = eg2.AttentionPlan(offs, gpu, rows)
+        plan.GRID = grid
+        cq, cd = qbuf(eg2, rows, N_EMBD, gpu), empty((24, rows), torch.float32, gpu)
+        eg2.ops.attention_planned(dev(qkv, gpu), plan, 0, cq, cd)
+        got = qvals(eg2, cq, rows, N_EMBD)[:T], np.ascontiguousarray(host(cd).T)[:T]
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(bits(got[1]), bits(ref[1])), grid
+
+
 def test_attention_reads_only_scores_it_wrote(eg2, gpu):
     """The scores scratch is written before it is read: any prior content
     (zeros, huge values, NaN) gives the same bits."""
