@@ -318,7 +318,13 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
   __syncthreads();
-  const uint32_t pair = kSmWaves * blockIdx.x + w, t = pair / 3, h = pair % 3;
+  // XCD-aware order (a grid that is a multiple of 8): XCD b % 8 takes the
+  // contiguous eighth of the pair blocks, the pairs whose scores its L2
+  // holds from the scores kernel.
+  const uint32_t blk = gridDim.x % kXcdCount == 0
+                           ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
+                           : blockIdx.x;
+  const uint32_t pair = kSmWaves * blk + w, t = pair / 3, h = pair % 3;
   uint32_t n = 0;
   if (t < (uint32_t)rows) {
     const uint4 meta = tok[t];
@@ -349,7 +355,7 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   __syncthreads();
   if (w == 0 && lane < kSmWaves) {
     const uint32_t cnt = plen[lane];
-    const uint32_t own = kSmWaves * blockIdx.x + lane;
+    const uint32_t own = kSmWaves * blk + lane;
     if (cnt > 0) {
       const float* pr = prow[lane];
       float sum = 0.0f;

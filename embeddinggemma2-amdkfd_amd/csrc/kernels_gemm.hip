@@ -116,21 +116,28 @@ __device__ __forceinline__ void accumulate_products(floatx16& acc, const floatx1
 // of 16 MB for gate|up at 2048 rows); the Q|K|V projection's 5 head columns
 // split evenly only over 8 row parts (40 tiles per XCD at 2048 rows, where
 // 2 row parts would give two XCDs nothing and two half the others' 64).
+// rows_first (the O and down projections, whose output the residual kernel
+// reads row by row) breaks ties toward 8 row parts instead: each XCD then
+// computes whole rows, 256 of 2048, and the residual kernel's workgroups on
+// that XCD take the same rows from its L2.
 struct XcdRegions {
   int cparts, rows, cols;  // column parts; row and column tiles per region
 };
-__host__ __device__ inline XcdRegions xcd_split(int tr_count, int tc_count) {
+__host__ __device__ inline XcdRegions xcd_split(int tr_count, int tc_count, bool rows_first = false) {
   XcdRegions best{0, 0, 0};
-  for (int rparts : {2, 4, 8, 1}) {
+  const int order[2][4] = {{2, 4, 8, 1}, {8, 4, 2, 1}};
+  for (int rparts : order[rows_first ? 1 : 0]) {
     const int cparts = kXcds / rparts;
     const XcdRegions r{cparts, (tr_count + rparts - 1) / rparts, (tc_count + cparts - 1) / cparts};
     if (best.cparts == 0 || r.rows * r.cols < best.rows * best.cols) best = r;
   }
   return best;
 }
-__host__ __device__ inline XcdRegions xcd_regions(int n, int m) { return xcd_split((n + 63) / 64, (m + 63) / 64); }
-__host__ inline dim3 gemm_grid(int n, int m) {
-  const XcdRegions reg = xcd_regions(n, m);
+__host__ __device__ inline XcdRegions xcd_regions(int n, int m, bool rows_first = false) {
+  return xcd_split((n + 63) / 64, (m + 63) / 64, rows_first);
+}
+__host__ inline dim3 gemm_grid(int n, int m, bool rows_first = false) {
+  const XcdRegions reg = xcd_regions(n, m, rows_first);
   return dim3(kXcds * reg.rows * reg.cols);
 }
 
@@ -253,7 +260,7 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   __builtin_amdgcn_s_setprio(1);
   // XCD-aware order: workgroup b runs on XCD b % 8, which takes one region
   // of the tile grid (column-group major inside it).
-  const XcdRegions reg = xcd_regions(n, m);
+  const XcdRegions reg = xcd_regions(n, m, !GEGLU);
   const int x = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
   const int r0 = (x / reg.cparts) * reg.rows, c0 = (x % reg.cparts) * reg.cols;
   const int rows_here = min(reg.rows, (n + 63) / 64 - r0), cols_here = min(reg.cols, (m + 63) / 64 - c0);
@@ -369,7 +376,7 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st) {
   if (n <= 0 || m <= 0 || k <= 0 || k % kQK != 0 || ldy < m || ldx < n || ldw < m) return hipErrorInvalidValue;
-  const dim3 grid = gemm_grid(n, m);
+  const dim3 grid = gemm_grid(n, m, true);
   const int nb = k / kQK;
   if (nb % kStages == 0)
     hipLaunchKernelGGL((gemm_q8_kernel<false, false>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,

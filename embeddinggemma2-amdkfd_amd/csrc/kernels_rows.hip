@@ -249,7 +249,11 @@ residual_norm_quant_kernel(float* __restrict__ x, const float* __restrict__ h, c
   // whose throughput-bound work fills the gaps it leaves.
   __builtin_amdgcn_s_setprio(3);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * kRowsPerGroup + w;
+  // XCD-aware order (a grid that is a multiple of 8): XCD b % 8 takes the
+  // contiguous eighth of the row groups, the rows the O and down GEMMs
+  // computed on it (their tile grid splits into 8 row parts).
+  const int grp = gridDim.x % 8 == 0 ? (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8) : (int)blockIdx.x;
+  const int t = grp * kRowsPerGroup + w;
   const bool live = t < rows;
   if (threadIdx.x < kEmbd / 4) {
     wl[0][threadIdx.x] = reinterpret_cast<const float4*>(post_w)[threadIdx.x];
