@@ -30,7 +30,9 @@
 // pair of a sequence starting at lo is numbered 3 (t - lo) + h.
 //
 // The kernels:
-//  - attention_scores_kernel: work items of (sequence, 32 keys, 32 pairs).
+//  - attention_scores_kernel: work items of (sequence, 32 pairs, 32 keys),
+//    listed pair block by pair block (an XCD's contiguous share of a long
+//    sequence then needs a band of q rows and the k rows, which fit its L2).
 //    The workgroup stages the q rows of its pairs and the k rows of its
 //    keys in LDS, 128 dimensions at a time, reordered so that chain c's
 //    values (dimensions c, c + 4, ...) are contiguous. Each wave owns 16
@@ -674,8 +676,8 @@ bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCo
   size_t ns = 0, nc = need.score_items, sbase = inv_floats(batch ? offsets[batch] : 0);
   for (size_t s = 0; s < batch; ++s) {
     const size_t lo = offsets[s], hi = offsets[s + 1], len = hi - lo, pairs = 3 * len;
-    for (size_t k0 = lo; k0 < hi; k0 += kSKeys)
-      for (size_t p0 = 0; p0 < pairs; p0 += kSPairs) {
+    for (size_t p0 = 0; p0 < pairs; p0 += kSPairs)
+      for (size_t k0 = lo; k0 < hi; k0 += kSKeys) {
         uint32_t* it = items + 8 * ns++;
         it[0] = (uint32_t)lo;
         it[1] = (uint32_t)hi;
@@ -859,8 +861,8 @@ attention_plan_kernel(const uint32_t* __restrict__ offsets, int batch, int rows,
   for (uint32_t i = tid; i < total_sitems; i += kPlanThreads) {
     const int s = last_le(first_sitem, batch, i);  // a sequence with items has first_sitem[s] < first_sitem[s + 1]
     const uint32_t lo = bound[s], hi = bound[s + 1], pairs = 3 * (hi - lo);
-    const uint32_t np = (pairs + kSPairs - 1) / kSPairs, local = i - first_sitem[s];
-    const uint32_t k0 = lo + kSKeys * (local / np), p0 = kSPairs * (local % np);
+    const uint32_t nk = (hi - lo + kSKeys - 1) / kSKeys, local = i - first_sitem[s];
+    const uint32_t p0 = kSPairs * (local / nk), k0 = lo + kSKeys * (local % nk);
     items[2 * i] = make_uint4(lo, hi, k0, p0);
     items[2 * i + 1] = make_uint4(min(pairs, p0 + kSPairs), first_score[s], 0u, 0u);
   }
