@@ -359,6 +359,37 @@ def test_gemm_q8_geglu_equals_gemm_then_gelu_quant(eg2, gpu, n):
     assert (d[:, n:] == -3.0).all()
 
 
+def test_gemm_q8_geglu_tied_block_maxima(eg2, gpu):
+    """Blocks whose largest GeGLU value occurs more than once (repeated
+    weight rows): the first candidate of each block is evaluated in the
+    workgroup's shared pass, the others in the per-wave passes. Block 0 has
+    32 equal rows (every value a candidate, in all four lanes), block 1
+    equal pairs (extra candidates in the owner lane), block 2 rows repeated
+    16 apart (an extra candidate in another lane); the rest are random. Bit
+    for bit the oracle's and the two-kernel path's."""
+    import torch
+
+    k, ff, n = N_EMBD, N_FF, 96
+    wg = (RNG.standard_normal((ff, k)) * 0.02).astype(np.float32)
+    wu = (RNG.standard_normal((ff, k)) * 0.02).astype(np.float32)
+    for w in (wg, wu):
+        w[1:32] = w[0]
+        w[33:64:2] = w[32:64:2]
+        w[80:96] = w[64:80]
+    wg, wu = quantize_q8_0(wg), quantize_q8_0(wu)
+    xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
+    q, d = run_geglu(eg2, gpu, xb, wg, wu, k, ff, n)
+    wq, wd = oracle_gelu_q8(OL.gemm_q8_0(wg, xb), OL.gemm_q8_0(wu, xb))
+    assert np.array_equal(q, wq)
+    assert np.array_equal(bits(d.T), bits(wd))
+    y = empty((n, 2 * ff), torch.float32, gpu)
+    eg2.ops.gemm_q8(*device_q8(eg2, xb, k, gpu), *device_weights(eg2, np.concatenate([wg, wu]), k, gpu), y)
+    rq, rd = qbuf(eg2, n, ff, gpu), empty((ff // 32, n), torch.float32, gpu)
+    eg2.ops.gelu_quant(y, rq, rd)
+    assert np.array_equal(q, qvals(eg2, rq, n, ff))
+    assert np.array_equal(bits(d), bits(host(rd)))
+
+
 @pytest.mark.parametrize("n,ff,k", [(64, 32, 32), (100, 96, 160), (65, 1152, 768)])
 def test_gemm_q8_geglu_against_oracle(eg2, gpu, n, ff, k):
     """Other widths (k = 160: a block count that is not a multiple of the
