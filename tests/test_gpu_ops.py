@@ -121,6 +121,38 @@ def test_residual_norm_quant_bit_exact(eg2, gpu, with_next, rows):
         assert np.array_equal(host(xd).T, wd)
 
 
+def test_residual_norm_quant_zero_and_subnormal_blocks(eg2, gpu):
+    """The next norm's weight zero over block 0 and subnormal over block 1 of
+    every row: an all-zero block (1/d = 0, every value quantizes to 0) and a
+    block whose 1/d overflows (every value -128, as the reference's
+    conversion gives), each from the lane that computes its group's scale and
+    broadcast to the group; the other blocks as usual. Bit for bit the
+    oracle's."""
+    import torch
+
+    rows = 48
+    x = (RNG.standard_normal((rows, N_EMBD)) * 5).astype(np.float32)
+    h = (RNG.standard_normal((rows, N_EMBD)) * 0.7).astype(np.float32)
+    pw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
+    nw = (1 + 0.1 * RNG.standard_normal(N_EMBD)).astype(np.float32)
+    nw[:32] = 0.0
+    nw[32:64] = np.float32(1e-41)
+    xg = dev(x, gpu)
+    xq, xd = qbuf(eg2, rows, N_EMBD, gpu), empty((24, rows), torch.float32, gpu)
+    eg2.ops.residual_norm_quant(xg, dev(h, gpu), dev(pw, gpu), dev(nw, gpu), 1e-6, xq, xd)
+    o = oracle()
+    want = x.copy()
+    blocks = np.zeros((rows, 24), dtype=Q8)
+    for t in range(rows):
+        o.or_rms_norm_residual_inplace(fptr(want[t]), fptr(h[t]), fptr(pw), N_EMBD, 1e-6)
+        o.or_rms_norm_quantize_q8_0(fptr(want[t]), fptr(nw), N_EMBD, 1e-6, vptr(blocks[t]))
+    wq, wd = split(blocks, N_EMBD)
+    assert (wq[:, :32] == 0).all() and (wq[:, 32:64] == -128).all()  # the two cases do occur
+    assert np.array_equal(host(xg), want)
+    assert np.array_equal(qvals(eg2, xq, rows, N_EMBD), wq)
+    assert np.array_equal(bits(host(xd).T), bits(wd))
+
+
 def oracle_qk_norm_rope(qkv, qw, kw, pos, base):
     q, k = qkv[:, :N_EMBD].copy(), qkv[:, N_EMBD:N_EMBD + HEAD_DIM].copy()
     o = oracle()
