@@ -60,7 +60,7 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
 
 // The plan of launch_attention for the sequences [offsets[s], offsets[s+1])
 // (rows = offsets[batch]): a sequence of n tokens has ceil(n/32) key
-// blocks times ceil(3n/32) pair blocks of score items, ceil(3n/64)
+// blocks times ceil(3n/32) pair blocks of score items, ceil(3n/32)
 // context items and 3 n ceil4(n) score floats, after the 1/sum area of
 // ceil4(3 rows). attention_counts gives the counts of a packing
 // (items = both kinds); build_attention_plan writes the lists when they

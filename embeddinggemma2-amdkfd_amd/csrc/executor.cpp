@@ -44,10 +44,10 @@ namespace {
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
 constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
 // The attention's softmax takes one of two equivalent kernel forms by the
-// wave's longest sequence (up to 512 tokens: one kernel); a graph is kept
-// per padded row count and form.
+// wave's longest sequence (up to 512 tokens: 16 pairs per workgroup, else
+// 8); a graph is kept per padded row count and form.
 constexpr unsigned kShortSoftmaxLen = 512;
-inline unsigned attention_form(unsigned longest) { return longest <= kShortSoftmaxLen ? kShortSoftmaxLen : 0; }
+inline unsigned attention_form(unsigned longest) { return longest <= kShortSoftmaxLen ? kShortSoftmaxLen : kCap; }
 inline unsigned graph_key(unsigned rows, unsigned longest) { return 2 * rows + (longest <= kShortSoftmaxLen ? 1 : 0); }
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;

@@ -49,9 +49,12 @@
 //    row in key order (a serial chain, so 16 pairs share a wave's
 //    instructions), 1/sum into the scratch's head.
 //  - attention_softmax_kernel: the two above in one, for waves whose
-//    sequences are at most kShortSoftmax tokens: a workgroup of 16 waves
-//    (pairs) keeps their p rows in LDS, and lanes 0-15 of its first wave
-//    add them, one pair each, which saves a launch.
+//    sequences are at most kLongSoftmax tokens: a workgroup of 16 waves
+//    (pairs; rows up to 512 keys) or 8 waves (up to 2048 keys, 66 KB of
+//    LDS, two workgroups per CU) keeps their p rows in LDS, and the first
+//    lanes of its first wave add them, one pair each: one read of the
+//    scores instead of the three of the two kernels, and the serial sums
+//    read the LDS instead of global memory.
 //  - attention_context_kernel: work items of (sequence, 32 pairs), each
 //    taken by 4 workgroups of 64 dimensions (768 workgroups for a wave of
 //    16 x 128 tokens or for one 2048-token sequence: three per CU). Per
@@ -86,7 +89,7 @@ constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apar
 constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
-constexpr int kShortSoftmax = 512;        // longest sequence for the one-kernel softmax
+constexpr int kShortSoftmax = 512;        // longest sequence for the 16-pair one-kernel softmax
 constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
 
 // Work items of any packing of `tokens` rows into at most `batch`
@@ -123,6 +126,16 @@ struct Stage16 {
 __device__ __forceinline__ Stage16 load16(const float* __restrict__ src) {
   return {*reinterpret_cast<const float4*>(src), *reinterpret_cast<const float4*>(src + 4),
           *reinterpret_cast<const float4*>(src + 8), *reinterpret_cast<const float4*>(src + 12)};
+}
+// An empty asm statement that takes and returns the 16 values: code after
+// it cannot use them before it, so a load's wait lands there.
+__device__ __forceinline__ void hold(Stage16& v) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 a = __builtin_bit_cast(f4, v.a), b = __builtin_bit_cast(f4, v.b), c = __builtin_bit_cast(f4, v.c),
+     d = __builtin_bit_cast(f4, v.d);
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  v = {__builtin_bit_cast(float4, a), __builtin_bit_cast(float4, b), __builtin_bit_cast(float4, c),
+       __builtin_bit_cast(float4, d)};
 }
 __device__ __forceinline__ void store16(const Stage16& v, float* row, int grp) {
   *reinterpret_cast<float4*>(row + 0 * 32 + 4 * grp) = make_float4(v.a.x, v.b.x, v.c.x, v.d.x);
@@ -283,6 +296,13 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
         }
       }
       scores_half(qs + (pr + r16) * kSPitch + 32 * g, ks + (kr + r16) * kSPitch + 32 * g, acc);
+      // The prefetched values are used (transposed into the staging order)
+      // only from here on: without this, the compiler builds the staging
+      // registers right after the loads, which waits for them before the
+      // half above computes.
+      __builtin_amdgcn_sched_barrier(0);
+      hold(qn);
+      hold(kn);
     }
     store_scores(acc, t.lo, t.hi, t.key0, t.pair0, t.pair1, t.sbase, window, pr, kr, g, r16, scores);
     item = nitem;
@@ -300,23 +320,27 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// The softmax in one kernel, for waves whose sequences are short: one wave
-// per (token, head) pair takes the row maximum, then every lane's
-// p = expf(score - m) for its keys, written back over the scores and into
-// the pair's LDS row; then lane i of the first wave adds pair i's p values
-// in key order (a serial chain: 16 pairs share each add instruction) and
-// writes 1/sum into the scratch's head. The same operations in the same
-// order as attention_exp_kernel followed by attention_sum_kernel, which
-// long rows take instead (their rows would not fit the LDS).
-constexpr int kSmWaves = 16;  // pairs (waves) per workgroup
-constexpr int kSmPitch = kShortSoftmax + 4;
+// The softmax in one kernel: one wave per (token, head) pair takes the row
+// maximum, then every lane's p = expf(score - m) for its keys, written back
+// over the scores and, for a row of at most ROW keys, into the pair's LDS
+// row; then lane i of the first wave adds pair i's p values in key order (a
+// serial chain: the workgroup's pairs share each add instruction), reading
+// the LDS row 32 keys at a time with the next 32 in flight, and writes 1/sum
+// into the scratch's head. A longer row (a packing longer than the caller's
+// `longest`) is summed from the scores in global memory instead: slower,
+// same bits. The same operations in the same order as attention_exp_kernel
+// followed by attention_sum_kernel, which packings with sequences over
+// kLongSoftmax tokens take instead.
+constexpr int kLongSoftmax = kCtx;  // longest row of the LDS softmax's long form
 
-__global__ void __launch_bounds__(64 * kSmWaves)
+template <int ROW, int PAIRS>
+__global__ void __launch_bounds__(64 * PAIRS)
 attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
   __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
-  __shared__ __align__(16) float prow[kSmWaves][kSmPitch];  // each pair's p values from its first key
-  __shared__ uint32_t plen[kSmWaves];                        // and their count (0: no such pair)
+  __shared__ __align__(16) float prow[PAIRS][ROW + 4];  // each pair's p values from its first key (4 banks apart)
+  __shared__ uint32_t plen[PAIRS];                      // and their count (0: no such pair)
+  __shared__ uint32_t pbase[PAIRS];                     // index in scores of the row's first key
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
   __syncthreads();
@@ -326,50 +350,131 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   const uint32_t blk = gridDim.x % kXcdCount == 0
                            ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
                            : blockIdx.x;
-  const uint32_t pair = kSmWaves * blk + w, t = pair / 3, h = pair % 3;
-  uint32_t n = 0;
+  const uint32_t pair = PAIRS * blk + w, t = pair / 3, h = pair % 3;
+  uint32_t n = 0, base = 0;
   if (t < (uint32_t)rows) {
     const uint4 meta = tok[t];
     const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
-    // a malformed entry (t outside its sequence, or a row longer than the
-    // LDS row): nothing is written for this token
-    if (t >= lo && t < hi && hi - lo <= (uint32_t)kShortSoftmax) {
+    if (t >= lo && t < hi) {  // else a malformed entry: nothing is written for this token
       uint32_t first, last;
       key_range(t, lo, hi, window, first, last);
       float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
-      float m = -__builtin_inff();
-      uint32_t kt = first + lane;
-      for (; kt + 192 < last; kt += 256) {
-        const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
-        m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
-      }
-      for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
-      m = wave_max(m);
-      for (uint32_t k = first + lane; k < last; k += 64) {
-        const float p = libm::expf_tab(srow[k - lo] - m, tab);
-        srow[k - lo] = p;
-        prow[w][k - first] = p;
-      }
       n = last - first;
+      base = meta.z + (3 * (t - lo) + h) * score_pitch(hi - lo) + (first - lo);
+      if (ROW > kShortSoftmax && n <= (uint32_t)ROW) {
+        // The row in registers (key first + lane + 64 i in v[i]): one read,
+        // every load in flight at once.
+        constexpr int kPer = ROW / 64;
+        float v[kPer];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const uint32_t k = first + lane + 64 * i;
+          v[i] = k < last ? srow[k - lo] : -__builtin_inff();
+          m = fmaxf(m, v[i]);
+        }
+        m = wave_max(m);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const uint32_t k = first + lane + 64 * i;
+          const float p = libm::expf_tab(v[i] - m, tab);  // computed for every slot: no branch per key
+          if (k < last) {
+            srow[k - lo] = p;
+            prow[w][k - first] = p;
+          }
+        }
+      } else {
+        // Short rows (and rows too long for the LDS): the maximum, then the
+        // exps, each a pass over the row (the second from the L2).
+        float m = -__builtin_inff();
+        uint32_t kt = first + lane;
+        for (; kt + 192 < last; kt += 256) {
+          const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
+          m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+        }
+        for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
+        m = wave_max(m);
+        const bool to_lds = n <= (uint32_t)ROW;
+        for (uint32_t k = first + lane; k < last; k += 64) {
+          const float p = libm::expf_tab(srow[k - lo] - m, tab);
+          srow[k - lo] = p;
+          if (to_lds) prow[w][k - first] = p;
+        }
+      }
     }
   }
-  if (lane == 0) plen[w] = n;
+  if (lane == 0) {
+    plen[w] = n;
+    pbase[w] = base;
+  }
   __syncthreads();
-  if (w == 0 && lane < kSmWaves) {
+  if (w == 0 && lane < PAIRS) {
     const uint32_t cnt = plen[lane];
-    const uint32_t own = kSmWaves * blk + lane;
+    const uint32_t own = PAIRS * blk + lane;
     if (cnt > 0) {
-      const float* pr = prow[lane];
       float sum = 0.0f;
-      uint32_t j = 0;
-      for (; j + 4 <= cnt; j += 4) {
-        const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
-        sum = sum + p4.x;
-        sum = sum + p4.y;
-        sum = sum + p4.z;
-        sum = sum + p4.w;
+      if (cnt <= (uint32_t)ROW) {
+        const float* pr = prow[lane];
+        constexpr uint32_t kB = 8;  // float4 per batch
+        uint32_t j = 0;
+        // Short rows: one 16-byte read at a time (22 VGPRs, not 68: the
+        // kernel shares its CUs with other lanes' work).
+        if (ROW > kShortSoftmax) {
+          // Batches of 32 keys in two register sets: a set is reloaded
+          // right after it is added, and added again only after the other
+          // set's 32 adds, which cover the read's latency.
+          const uint32_t nb = cnt / (4 * kB);
+          const float4* p4 = reinterpret_cast<const float4*>(pr);
+          float4 a[kB], b[kB];
+          auto load = [&](float4 (&x)[kB], uint32_t batch) {
+#pragma unroll
+            for (uint32_t i = 0; i < kB; ++i) x[i] = p4[kB * batch + i];
+          };
+          auto add = [&](const float4 (&x)[kB]) {
+#pragma unroll
+            for (uint32_t i = 0; i < kB; ++i) {
+              sum = sum + x[i].x;
+              sum = sum + x[i].y;
+              sum = sum + x[i].z;
+              sum = sum + x[i].w;
+            }
+          };
+          if (nb > 0) {
+            // Reads past the last batch are clamped to it (read again, not
+            // added), so every load is unconditional.
+            const uint32_t last_b = nb - 1;
+            load(a, 0);
+            load(b, min(1u, last_b));
+            for (uint32_t bt = 0; bt + 2 <= nb; bt += 2) {
+              // scheduling barriers keep each reload ahead of the other
+              // set's adds (the scheduler would sink it to its use)
+              add(a);
+              __builtin_amdgcn_sched_barrier(0);
+              load(a, min(bt + 2, last_b));
+              __builtin_amdgcn_sched_barrier(0);
+              add(b);
+              __builtin_amdgcn_sched_barrier(0);
+              load(b, min(bt + 3, last_b));
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            if (nb & 1) add(a);
+          }
+          j = 4 * kB * nb;
+        }
+#pragma unroll 2
+        for (; j + 4 <= cnt; j += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
+          sum = sum + p4.x;
+          sum = sum + p4.y;
+          sum = sum + p4.z;
+          sum = sum + p4.w;
+        }
+        for (; j < cnt; ++j) sum = sum + pr[j];
+      } else {
+        const float* pr = scores + pbase[lane];
+#pragma unroll 1
+        for (uint32_t j = 0; j < cnt; ++j) sum = sum + pr[j];
       }
-      for (; j < cnt; ++j) sum = sum + pr[j];
       scores[3 * (size_t)(own / 3) + own % 3] = 1.0f / sum;
     }
   }
@@ -673,6 +778,9 @@ bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCo
   const AttentionCounts need = attention_counts(offsets, batch);
   if (used) *used = need;
   if (need.items > cap.items || need.score_floats > cap.score_floats) return false;
+  // The records hold 32-bit score indices and counts: a packing whose
+  // scores or items exceed them (sequences of some 37k tokens) is refused.
+  if (need.score_floats > 0xFFFFFFFFull || need.items > 0xFFFFFFFFull) return false;
   size_t ns = 0, nc = need.score_items, sbase = inv_floats(batch ? offsets[batch] : 0);
   for (size_t s = 0; s < batch; ++s) {
     const size_t lo = offsets[s], hi = offsets[s + 1], len = hi - lo, pairs = 3 * len;
@@ -726,8 +834,13 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (longest > 0 && longest <= kShortSoftmax) {
-    hipLaunchKernelGGL(attention_softmax_kernel, dim3((3 * rows + kSmWaves - 1) / kSmWaves), dim3(64 * kSmWaves), 0,
-                       st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+    constexpr int kPairs = 16;
+    hipLaunchKernelGGL((attention_softmax_kernel<kShortSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
+                       dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+  } else if (longest > 0 && longest <= kLongSoftmax) {
+    constexpr int kPairs = 8;  // 66 KB of p rows: two workgroups per CU
+    hipLaunchKernelGGL((attention_softmax_kernel<kLongSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
+                       dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
   } else {
     hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
                        reinterpret_cast<const uint4*>(tok), window, rows);

@@ -72,9 +72,10 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * of the `rows` rows, so every row must belong to a planned sequence, e.g.
  * a padding one. scores: scratch of at least the plan's score floats
  * (counts[1]). rows % 4 == 0. longest: the longest sequence of the
- * packing (it picks one of two equivalent softmax kernel forms; 0 = not
- * known, valid for any packing). A sequence's result does not depend on
- * its place in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
+ * packing, a hint (at most rows) that picks one of three equivalent
+ * softmax kernel forms (<= 512, <= 2048, 0 = not known); a wrong hint
+ * costs time, never bits. A sequence's result does not depend on its place
+ * in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
                       const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores, int8_t *cq,
                       float *cd, void *stream);
@@ -101,7 +102,7 @@ int eg2_hip_attention_static(const float *qkv, const uint32_t *offsets, unsigned
 /* Host: the plan of eg2_hip_attention for the sequences [offsets[s],
  * offsets[s+1]) (rows = offsets[batch]): the score items of every
  * sequence (per sequence of n tokens, ceil(n/32) key blocks x ceil(3n/32)
- * pair blocks), then its context items (ceil(3n/64) pair blocks), 8
+ * pair blocks), then its context items (ceil(3n/32) pair blocks), 8
  * uint32 each as eg2_hip_attention reads them, and one token record per
  * token (4 uint32: sequence start, end, first score index, 0) at tok[4 t].
  * counts[0] = items of both kinds, counts[1] = score floats (ceil4(3 rows)

@@ -600,18 +600,23 @@ def test_attention_independent_of_packing(eg2, gpu, window):
 
 
 @pytest.mark.parametrize("window", [0, 64])
-def test_attention_softmax_forms_agree(eg2, gpu, window):
-    """The one-kernel softmax (waves of sequences up to 512 tokens) and the
-    exp + serial-sum pair (any length) give the same bits."""
-    rng = np.random.default_rng(10)
-    lens = [1, 130, 512, 7, 300]
+@pytest.mark.parametrize("lens", [[1, 130, 512, 7, 300], [1, 513, 2, 1200, 37]])
+def test_attention_softmax_forms_agree(eg2, gpu, window, lens):
+    """The one-kernel softmax (16 pairs per workgroup for waves of sequences
+    up to 512 tokens, 8 pairs with rows up to 2048 keys in LDS otherwise)
+    and the exp + serial-sum pair (any length) give the same bits, and so
+    does a `longest` below the wave's real longest sequence (rows too long
+    for the chosen form's LDS are summed from global memory): the hint picks
+    a kernel form, never the results."""
+    rng = np.random.default_rng(10 + len(lens))
     T = sum(lens)
     offsets = np.concatenate([[0], np.cumsum(lens)])
     q, k, v = qkv_inputs(rng, T)
-    short = run_attention(eg2, gpu, q, k, v, offsets, window)
-    split = run_attention(eg2, gpu, q, k, v, offsets, window, longest=0)
-    assert np.array_equal(short[0], split[0]) and np.array_equal(bits(short[1]), bits(split[1]))
-    assert_attention_bit_exact(*short, oracle_attention(q, k, v, offsets, window))
+    ref = run_attention(eg2, gpu, q, k, v, offsets, window)
+    for longest in (h for h in (0, 1, 512, 513, 2048) if h <= T):
+        got = run_attention(eg2, gpu, q, k, v, offsets, window, longest=longest)
+        assert np.array_equal(ref[0], got[0]) and np.array_equal(bits(ref[1]), bits(got[1])), longest
+    assert_attention_bit_exact(*ref, oracle_attention(q, k, v, offsets, window))
 
 
 @pytest.mark.parametrize("lens", [[128] * 8 + [60, 4], [700, 5, 300, 39]])

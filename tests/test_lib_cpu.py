@@ -152,6 +152,22 @@ def test_attention_plan_checks_capacity_before_writing(eg2):
         assert (items == 7).all() and (tok == 7).all()
 
 
+def test_attention_plan_refuses_scores_past_32_bits(eg2):
+    """The plan's records hold 32-bit score indices: a packing whose score
+    floats pass 2^32 (one sequence of 40,000 tokens: 3 n ceil4(n) = 4.8e9)
+    is refused even with room to spare, with nothing written."""
+    import ctypes as C
+
+    n = 40000
+    arr = (C.c_size_t * 2)(0, n)
+    items = np.full((8, 8), 7, np.uint32)
+    tok = np.full((8, 4), 7, np.uint32)
+    counts = (C.c_size_t * 3)()
+    rc = eg2.lib().eg2_attention_plan(arr, 1, 1 << 40, 1 << 40, items.ctypes.data, tok.ctypes.data, counts)
+    assert rc == -1 and counts[1] == 3 * n + 3 * n * n and counts[1] > 2 ** 32
+    assert (items == 7).all() and (tok == 7).all()
+
+
 def test_attention_capacity_bounds_every_packing(eg2):
     """The executor sizes its plan with eg2_attention_capacity(2080, 2049)
     (a 2048-token wave plus a padding sequence of up to 31 rows): no packing
