@@ -53,6 +53,12 @@ constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDe
 constexpr int kVocab = 262144;
 constexpr double kTimeoutSeconds = 30.0;  // src/gemma2_kfd.cpp:21
 
+std::string fixed3(double v) {
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%.3f", v);
+  return buf;
+}
+
 void check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -221,6 +227,11 @@ struct Lane {
   std::map<unsigned, hipGraphExec_t> graphs;  // key: graph_key(padded rows, longest sequence)
   unsigned staged_tokens = 0, staged_rows = 0, staged_longest = 0;
   size_t staged_batch = 0;
+  // EG2_HIP_PROFILE (only then non-empty): a pool of events, one recorded
+  // before the first launch of an eager forward and one after every
+  // launch, the launch names, and the per-name sums in ms.
+  std::vector<hipEvent_t> prof_events;
+  std::vector<const char*> prof_names;
   std::map<std::string, double> timings;
 };
 
@@ -324,9 +335,12 @@ class Backend {
   DevMat upload_q8(const std::vector<const std::vector<uint8_t>*>& parts, int k);
   DevMat upload_q8_geglu(const std::vector<uint8_t>& gate, const std::vector<uint8_t>& up, int k);
   void alloc_lane(Lane& L);
-  void launch(const char* name, hipError_t e);
+  // Checks a launch's status; while the lane is profiled, also records an
+  // event after it on the lane's stream under `name`.
+  void launch(Lane& L, const char* name, hipError_t e);
   void record_layers(Lane& L, unsigned rows, unsigned longest);
-  void gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
+  void record_head(Lane& L, int batch);
+  void gemm(Lane& L, const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
             hipStream_t s);
   void wait(Lane& L, const char* what);
   // Runs device work; any exception it throws marks the context failed.
@@ -529,6 +543,7 @@ void Backend::alloc_lane(Lane& L) {
 Backend::~Backend() {
   for (auto& L : lanes_) {
     if (L->stream) (void)hipStreamSynchronize(L->stream);
+    for (hipEvent_t ev : L->prof_events) (void)hipEventDestroy(ev);
     for (auto& kvp : L->graphs) (void)hipGraphExecDestroy(kvp.second);
     if (L->stream) (void)hipStreamDestroy(L->stream);
   }
@@ -536,15 +551,20 @@ Backend::~Backend() {
   for (void* p : host_allocs_) (void)hipHostFree(p);
 }
 
-void Backend::launch(const char* name, hipError_t e) {
+void Backend::launch(Lane& ln, const char* name, hipError_t e) {
   if (e != hipSuccess) throw std::runtime_error(std::string(name) + ": " + hipGetErrorString(e));
+  if (ln.prof_events.empty()) return;  // not profiled
+  const size_t i = ln.prof_names.size();
+  if (i + 1 >= ln.prof_events.size()) throw std::runtime_error("profile event pool exhausted");
+  check(hipEventRecord(ln.prof_events[i + 1], ln.stream), "hipEventRecord");
+  ln.prof_names.push_back(name);
 }
 
 // y[n][w.m] (row stride ldy) = activations (row tiles xq, scales xd
 // [k/32][n]) times the weights w.
-void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n, int ldy,
-                   hipStream_t s) {
-  launch(name, eg2::launch_gemm_q8(xq, xd, n, w.q, w.d, w.ld, y, n, w.m, w.k, ldy, s));
+void Backend::gemm(Lane& ln, const char* name, const int8_t* xq, const float* xd, const DevMat& w, float* y, int n,
+                   int ldy, hipStream_t s) {
+  launch(ln, name, eg2::launch_gemm_q8(xq, xd, n, w.q, w.d, w.ld, y, n, w.m, w.k, ldy, s));
 }
 
 // The per-wave layer stack for `rows` (padded) token rows: embedding + norm,
@@ -556,28 +576,56 @@ void Backend::gemm(const char* name, const int8_t* xq, const float* xd, const De
 void Backend::record_layers(Lane& ln, unsigned rows, unsigned longest) {
   hipStream_t s = ln.stream;
   const int n = (int)rows;
-  launch("embed", eg2::launch_embed_norm_quant(token_embd_, ln.ids_d, n, std::sqrt((float)kEmbd),
-                                               layers_[0].attn_norm, eps_, ln.x, ln.xq, ln.xd, s));
+  launch(ln, "embed", eg2::launch_embed_norm_quant(token_embd_, ln.ids_d, n, std::sqrt((float)kEmbd),
+                                                   layers_[0].attn_norm, eps_, ln.x, ln.xq, ln.xd, s));
   for (size_t il = 0; il < layers_.size(); ++il) {
     const Layer& L = layers_[il];
     // Q|K|V projection with QK-norm / RoPE in its epilogue: the attention
     // operand rows, no unnormalised projection in HBM.
-    launch("gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
-                                                         L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
-    launch("attention", eg2::launch_attention(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid, ln.tok_d, L.window, n,
-                                              (int)longest, ln.scores, ln.cq, ln.cd, s));
-    gemm("gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
+    launch(ln, "gemm_qkv_rope", eg2::launch_gemm_q8_qkv_rope(ln.xq, ln.xd, n, L.qkv.q, L.qkv.d, L.qkv.ld, n, kEmbd,
+                                                             L.q_norm, L.k_norm, L.rope, ln.pos_d, eps_, ln.qkv, s));
+    launch(ln, "attention_scores", eg2::launch_attention_scores(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid,
+                                                                L.window, n, ln.scores, s));
+    launch(ln, "attention_softmax", eg2::launch_attention_softmax(ln.tok_d, L.window, n, (int)longest, ln.scores, s));
+    launch(ln, "attention_context", eg2::launch_attention_context(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid,
+                                                                  L.window, n, (int)longest, ln.scores, ln.cq, ln.cd,
+                                                                  s));
+    gemm(ln, "gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
     // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.
-    launch("residual",
+    launch(ln, "residual",
            eg2::launch_residual_norm_quant(ln.x, ln.h, L.post_attn, L.ffn_norm, eps_, ln.cq, ln.cd, n, s));
-    launch("gemm_gate_up_geglu", eg2::launch_gemm_q8_geglu(ln.cq, ln.cd, n, L.gu.q, L.gu.d, L.gu.ld, ln.xq, ln.xd, n,
-                                                            n, kFF, kEmbd, s));
-    gemm("gemm_down", ln.xq, ln.xd, L.down, ln.h, n, kEmbd, s);
+    launch(ln, "gemm_gate_up_geglu", eg2::launch_gemm_q8_geglu(ln.cq, ln.cd, n, L.gu.q, L.gu.d, L.gu.ld, ln.xq,
+                                                                ln.xd, n, n, kFF, kEmbd, s));
+    gemm(ln, "gemm_down", ln.xq, ln.xd, L.down, ln.h, n, kEmbd, s);
     const float* next = il + 1 < layers_.size() ? layers_[il + 1].attn_norm : nullptr;
-    launch("residual", eg2::launch_residual_norm_quant(ln.x, ln.h, L.post_ffw, next, eps_, ln.xq, ln.xd, n, s));
+    launch(ln, "residual", eg2::launch_residual_norm_quant(ln.x, ln.h, L.post_ffw, next, eps_, ln.xq, ln.xd, n, s));
   }
-  launch("output_norm", eg2::launch_rms_norm_rows(ln.x, output_norm_, eps_, n, s));
+  launch(ln, "output_norm", eg2::launch_rms_norm_rows(ln.x, output_norm_, eps_, n, s));
+}
+
+// kernels.c:417-427 (mean + L2 per sequence) and the dense head.
+void Backend::record_head(Lane& ln, int B) {
+  hipStream_t s = ln.stream;
+  if (dense_) {
+    // EXTRACTION.md:178-181: dense_2 then dense_3 on the mean pool
+    // (kernels.c:417-425 without its L2), each input Q8_0-quantized,
+    // then the L2 of kernels.c:393-396.
+    launch(ln, "pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
+    launch(ln, "dense_quant", eg2::launch_quantize_rows(ln.pooled, kEmbd, ln.cq, ln.cd, B, s));
+    gemm(ln, "dense_2", ln.cq, ln.cd, dense2_, ln.mid, B, kDenseFF, s);
+    launch(ln, "dense_quant", eg2::launch_quantize_rows(ln.mid, kDenseFF, ln.mid_q, ln.mid_d, B, s));
+    gemm(ln, "dense_3", ln.mid_q, ln.mid_d, dense3_, ln.pooled, B, kEmbd, s);
+    launch(ln, "dense_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+  } else if (ln.staged_longest > kPoolSplitLen) {
+    // One workgroup per sequence reads it through one CU; past 256
+    // tokens the mean spreads over 12 workgroups per sequence and the
+    // L2 follows (the same result, bit for bit).
+    launch(ln, "pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
+    launch(ln, "pool_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
+  } else {
+    launch(ln, "pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
+  }
 }
 
 void Backend::wait(Lane& ln, const char* what) {
@@ -608,8 +656,18 @@ void Backend::batch(const int32_t* ids, const size_t* offsets, size_t batch, flo
   collect(ln, out);
   if (profile_) {
     const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    std::fprintf(stderr, "HIP_PROFILE {\"lane\":%u,\"tokens\":%u,\"batch\":%zu,\"wall_ms\":%.3f,\"layers_ms\":%.3f}\n",
-                 ln.index, ln.staged_tokens, ln.staged_batch, ms, ln.timings["layers"]);
+    // src/gemma2_kfd.cpp:346-352's KFD_PROFILE line: per launch name, the
+    // summed GPU time of its launches (names in sorted order).
+    std::string line = "HIP_PROFILE {\"tokens\":" + std::to_string(ln.staged_tokens) +
+                       ",\"batch\":" + std::to_string(ln.staged_batch) + ",\"wall_ms\":" + fixed3(ms) +
+                       ",\"command_ms\":{";
+    bool first = true;
+    for (const auto& kv : ln.timings) {
+      line += (first ? "\"" : ",\"") + kv.first + "\":" + fixed3(kv.second);
+      first = false;
+    }
+    line += "}}\n";
+    std::fputs(line.c_str(), stderr);
     ln.timings.clear();
   }
 }
@@ -699,44 +757,33 @@ void Backend::launch_staged(Lane& ln, unsigned repeats) {
   const int B = (int)ln.staged_batch;
   device_step([&] {
     for (unsigned r = 0; r < repeats; ++r) {
-      if (use_graph_ && !profile_) {
+      if (profile_) {
+        // Per-kernel timing (the reference's KFD_PROFILE, src/gemma2_kfd.cpp:
+        // 173-186, 216-222): an eager forward with an event after every
+        // launch, each kernel's time (from the previous event to its own)
+        // summed per launch name.
+        if (ln.prof_events.empty()) {
+          ln.prof_events.resize(1024);
+          for (auto& ev : ln.prof_events) check(hipEventCreate(&ev), "hipEventCreate");
+        }
+        ln.prof_names.clear();
+        check(hipEventRecord(ln.prof_events[0], s), "hipEventRecord");
+        record_layers(ln, ln.staged_rows, attention_form(ln.staged_longest));
+        record_head(ln, B);
+        const size_t k = ln.prof_names.size();
+        check(hipEventSynchronize(ln.prof_events[k]), "hipEventSynchronize");
+        for (size_t i = 0; i < k; ++i) {
+          float ms = 0;
+          check(hipEventElapsedTime(&ms, ln.prof_events[i], ln.prof_events[i + 1]), "hipEventElapsedTime");
+          ln.timings[ln.prof_names[i]] += ms;
+        }
+        ln.prof_names.clear();
+      } else if (use_graph_) {
         check(hipGraphLaunch(ln.graphs.at(graph_key(ln.staged_rows, ln.staged_longest)), s), "hipGraphLaunch");
-      } else if (profile_) {
-        // Per-stage timing needs events around eager launches; the totals are
-        // printed like the reference's KFD_PROFILE line (src/gemma2_kfd.cpp:346-352).
-        hipEvent_t a, b;
-        check(hipEventCreate(&a), "hipEventCreate");
-        check(hipEventCreate(&b), "hipEventCreate");
-        check(hipEventRecord(a, s), "hipEventRecord");
-        record_layers(ln, ln.staged_rows, attention_form(ln.staged_longest));
-        check(hipEventRecord(b, s), "hipEventRecord");
-        check(hipEventSynchronize(b), "hipEventSynchronize");
-        float ms = 0;
-        (void)hipEventElapsedTime(&ms, a, b);
-        ln.timings["layers"] += ms;
-        (void)hipEventDestroy(a);
-        (void)hipEventDestroy(b);
+        record_head(ln, B);
       } else {
         record_layers(ln, ln.staged_rows, attention_form(ln.staged_longest));
-      }
-      if (dense_) {
-        // EXTRACTION.md:178-181: dense_2 then dense_3 on the mean pool
-        // (kernels.c:417-425 without its L2), each input Q8_0-quantized,
-        // then the L2 of kernels.c:393-396.
-        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
-        launch("dense_quant", eg2::launch_quantize_rows(ln.pooled, kEmbd, ln.cq, ln.cd, B, s));
-        gemm("dense_2", ln.cq, ln.cd, dense2_, ln.mid, B, kDenseFF, s);
-        launch("dense_quant", eg2::launch_quantize_rows(ln.mid, kDenseFF, ln.mid_q, ln.mid_d, B, s));
-        gemm("dense_3", ln.mid_q, ln.mid_d, dense3_, ln.pooled, B, kEmbd, s);
-        launch("dense_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
-      } else if (ln.staged_longest > kPoolSplitLen) {
-        // One workgroup per sequence reads it through one CU; past 256
-        // tokens the mean spreads over 12 workgroups per sequence and the
-        // L2 follows (the same result, bit for bit).
-        launch("pool", eg2::launch_pool_mean(ln.x, ln.off_d, ln.pooled, B, s));
-        launch("pool_l2", eg2::launch_l2_prefix(ln.pooled, kEmbd, kEmbd, B, s));
-      } else {
-        launch("pool", eg2::launch_pool_l2(ln.x, ln.off_d, ln.pooled, B, s));
+        record_head(ln, B);
       }
     }
   });

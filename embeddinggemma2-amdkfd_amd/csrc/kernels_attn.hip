@@ -825,36 +825,57 @@ AttentionCounts attention_capacity(size_t tokens, size_t batch) {
   return c;
 }
 
-hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
-                            const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
-                            float* cd, hipStream_t st) {
-  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
+hipError_t launch_attention_scores(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
+                                   int window, int rows, float* scores, hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_scores_kernel, dim3(grid), dim3(256), 0, st, qkv,
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, scores);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, int longest, float* scores,
+                                    hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
   if (longest > 0 && longest <= kShortSoftmax) {
     constexpr int kPairs = 16;
     hipLaunchKernelGGL((attention_softmax_kernel<kShortSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
                        dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
-  } else if (longest > 0 && longest <= kLongSoftmax) {
+    return hipGetLastError();
+  }
+  if (longest > 0 && longest <= kLongSoftmax) {
     constexpr int kPairs = 8;  // 66 KB of p rows: two workgroups per CU
     hipLaunchKernelGGL((attention_softmax_kernel<kLongSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
                        dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
-  } else {
-    hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
-                       reinterpret_cast<const uint4*>(tok), window, rows);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_sum_kernel, dim3((3 * rows + 4 * kSumPairsPerWave - 1) / (4 * kSumPairsPerWave)),
-                       dim3(256), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+    return hipGetLastError();
   }
-  e = hipGetLastError();
+  hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
+                     reinterpret_cast<const uint4*>(tok), window, rows);
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attention_sum_kernel, dim3((3 * rows + 4 * kSumPairsPerWave - 1) / (4 * kSumPairsPerWave)),
+                     dim3(256), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_context(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
+                                    int window, int rows, int longest, const float* scores, int8_t* cq, float* cd,
+                                    hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_context_kernel, dim3(grid), dim3(256), 0, st, qkv, scores,
                      reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd,
                      longest > 0 && longest <= kShortSoftmax ? 1 : 0);
   return hipGetLastError();
+}
+
+hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
+                            const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
+                            float* cd, hipStream_t st) {
+  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
+  hipError_t e = launch_attention_scores(qkv, items, item_count, grid, window, rows, scores, st);
+  if (e != hipSuccess) return e;
+  e = launch_attention_softmax(tok, window, rows, longest, scores, st);
+  if (e != hipSuccess) return e;
+  return launch_attention_context(qkv, items, item_count, grid, window, rows, longest, scores, cq, cd, st);
 }
 
 // ---------------------------------------------------------------- allocation-free form

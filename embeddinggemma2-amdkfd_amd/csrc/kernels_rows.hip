@@ -2,7 +2,9 @@
 // fuses the element-wise work between two GEMMs so a token row is read and
 // written once, and each reproduces the reference's operation order, so its
 // results are bit-identical to the CPU path for identical inputs (the GeGLU
-// kernel's GELU, evaluated through exp2 instead of tanhf, is the exception).
+// kernel decides most Q8_0 values from a bounded tanh approximation and
+// evaluates the host libm's tanhf for the rest: the same bits, see
+// geglu_quantize_part4).
 //
 // Work mapping. One 64-lane wave per 768-wide token row (a 2048-token wave
 // gives two waves per SIMD), so latency, not bandwidth, is what the design

@@ -88,6 +88,50 @@ def test_repeatable_and_graph_matches_eager(eg2, small_encoder, small_model):
     assert np.array_equal(a, c)
 
 
+def test_profile_line_times_every_kernel(eg2, small_model, capfd):
+    """EG2_HIP_PROFILE=1 runs the forward eagerly with an event after every
+    launch and prints, per batch call, the reference's KFD_PROFILE line
+    (src/gemma2_kfd.cpp:346-352) as HIP_PROFILE: tokens, batch, wall_ms and
+    command_ms, the summed GPU time of each launch name. The embeddings are
+    the graph run's bit for bit; every kernel of the forward has a positive
+    time; the per-kernel times add up to less than the wall time (which also
+    holds the host staging and copies) and to most of it."""
+    import json
+
+    rng = np.random.default_rng(12)
+    ids = rng.integers(0, OL.VOCAB, 900).astype(np.int32)
+    offsets = [0, 700, 900]  # a wave over 512 tokens: the 2048-key softmax form
+    ref = eg2.Encoder(small_model)
+    want = ref.batch(ids, offsets)
+    ref.close()
+    os.environ["EG2_HIP_PROFILE"] = "1"
+    try:
+        enc = eg2.Encoder(small_model)
+        capfd.readouterr()
+        got = [enc.batch(ids, offsets) for _ in range(2)]
+        enc.close()
+    finally:
+        del os.environ["EG2_HIP_PROFILE"]
+    err = capfd.readouterr().err
+    lines = [l for l in err.splitlines() if l.startswith("HIP_PROFILE ")]
+    assert len(lines) == 2, err[-2000:]
+    for g in got:
+        assert np.array_equal(g, want)
+    kernels = {"embed", "gemm_qkv_rope", "attention_scores", "attention_softmax", "attention_context", "gemm_o",
+               "residual", "gemm_gate_up_geglu", "gemm_down", "output_norm", "pool", "dense_quant", "dense_2",
+               "dense_3", "dense_l2"}
+    for line in lines:
+        rec = json.loads(line[len("HIP_PROFILE "):])
+        assert list(rec) == ["tokens", "batch", "wall_ms", "command_ms"]
+        assert rec["tokens"] == 900 and rec["batch"] == 2
+        ms = rec["command_ms"]
+        assert set(ms) == kernels and list(ms) == sorted(ms)
+        assert all(v > 0 for v in ms.values()), ms
+        total = sum(ms.values())
+        print(f"wall {rec['wall_ms']:.3f} ms, kernels {total:.3f} ms: {ms}")
+        assert 0.3 * rec["wall_ms"] < total <= rec["wall_ms"]
+
+
 def test_invalid_batches_fail_without_poisoning(eg2, small_encoder):
     ids = np.zeros(10, np.int32)
     cases = [([0, 5, 5, 10], "offsets"), ([1, 10], "1..2048"), ([0, 0], "offsets")]

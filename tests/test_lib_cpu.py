@@ -474,3 +474,35 @@ def test_code_object_exports_the_operator_kernels(eg2):
     for i in range(lib.eg2_op_count()):
         name = lib.eg2_op_name(i).decode()
         assert name in syms and name + ".kd" in syms, name
+
+
+def test_gemm_dma_is_the_only_m0_user(tmp_path):
+    """The GEMM kernels set M0 in inline asm for their LDS DMA and declare it
+    clobbered; that is sound only while no compiler-generated instruction
+    in those kernels reads M0. Compiles kernels_gemm.hip for gfx950 with the
+    library's flags and checks that every mention of m0 in the ISA is the
+    asm's own write (a compiler update or a new M0 user fails here)."""
+    import shutil
+    import subprocess
+
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    if not shutil.which(hipcc):
+        pytest.skip("hipcc not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "embeddinggemma2-amdkfd_amd")
+    out = tmp_path / "gemm.s"
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+           "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-mllvm", "-amdgpu-mfma-vgpr-form", "-I" + os.path.join(root, "include"), "-I" + os.path.join(pkg, "csrc"),
+           "--cuda-device-only", "-S", os.path.join(pkg, "csrc", "kernels_gemm.hip"), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    writes = others = 0
+    for line in out.read_text().splitlines():
+        code = line.split(";")[0]
+        if not re.search(r"\bm0\b", code):
+            continue
+        if re.match(r"\s*s_mov_b32 m0, s\d+\s*$", code):
+            writes += 1
+        else:
+            others += 1
+    assert writes > 0 and others == 0, (writes, others)
