@@ -5,8 +5,12 @@
  * ei_kv layout the engine passes to ei_gemma2_kfd_create). The field order,
  * types and scalar normalisation (unsigned -> v.u64, signed -> v.i64,
  * F32/F64 -> v.f64, BOOL -> v.b; gguf.c:46-61) are identical so the engine's
- * own mmapped ei_gguf can be handed to this library unchanged. Inside the
- * engine build its own gguf.h (same include guard) is found first.
+ * own mmapped ei_gguf can be handed to this library unchanged. This header
+ * and the engine's share an include guard: a translation unit uses
+ * whichever it includes first (engine.c includes gemma2_kfd.h, hence this
+ * one, first; model.c and gguf.c use the engine's), and the two layouts
+ * are identical, so records parsed by the engine's gguf.c read correctly
+ * here.
  */
 #ifndef EI_GGUF_H
 #define EI_GGUF_H
