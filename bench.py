@@ -33,28 +33,36 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-# The serving configuration: at least 8 hardware queues per process (the
-# HIP runtime reads this when it initialises, before torch touches the
-# GPU), so each of the executor's four lanes runs on a queue of its own;
-# with the runtime's default of 4 the executor keeps three lanes.
-try:
-    _queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
-except ValueError:
-    _queues = 4
-os.environ["GPU_MAX_HW_QUEUES"] = str(max(_queues, 8))
-
 TOKENS, SEQS, LAYERS = 2048, 16, 24
 GEMM_N, GEMM_M, GEMM_K = 2048, 2 * 1152, 768
 PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA (the projection GEMMs)
-# The VALU: 16 lanes per SIMD, 1024 SIMDs at 2.4 GHz = 39.3 T fp32
-# operations/s without packed fp32 (not used here); a wave64 instruction
-# occupies its SIMD for 4 cycles. Exact attention adds its products (made
-# on fp32 MFMA) one rounded VALU add at a time: its floor is those adds.
-PEAK_VALU_TOPS = 1024 * 16 * 2.4e9 / 1e12
+# The VALU: MI355X's fp32 vector peak (157.3 TFLOP/s counting an FMA as two)
+# is 32 lanes per cycle per SIMD, i.e. a wave64 fp32 instruction every 2
+# cycles on each of 1024 SIMDs at 2.4 GHz = 78.6 T fp32 operations/s
+# (packed fp32 is not used). Measured on the part with s_memtime around
+# independent v_add_f32 / v_mul_f32: 2.25-2.5 cycles per instruction with
+# two or more waves per SIMD, 4.9 with one.
+PEAK_VALU_TOPS = 1024 * 32 * 2.4e9 / 1e12
+VALU_CYCLES = 2
+# Matrix-core cycles per instruction (the published dense peaks: int8 5.0
+# POP/s, fp32 157.3 TFLOP/s): v_mfma_i32_32x32x32_i8 and
+# v_mfma_f32_16x16x1_4b_f32 each occupy their SIMD's matrix core for 32
+# cycles. On this part a SIMD does not execute VALU and MFMA work at the
+# same time (measured: 4 MFMAs + 64 dependent adds per iteration take 288-
+# 330 cycles against 128 + 144 for the two alone), so an issue floor adds
+# the two.
+MFMA_CYCLES = 32
 HEAD_DIM = 256
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
-# The exact Q8_0 scaling is 3 fp32 VALU operations per output per 32-block.
-VALU_WAVE_INSTR_PER_US = 1024 * 2400.0 / 4
+SIMD_CYCLES_PER_US = 1024 * 2400.0
+
+
+def issue_floor_us(valu_instr, mfma_instr=0):
+    """Time the given wave64 VALU and MFMA instructions need at the peak
+    issue rates, executed one after the other on every SIMD."""
+    return (valu_instr * VALU_CYCLES + mfma_instr * MFMA_CYCLES) / SIMD_CYCLES_PER_US
+
+
 METRIC = "embedded tokens/s @2048-tok packed waves (1 GPU); Q8_0 GEMM % MFMA peak"
 
 
@@ -175,17 +183,8 @@ def kernel_table(eg2, torch, steps):
     T, E, F, D = TOKENS, 768, 1152, 256
     out = {}
 
-    def rec(name, ms, work, unit, peak, valu_instr=None):
-        rate = work / (ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
-        out[name] = {"us": round(ms * 1e3, 2), "achieved": round(rate, 1), "unit": unit, "peak": peak,
-                     "frac": round(rate / peak, 4)}
-        if valu_instr is not None:
-            floor = valu_instr / VALU_WAVE_INSTR_PER_US
-            out[name]["valu_floor_us"] = round(floor, 2)
-            out[name]["valu_floor_frac"] = round(floor / (ms * 1e3), 4)
-
-    def scaling_instr(m, k):
-        return T * m * (k // 32) * 3 // 64
+    def rec(name, ms, work, unit, peak, valu_instr=None, mfma_instr=0):
+        out[name] = rate_entry(ms, work, unit, peak, valu_instr, mfma_instr)
 
     for name, (m, k) in {"gemm_o 2048x768x768": (E, E),
                          "gemm_gate_up_geglu 2048x2304x768": (2 * F, E), "gemm_down 2048x768x1152": (E, F)}.items():
@@ -195,7 +194,7 @@ def kernel_table(eg2, torch, steps):
             ms = time_launches(torch, lambda: eg2.ops.gemm_q8_geglu(xq, xd, wq, wd, gq, gd, T), steps, 3)
         else:
             ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
-        rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS, scaling_instr(m, k))
+        rec(name, ms, 2.0 * T * m * k, "TFLOP/s", PEAK_INT8_TOPS, scaling_instr(T, m, k), mfma_tiles(T, m, k))
 
     rnd = lambda *shape: torch.randn(*shape, generator=g).to(dev)
     w_e, w_d = torch.ones(E, device=dev), torch.ones(D, device=dev)
@@ -223,21 +222,359 @@ def kernel_table(eg2, torch, steps):
     ms = time_launches(torch, lambda: eg2.ops.gemm_q8_qkv_rope(xq, xd, wq, wd, T, w_d, w_d, rope, pos, 1e-6, qkv),
                        steps, 3)
     rec("gemm_qkv_rope 2048x1280x768", ms, 2.0 * T * eg2.QKV_COLS * E, "TFLOP/s", PEAK_INT8_TOPS,
-        scaling_instr(eg2.QKV_COLS, E))
-    # Attention on realistic operands: the QKV rows of unit-scale activations.
+        scaling_instr(T, eg2.QKV_COLS, E), mfma_tiles(T, eg2.QKV_COLS, E))
+    # Attention on realistic operands (the QKV rows of unit-scale
+    # activations after QK-norm/RoPE): the 16 x 128 packing of the headline,
+    # and one 2048-token sequence, the longest wave of the stream.
     qkv.copy_(torch.randn((T, eg2.QKV_COLS), generator=g).to(dev))
     eg2.ops.qk_norm_rope(qkv, w_d, w_d, rope, pos, 1e-6, qkv)
-    cq = torch.zeros(eg2.q8_tile_bytes(T, E), dtype=torch.int8, device=dev)
-    cd = torch.zeros((E // 32, T), device=dev)
-    att = eg2.AttentionPlan(offsets, dev)
-    ms = time_launches(torch, lambda: eg2.ops.attention_planned(qkv, att, 0, cq, cd), steps, 3)
-    # Exact (reference-order) attention: every product on fp32 MFMA, every
-    # addition a rounded VALU add -- one per dimension per (query, key,
-    # head) for the scores and again for the context; the rate below counts
-    # those adds against the VALU peak.
-    adds = 2.0 * 3 * HEAD_DIM * sum((offsets[i + 1] - offsets[i]) ** 2 for i in range(SEQS))
-    rec("attention 16x128", ms, adds, "TFLOP/s", PEAK_VALU_TOPS, adds / 64)
+    out["attention 16x128"] = attention_entry(eg2, torch, qkv, offsets, steps)
+    pos_long = torch.arange(T, dtype=torch.int32, device=dev)
+    qkv.copy_(torch.randn((T, eg2.QKV_COLS), generator=g).to(dev))
+    eg2.ops.qk_norm_rope(qkv, w_d, w_d, rope, pos_long, 1e-6, qkv)
+    out["attention 1x2048"] = attention_entry(eg2, torch, qkv, [0, T], max(5, steps // 4))
     return out
+
+
+def scaling_instr(n, m, k):
+    """Wave64 VALU instructions of the exact Q8_0 scaling of an n x m x k
+    GEMM: 3 fp32 operations per output per 32-block (gemma2.c:128-133)."""
+    return n * m * (k // 32) * 3 // 64
+
+
+def mfma_tiles(n, m, k):
+    """v_mfma_i32_32x32x32_i8 instructions of an n x m x k GEMM."""
+    return n * m * k // (32 * 32 * 32)
+
+
+def rate_entry(ms, work, unit, peak, valu_instr=None, mfma_instr=0):
+    """A kernel's time, achieved rate against its roofline peak and, for
+    VALU-bound kernels, its issue floors: the VALU instructions its exact
+    arithmetic needs alone (valu_floor) and with its MFMA instructions
+    (issue_floor; a SIMD runs them one after the other)."""
+    rate = work / (ms / 1e3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    e = {"us": round(ms * 1e3, 2), "achieved": round(rate, 1), "unit": unit, "peak": peak,
+         "frac": round(rate / peak, 4)}
+    if valu_instr is not None:
+        v = issue_floor_us(valu_instr)
+        f = issue_floor_us(valu_instr, mfma_instr)
+        e.update(valu_floor_us=round(v, 2), valu_floor_frac=round(v / (ms * 1e3), 4), issue_floor_us=round(f, 2),
+                 issue_floor_frac=round(f / (ms * 1e3), 4))
+    return e
+
+
+def attention_adds(offsets):
+    """Ordered fp32 adds of exact attention over the packing: one per
+    dimension per (query, key, head) for the scores and again for the
+    context (each with one fp32 MFMA product)."""
+    return 2.0 * 3 * HEAD_DIM * sum((int(offsets[i + 1]) - int(offsets[i])) ** 2 for i in range(len(offsets) - 1))
+
+
+def attention_entry(eg2, torch, qkv, offsets, steps):
+    """Attention over the rows qkv of the packing `offsets`: the whole
+    operator, and each of its three stages launched alone (scores, softmax,
+    context), with the rate of its ordered adds against the VALU peak and
+    its issue floors (the adds on the VALU, the products on fp32 MFMA)."""
+    T = qkv.shape[0]
+    dev = qkv.device
+    cq = torch.zeros(eg2.q8_tile_bytes(T, 768), dtype=torch.int8, device=dev)
+    cd = torch.zeros((768 // 32, T), device=dev)
+    att = eg2.AttentionPlan(offsets, dev)
+    adds = attention_adds(offsets)
+    ms = time_launches(torch, lambda: eg2.ops.attention_planned(qkv, att, 0, cq, cd), steps, 3)
+    e = rate_entry(ms, adds, "TFLOP/s", PEAK_VALU_TOPS, adds / 64, adds / 1024)
+    e["stages"] = {}
+    for stage in ("scores", "softmax", "context"):
+        sms = time_launches(torch, lambda: eg2.ops.attention_stage(stage, qkv, att, 0, cq, cd), steps, 2)
+        if stage == "softmax":
+            e["stages"][stage] = {"us": round(sms * 1e3, 2)}
+        else:
+            e["stages"][stage] = rate_entry(sms, adds / 2, "TFLOP/s", PEAK_VALU_TOPS, adds / 128, adds / 2048)
+    eg2.ops.attention_planned(qkv, att, 0, cq, cd)  # leaves the whole operator's result
+    return e
+
+
+# ---------------------------------------------------------------- configurations 1-3
+# The three single-kernel / single-layer workloads of the benchmark plan,
+# each on its seeded inputs: the GPU time (HIP events on the launching
+# stream), the rate against its roofline and issue floors, the oracle (the
+# C restatement of the reference CPU path) on the same inputs timed on the
+# host's cores (median of CPU_SAMPLES after a warmup, at each thread
+# count), and the GPU result compared with the oracle's bit for bit.
+
+CPU_SAMPLES = 5
+
+
+def segments_log_uniform(rng, n_seg=16, total=2048, lo=8, hi=512):
+    """Configuration 2's packing: sequence lengths ~ exp(U(ln lo, ln hi)),
+    scaled to sum `total`, rounded, each clipped to [lo, hi]; the remainder
+    goes to the last one (clipped as well, any leftover is spread over the
+    others)."""
+    import numpy as np
+
+    raw = np.exp(rng.uniform(np.log(lo), np.log(hi), n_seg))
+    lens = np.clip(np.round(raw / raw.sum() * total).astype(np.int64), lo, hi)
+    lens[-1] = np.clip(total - lens[:-1].sum(), lo, hi)
+    i = 0
+    while lens.sum() != total:
+        step = 1 if lens.sum() < total else -1
+        if lo <= lens[i % (n_seg - 1)] + step <= hi:
+            lens[i % (n_seg - 1)] += step
+        i += 1
+    return lens
+
+
+def cpu_median(fn, thread_counts, samples=CPU_SAMPLES):
+    """{threads: median seconds} of fn(threads) over `samples` timed runs
+    after one untimed run, and the samples."""
+    import numpy as np
+
+    res = {}
+    for th in thread_counts:
+        fn(th)
+        ts = []
+        for _ in range(samples):
+            t0 = time.perf_counter()
+            fn(th)
+            ts.append(time.perf_counter() - t0)
+        res[str(th)] = {"median_ms": round(float(np.median(ts)) * 1e3, 3),
+                        "samples_ms": [round(t * 1e3, 3) for t in ts]}
+    return res
+
+
+def q8_activations(eg2, torch, x):
+    """Device Q8_0 activations of the fp32 rows x (device [n, k]): row tiles
+    and scales [k/32, n], by the library's quantizer (the reference's)."""
+    n, k = x.shape
+    xq = torch.zeros(eg2.q8_tile_bytes(n, k), dtype=torch.int8, device=x.device)
+    xd = torch.zeros((k // 32, n), dtype=torch.float32, device=x.device)
+    eg2.ops.quantize_rows(x, xq, xd)
+    return xq, xd
+
+
+def config1_gemm(eg2, torch, steps, thread_counts):
+    """Configuration 1: the gate/up projection alone, X fp32 [512, 768] ~
+    N(0,1) (quantized to Q8_0 as the reference's activations are), W
+    [2304, 768] ~ N(0, 0.02) -> Q8_0, fp32 Y [512, 2304]; seed 0."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_lib as OL
+
+    n, m, k = 512, 2304, 768
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    w = OL.quantize_q8_0((rng.standard_normal((m, k)) * 0.02).astype(np.float32))
+    dev = torch.device("cuda:0")
+    xq, xd = q8_activations(eg2, torch, torch.from_numpy(x).to(dev))
+    wq_h, wd_h = eg2.q8_weight_tiles(w.view(np.uint8), m, k)
+    wq, wd = torch.from_numpy(wq_h).to(dev), torch.from_numpy(wd_h).to(dev)
+    y = torch.zeros((n, m), dtype=torch.float32, device=dev)
+    ms = time_launches(torch, lambda: eg2.ops.gemm_q8(xq, xd, wq, wd, y), steps, 3)
+    xq_h = OL.quantize_q8_0(x)
+    want = OL.gemm_q8_0(w, xq_h, threads=thread_counts[0])
+    got = y.cpu().numpy()
+    e = rate_entry(ms, 2.0 * n * m * k, "TFLOP/s", PEAK_INT8_TOPS, scaling_instr(n, m, k), mfma_tiles(n, m, k))
+    e.update(workload="gemm_q8 512x2304x768 (gate|up rows, fp32 output), X ~ N(0,1) -> Q8_0, W ~ N(0,0.02) -> "
+                      "Q8_0, seed 0",
+             bit_exact_vs_oracle=bool(np.array_equal(got, want)),
+             cpu=cpu_median(lambda th: OL.gemm_q8_0(w, xq_h, threads=th), thread_counts))
+    return e
+
+
+def rope_rows(x, table, pos):
+    """The NeoX rotation of kernels.c:233-264 (pairs d, d + 128) of the
+    256-wide rows x [T, 256] at positions pos, with the host cos/sin table
+    [n_pos][cos 0..127 | sin 0..127], in fp32 with one rounding per
+    operation as the reference writes it."""
+    import numpy as np
+
+    c, s_ = table[pos, :128], table[pos, 128:]
+    x0, x1 = x[:, :128], x[:, 128:]
+    lo = (x0 * c).astype(np.float32) - (x1 * s_).astype(np.float32)
+    hi = (x0 * s_).astype(np.float32) + (x1 * c).astype(np.float32)
+    return np.concatenate([lo, hi], axis=1).astype(np.float32)
+
+
+def config2_attention(eg2, torch, steps, thread_counts):
+    """Configuration 2: packed bidirectional GQA attention alone, T = 2048
+    from 16 log-uniform segments in [8, 512]; Q [T, 3, 256], K and V [T,
+    256] ~ N(0,1), RoPE base 1e4 on Q and K, Q scaled by 1/16 (=
+    1/sqrt(256), exact); full attention inside each segment; seed 0. The
+    context is computed in fp32 in the reference's order (the reference
+    CPU path's arithmetic) and quantized to Q8_0 for the O projection as
+    the forward does."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_lib as OL
+
+    rng = np.random.default_rng(0)
+    lens = segments_log_uniform(rng)
+    T = int(lens.sum())
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.int64)
+    table = eg2.rope_table(1e4)
+    q = rng.standard_normal((T, 3, 256)).astype(np.float32)
+    k = rng.standard_normal((T, 256)).astype(np.float32)
+    v = rng.standard_normal((T, 256)).astype(np.float32)
+    q = np.stack([rope_rows(q[:, h], table, pos) for h in range(3)], axis=1).reshape(T, 768)
+    q = (q * np.float32(0.0625)).astype(np.float32)
+    k = rope_rows(k, table, pos)
+    dev = torch.device("cuda:0")
+    qkv = torch.from_numpy(np.concatenate([q, k, v], axis=1)).to(dev)
+    e = attention_entry(eg2, torch, qkv, list(offsets), steps)
+    cq, cd = torch.zeros(eg2.q8_tile_bytes(T, 768), dtype=torch.int8, device=dev), torch.zeros((24, T), device=dev)
+    att = eg2.AttentionPlan(list(offsets), dev)
+    eg2.ops.attention_planned(qkv, att, 0, cq, cd)
+    got_q = eg2.q8_unpack_rows(cq.cpu().numpy(), T, 768)
+    got_d = np.ascontiguousarray(cd.cpu().numpy().T)
+
+    def oracle_ctx(threads):
+        """The oracle's attention per sequence, query ranges spread over
+        `threads` host threads (each call releases the GIL)."""
+        ctx = np.zeros((T, 768), np.float32)
+        jobs = []
+        for s in range(len(lens)):
+            a, b = int(offsets[s]), int(offsets[s + 1])
+            step = max(1, (b - a + 3) // 4)
+            for q0 in range(0, b - a, step):
+                jobs.append((a, b, q0, min(b - a, q0 + step)))
+
+        def run(job):
+            a, b, q0, q1 = job
+            sc = np.zeros(4096, np.float32)
+            OL.oracle().or_attention_range(OL.fptr(np.ascontiguousarray(q[a:b])), OL.fptr(np.ascontiguousarray(k[a:b])),
+                                           OL.fptr(np.ascontiguousarray(v[a:b])), b - a, 0, q0, q1, OL.fptr(ctx[a:b]),
+                                           OL.fptr(sc))
+
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(run, jobs))
+        return ctx
+
+    want = OL.quantize_q8_0(oracle_ctx(thread_counts[0]))
+    want_d = np.frombuffer(np.ascontiguousarray(want["d"]).tobytes(), np.float16).astype(np.float32).reshape(T, 24)
+    e.update(workload=f"attention, 16 log-uniform segments in [8, 512] summing to 2048 (lengths {lens.tolist()}), "
+                      "Q [T,3,256], K/V [T,256] ~ N(0,1), RoPE 1e4, scale 1/16, seed 0",
+             bit_exact_vs_oracle=bool(np.array_equal(got_q, want["qs"].reshape(T, 768)) and
+                                      np.array_equal(got_d.view(np.uint32), want_d.view(np.uint32))),
+             cpu=cpu_median(oracle_ctx, thread_counts))
+    return e
+
+
+def layer_weights(rng):
+    """One encoder layer's weights as the reference stores them: Q8_0
+    matrices ~ N(0, 0.02) (the GGUF blocks the oracle reads) and fp32 norm
+    weights 1 + 0.1 N(0,1)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_lib as OL
+
+    def mat(rows, cols):
+        return OL.quantize_q8_0((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+
+    def norm(n):
+        return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+    return {"attn_q": mat(768, 768), "attn_k": mat(256, 768), "attn_v": mat(256, 768), "attn_output": mat(768, 768),
+            "ffn_gate": mat(1152, 768), "ffn_up": mat(1152, 768), "ffn_down": mat(768, 1152),
+            "attn_norm": norm(768), "attn_q_norm": norm(256), "attn_k_norm": norm(256),
+            "post_attention_norm": norm(768), "ffn_norm": norm(768), "post_ffw_norm": norm(768)}
+
+
+class DeviceLayer:
+    """One layer on the GPU through the operator entry points, the kernels
+    and order the executor records per layer (executor.cpp record_layers):
+    Q|K|V GEMM + QK-norm/RoPE, attention (scores, softmax, context + Q8_0),
+    O GEMM, residual + post-attention norm + ffn_norm + Q8_0, gate|up GEMM +
+    GeGLU + Q8_0, down GEMM, residual + post-FFN norm + the next layer's
+    attn_norm + Q8_0 (here the same layer's). The layer's input x (fp32
+    rows) enters as the Q8_0 of attn_norm(x), which the previous layer's
+    last kernel leaves in the forward; prepare() makes it."""
+
+    def __init__(self, eg2, torch, L, offsets, rope_base=1e4, eps=1e-6):
+        import numpy as np
+
+        self.eg2, self.torch, self.eps = eg2, torch, eps
+        dev = self.dev = torch.device("cuda:0")
+        T = self.T = int(offsets[-1])
+        up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        qkv = np.concatenate([L["attn_q"], L["attn_k"], L["attn_v"]], axis=0)
+        self.w_qkv = [up(a) for a in eg2.q8_weight_tiles(qkv.view(np.uint8), 1280, 768)]
+        self.w_o = [up(a) for a in eg2.q8_weight_tiles(L["attn_output"].view(np.uint8), 768, 768)]
+        self.w_gu = [up(a) for a in eg2.q8_geglu_weight_tiles(L["ffn_gate"].view(np.uint8),
+                                                              L["ffn_up"].view(np.uint8), 1152, 768)]
+        self.w_down = [up(a) for a in eg2.q8_weight_tiles(L["ffn_down"].view(np.uint8), 768, 1152)]
+        self.norms = {n: up(L[n]) for n in ("attn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm",
+                                            "ffn_norm", "post_ffw_norm")}
+        self.rope = up(eg2.rope_table(rope_base))
+        lens = np.diff(np.asarray(offsets))
+        self.pos = up(np.concatenate([np.arange(n) for n in lens]).astype(np.int32))
+        self.plan = eg2.AttentionPlan(list(offsets), dev)
+        f32 = lambda *shape: torch.zeros(shape, dtype=torch.float32, device=dev)
+        i8 = lambda k: torch.zeros(eg2.q8_tile_bytes(T, k), dtype=torch.int8, device=dev)
+        self.x, self.h, self.qkv = f32(T, 768), f32(T, 768), f32(T, 1280)
+        self.xq, self.xd = i8(1152), f32(36, T)
+        self.cq, self.cd = i8(768), f32(24, T)
+
+    def prepare(self, x):
+        """x (host fp32 [T, 768]) -> self.x, and self.xq / xd = Q8_0 of
+        attn_norm(x)."""
+        torch, eg2 = self.torch, self.eg2
+        self.x.copy_(torch.from_numpy(x))
+        t = self.x.clone()
+        eg2.ops.rms_norm_rows(t, self.norms["attn_norm"], self.eps)
+        eg2.ops.quantize_rows(t, self.xq[:eg2.q8_tile_bytes(self.T, 768)], self.xd[:24])
+        torch.cuda.synchronize()
+
+    def run(self):
+        eg2, n, T = self.eg2, self.norms, self.T
+        eg2.ops.gemm_q8_qkv_rope(self.xq[:eg2.q8_tile_bytes(T, 768)], self.xd[:24], *self.w_qkv, T,
+                                 n["attn_q_norm"], n["attn_k_norm"], self.rope, self.pos, self.eps, self.qkv)
+        eg2.ops.attention_planned(self.qkv, self.plan, 0, self.cq, self.cd)
+        eg2.ops.gemm_q8(self.cq, self.cd, *self.w_o, self.h)
+        eg2.ops.residual_norm_quant(self.x, self.h, n["post_attention_norm"], n["ffn_norm"], self.eps, self.cq,
+                                    self.cd)
+        eg2.ops.gemm_q8_geglu(self.cq, self.cd, *self.w_gu, self.xq, self.xd, T)
+        eg2.ops.gemm_q8(self.xq, self.xd, *self.w_down, self.h)
+        eg2.ops.residual_norm_quant(self.x, self.h, n["post_ffw_norm"], n["attn_norm"], self.eps,
+                                    self.xq[:eg2.q8_tile_bytes(T, 768)], self.xd[:24])
+
+
+def config3_layer(eg2, torch, steps, thread_counts):
+    """Configuration 3: one encoder layer over configuration 2's packing,
+    hidden state ~ N(0,1) [2048, 768], weights ~ N(0, 0.02) -> Q8_0 (norms
+    1 + 0.1 N(0,1)), full attention, RoPE base 1e4; seed 0."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_lib as OL
+
+    rng = np.random.default_rng(0)
+    lens = segments_log_uniform(rng)
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    T = int(offsets[-1])
+    x0 = rng.standard_normal((T, 768)).astype(np.float32)
+    L = layer_weights(rng)
+    lay = DeviceLayer(eg2, torch, L, offsets)
+    lay.prepare(x0)
+    lay.run()
+    got = lay.x.cpu().numpy()
+    want = OL.layer_forward(L, x0, offsets, 1e4, 0, 1e-6, thread_counts[0])
+    ms = time_launches(torch, lay.run, steps, 2)
+    valu = (scaling_instr(T, 1280, 768) + scaling_instr(T, 768, 768) + scaling_instr(T, 2304, 768) +
+            scaling_instr(T, 768, 1152) + attention_adds(offsets) / 64)
+    mfma = (mfma_tiles(T, 1280, 768) + mfma_tiles(T, 768, 768) + mfma_tiles(T, 2304, 768) +
+            mfma_tiles(T, 768, 1152) + attention_adds(offsets) / 1024)
+    f = issue_floor_us(valu, mfma)
+    return {"workload": "one encoder layer (norm, QKV + QK-norm/RoPE, attention, O, residual + norms, gate|up + "
+                        "GeGLU, down, residual) over configuration 2's packing, hidden ~ N(0,1), seed 0",
+            "us": round(ms * 1e3, 2), "issue_floor_us": round(f, 2), "issue_floor_frac": round(f / (ms * 1e3), 4),
+            "tokens_per_s_per_layer": round(T / (ms / 1e3), 1),
+            "bit_exact_vs_oracle": bool(np.array_equal(got, want)),
+            "cpu": cpu_median(lambda th: OL.layer_forward(L, x0, offsets, 1e4, 0, 1e-6, th), thread_counts)}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q8_geglu_gate_up_2048x2304x768_traffic.md")
@@ -274,6 +611,9 @@ def kernel_only(kind, steps):
     torch.cuda.set_device(0)
     if kind == "table":
         print(json.dumps(kernel_table(eg2, torch, steps)))
+    elif kind == "configs":
+        nproc = host_cpus()
+        print(json.dumps(run_configs(eg2, torch, steps, [nproc] + ([32] if nproc != 32 else []))))
     elif kind == "gate_up":
         ms = time_gemm(eg2, torch, steps, 2)
         print(json.dumps({"kernel": "gemm_q8_geglu gate|up 2048x2304x768", "avg_us": round(ms * 1e3, 2), "launches": steps + 2}))
@@ -330,6 +670,72 @@ def run_stream(eg2, enc, n_requests):
             "mean_wave_tokens": round(tokens / waves, 1)}
 
 
+def synth_model(eg2, path, threads):
+    eg2.synth_gguf(path, seed=0, n_layer=LAYERS, dense_head=True, sliding_window=0, rope_base_full=1e4,
+                   rope_base_swa=1e4, threads=threads)
+
+
+def default_queues_child(steps, warmup):
+    """The headline's lanes measurement under the environment's hardware
+    queues (child process of run_default_queues_child): one JSON line."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    eg2 = __graft_entry__._package()
+    torch.cuda.set_device(0)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, eg2.VOCAB, TOKENS).astype(np.int32)
+    offsets = list(range(0, TOKENS + 1, TOKENS // SEQS))
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "bench.gguf")
+        synth_model(eg2, path, min(host_cpus(), 64))
+        enc = eg2.Encoder(path)
+        lanes = enc.lanes
+        for lane in range(lanes):
+            enc.stage(ids, offsets, lane)
+        for i in range(warmup * lanes):
+            enc.launch(1, i % lanes)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            enc.launch(1, i % lanes)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        enc.close()
+    print(json.dumps({"hw_queues": int(os.environ.get("GPU_MAX_HW_QUEUES", "4")), "lanes": lanes,
+                      "ms_per_step": round(ms, 4), "tokens_per_s": round(TOKENS / ms * 1e3, 1)}), flush=True)
+
+
+def run_default_queues_child(steps, warmup):
+    import subprocess
+
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--default-queues-child", "--steps", str(steps),
+                        "--warmup", str(warmup)], capture_output=True, text=True, timeout=600)
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    if r.returncode != 0 or not lines:
+        log(f"default-queue measurement failed (rc {r.returncode}): {r.stderr[-500:]}")
+        return None
+    res = json.loads(lines[-1])
+    log(f"runtime default queues ({res['hw_queues']}): {res['lanes']} lanes, {res['ms_per_step']:.3f} ms/step, "
+        f"{res['tokens_per_s']:,.0f} tokens/s")
+    return res
+
+
+def run_configs(eg2, torch, steps, thread_counts):
+    out = {}
+    for name, fn in (("1_gemm_q8", config1_gemm), ("2_attention", config2_attention), ("3_layer", config3_layer)):
+        t0 = time.perf_counter()
+        out[name] = fn(eg2, torch, steps, thread_counts)
+        e = out[name]
+        cpu = ", ".join(f"{th} threads {v['median_ms']:.2f} ms" for th, v in e["cpu"].items())
+        log(f"config {name}: GPU {e['us']:.2f} us, issue floor {e['issue_floor_us']:.2f} us "
+            f"({100 * e['issue_floor_frac']:.0f}%), bit-exact vs oracle {e['bit_exact_vs_oracle']}; CPU {cpu} "
+            f"({time.perf_counter() - t0:.1f} s)")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,17 +748,40 @@ def main():
                     help="requests in the dynamic-batching stream measurement (0 skips it)")
     ap.add_argument("--no-kernel-table", action="store_true",
                     help="skip the per-kernel table (keeps a kernel trace to the forward and the roofline GEMM)")
-    ap.add_argument("--kernel-only", choices=["gate_up", "copy", "table"],
+    ap.add_argument("--kernel-only", choices=["gate_up", "copy", "table", "configs"],
                     help="run only the dominant GEMM (or the copy calibration kernel) for counter runs, "
-                         "or only the per-kernel table")
+                         "or only the per-kernel table, or only configurations 1-3")
+    ap.add_argument("--no-configs", action="store_true", help="skip configurations 1-3")
+    ap.add_argument("--no-default-queues", action="store_true",
+                    help="skip the measurement under the runtime's default hardware queues")
+    ap.add_argument("--default-queues-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has a single MI355X and this path runs "
               "independent waves per GPU (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.default_queues_child:
+        default_queues_child(args.steps, args.warmup)
+        return
     if args.kernel_only:
         kernel_only(args.kernel_only, args.steps)
         return
+    # The library's own configuration, as a service started on this box
+    # runs it: HIP's default hardware queues (GPU_MAX_HW_QUEUES as the
+    # environment has it, 4 unless set), where the executor opens
+    # min(4, queues - 1) lanes. Measured in a child process, before this
+    # process touches the GPU (the HIP runtime reads the variable once).
+    default_queues = None
+    if not args.no_default_queues:
+        default_queues = run_default_queues_child(args.steps, args.warmup)
+    # The serving configuration of the headline: at least 8 hardware queues
+    # per process, so each of the executor's four lanes runs on a queue of
+    # its own; set before torch or the library initialises HIP.
+    try:
+        queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+    except ValueError:
+        queues = 4
+    os.environ["GPU_MAX_HW_QUEUES"] = str(max(queues, 8))
 
     import numpy as np
     import torch
@@ -438,14 +867,26 @@ def main():
         gemm_ms = time_gemm(eg2, torch, max(20, args.steps), 5)
         flops = 2.0 * GEMM_N * GEMM_M * GEMM_K
         achieved = flops / (gemm_ms / 1e3) / 1e12
-        scaling_instr = GEMM_N * GEMM_M * (GEMM_K // 32) * 3 // 64
-        valu_floor_us = scaling_instr / VALU_WAVE_INSTR_PER_US
+        gu_valu = scaling_instr(GEMM_N, GEMM_M, GEMM_K)
+        gu_mfma = mfma_tiles(GEMM_N, GEMM_M, GEMM_K)
+        valu_floor_us = issue_floor_us(gu_valu)
+        gu_issue_us = issue_floor_us(gu_valu, gu_mfma)
         log(f"gate|up + GeGLU GEMM {gemm_ms * 1e3:.1f} us, {achieved:.1f} T int8 op/s; exact-scaling VALU floor "
-            f"{valu_floor_us:.2f} us ({100 * valu_floor_us / (gemm_ms * 1e3):.0f}% of the kernel's time)")
+            f"{valu_floor_us:.2f} us, with its MFMAs {gu_issue_us:.2f} us "
+            f"({100 * gu_issue_us / (gemm_ms * 1e3):.0f}% of the kernel's time)")
         kernels = {} if args.no_kernel_table else kernel_table(eg2, torch, max(20, args.steps))
         for name, k in kernels.items():
-            floor = f"  VALU floor {k['valu_floor_us']:.2f} us ({100 * k['valu_floor_frac']:.0f}%)" if "valu_floor_us" in k else ""
+            floor = (f"  issue floor {k['issue_floor_us']:.2f} us ({100 * k['issue_floor_frac']:.0f}%)"
+                     if "issue_floor_us" in k else "")
             log(f"  {name:28s} {k['us']:8.2f} us  {k['achieved']:8.1f} {k['unit']:8s} {100 * k['frac']:5.1f}% of peak{floor}")
+            for st, v in k.get("stages", {}).items():
+                floor = (f"  issue floor {v['issue_floor_us']:.2f} us ({100 * v['issue_floor_frac']:.0f}%)"
+                         if "issue_floor_us" in v else "")
+                log(f"      {st:24s} {v['us']:8.2f} us{floor}")
+        configs = None
+        if not args.no_configs:
+            counts = [cpu_threads] + ([32] if cpu_threads != 32 else [])
+            configs = run_configs(eg2, torch, max(20, args.steps), counts)
 
         cpu = None
         if not args.no_cpu_baseline:
@@ -484,17 +925,24 @@ def main():
                    "layers": LAYERS, "hidden": 768, "ffn": 1152, "heads": "3q/1kv x 256", "weights": "Q8_0",
                    "attention": "full within sequence, RoPE base 1e4", "lanes": lanes,
                    "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"])},
+        "default_queues": default_queues,
         "roofline": {"bound": "mfma", "kernel": "gemm_q8_geglu gate|up 2048x2304x768 + GeGLU + Q8_0 (v_mfma_i32_32x32x32_i8; "
                                                 "achieved/peak in T int8 op/s)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
                      "avg_us": round(gemm_ms * 1e3, 2),
-                     "valu_floor": {"wave_instructions": scaling_instr, "floor_us": round(valu_floor_us, 2),
+                     "valu_floor": {"wave_instructions": gu_valu, "floor_us": round(valu_floor_us, 2),
                                     "frac": round(valu_floor_us / (gemm_ms * 1e3), 4),
                                     "what": "exact per-block scaling only: 3 fp32 VALU ops per output per "
-                                            "32-block at 4 cycles per wave64 instruction on 1024 SIMDs, 2.4 GHz"},
-                     "mfma_cap_at_valu_floor": round(flops / (valu_floor_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)},
+                                            "32-block at 2 cycles per wave64 instruction on 1024 SIMDs, 2.4 GHz"},
+                     "issue_floor": {"mfma_instructions": gu_mfma, "floor_us": round(gu_issue_us, 2),
+                                     "frac": round(gu_issue_us / (gemm_ms * 1e3), 4),
+                                     "what": "the scaling's VALU instructions plus the kernel's "
+                                             "v_mfma_i32_32x32x32_i8 (32 cycles each), one after the other"},
+                     "mfma_cap_at_valu_floor": round(flops / (valu_floor_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+                     "mfma_cap_at_issue_floor": round(flops / (gu_issue_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)},
         "kernels": kernels,
+        "configs": configs,
         "cpu_baseline": cpu,
         "host_inclusive_tokens_per_s": round(host_rate, 1),
         "one_wave_in_flight": {"ms_per_wave": round(single_ms, 4), "tokens_per_s": round(TOKENS / single_ms * 1e3, 1)},

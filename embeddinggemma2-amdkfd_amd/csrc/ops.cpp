@@ -75,6 +75,32 @@ int eg2_hip_attention(const float* qkv, const uint32_t* items, const uint32_t* i
                                     scores, cq, cd, as_stream(stream)));
 }
 
+int eg2_hip_attention_scores(const float* qkv, const uint32_t* items, const uint32_t* item_count, unsigned grid,
+                             unsigned window, unsigned rows, float* scores, void* stream) {
+  if (!qkv || !items || !item_count || !scores || rows == 0 || rows % 4 != 0 || rows > (1u << 24) || grid == 0 ||
+      grid > 65536 || window > 4096u)
+    return kInvalid;
+  return code(eg2::launch_attention_scores(qkv, items, item_count, (int)grid, (int)window, (int)rows, scores,
+                                           as_stream(stream)));
+}
+
+int eg2_hip_attention_softmax(const uint32_t* tok, unsigned window, unsigned rows, unsigned longest, float* scores,
+                              void* stream) {
+  if (!tok || !scores || rows == 0 || rows % 4 != 0 || rows > (1u << 24) || window > 4096u || longest > rows)
+    return kInvalid;
+  return code(eg2::launch_attention_softmax(tok, (int)window, (int)rows, (int)longest, scores, as_stream(stream)));
+}
+
+int eg2_hip_attention_context(const float* qkv, const uint32_t* items, const uint32_t* item_count, unsigned grid,
+                              unsigned window, unsigned rows, unsigned longest, const float* scores, int8_t* cq,
+                              float* cd, void* stream) {
+  if (!qkv || !items || !item_count || !scores || !cq || !cd || rows == 0 || rows % 4 != 0 || rows > (1u << 24) ||
+      grid == 0 || grid > 65536 || window > 4096u || longest > rows)
+    return kInvalid;
+  return code(eg2::launch_attention_context(qkv, items, item_count, (int)grid, (int)window, (int)rows, (int)longest,
+                                            scores, cq, cd, as_stream(stream)));
+}
+
 int eg2_hip_attention_static(const float* qkv, const uint32_t* offsets, unsigned batch, unsigned window,
                              unsigned rows, int8_t* cq, float* cd, void* stream) {
   if (!qkv || !offsets || !cq || !cd || rows == 0 || rows % 4 != 0 || rows > EG2_ATTENTION_STATIC_ROWS ||

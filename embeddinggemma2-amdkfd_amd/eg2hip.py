@@ -112,6 +112,9 @@ SIGNATURES = {
     "eg2_hip_qk_norm_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _u, _vp]),
     "eg2_hip_attention": (C.c_int, [_vp, _vp, _vp, _u, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
     "eg2_hip_attention_static": (C.c_int, [_vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
+    "eg2_hip_attention_scores": (C.c_int, [_vp, _vp, _vp, _u, _u, _u, _vp, _vp]),
+    "eg2_hip_attention_softmax": (C.c_int, [_vp, _u, _u, _u, _vp, _vp]),
+    "eg2_hip_attention_context": (C.c_int, [_vp, _vp, _vp, _u, _u, _u, _u, _vp, _vp, _vp, _vp]),
     "eg2_attention_plan": (C.c_int, [C.POINTER(C.c_size_t), C.c_size_t, C.c_size_t, C.c_size_t, _vp, _vp,
                                      C.POINTER(C.c_size_t)]),
     "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -633,6 +636,26 @@ class ops:
                                       cls._p(plan.tok), window, qkv.shape[0],
                                       plan.longest if longest is None else longest, cls._p(plan.scores),
                                       cls._p(cq), cls._p(cd), cls._stream()), "attention")
+
+    @classmethod
+    def attention_stage(cls, stage, qkv, plan, window, cq=None, cd=None, longest=None):
+        """One of attention_planned's three kernels stages ("scores",
+        "softmax", "context"), for timing them one by one."""
+        longest = plan.longest if longest is None else longest
+        L = lib()
+        if stage == "scores":
+            rc = L.eg2_hip_attention_scores(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID, window,
+                                            qkv.shape[0], cls._p(plan.scores), cls._stream())
+        elif stage == "softmax":
+            rc = L.eg2_hip_attention_softmax(cls._p(plan.tok), window, qkv.shape[0], longest, cls._p(plan.scores),
+                                             cls._stream())
+        elif stage == "context":
+            rc = L.eg2_hip_attention_context(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID, window,
+                                             qkv.shape[0], longest, cls._p(plan.scores), cls._p(cq), cls._p(cd),
+                                             cls._stream())
+        else:
+            raise ValueError(stage)
+        check(rc, "attention_" + stage)
 
     STATIC_ROWS, STATIC_BATCH = 2048, 2048  # EG2_ATTENTION_STATIC_ROWS / _BATCH
 

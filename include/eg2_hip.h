@@ -80,6 +80,22 @@ int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *i
                       const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores, int8_t *cq,
                       float *cd, void *stream);
 
+/* eg2_hip_attention's three stages, launched one at a time (same
+ * arguments and checks; run in this order they are eg2_hip_attention):
+ * the scores of every planned (token, head, key) into `scores`; the
+ * softmax of each score row in place (p values) with 1/sum at the head of
+ * `scores` (two kernels when longest is 0 or above 2048); the context,
+ * quantized to Q8_0 into cq / cd. For per-kernel timing (the reference
+ * times each dispatch, src/gemma2_kfd.cpp:173-186). Replace, together,
+ * kernels/eg2.c:145-170 eg2_attention256. */
+int eg2_hip_attention_scores(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
+                             unsigned window, unsigned rows, float *scores, void *stream);
+int eg2_hip_attention_softmax(const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores,
+                              void *stream);
+int eg2_hip_attention_context(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
+                              unsigned window, unsigned rows, unsigned longest, const float *scores, int8_t *cq,
+                              float *cd, void *stream);
+
 /* eg2_hip_attention without allocation. It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops and harnesses that forbid

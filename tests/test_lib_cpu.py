@@ -84,6 +84,15 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 30, 0, p, p, p, None) == inval  # rows % 4
     assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, 0, None, p, p, None) == inval  # no scratch
     assert lib.eg2_hip_attention(p, p, p, 64, p, 0, 32, 33, p, p, p, None) == inval  # longest > rows
+    # the three stages of attention
+    assert lib.eg2_hip_attention_scores(p, p, p, 0, 0, 32, p, None) == inval  # grid 0
+    assert lib.eg2_hip_attention_scores(p, p, p, 64, 0, 30, p, None) == inval  # rows % 4
+    assert lib.eg2_hip_attention_scores(p, p, p, 64, 0, 32, None, None) == inval  # no scratch
+    assert lib.eg2_hip_attention_softmax(None, 0, 32, 0, p, None) == inval
+    assert lib.eg2_hip_attention_softmax(p, 0, 32, 33, p, None) == inval  # longest > rows
+    assert lib.eg2_hip_attention_softmax(p, 99999, 32, 0, p, None) == inval  # window
+    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 32, 0, p, None, p, None) == inval
+    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 32, 33, p, p, p, None) == inval  # longest > rows
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, None, 4, None) == inval
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, p, 0, None) == inval
     assert lib.eg2_hip_libm_eval(p, 0, p, p, None) == inval
