@@ -84,6 +84,63 @@ def test_config5_stream_against_oracle(eg2, gpu, full_model):
     assert worst_cos >= COS_MIN and worst_abs <= MAX_ABS
 
 
+def stream_subset_against_oracle(eg2, enc, model, ids, offsets, dims, texts):
+    """The stream on the given texts (indices into the config-5 text list),
+    compared with the oracle after the Matryoshka prefix: (waves, min cos,
+    max abs, bit-exact)."""
+    lens = np.diff(offsets)[texts]
+    sub_offs = np.concatenate([[0], np.cumsum(lens)])
+    sub_ids = np.concatenate([ids[int(offsets[t]):int(offsets[t + 1])] for t in texts])
+    sub_dims = dims[texts]
+    out, waves = enc.stream(sub_ids, sub_offs, sub_dims)
+    want = oracle_waves(model, sub_ids, sub_offs)
+    cos, mx, exact = 1.0, 0.0, True
+    for i, d in enumerate(sub_dims):
+        w = want[i].copy()
+        assert OL.oracle().or_normalize_prefix(OL.fptr(w), int(d)) == 1
+        c, a = margins(out[i:i + 1, :d], w[None, :d])
+        cos, mx = min(cos, c), max(mx, a)
+        exact = exact and bool(np.array_equal(out[i, :d], w[:d])) and not out[i, d:].any()
+    return waves, cos, mx, exact
+
+
+def test_config5_long_request_and_full_wave_against_oracle(eg2, gpu, full_model):
+    """Three more pieces of the config-5 stream against the oracle: the
+    first request holding a text of at least 1,900 tokens (all of its
+    texts); the most populous wave of the batcher's packing of the whole
+    stream (25 sequences: its log-uniform lengths never fill 32); and 32
+    texts of the stream that make a full 32-sequence wave (the first 32 of
+    at most 64 tokens), each embedded as its own stream (the packer keeps
+    each of the last two in one wave)."""
+    sys.path.insert(0, ROOT)
+    import bench
+
+    ids, offsets, dims, texts = bench.config5_stream(eg2.VOCAB, with_requests=True)
+    lens = np.diff(offsets)
+    ends = np.cumsum(texts)
+    starts = ends - texts
+    long_req = next(r for r in range(len(texts)) if lens[starts[r]:ends[r]].max() >= 1900)
+    req_texts = list(range(int(starts[long_req]), int(ends[long_req])))
+    wave_texts = sorted(max(eg2.pack_waves(lens), key=len))
+    full_texts = [int(t) for t in np.flatnonzero(lens <= 64)[:32]]
+    model = gguf_py.oracle_model(full_model)
+    enc = eg2.Encoder(full_model)
+    rows = {}
+    try:
+        for name, sel in (("long_request", req_texts), ("largest_wave", wave_texts), ("full_wave", full_texts)):
+            waves, c, a, exact = stream_subset_against_oracle(eg2, enc, model, ids, offsets, dims, sel)
+            rows[name] = {"texts": len(sel), "tokens": int(lens[sel].sum()), "longest": int(lens[sel].max()),
+                          "waves": waves, "min_cos": c, "max_abs": a, "bit_exact": exact}
+    finally:
+        enc.close()
+    print(json.dumps({"config5_more": {"request": int(long_req), **rows}}))
+    assert rows["long_request"]["longest"] >= 1900
+    assert rows["largest_wave"]["texts"] >= 25 and rows["largest_wave"]["waves"] == 1
+    assert rows["full_wave"]["texts"] == 32 and rows["full_wave"]["waves"] == 1
+    for row in rows.values():
+        assert row["min_cos"] >= COS_MIN and row["max_abs"] <= MAX_ABS and row["bit_exact"], row
+
+
 def test_config4_margins_over_seeds(eg2, gpu, full_model):
     """The 16x128 wave with five more id seeds: every seed within the bar,
     margins printed for the record."""
