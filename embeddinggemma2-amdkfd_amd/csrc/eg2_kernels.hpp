@@ -45,8 +45,10 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // score items (8 uint32: sequence start, end, first key of a 32-key
 // block, first pair, end of the pairs, the sequence's first score index,
 // 0, 0) followed by item_count[1] context items (sequence start, end,
-// first pair of a 32-pair block, end of the pairs, first score index, 0,
-// 0, 0); a pair is 3 (token - start) + head. tok: one record per row (4
+// first pair of a 32-pair block, end of the pairs, first score index, the
+// context kernel's unit order (1: XCD-contiguous eighths, 0: plain stride;
+// the same in every context item), 0, 0); a pair is 3 (token - start) +
+// head. tok: one record per row (4
 // uint32: sequence start, end, first score index, 0). `grid` workgroups
 // stride over each item list. scores: the plan's score floats (the 1/sum
 // of each (token, head) at [3 t + h], then a row of ceil4(n) scores per
@@ -65,7 +67,7 @@ hipError_t launch_attention_scores(const float* qkv, const uint32_t* items, cons
 hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, int longest, float* scores,
                                     hipStream_t st);
 hipError_t launch_attention_context(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
-                                    int window, int rows, int longest, const float* scores, int8_t* cq, float* cd,
+                                    int window, int rows, const float* scores, int8_t* cq, float* cd,
                                     hipStream_t st);
 
 // The plan of launch_attention for the sequences [offsets[s], offsets[s+1])

@@ -588,8 +588,7 @@ void Backend::record_layers(Lane& ln, unsigned rows, unsigned longest) {
                                                                 L.window, n, ln.scores, s));
     launch(ln, "attention_softmax", eg2::launch_attention_softmax(ln.tok_d, L.window, n, (int)longest, ln.scores, s));
     launch(ln, "attention_context", eg2::launch_attention_context(ln.qkv, ln.items_d, ln.count_d, eg2::kAttentionGrid,
-                                                                  L.window, n, (int)longest, ln.scores, ln.cq, ln.cd,
-                                                                  s));
+                                                                  L.window, n, ln.scores, ln.cq, ln.cd, s));
     gemm(ln, "gemm_o", ln.cq, ln.cd, L.o, ln.h, n, kEmbd, s);
     // The FFN input goes to the attention context's buffers (free after the
     // O GEMM), so the fused gate|up + GeGLU kernel reads them and writes xq.

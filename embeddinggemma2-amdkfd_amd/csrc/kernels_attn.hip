@@ -71,6 +71,7 @@
 // packing never changes a bit.
 #include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "eg2_device.hpp"
 #include "eg2_kernels.hpp"
@@ -90,6 +91,7 @@ constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
 constexpr int kShortSoftmax = 512;        // longest sequence for the 16-pair one-kernel softmax
+constexpr int kCBatch = 4;                // context MFMAs in flight per wave
 constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
 
 // Work items of any packing of `tokens` rows into at most `batch`
@@ -145,31 +147,37 @@ __device__ __forceinline__ void store16(const Stage16& v, float* row, int grp) {
 }
 
 // One staged half (kSDims dimensions) of the wave's 16 pairs x 16 keys:
-// per 4 steps the 4 MFMAs into separate registers, then their adds (the
-// adds of one overlap the next ones' execution), with the next 4 steps'
-// operands read from LDS before the adds.
+// per kSBatch steps that many MFMAs into separate registers, then their
+// adds, with the next 4 steps' operands read from LDS before the adds. Two
+// in flight, not four: the kernel then holds 112 VGPRs instead of 148, four
+// waves per SIMD instead of three, whose MFMAs and adds interleave (one
+// 2048-token sequence 148 -> 138 us, a mixed packing 64 -> 55 us).
+constexpr int kSBatch = 2;
 __device__ __forceinline__ void scores_half(const float* qa, const float* kb, float (&acc)[4][4]) {
   const floatx16 zero = {};
   float4 q4 = *reinterpret_cast<const float4*>(qa), k4 = *reinterpret_cast<const float4*>(kb);
 #pragma unroll
   for (int s = 0; s < kSDims / 4; s += 4) {
     const float qv[4] = {q4.x, q4.y, q4.z, q4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
-    floatx16 prod[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
-      prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e], kv[e], zero, 0, 0, 0);
-    if (s + 4 < kSDims / 4) {
-      q4 = *reinterpret_cast<const float4*>(qa + s + 4);
-      k4 = *reinterpret_cast<const float4*>(kb + s + 4);
+    for (int e0 = 0; e0 < 4; e0 += kSBatch) {
+      floatx16 prod[kSBatch];
+#pragma unroll
+      for (int e = 0; e < kSBatch; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
+        prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e0 + e], kv[e0 + e], zero, 0, 0, 0);
+      if (e0 + kSBatch == 4 && s + 4 < kSDims / 4) {
+        q4 = *reinterpret_cast<const float4*>(qa + s + 4);
+        k4 = *reinterpret_cast<const float4*>(kb + s + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < kSBatch; ++e)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -573,20 +581,20 @@ attention_sum_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, 
 __global__ void __launch_bounds__(256)
 attention_context_kernel(const float* __restrict__ qkv, const float* __restrict__ scores,
                          const uint4* __restrict__ items, const uint32_t* __restrict__ item_count, int window,
-                         int rows, int8_t* __restrict__ cq, float* __restrict__ cd, int xcd_order) {
+                         int rows, int8_t* __restrict__ cq, float* __restrict__ cd) {
   __shared__ __align__(16) float wl[kCKeys * kCPitchW];  // [key][pair]: w = p * (1/sum), 0 outside the window
   __shared__ __align__(16) float vl[kCKeys * kCPitchV];  // [key][dimension]
   __shared__ uint32_t range[kCPairs][2];                  // each pair's key range
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const uint4* citems = items + 2 * (size_t)item_count[0];  // the context items follow the score items
-  // XCD-aware order as in the scores kernel when xcd_order is set (waves
-  // of sequences up to 512 tokens): XCD b % 8 takes the contiguous eighth
-  // of the work (items x 4 dimension quarters). Waves with longer
-  // sequences keep the plain stride, which spreads an item's four
-  // quarters over four XCDs (measured faster for them).
-  const bool by_xcd = xcd_order && gridDim.x % kXcdCount == 0;
+  // XCD-aware order as in the scores kernel when the plan asks for it (the
+  // first context item's it[5]: a packing whose contiguous eighths of
+  // units cost alike): XCD b % 8 takes the contiguous eighth of the work
+  // (items x 4 dimension quarters). Otherwise the plain stride, which
+  // spreads every sequence's units over the XCDs.
   const uint32_t total = 4 * item_count[1], xcd = blockIdx.x % kXcdCount;
+  const bool by_xcd = total > 0 && citems[1].y == 1u && gridDim.x % kXcdCount == 0;
   const uint32_t count = by_xcd ? total * (xcd + 1) / kXcdCount : total;
   const uint32_t stride = by_xcd ? gridDim.x / kXcdCount : gridDim.x;
   const floatx16 zero = {};
@@ -698,25 +706,28 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
         bn[e] = vb[2 * e * kCPitchV];
       }
       for (int j = 0; j < n8; j += 8) {
-        floatx16 prod[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)  // keys j + 2 e, j + 2 e + 1
-          prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(an[e], bn[e], zero, 0, 0, 0);
-        if (j + 8 < n8) {
+        for (int e0 = 0; e0 < 4; e0 += kCBatch) {
+          floatx16 prod[kCBatch];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            an[e] = wa[(j + 8 + 2 * e) * kCPitchW];
-            bn[e] = vb[(j + 8 + 2 * e) * kCPitchV];
+          for (int e = 0; e < kCBatch; ++e)  // keys j + 2 e, j + 2 e + 1
+            prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(an[e0 + e], bn[e0 + e], zero, 0, 0, 0);
+          if (e0 + kCBatch == 4 && j + 8 < n8) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              an[e] = wa[(j + 8 + 2 * e) * kCPitchW];
+              bn[e] = vb[(j + 8 + 2 * e) * kCPitchV];
+            }
           }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int e = 0; e < kCBatch; ++e)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)  // key j + 2 (e0 + e) + kk: blocks 2 kk, 2 kk + 1
+#pragma unroll
+              for (int v = 0; v < 8; ++v) acc[v] = acc[v] + prod[e][8 * kk + v];
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)  // key j + 2 e + kk: blocks 2 kk, 2 kk + 1
-#pragma unroll
-            for (int v = 0; v < 8; ++v) acc[v] = acc[v] + prod[e][8 * kk + v];
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // Through LDS to [pair][64 dimensions], then Q8_0: block (32 values) of
@@ -812,6 +823,27 @@ bool build_attention_plan(const size_t* offsets, size_t batch, const AttentionCo
     }
     sbase += seq_plan(len).score_floats;
   }
+  // The context kernel's unit order: its units (4 per context item, one per
+  // 64 dimensions) cost about their sequence's 64-key chunks. When the eight
+  // contiguous eighths of the unit list cost alike (waves of equal
+  // sequences), each XCD takes one (its L2 then holds few sequences' rows);
+  // otherwise the workgroups stride over the whole list, so each XCD gets a
+  // share of every sequence (a contiguous split of a mixed packing loads
+  // some XCDs with its long sequences: 1.5x the time on 16 log-uniform
+  // segments). The decision rides in the context items (it[5]).
+  const size_t citems = need.items - need.score_items, units = 4 * citems;
+  if (units > 0) {
+    std::vector<size_t> prefix(units + 1, 0);
+    for (size_t u = 0; u < units; ++u) {
+      const uint32_t* it = items + 8 * (need.score_items + u / 4);
+      prefix[u + 1] = prefix[u] + (it[1] - it[0] + kCKeys - 1) / kCKeys;
+    }
+    size_t most = 0;
+    for (size_t x = 0; x < kXcdCount; ++x)
+      most = std::max(most, prefix[units * (x + 1) / kXcdCount] - prefix[units * x / kXcdCount]);
+    const bool by_xcd = units >= kXcdCount && most * kXcdCount <= prefix[units] + prefix[units] / 32;
+    for (size_t c = 0; c < citems; ++c) items[8 * (need.score_items + c) + 5] = by_xcd ? 1u : 0u;
+  }
   return true;
 }
 
@@ -858,12 +890,11 @@ hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, i
 }
 
 hipError_t launch_attention_context(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
-                                    int window, int rows, int longest, const float* scores, int8_t* cq, float* cd,
+                                    int window, int rows, const float* scores, int8_t* cq, float* cd,
                                     hipStream_t st) {
-  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
+  if (rows <= 0 || rows % 4 != 0 || grid <= 0 || window < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_context_kernel, dim3(grid), dim3(256), 0, st, qkv, scores,
-                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd,
-                     longest > 0 && longest <= kShortSoftmax ? 1 : 0);
+                     reinterpret_cast<const uint4*>(items), item_count, window, rows, cq, cd);
   return hipGetLastError();
 }
 
@@ -875,7 +906,7 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
   if (e != hipSuccess) return e;
   e = launch_attention_softmax(tok, window, rows, longest, scores, st);
   if (e != hipSuccess) return e;
-  return launch_attention_context(qkv, items, item_count, grid, window, rows, longest, scores, cq, cd, st);
+  return launch_attention_context(qkv, items, item_count, grid, window, rows, scores, cq, cd, st);
 }
 
 // ---------------------------------------------------------------- allocation-free form

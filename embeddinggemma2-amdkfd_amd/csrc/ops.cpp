@@ -92,13 +92,13 @@ int eg2_hip_attention_softmax(const uint32_t* tok, unsigned window, unsigned row
 }
 
 int eg2_hip_attention_context(const float* qkv, const uint32_t* items, const uint32_t* item_count, unsigned grid,
-                              unsigned window, unsigned rows, unsigned longest, const float* scores, int8_t* cq,
-                              float* cd, void* stream) {
+                              unsigned window, unsigned rows, const float* scores, int8_t* cq, float* cd,
+                              void* stream) {
   if (!qkv || !items || !item_count || !scores || !cq || !cd || rows == 0 || rows % 4 != 0 || rows > (1u << 24) ||
-      grid == 0 || grid > 65536 || window > 4096u || longest > rows)
+      grid == 0 || grid > 65536 || window > 4096u)
     return kInvalid;
-  return code(eg2::launch_attention_context(qkv, items, item_count, (int)grid, (int)window, (int)rows, (int)longest,
-                                            scores, cq, cd, as_stream(stream)));
+  return code(eg2::launch_attention_context(qkv, items, item_count, (int)grid, (int)window, (int)rows, scores, cq, cd,
+                                            as_stream(stream)));
 }
 
 int eg2_hip_attention_static(const float* qkv, const uint32_t* offsets, unsigned batch, unsigned window,

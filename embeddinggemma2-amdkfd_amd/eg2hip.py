@@ -114,7 +114,7 @@ SIGNATURES = {
     "eg2_hip_attention_static": (C.c_int, [_vp, _vp, _u, _u, _u, _vp, _vp, _vp]),
     "eg2_hip_attention_scores": (C.c_int, [_vp, _vp, _vp, _u, _u, _u, _vp, _vp]),
     "eg2_hip_attention_softmax": (C.c_int, [_vp, _u, _u, _u, _vp, _vp]),
-    "eg2_hip_attention_context": (C.c_int, [_vp, _vp, _vp, _u, _u, _u, _u, _vp, _vp, _vp, _vp]),
+    "eg2_hip_attention_context": (C.c_int, [_vp, _vp, _vp, _u, _u, _u, _vp, _vp, _vp, _vp]),
     "eg2_attention_plan": (C.c_int, [C.POINTER(C.c_size_t), C.c_size_t, C.c_size_t, C.c_size_t, _vp, _vp,
                                      C.POINTER(C.c_size_t)]),
     "eg2_attention_capacity": (None, [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -651,7 +651,7 @@ class ops:
                                              cls._stream())
         elif stage == "context":
             rc = L.eg2_hip_attention_context(cls._p(qkv), cls._p(plan.items), cls._p(plan.count), plan.GRID, window,
-                                             qkv.shape[0], longest, cls._p(plan.scores), cls._p(cq), cls._p(cd),
+                                             qkv.shape[0], cls._p(plan.scores), cls._p(cq), cls._p(cd),
                                              cls._stream())
         else:
             raise ValueError(stage)

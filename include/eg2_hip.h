@@ -93,8 +93,8 @@ int eg2_hip_attention_scores(const float *qkv, const uint32_t *items, const uint
 int eg2_hip_attention_softmax(const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores,
                               void *stream);
 int eg2_hip_attention_context(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
-                              unsigned window, unsigned rows, unsigned longest, const float *scores, int8_t *cq,
-                              float *cd, void *stream);
+                              unsigned window, unsigned rows, const float *scores, int8_t *cq, float *cd,
+                              void *stream);
 
 /* eg2_hip_attention without allocation. It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
@@ -118,8 +118,11 @@ int eg2_hip_attention_static(const float *qkv, const uint32_t *offsets, unsigned
 /* Host: the plan of eg2_hip_attention for the sequences [offsets[s],
  * offsets[s+1]) (rows = offsets[batch]): the score items of every
  * sequence (per sequence of n tokens, ceil(n/32) key blocks x ceil(3n/32)
- * pair blocks), then its context items (ceil(3n/32) pair blocks), 8
- * uint32 each as eg2_hip_attention reads them, and one token record per
+ * pair blocks), then its context items (ceil(3n/32) pair blocks; their
+ * sixth word is 1 when the context kernel should take its units in
+ * per-XCD contiguous eighths, which the plan decides from the packing's
+ * balance, else 0), 8 uint32 each as eg2_hip_attention reads them, and
+ * one token record per
  * token (4 uint32: sequence start, end, first score index, 0) at tok[4 t].
  * counts[0] = items of both kinds, counts[1] = score floats (ceil4(3 rows)
  * for the 1/sum values, then 3 n ceil4(n) per sequence), counts[2] = score

@@ -91,8 +91,8 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_attention_softmax(None, 0, 32, 0, p, None) == inval
     assert lib.eg2_hip_attention_softmax(p, 0, 32, 33, p, None) == inval  # longest > rows
     assert lib.eg2_hip_attention_softmax(p, 99999, 32, 0, p, None) == inval  # window
-    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 32, 0, p, None, p, None) == inval
-    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 32, 33, p, p, p, None) == inval  # longest > rows
+    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 32, p, None, p, None) == inval
+    assert lib.eg2_hip_attention_context(p, p, p, 64, 0, 30, p, p, p, None) == inval  # rows % 4
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, None, 4, None) == inval
     assert lib.eg2_hip_qk_norm_rope(p, p, p, p, p, f, p, 0, None) == inval
     assert lib.eg2_hip_libm_eval(p, 0, p, p, None) == inval
@@ -132,7 +132,7 @@ def test_attention_plan_covers_each_sequence(eg2):
             covered[s][p0:p1, k0 - lo:min(hi, k0 + 32) - lo] += 1
         else:
             p0, p1, sb = f2, f3, f4
-            assert sb == base[s] and f5 == f6 == f7 == 0
+            assert sb == base[s] and f5 == items[n_score][5] and f6 == f7 == 0
             assert p0 % 32 == 0 and p1 == min(3 * n, p0 + 32)
             ctx[s][p0:p1] += 1
     for s in covered:
@@ -140,6 +140,26 @@ def test_attention_plan_covers_each_sequence(eg2):
         assert (ctx[s] == 1).all(), s
     for s, (lo, hi) in enumerate(seqs):
         assert (tok[lo:hi] == [lo, hi, base[s], 0]).all()
+
+
+def test_attention_plan_context_order_follows_balance(eg2):
+    """The context items carry the context kernel's unit order: XCD-contiguous
+    eighths (1) for packings whose eighths of units cost alike (equal
+    sequences, the 16 x 128 wave, also with a short padding sequence after
+    it), the plain stride (0) for mixed ones, whose contiguous eighths would
+    give some XCDs all the long sequences."""
+    def flag(offs):
+        items, _, _, n_score = eg2.attention_plan(offs)
+        f = set(items[n_score:, 5].tolist())
+        assert len(f) == 1
+        return f.pop()
+
+    assert flag(list(range(0, 2049, 128))) == 1
+    assert flag(list(range(0, 2049, 512))) == 1
+    assert flag(list(range(0, 1601, 100)) + [1632]) == 1
+    assert flag([0, 105, 128, 137, 145, 364, 695, 788, 943, 1014, 1377, 1598, 1606, 1869, 1878, 2033, 2048]) == 0
+    assert flag([0, 2048]) == 1
+    assert flag([0, 1]) == 0  # 4 units: fewer than the XCDs
 
 
 def test_attention_plan_checks_capacity_before_writing(eg2):
