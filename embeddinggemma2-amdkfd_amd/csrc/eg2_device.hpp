@@ -32,6 +32,28 @@ __host__ __device__ inline size_t q8_tile_offset(size_t r, unsigned e, unsigned 
   return (((r >> 5) * nb + (e >> 5)) * 2 + ((e >> 4) & 1)) * 512 + (r & 31) * 16 + (e & 15);
 }
 
+// LDS DMA from a wave-uniform global base (SGPR pair) plus a per-lane byte
+// offset, 16 or 4 bytes per lane, to the wave-uniform LDS address `lds`
+// (+16 or +4 bytes per lane), which the instruction takes from M0. Written
+// as asm, not as __builtin_amdgcn_global_load_lds: with this compiler (ROCm
+// 7.2 clang) the builtin's write to LDS is invisible to the optimizer, which
+// then folded away a later read of the same LDS words in a test kernel.
+// The asm declares M0 clobbered (the compiler warns that M0 is reserved):
+// nothing in the kernels that call these uses M0 otherwise (their LDS
+// accesses are plain ds_read/ds_write and ds_bpermute, which need no M0 on
+// gfx950), so the value this code leaves there is never read by
+// compiler-generated code; a test compiles them and checks the ISA. A
+// kernel that adds an M0 user (s_movrels, LDS-direct, GWS) must not call
+// these. The DMA is not tracked by the compiler: callers wait for it with
+// s_waitcnt vmcnt and a barrier of their own before reading the LDS.
+__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+
 // Four int8 values (low byte of each) in one little-endian word.
 __device__ __forceinline__ uint32_t pack_i8x4(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |

@@ -57,12 +57,13 @@
 //    read the LDS instead of global memory.
 //  - attention_context_kernel: work items of (sequence, 32 pairs), each
 //    taken by 4 workgroups of 64 dimensions (768 workgroups for a wave of
-//    16 x 128 tokens or for one 2048-token sequence: three per CU). Per
-//    64-key chunk the workgroup stages w = p * (1/sum) for its pairs (0 for
-//    keys outside a pair's window, which adds +0 and changes no sum) and the
-//    chunk's v values in LDS (a chunk inside every pair's window, the usual
-//    case, skips those bounds and the zero fill of rows past the sequence:
-//    about 56 fewer VALU instructions per chunk and wave); per 2 keys each
+//    16 x 128 tokens or for one 2048-token sequence). Per 64-key chunk the
+//    workgroup stages w = p * (1/sum) for its pairs through registers (0
+//    for keys outside a pair's window, which adds +0 and changes no sum; a
+//    chunk inside every pair's window, the usual case, skips those bounds)
+//    and the chunk's v rows by LDS DMA into one of two buffers, the next
+//    chunk's while the current one is computed (128 VGPRs and 40 KB of LDS:
+//    four workgroups per CU); per 2 keys each
 //    wave issues one 4-block MFMA (block b = pairs 16 (b % 2) .. + 15 of key
 //    b / 2, columns = its 16 dimensions) and adds the products to its 8
 //    accumulators, in key order. The Q8_0 epilogue quantizes 32-value
@@ -89,7 +90,7 @@ constexpr int kSDims = 128;               // dimensions staged at a time
 constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apart
 constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
-constexpr int kCPitchW = kCPairs + 4, kCPitchV = kCDims + 4;
+constexpr int kCPitchV = kCDims + 4;       // floats per row of the context's epilogue tile
 constexpr int kShortSoftmax = 512;        // longest sequence for the 16-pair one-kernel softmax
 constexpr int kCBatch = 4;                // context MFMAs in flight per wave
 constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
@@ -582,10 +583,9 @@ __global__ void __launch_bounds__(256)
 attention_context_kernel(const float* __restrict__ qkv, const float* __restrict__ scores,
                          const uint4* __restrict__ items, const uint32_t* __restrict__ item_count, int window,
                          int rows, int8_t* __restrict__ cq, float* __restrict__ cd) {
-  __shared__ __align__(16) float wl[kCKeys * kCPitchW];  // [key][pair]: w = p * (1/sum), 0 outside the window
-  __shared__ __align__(16) float vl[kCKeys * kCPitchV];  // [key][dimension]
-  __shared__ uint32_t range[kCPairs][2];                  // each pair's key range
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ __align__(16) float wl[kCKeys * kCPairs];      // [key][pair]: w = p * (1/sum), 0 outside the window
+  __shared__ __align__(16) float vl[2][kCKeys * kCDims];    // [key][dimension], two chunks, filled by DMA
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r16 = lane & 15;
   const uint4* citems = items + 2 * (size_t)item_count[0];  // the context items follow the score items
   // XCD-aware order as in the scores kernel when the plan asks for it (the
@@ -597,6 +597,7 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
   const bool by_xcd = total > 0 && citems[1].y == 1u && gridDim.x % kXcdCount == 0;
   const uint32_t count = by_xcd ? total * (xcd + 1) / kXcdCount : total;
   const uint32_t stride = by_xcd ? gridDim.x / kXcdCount : gridDim.x;
+  const unsigned vl0 = (unsigned)(uintptr_t)&vl[0][0];  // LDS byte address of the v chunks
   const floatx16 zero = {};
   for (uint32_t work = by_xcd ? total * xcd / kXcdCount + blockIdx.x / kXcdCount : blockIdx.x; work < count;
        work += stride) {
@@ -607,70 +608,67 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     const size_t sbase = b.x;
     const uint32_t pitch = score_pitch(len);
     const int dblk = (int)(work & 3) * kCDims;  // the workgroup's 64 dimensions of each head
-    __syncthreads();  // the previous item's ranges and tile are no longer read
-    if (tid < kCPairs) {
-      const uint32_t pair = min(pair0 + (uint32_t)tid, pair1 - 1);
-      uint32_t first, last;
-      key_range(lo + pair / 3, lo, hi, window, first, last);
-      range[tid][0] = first;
-      range[tid][1] = last;
-    }
-    __syncthreads();
-    // Keys the tile's pairs need (ranges grow with the token), from a
-    // multiple of 4 past lo so that the float4 reads of the rows align.
-    const uint32_t kfirst = lo + ((range[0][0] - lo) & ~3u);
-    const uint32_t npairs = min(pair1 - pair0, (uint32_t)kCPairs);
-    const uint32_t klast = range[npairs - 1][1];
-    // A chunk inside every pair's window (from the last pair's first key to
-    // the first pair's last key) needs no bound on its keys: its p and v
-    // rows all lie inside the sequence and every w is p * (1/sum).
-    const uint32_t in_first = __builtin_amdgcn_readfirstlane(range[npairs - 1][0]);
-    const uint32_t in_last = __builtin_amdgcn_readfirstlane(range[0][1]);
+    // Key ranges (ranges grow with the token): the keys the item needs, from
+    // a multiple of 4 past lo so that the float4 reads of the p rows align,
+    // to the last pair's last key; a chunk inside every pair's window (from
+    // the last pair's first key to the first pair's last key) needs no
+    // bound on its keys: its p rows lie inside the sequence and every w is
+    // p * (1/sum).
+    uint32_t f0, l0, fl, ll;
+    key_range(lo + pair0 / 3, lo, hi, window, f0, l0);
+    key_range(lo + (pair1 - 1) / 3, lo, hi, window, fl, ll);
+    const uint32_t kfirst = lo + ((f0 - lo) & ~3u), klast = ll, in_first = fl, in_last = l0;
     auto inside = [&](uint32_t c0) { return c0 >= in_first && c0 + kCKeys <= in_last; };
     float acc[8];  // pairs 16 (v / 4) + 4 g + v % 4, dimension dblk + 16 w + r16
 #pragma unroll
     for (int v = 0; v < 8; ++v) acc[v] = 0.0f;
-    // Staging roles: w by (pair = tid % 32, the 8 keys 8 (tid / 32) ..);
-    // v by (key = tid / 4, 16 dimensions of quarter tid % 4).
+    // w staging: thread (pair tid % 32, the 8 keys 8 (tid / 32) ..), from
+    // registers loaded while the previous chunk is computed.
     const uint32_t wp = (uint32_t)tid & (kCPairs - 1), wk = 8 * ((uint32_t)tid / kCPairs);
     const uint32_t wpair = min(pair0 + wp, pair1 - 1);
     const float winv = scores[3 * (size_t)(lo + wpair / 3) + wpair % 3];
     const float* wsrc = scores + sbase + (size_t)wpair * pitch;
-    const uint32_t wfirst = range[wp][0], wlast = pair0 + wp < pair1 ? range[wp][1] : wfirst;
-    const uint32_t vk = (uint32_t)tid >> 2, vq = 16 * (tid & 3);
-    // A chunk's staging values (this thread's 8 p values and 16 v values)
-    // are loaded while the previous chunk is computed.
-    float4 pw[2], pv[4];
-    auto load_chunk = [&](uint32_t c0) {
-      const uint32_t kt = c0 + vk;
-      if (inside(c0)) {
-#pragma unroll
-        for (int j4 = 0; j4 < 2; ++j4)
-          pw[j4] = *reinterpret_cast<const float4*>(wsrc + (c0 + wk + 4 * j4 - lo));
-        const float* src = qkv + (size_t)kt * kLd + kVOff + dblk + vq;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pv[j] = *reinterpret_cast<const float4*>(src + 4 * j);
-        return;
-      }
+    uint32_t wfirst, wlast;
+    key_range(lo + wpair / 3, lo, hi, window, wfirst, wlast);
+    if (pair0 + wp >= pair1) wlast = wfirst;  // no such pair: w = 0
+    float4 pw[2];
+    auto load_w = [&](uint32_t c0) {
 #pragma unroll
       for (int j4 = 0; j4 < 2; ++j4) {
         const uint32_t k4 = c0 + wk + 4 * j4;  // 4 keys, 16-byte aligned in the row
-        pw[j4] = k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pw[j4] = inside(c0) || k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo))
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
-      const float* src = qkv + (size_t)min(kt, hi - 1) * kLd + kVOff + dblk + vq;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        pv[j] = kt < hi ? *reinterpret_cast<const float4*>(src + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
-    if (kfirst < klast) load_chunk(kfirst);
-    for (uint32_t c0 = kfirst; c0 < klast; c0 += kCKeys) {
-      __syncthreads();  // the previous chunk is no longer read
+    // v staging by DMA, no registers: wave w moves keys c0 + 16 w .. + 15 of
+    // the chunk, 4 keys (64 lanes x 16 bytes) per instruction. Keys past the
+    // sequence read its last row: every pair's w is 0 there (a finite v
+    // times +0 adds +0 or -0, which changes no sum).
+    auto issue_v = [&](uint32_t c0, int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t row = min(c0 + 16 * (uint32_t)w + 4 * i + (uint32_t)(lane >> 4), hi - 1);
+        dma16(qkv, (row * kLd + kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
+              vl0 + (unsigned)buf * (kCKeys * kCDims * 4) + (16 * w + 4 * i) * (kCDims * 4));
+      }
+    };
+    __syncthreads();  // the previous item's epilogue tile (in vl[0]) is no longer read
+    if (kfirst < klast) {
+      issue_v(kfirst, 0);
+      load_w(kfirst);
+    }
+    int buf = 0;
+    for (uint32_t c0 = kfirst; c0 < klast; c0 += kCKeys, buf ^= 1) {
+      // This wave's v DMA and w loads of the chunk have landed; after the
+      // barrier every wave's have, and the previous chunk is no longer read.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
       if (inside(c0)) {
 #pragma unroll
         for (int j4 = 0; j4 < 2; ++j4) {
           const float pr[4] = {pw[j4].x, pw[j4].y, pw[j4].z, pw[j4].w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) wl[(wk + 4 * j4 + e) * kCPitchW + wp] = pr[e] * winv;
+          for (int e = 0; e < 4; ++e) wl[(wk + 4 * j4 + e) * kCPairs + wp] = pr[e] * winv;
         }
       } else {
 #pragma unroll
@@ -680,30 +678,28 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
           for (int e = 0; e < 4; ++e) {
             const uint32_t kt = c0 + wk + 4 * j4 + e;
             const float wv = pr[e] * winv;
-            wl[(wk + 4 * j4 + e) * kCPitchW + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
+            wl[(wk + 4 * j4 + e) * kCPairs + wp] = kt >= wfirst && kt < wlast ? wv : 0.0f;
           }
         }
       }
-      {
-        float* dst = vl + vk * kCPitchV + vq;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(dst + 4 * j) = pv[j];
-      }
       __syncthreads();
-      if (c0 + kCKeys < klast) load_chunk(c0 + kCKeys);
+      if (c0 + kCKeys < klast) {
+        issue_v(c0 + kCKeys, buf ^ 1);
+        load_w(c0 + kCKeys);
+      }
       // Keys in groups of 8 (keys past klast carry w = 0 for every pair and
       // add +0): per 2 keys one MFMA whose block b holds pairs 16 (b % 2) ..
       // + 15 (rows) x the wave's 16 dimensions for key 2 i + b / 2; the
-      // group's 4 MFMAs into separate registers, the next group's operands
+      // group's MFMAs into separate registers, the next group's operands
       // read from LDS, then the adds in key order.
       const int n8 = (int)((min((uint32_t)kCKeys, klast - c0) + 7) & ~7u);
-      const float* wa = wl + (g >> 1) * kCPitchW + 16 * (g & 1) + r16;
-      const float* vb = vl + (g >> 1) * kCPitchV + 16 * w + r16;
+      const float* wa = wl + (g >> 1) * kCPairs + 16 * (g & 1) + r16;
+      const float* vb = vl[buf] + (g >> 1) * kCDims + 16 * w + r16;
       float an[4], bn[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        an[e] = wa[2 * e * kCPitchW];
-        bn[e] = vb[2 * e * kCPitchV];
+        an[e] = wa[2 * e * kCPairs];
+        bn[e] = vb[2 * e * kCDims];
       }
       for (int j = 0; j < n8; j += 8) {
 #pragma unroll
@@ -715,8 +711,8 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
           if (e0 + kCBatch == 4 && j + 8 < n8) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              an[e] = wa[(j + 8 + 2 * e) * kCPitchW];
-              bn[e] = vb[(j + 8 + 2 * e) * kCPitchV];
+              an[e] = wa[(j + 8 + 2 * e) * kCPairs];
+              bn[e] = vb[(j + 8 + 2 * e) * kCDims];
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -730,10 +726,10 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
         }
       }
     }
-    // Through LDS to [pair][64 dimensions], then Q8_0: block (32 values) of
-    // 4 lanes x 8 values.
+    // Through LDS (the first v chunk's space) to [pair][64 dimensions], then
+    // Q8_0: block (32 values) of 4 lanes x 8 values.
     __syncthreads();
-    float* tile = wl;  // kCPairs x kCPitchV floats
+    float* tile = vl[0];  // kCPairs x kCPitchV floats
 #pragma unroll
     for (int v = 0; v < 8; ++v) tile[(16 * (v >> 2) + 4 * g + (v & 3)) * kCPitchV + 16 * w + r16] = acc[v];
     __syncthreads();

@@ -57,25 +57,6 @@ constexpr int kMagicBits = 0x4B400000;
 
 extern __shared__ __align__(16) unsigned char gemm_lds[];
 
-// LDS DMA from a wave-uniform global base (SGPR pair) plus a per-lane byte
-// offset, 16 or 4 bytes per lane, to the wave-uniform LDS address `lds`
-// (+16 or +4 bytes per lane), which the instruction takes from M0. Written
-// as asm, not as __builtin_amdgcn_global_load_lds: with this compiler (ROCm
-// 7.2 clang) the builtin's write to LDS is invisible to the optimizer, which
-// then folded away a later read of the same LDS words in a test kernel.
-// The asm declares M0 clobbered (the compiler warns that M0 is reserved):
-// nothing in these GEMM kernels uses M0 otherwise (their LDS accesses are
-// plain ds_read/ds_write, which need no M0 on gfx950), so the value this
-// code leaves there is never read by compiler-generated code. A kernel that
-// adds an M0 user (s_movrels, LDS-direct, GWS) must not call these.
-__device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-
 // Waits until at most N vector-memory operations of this wave are in flight
 // and its LDS reads are done, then joins the workgroup barrier. The ring is
 // filled by DMA, which the compiler does not track, so the wait is

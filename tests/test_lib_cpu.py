@@ -505,12 +505,13 @@ def test_code_object_exports_the_operator_kernels(eg2):
         assert name in syms and name + ".kd" in syms, name
 
 
-def test_gemm_dma_is_the_only_m0_user(tmp_path):
-    """The GEMM kernels set M0 in inline asm for their LDS DMA and declare it
-    clobbered; that is sound only while no compiler-generated instruction
-    in those kernels reads M0. Compiles kernels_gemm.hip for gfx950 with the
-    library's flags and checks that every mention of m0 in the ISA is the
-    asm's own write (a compiler update or a new M0 user fails here)."""
+@pytest.mark.parametrize("source", ["kernels_gemm.hip", "kernels_attn.hip"])
+def test_dma_is_the_only_m0_user(tmp_path, source):
+    """The GEMM and attention kernels set M0 in inline asm for their LDS DMA
+    and declare it clobbered; that is sound only while no compiler-generated
+    instruction in those kernels reads M0. Compiles the source for gfx950
+    with the library's flags and checks that every mention of m0 in the ISA
+    is the asm's own write (a compiler update or a new M0 user fails here)."""
     import shutil
     import subprocess
 
@@ -523,7 +524,7 @@ def test_gemm_dma_is_the_only_m0_user(tmp_path):
     cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
            "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            "-mllvm", "-amdgpu-mfma-vgpr-form", "-I" + os.path.join(root, "include"), "-I" + os.path.join(pkg, "csrc"),
-           "--cuda-device-only", "-S", os.path.join(pkg, "csrc", "kernels_gemm.hip"), "-o", str(out)]
+           "--cuda-device-only", "-S", os.path.join(pkg, "csrc", source), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     writes = others = 0
     for line in out.read_text().splitlines():
