@@ -34,15 +34,17 @@
 //    listed pair block by pair block (an XCD's contiguous share of a long
 //    sequence then needs a band of q rows and the k rows, which fit its L2).
 //    The workgroup stages the q rows of its pairs and the k rows of its
-//    keys in LDS, 128 dimensions at a time, reordered so that chain c's
-//    values (dimensions c, c + 4, ...) are contiguous. Each wave owns 16
-//    pairs x 16 keys; per 4 dimensions one 4-block MFMA whose block c
-//    multiplies chain c (lane group c feeds chain c's q and k values), and
-//    each lane adds its 16 products to its 4 pairs' 4 chain sums. The
-//    scores go to a scratch row per pair (row length rounded up to 4). A
-//    workgroup takes items in turn (the workgroups of an XCD, a contiguous
-//    eighth of the list) and loads the next item's first half while its
-//    current item's second half computes.
+//    keys in LDS by 16-byte DMA (no registers), 64 dimensions at a time,
+//    laid out [16-row block][4-dimension chunk][row] so that the lane of
+//    chain c and row r reads chunk s's element c with a 4-byte read and
+//    the wave's 64 lanes hit 64 distinct banks. Each wave owns 16 pairs x
+//    16 keys; per 4 dimensions one 4-block MFMA whose block c multiplies
+//    chain c (lane group c feeds chain c's q and k values), and each lane
+//    adds its 16 products to its 4 pairs' 4 chain sums. The scores go to a
+//    scratch row per pair (row length rounded up to 4). A workgroup takes
+//    items in turn (the workgroups of an XCD, a contiguous eighth of the
+//    list) and stages the next quarter (the next item's first during the
+//    current item's last) while the current one computes.
 //  - attention_exp_kernel: one wave per (token, head): the row maximum,
 //    then every lane's expf of its keys, written back over the scores.
 //  - attention_sum_kernel: one lane per (token, head): the sum of its p
@@ -86,8 +88,6 @@ constexpr int kLd = kQKVCols;  // floats per operand row [q0 q1 q2 | k | v]
 constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 
 constexpr int kSKeys = 32, kSPairs = 32;  // scores workgroup tile
-constexpr int kSDims = 128;               // dimensions staged at a time
-constexpr int kSPitch = kSDims + 4;       // floats per staged row: 4 banks apart
 constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchV = kCDims + 4;       // floats per row of the context's epilogue tile
@@ -120,65 +120,50 @@ __host__ __device__ inline void key_range(uint32_t t, uint32_t lo, uint32_t hi, 
 
 // ----------------------------------------------------------------- scores
 
-// 16 values of dimensions d0 .. d0 + 15 (d0 = 128 part + 16 grp), loaded,
-// then stored to the chain-major staged row: chain c's values (d0 + c,
-// d0 + 4 + c, ...) at [32 c + 4 grp .. 32 c + 4 grp + 3].
-struct Stage16 {
-  float4 a, b, c, d;
-};
-__device__ __forceinline__ Stage16 load16(const float* __restrict__ src) {
-  return {*reinterpret_cast<const float4*>(src), *reinterpret_cast<const float4*>(src + 4),
-          *reinterpret_cast<const float4*>(src + 8), *reinterpret_cast<const float4*>(src + 12)};
-}
-// An empty asm statement that takes and returns the 16 values: code after
-// it cannot use them before it, so a load's wait lands there.
-__device__ __forceinline__ void hold(Stage16& v) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 a = __builtin_bit_cast(f4, v.a), b = __builtin_bit_cast(f4, v.b), c = __builtin_bit_cast(f4, v.c),
-     d = __builtin_bit_cast(f4, v.d);
-  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-  v = {__builtin_bit_cast(float4, a), __builtin_bit_cast(float4, b), __builtin_bit_cast(float4, c),
-       __builtin_bit_cast(float4, d)};
-}
-__device__ __forceinline__ void store16(const Stage16& v, float* row, int grp) {
-  *reinterpret_cast<float4*>(row + 0 * 32 + 4 * grp) = make_float4(v.a.x, v.b.x, v.c.x, v.d.x);
-  *reinterpret_cast<float4*>(row + 1 * 32 + 4 * grp) = make_float4(v.a.y, v.b.y, v.c.y, v.d.y);
-  *reinterpret_cast<float4*>(row + 2 * 32 + 4 * grp) = make_float4(v.a.z, v.b.z, v.c.z, v.d.z);
-  *reinterpret_cast<float4*>(row + 3 * 32 + 4 * grp) = make_float4(v.a.w, v.b.w, v.c.w, v.d.w);
-}
+// The scores' staging: per item, four quarters of 64 dimensions, each a
+// plain copy by 16-byte LDS DMA into blocks of 16 rows (block 0, 1: the q
+// rows of pairs pair0 .. + 15, + 16 .. + 31; block 2, 3: the k rows of keys
+// key0 .. + 15, + 16 .. + 31), laid out [block][chunk][row] with a chunk =
+// 4 dimensions (all four chains at one step). A lane of chain g and row
+// r16 reads its step-s value with one 4-byte read at chunk s, row r16,
+// element g: the wave's 64 lanes touch 64 distinct banks.
+constexpr int kSQDims = 64;
+constexpr int kSQChunks = kSQDims / 4;
+constexpr int kSBlockFloats = kSQChunks * 16 * 4;  // one block of 16 rows
 
-// One staged half (kSDims dimensions) of the wave's 16 pairs x 16 keys:
-// per kSBatch steps that many MFMAs into separate registers, then their
-// adds, with the next 4 steps' operands read from LDS before the adds. Two
-// in flight, not four: the kernel then holds 112 VGPRs instead of 148, four
-// waves per SIMD instead of three, whose MFMAs and adds interleave (one
-// 2048-token sequence 148 -> 138 us, a mixed packing 64 -> 55 us).
+// One staged quarter of the wave's 16 pairs x 16 keys: per kSBatch steps
+// that many MFMAs into separate registers, then their adds, with the next
+// steps' operands read from LDS before the adds.
 constexpr int kSBatch = 2;
-__device__ __forceinline__ void scores_half(const float* qa, const float* kb, float (&acc)[4][4]) {
+__device__ __forceinline__ void scores_quarter(const float* qa, const float* kb, float (&acc)[4][4]) {
   const floatx16 zero = {};
-  float4 q4 = *reinterpret_cast<const float4*>(qa), k4 = *reinterpret_cast<const float4*>(kb);
+  float qv[kSBatch], kv[kSBatch];
 #pragma unroll
-  for (int s = 0; s < kSDims / 4; s += 4) {
-    const float qv[4] = {q4.x, q4.y, q4.z, q4.w}, kv[4] = {k4.x, k4.y, k4.z, k4.w};
+  for (int e = 0; e < kSBatch; ++e) {
+    qv[e] = qa[64 * e];
+    kv[e] = kb[64 * e];
+  }
 #pragma unroll
-    for (int e0 = 0; e0 < 4; e0 += kSBatch) {
-      floatx16 prod[kSBatch];
+  for (int s = 0; s < kSQChunks; s += kSBatch) {
+    floatx16 prod[kSBatch];
 #pragma unroll
-      for (int e = 0; e < kSBatch; ++e)  // block c: chain c; rows = pairs 4 g' + r, columns = keys
-        prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e0 + e], kv[e0 + e], zero, 0, 0, 0);
-      if (e0 + kSBatch == 4 && s + 4 < kSDims / 4) {
-        q4 = *reinterpret_cast<const float4*>(qa + s + 4);
-        k4 = *reinterpret_cast<const float4*>(kb + s + 4);
+    for (int e = 0; e < kSBatch; ++e)  // block c: chain c; rows = pairs, columns = keys
+      prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(qv[e], kv[e], zero, 0, 0, 0);
+    if (s + kSBatch < kSQChunks) {
+#pragma unroll
+      for (int e = 0; e < kSBatch; ++e) {
+        qv[e] = qa[64 * (s + kSBatch + e)];
+        kv[e] = kb[64 * (s + kSBatch + e)];
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int e = 0; e < kSBatch; ++e)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < kSBatch; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[c][r] = acc[c][r] + prod[e][4 * c + r];
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -228,12 +213,17 @@ __device__ __forceinline__ ScoreTile score_tile(const uint4* __restrict__ items,
   return t;
 }
 
-// Offsets in qkv of staging row srow's pair row and key row of tile t
-// (clamped; the rows past the tile's end are computed and not stored).
-__device__ __forceinline__ void score_sources(const ScoreTile& t, int srow, size_t& qoff, size_t& koff) {
-  const uint32_t spair = min(t.pair0 + (uint32_t)srow, t.pair1 - 1), skey = min(t.key0 + (uint32_t)srow, t.hi - 1);
-  qoff = (size_t)(t.lo + spair / 3) * kLd + (spair % 3) * kHeadDim;
-  koff = (size_t)skey * kLd + kKOff;
+// Float offset of staging row r of tile t from the sequence's first row
+// (r < 32: the q row of pair pair0 + r, else the k row of key key0 + r -
+// 32), clamped (the rows past the tile's end are computed and not stored).
+// Relative to the sequence, so that the DMA's 32-bit byte offsets hold for
+// any row count (a planned sequence is below 37,838 rows: 194 MB of qkv).
+__device__ __forceinline__ uint32_t stage_row(const ScoreTile& t, uint32_t r) {
+  if (r < (uint32_t)kSPairs) {
+    const uint32_t spair = min(t.pair0 + r, t.pair1 - 1);
+    return spair / 3 * kLd + (spair % 3) * kHeadDim;
+  }
+  return (min(t.key0 + r - kSPairs, t.hi - 1) - t.lo) * kLd + kKOff;
 }
 
 // The first item from `item` on (stride `stride`) below `count` that has
@@ -247,19 +237,17 @@ __device__ __forceinline__ uint32_t next_score_item(const uint4* __restrict__ it
   return item;
 }
 
-// The workgroup takes items in turn (grid-stride); each half's values are
-// loaded while the previous half computes: the second half's during the
-// first, the next item's first half during the second.
+// The workgroup takes items in turn (grid-stride); each quarter's rows are
+// staged by DMA into one of two LDS buffers while the previous quarter
+// computes (the next item's first quarter during the current item's last).
 __global__ void __launch_bounds__(256)
 attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__ items,
                                  const uint32_t* __restrict__ item_count, int window, int rows,
                                  float* __restrict__ scores) {
-  __shared__ __align__(16) float qs[kSPairs * kSPitch];
-  __shared__ __align__(16) float ks[kSKeys * kSPitch];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ __align__(16) float stg[2][4 * kSBlockFloats];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r16 = lane & 15;
   const int pr = 16 * (w >> 1), kr = 16 * (w & 1);
-  const int srow = tid >> 3, grp = tid & 7;
   // XCD-aware order (a grid that is a multiple of 8): workgroup b runs on
   // XCD b % 8, which takes the contiguous eighth of the item list, so an
   // XCD's L2 holds the rows of few sequences; any other grid strides over
@@ -268,16 +256,29 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
   const uint32_t total = item_count[0], xcd = blockIdx.x % kXcdCount;
   const uint32_t count = by_xcd ? total * (xcd + 1) / kXcdCount : total;
   const uint32_t stride = by_xcd ? gridDim.x / kXcdCount : gridDim.x;
+  const unsigned stg0 = (unsigned)(uintptr_t)&stg[0][0];
+  // Wave w stages block w: per instruction 4 chunks of its 16 rows, lane L
+  // row L % 16, chunk 4 j + L / 16, i.e. LDS position 64 j + L of the block.
+  const float* seq = qkv;
+  uint32_t roff = 0;  // the lane's row, in bytes from the sequence's first row
+  auto locate = [&](const ScoreTile& t) {
+    seq = qkv + (size_t)t.lo * kLd;
+    roff = 4 * stage_row(t, 16 * (uint32_t)w + (uint32_t)r16) + 16 * (uint32_t)g;
+  };
+  auto issue = [&](int q, int buf) {
+#pragma unroll
+    for (int j = 0; j < kSQChunks / 4; ++j)
+      dma16(seq, roff + 4 * (uint32_t)(kSQDims * q + 16 * j),
+            stg0 + (unsigned)((buf * 4 + w) * kSBlockFloats + 256 * j) * 4u);
+  };
   ScoreTile t;
   uint32_t item = next_score_item(items, by_xcd ? total * xcd / kXcdCount + blockIdx.x / kXcdCount : blockIdx.x,
                                   count, stride, window, rows, t);
-  size_t qoff = 0, koff = 0;
-  Stage16 qn, kn;
   if (item < count) {
-    score_sources(t, srow, qoff, koff);
-    qn = load16(qkv + qoff + 16 * grp);
-    kn = load16(qkv + koff + 16 * grp);
+    locate(t);
+    issue(0, 0);
   }
+  int buf = 0;
   while (item < count) {
     float acc[4][4];
 #pragma unroll
@@ -286,38 +287,28 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
       for (int r = 0; r < 4; ++r) acc[c][r] = 0.0f;
     ScoreTile nt = t;
     uint32_t nitem = count;
-    size_t nqoff = qoff, nkoff = koff;
 #pragma unroll 1
-    for (int part = 0; part < kHeadDim / kSDims; ++part) {
-      __syncthreads();  // the previous half's (or item's) rows are no longer read
-      store16(qn, qs + srow * kSPitch, grp);
-      store16(kn, ks + srow * kSPitch, grp);
+    for (int q = 0; q < kHeadDim / kSQDims; ++q) {
+      // This wave's DMA of the quarter has landed; after the barrier every
+      // wave's has, and the other buffer is no longer read.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (part + 1 < kHeadDim / kSDims) {
-        qn = load16(qkv + qoff + (part + 1) * kSDims + 16 * grp);
-        kn = load16(qkv + koff + (part + 1) * kSDims + 16 * grp);
+      if (q + 1 < kHeadDim / kSQDims) {
+        issue(q + 1, buf ^ 1);
       } else {
         nitem = next_score_item(items, item + stride, count, stride, window, rows, nt);
         if (nitem < count) {
-          score_sources(nt, srow, nqoff, nkoff);
-          qn = load16(qkv + nqoff + 16 * grp);
-          kn = load16(qkv + nkoff + 16 * grp);
+          locate(nt);
+          issue(0, buf ^ 1);
         }
       }
-      scores_half(qs + (pr + r16) * kSPitch + 32 * g, ks + (kr + r16) * kSPitch + 32 * g, acc);
-      // The prefetched values are used (transposed into the staging order)
-      // only from here on: without this, the compiler builds the staging
-      // registers right after the loads, which waits for them before the
-      // half above computes.
-      __builtin_amdgcn_sched_barrier(0);
-      hold(qn);
-      hold(kn);
+      const float* base = stg[buf] + 4 * r16 + g;  // chunk s of row r16 at 64 s + 4 r16
+      scores_quarter(base + (w >> 1) * kSBlockFloats, base + (2 + (w & 1)) * kSBlockFloats, acc);
+      buf ^= 1;
     }
     store_scores(acc, t.lo, t.hi, t.key0, t.pair0, t.pair1, t.sbase, window, pr, kr, g, r16, scores);
     item = nitem;
     t = nt;
-    qoff = nqoff;
-    koff = nkoff;
   }
 }
 
@@ -643,12 +634,15 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     // v staging by DMA, no registers: wave w moves keys c0 + 16 w .. + 15 of
     // the chunk, 4 keys (64 lanes x 16 bytes) per instruction. Keys past the
     // sequence read its last row: every pair's w is 0 there (a finite v
-    // times +0 adds +0 or -0, which changes no sum).
+    // times +0 adds +0 or -0, which changes no sum). Byte offsets are taken
+    // from the sequence's first row, so that 32 bits hold them for any row
+    // count (a planned sequence is below 37,838 rows: 194 MB of qkv).
+    const float* seq = qkv + (size_t)lo * kLd;
     auto issue_v = [&](uint32_t c0, int buf) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t row = min(c0 + 16 * (uint32_t)w + 4 * i + (uint32_t)(lane >> 4), hi - 1);
-        dma16(qkv, (row * kLd + kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
+        const uint32_t row = min(c0 + 16 * (uint32_t)w + 4 * i + (uint32_t)(lane >> 4), hi - 1) - lo;
+        dma16(seq, (row * kLd + kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
               vl0 + (unsigned)buf * (kCKeys * kCDims * 4) + (16 * w + 4 * i) * (kCDims * 4));
       }
     };
