@@ -54,6 +54,14 @@ __device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned ld
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
 }
 
+// A raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor:
+// stride 0, word 3 = 0x00020000, 32-bit data format). Loads through it take
+// a per-lane offset and a scalar one, so a loop's advance costs no vector
+// registers; offsets at or past `bytes` read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // Four int8 values (low byte of each) in one little-endian word.
 __device__ __forceinline__ uint32_t pack_i8x4(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |

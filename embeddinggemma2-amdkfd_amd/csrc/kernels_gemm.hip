@@ -22,19 +22,23 @@
 // it, eg2_q8_weight_tiles writes weights): int8 [rows/32][k/32][2][32][16],
 // so each 32-row x 32-value block is 1 KB in the register order of the
 // MFMA operand (lane 32h + r holds row r, values 16h .. 16h + 15): one
-// 1 KB global_load_lds_dwordx4 moves it, one ds_read_b128 per lane reads
-// it. Block scales are stored transposed, [k/32][ld], one float per row.
+// 16-byte load per lane at 16 lane moves it into the operand registers
+// (gemm_q8_kernel), or one 1 KB global_load_lds_dwordx4 into LDS (the
+// Q|K|V kernel, whose eight waves share the activation block). Block
+// scales are stored transposed, [k/32][ld], one float per row.
 //
 // Work: a workgroup of 4 waves computes a 64 x 64 output tile, wave w the
-// 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Per block, the
-// four operand tiles and the 64 + 64 scales go by DMA into a 4-stage LDS
-// ring (each wave moves one tile and one scale vector), two blocks in
-// flight beyond the one being read. After each barrier the fragments of
-// block kb + 1 are requested from LDS, the two multiply phases of block
-// kb's scaling cover their latency, then the MFMA of block kb + 1 is
-// issued and block kb's adds follow. In the MFMA 32x32 output layout a lane
-// holds one column and 16 rows; each row's activation scale reaches it
-// through a DPP row broadcast folded into the multiply.
+// 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Each wave loads
+// its own activation and weight blocks and their scales straight into
+// registers by buffer loads, four blocks ahead, with no LDS and no barrier
+// (an LDS ring shared by the four waves, with a barrier per block, was no
+// faster: the loop is bound by each wave's instruction stream, 24 or 36
+// blocks of one MFMA and 48 VALU operations, not by its loads). Per block:
+// block kb's two multiply phases, the MFMA of block kb + 1, block kb's
+// adds, then the refill of kb's registers with block kb + 4. In the MFMA
+// 32x32 output layout a lane holds one column and 16 rows; each row's
+// activation scale reaches it through a DPP row broadcast folded into the
+// multiply.
 #include <algorithm>
 #include <utility>
 
@@ -48,7 +52,8 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kXcds = 8;     // MI355X: 8 XCDs of 32 CUs, each with its own L2
-constexpr int kStages = 4;   // LDS ring depth (even: see the loop below)
+constexpr int kStages = 4;   // LDS ring depth of the Q|K|V kernel (even: see its loop)
+constexpr int kDepth = 4;    // blocks in flight per wave in gemm_q8_kernel (6 and 8 measured no faster)
 constexpr int kTile = 1024;  // one 32 x 32 int8 operand block
 constexpr int kDxOff = 4 * kTile, kDwOff = kDxOff + 64 * 4;
 constexpr int kStageBytes = kDwOff + 64 * 4;  // A0 A1 B0 B1 | d_x[64] | d_w[64]
@@ -232,7 +237,7 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
                      gd + (size_t)tc * ldg + t);
 }
 
-// TAIL: nb % kStages != 0 (a separate instantiation: the tail code costs
+// TAIL: nb % kDepth != 0 (a separate instantiation: the tail code costs
 // registers, and every projection of the model has nb % 4 == 0). GEGLU:
 // the epilogue above replaces the fp32 store (y and ldy unused; m = 2 ff).
 template <bool TAIL, bool GEGLU>
@@ -253,100 +258,89 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   if (rows_here <= 0 || cols_here <= 0 || i >= rows_here * cols_here) return;
   const int tr = r0 + i % rows_here, tc = c0 + i / rows_here;
 
-  // DMA roles: wave w moves operand tile w of each block -- activation rows
-  // 64 tr + 32 w (w < 2) or weight rows 64 tc + 32 (w - 2), clamped to the
-  // last tile -- and one scale vector: the 64 activation scales (waves 0-1)
-  // or weight scales (waves 2-3), clamped to the last row. Each pair writes
-  // identical data, so every wave has the same loads in flight.
-  const int8_t* tbase;
-  const float* sbase;
-  unsigned soff;
-  int sld;
-  if (w < 2) {
-    tbase = xq + (size_t)min(2 * tr + w, (n + 31) / 32 - 1) * nb * kTile;
-    sbase = xd;
-    sld = ldx;
-    soff = 4u * (unsigned)min(64 * tr + lane, n - 1);
-  } else {
-    tbase = wq + (size_t)min(2 * tc + w - 2, (m + 31) / 32 - 1) * nb * kTile;
-    sbase = wd;
-    sld = ldw;
-    soff = 4u * (unsigned)min(64 * tc + lane, m - 1);
-  }
-  const unsigned lds0 = (unsigned)(uintptr_t)gemm_lds;
-  const unsigned t_lds = lds0 + kTile * w, s_lds = lds0 + (w < 2 ? kDxOff : kDwOff);
-  auto issue = [&](int slot, int kb) {
-    kb = min(kb, nb - 1);
-    dma16(tbase + (size_t)kb * kTile, 16u * lane, __builtin_amdgcn_readfirstlane(t_lds + slot * kStageBytes));
-    dma4(sbase + (size_t)kb * sld, soff, __builtin_amdgcn_readfirstlane(s_lds + slot * kStageBytes));
-  };
-
+  // Operands straight to registers: the row-tile layout is the MFMA's
+  // register order, so lane L's 16 bytes of a 1 KB block are one
+  // global_load_dwordx4 at 16 L. Wave (wr, wc) loads its own activation
+  // block (rows 64 tr + 32 wr, clamped to the last tile) and weight block
+  // (columns 64 tc + 32 wc), its row's activation scale and its column's
+  // weight scale (clamped to the last row / column), kDepth blocks ahead;
+  // no LDS and no barrier, so the four waves never wait for each other.
   const int wr = w >> 1, wc = w & 1, g = lane >> 5;
   // Row whose scale this lane supplies to the DPP broadcast: lane 16r + v
   // carries the scale of output register v for the lanes of 16-lane row r.
   const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
-  const unsigned char* a_p = gemm_lds + kTile * wr + 16 * lane;
-  const unsigned char* b_p = gemm_lds + 2 * kTile + kTile * wc + 16 * lane;
-  const unsigned char* dx_p = gemm_lds + kDxOff + 4 * (32 * wr + srow);
-  const unsigned char* dw_p = gemm_lds + kDwOff + 4 * (32 * wc + (lane & 31));
-  intx16 magic = (intx16)(kMagicBits);
-  asm volatile("" : "+v"(magic));  // one register copy, not rebuilt per MFMA
+  // Buffer loads: the per-block advance is a scalar offset, so no vector
+  // address is kept per block in flight.
+  const __amdgpu_buffer_rsrc_t ra =
+      buffer_rsrc(xq + (size_t)min(2 * tr + wr, (n + 31) / 32 - 1) * nb * kTile, (uint32_t)nb * kTile);
+  const __amdgpu_buffer_rsrc_t rb =
+      buffer_rsrc(wq + (size_t)min(2 * tc + wc, (m + 31) / 32 - 1) * nb * kTile, (uint32_t)nb * kTile);
+  const uint32_t xoff = 4u * (uint32_t)min(64 * tr + 32 * wr + srow, n - 1);
+  const uint32_t woff = 4u * (uint32_t)min(64 * tc + 32 * wc + (lane & 31), m - 1);
   struct Frag {
     intx4 a, b;
     float dx, dw;
   };
-  auto frag = [&](int slot) {
-    Frag f;
-    f.a = *reinterpret_cast<const intx4*>(a_p + slot * kStageBytes);
-    f.b = *reinterpret_cast<const intx4*>(b_p + slot * kStageBytes);
-    f.dx = *reinterpret_cast<const float*>(dx_p + slot * kStageBytes);
-    f.dw = *reinterpret_cast<const float*>(dw_p + slot * kStageBytes);
-    return f;
+  auto load = [&](Frag& f, int kb) {
+    kb = min(kb, nb - 1);
+    f.a = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(ra, 16u * lane, kb * kTile, 0));
+    f.b = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rb, 16u * lane, kb * kTile, 0));
+    // the block's scale rows: 64-bit scalar bases, any leading dimension
+    f.dx = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(xd + (size_t)kb * ldx, 4u * n), xoff, 0, 0));
+    f.dw = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(wd + (size_t)kb * ldw, 4u * m), woff, 0, 0));
   };
-
-  // Ring protocol: block kb sits in slot kb % kStages. Iteration kb refills
-  // slot (kb - 1) % kStages, last read in iteration kb - 2 (a barrier
-  // ago), then waits until block kb + 1 has landed for every wave.
+  intx16 magic = (intx16)(kMagicBits);
+  asm volatile("" : "+v"(magic));  // one register copy, not rebuilt per MFMA
+  // Loads stay in block order (a, b, dx, dw per block; the scheduling
+  // barriers keep the compiler from regrouping them), so that each wait
+  // the compiler derives covers only the block it needs, here and across
+  // the loop's back edge.
+  Frag f[kDepth];
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue(s, s);
-  wait_barrier<2 * (kStages - 2)>();
-  Frag f[2];
+  for (int s = 0; s < kDepth; ++s) {
+    load(f[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   intx16 d[2];
-  f[0] = frag(0);
   d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[0].a, f[0].b, magic, 0, 0, 0);
   floatx16 acc = floatx16{};
-  // One block: j = kb % kStages (a constant after unrolling, so slots are
-  // immediate offsets and the register pair alternates with kb's parity).
+  // One block: j = kb % kDepth (a constant after unrolling, so the
+  // fragment registers rotate and the MFMA result pair alternates). Block
+  // kb's scaling, the MFMA of block kb + 1, block kb's adds, then slot j
+  // refilled with block kb + kDepth.
   auto step = [&](int j, int kb) {
     const int cur = j & 1, nxt = cur ^ 1;
-    issue((j + kStages - 1) % kStages, kb + kStages - 1);
-    // The barrier's wait is asm the compiler does not see; marking these
-    // registers redefined here puts its own wait for their loads before
-    // the barrier, not after the next fragment reads.
-    asm volatile("" : "+v"(f[cur].dx), "+v"(f[cur].dw));
-    wait_barrier<2 * (kStages - 2)>();
-    f[nxt] = frag((j + 1) % kStages);
-    const floatx16 t = scale_products(d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
+    const floatx16 t = scale_products(d[cur], f[j].dw, f[j].dx, std::make_integer_sequence<int, 16>{});
     __builtin_amdgcn_sched_barrier(0);
-    d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
+    d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[(j + 1) % kDepth].a, f[(j + 1) % kDepth].b, magic, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     accumulate_products(acc, t, std::make_integer_sequence<int, 16>{});
+    __builtin_amdgcn_sched_barrier(0);
+    load(f[j], kb + kDepth);
+    __builtin_amdgcn_sched_barrier(0);
   };
   int kb0 = 0;
-  for (; kb0 + kStages <= nb; kb0 += kStages) {
+  if constexpr (!TAIL) {
+    // nb is a positive multiple of kDepth: a loop without the entry test,
+    // so the loads above stay in front of it in their order.
+    do {
 #pragma unroll
-    for (int j = 0; j < kStages; ++j) step(j, kb0 + j);
-  }
-  // The last nb % kStages blocks (the branch stays out of the main loop,
-  // whose straight-line body lets the DPP broadcasts fold into the multiplies).
-  if constexpr (TAIL) {
+      for (int j = 0; j < kDepth; ++j) step(j, kb0 + j);
+      kb0 += kDepth;
+    } while (kb0 < nb);
+  } else {
+    for (; kb0 + kDepth <= nb; kb0 += kDepth) {
 #pragma unroll
-    for (int j = 0; j < kStages - 1; ++j)
+      for (int j = 0; j < kDepth; ++j) step(j, kb0 + j);
+    }
+    // The last nb % kDepth blocks (the branch stays out of the main loop,
+    // whose straight-line body lets the DPP broadcasts fold into the multiplies).
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j)
       if (kb0 + j < nb) step(j, kb0 + j);
   }
-  // The ring's last refills are redundant; they must land before the
-  // workgroup's LDS is released.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if constexpr (GEGLU) {
     geglu_epilogue(acc, tr, tc, wr, wc, n, m / 64, gq, gd, ldy);
   } else {
@@ -359,18 +353,25 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   }
 }
 
+// The kernel for nb blocks (TAIL: nb is not a multiple of kDepth).
+template <bool GEGLU>
+static hipError_t launch_gemm_kernel(dim3 grid, size_t lds, hipStream_t st, const int8_t* xq, const float* xd,
+                                     int ldx, const int8_t* wq, const float* wd, int ldw, float* y, int n, int m,
+                                     int nb, int ldy, int8_t* gq, float* gd) {
+  if (nb % kDepth == 0)
+    hipLaunchKernelGGL((gemm_q8_kernel<false, GEGLU>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, y, n, m, nb,
+                       ldy, gq, gd);
+  else
+    hipLaunchKernelGGL((gemm_q8_kernel<true, GEGLU>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, y, n, m, nb,
+                       ldy, gq, gd);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st) {
   if (n <= 0 || m <= 0 || k <= 0 || k % kQK != 0 || ldy < m || ldx < n || ldw < m) return hipErrorInvalidValue;
-  const dim3 grid = gemm_grid(n, m, true);
-  const int nb = k / kQK;
-  if (nb % kStages == 0)
-    hipLaunchKernelGGL((gemm_q8_kernel<false, false>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
-                       ldw, y, n, m, nb, ldy, nullptr, nullptr);
-  else
-    hipLaunchKernelGGL((gemm_q8_kernel<true, false>), grid, dim3(256), kStages * kStageBytes, st, xq, xd, ldx, wq, wd,
-                       ldw, y, n, m, nb, ldy, nullptr, nullptr);
-  return hipGetLastError();
+  return launch_gemm_kernel<false>(gemm_grid(n, m, true), 0, st, xq, xd, ldx, wq, wd, ldw, y, n, m, k / kQK, ldy,
+                                   nullptr, nullptr);
 }
 
 hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
@@ -378,18 +379,11 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
   const int m = 2 * ff;
   if (n <= 0 || ff <= 0 || ff % kQK != 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < m || ldg < n)
     return hipErrorInvalidValue;
-  const dim3 grid = gemm_grid(n, m);
-  const int nb = k / kQK;
-  // LDS: the ring, or the epilogue's exchange area and its gate and up tiles
-  constexpr size_t lds = std::max<size_t>(kStages * kStageBytes, 2 * 2 * 32 * kGPitch * sizeof(float));
+  // LDS: the epilogue's exchange area, then its gate and up tiles
+  constexpr size_t lds = 2 * 2 * 32 * kGPitch * sizeof(float);
   static_assert(2 * 2048 * sizeof(float) <= lds, "the GeGLU exchange fits");
-  if (nb % kStages == 0)
-    hipLaunchKernelGGL((gemm_q8_kernel<false, true>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m,
-                       nb, ldg, gq, gd);
-  else
-    hipLaunchKernelGGL((gemm_q8_kernel<true, true>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m,
-                       nb, ldg, gq, gd);
-  return hipGetLastError();
+  return launch_gemm_kernel<true>(gemm_grid(n, m), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m, k / kQK, ldg, gq,
+                                  gd);
 }
 
 // ---------------------------------------------------------------------------
