@@ -624,11 +624,17 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     if (pair0 + wp >= pair1) wlast = wfirst;  // no such pair: w = 0
     float4 pw[2];
     auto load_w = [&](uint32_t c0) {
+      if (inside(c0)) {  // uniform: no bound
+#pragma unroll
+        for (int j4 = 0; j4 < 2; ++j4)
+          pw[j4] = *reinterpret_cast<const float4*>(wsrc + (c0 + wk + 4 * j4 - lo));
+        return;
+      }
 #pragma unroll
       for (int j4 = 0; j4 < 2; ++j4) {
         const uint32_t k4 = c0 + wk + 4 * j4;  // 4 keys, 16-byte aligned in the row
-        pw[j4] = inside(c0) || k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo))
-                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pw[j4] = k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo))
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     };
     // v staging by DMA, no registers: wave w moves keys c0 + 16 w .. + 15 of
@@ -638,11 +644,14 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     // from the sequence's first row, so that 32 bits hold them for any row
     // count (a planned sequence is below 37,838 rows: 194 MB of qkv).
     const float* seq = qkv + (size_t)lo * kLd;
+    // Row min(c0 + 16 w + 4 i + lane / 16, hi - 1) as a scalar base row
+    // (clamped) plus a per-lane step of 0..3 (clamped to what is left).
     auto issue_v = [&](uint32_t c0, int buf) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t row = min(c0 + 16 * (uint32_t)w + 4 * i + (uint32_t)(lane >> 4), hi - 1) - lo;
-        dma16(seq, (row * kLd + kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
+        const uint32_t brow = min(c0 - lo + 16 * (uint32_t)w + 4 * i, hi - 1 - lo);  // uniform
+        const uint32_t step = min((uint32_t)(lane >> 4), hi - 1 - lo - brow);
+        dma16(seq + (size_t)brow * kLd, __umul24(step, kLd * 4u) + (uint32_t)(kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
               vl0 + (unsigned)buf * (kCKeys * kCDims * 4) + (16 * w + 4 * i) * (kCDims * 4));
       }
     };
