@@ -30,12 +30,13 @@
 // Work: a workgroup of 4 waves computes a 64 x 64 output tile, wave w the
 // 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Each wave loads
 // its own activation and weight blocks and their scales straight into
-// registers by buffer loads, four blocks ahead, with no LDS and no barrier
+// registers by buffer loads, three blocks ahead (93 VGPRs, five waves per
+// SIMD: the 4,608 waves of gate|up all resident), with no LDS and no barrier
 // (an LDS ring shared by the four waves, with a barrier per block, was no
 // faster: the loop is bound by each wave's instruction stream, 24 or 36
 // blocks of one MFMA and 48 VALU operations, not by its loads). Per block:
 // block kb's two multiply phases, the MFMA of block kb + 1, block kb's
-// adds, then the refill of kb's registers with block kb + 4. In the MFMA
+// adds, then the refill of kb's registers with block kb + 3. In the MFMA
 // 32x32 output layout a lane holds one column and 16 rows; each row's
 // activation scale reaches it through a DPP row broadcast folded into the
 // multiply.
@@ -53,7 +54,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kXcds = 8;     // MI355X: 8 XCDs of 32 CUs, each with its own L2
 constexpr int kStages = 4;   // LDS ring depth of the Q|K|V kernel (even: see its loop)
-constexpr int kDepth = 4;    // blocks in flight per wave in gemm_q8_kernel (6 and 8 measured no faster)
+constexpr int kDepth = 3;    // blocks in flight per wave in gemm_q8_kernel (93 VGPRs: five waves per SIMD)
+constexpr int kUnroll = 6;   // its loop's unrolling: slots rotate mod kDepth, MFMA results mod 2
 constexpr int kTile = 1024;  // one 32 x 32 int8 operand block
 constexpr int kDxOff = 4 * kTile, kDwOff = kDxOff + 64 * 4;
 constexpr int kStageBytes = kDwOff + 64 * 4;  // A0 A1 B0 B1 | d_x[64] | d_w[64]
@@ -237,7 +239,7 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
                      gd + (size_t)tc * ldg + t);
 }
 
-// TAIL: nb % kDepth != 0 (a separate instantiation: the tail code costs
+// TAIL: nb % kUnroll != 0 (a separate instantiation: the tail code costs
 // registers, and every projection of the model has nb % 4 == 0). GEGLU:
 // the epilogue above replaces the fp32 store (y and ldy unused; m = 2 ff).
 template <bool TAIL, bool GEGLU>
@@ -306,39 +308,39 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   intx16 d[2];
   d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[0].a, f[0].b, magic, 0, 0, 0);
   floatx16 acc = floatx16{};
-  // One block: j = kb % kDepth (a constant after unrolling, so the
-  // fragment registers rotate and the MFMA result pair alternates). Block
-  // kb's scaling, the MFMA of block kb + 1, block kb's adds, then slot j
-  // refilled with block kb + kDepth.
+  // One block: j = kb % kUnroll (a constant after unrolling, so the
+  // fragment slot j % kDepth and the MFMA result register j % 2 are fixed
+  // registers). Block kb's scaling, the MFMA of block kb + 1, block kb's
+  // adds, then the slot refilled with block kb + kDepth.
   auto step = [&](int j, int kb) {
-    const int cur = j & 1, nxt = cur ^ 1;
-    const floatx16 t = scale_products(d[cur], f[j].dw, f[j].dx, std::make_integer_sequence<int, 16>{});
+    const int cur = j & 1, nxt = cur ^ 1, slot = j % kDepth;
+    const floatx16 t = scale_products(d[cur], f[slot].dw, f[slot].dx, std::make_integer_sequence<int, 16>{});
     __builtin_amdgcn_sched_barrier(0);
     d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[(j + 1) % kDepth].a, f[(j + 1) % kDepth].b, magic, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     accumulate_products(acc, t, std::make_integer_sequence<int, 16>{});
     __builtin_amdgcn_sched_barrier(0);
-    load(f[j], kb + kDepth);
+    load(f[slot], kb + kDepth);
     __builtin_amdgcn_sched_barrier(0);
   };
   int kb0 = 0;
   if constexpr (!TAIL) {
-    // nb is a positive multiple of kDepth: a loop without the entry test,
+    // nb is a positive multiple of kUnroll: a loop without the entry test,
     // so the loads above stay in front of it in their order.
     do {
 #pragma unroll
-      for (int j = 0; j < kDepth; ++j) step(j, kb0 + j);
-      kb0 += kDepth;
+      for (int j = 0; j < kUnroll; ++j) step(j, kb0 + j);
+      kb0 += kUnroll;
     } while (kb0 < nb);
   } else {
-    for (; kb0 + kDepth <= nb; kb0 += kDepth) {
+    for (; kb0 + kUnroll <= nb; kb0 += kUnroll) {
 #pragma unroll
-      for (int j = 0; j < kDepth; ++j) step(j, kb0 + j);
+      for (int j = 0; j < kUnroll; ++j) step(j, kb0 + j);
     }
-    // The last nb % kDepth blocks (the branch stays out of the main loop,
+    // The last nb % kUnroll blocks (the branch stays out of the main loop,
     // whose straight-line body lets the DPP broadcasts fold into the multiplies).
 #pragma unroll
-    for (int j = 0; j < kDepth - 1; ++j)
+    for (int j = 0; j < kUnroll - 1; ++j)
       if (kb0 + j < nb) step(j, kb0 + j);
   }
   if constexpr (GEGLU) {
@@ -353,12 +355,12 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
   }
 }
 
-// The kernel for nb blocks (TAIL: nb is not a multiple of kDepth).
+// The kernel for nb blocks (TAIL: nb is not a multiple of kUnroll).
 template <bool GEGLU>
 static hipError_t launch_gemm_kernel(dim3 grid, size_t lds, hipStream_t st, const int8_t* xq, const float* xd,
                                      int ldx, const int8_t* wq, const float* wd, int ldw, float* y, int n, int m,
                                      int nb, int ldy, int8_t* gq, float* gd) {
-  if (nb % kDepth == 0)
+  if (nb % kUnroll == 0)
     hipLaunchKernelGGL((gemm_q8_kernel<false, GEGLU>), grid, dim3(256), lds, st, xq, xd, ldx, wq, wd, ldw, y, n, m, nb,
                        ldy, gq, gd);
   else
