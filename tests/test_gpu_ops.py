@@ -301,10 +301,13 @@ def device_weights(eg2, blocks, k, gpu):
 
 
 @pytest.mark.parametrize("n,m,k", [(512, 2304, 768), (2048, 1280, 768), (2048, 768, 1152), (33, 40, 64),
-                                   (16, 3072, 768), (16, 768, 3072), (300, 768, 1152), (1, 32, 32)])
+                                   (16, 3072, 768), (16, 768, 3072), (300, 768, 1152), (1, 32, 32),
+                                   (70, 96, 320), (40, 64, 224)])
 def test_gemm_q8_bit_exact(eg2, gpu, n, m, k):
-    """Config 1 (512 x 2304 x 768) and every projection shape of the forward:
-    identical to the reference's Q8_0 x Q8_0 dot (gemma2.c:120-141)."""
+    """Config 1 (512 x 2304 x 768) and every projection shape of the forward,
+    and block counts that take the block loop's tail (10 and 7 blocks: one
+    round of 6 and a remainder): identical to the reference's Q8_0 x Q8_0
+    dot (gemma2.c:120-141)."""
     import torch
 
     w = quantize_q8_0((RNG.standard_normal((m, k)) * 0.02).astype(np.float32))
@@ -422,11 +425,12 @@ def test_gemm_q8_geglu_tied_block_maxima(eg2, gpu):
     assert np.array_equal(bits(d), bits(host(rd)))
 
 
-@pytest.mark.parametrize("n,ff,k", [(64, 32, 32), (100, 96, 160), (65, 1152, 768)])
+@pytest.mark.parametrize("n,ff,k", [(64, 32, 32), (100, 96, 160), (65, 1152, 768), (40, 64, 448)])
 def test_gemm_q8_geglu_against_oracle(eg2, gpu, n, ff, k):
-    """Other widths (k = 160: a block count that is not a multiple of the
-    LDS ring depth): the projections, the GeGLU and its Q8_0 bit for bit
-    the oracle's."""
+    """Other widths (k = 160 and 448: 5 and 14 blocks, not multiples of the
+    block loop's unrolling by 6, so the loop's tail runs, after no full
+    round and after two): the projections, the GeGLU and its Q8_0 bit for
+    bit the oracle's."""
     wg = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.05).astype(np.float32))
     wu = quantize_q8_0((RNG.standard_normal((ff, k)) * 0.05).astype(np.float32))
     xb = quantize_q8_0(RNG.standard_normal((n, k)).astype(np.float32))
