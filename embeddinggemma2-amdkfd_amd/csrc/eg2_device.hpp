@@ -33,8 +33,9 @@ __host__ __device__ inline size_t q8_tile_offset(size_t r, unsigned e, unsigned 
 }
 
 // LDS DMA from a wave-uniform global base (SGPR pair) plus a per-lane byte
-// offset, 16 or 4 bytes per lane, to the wave-uniform LDS address `lds`
-// (+16 or +4 bytes per lane), which the instruction takes from M0. Written
+// offset, 16 bytes per lane, to the wave-uniform LDS address `lds` (+16
+// bytes per lane), which the instruction takes from M0 (the attention
+// kernels' staging). Written
 // as asm, not as __builtin_amdgcn_global_load_lds: with this compiler (ROCm
 // 7.2 clang) the builtin's write to LDS is invisible to the optimizer, which
 // then folded away a later read of the same LDS words in a test kernel.
@@ -49,9 +50,6 @@ __host__ __device__ inline size_t q8_tile_offset(size_t r, unsigned e, unsigned 
 __device__ __forceinline__ void dma16(const void* base, unsigned off, unsigned lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* base, unsigned off, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
 }
 
 // A raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor:

@@ -22,10 +22,8 @@
 // it, eg2_q8_weight_tiles writes weights): int8 [rows/32][k/32][2][32][16],
 // so each 32-row x 32-value block is 1 KB in the register order of the
 // MFMA operand (lane 32h + r holds row r, values 16h .. 16h + 15): one
-// 16-byte load per lane at 16 lane moves it into the operand registers
-// (gemm_q8_kernel), or one 1 KB global_load_lds_dwordx4 into LDS (the
-// Q|K|V kernel, whose eight waves share the activation block). Block
-// scales are stored transposed, [k/32][ld], one float per row.
+// 16-byte load per lane at 16 lane moves it into the operand registers.
+// Block scales are stored transposed, [k/32][ld], one float per row.
 //
 // Work: a workgroup of 4 waves computes a 64 x 64 output tile, wave w the
 // 32 x 32 quarter at rows 32 (w >> 1), columns 32 (w & 1). Each wave loads
@@ -53,25 +51,13 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kXcds = 8;     // MI355X: 8 XCDs of 32 CUs, each with its own L2
-constexpr int kStages = 4;   // LDS ring depth of the Q|K|V kernel (even: see its loop)
 constexpr int kDepth = 3;    // blocks in flight per wave in gemm_q8_kernel (93 VGPRs: five waves per SIMD)
 constexpr int kUnroll = 6;   // its loop's unrolling: slots rotate mod kDepth, MFMA results mod 2
 constexpr int kTile = 1024;  // one 32 x 32 int8 operand block
-constexpr int kDxOff = 4 * kTile, kDwOff = kDxOff + 64 * 4;
-constexpr int kStageBytes = kDwOff + 64 * 4;  // A0 A1 B0 B1 | d_x[64] | d_w[64]
 constexpr float kMagic = 12582912.0f;         // 1.5 * 2^23
 constexpr int kMagicBits = 0x4B400000;
 
 extern __shared__ __align__(16) unsigned char gemm_lds[];
-
-// Waits until at most N vector-memory operations of this wave are in flight
-// and its LDS reads are done, then joins the workgroup barrier. The ring is
-// filled by DMA, which the compiler does not track, so the wait is
-// explicit; the memory clobber keeps LDS reads from moving across it.
-template <int N>
-__device__ __forceinline__ void wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
 
 // Broadcast of lane V of each 16-lane row to the whole row (row_newbcast).
 template <int V>
@@ -239,46 +225,24 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
                      gd + (size_t)tc * ldg + t);
 }
 
-// TAIL: nb % kUnroll != 0 (a separate instantiation: the tail code costs
-// registers, and every projection of the model has nb % 4 == 0). GEGLU:
-// the epilogue above replaces the fp32 store (y and ldy unused; m = 2 ff).
-template <bool TAIL, bool GEGLU>
-__global__ void __launch_bounds__(256)
-gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx, const int8_t* __restrict__ wq,
-               const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy,
-               int8_t* __restrict__ gq, float* __restrict__ gd) {
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // Issue priority 1: above the attention kernels (0), below the short
-  // latency-bound row kernels (3), when other streams share the SIMDs.
-  __builtin_amdgcn_s_setprio(1);
-  // XCD-aware order: workgroup b runs on XCD b % 8, which takes one region
-  // of the tile grid (column-group major inside it).
-  const XcdRegions reg = xcd_regions(n, m, !GEGLU);
-  const int x = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
-  const int r0 = (x / reg.cparts) * reg.rows, c0 = (x % reg.cparts) * reg.cols;
-  const int rows_here = min(reg.rows, (n + 63) / 64 - r0), cols_here = min(reg.cols, (m + 63) / 64 - c0);
-  if (rows_here <= 0 || cols_here <= 0 || i >= rows_here * cols_here) return;
-  const int tr = r0 + i % rows_here, tc = c0 + i / rows_here;
-
-  // Operands straight to registers: the row-tile layout is the MFMA's
-  // register order, so lane L's 16 bytes of a 1 KB block are one
-  // global_load_dwordx4 at 16 L. Wave (wr, wc) loads its own activation
-  // block (rows 64 tr + 32 wr, clamped to the last tile) and weight block
-  // (columns 64 tc + 32 wc), its row's activation scale and its column's
-  // weight scale (clamped to the last row / column), kDepth blocks ahead;
-  // no LDS and no barrier, so the four waves never wait for each other.
-  const int wr = w >> 1, wc = w & 1, g = lane >> 5;
-  // Row whose scale this lane supplies to the DPP broadcast: lane 16r + v
-  // carries the scale of output register v for the lanes of 16-lane row r.
-  const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
+// The block loop of one wave's 32 x 32 output tile, shared by the
+// projection kernels: the activation block tile atile (1 KB per block, nb
+// blocks) and its scales xd[kb * ldx + xoff / 4] (n rows), the weight block
+// tile btile and its scales wd[kb * ldw + woff / 4] (m rows), xoff being
+// the row whose scale this lane feeds to the DPP broadcast (srow) and woff
+// the lane's column. Operands go straight to registers (the row-tile
+// layout is the MFMA's register order: lane L's 16 bytes of a block are
+// one load at 16 L) by buffer loads with a scalar offset per block, kDepth
+// blocks ahead, with no LDS and no barrier: the waves of a workgroup never
+// wait for each other. Returns the tile in the 32x32 MFMA output layout.
+template <bool TAIL>
+__device__ __forceinline__ floatx16 q8_block_loop(const int8_t* atile, const float* __restrict__ xd, int ldx, int n,
+                                                  uint32_t xoff, const int8_t* btile, const float* __restrict__ wd,
+                                                  int ldw, int m, uint32_t woff, int nb, int lane) {
   // Buffer loads: the per-block advance is a scalar offset, so no vector
   // address is kept per block in flight.
-  const __amdgpu_buffer_rsrc_t ra =
-      buffer_rsrc(xq + (size_t)min(2 * tr + wr, (n + 31) / 32 - 1) * nb * kTile, (uint32_t)nb * kTile);
-  const __amdgpu_buffer_rsrc_t rb =
-      buffer_rsrc(wq + (size_t)min(2 * tc + wc, (m + 31) / 32 - 1) * nb * kTile, (uint32_t)nb * kTile);
-  const uint32_t xoff = 4u * (uint32_t)min(64 * tr + 32 * wr + srow, n - 1);
-  const uint32_t woff = 4u * (uint32_t)min(64 * tc + 32 * wc + (lane & 31), m - 1);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(atile, (uint32_t)nb * kTile);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(btile, (uint32_t)nb * kTile);
   struct Frag {
     intx4 a, b;
     float dx, dw;
@@ -343,6 +307,42 @@ gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int 
     for (int j = 0; j < kUnroll - 1; ++j)
       if (kb0 + j < nb) step(j, kb0 + j);
   }
+  return acc;
+}
+
+// TAIL: nb % kUnroll != 0 (a separate instantiation: the tail code costs
+// registers, and every projection of the model has nb % 4 == 0). GEGLU:
+// the epilogue above replaces the fp32 store (y and ldy unused; m = 2 ff).
+template <bool TAIL, bool GEGLU>
+__global__ void __launch_bounds__(256)
+gemm_q8_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd, int ldx, const int8_t* __restrict__ wq,
+               const float* __restrict__ wd, int ldw, float* __restrict__ y, int n, int m, int nb, int ldy,
+               int8_t* __restrict__ gq, float* __restrict__ gd) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Issue priority 1: above the attention kernels (0), below the short
+  // latency-bound row kernels (3), when other streams share the SIMDs.
+  __builtin_amdgcn_s_setprio(1);
+  // XCD-aware order: workgroup b runs on XCD b % 8, which takes one region
+  // of the tile grid (column-group major inside it).
+  const XcdRegions reg = xcd_regions(n, m, !GEGLU);
+  const int x = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
+  const int r0 = (x / reg.cparts) * reg.rows, c0 = (x % reg.cparts) * reg.cols;
+  const int rows_here = min(reg.rows, (n + 63) / 64 - r0), cols_here = min(reg.cols, (m + 63) / 64 - c0);
+  if (rows_here <= 0 || cols_here <= 0 || i >= rows_here * cols_here) return;
+  const int tr = r0 + i % rows_here, tc = c0 + i / rows_here;
+
+  // Wave (wr, wc): activation rows 64 tr + 32 wr (clamped to the last
+  // tile), weight columns 64 tc + 32 wc; scales clamped to the last row
+  // and column.
+  const int wr = w >> 1, wc = w & 1, g = lane >> 5;
+  // Row whose scale this lane supplies to the DPP broadcast: lane 16r + v
+  // carries the scale of output register v for the lanes of 16-lane row r.
+  const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
+  const floatx16 acc = q8_block_loop<TAIL>(
+      xq + (size_t)min(2 * tr + wr, (n + 31) / 32 - 1) * nb * kTile, xd, ldx, n,
+      4u * (uint32_t)min(64 * tr + 32 * wr + srow, n - 1),
+      wq + (size_t)min(2 * tc + wc, (m + 31) / 32 - 1) * nb * kTile, wd, ldw, m,
+      4u * (uint32_t)min(64 * tc + 32 * wc + (lane & 31), m - 1), nb, lane);
   if constexpr (GEGLU) {
     geglu_epilogue(acc, tr, tc, wr, wc, n, m / 64, gq, gd, ldy);
   } else {
@@ -401,10 +401,6 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // qk_norm_rope kernel -- and writes the rows [q0 q1 q2 | k | v] attention
 // reads; the v head is the projection itself. The unnormalised projection
 // never reaches HBM.
-constexpr int kQkvTiles = 9;                      // A | B0 .. B7 per stage
-constexpr int kQDxOff = kQkvTiles * kTile;        // 64 floats (rows 0-31 used)
-constexpr int kQDwOff = kQDxOff + 64 * 4;         // 256 floats
-constexpr int kQStageBytes = kQDwOff + 256 * 4;
 constexpr int kRowPitch = kHeadDim + 8;  // floats per token row of the epilogue tile (8 banks apart)
 constexpr int kQkvHeads = kQKVCols / kHeadDim;  // 5
 
@@ -426,82 +422,15 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
   if (rows_here <= 0 || cols_here <= 0 || i >= rows_here * cols_here) return;
   const int tr = r0 + i % rows_here, hc = c0 + i / rows_here;
 
-  // DMA, the same three transfers for every wave (no branch in the loop):
-  // weight tile 8 hc + w of the block; a quarter of the activation tile
-  // (waves 0-3) or of the head's 256 weight scales (waves 4-7), 4 bytes a
-  // lane; and the activation scales of the tile's rows (identical data in
-  // every wave; lanes 32-63 repeat rows 0-31).
-  const int8_t* tbase = wq + (size_t)(8 * hc + w) * nb * kTile;
-  const unsigned lds0 = (unsigned)(uintptr_t)gemm_lds;
-  const unsigned t_lds = lds0 + kTile * (1 + w);
-  const bool aq = w < 4;
-  const char* q_base = aq ? reinterpret_cast<const char*>(xq + (size_t)tr * nb * kTile) + 256 * w
-                          : reinterpret_cast<const char*>(wd + 256 * hc + 64 * (w - 4));
-  const size_t q_step = aq ? (size_t)kTile : (size_t)ldw * 4;  // bytes per block
-  const unsigned q_lds = lds0 + (aq ? 256 * w : kQDwOff + 256 * (w - 4));
-  const unsigned x_off = 4u * (unsigned)min(32 * tr + (lane & 31), n - 1);
-  auto issue = [&](int slot, int kb) {
-    kb = min(kb, nb - 1);
-    const unsigned st = slot * kQStageBytes;
-    dma16(tbase + (size_t)kb * kTile, 16u * lane, __builtin_amdgcn_readfirstlane(t_lds + st));
-    dma4(q_base + kb * q_step, 4u * lane, __builtin_amdgcn_readfirstlane(q_lds + st));
-    dma4(xd + (size_t)kb * ldx, x_off, __builtin_amdgcn_readfirstlane(lds0 + st + kQDxOff));
-  };
-
+  // Wave w: the activation rows of tile tr and weight columns 32 w of head
+  // hc, through the projection kernels' block loop (no LDS ring, no
+  // barrier).
   const int g = lane >> 5;
   const int srow = 8 * ((lane & 15) >> 2) + 4 * g + (lane & 3);
-  const unsigned char* a_p = gemm_lds + 16 * lane;
-  const unsigned char* b_p = gemm_lds + kTile * (1 + w) + 16 * lane;
-  const unsigned char* dx_p = gemm_lds + kQDxOff + 4 * srow;
-  const unsigned char* dw_p = gemm_lds + kQDwOff + 4 * (32 * w + (lane & 31));
-  intx16 magic = (intx16)(kMagicBits);
-  asm volatile("" : "+v"(magic));
-  struct Frag {
-    intx4 a, b;
-    float dx, dw;
-  };
-  auto frag = [&](int slot) {
-    Frag f;
-    f.a = *reinterpret_cast<const intx4*>(a_p + slot * kQStageBytes);
-    f.b = *reinterpret_cast<const intx4*>(b_p + slot * kQStageBytes);
-    f.dx = *reinterpret_cast<const float*>(dx_p + slot * kQStageBytes);
-    f.dw = *reinterpret_cast<const float*>(dw_p + slot * kQStageBytes);
-    return f;
-  };
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue(s, s);
-  wait_barrier<3 * (kStages - 2)>();
-  Frag f[2];
-  intx16 d[2];
-  f[0] = frag(0);
-  d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[0].a, f[0].b, magic, 0, 0, 0);
-  floatx16 acc = floatx16{};
-  auto step = [&](int j, int kb) {
-    const int cur = j & 1, nxt = cur ^ 1;
-    issue((j + kStages - 1) % kStages, kb + kStages - 1);
-    // The barrier's wait is asm the compiler does not see; marking these
-    // registers redefined here puts its own wait for their loads before
-    // the barrier, not after the next fragment reads.
-    asm volatile("" : "+v"(f[cur].dx), "+v"(f[cur].dw));
-    wait_barrier<3 * (kStages - 2)>();
-    f[nxt] = frag((j + 1) % kStages);
-    const floatx16 t = scale_products(d[cur], f[cur].dw, f[cur].dx, std::make_integer_sequence<int, 16>{});
-    __builtin_amdgcn_sched_barrier(0);
-    d[nxt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[nxt].a, f[nxt].b, magic, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    accumulate_products(acc, t, std::make_integer_sequence<int, 16>{});
-  };
-  int kb0 = 0;
-  for (; kb0 + kStages <= nb; kb0 += kStages) {
-#pragma unroll
-    for (int j = 0; j < kStages; ++j) step(j, kb0 + j);
-  }
-  if constexpr (TAIL) {
-#pragma unroll
-    for (int j = 0; j < kStages - 1; ++j)
-      if (kb0 + j < nb) step(j, kb0 + j);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const floatx16 acc = q8_block_loop<TAIL>(
+      xq + (size_t)tr * nb * kTile, xd, ldx, n, 4u * (uint32_t)min(32 * tr + srow, n - 1),
+      wq + (size_t)(8 * hc + w) * nb * kTile, wd, ldw, kQKVCols,
+      4u * (uint32_t)(kHeadDim * hc + 32 * w + (lane & 31)), nb, lane);
   // The epilogue's global inputs go out now, so their latency overlaps the
   // tile's trip through LDS and the sums of squares: the cos/sin and norm
   // weights of this wave's rows 4w..4w+3 (q, k), or the v columns.
@@ -524,8 +453,6 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
       cs_r[rr][2 * j + 1] = cs[half + lane + 64 * j];
     }
   }
-  __syncthreads();  // the ring becomes the epilogue tile
-
   float* tile = reinterpret_cast<float*>(gemm_lds);  // [32][kRowPitch]
 #pragma unroll
   for (int v = 0; v < 16; ++v) tile[(8 * (v >> 2) + 4 * g + (v & 3)) * kRowPitch + 32 * w + (lane & 31)] = acc[v];
@@ -577,16 +504,16 @@ hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, c
                                    int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
                                    const int32_t* pos, float eps, float* out, hipStream_t st) {
   if (n <= 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < kQKVCols) return hipErrorInvalidValue;
-  static_assert(32 * kRowPitch * 4 <= kStages * kQStageBytes, "the epilogue tile fits in the ring");
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
   const dim3 grid(kXcds * reg.rows * reg.cols);
   const int nb = k / kQK;
-  if (nb % kStages == 0)
-    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<false>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
-                       wd, ldw, n, nb, q_w, k_w, rope, pos, eps, out);
+  constexpr size_t lds = 32 * kRowPitch * sizeof(float);  // the epilogue tile
+  if (nb % kUnroll == 0)
+    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<false>, grid, dim3(512), lds, st, xq, xd, ldx, wq, wd, ldw, n, nb, q_w,
+                       k_w, rope, pos, eps, out);
   else
-    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<true>, grid, dim3(512), kStages * kQStageBytes, st, xq, xd, ldx, wq,
-                       wd, ldw, n, nb, q_w, k_w, rope, pos, eps, out);
+    hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<true>, grid, dim3(512), lds, st, xq, xd, ldx, wq, wd, ldw, n, nb, q_w,
+                       k_w, rope, pos, eps, out);
   return hipGetLastError();
 }
 
