@@ -121,10 +121,11 @@ __host__ inline dim3 gemm_grid(int n, int m, bool rows_first = false) {
 }
 
 // Floats per row of the GeGLU epilogue's transposed tile: 36 (4 banks past
-// a multiple of 32), so that the eight lanes of a 16-byte read (two rows,
-// four 8-float parts each) cover 32 distinct banks; at 40 the second row's
-// parts fell on the first row's banks (1.03 M bank-conflict cycles per
-// launch at 2048 x 2304 against 0.44 M now).
+// a multiple of 32): 1.03 M bank-conflict cycles per launch at 2048 x 2304
+// with 40, 0.44 M with 36, 44 or 52. The compiler splits each lane's two
+// 16-byte reads of a row into 4-byte pairs (ds_read2_b32), and 16 rows of
+// 4 lanes reading the same dword of their 8-float parts cannot take 32
+// distinct banks at any pitch; those pairs are what remains.
 constexpr int kGPitch = 36;
 
 // GeGLU epilogue (kernels.c:367-391, engine.c's gelu(gate) * up then the
