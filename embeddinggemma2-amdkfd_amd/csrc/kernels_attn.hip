@@ -168,21 +168,33 @@ __device__ __forceinline__ void scores_quarter(const float* qa, const float* kb,
 }
 
 // The wave's 16 x 16 scores ((chain 0 + chain 2) + (chain 1 + chain 3),
-// kernels.c:35-39) for the (pair, key)s inside the pair's window.
+// kernels.c:35-39) for the (pair, key)s inside the pair's window. Stored
+// through a buffer resource over the sequence's score rows (a scalar base
+// and a 32-bit offset per lane) when they span less than 4 GiB, which every
+// sequence of up to 18,900 tokens does.
 __device__ __forceinline__ void store_scores(const float (&acc)[4][4], uint32_t lo, uint32_t hi, uint32_t key0,
                                              uint32_t pair0, uint32_t pair1, size_t sbase, int window, int pr,
                                              int kr, int g, int r16, float* __restrict__ scores) {
-  const uint32_t pitch = score_pitch(hi - lo);
+  const uint32_t len = hi - lo, pitch = score_pitch(len);
   const uint32_t key = key0 + kr + r16;
+  const bool small = (uint64_t)3 * len * pitch * 4 < 0x100000000ull;  // uniform
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(scores + sbase, 0xffffffffu);
+  const uint32_t p0 = pair0 + pr + 4 * g, off0 = p0 * pitch + (key - lo);  // pair p0 + r at off0 + r pitch
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const uint32_t pair = pair0 + pr + 4 * g + r;
+    const uint32_t pair = p0 + r;
     const float score = (acc[0][r] + acc[2][r]) + (acc[1][r] + acc[3][r]);
-    if (pair < pair1 && key < hi) {
+    bool in = pair < pair1 && key < hi;
+    if (window > 0) {  // uniform
       uint32_t first, last;
       key_range(lo + pair / 3, lo, hi, window, first, last);
-      if (key >= first && key < last) scores[sbase + (size_t)pair * pitch + (key - lo)] = score;
+      in = in && key >= first && key < last;
     }
+    if (!in) continue;
+    if (small)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, score), rs, 4u * (off0 + r * pitch), 0, 0);
+    else
+      scores[sbase + (size_t)pair * pitch + (key - lo)] = score;
   }
 }
 
