@@ -133,10 +133,10 @@ constexpr int kGPitch = 36;
 // interleaved in 32-row groups (gate group j, then up group j), so output
 // tile tc holds gate columns 32 tc .. 32 tc + 31 in its waves wc = 0 and
 // the matching up columns in its waves wc = 1, and its 32 GeGLU outputs per
-// row are exactly Q8_0 block tc. The two waves of a row pair swap their
-// results through LDS (the gate wave finishes rows 0-15 of the pair, the
-// up wave rows 16-31), transpose the gate and up values so that four lanes
-// hold one row's block, and run the standalone GeGLU kernel's code
+// row are exactly Q8_0 block tc. The two waves of a row pair write their
+// tiles to LDS row-major and read them back transposed (the gate wave
+// finishes rows 0-15 of the pair, the up wave rows 16-31), four lanes
+// holding one row's block, and run the standalone GeGLU kernel's code
 // (geglu_quantize_part4): the int8 values go to gq in the row-tile layout
 // (nbf blocks per row), the scales to gd[tc * ldg + row].
 // Minimum over each aligned quad of lanes, on every lane of it (all 64 lanes
@@ -188,31 +188,15 @@ __device__ __forceinline__ void geglu_block_candidates(const float (&g)[8], cons
 __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int tc, int wr, int wc, int n, int nbf,
                                                int8_t* __restrict__ gq, float* __restrict__ gd, int ldg) {
   const int lane = threadIdx.x & 63, g = lane >> 5;
-  // The ring is free once every wave is past its last fragment reads.
-  __syncthreads();
-  // Every wave puts all 16 of its registers in LDS ([2 wc][16 v][64 lanes]
-  // per row pair) and reads back the gate and up values of its own half by
-  // address, so no register is selected at run time.
-  float* xch = reinterpret_cast<float*>(gemm_lds) + wr * 2048;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) xch[(wc * 16 + v) * 64 + lane] = acc[v];
-  __syncthreads();
-  float gv[8], uv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    gv[i] = xch[(8 * wc + i) * 64 + lane];
-    uv[i] = xch[(16 + 8 * wc + i) * 64 + lane];
-  }
-  __syncthreads();  // the exchange area becomes the transposed gate and up tiles
+  // Wave (wr, wc) writes its 32 x 32 tile -- gate for wc = 0, up for wc = 1
+  // -- into its matrix's transposed tile (register v: row 8 (v >> 2) + 4 g
+  // + (v & 3), column lane & 31); the block loop leaves the LDS unused.
   float* tg = reinterpret_cast<float*>(gemm_lds) + wr * 2 * 32 * kGPitch;  // [32][kGPitch] gate, then up
   float* tu = tg + 32 * kGPitch;
-  // register v = 8 wc + i of the 32x32 output layout: row 8 (v >> 2) + 4 g + (v & 3), column lane & 31
-  const int trow = (16 * wc + 4 * g) * kGPitch + (lane & 31);
+  float* mine = wc == 0 ? tg : tu;
+  const int trow = 4 * g * kGPitch + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    tg[trow + (8 * (i >> 2) + (i & 3)) * kGPitch] = gv[i];
-    tu[trow + (8 * (i >> 2) + (i & 3)) * kGPitch] = uv[i];
-  }
+  for (int v = 0; v < 16; ++v) mine[trow + (8 * (v >> 2) + (v & 3)) * kGPitch] = acc[v];
   __syncthreads();
   const int rr = 16 * wc + (lane >> 2), part = lane & 3;
   float gs[8], us[8];
@@ -387,9 +371,8 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
   const int m = 2 * ff;
   if (n <= 0 || ff <= 0 || ff % kQK != 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < m || ldg < n)
     return hipErrorInvalidValue;
-  // LDS: the epilogue's exchange area, then its gate and up tiles
+  // LDS: the epilogue's gate and up tiles
   constexpr size_t lds = 2 * 2 * 32 * kGPitch * sizeof(float);
-  static_assert(2 * 2048 * sizeof(float) <= lds, "the GeGLU exchange fits");
   return launch_gemm_kernel<true>(gemm_grid(n, m), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m, k / kQK, ldg, gq,
                                   gd);
 }
