@@ -120,13 +120,13 @@ __host__ inline dim3 gemm_grid(int n, int m, bool rows_first = false) {
   return dim3(kXcds * reg.rows * reg.cols);
 }
 
-// Floats per row of the GeGLU epilogue's transposed tile: 36 (4 banks past
-// a multiple of 32): 1.03 M bank-conflict cycles per launch at 2048 x 2304
-// with 40, 0.44 M with 36, 44 or 52. The compiler splits each lane's two
-// 16-byte reads of a row into 4-byte pairs (ds_read2_b32), and 16 rows of
-// 4 lanes reading the same dword of their 8-float parts cannot take 32
-// distinct banks at any pitch; those pairs are what remains.
-constexpr int kGPitch = 36;
+// Floats per row of the GeGLU epilogue's transposed tile: odd, so that the
+// 32 lanes of a half-wave reading one dword each of their row's 8-value
+// part (8 rows x 4 parts) hit 32 distinct banks (row r at bank offset r,
+// part p at 8 p). The reads are 4-byte (the compiler splits wider ones
+// anyway), so nothing needs 16-byte alignment. Bank-conflict cycles per
+// launch at 2048 x 2304: 1.03 M with a pitch of 40, 0.44 M with 36, 0 now.
+constexpr int kGPitch = 33;
 
 // GeGLU epilogue (kernels.c:367-391, engine.c's gelu(gate) * up then the
 // Q8_0 quantization of the down projection's input). The weight rows are
@@ -201,11 +201,9 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
   const int rr = 16 * wc + (lane >> 2), part = lane & 3;
   float gs[8], us[8];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float4 g4 = *reinterpret_cast<const float4*>(tg + rr * kGPitch + 8 * part + 4 * h);
-    const float4 u4 = *reinterpret_cast<const float4*>(tu + rr * kGPitch + 8 * part + 4 * h);
-    gs[4 * h] = g4.x, gs[4 * h + 1] = g4.y, gs[4 * h + 2] = g4.z, gs[4 * h + 3] = g4.w;
-    us[4 * h] = u4.x, us[4 * h + 1] = u4.y, us[4 * h + 2] = u4.z, us[4 * h + 3] = u4.w;
+  for (int i = 0; i < 8; ++i) {
+    gs[i] = tg[rr * kGPitch + 8 * part + i];
+    us[i] = tu[rr * kGPitch + 8 * part + i];
   }
   const int t = 64 * tr + 32 * wr + rr;
   float a[8], bound[8];
