@@ -92,6 +92,8 @@ constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchV = kCDims + 4;       // floats per row of the context's epilogue tile
 constexpr int kShortSoftmax = 512;        // longest sequence for the 16-pair one-kernel softmax
+constexpr int kGroup16Softmax = 128;      // longest for the softmax with 16 lanes per pair
+constexpr int kGroup32Softmax = 256;      // and with 32
 constexpr int kCBatch = 4;                // context MFMAs in flight per wave
 constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
 
@@ -492,6 +494,129 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   }
 }
 
+// The softmax for waves of short sequences: LANES (16 or 32) lanes per
+// (token, head) pair, 64 / LANES pairs per wave, 16 pairs per workgroup, so
+// several pairs share each instruction of the per-pair set-up and of the
+// maximum's combination. Lane j of a pair's LANES takes keys
+// first + j + LANES i: the row maximum (order-free; combined over the pair's
+// lanes by DPP), then p = expf(score - m) written back over the scores and
+// into the pair's LDS row; then lane i of the first wave adds pair i's p
+// values in key order and writes 1/sum into the scratch's head. A row longer
+// than kShortSoftmax (a packing longer than the caller's `longest`) is summed
+// from the scores in global memory instead: slower, same bits. The same
+// operations in the same order as attention_softmax_kernel, which takes
+// waves of longer sequences (fewer pairs per wave hide more latency there).
+constexpr int kGroupPairs = 16;  // pairs per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+// Maximum over each aligned group of LANES lanes, on every lane of it (all
+// 64 lanes active): quad permutations, the other quad of each 8 lanes
+// (row_half_mirror), the other 8 of each 16 (row_mirror), then for 32 the
+// other 16 (a swizzle).
+template <int LANES>
+__device__ __forceinline__ float group_max(float m) {
+  static_assert(LANES == 16 || LANES == 32, "16 or 32 lanes per pair");
+  m = fmaxf(m, dpp_move<0xB1>(m));   // quad_perm [1,0,3,2]
+  m = fmaxf(m, dpp_move<0x4E>(m));   // quad_perm [2,3,0,1]
+  m = fmaxf(m, dpp_move<0x141>(m));  // row_half_mirror
+  m = fmaxf(m, dpp_move<0x140>(m));  // row_mirror
+  if constexpr (LANES == 32) m = fmaxf(m, __shfl_xor(m, 16, 64));
+  return m;
+}
+
+template <int LANES>
+__global__ void __launch_bounds__(LANES * kGroupPairs)
+attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
+  __shared__ uint64_t tab[32];
+  __shared__ __align__(16) float prow[kGroupPairs][kShortSoftmax + 4];  // each pair's p values (4 banks apart)
+  __shared__ uint32_t plen[kGroupPairs];                                // and their count (0: no such pair)
+  __shared__ uint32_t pbase[kGroupPairs];                               // index in scores of the row's first key
+  __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
+  const int tid = threadIdx.x, slot = tid / LANES, sub = tid % LANES;
+  if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
+  __syncthreads();
+  // XCD-aware order, as in attention_softmax_kernel.
+  const uint32_t blk = gridDim.x % kXcdCount == 0
+                           ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
+                           : blockIdx.x;
+  const uint32_t pair = kGroupPairs * blk + slot, t = pair / 3, h = pair % 3;
+  uint32_t n = 0, base = 0;
+  if (t < (uint32_t)rows) {
+    const uint4 meta = tok[t];
+    const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
+    if (t >= lo && t < hi) {  // else a malformed entry: nothing is written for this token
+      uint32_t first, last;
+      key_range(t, lo, hi, window, first, last);
+      n = last - first;
+      base = meta.z + (3 * (t - lo) + h) * score_pitch(hi - lo) + (first - lo);
+    }
+  }
+  float* row = scores + base;  // key first + j at row[j]
+  float m = -__builtin_inff();
+  uint32_t j = sub;
+  for (; j + 3 * LANES < n; j += 4 * LANES) {
+    const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
+    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+  }
+  for (; j < n; j += LANES) m = fmaxf(m, row[j]);
+  m = group_max<LANES>(m);
+  const bool to_lds = n <= (uint32_t)kShortSoftmax;
+  float* lrow = prow[slot];
+  for (j = sub; j + 3 * LANES < n; j += 4 * LANES) {
+    const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
+    const float pa = libm::expf_tab(a - m, tab), pb = libm::expf_tab(b - m, tab);
+    const float pc = libm::expf_tab(c - m, tab), pd = libm::expf_tab(d - m, tab);
+    row[j] = pa;
+    row[j + LANES] = pb;
+    row[j + 2 * LANES] = pc;
+    row[j + 3 * LANES] = pd;
+    if (to_lds) {
+      lrow[j] = pa;
+      lrow[j + LANES] = pb;
+      lrow[j + 2 * LANES] = pc;
+      lrow[j + 3 * LANES] = pd;
+    }
+  }
+  for (; j < n; j += LANES) {
+    const float p = libm::expf_tab(row[j] - m, tab);
+    row[j] = p;
+    if (to_lds) lrow[j] = p;
+  }
+  if (sub == 0) {
+    plen[slot] = n;
+    pbase[slot] = base;
+  }
+  __syncthreads();
+  if (tid < kGroupPairs) {
+    const uint32_t cnt = plen[tid];
+    const uint32_t own = kGroupPairs * blk + tid;
+    if (cnt > 0) {
+      float sum = 0.0f;
+      if (cnt <= (uint32_t)kShortSoftmax) {
+        const float* pr = prow[tid];
+        uint32_t k = 0;
+#pragma unroll 2
+        for (; k + 4 <= cnt; k += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(pr + k);
+          sum = sum + p4.x;
+          sum = sum + p4.y;
+          sum = sum + p4.z;
+          sum = sum + p4.w;
+        }
+        for (; k < cnt; ++k) sum = sum + pr[k];
+      } else {
+        const float* pr = scores + pbase[tid];
+#pragma unroll 1
+        for (uint32_t k = 0; k < cnt; ++k) sum = sum + pr[k];
+      }
+      scores[own] = 1.0f / sum;
+    }
+  }
+}
+
 // One wave per (token, head) pair: the row maximum (order-free), then
 // every lane's p = expf(score - m) for its keys, written back over the
 // scores. The sums come in attention_sum_kernel.
@@ -876,9 +1001,18 @@ hipError_t launch_attention_scores(const float* qkv, const uint32_t* items, cons
   return hipGetLastError();
 }
 
+template <int LANES>
+hipError_t launch_group_softmax(const uint32_t* tok, int window, int rows, float* scores, hipStream_t st) {
+  hipLaunchKernelGGL(attention_softmax_group_kernel<LANES>, dim3((3 * rows + kGroupPairs - 1) / kGroupPairs),
+                     dim3(LANES * kGroupPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+  return hipGetLastError();
+}
+
 hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, int longest, float* scores,
                                     hipStream_t st) {
   if (rows <= 0 || rows % 4 != 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
+  if (longest > 0 && longest <= kGroup16Softmax) return launch_group_softmax<16>(tok, window, rows, scores, st);
+  if (longest > 0 && longest <= kGroup32Softmax) return launch_group_softmax<32>(tok, window, rows, scores, st);
   if (longest > 0 && longest <= kShortSoftmax) {
     constexpr int kPairs = 16;
     hipLaunchKernelGGL((attention_softmax_kernel<kShortSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),

@@ -606,18 +606,19 @@ def test_attention_independent_of_packing(eg2, gpu, window):
 @pytest.mark.parametrize("window", [0, 64])
 @pytest.mark.parametrize("lens", [[1, 130, 512, 7, 300], [1, 513, 2, 1200, 37]])
 def test_attention_softmax_forms_agree(eg2, gpu, window, lens):
-    """The one-kernel softmax (16 pairs per workgroup for waves of sequences
-    up to 512 tokens, 8 pairs with rows up to 2048 keys in LDS otherwise)
-    and the exp + serial-sum pair (any length) give the same bits, and so
-    does a `longest` below the wave's real longest sequence (rows too long
-    for the chosen form's LDS are summed from global memory): the hint picks
-    a kernel form, never the results."""
+    """The one-kernel softmax forms (16 or 32 lanes per pair for waves of
+    sequences up to 128 or 256 tokens, a wave per pair up to 512, 8 pairs
+    with rows up to 2048 keys in LDS otherwise) and the exp + serial-sum
+    pair (any length) give the same bits, and so does a `longest` below the
+    wave's real longest sequence (rows too long for the chosen form's LDS are
+    summed from global memory): the hint picks a kernel form, never the
+    results."""
     rng = np.random.default_rng(10 + len(lens))
     T = sum(lens)
     offsets = np.concatenate([[0], np.cumsum(lens)])
     q, k, v = qkv_inputs(rng, T)
     ref = run_attention(eg2, gpu, q, k, v, offsets, window)
-    for longest in (h for h in (0, 1, 512, 513, 2048) if h <= T):
+    for longest in (h for h in (0, 1, 128, 129, 256, 257, 512, 513, 2048) if h <= T):
         got = run_attention(eg2, gpu, q, k, v, offsets, window, longest=longest)
         assert np.array_equal(ref[0], got[0]) and np.array_equal(bits(ref[1]), bits(got[1])), longest
     assert_attention_bit_exact(*ref, oracle_attention(q, k, v, offsets, window))
