@@ -59,9 +59,8 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
                             const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
                             float* cd, hipStream_t st);
-// launch_attention's three stages, in that order (one kernel each, two for
-// the softmax of a packing longer than 2048 tokens or of unknown longest),
-// for callers that time them one by one.
+// launch_attention's three stages, in that order (one kernel each), for
+// callers that time them one by one.
 hipError_t launch_attention_scores(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
                                    int window, int rows, float* scores, hipStream_t st);
 hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, int longest, float* scores,

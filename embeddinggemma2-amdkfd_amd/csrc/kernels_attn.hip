@@ -45,18 +45,19 @@
 //    items in turn (the workgroups of an XCD, a contiguous eighth of the
 //    list) and stages the next quarter (the next item's first during the
 //    current item's last) while the current one computes.
-//  - attention_exp_kernel: one wave per (token, head): the row maximum,
-//    then every lane's expf of its keys, written back over the scores.
-//  - attention_sum_kernel: one lane per (token, head): the sum of its p
-//    row in key order (a serial chain, so 16 pairs share a wave's
-//    instructions), 1/sum into the scratch's head.
-//  - attention_softmax_kernel: the two above in one, for waves whose
-//    sequences are at most kLongSoftmax tokens: a workgroup of 16 waves
-//    (pairs; rows up to 512 keys) or 8 waves (up to 2048 keys, 66 KB of
-//    LDS, two workgroups per CU) keeps their p rows in LDS, and the first
-//    lanes of its first wave add them, one pair each: one read of the
-//    scores instead of the three of the two kernels, and the serial sums
-//    read the LDS instead of global memory.
+//  - the softmax, one kernel in one of four forms picked by the wave's
+//    longest sequence (the same operations in the same order in each):
+//    each (token, head) pair's row maximum, p = expf(score - m) written
+//    back over the scores, then the sum of the p row in key order (a serial
+//    chain: one lane per pair, the workgroup's pairs sharing each add
+//    instruction) and 1/sum into the scratch's head. Up to 512 keys the
+//    workgroup's 16 pairs keep their p rows in LDS for the sums, with 16 or
+//    32 lanes per pair up to 128 or 256 keys (attention_softmax_group_kernel)
+//    and a wave per pair beyond (attention_softmax_kernel); longer rows
+//    stream through a two-chunk LDS ring of 256 keys per pair, the first
+//    wave adding chunk c while the workgroup computes chunk c + 1
+//    (attention_softmax_ring_kernel, any length: every workgroup of a
+//    2048-token wave is resident at once).
 //  - attention_context_kernel: work items of (sequence, 32 pairs), each
 //    taken by 4 workgroups of 64 dimensions (768 workgroups for a wave of
 //    16 x 128 tokens or for one 2048-token sequence). Per 64-key chunk the
@@ -334,27 +335,24 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// The softmax in one kernel: one wave per (token, head) pair takes the row
+// The softmax of waves of sequences up to kShortSoftmax tokens: one wave per
+// (token, head) pair, 16 pairs per workgroup. Each wave takes the row
 // maximum, then every lane's p = expf(score - m) for its keys, written back
-// over the scores and, for a row of at most ROW keys, into the pair's LDS
-// row; then lane i of the first wave adds pair i's p values in key order (a
-// serial chain: the workgroup's pairs share each add instruction), reading
-// the LDS row 32 keys at a time with the next 32 in flight, and writes 1/sum
-// into the scratch's head. A longer row (a packing longer than the caller's
+// over the scores and into the pair's LDS row; then lane i of the first
+// wave adds pair i's p values in key order (a serial chain: the
+// workgroup's pairs share each add instruction) and writes 1/sum into the
+// scratch's head. A longer row (a packing longer than the caller's
 // `longest`) is summed from the scores in global memory instead: slower,
-// same bits. The same operations in the same order as attention_exp_kernel
-// followed by attention_sum_kernel, which packings with sequences over
-// kLongSoftmax tokens take instead.
-constexpr int kLongSoftmax = kCtx;  // longest row of the LDS softmax's long form
+// same bits.
+constexpr int kWavePairs = 16;
 
-template <int ROW, int PAIRS>
-__global__ void __launch_bounds__(64 * PAIRS)
+__global__ void __launch_bounds__(64 * kWavePairs)
 attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
   __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
-  __shared__ __align__(16) float prow[PAIRS][ROW + 4];  // each pair's p values from its first key (4 banks apart)
-  __shared__ uint32_t plen[PAIRS];                      // and their count (0: no such pair)
-  __shared__ uint32_t pbase[PAIRS];                     // index in scores of the row's first key
+  __shared__ __align__(16) float prow[kWavePairs][kShortSoftmax + 4];  // each pair's p values (4 banks apart)
+  __shared__ uint32_t plen[kWavePairs];                                // and their count (0: no such pair)
+  __shared__ uint32_t pbase[kWavePairs];                               // index in scores of the row's first key
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
   __syncthreads();
@@ -364,7 +362,7 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
   const uint32_t blk = gridDim.x % kXcdCount == 0
                            ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
                            : blockIdx.x;
-  const uint32_t pair = PAIRS * blk + w, t = pair / 3, h = pair % 3;
+  const uint32_t pair = kWavePairs * blk + w, t = pair / 3, h = pair % 3;
   uint32_t n = 0, base = 0;
   if (t < (uint32_t)rows) {
     const uint4 meta = tok[t];
@@ -375,45 +373,21 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
       float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
       n = last - first;
       base = meta.z + (3 * (t - lo) + h) * score_pitch(hi - lo) + (first - lo);
-      if (ROW > kShortSoftmax && n <= (uint32_t)ROW) {
-        // The row in registers (key first + lane + 64 i in v[i]): one read,
-        // every load in flight at once.
-        constexpr int kPer = ROW / 64;
-        float v[kPer];
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const uint32_t k = first + lane + 64 * i;
-          v[i] = k < last ? srow[k - lo] : -__builtin_inff();
-          m = fmaxf(m, v[i]);
-        }
-        m = wave_max(m);
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const uint32_t k = first + lane + 64 * i;
-          const float p = libm::expf_tab(v[i] - m, tab);  // computed for every slot: no branch per key
-          if (k < last) {
-            srow[k - lo] = p;
-            prow[w][k - first] = p;
-          }
-        }
-      } else {
-        // Short rows (and rows too long for the LDS): the maximum, then the
-        // exps, each a pass over the row (the second from the L2).
-        float m = -__builtin_inff();
-        uint32_t kt = first + lane;
-        for (; kt + 192 < last; kt += 256) {
-          const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
-          m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
-        }
-        for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
-        m = wave_max(m);
-        const bool to_lds = n <= (uint32_t)ROW;
-        for (uint32_t k = first + lane; k < last; k += 64) {
-          const float p = libm::expf_tab(srow[k - lo] - m, tab);
-          srow[k - lo] = p;
-          if (to_lds) prow[w][k - first] = p;
-        }
+      // The maximum, then the exps, each a pass over the row (the second
+      // from the L2).
+      float m = -__builtin_inff();
+      uint32_t kt = first + lane;
+      for (; kt + 192 < last; kt += 256) {
+        const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
+        m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+      }
+      for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
+      m = wave_max(m);
+      const bool to_lds = n <= (uint32_t)kShortSoftmax;
+      for (uint32_t k = first + lane; k < last; k += 64) {
+        const float p = libm::expf_tab(srow[k - lo] - m, tab);
+        srow[k - lo] = p;
+        if (to_lds) prow[w][k - first] = p;
       }
     }
   }
@@ -422,59 +396,16 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
     pbase[w] = base;
   }
   __syncthreads();
-  if (w == 0 && lane < PAIRS) {
+  if (w == 0 && lane < kWavePairs) {
     const uint32_t cnt = plen[lane];
-    const uint32_t own = PAIRS * blk + lane;
+    const uint32_t own = kWavePairs * blk + lane;
     if (cnt > 0) {
       float sum = 0.0f;
-      if (cnt <= (uint32_t)ROW) {
+      if (cnt <= (uint32_t)kShortSoftmax) {
+        // One 16-byte read at a time (22 VGPRs: the kernel shares its CUs
+        // with other lanes' work).
         const float* pr = prow[lane];
-        constexpr uint32_t kB = 8;  // float4 per batch
         uint32_t j = 0;
-        // Short rows: one 16-byte read at a time (22 VGPRs, not 68: the
-        // kernel shares its CUs with other lanes' work).
-        if (ROW > kShortSoftmax) {
-          // Batches of 32 keys in two register sets: a set is reloaded
-          // right after it is added, and added again only after the other
-          // set's 32 adds, which cover the read's latency.
-          const uint32_t nb = cnt / (4 * kB);
-          const float4* p4 = reinterpret_cast<const float4*>(pr);
-          float4 a[kB], b[kB];
-          auto load = [&](float4 (&x)[kB], uint32_t batch) {
-#pragma unroll
-            for (uint32_t i = 0; i < kB; ++i) x[i] = p4[kB * batch + i];
-          };
-          auto add = [&](const float4 (&x)[kB]) {
-#pragma unroll
-            for (uint32_t i = 0; i < kB; ++i) {
-              sum = sum + x[i].x;
-              sum = sum + x[i].y;
-              sum = sum + x[i].z;
-              sum = sum + x[i].w;
-            }
-          };
-          if (nb > 0) {
-            // Reads past the last batch are clamped to it (read again, not
-            // added), so every load is unconditional.
-            const uint32_t last_b = nb - 1;
-            load(a, 0);
-            load(b, min(1u, last_b));
-            for (uint32_t bt = 0; bt + 2 <= nb; bt += 2) {
-              // scheduling barriers keep each reload ahead of the other
-              // set's adds (the scheduler would sink it to its use)
-              add(a);
-              __builtin_amdgcn_sched_barrier(0);
-              load(a, min(bt + 2, last_b));
-              __builtin_amdgcn_sched_barrier(0);
-              add(b);
-              __builtin_amdgcn_sched_barrier(0);
-              load(b, min(bt + 3, last_b));
-              __builtin_amdgcn_sched_barrier(0);
-            }
-            if (nb & 1) add(a);
-          }
-          j = 4 * kB * nb;
-        }
 #pragma unroll 2
         for (; j + 4 <= cnt; j += 4) {
           const float4 p4 = *reinterpret_cast<const float4*>(pr + j);
@@ -489,7 +420,7 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
 #pragma unroll 1
         for (uint32_t j = 0; j < cnt; ++j) sum = sum + pr[j];
       }
-      scores[3 * (size_t)(own / 3) + own % 3] = 1.0f / sum;
+      scores[own] = 1.0f / sum;
     }
   }
 }
@@ -617,92 +548,138 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
   }
 }
 
-// One wave per (token, head) pair: the row maximum (order-free), then
-// every lane's p = expf(score - m) for its keys, written back over the
-// scores. The sums come in attention_sum_kernel.
-__global__ void __launch_bounds__(256)
-attention_exp_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
+// The softmax of rows of any length, streamed through LDS: one wave per
+// (token, head) pair, kRingPairs pairs per workgroup. Each wave takes its
+// row's maximum, then p = expf(score - m) a chunk of kRingKeys keys at a
+// time, written back over the scores and into the pair's slot of a
+// two-chunk LDS ring; lane i of the first wave adds pair i's p values in
+// key order from the ring, chunk c while the waves compute chunk c + 1 (a
+// barrier per chunk). The ring is 17 KB per workgroup where whole rows of
+// 2048 keys take 66 KB, so every pair of a 2048-token wave has its
+// workgroup resident at once and the serial sums run in one round. The same
+// operations in the same order as attention_softmax_kernel.
+constexpr int kRingPairs = 8;
+constexpr int kRingKeys = 256;
+
+// Six waves per SIMD (at most 80 VGPRs): three workgroups per CU, every
+// pair of a 2048-token wave resident at once.
+__global__ void __launch_bounds__(64 * kRingPairs, 6)
+attention_softmax_ring_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
+  __shared__ __align__(16) float ring[2][kRingPairs][kRingKeys + 4];  // pairs' chunks, 4 banks apart
+  __shared__ uint32_t plen[kRingPairs];                                // keys per pair (0: no such pair)
+  __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
-  __syncthreads();
-  const uint32_t pair = 4 * blockIdx.x + w, t = pair / 3, h = pair % 3;
-  if (t >= (uint32_t)rows) return;
-  const uint4 meta = tok[t];
-  const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
-  if (t < lo || t >= hi) return;  // a malformed entry: nothing is written for this token
-  uint32_t first, last;
-  key_range(t, lo, hi, window, first, last);
-  float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
-  float m = -__builtin_inff();
-  uint32_t kt = first + lane;
-  for (; kt + 192 < last; kt += 256) {
-    const float a = srow[kt - lo], b = srow[kt - lo + 64], c = srow[kt - lo + 128], d = srow[kt - lo + 192];
-    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
-  }
-  for (; kt < last; kt += 64) m = fmaxf(m, srow[kt - lo]);
-  m = wave_max(m);
-  for (uint32_t k = first + lane; k < last; k += 64) srow[k - lo] = libm::expf_tab(srow[k - lo] - m, tab);
-}
-
-// sum = p[first] + p[first + 1] + ... in key order for each (token, head)
-// pair, then 1/sum into the scratch's head at [3 t + h]. The sum is a
-// serial chain, so a lane takes a whole pair: lanes 0-15 of each wave,
-// 16 pairs per wave (more waves to overlap the row reads than 64 pairs
-// per wave would give), the row read in batches of 32 keys with the next
-// three batches in flight while the current one is added.
-constexpr int kSumPairsPerWave = 16;
-constexpr int kSumBatch = 8;  // float4 per batch
-constexpr int kSumRing = 4;   // batches in the ring
-
-__global__ void __launch_bounds__(256)
-attention_sum_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane >= kSumPairsPerWave) return;
-  const uint32_t pair = (blockIdx.x * 4 + w) * kSumPairsPerWave + lane, t = pair / 3, h = pair % 3;
-  if (t >= (uint32_t)rows) return;
-  const uint4 meta = tok[t];
-  const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
-  if (t < lo || t >= hi) return;
-  uint32_t first, last;
-  key_range(t, lo, hi, window, first, last);
-  const float* srow = scores + meta.z + ((size_t)3 * (t - lo) + h) * score_pitch(hi - lo);  // key kt at srow[kt - lo]
-  uint32_t k = first - lo;
-  const uint32_t end = last - lo;
-  float sum = 0.0f;
-  for (; (k & 3) != 0 && k < end; ++k) sum = sum + srow[k];  // up to the row's next 16-byte boundary
-  const uint32_t n4 = (end - k) / 4;                         // whole float4 of the row from k
-  const float4* r4 = reinterpret_cast<const float4*>(srow + k);
-  // A ring of kSumRing batches: batch i is added while batches i + 1 ..
-  // i + kSumRing - 1 are in flight.
-  float4 ring[kSumRing][kSumBatch];
-  auto load = [&](float4 (&dst)[kSumBatch], uint32_t j0) {
-#pragma unroll
-    for (int j = 0; j < kSumBatch; ++j) dst[j] = r4[min(j0 + j, n4 - 1)];
-  };
-  if (n4 > 0) {
-#pragma unroll
-    for (int b = 0; b < kSumRing - 1; ++b) load(ring[b], b * kSumBatch);
-  }
-  for (uint32_t j0 = 0; j0 < n4; j0 += kSumRing * kSumBatch) {
-#pragma unroll
-    for (int b = 0; b < kSumRing; ++b) {
-      const uint32_t jb = j0 + b * kSumBatch;
-      if (jb >= n4) break;
-      load(ring[(b + kSumRing - 1) % kSumRing], jb + (kSumRing - 1) * kSumBatch);
-#pragma unroll
-      for (int j = 0; j < kSumBatch; ++j) {
-        if (jb + j < n4) {
-          sum = sum + ring[b][j].x;
-          sum = sum + ring[b][j].y;
-          sum = sum + ring[b][j].z;
-          sum = sum + ring[b][j].w;
-        }
-      }
+  // XCD-aware order, as in attention_softmax_kernel.
+  const uint32_t blk = gridDim.x % kXcdCount == 0
+                           ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
+                           : blockIdx.x;
+  const uint32_t pair = kRingPairs * blk + w, t = pair / 3, h = pair % 3;
+  uint32_t n = 0, base = 0;
+  if (t < (uint32_t)rows) {
+    const uint4 meta = tok[t];
+    const uint32_t hi = min(meta.y, (uint32_t)rows), lo = min(meta.x, hi);
+    if (t >= lo && t < hi) {  // else a malformed entry: nothing is written for this token
+      uint32_t first, last;
+      key_range(t, lo, hi, window, first, last);
+      n = last - first;
+      base = meta.z + (3 * (t - lo) + h) * score_pitch(hi - lo) + (first - lo);
     }
   }
-  for (k += 4 * n4; k < end; ++k) sum = sum + srow[k];
-  scores[3 * (size_t)t + h] = 1.0f / sum;
+  if (lane == 0) plen[w] = n;
+  __syncthreads();
+  uint32_t chunks = 0;  // the workgroup's chunk count: its longest row's
+#pragma unroll
+  for (int i = 0; i < kRingPairs; ++i) chunks = max(chunks, (plen[i] + kRingKeys - 1) / kRingKeys);
+  float* row = scores + base;  // key first + k at row[k]
+  float m = -__builtin_inff();
+  uint32_t k = lane;
+  for (; k + 192 < n; k += 256) {
+    const float a = row[k], b = row[k + 64], c = row[k + 128], d = row[k + 192];
+    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+  }
+  for (; k < n; k += 64) m = fmaxf(m, row[k]);
+  m = wave_max(m);
+  // Chunk c of this wave's row: lane l takes keys kRingKeys c + l + 64 j.
+  constexpr int kPer = kRingKeys / 64;
+  float s[kPer];
+  auto load = [&](uint32_t c) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const uint32_t kk = kRingKeys * c + (uint32_t)lane + 64 * j;
+      s[j] = kk < n ? row[kk] : 0.0f;
+    }
+  };
+  auto put = [&](uint32_t c) {
+    float* slot = ring[c & 1][w];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const uint32_t kk = kRingKeys * c + (uint32_t)lane + 64 * j;
+      const float p = libm::expf_tab(s[j] - m, tab);  // computed for every slot: no branch per key
+      if (kk < n) {
+        row[kk] = p;
+        slot[lane + 64 * j] = p;
+      }
+    }
+  };
+  if (chunks > 0) {
+    load(0);
+    put(0);
+  }
+  __syncthreads();
+  const bool adder = w == 0 && lane < kRingPairs;
+  const uint32_t cnt = adder ? plen[lane] : 0;
+  float sum = 0.0f;
+  for (uint32_t c = 0; c < chunks; ++c) {
+    if (c + 1 < chunks) load(c + 1);
+    if (adder && kRingKeys * c < cnt) {
+      const float* pr = ring[c & 1][lane];
+      const uint32_t m4 = min((uint32_t)kRingKeys, cnt - kRingKeys * c);
+      uint32_t j = 0;
+      // Batches of 32 keys in two register sets: a set is reloaded right
+      // after it is added and added again only after the other set's 32
+      // adds, which cover the read's latency (reads past the chunk's end
+      // stay inside the slot and are not added).
+      const float4* p4 = reinterpret_cast<const float4*>(pr);
+      constexpr uint32_t kB = 8, kSets = kRingKeys / (4 * kB);
+      const uint32_t nb = m4 / (4 * kB);
+      float4 a[kB], b[kB];
+      auto fill = [&](float4 (&x)[kB], uint32_t batch) {
+#pragma unroll
+        for (uint32_t i = 0; i < kB; ++i) x[i] = p4[kB * min(batch, kSets - 1) + i];
+      };
+      auto add = [&](const float4 (&x)[kB]) {
+#pragma unroll
+        for (uint32_t i = 0; i < kB; ++i) {
+          sum = sum + x[i].x;
+          sum = sum + x[i].y;
+          sum = sum + x[i].z;
+          sum = sum + x[i].w;
+        }
+      };
+      if (nb > 0) {
+        fill(a, 0);
+        fill(b, 1);
+        for (uint32_t bt = 0; bt + 2 <= nb; bt += 2) {
+          add(a);
+          __builtin_amdgcn_sched_barrier(0);
+          fill(a, bt + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          add(b);
+          __builtin_amdgcn_sched_barrier(0);
+          fill(b, bt + 3);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (nb & 1) add(a);
+        j = 4 * kB * nb;
+      }
+      for (; j < m4; ++j) sum = sum + pr[j];
+    }
+    if (c + 1 < chunks) put(c + 1);
+    __syncthreads();
+  }
+  if (adder && cnt > 0) scores[kRingPairs * blk + (uint32_t)lane] = 1.0f / sum;
 }
 
 // ---------------------------------------------------------------- context
@@ -1014,23 +991,12 @@ hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, i
   if (longest > 0 && longest <= kGroup16Softmax) return launch_group_softmax<16>(tok, window, rows, scores, st);
   if (longest > 0 && longest <= kGroup32Softmax) return launch_group_softmax<32>(tok, window, rows, scores, st);
   if (longest > 0 && longest <= kShortSoftmax) {
-    constexpr int kPairs = 16;
-    hipLaunchKernelGGL((attention_softmax_kernel<kShortSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
-                       dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+    hipLaunchKernelGGL(attention_softmax_kernel, dim3((3 * rows + kWavePairs - 1) / kWavePairs), dim3(64 * kWavePairs),
+                       0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
     return hipGetLastError();
   }
-  if (longest > 0 && longest <= kLongSoftmax) {
-    constexpr int kPairs = 8;  // 66 KB of p rows: two workgroups per CU
-    hipLaunchKernelGGL((attention_softmax_kernel<kLongSoftmax, kPairs>), dim3((3 * rows + kPairs - 1) / kPairs),
-                       dim3(64 * kPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(attention_exp_kernel, dim3(3 * rows / 4), dim3(256), 0, st, scores,
-                     reinterpret_cast<const uint4*>(tok), window, rows);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attention_sum_kernel, dim3((3 * rows + 4 * kSumPairsPerWave - 1) / (4 * kSumPairsPerWave)),
-                     dim3(256), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
+  hipLaunchKernelGGL(attention_softmax_ring_kernel, dim3((3 * rows + kRingPairs - 1) / kRingPairs),
+                     dim3(64 * kRingPairs), 0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
   return hipGetLastError();
 }
 
@@ -1064,8 +1030,8 @@ hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint3
 // of at most kStaticRows rows into at most kStaticBatch sequences fits
 // (the bounds of attention_capacity). Nothing in it has to start at zero:
 // the plan kernel writes the counts and every record the other kernels
-// read, the sum kernel every 1/sum the context kernel reads, and the
-// exp, sum and context kernels use only scores written in the same call.
+// read, the softmax kernel every 1/sum the context kernel reads, and the
+// softmax and context kernels use only scores written in the same call.
 // Calls that overlap on one GPU share the array and race.
 
 constexpr size_t kStaticRows = 2048, kStaticBatch = 2048;

@@ -72,9 +72,9 @@ int eg2_hip_qk_norm_rope(const float *qkv, const float *q_w, const float *k_w, c
  * of the `rows` rows, so every row must belong to a planned sequence, e.g.
  * a padding one. scores: scratch of at least the plan's score floats
  * (counts[1]). rows % 4 == 0. longest: the longest sequence of the
- * packing, a hint (at most rows) that picks one of three equivalent
- * softmax kernel forms (<= 512, <= 2048, 0 = not known); a wrong hint
- * costs time, never bits. A sequence's result does not depend on its place
+ * packing, a hint (at most rows) that picks one of four equivalent
+ * softmax kernel forms (<= 128, <= 256, <= 512, and any length for a
+ * longer or unknown (0) longest); a wrong hint costs time, never bits. A sequence's result does not depend on its place
  * in the wave. Replaces kernels/eg2.c:145-170 eg2_attention256. */
 int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *item_count, unsigned grid,
                       const uint32_t *tok, unsigned window, unsigned rows, unsigned longest, float *scores, int8_t *cq,
@@ -84,7 +84,7 @@ int eg2_hip_attention(const float *qkv, const uint32_t *items, const uint32_t *i
  * arguments and checks; run in this order they are eg2_hip_attention):
  * the scores of every planned (token, head, key) into `scores`; the
  * softmax of each score row in place (p values) with 1/sum at the head of
- * `scores` (two kernels when longest is 0 or above 2048); the context,
+ * `scores`; the context,
  * quantized to Q8_0 into cq / cd. For per-kernel timing (the reference
  * times each dispatch, src/gemma2_kfd.cpp:173-186). Replace, together,
  * kernels/eg2.c:145-170 eg2_attention256. */

@@ -606,13 +606,12 @@ def test_attention_independent_of_packing(eg2, gpu, window):
 @pytest.mark.parametrize("window", [0, 64])
 @pytest.mark.parametrize("lens", [[1, 130, 512, 7, 300], [1, 513, 2, 1200, 37]])
 def test_attention_softmax_forms_agree(eg2, gpu, window, lens):
-    """The one-kernel softmax forms (16 or 32 lanes per pair for waves of
-    sequences up to 128 or 256 tokens, a wave per pair up to 512, 8 pairs
-    with rows up to 2048 keys in LDS otherwise) and the exp + serial-sum
-    pair (any length) give the same bits, and so does a `longest` below the
-    wave's real longest sequence (rows too long for the chosen form's LDS are
-    summed from global memory): the hint picks a kernel form, never the
-    results."""
+    """The softmax forms (16 or 32 lanes per pair for waves of sequences up
+    to 128 or 256 tokens, a wave per pair up to 512, rows streamed through
+    an LDS ring for any length) give the same bits, and so does a `longest`
+    below the wave's real longest sequence (rows too long for the chosen
+    form's LDS are summed from global memory): the hint picks a kernel form,
+    never the results."""
     rng = np.random.default_rng(10 + len(lens))
     T = sum(lens)
     offsets = np.concatenate([[0], np.cumsum(lens)])
