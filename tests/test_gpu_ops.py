@@ -564,10 +564,12 @@ def test_attention_packed_bit_exact(eg2, gpu, window):
 
 
 @pytest.mark.parametrize("lens,window", [([1100, 600, 300, 48], 0), ([2048], 0), ([700, 5, 900], 64),
-                                         ([30, 31, 3], 1), ([17, 40], 2)])
+                                         ([30, 31, 3], 1), ([17, 40], 2), ([2500, 52], 0), ([2600], 512)])
 def test_attention_long_and_windowed_bit_exact(eg2, gpu, lens, window):
-    """Long sequences (many 64-key blocks and query chunks) and narrow
-    windows (down to the token and its neighbours): the oracle's bits."""
+    """Long sequences (many 64-key blocks and query chunks, and rows past
+    the 2048 keys of an executor wave: ten chunks of the softmax's LDS ring)
+    and narrow windows (down to the token and its neighbours): the oracle's
+    bits."""
     rng = np.random.default_rng(sum(lens) + window)
     T = sum(lens)
     offsets = np.concatenate([[0], np.cumsum(lens)])
