@@ -56,6 +56,11 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // into cq (row tiles, k = 768) and cd [24][rows]. rows % 4 == 0. longest:
 // the longest sequence of the packing, which picks the softmax's kernel
 // form (0 = not known: the form for any length); the results are the same.
+// The forms change at these lengths: up to kSoftmaxLanes16 tokens 16 lanes
+// per (token, head) pair, up to kSoftmaxLanes32 32 lanes, up to
+// kSoftmaxWave a wave per pair, any length beyond (a caller that keeps one
+// graph per form can round its longest up to the next of them).
+constexpr int kSoftmaxLanes16 = 128, kSoftmaxLanes32 = 256, kSoftmaxWave = 512;
 hipError_t launch_attention(const float* qkv, const uint32_t* items, const uint32_t* item_count, int grid,
                             const uint32_t* tok, int window, int rows, int longest, float* scores, int8_t* cq,
                             float* cd, hipStream_t st);

@@ -43,12 +43,22 @@ namespace {
 
 constexpr unsigned kCap = 2048;  // packed tokens per wave (src/gemma2_kfd.cpp:20)
 constexpr unsigned kPoolSplitLen = 256;  // longest sequence above which pooling spreads over columns
-// The attention's softmax takes one of two equivalent kernel forms by the
-// wave's longest sequence (up to 512 tokens: 16 pairs per workgroup, else
-// 8); a graph is kept per padded row count and form.
-constexpr unsigned kShortSoftmaxLen = 512;
-inline unsigned attention_form(unsigned longest) { return longest <= kShortSoftmaxLen ? kShortSoftmaxLen : kCap; }
-inline unsigned graph_key(unsigned rows, unsigned longest) { return 2 * rows + (longest <= kShortSoftmaxLen ? 1 : 0); }
+// The attention's softmax takes one of four equivalent kernel forms by the
+// wave's longest sequence (eg2::kSoftmaxLanes16, kSoftmaxLanes32,
+// kSoftmaxWave, longer); a graph is kept per padded row count and form, and
+// records the form's bound as its longest.
+inline unsigned softmax_form(unsigned longest) {
+  return longest <= (unsigned)eg2::kSoftmaxLanes16 ? 0u
+         : longest <= (unsigned)eg2::kSoftmaxLanes32 ? 1u
+         : longest <= (unsigned)eg2::kSoftmaxWave ? 2u
+                                                  : 3u;
+}
+inline unsigned attention_form(unsigned longest) {
+  const unsigned bound[4] = {(unsigned)eg2::kSoftmaxLanes16, (unsigned)eg2::kSoftmaxLanes32,
+                             (unsigned)eg2::kSoftmaxWave, kCap};
+  return bound[softmax_form(longest)];
+}
+inline unsigned graph_key(unsigned rows, unsigned longest) { return 4 * rows + softmax_form(longest); }
 constexpr int kEmbd = 768, kFF = 1152, kHeadDim = 256, kQKV = 768 + 2 * 256, kDenseFF = 3072;
 constexpr int kVocab = 262144;
 constexpr double kTimeoutSeconds = 30.0;  // src/gemma2_kfd.cpp:21

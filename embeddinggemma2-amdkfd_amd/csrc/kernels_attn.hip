@@ -92,9 +92,7 @@ constexpr int kSKeys = 32, kSPairs = 32;  // scores workgroup tile
 constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
 constexpr int kCKeys = 64;                // keys per staged chunk
 constexpr int kCPitchV = kCDims + 4;       // floats per row of the context's epilogue tile
-constexpr int kShortSoftmax = 512;        // longest sequence for the 16-pair one-kernel softmax
-constexpr int kGroup16Softmax = 128;      // longest for the softmax with 16 lanes per pair
-constexpr int kGroup32Softmax = 256;      // and with 32
+constexpr int kShortSoftmax = kSoftmaxWave;  // longest row of the softmax forms that keep p rows in LDS
 constexpr int kCBatch = 4;                // context MFMAs in flight per wave
 constexpr uint32_t kXcdCount = 8;         // MI355X: 8 XCDs, workgroup b on XCD b % 8
 
@@ -988,8 +986,8 @@ hipError_t launch_group_softmax(const uint32_t* tok, int window, int rows, float
 hipError_t launch_attention_softmax(const uint32_t* tok, int window, int rows, int longest, float* scores,
                                     hipStream_t st) {
   if (rows <= 0 || rows % 4 != 0 || window < 0 || longest < 0) return hipErrorInvalidValue;
-  if (longest > 0 && longest <= kGroup16Softmax) return launch_group_softmax<16>(tok, window, rows, scores, st);
-  if (longest > 0 && longest <= kGroup32Softmax) return launch_group_softmax<32>(tok, window, rows, scores, st);
+  if (longest > 0 && longest <= kSoftmaxLanes16) return launch_group_softmax<16>(tok, window, rows, scores, st);
+  if (longest > 0 && longest <= kSoftmaxLanes32) return launch_group_softmax<32>(tok, window, rows, scores, st);
   if (longest > 0 && longest <= kShortSoftmax) {
     hipLaunchKernelGGL(attention_softmax_kernel, dim3((3 * rows + kWavePairs - 1) / kWavePairs), dim3(64 * kWavePairs),
                        0, st, scores, reinterpret_cast<const uint4*>(tok), window, rows);
