@@ -42,8 +42,13 @@ def run_oracle(path, ids, offsets):
     return OL.forward(gguf_py.oracle_model(path), ids, np.asarray(offsets, np.uint64), threads=16)
 
 
-@pytest.mark.parametrize("lens", [[5], [1, 1, 1], [37, 3, 100, 1, 64], [700, 300, 1], [2048]])
+@pytest.mark.parametrize("lens", [[5], [1, 1, 1], [37, 3, 100, 1, 64], [200, 50, 9], [400, 7, 90], [700, 300, 1],
+                                  [2048]])
 def test_small_model_parity(small_encoder, small_model, lens):
+    """3-layer model, several packings (single token, many tiny sequences,
+    ragged, long, one full 2048-token wave; their longest sequences pick
+    each of the softmax's four kernel forms): bit-exact vs the oracle's
+    embeddings."""
     rng = np.random.default_rng(sum(lens))
     ids = rng.integers(0, OL.VOCAB, sum(lens)).astype(np.int32)
     offsets = np.concatenate([[0], np.cumsum(lens)])
