@@ -429,10 +429,12 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
 // maximum's combination. Lane j of a pair's LANES takes keys
 // first + j + LANES i: the row maximum (order-free; combined over the pair's
 // lanes by DPP), then p = expf(score - m) written back over the scores and
-// into the pair's LDS row; then lane i of the first wave adds pair i's p
-// values in key order and writes 1/sum into the scratch's head. A row longer
-// than kShortSoftmax (a packing longer than the caller's `longest`) is summed
-// from the scores in global memory instead: slower, same bits. The same
+// into the pair's LDS row (as long as the form's bound, kSoftmaxLanes16 or
+// kSoftmaxLanes32 keys: 8 or 17 KB per workgroup, which leaves room on a CU
+// for other lanes' kernels); then lane i of the first wave adds pair i's p
+// values in key order and writes 1/sum into the scratch's head. A longer
+// row (a packing longer than the caller's `longest`) is summed from the
+// scores in global memory instead: slower, same bits. The same
 // operations in the same order as attention_softmax_kernel, which takes
 // waves of longer sequences (fewer pairs per wave hide more latency there).
 constexpr int kGroupPairs = 16;  // pairs per workgroup
@@ -460,7 +462,8 @@ template <int LANES>
 __global__ void __launch_bounds__(LANES * kGroupPairs)
 attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restrict__ tok, int window, int rows) {
   __shared__ uint64_t tab[32];
-  __shared__ __align__(16) float prow[kGroupPairs][kShortSoftmax + 4];  // each pair's p values (4 banks apart)
+  constexpr int kRow = LANES == 16 ? kSoftmaxLanes16 : kSoftmaxLanes32;  // the form's longest row
+  __shared__ __align__(16) float prow[kGroupPairs][kRow + 4];  // each pair's p values (4 banks apart)
   __shared__ uint32_t plen[kGroupPairs];                                // and their count (0: no such pair)
   __shared__ uint32_t pbase[kGroupPairs];                               // index in scores of the row's first key
   __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
@@ -492,7 +495,7 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
   }
   for (; j < n; j += LANES) m = fmaxf(m, row[j]);
   m = group_max<LANES>(m);
-  const bool to_lds = n <= (uint32_t)kShortSoftmax;
+  const bool to_lds = n <= (uint32_t)kRow;
   float* lrow = prow[slot];
   for (j = sub; j + 3 * LANES < n; j += 4 * LANES) {
     const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
@@ -524,7 +527,7 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
     const uint32_t own = kGroupPairs * blk + tid;
     if (cnt > 0) {
       float sum = 0.0f;
-      if (cnt <= (uint32_t)kShortSoftmax) {
+      if (cnt <= (uint32_t)kRow) {
         const float* pr = prow[tid];
         uint32_t k = 0;
 #pragma unroll 2
