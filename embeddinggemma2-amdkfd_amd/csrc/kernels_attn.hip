@@ -34,7 +34,7 @@
 //    listed pair block by pair block (an XCD's contiguous share of a long
 //    sequence then needs a band of q rows and the k rows, which fit its L2).
 //    The workgroup stages the q rows of its pairs and the k rows of its
-//    keys in LDS by 16-byte DMA (no registers), 64 dimensions at a time,
+//    keys in LDS by 16-byte DMA (no registers), 32 dimensions at a time,
 //    laid out [16-row block][4-dimension chunk][row] so that the lane of
 //    chain c and row r reads chunk s's element c with a 4-byte read and
 //    the wave's 64 lanes hit 64 distinct banks. Each wave owns 16 pairs x
@@ -43,8 +43,8 @@
 //    adds its 16 products to its 4 pairs' 4 chain sums. The scores go to a
 //    scratch row per pair (row length rounded up to 4). A workgroup takes
 //    items in turn (the workgroups of an XCD, a contiguous eighth of the
-//    list) and stages the next quarter (the next item's first during the
-//    current item's last) while the current one computes.
+//    list) and stages the next stage of 32 dimensions (the next item's
+//    first during the current item's last) while the current one computes.
 //  - the softmax, one kernel in one of four forms picked by the wave's
 //    longest sequence (the same operations in the same order in each):
 //    each (token, head) pair's row maximum, p = expf(score - m) written
@@ -121,22 +121,25 @@ __host__ __device__ inline void key_range(uint32_t t, uint32_t lo, uint32_t hi, 
 
 // ----------------------------------------------------------------- scores
 
-// The scores' staging: per item, four quarters of 64 dimensions, each a
+// The scores' staging: per item, eight stages of 32 dimensions, each a
 // plain copy by 16-byte LDS DMA into blocks of 16 rows (block 0, 1: the q
 // rows of pairs pair0 .. + 15, + 16 .. + 31; block 2, 3: the k rows of keys
 // key0 .. + 15, + 16 .. + 31), laid out [block][chunk][row] with a chunk =
 // 4 dimensions (all four chains at one step). A lane of chain g and row
 // r16 reads its step-s value with one 4-byte read at chunk s, row r16,
-// element g: the wave's 64 lanes touch 64 distinct banks.
-constexpr int kSQDims = 64;
+// element g: the wave's 64 lanes touch 64 distinct banks. Two buffers of
+// 8 KB: at 16 KB per workgroup the kernel leaves room on a CU for the
+// other lanes' kernels (with 64-dimension stages, 32 KB, it ran 1-7%
+// slower at 16-512 keys and the 16 x 128 forward 0.8% slower).
+constexpr int kSQDims = 32;
 constexpr int kSQChunks = kSQDims / 4;
 constexpr int kSBlockFloats = kSQChunks * 16 * 4;  // one block of 16 rows
 
-// One staged quarter of the wave's 16 pairs x 16 keys: per kSBatch steps
+// One stage of the wave's 16 pairs x 16 keys: per kSBatch steps
 // that many MFMAs into separate registers, then their adds, with the next
 // steps' operands read from LDS before the adds.
 constexpr int kSBatch = 2;
-__device__ __forceinline__ void scores_quarter(const float* qa, const float* kb, float (&acc)[4][4]) {
+__device__ __forceinline__ void scores_stage(const float* qa, const float* kb, float (&acc)[4][4]) {
   const floatx16 zero = {};
   float qv[kSBatch], kv[kSBatch];
 #pragma unroll
@@ -250,9 +253,9 @@ __device__ __forceinline__ uint32_t next_score_item(const uint4* __restrict__ it
   return item;
 }
 
-// The workgroup takes items in turn (grid-stride); each quarter's rows are
-// staged by DMA into one of two LDS buffers while the previous quarter
-// computes (the next item's first quarter during the current item's last).
+// The workgroup takes items in turn (grid-stride); each stage's rows are
+// staged by DMA into one of two LDS buffers while the previous stage
+// computes (the next item's first stage during the current item's last).
 __global__ void __launch_bounds__(256)
 attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__ items,
                                  const uint32_t* __restrict__ item_count, int window, int rows,
@@ -302,7 +305,7 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
     uint32_t nitem = count;
 #pragma unroll 1
     for (int q = 0; q < kHeadDim / kSQDims; ++q) {
-      // This wave's DMA of the quarter has landed; after the barrier every
+      // This wave's DMA of the stage has landed; after the barrier every
       // wave's has, and the other buffer is no longer read.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -316,7 +319,7 @@ attention_scores_kernel(const float* __restrict__ qkv, const uint4* __restrict__
         }
       }
       const float* base = stg[buf] + 4 * r16 + g;  // chunk s of row r16 at 64 s + 4 r16
-      scores_quarter(base + (w >> 1) * kSBlockFloats, base + (2 + (w & 1)) * kSBlockFloats, acc);
+      scores_stage(base + (w >> 1) * kSBlockFloats, base + (2 + (w & 1)) * kSBlockFloats, acc);
       buf ^= 1;
     }
     store_scores(acc, t.lo, t.hi, t.key0, t.pair0, t.pair1, t.sbase, window, pr, kr, g, r16, scores);
