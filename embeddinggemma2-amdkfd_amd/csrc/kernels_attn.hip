@@ -90,7 +90,9 @@ constexpr int kKOff = kHeads * kHeadDim, kVOff = kKOff + kHeadDim;
 
 constexpr int kSKeys = 32, kSPairs = 32;  // scores workgroup tile
 constexpr int kCPairs = 32, kCDims = 64;  // context workgroup tile
-constexpr int kCKeys = 64;                // keys per staged chunk
+constexpr int kCKeys = 64;                // keys per staged chunk (a multiple of 32)
+constexpr int kCWKeys = kCKeys / 8;       // keys per thread in the w staging (8 threads per pair)
+static_assert(kCKeys % 32 == 0, "whole float4s per staging thread, whole DMA instructions per wave");
 constexpr int kCPitchV = kCDims + 4;       // floats per row of the context's epilogue tile
 constexpr int kShortSoftmax = kSoftmaxWave;  // longest row of the softmax forms that keep p rows in LDS
 constexpr int kCBatch = 4;                // context MFMAs in flight per wave
@@ -733,47 +735,48 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
     for (int v = 0; v < 8; ++v) acc[v] = 0.0f;
     // w staging: thread (pair tid % 32, the 8 keys 8 (tid / 32) ..), from
     // registers loaded while the previous chunk is computed.
-    const uint32_t wp = (uint32_t)tid & (kCPairs - 1), wk = 8 * ((uint32_t)tid / kCPairs);
+    const uint32_t wp = (uint32_t)tid & (kCPairs - 1), wk = kCWKeys * ((uint32_t)tid / kCPairs);
     const uint32_t wpair = min(pair0 + wp, pair1 - 1);
     const float winv = scores[3 * (size_t)(lo + wpair / 3) + wpair % 3];
     const float* wsrc = scores + sbase + (size_t)wpair * pitch;
     uint32_t wfirst, wlast;
     key_range(lo + wpair / 3, lo, hi, window, wfirst, wlast);
     if (pair0 + wp >= pair1) wlast = wfirst;  // no such pair: w = 0
-    float4 pw[2];
+    float4 pw[kCWKeys / 4];
     auto load_w = [&](uint32_t c0) {
       if (inside(c0)) {  // uniform: no bound
 #pragma unroll
-        for (int j4 = 0; j4 < 2; ++j4)
+        for (int j4 = 0; j4 < kCWKeys / 4; ++j4)
           pw[j4] = *reinterpret_cast<const float4*>(wsrc + (c0 + wk + 4 * j4 - lo));
         return;
       }
 #pragma unroll
-      for (int j4 = 0; j4 < 2; ++j4) {
+      for (int j4 = 0; j4 < kCWKeys / 4; ++j4) {
         const uint32_t k4 = c0 + wk + 4 * j4;  // 4 keys, 16-byte aligned in the row
         pw[j4] = k4 - lo < pitch ? *reinterpret_cast<const float4*>(wsrc + (k4 - lo))
                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     };
-    // v staging by DMA, no registers: wave w moves keys c0 + 16 w .. + 15 of
-    // the chunk, 4 keys (64 lanes x 16 bytes) per instruction. Keys past the
+    // v staging by DMA, no registers: wave w moves keys c0 + R w .. + R - 1
+    // of the chunk (R = kCKeys / 4), 4 keys (64 lanes x 16 bytes) per
+    // instruction. Keys past the
     // sequence read its last row: every pair's w is 0 there (a finite v
     // times +0 adds +0 or -0, which changes no sum). Byte offsets are taken
     // from the sequence's first row, so that 32 bits hold them for any row
     // count (a planned sequence is below 37,838 rows: 194 MB of qkv).
     const float* seq = qkv + (size_t)lo * kLd;
-    // Row min(c0 + 16 w + 4 i + lane / 16, hi - 1) as a scalar base row
+    // Row min(c0 + R w + 4 i + lane / 16, hi - 1) as a scalar base row
     // (clamped) plus a per-lane step of 0..3 (clamped to what is left).
     auto issue_v = [&](uint32_t c0, int buf) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t brow = min(c0 - lo + 16 * (uint32_t)w + 4 * i, hi - 1 - lo);  // uniform
+      for (int i = 0; i < kCKeys / 16; ++i) {
+        const uint32_t brow = min(c0 - lo + (kCKeys / 4) * (uint32_t)w + 4 * i, hi - 1 - lo);  // uniform
         const uint32_t step = min((uint32_t)(lane >> 4), hi - 1 - lo - brow);
         dma16(seq + (size_t)brow * kLd, __umul24(step, kLd * 4u) + (uint32_t)(kVOff + dblk) * 4u + 16u * (uint32_t)(lane & 15),
-              vl0 + (unsigned)buf * (kCKeys * kCDims * 4) + (16 * w + 4 * i) * (kCDims * 4));
+              vl0 + (unsigned)buf * (kCKeys * kCDims * 4) + ((kCKeys / 4) * w + 4 * i) * (kCDims * 4));
       }
     };
-    __syncthreads();  // the previous item's epilogue tile (in vl[0]) is no longer read
+    __syncthreads();  // the previous item's epilogue tile (in vl) is no longer read
     if (kfirst < klast) {
       issue_v(kfirst, 0);
       load_w(kfirst);
@@ -786,14 +789,14 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
       __syncthreads();
       if (inside(c0)) {
 #pragma unroll
-        for (int j4 = 0; j4 < 2; ++j4) {
+        for (int j4 = 0; j4 < kCWKeys / 4; ++j4) {
           const float pr[4] = {pw[j4].x, pw[j4].y, pw[j4].z, pw[j4].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) wl[(wk + 4 * j4 + e) * kCPairs + wp] = pr[e] * winv;
         }
       } else {
 #pragma unroll
-        for (int j4 = 0; j4 < 2; ++j4) {
+        for (int j4 = 0; j4 < kCWKeys / 4; ++j4) {
           const float pr[4] = {pw[j4].x, pw[j4].y, pw[j4].z, pw[j4].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -847,10 +850,11 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
         }
       }
     }
-    // Through LDS (the first v chunk's space) to [pair][64 dimensions], then
+    // Through LDS (the v chunks' space) to [pair][64 dimensions], then
     // Q8_0: block (32 values) of 4 lanes x 8 values.
+    static_assert(kCPairs * kCPitchV <= 2 * kCKeys * kCDims, "the epilogue tile fits in the v buffers");
     __syncthreads();
-    float* tile = vl[0];  // kCPairs x kCPitchV floats
+    float* tile = &vl[0][0];  // kCPairs x kCPitchV floats
 #pragma unroll
     for (int v = 0; v < 8; ++v) tile[(16 * (v >> 2) + 4 * g + (v & 3)) * kCPitchV + 16 * w + r16] = acc[v];
     __syncthreads();
