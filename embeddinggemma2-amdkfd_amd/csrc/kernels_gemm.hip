@@ -222,7 +222,12 @@ __device__ __forceinline__ void geglu_epilogue(const floatx16& acc, int tr, int 
 // layout is the MFMA's register order: lane L's 16 bytes of a block are
 // one load at 16 L) by buffer loads with a scalar offset per block, kDepth
 // blocks ahead, with no LDS and no barrier: the waves of a workgroup never
-// wait for each other. Returns the tile in the 32x32 MFMA output layout.
+// wait for each other. Each scale array is read through one descriptor,
+// block kb's row at the scalar offset 4 kb ld (the launchers keep both
+// arrays below 4 GiB: scales_fit), so a block's scale loads cost one
+// scalar multiply each rather than a new 64-bit base and descriptor (12
+// scalar instructions fewer per block and wave). Returns the tile in the
+// 32x32 MFMA output layout.
 template <bool TAIL>
 __device__ __forceinline__ floatx16 q8_block_loop(const int8_t* atile, const float* __restrict__ xd, int ldx, int n,
                                                   uint32_t xoff, const int8_t* btile, const float* __restrict__ wd,
@@ -231,6 +236,9 @@ __device__ __forceinline__ floatx16 q8_block_loop(const int8_t* atile, const flo
   // address is kept per block in flight.
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(atile, (uint32_t)nb * kTile);
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(btile, (uint32_t)nb * kTile);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(xd, 4u * ((uint32_t)(nb - 1) * (uint32_t)ldx + (uint32_t)n));
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wd, 4u * ((uint32_t)(nb - 1) * (uint32_t)ldw + (uint32_t)m));
+  const uint32_t ldx4 = 4u * (uint32_t)ldx, ldw4 = 4u * (uint32_t)ldw;
   struct Frag {
     intx4 a, b;
     float dx, dw;
@@ -239,11 +247,8 @@ __device__ __forceinline__ floatx16 q8_block_loop(const int8_t* atile, const flo
     kb = min(kb, nb - 1);
     f.a = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(ra, 16u * lane, kb * kTile, 0));
     f.b = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rb, 16u * lane, kb * kTile, 0));
-    // the block's scale rows: 64-bit scalar bases, any leading dimension
-    f.dx = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(xd + (size_t)kb * ldx, 4u * n), xoff, 0, 0));
-    f.dw = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(wd + (size_t)kb * ldw, 4u * m), woff, 0, 0));
+    f.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, xoff, (uint32_t)kb * ldx4, 0));
+    f.dw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, woff, (uint32_t)kb * ldw4, 0));
   };
   intx16 magic = (intx16)(kMagicBits);
   asm volatile("" : "+v"(magic));  // one register copy, not rebuilt per MFMA
@@ -357,9 +362,14 @@ static hipError_t launch_gemm_kernel(dim3 grid, size_t lds, hipStream_t st, cons
   return hipGetLastError();
 }
 
+// The block loop's scale descriptors: k / 32 rows of ld floats in at most
+// 4 GiB - 1 bytes (the executor's arrays take a few hundred KB).
+inline bool scales_fit(int k, int ld) { return (uint64_t)(k / kQK) * (uint64_t)ld * 4u <= 0xFFFFFFFFull; }
+
 hipError_t launch_gemm_q8(const int8_t* xq, const float* xd, int ldx, const int8_t* wq, const float* wd, int ldw,
                           float* y, int n, int m, int k, int ldy, hipStream_t st) {
   if (n <= 0 || m <= 0 || k <= 0 || k % kQK != 0 || ldy < m || ldx < n || ldw < m) return hipErrorInvalidValue;
+  if (!scales_fit(k, ldx) || !scales_fit(k, ldw)) return hipErrorInvalidValue;
   return launch_gemm_kernel<false>(gemm_grid(n, m, true), 0, st, xq, xd, ldx, wq, wd, ldw, y, n, m, k / kQK, ldy,
                                    nullptr, nullptr);
 }
@@ -369,6 +379,7 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
   const int m = 2 * ff;
   if (n <= 0 || ff <= 0 || ff % kQK != 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < m || ldg < n)
     return hipErrorInvalidValue;
+  if (!scales_fit(k, ldx) || !scales_fit(k, ldw)) return hipErrorInvalidValue;
   // LDS: the epilogue's gate and up tiles
   constexpr size_t lds = 2 * 2 * 32 * kGPitch * sizeof(float);
   return launch_gemm_kernel<true>(gemm_grid(n, m), lds, st, xq, xd, ldx, wq, wd, ldw, nullptr, n, m, k / kQK, ldg, gq,
@@ -491,6 +502,7 @@ hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, c
                                    int ldw, int n, int k, const float* q_w, const float* k_w, const float* rope,
                                    const int32_t* pos, float eps, float* out, hipStream_t st) {
   if (n <= 0 || k <= 0 || k % kQK != 0 || ldx < n || ldw < kQKVCols) return hipErrorInvalidValue;
+  if (!scales_fit(k, ldx) || !scales_fit(k, ldw)) return hipErrorInvalidValue;
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
   const dim3 grid(kXcds * reg.rows * reg.cols);
   const int nb = k / kQK;

@@ -187,7 +187,8 @@ int eg2_hip_l2_prefix(float *x, unsigned width, unsigned dims, unsigned rows, vo
  * tiles; xd holds the activation block scales [k/32][ldx] (ldx >= n), wd
  * the weight block scales [k/32][ldw] (ldw >= m; eg2_q8_weight_tiles writes
  * both weight arrays). Replaces kernels/eg2.c:41-119 eg2_mm*. k % 32 == 0;
- * n, m, k and the strides at most 2^24. */
+ * n, m, k and the strides at most 2^24, and each scale array ((k/32) rows
+ * of ldx or ldw floats) below 4 GiB (the same for the two fused forms). */
 int eg2_hip_gemm_q8(const int8_t *xq, const float *xd, unsigned ldx, const int8_t *wq, const float *wd, unsigned ldw,
                     float *y, unsigned n, unsigned m, unsigned k, unsigned ldy, void *stream);
 

@@ -62,6 +62,9 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 3, p, 4, 4, 32, 4, None) == inval  # ldw < m
     assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 4, p, 4, 4, 1 << 25, 4, None) == inval  # k above 2^24
     assert lib.eg2_hip_gemm_q8(None, p, 4, p, p, 4, p, 4, 4, 32, 4, None) == inval
+    # scale arrays of 4 GiB or more: (k/32) ldx 4 = 2^19 * 8192 * 4 bytes
+    assert lib.eg2_hip_gemm_q8(p, p, 8192, p, p, 4, p, 4, 4, 1 << 24, 4, None) == inval
+    assert lib.eg2_hip_gemm_q8(p, p, 4, p, p, 8192, p, 4, 4, 1 << 24, 4, None) == inval
     # gemm_q8_qkv_rope(xq, xd, ldx, wq, wd, ldw, n, k, q_w, k_w, rope, pos, eps, out)
     f = C.c_float(1e-6)
     assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 48, p, p, p, p, f, p, None) == inval  # k % 32
@@ -69,6 +72,7 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 3, p, p, 1280, 4, 32, p, p, p, p, f, p, None) == inval  # ldx < n
     assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, None, f, p, None) == inval
     assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 4, p, p, 1280, 4, 32, p, p, p, p, f, None, None) == inval
+    assert lib.eg2_hip_gemm_q8_qkv_rope(p, p, 8192, p, p, 1280, 4, 1 << 24, p, p, p, p, f, p, None) == inval
     # gemm_q8_geglu(xq, xd, ldx, wq, wd, ldw, gq, gd, ldg, n, ff, k)
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 96, p, p, 4, 4, 48, 32, None) == inval  # ff % 32
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 4, 32, 48, None) == inval  # k % 32
@@ -77,6 +81,7 @@ def test_ops_reject_bad_arguments_without_launching(eg2):
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 3, 4, 32, 32, None) == inval  # ldg < n
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, None, 4, 4, 32, 32, None) == inval
     assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 64, p, p, 4, 0, 32, 32, None) == inval  # n = 0
+    assert lib.eg2_hip_gemm_q8_geglu(p, p, 4, p, p, 8192, p, p, 4, 4, 32, 1 << 24, None) == inval  # w scales 16 GiB
     # attention(qkv, items, item_count, grid, tok, window, rows, longest, scores, cq, cd)
     assert lib.eg2_hip_attention(p, p, p, 0, p, 0, 32, 0, p, p, p, None) == inval  # grid 0
     assert lib.eg2_hip_attention(p, p, p, 64, p, 99999, 32, 0, p, p, p, None) == inval  # window
