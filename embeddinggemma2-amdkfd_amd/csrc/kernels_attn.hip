@@ -815,7 +815,8 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
       // add +0): per 2 keys one MFMA whose block b holds pairs 16 (b % 2) ..
       // + 15 (rows) x the wave's 16 dimensions for key 2 i + b / 2; the
       // group's MFMAs into separate registers, the next group's operands
-      // read from LDS, then the adds in key order.
+      // read from LDS, then the adds in key order; the chunk's groups as
+      // straight-line code (one uniform test per group, no loop counter).
       const int n8 = (int)((min((uint32_t)kCKeys, klast - c0) + 7) & ~7u);
       const float* wa = wl + (g >> 1) * kCPairs + 16 * (g & 1) + r16;
       const float* vb = vl[buf] + (g >> 1) * kCDims + 16 * w + r16;
@@ -825,14 +826,14 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
         an[e] = wa[2 * e * kCPairs];
         bn[e] = vb[2 * e * kCDims];
       }
-      for (int j = 0; j < n8; j += 8) {
+      auto group = [&](int j, bool more) {
 #pragma unroll
         for (int e0 = 0; e0 < 4; e0 += kCBatch) {
           floatx16 prod[kCBatch];
 #pragma unroll
           for (int e = 0; e < kCBatch; ++e)  // keys j + 2 e, j + 2 e + 1
             prod[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(an[e0 + e], bn[e0 + e], zero, 0, 0, 0);
-          if (e0 + kCBatch == 4 && j + 8 < n8) {
+          if (e0 + kCBatch == 4 && more) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               an[e] = wa[(j + 8 + 2 * e) * kCPairs];
@@ -848,7 +849,10 @@ attention_context_kernel(const float* __restrict__ qkv, const float* __restrict_
               for (int v = 0; v < 8; ++v) acc[v] = acc[v] + prod[e][8 * kk + v];
           __builtin_amdgcn_sched_barrier(0);
         }
-      }
+      };
+#pragma unroll
+      for (int j = 0; j < kCKeys; j += 8)
+        if (j < n8) group(j, j + 8 < kCKeys);  // the operands of a group past n8 are read, not used
     }
     // Through LDS (the v chunks' space) to [pair][64 dimensions], then
     // Q8_0: block (32 values) of 4 lanes x 8 values.
