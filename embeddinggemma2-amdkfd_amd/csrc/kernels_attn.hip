@@ -473,8 +473,6 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
   __shared__ uint32_t pbase[kGroupPairs];                               // index in scores of the row's first key
   __builtin_amdgcn_s_setprio(3);  // latency-bound (max, exp, serial sums): issued first on its SIMDs
   const int tid = threadIdx.x, slot = tid / LANES, sub = tid % LANES;
-  if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
-  __syncthreads();
   // XCD-aware order, as in attention_softmax_kernel.
   const uint32_t blk = gridDim.x % kXcdCount == 0
                            ? (blockIdx.x % kXcdCount) * (gridDim.x / kXcdCount) + blockIdx.x / kXcdCount
@@ -492,35 +490,43 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
     }
   }
   float* row = scores + base;  // key first + j at row[j]
-  float m = -__builtin_inff();
-  uint32_t j = sub;
-  for (; j + 3 * LANES < n; j += 4 * LANES) {
-    const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
-    m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
-  }
-  for (; j < n; j += LANES) m = fmaxf(m, row[j]);
-  m = group_max<LANES>(m);
-  const bool to_lds = n <= (uint32_t)kRow;
   float* lrow = prow[slot];
-  for (j = sub; j + 3 * LANES < n; j += 4 * LANES) {
-    const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
-    const float pa = libm::expf_tab(a - m, tab), pb = libm::expf_tab(b - m, tab);
-    const float pc = libm::expf_tab(c - m, tab), pd = libm::expf_tab(d - m, tab);
-    row[j] = pa;
-    row[j + LANES] = pb;
-    row[j + 2 * LANES] = pc;
-    row[j + 3 * LANES] = pd;
-    if (to_lds) {
-      lrow[j] = pa;
-      lrow[j + LANES] = pb;
-      lrow[j + 2 * LANES] = pc;
-      lrow[j + 3 * LANES] = pd;
+  const bool to_lds = n <= (uint32_t)kRow;
+  // A row of at most kRow keys is read once into registers (kPer keys per
+  // lane), its maximum taken and its p computed from them; a longer one (a
+  // packing longer than the caller's `longest`) is read twice from global
+  // memory. The exp table is staged while the first reads are in flight.
+  constexpr int kPer = kRow / LANES;
+  float v[kPer];
+  float m = -__builtin_inff();
+  if (to_lds) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t j = sub + LANES * i;
+      v[i] = j < n ? row[j] : -__builtin_inff();
+      m = fmaxf(m, v[i]);
     }
+  } else {
+    uint32_t j = sub;
+    for (; j + 3 * LANES < n; j += 4 * LANES) {
+      const float a = row[j], b = row[j + LANES], c = row[j + 2 * LANES], d = row[j + 3 * LANES];
+      m = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+    }
+    for (; j < n; j += LANES) m = fmaxf(m, row[j]);
   }
-  for (; j < n; j += LANES) {
-    const float p = libm::expf_tab(row[j] - m, tab);
-    row[j] = p;
-    if (to_lds) lrow[j] = p;
+  if (tid < 32) tab[tid] = libm::kExp2Tab.t[tid];
+  m = group_max<LANES>(m);
+  __syncthreads();  // tab
+  if (to_lds) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t j = sub + LANES * i;
+      const float p = libm::expf_tab(v[i] - m, tab);  // computed for every slot: no branch per key
+      if (j < n) row[j] = p;
+      lrow[j] = j < n ? p : 0.0f;  // +0 past the row: the sum below adds whole batches
+    }
+  } else {
+    for (uint32_t j = sub; j < n; j += LANES) row[j] = libm::expf_tab(row[j] - m, tab);
   }
   if (sub == 0) {
     plen[slot] = n;
@@ -533,17 +539,39 @@ attention_softmax_group_kernel(float* __restrict__ scores, const uint4* __restri
     if (cnt > 0) {
       float sum = 0.0f;
       if (cnt <= (uint32_t)kRow) {
-        const float* pr = prow[tid];
-        uint32_t k = 0;
-#pragma unroll 2
-        for (; k + 4 <= cnt; k += 4) {
-          const float4 p4 = *reinterpret_cast<const float4*>(pr + k);
-          sum = sum + p4.x;
-          sum = sum + p4.y;
-          sum = sum + p4.z;
-          sum = sum + p4.w;
+        // Whole batches of 16 keys (the row's LDS slots past cnt hold +0,
+        // and adding +0 to a sum of non-negative values changes no bit),
+        // from two register sets: a set is reloaded right after it is
+        // added, so its reads are in flight during the other set's adds.
+        const float4* p4 = reinterpret_cast<const float4*>(prow[tid]);
+        constexpr uint32_t kB = 4, kSets = kRow / (4 * kB);
+        const uint32_t nb = (cnt + 4 * kB - 1) / (4 * kB);
+        float4 a[kB], b[kB];
+        auto fill = [&](float4 (&x)[kB], uint32_t batch) {
+#pragma unroll
+          for (uint32_t i = 0; i < kB; ++i) x[i] = p4[kB * min(batch, kSets - 1) + i];
+        };
+        auto add = [&](const float4 (&x)[kB]) {
+#pragma unroll
+          for (uint32_t i = 0; i < kB; ++i) {
+            sum = sum + x[i].x;
+            sum = sum + x[i].y;
+            sum = sum + x[i].z;
+            sum = sum + x[i].w;
+          }
+        };
+        fill(a, 0);
+        fill(b, 1);
+        for (uint32_t bt = 0; bt < nb; bt += 2) {
+          add(a);
+          __builtin_amdgcn_sched_barrier(0);
+          fill(a, bt + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          if (bt + 1 < nb) add(b);
+          __builtin_amdgcn_sched_barrier(0);
+          fill(b, bt + 3);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        for (; k < cnt; ++k) sum = sum + pr[k];
       } else {
         const float* pr = scores + pbase[tid];
 #pragma unroll 1
