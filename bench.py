@@ -675,54 +675,6 @@ def synth_model(eg2, path, threads):
                    rope_base_swa=1e4, threads=threads)
 
 
-def default_queues_child(steps, warmup):
-    """The headline's lanes measurement under the environment's hardware
-    queues (child process of run_default_queues_child): one JSON line."""
-    import numpy as np
-    import torch
-
-    import __graft_entry__
-
-    eg2 = __graft_entry__._package()
-    torch.cuda.set_device(0)
-    rng = np.random.default_rng(0)
-    ids = rng.integers(0, eg2.VOCAB, TOKENS).astype(np.int32)
-    offsets = list(range(0, TOKENS + 1, TOKENS // SEQS))
-    with tempfile.TemporaryDirectory() as d:
-        path = os.path.join(d, "bench.gguf")
-        synth_model(eg2, path, min(host_cpus(), 64))
-        enc = eg2.Encoder(path)
-        lanes = enc.lanes
-        for lane in range(lanes):
-            enc.stage(ids, offsets, lane)
-        for i in range(warmup * lanes):
-            enc.launch(1, i % lanes)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(steps):
-            enc.launch(1, i % lanes)
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) / steps * 1e3
-        enc.close()
-    print(json.dumps({"hw_queues": int(os.environ.get("GPU_MAX_HW_QUEUES", "4")), "lanes": lanes,
-                      "ms_per_step": round(ms, 4), "tokens_per_s": round(TOKENS / ms * 1e3, 1)}), flush=True)
-
-
-def run_default_queues_child(steps, warmup):
-    import subprocess
-
-    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--default-queues-child", "--steps", str(steps),
-                        "--warmup", str(warmup)], capture_output=True, text=True, timeout=600)
-    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
-    if r.returncode != 0 or not lines:
-        log(f"default-queue measurement failed (rc {r.returncode}): {r.stderr[-500:]}")
-        return None
-    res = json.loads(lines[-1])
-    log(f"runtime default queues ({res['hw_queues']}): {res['lanes']} lanes, {res['ms_per_step']:.3f} ms/step, "
-        f"{res['tokens_per_s']:,.0f} tokens/s")
-    return res
-
-
 def run_configs(eg2, torch, steps, thread_counts):
     out = {}
     for name, fn in (("1_gemm_q8", config1_gemm), ("2_attention", config2_attention), ("3_layer", config3_layer)):
@@ -752,37 +704,18 @@ def main():
                     help="run only the dominant GEMM (or the copy calibration kernel) for counter runs, "
                          "or only the per-kernel table, or only configurations 1-3")
     ap.add_argument("--no-configs", action="store_true", help="skip configurations 1-3")
-    ap.add_argument("--no-default-queues", action="store_true",
-                    help="skip the measurement under the runtime's default hardware queues")
-    ap.add_argument("--default-queues-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has a single MI355X and this path runs "
               "independent waves per GPU (no collectives); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    if args.default_queues_child:
-        default_queues_child(args.steps, args.warmup)
-        return
     if args.kernel_only:
         kernel_only(args.kernel_only, args.steps)
         return
     # The library's own configuration, as a service started on this box
-    # runs it: HIP's default hardware queues (GPU_MAX_HW_QUEUES as the
-    # environment has it, 4 unless set), where the executor opens
-    # min(4, queues - 1) lanes. Measured in a child process, before this
-    # process touches the GPU (the HIP runtime reads the variable once).
-    default_queues = None
-    if not args.no_default_queues:
-        default_queues = run_default_queues_child(args.steps, args.warmup)
-    # The serving configuration of the headline: at least 8 hardware queues
-    # per process, so each of the executor's four lanes runs on a queue of
-    # its own; set before torch or the library initialises HIP.
-    try:
-        queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
-    except ValueError:
-        queues = 4
-    os.environ["GPU_MAX_HW_QUEUES"] = str(max(queues, 8))
-
+    # runs it: the HIP runtime's hardware queues as the environment sets
+    # them (GPU_MAX_HW_QUEUES, 4 unless set); each of the executor's four
+    # lanes has a queue of its own either way (its streams carry a CU mask).
     import numpy as np
     import torch
 
@@ -924,8 +857,7 @@ def main():
                                "packed wave of 16x128 tokens", "tokens_per_wave": TOKENS, "sequences": SEQS,
                    "layers": LAYERS, "hidden": 768, "ffn": 1152, "heads": "3q/1kv x 256", "weights": "Q8_0",
                    "attention": "full within sequence, RoPE base 1e4", "lanes": lanes,
-                   "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"])},
-        "default_queues": default_queues,
+                   "hw_queues": os.environ.get("GPU_MAX_HW_QUEUES", "runtime default (4)")},
         "roofline": {"bound": "mfma", "kernel": "gemm_q8_geglu gate|up 2048x2304x768 + GeGLU + Q8_0 (v_mfma_i32_32x32x32_i8; "
                                                 "achieved/peak in T int8 op/s)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",

@@ -219,10 +219,10 @@ int eg2_hip_gemm_q8_geglu(const int8_t *xq, const float *xd, unsigned ldx, const
                           void *stream);
 
 /* ------------------------------------------------------------ executor phases
- * A context has several lanes (EG2_HIP_LANES, 1..8; by default min(4,
- * GPU_MAX_HW_QUEUES - 1), i.e. 3 under the HIP runtime's default of 4
- * hardware queues per process, so that each lane has a queue): each lane
- * is a stream with its own 2048-token workspace, pinned staging and
+ * A context has several lanes (EG2_HIP_LANES, 1..8, 4 by default): each
+ * lane is a stream on a hardware queue of its own (the stream carries a
+ * CU mask of every CU, which the HIP runtime serves from a dedicated queue
+ * whatever GPU_MAX_HW_QUEUES says) with its own 2048-token workspace, pinned staging and
  * hipGraphs, over the context's one copy of the weights, so waves on
  * different lanes run on the device at the same time. ei_gemma2_kfd_batch
  * (gemma2_kfd.h) takes any free lane and runs stage + launch(1) + collect
