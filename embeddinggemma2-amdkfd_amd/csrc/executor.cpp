@@ -898,6 +898,16 @@ extern "C" bool eg2_kfd_collect_lane(void* ctx, unsigned lane, float* out, char*
   return on_lane(ctx, lane, err, len, [&](Backend& b, Lane& ln) { b.collect(ln, out); });
 }
 
+extern "C" int eg2_kfd_lane_ready(void* ctx, unsigned lane, char* err, size_t len) {
+  int ready = -1;
+  const bool ok = on_lane(ctx, lane, err, len, [&](Backend&, Lane& ln) {
+    const hipError_t e = hipStreamQuery(ln.stream);
+    if (e != hipSuccess && e != hipErrorNotReady) throw std::runtime_error(std::string("HIP lane query: ") + hipGetErrorString(e));
+    ready = e == hipSuccess ? 1 : 0;
+  });
+  return ok ? ready : -1;
+}
+
 // Lane 0 through the pool: eg2_kfd_stage takes it (unless a wave staged
 // by it is still uncollected) and keeps it after a successful stage;
 // eg2_kfd_collect gives it back.

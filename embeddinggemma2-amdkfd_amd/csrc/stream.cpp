@@ -3,12 +3,14 @@
 #include "eg2_stream.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <list>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "eg2_hip.h"
@@ -17,6 +19,7 @@
 namespace {
 
 constexpr int kEmbd = 768;
+constexpr double kWaitSeconds = 30.0;  // polling for a finished lane, as long as a lane's own wait
 
 bool valid(const eg2_batch_config* c) {
   return c && c->max_batch_tokens > 0 && c->max_batch_sequence_tokens > 0 && c->max_batch_requests > 0;
@@ -154,9 +157,10 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
     const size_t waves = eg2_pack_waves(lengths.data(), n_texts, cfg, order.data(), wave_end.data());
     if (!waves) throw std::runtime_error("packing failed");
 
-    // Wave w runs on slot w % L, each slot a lane held for the whole stream;
-    // a slot's previous wave is collected just before the slot is reused,
-    // so up to L waves are in flight. The lanes are taken before the first
+    // Each slot is a lane held for the whole stream; wave w runs on a free
+    // slot, or else on the first slot whose wave finishes (collected just
+    // before the slot is reused), so up to L waves are in flight and a long
+    // wave never holds up the slots behind it. The lanes are taken before the first
     // wave: one waiting for a free lane (nothing is held yet), the others
     // only if free at once, so that a stream never waits while holding
     // lanes (concurrent streams could otherwise each hold some lanes and
@@ -190,10 +194,32 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
         std::fill(e + dims[i], e + kEmbd, 0.0f);
       }
     };
+    // A free slot, or the first busy one whose wave is done (polled, as the
+    // executor's own waits are); past kWaitSeconds the oldest wave's
+    // collect takes over, whose wait reports a time-out or failure.
+    std::vector<size_t> started(L, 0);
+    auto free_slot = [&]() -> size_t {
+      for (size_t s = 0; s < L; ++s)
+        if (!busy[s]) return s;
+      const auto t0 = std::chrono::steady_clock::now();
+      for (;;) {
+        for (size_t s = 0; s < L; ++s) {
+          if (eg2_kfd_lane_ready(ctx, (unsigned)held.lanes[s], msg, sizeof msg) != 0) {
+            finish(s);  // done, or failed: collect reports the failure
+            return s;
+          }
+        }
+        if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kWaitSeconds) {
+          const size_t oldest = (size_t)(std::min_element(started.begin(), started.end()) - started.begin());
+          finish(oldest);
+          return oldest;
+        }
+        std::this_thread::yield();
+      }
+    };
     size_t begin = 0;
     for (size_t w = 0; w < waves; ++w) {
-      const size_t slot = w % L, end = wave_end[w];
-      if (busy[slot]) finish(slot);
+      const size_t slot = free_slot(), end = wave_end[w];
       wave_ids.clear();
       offsets.assign(1, 0);
       for (size_t k = begin; k < end; ++k) {
@@ -208,10 +234,11 @@ extern "C" bool eg2_stream_embed(void* ctx, const int32_t* ids, const size_t* te
       pend_begin[slot] = begin;
       pend_end[slot] = end;
       busy[slot] = true;
+      started[slot] = w;
       begin = end;
     }
-    for (size_t w = waves - L; w < waves; ++w)
-      if (busy[w % L]) finish(w % L);
+    for (size_t s = 0; s < L; ++s)
+      if (busy[s]) finish(s);
     if (n_waves) *n_waves = waves;
     return true;
   } catch (const std::exception& e) {

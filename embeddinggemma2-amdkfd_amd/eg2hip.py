@@ -173,6 +173,7 @@ SIGNATURES = {
                                       C.c_size_t]),
     "eg2_kfd_launch_lane": (C.c_bool, [C.c_void_p, C.c_uint, C.c_uint, C.c_char_p, C.c_size_t]),
     "eg2_kfd_collect_lane": (C.c_bool, [C.c_void_p, C.c_uint, _f, C.c_char_p, C.c_size_t]),
+    "eg2_kfd_lane_ready": (C.c_int, [C.c_void_p, C.c_uint, C.c_char_p, C.c_size_t]),
     "ei_gemma2_kfd_batch": (C.c_bool, [C.c_void_p, _i32, C.POINTER(C.c_size_t), C.c_size_t, _f, C.c_char_p,
                                        C.c_size_t]),
 }

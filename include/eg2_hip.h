@@ -256,6 +256,12 @@ bool eg2_kfd_stage_lane(void *ctx, unsigned lane, const int32_t *ids, const size
 bool eg2_kfd_launch_lane(void *ctx, unsigned lane, unsigned repeats, char *err, size_t len);
 /* Waits for the lane's wave and copies its [batch][768] embeddings to out. */
 bool eg2_kfd_collect_lane(void *ctx, unsigned lane, float *out, char *err, size_t len);
+/* No counterpart in the reference; for a caller holding several lanes (the
+ * stream driver) that collects whichever wave finishes first: 1 when the
+ * lane's enqueued work is done (eg2_kfd_collect_lane then returns without
+ * waiting), 0 while it runs, -1 on an error (message in err; collect
+ * reports it too). Never waits. */
+int eg2_kfd_lane_ready(void *ctx, unsigned lane, char *err, size_t len);
 /* The same on lane 0, which eg2_kfd_stage takes from the pool (waiting
  * while a batch call holds it) and keeps until eg2_kfd_collect hands it
  * back; launch and collect without a staged wave fail. */
