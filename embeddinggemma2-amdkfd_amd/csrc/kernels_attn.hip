@@ -432,12 +432,13 @@ attention_softmax_kernel(float* __restrict__ scores, const uint4* __restrict__ t
 // (token, head) pair, 64 / LANES pairs per wave, 16 pairs per workgroup, so
 // several pairs share each instruction of the per-pair set-up and of the
 // maximum's combination. Lane j of a pair's LANES takes keys
-// first + j + LANES i: the row maximum (order-free; combined over the pair's
-// lanes by DPP), then p = expf(score - m) written back over the scores and
-// into the pair's LDS row (as long as the form's bound, kSoftmaxLanes16 or
-// kSoftmaxLanes32 keys: 8 or 17 KB per workgroup, which leaves room on a CU
-// for other lanes' kernels); then lane i of the first wave adds pair i's p
-// values in key order and writes 1/sum into the scratch's head. A longer
+// first + j + LANES i, held in registers: the row maximum (order-free;
+// combined over the pair's lanes by DPP), then p = expf(score - m) written
+// back over the scores and into the pair's LDS row (as long as the form's
+// bound, kSoftmaxLanes16 or kSoftmaxLanes32 keys: 8 or 17 KB per workgroup,
+// which leaves room on a CU for other lanes' kernels; +0 past the row);
+// then lane i of the first wave adds pair i's p values in key order, 16 at
+// a time from two register sets, and writes 1/sum into the scratch's head. A longer
 // row (a packing longer than the caller's `longest`) is summed from the
 // scores in global memory instead: slower, same bits. The same
 // operations in the same order as attention_softmax_kernel, which takes
