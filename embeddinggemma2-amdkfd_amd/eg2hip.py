@@ -350,6 +350,15 @@ class Encoder:
         if not lib().eg2_kfd_launch_lane(self.ctx, lane, repeats, err, 1024):
             raise HipError(err.value.decode())
 
+    def ready(self, lane=0):
+        """eg2_kfd_lane_ready: True once the lane's enqueued work is done,
+        False while it runs (never waits)."""
+        err = C.create_string_buffer(1024)
+        r = lib().eg2_kfd_lane_ready(self.ctx, lane, err, 1024)
+        if r < 0:
+            raise HipError(err.value.decode())
+        return bool(r)
+
     def collect(self, lane=0):
         import numpy as np
 

@@ -1,8 +1,8 @@
 """The reference's own engine, built against this library (CPU only).
 
 The executor boundary claims that the reference's engine drops onto
-libeg2hip.so with the three engine edits INTEGRATION.md gives (a Q8_0
-`gemma-embedding` file routed to the kfd executor). This test builds that:
+libeg2hip.so with three engine edits (apply_integration_edits below: a
+Q8_0 `gemma-embedding` file routed to the kfd executor). This test builds that:
 it copies the engine's C sources from the reference tree (present only in
 the build container; the test is skipped elsewhere) into a temporary
 directory, applies those edits there, compiles them with EI_ENABLE_KFD=1
@@ -42,7 +42,10 @@ def edit(path, old, new, count=1):
 
 
 def apply_integration_edits(d):
-    """The engine edits of INTEGRATION.md section 1."""
+    """The three engine edits that route a Q8_0 gemma-embedding file to the
+    kfd executor: a q8_matrices flag in the model, the layer matrices typed
+    after the first layer's attention weight (Q8_0 or Q4_0), and the engine
+    creating the kfd executor when that backend is asked for."""
     edit(os.path.join(d, "model.h"), "    bool embeddinggemma2;\n",
          "    bool embeddinggemma2;\n    bool q8_matrices;\n")
     model_c = os.path.join(d, "model.c")

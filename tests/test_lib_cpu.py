@@ -52,6 +52,12 @@ def test_operator_abi_header_matches_reference_records():
         assert f"typedef struct {{ {fields} }} {name};" in text, name
 
 
+def test_lane_query_rejects_an_empty_context(eg2):
+    err = C.create_string_buffer(256)
+    assert eg2.lib().eg2_kfd_lane_ready(None, 0, err, 256) == -1
+    assert b"empty context" in err.value
+
+
 def test_ops_reject_bad_arguments_without_launching(eg2):
     lib = eg2.lib()
     inval = 1  # hipErrorInvalidValue
