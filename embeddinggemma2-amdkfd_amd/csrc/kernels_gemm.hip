@@ -392,8 +392,8 @@ hipError_t launch_gemm_q8_geglu(const int8_t* xq, const float* xd, int ldx, cons
 // token rows x one 256-wide head (head hc of [q0 q1 q2 | k | v]), wave w the
 // 32 x 32 piece at columns 32 w, with the block loop of gemm_q8_kernel (so
 // the projection's fp32 values are bit-identical to it). The epilogue puts
-// the tile in LDS and, for q and k heads, runs each row's SSE2-order sum of
-// squares (waves 0-3, 8 lanes per row), then (x*w)*inv, the NeoX rotation of
+// the tile in LDS 16 rows at a time and, for q and k heads, runs each row's
+// SSE2-order sum of squares (waves 0-1, 8 lanes per row), then (x*w)*inv, the NeoX rotation of
 // pairs (d, d+128) with the host cos/sin row of the token's position, the
 // 1/16 scale of q -- the operations and order of the standalone
 // qk_norm_rope kernel -- and writes the rows [q0 q1 q2 | k | v] attention
@@ -429,71 +429,84 @@ gemm_q8_qkv_rope_kernel(const int8_t* __restrict__ xq, const float* __restrict__
       xq + (size_t)tr * nb * kTile, xd, ldx, n, 4u * (uint32_t)min(32 * tr + srow, n - 1),
       wq + (size_t)(8 * hc + w) * nb * kTile, wd, ldw, kQKVCols,
       4u * (uint32_t)(kHeadDim * hc + 32 * w + (lane & 31)), nb, lane);
-  // The epilogue's global inputs go out now, so their latency overlaps the
-  // tile's trip through LDS and the sums of squares: the cos/sin and norm
-  // weights of this wave's rows 4w..4w+3 (q, k), or the v columns.
+  // The epilogue runs on the tile in two halves of 16 token rows through a
+  // 16-row LDS tile (17 KB per workgroup, not 34 KB). Its global inputs go
+  // out now, so their latency overlaps the tile's trip through LDS and the
+  // sums of squares: the norm weights, and the cos/sin of this wave's two
+  // rows of each half (rows 16 hf + 2 w + rr).
   constexpr int half = kHeadDim / 2;
   const bool is_v = hc == kHeads + 1;
   const float* wgt = hc < kHeads ? q_w : k_w;
-  float cs_r[4][4], w_r[4];
+  float cs_r[2][2][4], w_r[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     w_r[2 * j] = wgt[lane + 64 * j];
     w_r[2 * j + 1] = wgt[lane + 64 * j + half];
   }
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int t = min(32 * tr + 4 * w + rr, n - 1);
-    const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      cs_r[rr][2 * j] = cs[lane + 64 * j];
-      cs_r[rr][2 * j + 1] = cs[half + lane + 64 * j];
-    }
-  }
-  float* tile = reinterpret_cast<float*>(gemm_lds);  // [32][kRowPitch]
+    for (int rr = 0; rr < 2; ++rr) {
+      const int t = min(32 * tr + 16 * hf + 2 * w + rr, n - 1);
+      const float* cs = rope + (size_t)pos[t] * kHeadDim;  // [cos 0..127 | sin 0..127]
 #pragma unroll
-  for (int v = 0; v < 16; ++v) tile[(8 * (v >> 2) + 4 * g + (v & 3)) * kRowPitch + 32 * w + (lane & 31)] = acc[v];
-  __syncthreads();
-  if (is_v) {
-    // v: the projection as it is; wave w copies rows 4w .. 4w + 3.
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int row = 4 * w + rr, t = 32 * tr + row;
-      if (t >= n) break;
-      float* vrow = out + (size_t)t * kQKVCols + kHeads * kHeadDim + kHeadDim;
-      *reinterpret_cast<float4*>(vrow + 4 * lane) = *reinterpret_cast<const float4*>(tile + row * kRowPitch + 4 * lane);
-    }
-    return;
-  }
-  // kernels.c:233-264 for q head hc (hc < 3) or k (hc == 3).
-  if (w < 4) {
-    const int row = 8 * w + (lane >> 3);
-    const float ss = sse2_combine(sse2_chain<kHeadDim>(tile + row * kRowPitch, lane & 7));
-    if ((lane & 7) == 0) invs[row] = rms_inverse(ss, kHeadDim, eps);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int row = 4 * w + rr, t = 32 * tr + row;
-    if (t >= n) break;
-    const float inv = invs[row];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int dd = lane + 64 * j;
-      const float c = cs_r[rr][2 * j], s = cs_r[rr][2 * j + 1];
-      const float x0 = tile[row * kRowPitch + dd] * w_r[2 * j] * inv;
-      const float x1 = tile[row * kRowPitch + dd + half] * w_r[2 * j + 1] * inv;
-      const float a0 = x0 * c, a1 = x1 * s;
-      const float b0 = x0 * s, b1 = x1 * c;
-      float lo = a0 - a1, hi = b0 + b1;
-      if (hc < kHeads) {
-        lo = lo * 0.0625f;
-        hi = hi * 0.0625f;
+      for (int j = 0; j < 2; ++j) {
+        cs_r[hf][rr][2 * j] = cs[lane + 64 * j];
+        cs_r[hf][rr][2 * j + 1] = cs[half + lane + 64 * j];
       }
-      float* orow = out + (size_t)t * kQKVCols + hc * kHeadDim;
-      orow[dd] = lo;
-      orow[dd + half] = hi;
+    }
+  float* tile = reinterpret_cast<float*>(gemm_lds);  // [16][kRowPitch]
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    if (hf) __syncthreads();  // the first half's tile is no longer read
+    // Register v holds row 8 (v >> 2) + 4 g + (v & 3): rows 0-15 are
+    // v = 0..7, rows 16-31 v = 8..15.
+#pragma unroll
+    for (int v = 8 * hf; v < 8 * hf + 8; ++v)
+      tile[(8 * (v >> 2) + 4 * g + (v & 3) - 16 * hf) * kRowPitch + 32 * w + (lane & 31)] = acc[v];
+    __syncthreads();
+    if (is_v) {
+      // v: the projection as it is; wave w copies rows 2w, 2w + 1 of the half.
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int row = 2 * w + rr, t = 32 * tr + 16 * hf + row;
+        if (t >= n) break;
+        float* vrow = out + (size_t)t * kQKVCols + kHeads * kHeadDim + kHeadDim;
+        *reinterpret_cast<float4*>(vrow + 4 * lane) =
+            *reinterpret_cast<const float4*>(tile + row * kRowPitch + 4 * lane);
+      }
+      continue;
+    }
+    // kernels.c:233-264 for q head hc (hc < 3) or k (hc == 3): waves 0-1
+    // run the half's 16 rows' SSE2 sums of squares, 8 lanes per row.
+    if (w < 2) {
+      const int row = 8 * w + (lane >> 3);
+      const float ss = sse2_combine(sse2_chain<kHeadDim>(tile + row * kRowPitch, lane & 7));
+      if ((lane & 7) == 0) invs[16 * hf + row] = rms_inverse(ss, kHeadDim, eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int row = 2 * w + rr, t = 32 * tr + 16 * hf + row;
+      if (t >= n) break;
+      const float inv = invs[16 * hf + row];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int dd = lane + 64 * j;
+        const float c = cs_r[hf][rr][2 * j], s = cs_r[hf][rr][2 * j + 1];
+        const float x0 = tile[row * kRowPitch + dd] * w_r[2 * j] * inv;
+        const float x1 = tile[row * kRowPitch + dd + half] * w_r[2 * j + 1] * inv;
+        const float a0 = x0 * c, a1 = x1 * s;
+        const float b0 = x0 * s, b1 = x1 * c;
+        float lo = a0 - a1, hi = b0 + b1;
+        if (hc < kHeads) {
+          lo = lo * 0.0625f;
+          hi = hi * 0.0625f;
+        }
+        float* orow = out + (size_t)t * kQKVCols + hc * kHeadDim;
+        orow[dd] = lo;
+        orow[dd + half] = hi;
+      }
     }
   }
 }
@@ -506,7 +519,7 @@ hipError_t launch_gemm_q8_qkv_rope(const int8_t* xq, const float* xd, int ldx, c
   const XcdRegions reg = xcd_split((n + 31) / 32, kQkvHeads);
   const dim3 grid(kXcds * reg.rows * reg.cols);
   const int nb = k / kQK;
-  constexpr size_t lds = 32 * kRowPitch * sizeof(float);  // the epilogue tile
+  constexpr size_t lds = 16 * kRowPitch * sizeof(float);  // the epilogue's 16-row tile
   if (nb % kUnroll == 0)
     hipLaunchKernelGGL(gemm_q8_qkv_rope_kernel<false>, grid, dim3(512), lds, st, xq, xd, ldx, wq, wd, ldw, n, nb, q_w,
                        k_w, rope, pos, eps, out);
